@@ -1,0 +1,169 @@
+/*
+ * joule_amd.h -- C ABI of the MI355X (gfx950) MoE decode block.
+ *
+ * Drop-in boundary for the reference's MoE hot path.  Citations are to the
+ * reference repository (SatPaingOo/joule):
+ *
+ *   layer_ffn_batch        src/jouleai/native/decode_kernel.c:1387-1508
+ *   KernelCfg              src/jouleai/native/decode_kernel.c:269-286
+ *                          (ctypes mirror src/jouleai/native/decoder3.py:35-46)
+ *   KernelW expert tables  src/jouleai/native/decode_kernel.c:303, 318-321
+ *                          (built by decoder3.py:329-367 _load_experts)
+ *   q4_gemv_f32            src/jouleai/native/quant_gemv.c:35, expert_ffn.c:132
+ *   q4_gemm_f32            src/jouleai/native/expert_ffn.c:200-215
+ *   KernelBackend API      src/jouleai/native/backend.py:45-69
+ *
+ * Conventions
+ *   - Every function returns int: 0 on success, a negative JM_ERR_* code on
+ *     failure; jm_last_error() then holds a message (per calling thread).
+ *     The reference's functions return void and clamp or ignore bad shapes
+ *     (decode_kernel.c:1390, 1522); here bad shapes are errors.
+ *   - Tensor pointers are DEVICE pointers (HIP), caller-owned.  The library
+ *     allocates only its own workspace and offset table.
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *     Work is stream-ordered; calls return before the GPU finishes.
+ *   - A jm_store is used by one stream at a time (its workspace is shared
+ *     by the calls made through it), the per-handle counterpart of the
+ *     reference's process-global workspace g_ws (decode_kernel.c:356).
+ */
+#ifndef JOULE_AMD_H
+#define JOULE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JM_ABI_VERSION 1
+
+#define JM_OK 0
+#define JM_ERR_ARG (-1)
+#define JM_ERR_SHAPE (-2)
+#define JM_ERR_HIP (-3)
+
+#define JM_DTYPE_F32 0
+#define JM_DTYPE_BF16 1
+
+/* Byte-identical to the reference's KernelCfg (decode_kernel.c:269-286), so
+ * a host that already fills one (decoder3.py:95-119) passes it unchanged.
+ * Fields read here: L, d, E, topk, intermediate, norm_topk_prob, expert_i8,
+ * expert_bf16 (the last two must be 0: the Q4 store). */
+typedef struct jm_kernel_cfg {
+    int L, d, n_heads, n_kv, hd, E, topk, V;
+    float eps;
+    int maxT;
+    int intermediate;
+    int qk_norm_type;
+    int bias_qkv;
+    int norm_topk_prob;
+    int expert_i8;
+    int expert_bf16;
+} jm_kernel_cfg;
+
+typedef struct jm_store jm_store;
+
+/* ABI version (JM_ABI_VERSION) and the last error message of this thread. */
+int jm_version(void);
+const char* jm_last_error(void);
+
+/* sizeof(jm_kernel_cfg) and the compile-time kernel parameters: digits per
+ * activation value in the Q4 dot, tokens per pass over an expert. */
+int jm_abi_sizes(int* kernel_cfg_bytes, int* ndig, int* nt);
+
+/*
+ * HBM-resident expert store.  Replaces the KernelW expert pointer tables
+ * expert_pk[3][L*E] / expert_sc[3][L*E] (decode_kernel.c:318-321) that
+ * _load_experts (decoder3.py:329-367) builds over an mmap of experts_q4.bin.
+ *   blob     device copy of experts_q4.bin, byte for byte (16-byte aligned)
+ *   offsets  host uint64 [3][L*E][2]: for part p in (gate, up, down) and
+ *            key l*E+e, the byte offsets of the scales and of the packed
+ *            nibbles of that record within blob (the index's offset and
+ *            offset + scales_bytes)
+ *   group    Q4 group size, 64 (the reference store) or 32
+ * Checks that every record lies inside the blob.  The blob stays owned by
+ * the caller and must outlive the store.
+ */
+int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint64_t blob_bytes,
+                    const uint64_t* offsets, jm_store** out);
+int jm_store_destroy(jm_store* s);
+
+/* Router weights, the reference's KernelW.gate_w [L][E][d]
+ * (decode_kernel.c:303).  dtype JM_DTYPE_BF16 takes the reference's bf16
+ * table as is; JM_DTYPE_F32 takes float32.  Device memory, caller-owned. */
+int jm_store_set_router(jm_store* s, const void* gate_w, int dtype);
+
+/* Size the workspace for batches of up to max_B tokens now, so that later
+ * calls with B <= max_B allocate nothing. */
+int jm_store_reserve(jm_store* s, int max_B);
+
+int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, int* group);
+
+/*
+ * The MoE block of one layer: layer_ffn_batch(cfg, W, l, x, B, out)
+ * (decode_kernel.c:1387-1508), for any B >= 0 (the reference clamps B to 16
+ * at decode_kernel.c:1522).
+ *   x        [B][d] float32, out [B][d] float32 (16-byte aligned)
+ *   topk_idx optional [B][topk] int32 receives the selected experts
+ *   topk_w   optional [B][topk] float32 receives their routing weights
+ * Router indices and weights are bit-identical to the reference arithmetic.
+ */
+int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out,
+                       int32_t* topk_idx, float* topk_w, void* stream);
+
+/* Copy an intermediate of the last jm_layer_ffn_batch call out of the
+ * store's workspace into caller device memory (stream-ordered), for tests and
+ * profiling.  `bytes` must not exceed the field's size at the last call's B:
+ *   JM_WS_LOGITS     float [B][E] router scores
+ *   JM_WS_SEG_OFF    int32 [E+1] segment starts (slots grouped by expert)
+ *   JM_WS_SEG_SLOT   int32 [B*topk] slot ids b*topk+i grouped by expert
+ *   JM_WS_ACTIVE     int32 [E] expert ids with tokens, ascending
+ *   JM_WS_N_ACTIVE   int32 [1] how many of them
+ *   JM_WS_FIRST_SLOT int32 [E] first slot of each active expert
+ *   JM_WS_ACT        float [B*topk][intermediate] SiLU(gate)*up per slot
+ *   JM_WS_Y          float [B*topk][d] weighted expert output per slot */
+#define JM_WS_LOGITS 0
+#define JM_WS_SEG_OFF 1
+#define JM_WS_SEG_SLOT 2
+#define JM_WS_ACTIVE 3
+#define JM_WS_N_ACTIVE 4
+#define JM_WS_FIRST_SLOT 5
+#define JM_WS_ACT 6
+#define JM_WS_Y 7
+int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t bytes, void* stream);
+
+/* ---- stage entry points (the steps of layer_ffn_batch, for tests) ---- */
+
+/* Router scores, softmax, top-k and renormalisation
+ * (decode_kernel.c:1424-1448): logits [B][E], top [B][topk], tw [B][topk]. */
+int jm_router(const void* gate_w, int dtype, const float* x, int B, int E, int d, int topk,
+              int renorm, float* logits, int32_t* top, float* tw, void* stream);
+
+/* Token-to-expert dispatch (decode_kernel.c:1449-1485) as a stable counting
+ * sort by expert id: seg_off [E+1], seg_slot [nslot], active [E],
+ * n_active [1], first_slot [E]. */
+int jm_dispatch(const int32_t* top, int nslot, int E, int32_t* seg_off, int32_t* seg_slot,
+                int32_t* active, int32_t* n_active, int32_t* first_slot, void* stream);
+
+/* Exact dequantisation (q - 8) * float(scale) of one record
+ * (q4_store.py:58-67 _dequantize). */
+int jm_q4_dequant(float* out, const uint8_t* packed, const uint16_t* scales, int64_t numel, int group,
+                  void* stream);
+
+/* ---- the KernelBackend products (backend.py:45-69), device pointers ---- */
+
+/* out[m] = dequant(W[m][d]) . x[d]; argument order of q4_gemv_f32
+ * (quant_gemv.c:35) plus the stream. */
+int jm_q4_gemv_f32(float* out, const float* x, const uint8_t* packed, const uint16_t* scales,
+                   int m, int d, int group, void* stream);
+
+/* out[T][m] = X[T][d] . dequant(W[m][d])^T; argument order of q4_gemm_f32
+ * (expert_ffn.c:201) plus the stream. */
+int jm_q4_gemm_f32(float* out, const float* X, int T, const uint8_t* packed, const uint16_t* scales,
+                   int m, int d, int group, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JOULE_AMD_H */

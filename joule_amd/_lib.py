@@ -1,0 +1,97 @@
+"""ctypes binding of libjoule_amd.so (include/joule_amd.h).
+
+Plays the role of the reference's DLL cache ``get_dll``
+(src/jouleai/native/backend.py:32-42): one handle per process, loaded from
+the package directory.  There is no fallback: if the library is missing the
+import of anything that needs it fails with an error saying how to build it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libjoule_amd.so"
+
+JM_DTYPE_F32 = 0
+JM_DTYPE_BF16 = 1
+
+# Every function declared in include/joule_amd.h, with its argument types.
+_c = ctypes
+_vp, _i, _u64, _i64 = _c.c_void_p, _c.c_int, _c.c_uint64, _c.c_int64
+SIGNATURES = {
+    "jm_version": ([], _i),
+    "jm_last_error": ([], _c.c_char_p),
+    "jm_abi_sizes": ([_vp, _vp, _vp], _i),
+    "jm_store_create": ([_vp, _i, _vp, _u64, _vp, _vp], _i),
+    "jm_store_destroy": ([_vp], _i),
+    "jm_store_set_router": ([_vp, _vp, _i], _i),
+    "jm_store_reserve": ([_vp, _i], _i),
+    "jm_store_info": ([_vp] + [_vp] * 6, _i),
+    "jm_layer_ffn_batch": ([_vp, _i, _vp, _i, _vp, _vp, _vp, _vp], _i),
+    "jm_store_copy_workspace": ([_vp, _i, _vp, _u64, _vp], _i),
+    "jm_router": ([_vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp], _i),
+    "jm_dispatch": ([_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp], _i),
+    "jm_q4_dequant": ([_vp, _vp, _vp, _i64, _i, _vp], _i),
+    "jm_q4_gemv_f32": ([_vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
+    "jm_q4_gemm_f32": ([_vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
+}
+
+
+class KernelCfg(ctypes.Structure):
+    """The reference's KernelCfg (decode_kernel.c:269-286, decoder3.py:35-46)."""
+    _fields_ = [("L", _i), ("d", _i), ("n_heads", _i), ("n_kv", _i), ("hd", _i),
+                ("E", _i), ("topk", _i), ("V", _i), ("eps", _c.c_float), ("maxT", _i),
+                ("intermediate", _i), ("qk_norm_type", _i), ("bias_qkv", _i),
+                ("norm_topk_prob", _i), ("expert_i8", _i), ("expert_bf16", _i)]
+
+
+# jm_store_copy_workspace fields
+WS_LOGITS, WS_SEG_OFF, WS_SEG_SLOT, WS_ACTIVE, WS_N_ACTIVE, WS_FIRST_SLOT, WS_ACT, WS_Y = range(8)
+
+
+class JouleError(RuntimeError):
+    """A libjoule_amd call returned a non-zero status."""
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libjoule_amd.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m joule_amd.build` "
+                "(hipcc, gfx950). There is no CPU fallback.")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (args, res) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib().jm_last_error().decode(errors="replace")
+        raise JouleError(f"{what or 'libjoule_amd'} failed ({rc}): {msg}")
+
+
+def ptr(t) -> ctypes.c_void_p:
+    """Device (or host) address of a torch tensor / numpy array, None -> NULL."""
+    if t is None:
+        return ctypes.c_void_p(0)
+    if hasattr(t, "data_ptr"):
+        return ctypes.c_void_p(t.data_ptr())
+    return ctypes.c_void_p(t.ctypes.data)
+
+
+def stream_handle(stream=None) -> ctypes.c_void_p:
+    """hipStream_t of a torch stream (default: torch's current stream)."""
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)

@@ -1,0 +1,373 @@
+// C ABI of the MI355X MoE decode block (declared in include/joule_amd.h).
+//
+// Every entry point returns an int status (0 = ok, negative = error) and
+// records a message readable with jm_last_error().  Pointers to tensors are
+// device pointers; the library never frees caller memory.  Work is enqueued
+// on the caller's stream (NULL = the default stream); nothing synchronises
+// except workspace growth, which the caller can do ahead of time with
+// jm_store_reserve().
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/joule_amd.h"
+#include "jm_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(JM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define JM_HIP(expr, what)                              \
+    do {                                                \
+        hipError_t _e = (expr);                         \
+        if (_e != hipSuccess) return hip_fail(_e, what); \
+    } while (0)
+
+inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_group_shape(int d, int m, int group) {
+    if (group != 32 && group != 64) return fail(JM_ERR_SHAPE, "group must be 32 or 64, got %d", group);
+    if (d <= 0 || m <= 0) return fail(JM_ERR_SHAPE, "d and intermediate must be positive");
+    if (d % group || m % group) return fail(JM_ERR_SHAPE, "d=%d and intermediate=%d must be multiples of the group %d", d, m, group);
+    const int lpr = d / group;
+    if (lpr != 16 && lpr != 32 && lpr != 64)
+        return fail(JM_ERR_SHAPE, "d / group must be 16, 32 or 64 (got %d)", lpr);
+    if (m / group > 64) return fail(JM_ERR_SHAPE, "intermediate / group must be <= 64 (got %d)", m / group);
+    if (m % 64) return fail(JM_ERR_SHAPE, "intermediate must be a multiple of 64 (got %d)", m);
+    if (d % 128) return fail(JM_ERR_SHAPE, "d must be a multiple of 128 (got %d)", d);
+    return 0;
+}
+
+}  // namespace
+
+struct jm_store {
+    int L, E, d, m, topk, renorm, group;
+    const uint8_t* blob;
+    uint64_t blob_bytes;
+    uint64_t* off_dev;          // [3][L*E][2]
+    const void* router;         // [L][E][d]
+    int router_bf16;
+    int device;
+    // workspace, sized for cap_B tokens; last_B = B of the last call
+    int cap_B;
+    int last_B;
+    void* ws;
+    float* logits;
+    int* top;
+    float* tw;
+    uint32_t* xdig;
+    float* xscale;
+    int* seg_off;
+    int* seg_slot;
+    int* active;
+    int* n_active;
+    int* first_slot;
+    int* rank;
+    float* act;
+    uint32_t* adig;
+    float* ascale;
+    float* y;
+};
+
+namespace {
+
+int reserve(jm_store* s, int B) {
+    if (B <= s->cap_B) return 0;
+    const int E = s->E, d = s->d, m = s->m, k = s->topk, G = s->group;
+    const size_t nslot = (size_t)B * k;
+    const size_t words_d = (size_t)(d / G) * JM_NDIG * (G / 8);
+    const size_t words_m = (size_t)(m / G) * JM_NDIG * (G / 8);
+    size_t sz[15] = {
+        (size_t)B * E * 4,            // logits
+        nslot * 4,                    // top
+        nslot * 4,                    // tw
+        (size_t)B * words_d * 4,      // xdig
+        (size_t)B * (d / G) * 4,      // xscale
+        (size_t)(E + 1) * 4,          // seg_off
+        nslot * 4,                    // seg_slot
+        (size_t)E * 4,                // active
+        4,                            // n_active
+        (size_t)E * 4,                // first_slot
+        nslot * 4,                    // rank
+        nslot * m * 4,                // act
+        nslot * words_m * 4,          // adig
+        nslot * (m / G) * 4,          // ascale
+        nslot * d * 4,                // y
+    };
+    size_t total = 0;
+    for (size_t v : sz) total += align256(v);
+    void* mem = nullptr;
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize before workspace growth");
+    JM_HIP(hipMalloc(&mem, total), "hipMalloc workspace");
+    if (s->ws) (void)hipFree(s->ws);
+    s->ws = mem;
+    char* p = (char*)mem;
+    void** slots[15] = {(void**)&s->logits, (void**)&s->top, (void**)&s->tw, (void**)&s->xdig,
+                        (void**)&s->xscale, (void**)&s->seg_off, (void**)&s->seg_slot,
+                        (void**)&s->active, (void**)&s->n_active, (void**)&s->first_slot,
+                        (void**)&s->rank, (void**)&s->act, (void**)&s->adig,
+                        (void**)&s->ascale, (void**)&s->y};
+    for (int i = 0; i < 15; i++) {
+        *slots[i] = p;
+        p += align256(sz[i]);
+    }
+    s->cap_B = B;
+    return 0;
+}
+
+int check_store(const jm_store* s) {
+    if (!s) return fail(JM_ERR_ARG, "store is NULL");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int jm_version(void) { return JM_ABI_VERSION; }
+
+const char* jm_last_error(void) { return g_err; }
+
+int jm_abi_sizes(int* kernel_cfg_bytes, int* ndig, int* nt) {
+    if (kernel_cfg_bytes) *kernel_cfg_bytes = (int)sizeof(jm_kernel_cfg);
+    if (ndig) *ndig = JM_NDIG;
+    if (nt) *nt = JM_NT;
+    return 0;
+}
+
+int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint64_t blob_bytes,
+                    const uint64_t* offsets, jm_store** out) {
+    if (!cfg || !blob || !offsets || !out) return fail(JM_ERR_ARG, "NULL argument to jm_store_create");
+    *out = nullptr;
+    const int L = cfg->L, E = cfg->E, d = cfg->d, m = cfg->intermediate, k = cfg->topk;
+    if (L <= 0 || E <= 0 || E > JM_MAX_E) return fail(JM_ERR_SHAPE, "need 0 < L and 0 < E <= %d (L=%d E=%d)", JM_MAX_E, L, E);
+    if (k <= 0 || k > E || k > JM_MAX_TOPK) return fail(JM_ERR_SHAPE, "need 0 < topk <= min(E, %d) (topk=%d)", JM_MAX_TOPK, k);
+    if (cfg->expert_i8 || cfg->expert_bf16)
+        return fail(JM_ERR_SHAPE, "only the Q4 expert store is supported (expert_i8/expert_bf16 set)");
+    if (int rc = check_group_shape(d, m, group)) return rc;
+    if (!aligned(blob, 16)) return fail(JM_ERR_ARG, "store blob must be 16-byte aligned");
+    // every record must lie inside the blob, with packed rows 16-byte aligned
+    const uint64_t sg = (uint64_t)m * d / group * 2, pg = (uint64_t)m * d / 2;
+    for (int p = 0; p < 3; p++)
+        for (int i = 0; i < L * E; i++) {
+            const uint64_t so = offsets[((size_t)p * L * E + i) * 2 + 0];
+            const uint64_t po = offsets[((size_t)p * L * E + i) * 2 + 1];
+            if (so % 2 || po % 16)
+                return fail(JM_ERR_ARG, "record %d of part %d is misaligned (scales %llu, packed %llu)",
+                            i, p, (unsigned long long)so, (unsigned long long)po);
+            if (so + sg > blob_bytes || po + pg > blob_bytes || so + sg < so || po + pg < po)
+                return fail(JM_ERR_ARG, "record %d of part %d lies outside the %llu-byte blob", i, p,
+                            (unsigned long long)blob_bytes);
+        }
+    hipPointerAttribute_t attr;
+    hipError_t pe = hipPointerGetAttributes(&attr, blob);
+    if (pe != hipSuccess || attr.type != hipMemoryTypeDevice) {
+        (void)hipGetLastError();
+        return fail(JM_ERR_ARG, "store blob must be device memory");
+    }
+    jm_store* s = new jm_store();
+    memset(s, 0, sizeof *s);
+    s->L = L; s->E = E; s->d = d; s->m = m; s->topk = k;
+    s->renorm = cfg->norm_topk_prob ? 1 : 0;
+    s->group = group;
+    s->blob = (const uint8_t*)blob;
+    s->blob_bytes = blob_bytes;
+    s->device = attr.device;
+    const size_t ob = (size_t)3 * L * E * 2 * sizeof(uint64_t);
+    hipError_t e = hipSetDevice(s->device);
+    if (e == hipSuccess) e = hipMalloc(&s->off_dev, ob);
+    if (e == hipSuccess) e = hipMemcpy(s->off_dev, offsets, ob, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (s->off_dev) (void)hipFree(s->off_dev);
+        delete s;
+        return hip_fail(e, "jm_store_create offset table");
+    }
+    *out = s;
+    return 0;
+}
+
+int jm_store_destroy(jm_store* s) {
+    if (!s) return 0;
+    (void)hipSetDevice(s->device);
+    (void)hipDeviceSynchronize();
+    if (s->off_dev) (void)hipFree(s->off_dev);
+    if (s->ws) (void)hipFree(s->ws);
+    delete s;
+    return 0;
+}
+
+int jm_store_set_router(jm_store* s, const void* gate_w, int dtype) {
+    if (int rc = check_store(s)) return rc;
+    if (!gate_w) return fail(JM_ERR_ARG, "router weights are NULL");
+    if (dtype != JM_DTYPE_F32 && dtype != JM_DTYPE_BF16) return fail(JM_ERR_ARG, "router dtype must be f32 or bf16");
+    if (!aligned(gate_w, 4)) return fail(JM_ERR_ARG, "router weights must be 4-byte aligned");
+    s->router = gate_w;
+    s->router_bf16 = dtype == JM_DTYPE_BF16;
+    return 0;
+}
+
+int jm_store_reserve(jm_store* s, int max_B) {
+    if (int rc = check_store(s)) return rc;
+    if (max_B < 0) return fail(JM_ERR_ARG, "max_B must be >= 0");
+    return reserve(s, max_B);
+}
+
+int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, int* group) {
+    if (int rc = check_store(s)) return rc;
+    if (L) *L = s->L;
+    if (E) *E = s->E;
+    if (d) *d = s->d;
+    if (m) *m = s->m;
+    if (topk) *topk = s->topk;
+    if (group) *group = s->group;
+    return 0;
+}
+
+int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out,
+                       int32_t* topk_idx, float* topk_w, void* stream) {
+    if (int rc = check_store(s)) return rc;
+    if (!s->router) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
+    if (layer < 0 || layer >= s->L) return fail(JM_ERR_ARG, "layer %d outside [0, %d)", layer, s->L);
+    if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
+    if (B == 0) return 0;
+    if (!x || !out) return fail(JM_ERR_ARG, "x and out must be non-NULL");
+    if (!aligned(x, 16) || !aligned(out, 16)) return fail(JM_ERR_ARG, "x and out must be 16-byte aligned");
+    if ((long long)B * s->topk > JM_MAX_SLOTS) return fail(JM_ERR_SHAPE, "B * topk must be <= %d", JM_MAX_SLOTS);
+    if (int rc = reserve(s, B)) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    const int E = s->E, d = s->d, k = s->topk, G = s->group;
+    const size_t rstride = (size_t)E * d * (s->router_bf16 ? 2 : 4);
+    const void* gw = (const char*)s->router + (size_t)layer * rstride;
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    JM_HIP(jm::launch_router(gw, s->router_bf16, x, s->logits, B, E, d, st), "router launch");
+    JM_HIP(jm::launch_topk(s->logits, B, E, k, s->renorm, s->top, s->tw, st), "top-k launch");
+    JM_HIP(jm::launch_dispatch(s->top, B * k, E, s->seg_off, s->seg_slot, s->active, s->n_active,
+                               s->first_slot, s->rank, st), "dispatch launch");
+    JM_HIP(jm::launch_prep_digits(x, d, B, d, G, s->xdig, s->xscale, st), "digit prep launch");
+    jm::ExpertArgs a;
+    a.blob = s->blob; a.off = s->off_dev; a.LE = s->L * E;
+    a.layer = layer; a.E = E; a.d = d; a.m = s->m; a.topk = k; a.group = G;
+    a.n_active = s->n_active; a.active = s->active; a.seg_off = s->seg_off; a.seg_slot = s->seg_slot;
+    a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
+    a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y;
+    const int umax = std::min(E, B * k);
+    JM_HIP(jm::launch_experts(a, umax, st), "expert launch");
+    JM_HIP(jm::launch_combine(s->y, s->top, s->first_slot, B, k, d, out, st), "combine launch");
+    s->last_B = B;
+    if (topk_idx) JM_HIP(hipMemcpyAsync(topk_idx, s->top, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k");
+    if (topk_w) JM_HIP(hipMemcpyAsync(topk_w, s->tw, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k weights");
+    return 0;
+}
+
+int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t bytes, void* stream) {
+    if (int rc = check_store(s)) return rc;
+    if (!dst) return fail(JM_ERR_ARG, "destination is NULL");
+    const size_t nslot = (size_t)s->last_B * s->topk;
+    const void* src = nullptr;
+    size_t cap = 0;
+    switch (field) {
+        case JM_WS_LOGITS: src = s->logits; cap = (size_t)s->last_B * s->E * 4; break;
+        case JM_WS_SEG_OFF: src = s->seg_off; cap = (size_t)(s->E + 1) * 4; break;
+        case JM_WS_SEG_SLOT: src = s->seg_slot; cap = nslot * 4; break;
+        case JM_WS_ACTIVE: src = s->active; cap = (size_t)s->E * 4; break;
+        case JM_WS_N_ACTIVE: src = s->n_active; cap = 4; break;
+        case JM_WS_FIRST_SLOT: src = s->first_slot; cap = (size_t)s->E * 4; break;
+        case JM_WS_ACT: src = s->act; cap = nslot * s->m * 4; break;
+        case JM_WS_Y: src = s->y; cap = nslot * s->d * 4; break;
+        default: return fail(JM_ERR_ARG, "unknown workspace field %d", field);
+    }
+    if (!src || s->last_B == 0) return fail(JM_ERR_ARG, "no call has run on this store yet");
+    if (bytes > cap) return fail(JM_ERR_ARG, "%llu bytes requested, field holds %zu", (unsigned long long)bytes, cap);
+    JM_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "workspace copy");
+    return 0;
+}
+
+int jm_router(const void* gate_w, int dtype, const float* x, int B, int E, int d, int topk,
+              int renorm, float* logits, int32_t* top, float* tw, void* stream) {
+    if (!gate_w || !x || !logits || !top || !tw) return fail(JM_ERR_ARG, "NULL argument to jm_router");
+    if (B < 0 || E <= 0 || E > JM_MAX_E || d <= 0 || d % 8 || topk <= 0 || topk > E || topk > JM_MAX_TOPK)
+        return fail(JM_ERR_SHAPE, "bad router shape (B=%d E=%d d=%d topk=%d)", B, E, d, topk);
+    if (B == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    JM_HIP(jm::launch_router(gate_w, dtype == JM_DTYPE_BF16, x, logits, B, E, d, st), "router launch");
+    JM_HIP(jm::launch_topk(logits, B, E, topk, renorm ? 1 : 0, top, tw, st), "top-k launch");
+    return 0;
+}
+
+int jm_dispatch(const int32_t* top, int nslot, int E, int32_t* seg_off, int32_t* seg_slot,
+                int32_t* active, int32_t* n_active, int32_t* first_slot, void* stream) {
+    if (!top || !seg_off || !seg_slot || !active || !n_active || !first_slot)
+        return fail(JM_ERR_ARG, "NULL argument to jm_dispatch");
+    if (nslot < 0 || nslot > JM_MAX_SLOTS || E <= 0 || E > JM_MAX_E)
+        return fail(JM_ERR_SHAPE, "need 0 <= nslot <= %d and 0 < E <= %d", JM_MAX_SLOTS, JM_MAX_E);
+    hipStream_t st = (hipStream_t)stream;
+    void* scratch = nullptr;
+    JM_HIP(hipMallocAsync(&scratch, align256((size_t)nslot * 4 + 4), st), "hipMallocAsync dispatch scratch");
+    hipError_t e = jm::launch_dispatch(top, nslot, E, seg_off, seg_slot, active, n_active, first_slot,
+                                       (int*)scratch, st);
+    hipError_t f = hipFreeAsync(scratch, st);
+    if (e != hipSuccess) return hip_fail(e, "dispatch launch");
+    if (f != hipSuccess) return hip_fail(f, "hipFreeAsync");
+    return 0;
+}
+
+int jm_q4_dequant(float* out, const uint8_t* packed, const uint16_t* scales, int64_t numel, int group,
+                  void* stream) {
+    if (!out || !packed || !scales) return fail(JM_ERR_ARG, "NULL argument to jm_q4_dequant");
+    if (group != 32 && group != 64) return fail(JM_ERR_SHAPE, "group must be 32 or 64");
+    if (numel < 0) return fail(JM_ERR_SHAPE, "numel must be >= 0");
+    JM_HIP(jm::launch_dequant(packed, scales, numel, group, out, (hipStream_t)stream), "dequant launch");
+    return 0;
+}
+
+int jm_q4_gemm_f32(float* out, const float* X, int T, const uint8_t* packed, const uint16_t* scales,
+                   int m, int d, int group, void* stream) {
+    if (!out || !X || !packed || !scales) return fail(JM_ERR_ARG, "NULL argument to jm_q4_gemm_f32");
+    if (group != 32 && group != 64) return fail(JM_ERR_SHAPE, "group must be 32 or 64");
+    if (T < 0 || m < 0 || d <= 0 || d % group) return fail(JM_ERR_SHAPE, "bad q4_gemm shape (T=%d m=%d d=%d)", T, m, d);
+    if (d / group > 64) return fail(JM_ERR_SHAPE, "d / group must be <= 64");
+    if ((d / 2) % 16) return fail(JM_ERR_SHAPE, "d must be a multiple of 32 (16-byte packed rows)");
+    if (!aligned(packed, 16) || !aligned(X, 16)) return fail(JM_ERR_ARG, "packed and X must be 16-byte aligned");
+    if (T == 0 || m == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    const size_t ng = (size_t)d / group;
+    const size_t dig_bytes = align256((size_t)T * ng * JM_NDIG * (group / 8) * 4);
+    const size_t sc_bytes = align256((size_t)T * ng * 4);
+    void* scratch = nullptr;
+    JM_HIP(hipMallocAsync(&scratch, dig_bytes + sc_bytes, st), "hipMallocAsync q4_gemm scratch");
+    uint32_t* dig = (uint32_t*)scratch;
+    float* dsc = (float*)((char*)scratch + dig_bytes);
+    hipError_t e = jm::launch_prep_digits(X, d, T, d, group, dig, dsc, st);
+    if (e == hipSuccess) e = jm::launch_q4_rows(packed, scales, m, d, group, dig, dsc, T, out, m, st);
+    hipError_t f = hipFreeAsync(scratch, st);
+    if (e != hipSuccess) return hip_fail(e, "q4_gemm launch");
+    if (f != hipSuccess) return hip_fail(f, "hipFreeAsync");
+    return 0;
+}
+
+int jm_q4_gemv_f32(float* out, const float* x, const uint8_t* packed, const uint16_t* scales,
+                   int m, int d, int group, void* stream) {
+    return jm_q4_gemm_f32(out, x, 1, packed, scales, m, d, group, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,228 @@
+"""HBM-resident Q4 expert store and the MoE decode block on the GPU.
+
+Host-side mirror of the reference's MoE call surface:
+
+* ``HbmExpertStore`` holds ``experts_q4.bin`` in device memory byte for byte
+  (the reference memory-maps it and builds pointer tables,
+  src/jouleai/native/decoder3.py:329-367).  ``ensure(l, e)`` returns the
+  same ``((scales, packed, numel) x 3)`` records as the raw
+  ``Q4ExpertPool.gather`` (src/jouleai/storage/q4_store.py:194-210), as
+  device views.
+* ``HbmExpertStore.layer_ffn_batch(l, x)`` is the reference's
+  ``layer_ffn_batch(cfg, W, l, x, B, out)``
+  (src/jouleai/native/decode_kernel.c:1387-1508) for one layer.
+
+PyTorch provides device memory and streams; the arithmetic is in
+libjoule_amd.so.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import _lib
+from .q4_store import BIN_NAME, INDEX_NAME, PARTS, Q4Index, record_sizes
+
+
+@dataclass(frozen=True)
+class MoEShape:
+    """MoE block shape: hidden d, intermediate m, experts E, top-k, renorm."""
+
+    d: int
+    m: int
+    E: int
+    topk: int
+    renorm: bool
+    name: str = ""
+
+    def kernel_cfg(self, n_layers: int) -> _lib.KernelCfg:
+        c = _lib.KernelCfg()
+        c.L, c.d, c.E, c.topk = n_layers, self.d, self.E, self.topk
+        c.intermediate = self.m
+        c.norm_topk_prob = int(self.renorm)
+        return c
+
+
+# Shapes of the reference's two MoE families (arch/registry.py:56-94 fills
+# the same fields from config.json).
+OLMOE = MoEShape(d=2048, m=1024, E=64, topk=8, renorm=False, name="olmoe-1b-7b")
+QWEN3 = MoEShape(d=2048, m=768, E=128, topk=8, renorm=True, name="qwen3-30b-a3b")
+
+
+def offsets_for_layout(shape: MoEShape, n_layers: int, group: int) -> tuple[np.ndarray, int]:
+    """(offset table [3, L*E, 2], total bytes) of a store written in the
+    reference order (layer, expert, part) with records [scales][packed]."""
+    sizes = [record_sizes(shape.m, shape.d, group), record_sizes(shape.m, shape.d, group),
+             record_sizes(shape.d, shape.m, group)]
+    per_expert = sum(a + b for a, b in sizes)
+    LE = n_layers * shape.E
+    tab = np.zeros((3, LE, 2), np.uint64)
+    base = np.arange(LE, dtype=np.uint64) * np.uint64(per_expert)
+    off = 0
+    for p, (sb, pb) in enumerate(sizes):
+        tab[p, :, 0] = base + np.uint64(off)
+        tab[p, :, 1] = base + np.uint64(off + sb)
+        off += sb + pb
+    return tab, per_expert * LE
+
+
+class HbmExpertStore:
+    """The Q4 expert store resident in HBM, plus its router table.
+
+    ``blob`` is a uint8 CUDA tensor holding the store file's bytes,
+    ``offsets`` the [3, L*E, 2] uint64 table of (scales offset, packed
+    offset) per (part, l*E+e).  The tensor stays referenced by this object.
+    """
+
+    def __init__(self, shape: MoEShape, n_layers: int, blob: torch.Tensor, offsets: np.ndarray,
+                 group: int = 64):
+        if blob.dtype != torch.uint8 or not blob.is_cuda or not blob.is_contiguous():
+            raise ValueError("blob must be a contiguous uint8 CUDA tensor")
+        self.shape, self.n_layers, self.group = shape, n_layers, group
+        self.blob = blob
+        self.offsets = np.ascontiguousarray(offsets, dtype=np.uint64).reshape(3, n_layers * shape.E, 2)
+        self._cfg = shape.kernel_cfg(n_layers)
+        handle = ctypes.c_void_p()
+        _lib.check(_lib.lib().jm_store_create(ctypes.byref(self._cfg), group, _lib.ptr(blob),
+                                              blob.numel(), _lib.ptr(self.offsets),
+                                              ctypes.byref(handle)), "jm_store_create")
+        self._h = handle
+        self.router: torch.Tensor | None = None
+
+    # ------------------------------------------------------------ loading
+
+    @classmethod
+    def from_dir(cls, store_dir: str | Path, shape: MoEShape, n_layers: int | None = None,
+                 device: str | torch.device = "cuda", chunk_bytes: int = 1 << 28) -> "HbmExpertStore":
+        """Upload ``experts_q4.bin`` (read in chunks) and index it."""
+        store_dir = Path(store_dir)
+        index = Q4Index.load(store_dir / INDEX_NAME)
+        L, E, _ = index.dims()
+        if E != shape.E:
+            raise ValueError(f"store has {E} experts, shape says {shape.E}")
+        n_layers = L if n_layers is None else n_layers
+        offsets = index.offset_table(n_layers, E)
+        path = store_dir / BIN_NAME
+        nbytes = path.stat().st_size
+        blob = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        with open(path, "rb") as f:
+            pos = 0
+            while pos < nbytes:
+                buf = f.read(min(chunk_bytes, nbytes - pos))
+                blob[pos:pos + len(buf)].copy_(torch.frombuffer(bytearray(buf), dtype=torch.uint8))
+                pos += len(buf)
+        return cls(shape, n_layers, blob, offsets, index.group)
+
+    def set_router(self, gate_w: torch.Tensor) -> None:
+        """Router table [L, E, d] (float32, or bfloat16 as in the reference)."""
+        s = self.shape
+        if tuple(gate_w.shape) != (self.n_layers, s.E, s.d):
+            raise ValueError(f"router must be [{self.n_layers}, {s.E}, {s.d}]")
+        if not gate_w.is_cuda or not gate_w.is_contiguous():
+            raise ValueError("router must be a contiguous CUDA tensor")
+        if gate_w.dtype == torch.float32:
+            dt = _lib.JM_DTYPE_F32
+        elif gate_w.dtype == torch.bfloat16:
+            dt = _lib.JM_DTYPE_BF16
+        else:
+            raise ValueError("router dtype must be float32 or bfloat16")
+        _lib.check(_lib.lib().jm_store_set_router(self._h, _lib.ptr(gate_w), dt), "jm_store_set_router")
+        self.router = gate_w
+
+    def reserve(self, max_B: int) -> None:
+        _lib.check(_lib.lib().jm_store_reserve(self._h, int(max_B)), "jm_store_reserve")
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            _lib.lib().jm_store_destroy(self._h)
+            self._h = None
+
+    def __del__(self):  # pragma: no cover - best effort at interpreter exit
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------- store surface
+
+    def expert_size_bytes(self, l: int, e: int) -> int:
+        s = self.shape
+        return sum(sum(record_sizes(r, c, self.group)) for r, c in ((s.m, s.d), (s.m, s.d), (s.d, s.m)))
+
+    def ensure(self, l: int, e: int):
+        """((scales int16 view, packed uint8 view, numel) for gate, up, down)
+        as device views, like the raw Q4ExpertPool.gather (q4_store.py:194-210)."""
+        s = self.shape
+        key = l * s.E + e
+        outs = []
+        for p, (rows, cols) in enumerate(((s.m, s.d), (s.m, s.d), (s.d, s.m))):
+            sb, pb = record_sizes(rows, cols, self.group)
+            so, po = (int(v) for v in self.offsets[p, key])
+            outs.append((self.blob[so:so + sb].view(torch.int16), self.blob[po:po + pb], rows * cols))
+        return tuple(outs)
+
+    # --------------------------------------------------------- the block
+
+    def layer_ffn_batch(self, l: int, x: torch.Tensor, out: torch.Tensor | None = None,
+                        topk_idx: torch.Tensor | None = None, topk_w: torch.Tensor | None = None,
+                        stream=None) -> torch.Tensor:
+        """out[B, d] = MoE block of layer l on x[B, d] (float32, CUDA)."""
+        if self.router is None:
+            raise RuntimeError("router weights not set (set_router)")
+        if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or x.dim() != 2:
+            raise ValueError("x must be a contiguous float32 CUDA tensor [B, d]")
+        B = x.shape[0]
+        if out is None:
+            out = torch.empty_like(x)
+        for t, dt in ((topk_idx, torch.int32), (topk_w, torch.float32)):
+            if t is not None and (t.dtype != dt or t.numel() != B * self.shape.topk or not t.is_contiguous()):
+                raise ValueError("topk outputs must be contiguous [B, topk] int32 / float32")
+        _lib.check(_lib.lib().jm_layer_ffn_batch(self._h, int(l), _lib.ptr(x), B, _lib.ptr(out),
+                                                 _lib.ptr(topk_idx), _lib.ptr(topk_w),
+                                                 _lib.stream_handle(stream)), "jm_layer_ffn_batch")
+        return out
+
+    def read_workspace(self, B: int, stream=None) -> dict:
+        """Host copies of the last call's dispatch and per-slot intermediates."""
+        s = self.shape
+        nslot = B * s.topk
+        dev = self.blob.device
+
+        def grab(field, shape, dtype):
+            t = torch.empty(shape, dtype=dtype, device=dev)
+            _lib.check(_lib.lib().jm_store_copy_workspace(self._h, field, _lib.ptr(t),
+                                                          t.numel() * t.element_size(),
+                                                          _lib.stream_handle(stream)),
+                       "jm_store_copy_workspace")
+            return t
+
+        res = {
+            "logits": grab(_lib.WS_LOGITS, (B, s.E), torch.float32),
+            "seg_off": grab(_lib.WS_SEG_OFF, (s.E + 1,), torch.int32),
+            "seg_slot": grab(_lib.WS_SEG_SLOT, (nslot,), torch.int32),
+            "active": grab(_lib.WS_ACTIVE, (s.E,), torch.int32),
+            "n_active": grab(_lib.WS_N_ACTIVE, (1,), torch.int32),
+            "first_slot": grab(_lib.WS_FIRST_SLOT, (s.E,), torch.int32),
+            "act": grab(_lib.WS_ACT, (nslot, s.m), torch.float32),
+            "y": grab(_lib.WS_Y, (nslot, s.d), torch.float32),
+        }
+        torch.cuda.synchronize(dev)
+        res = {k: v.cpu() for k, v in res.items()}
+        res["active"] = res["active"][: int(res["n_active"][0])]
+        return res
+
+
+def algorithmic_bytes(shape: MoEShape, group: int, B: int, n_active: int, router_bytes: int = 4) -> int:
+    """Bytes one block call must move: the routed experts' Q4 records, the
+    router table and x in / out (top-k outputs are negligible)."""
+    s = shape
+    eb = sum(sum(record_sizes(r, c, group)) for r, c in ((s.m, s.d), (s.m, s.d), (s.d, s.m)))
+    return n_active * eb + s.E * s.d * router_bytes + 2 * B * s.d * 4
+
+
+PART_NAMES = PARTS

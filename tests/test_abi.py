@@ -1,0 +1,95 @@
+"""The C ABI library loads and exports what include/joule_amd.h declares.
+
+CPU-only: no call here launches GPU work.  Argument and shape errors are
+checked before any HIP call, so they are exercised here as well.
+"""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from joule_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "joule_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(jm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_header_symbols():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libjoule_amd.so not built (run python -m joule_amd.build)")
+    syms = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                          text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (jm_[a-z0-9_]+)", syms))
+    declared = _declared()
+    assert declared, "no declarations parsed"
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+    # the ctypes table covers every declared function
+    assert set(declared) == set(_lib.SIGNATURES)
+    L = _lib.lib()
+    for name in declared:
+        assert hasattr(L, name)
+
+
+def test_kernel_cfg_layout():
+    # KernelCfg of decode_kernel.c:269-286: 15 ints and one float, 64 bytes,
+    # eps at byte 32 and norm_topk_prob at byte 52 (decoder3.py:35-46)
+    assert ctypes.sizeof(_lib.KernelCfg) == 64
+    assert _lib.KernelCfg.eps.offset == 32
+    assert _lib.KernelCfg.intermediate.offset == 40
+    assert _lib.KernelCfg.norm_topk_prob.offset == 52
+    assert _lib.KernelCfg.expert_bf16.offset == 60
+    if _lib.LIB_PATH.exists():
+        n, ndig, nt = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        assert _lib.lib().jm_abi_sizes(ctypes.byref(n), ctypes.byref(ndig), ctypes.byref(nt)) == 0
+        assert n.value == 64 and 3 <= ndig.value <= 5 and nt.value >= 1
+        assert _lib.lib().jm_version() == 1
+
+
+def _cfg(**kw):
+    c = _lib.KernelCfg()
+    c.L, c.d, c.E, c.topk, c.intermediate, c.norm_topk_prob = 2, 2048, 128, 8, 768, 1
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+@pytest.mark.parametrize("kw,group,code", [
+    (dict(topk=0), 64, -2), (dict(topk=129), 64, -2), (dict(E=0), 64, -2),
+    (dict(E=513), 64, -2), (dict(d=2000), 64, -2), (dict(intermediate=700), 64, -2),
+    (dict(d=8192), 64, -2), (dict(expert_i8=1), 64, -2), ({}, 48, -2),
+])
+def test_store_create_rejects_bad_shapes(kw, group, code):
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libjoule_amd.so not built")
+    L = _lib.lib()
+    cfg = _cfg(**kw)
+    offs = np.zeros(16, np.uint64)
+    h = ctypes.c_void_p()
+    rc = L.jm_store_create(ctypes.byref(cfg), group, ctypes.c_void_p(4096), 1 << 20,
+                           offs.ctypes.data, ctypes.byref(h))
+    assert rc == code
+    assert L.jm_last_error()
+    assert h.value is None
+
+
+def test_null_arguments_are_errors():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libjoule_amd.so not built")
+    L = _lib.lib()
+    assert L.jm_store_create(None, 64, None, 0, None, None) == -1
+    assert L.jm_layer_ffn_batch(None, 0, None, 1, None, None, None, None) == -1
+    assert L.jm_q4_gemm_f32(None, None, 1, None, None, 1, 64, 64, None) == -1
+    assert L.jm_store_destroy(None) == 0
+    with pytest.raises(_lib.JouleError):
+        _lib.check(L.jm_store_reserve(None, 4), "reserve")

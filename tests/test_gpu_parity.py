@@ -1,0 +1,296 @@
+"""GPU parity: the HIP path through the C ABI against the oracle.
+
+Bars (tolerances written here, from the target statement):
+* dequantised weights: bit-exact;
+* router logits, top-k indices and routing weights: bit-exact;
+* block outputs: max |gpu - oracle| / max |oracle| <= 1e-3 per token, fp32
+  accumulate (measured values are printed; expected ~1e-5);
+* dispatch: identical to a stable sort by expert id.
+Full-size layers (OLMoE and Qwen3-30B-A3B shapes) are generated and
+quantised on the GPU, copied to the host for the oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import banner
+from joule_amd import _lib
+from joule_amd import q4_store as Q
+from joule_amd.backend import HipBackend, q4_dequant
+from joule_amd.moe import OLMOE, QWEN3, HbmExpertStore, MoEShape
+from joule_amd.synth import (activations, apply_logit_bias, quantize_torch, router_weights,
+                             torch_store, zipf_bias)
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+class Layer:
+    """A full-size synthetic store on the GPU plus its host copy and oracle."""
+
+    def __init__(self, shape: MoEShape, group: int, n_layers: int, oracle_lib):
+        banner(f"build store {shape.name} G{group} L{n_layers}")
+        self.shape, self.group, self.L = shape, group, n_layers
+        blob, offsets = torch_store(shape, n_layers, group)
+        self.store = HbmExpertStore(shape, n_layers, blob, offsets, group)
+        self.gw = np.stack([router_weights(shape, l) for l in range(n_layers)])
+        self.store.set_router(torch.from_numpy(self.gw).cuda())
+        self.host = blob.cpu().numpy()
+        self.offsets = offsets
+        self.O = oracle_lib
+
+    def oracle(self, l: int, gw=None):
+        s = self.shape
+        offs = self.offsets[:, l * s.E:(l + 1) * s.E]
+        return self.O.OracleMoE(s.d, s.m, s.E, s.topk, s.renorm, self.group,
+                                self.gw[l] if gw is None else gw, self.host, offs)
+
+
+@pytest.fixture(scope="module")
+def qwen64(gpu, oracle_lib):
+    return Layer(QWEN3, 64, 2, oracle_lib)
+
+
+@pytest.fixture(scope="module")
+def olmoe64(gpu, oracle_lib):
+    return Layer(OLMOE, 64, 1, oracle_lib)
+
+
+@pytest.fixture(scope="module")
+def qwen32(gpu, oracle_lib):
+    return Layer(QWEN3, 32, 1, oracle_lib)
+
+
+def _rel(a, b):
+    den = np.abs(b).max(axis=1)
+    return float((np.abs(a - b).max(axis=1) / np.maximum(den, 1e-30)).max())
+
+
+def _run_block(layer: Layer, l: int, x: np.ndarray):
+    s = layer.shape
+    B = x.shape[0]
+    xd = torch.from_numpy(x).cuda()
+    top = torch.empty((B, s.topk), dtype=torch.int32, device="cuda")
+    tw = torch.empty((B, s.topk), dtype=torch.float32, device="cuda")
+    out = layer.store.layer_ffn_batch(l, xd, topk_idx=top, topk_w=tw)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), top.cpu().numpy(), tw.cpu().numpy()
+
+
+# ------------------------------------------------------------------ format
+
+def test_quantize_torch_matches_numpy(gpu):
+    banner("quantize_torch vs numpy")
+    rng = np.random.default_rng(9)
+    for group in (64, 32):
+        w = rng.normal(0, 0.02, (4, 96 * 256)).astype(np.float32)
+        w[0, :group] = 0.0                      # an all-zero group
+        sc, pk = quantize_torch(torch.from_numpy(w).cuda(), group)
+        sb, pb = Q.quantize(w, group)
+        assert sc.cpu().numpy().view(np.uint16).tobytes() == sb
+        assert pk.cpu().numpy().tobytes() == pb
+
+
+def test_dequant_bitexact_store(qwen64):
+    banner("dequant store records")
+    s = qwen64.shape
+    for (l, e, p) in [(0, 0, 0), (0, 77, 1), (1, 127, 2)]:
+        sc, pk, numel = qwen64.store.ensure(l, e)[p]
+        got = q4_dequant(pk, sc, numel, 64).cpu().numpy()
+        ref = Q.dequantize(sc.cpu().numpy().view(np.uint16), pk.cpu().numpy(), numel, 64)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_all_fp16_scales(gpu):
+    banner("dequant exhaustive fp16 scales")
+    codes = np.arange(65536, dtype=np.uint16)
+    for group in (64, 32):
+        sc = torch.from_numpy(codes.view(np.int16).copy()).cuda()
+        pk = torch.full((65536 * group // 2,), 0x99, dtype=torch.uint8, device="cuda")  # q - 8 = +1
+        got = q4_dequant(pk, sc, 65536 * group, group).cpu().numpy().reshape(65536, group)
+        assert np.all(got.view(np.uint32) == got[:, :1].view(np.uint32))
+        ref = codes.view(np.float16).astype(np.float32)
+        nan = np.isnan(ref)
+        assert np.array_equal(got[~nan, 0].view(np.uint32), ref[~nan].view(np.uint32))
+        assert np.all(np.isnan(got[nan, 0]))
+
+
+# ------------------------------------------------------------------ router
+
+def _gpu_router(gw: np.ndarray, x: np.ndarray, topk: int, renorm: bool, bf16=False):
+    B, d = x.shape
+    E = gw.shape[0]
+    w = torch.from_numpy(gw).cuda()
+    if bf16:
+        w = w.to(torch.bfloat16)
+    xd = torch.from_numpy(x).cuda()
+    logits = torch.empty((B, E), dtype=torch.float32, device="cuda")
+    top = torch.empty((B, topk), dtype=torch.int32, device="cuda")
+    tw = torch.empty((B, topk), dtype=torch.float32, device="cuda")
+    _lib.check(_lib.lib().jm_router(_lib.ptr(w), int(bf16), _lib.ptr(xd), B, E, d, topk, int(renorm),
+                                    _lib.ptr(logits), _lib.ptr(top), _lib.ptr(tw), _lib.stream_handle()))
+    torch.cuda.synchronize()
+    return logits.cpu().numpy(), top.cpu().numpy(), tw.cpu().numpy()
+
+
+@pytest.mark.parametrize("shape", [QWEN3, OLMOE], ids=lambda s: s.name)
+@pytest.mark.parametrize("B", [1, 8, 32, 512])
+def test_router_bitexact(gpu, oracle_lib, shape, B):
+    banner(f"router {shape.name} B={B}")
+    gw = router_weights(shape, 0)
+    x = activations(B, shape.d)
+    lg, top, tw = _gpu_router(gw, x, shape.topk, shape.renorm)
+    rl, rtop, rtw = oracle_lib.route(gw, x, shape.topk, shape.renorm)
+    assert np.array_equal(lg.view(np.uint32), rl.view(np.uint32))
+    assert np.array_equal(top, rtop)
+    assert np.array_equal(tw.view(np.uint32), rtw.view(np.uint32))
+    lg2, top2, tw2 = _gpu_router(gw, x, shape.topk, shape.renorm, bf16=True)
+    assert np.array_equal(lg2.view(np.uint32), lg.view(np.uint32)) and np.array_equal(top2, top)
+
+
+def test_router_ties_lowest_index(gpu, oracle_lib):
+    banner("router ties")
+    E, d, k = 64, 256, 6
+    gw = router_weights(MoEShape(d=d, m=64, E=E, topk=k, renorm=True), 0)
+    gw[[3, 17, 40, 63]] = gw[50]               # four experts with identical rows
+    gw[[5, 9]] = gw[60] * 0                    # zero rows tie with each other
+    x = activations(5, d)
+    x[:, :] = np.abs(x)                        # make row 50 likely in the top-k
+    gw[50] = np.abs(gw[50]) * 3
+    gw[[3, 17, 40, 63]] = gw[50]
+    lg, top, tw = _gpu_router(gw, x, k, True)
+    rl, rtop, rtw = oracle_lib.route(gw, x, k, True)
+    assert np.array_equal(top, rtop) and np.array_equal(tw.view(np.uint32), rtw.view(np.uint32))
+    for b in range(5):
+        sel = top[b].tolist()
+        assert sel[:5] == [3, 17, 40, 50, 63]   # equal probabilities, lowest index first
+
+
+# ---------------------------------------------------------------- dispatch
+
+@pytest.mark.parametrize("B,E,k", [(1, 128, 8), (8, 128, 8), (8, 64, 8), (512, 128, 8), (3, 16, 4)])
+def test_dispatch_stable_sort(gpu, B, E, k):
+    banner(f"dispatch B={B} E={E}")
+    rng = np.random.default_rng(B * 31 + E)
+    top = np.stack([rng.permutation(E)[:k] for _ in range(B)]).astype(np.int32)
+    if B >= 8:
+        top[1, 2] = -1                         # a slot without an expert (NaN scores)
+    t = torch.from_numpy(top.ravel()).cuda()
+    outs = [torch.full((n,), -7, dtype=torch.int32, device="cuda") for n in (E + 1, B * k, E, 1, E)]
+    _lib.check(_lib.lib().jm_dispatch(_lib.ptr(t), B * k, E, *[_lib.ptr(o) for o in outs],
+                                      _lib.stream_handle()))
+    torch.cuda.synchronize()
+    seg_off, seg_slot, active, n_active, first_slot = (o.cpu().numpy() for o in outs)
+    flat = top.ravel()
+    valid = np.where(flat >= 0)[0]
+    order = valid[np.argsort(flat[valid], kind="stable")]
+    assert np.array_equal(seg_slot[:len(order)], order)
+    counts = np.bincount(flat[valid], minlength=E)
+    assert np.array_equal(seg_off, np.concatenate([[0], np.cumsum(counts)]))
+    act = np.where(counts > 0)[0]
+    assert n_active[0] == len(act) and np.array_equal(active[:len(act)], act)
+    for e in act:
+        assert first_slot[e] == order[seg_off[e]]
+
+
+# ------------------------------------------------------------------- block
+
+CASES = [("olmoe64", 1), ("olmoe64", 8), ("qwen64", 1), ("qwen64", 8), ("qwen64", 32),
+         ("qwen32", 1), ("qwen32", 8)]
+
+
+@pytest.mark.parametrize("which,B", CASES)
+def test_block_parity(request, which, B):
+    layer = request.getfixturevalue(which)
+    banner(f"block {which} B={B}")
+    x = activations(B, layer.shape.d)
+    out, top, tw = _run_block(layer, 0, x)
+    rout, rtop, rtw = layer.oracle(0).forward(x)
+    assert np.array_equal(top, rtop)
+    assert np.array_equal(tw.view(np.uint32), rtw.view(np.uint32))
+    err = _rel(out, rout)
+    print(f"  max rel err {which} B={B}: {err:.3e}", flush=True)
+    assert err <= TOL
+
+
+def test_block_second_layer_and_determinism(qwen64):
+    banner("block layer 1, determinism")
+    x = activations(8, QWEN3.d)
+    a = _run_block(qwen64, 1, x)
+    b = _run_block(qwen64, 1, x)
+    for u, v in zip(a, b):
+        assert np.array_equal(u.view(np.uint8), v.view(np.uint8))
+    rout, rtop, rtw = qwen64.oracle(1).forward(x)
+    assert np.array_equal(a[1], rtop) and _rel(a[0], rout) <= TOL
+    c = _run_block(qwen64, 0, x)
+    assert not np.array_equal(a[1], c[1])
+
+
+def test_block_batch_invariance(qwen64):
+    banner("block batch invariance")
+    x = activations(8, QWEN3.d)
+    full = _run_block(qwen64, 0, x)
+    for t in (0, 5):
+        one = _run_block(qwen64, 0, x[t:t + 1])
+        assert np.array_equal(one[1][0], full[1][t])
+        assert np.array_equal(one[2][0].view(np.uint32), full[2][t].view(np.uint32))
+        assert np.abs(one[0][0] - full[0][t]).max() <= 1e-6 * np.abs(one[0][0]).max()
+
+
+def test_block_zipf_large_segments(qwen64):
+    """512 tokens with Zipf-biased routing: segments of 0 to ~200 tokens."""
+    banner("block zipf B=512")
+    s = QWEN3
+    B = 512
+    gw, x = apply_logit_bias(qwen64.gw[0], activations(B, s.d), zipf_bias(s.E, alpha=1.0))
+    w = torch.from_numpy(np.stack([gw, qwen64.gw[1]])).cuda()
+    qwen64.store.set_router(w)
+    try:
+        out, top, tw = _run_block(qwen64, 0, x)
+    finally:
+        qwen64.store.set_router(torch.from_numpy(qwen64.gw).cuda())
+    counts = np.bincount(top.ravel(), minlength=s.E)
+    print(f"  segment sizes: max {counts.max()} nonzero {np.count_nonzero(counts)}", flush=True)
+    assert counts.max() >= 64
+    rout, rtop, rtw = qwen64.oracle(0, gw=gw).forward(x)
+    assert np.array_equal(top, rtop)
+    err = _rel(out, rout)
+    print(f"  max rel err zipf B=512: {err:.3e}", flush=True)
+    assert err <= TOL
+
+
+def test_block_empty_and_errors(qwen64):
+    banner("block B=0 and argument errors")
+    s = QWEN3
+    x = torch.zeros((0, s.d), dtype=torch.float32, device="cuda")
+    out = qwen64.store.layer_ffn_batch(0, x)
+    assert out.shape == (0, s.d)
+    with pytest.raises(_lib.JouleError):
+        qwen64.store.layer_ffn_batch(2, torch.zeros((1, s.d), device="cuda"))
+    with pytest.raises(_lib.JouleError):
+        bad = torch.zeros(s.d + 1, device="cuda")[1:].view(1, s.d)
+        qwen64.store.layer_ffn_batch(0, bad)
+
+
+# ----------------------------------------------------------------- backend
+
+@pytest.mark.parametrize("group", [64, 32])
+@pytest.mark.parametrize("m,d,T", [(768, 2048, 1), (2048, 768, 3), (1024, 2048, 7)])
+def test_hip_backend_q4_gemm(gpu, oracle_lib, group, m, d, T):
+    banner(f"HipBackend q4_gemm m={m} d={d} T={T} G{group}")
+    rng = np.random.default_rng(m + d + T)
+    w = rng.normal(0, 0.02, (m, d)).astype(np.float32)
+    sb, pb = Q.quantize(w, group)
+    sc = np.frombuffer(sb, np.uint16).copy()
+    pk = np.frombuffer(pb, np.uint8).copy()
+    X = rng.standard_normal((T, d)).astype(np.float32)
+    be = HipBackend()
+    out = torch.empty((T, m), dtype=torch.float32, device="cuda")
+    be.q4_gemm(out, torch.from_numpy(X).cuda(), pk, sc, m, d, group)
+    ref = oracle_lib.q4_gemm_ffn(X, pk, sc, m, d, group)
+    torch.cuda.synchronize()
+    assert _rel(out.cpu().numpy(), ref) <= TOL
+    v = be.q4_gemv(torch.from_numpy(X[0]).cuda(), pk, sc, m, d, group).cpu().numpy()
+    assert _rel(v[None], ref[:1]) <= TOL
