@@ -90,7 +90,9 @@ int jm_store_destroy(jm_store* s);
 
 /* Router weights, the reference's KernelW.gate_w [L][E][d]
  * (decode_kernel.c:303).  dtype JM_DTYPE_BF16 takes the reference's bf16
- * table as is; JM_DTYPE_F32 takes float32.  Device memory, caller-owned. */
+ * table as is; JM_DTYPE_F32 takes float32.  The store keeps its own float32
+ * copy laid out residue-major (w[e][r][t] = gate_w[e][8t + r]); the caller's
+ * table may be freed after the call.  Synchronises the device. */
 int jm_store_set_router(jm_store* s, const void* gate_w, int dtype);
 
 /* Size the workspace for batches of up to max_B tokens now, so that later
@@ -110,6 +112,14 @@ int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, 
  */
 int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out,
                        int32_t* topk_idx, float* topk_w, void* stream);
+
+/* Per-stage timing.  With profiling on, jm_layer_ffn_batch records a HIP
+ * event around each of its JM_STAGES stages (route: router scores + digits,
+ * then top-k + dispatch; gate/up; down; combine); jm_store_stage_ms waits
+ * for the last call and returns the elapsed milliseconds of each stage. */
+#define JM_STAGES 4
+int jm_store_profile(jm_store* s, int enable);
+int jm_store_stage_ms(jm_store* s, float* ms, int n);
 
 /* Copy an intermediate of the last jm_layer_ffn_batch call out of the
  * store's workspace into caller device memory (stream-ordered), for tests and
@@ -141,9 +151,10 @@ int jm_router(const void* gate_w, int dtype, const float* x, int B, int E, int d
 
 /* Token-to-expert dispatch (decode_kernel.c:1449-1485) as a stable counting
  * sort by expert id: seg_off [E+1], seg_slot [nslot], active [E],
- * n_active [1], first_slot [E]. */
-int jm_dispatch(const int32_t* top, int nslot, int E, int32_t* seg_off, int32_t* seg_slot,
-                int32_t* active, int32_t* n_active, int32_t* first_slot, void* stream);
+ * n_active [1], first_slot [E], and comb [nslot]: each token's slots in the
+ * reference's union order (first appearance of their expert), -1 padded. */
+int jm_dispatch(const int32_t* top, int nslot, int E, int topk, int32_t* seg_off, int32_t* seg_slot,
+                int32_t* active, int32_t* n_active, int32_t* first_slot, int32_t* comb, void* stream);
 
 /* Exact dequantisation (q - 8) * float(scale) of one record
  * (q4_store.py:58-67 _dequantize). */

@@ -30,8 +30,10 @@ SIGNATURES = {
     "jm_store_info": ([_vp] + [_vp] * 6, _i),
     "jm_layer_ffn_batch": ([_vp, _i, _vp, _i, _vp, _vp, _vp, _vp], _i),
     "jm_store_copy_workspace": ([_vp, _i, _vp, _u64, _vp], _i),
+    "jm_store_profile": ([_vp, _i], _i),
+    "jm_store_stage_ms": ([_vp, _vp, _i], _i),
     "jm_router": ([_vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp], _i),
-    "jm_dispatch": ([_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp], _i),
+    "jm_dispatch": ([_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "jm_q4_dequant": ([_vp, _vp, _vp, _i64, _i, _vp], _i),
     "jm_q4_gemv_f32": ([_vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
     "jm_q4_gemm_f32": ([_vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
@@ -45,6 +47,8 @@ class KernelCfg(ctypes.Structure):
                 ("intermediate", _i), ("qk_norm_type", _i), ("bias_qkv", _i),
                 ("norm_topk_prob", _i), ("expert_i8", _i), ("expert_bf16", _i)]
 
+
+STAGES = ("route", "gateup", "down", "combine")
 
 # jm_store_copy_workspace fields
 WS_LOGITS, WS_SEG_OFF, WS_SEG_SLOT, WS_ACTIVE, WS_N_ACTIVE, WS_FIRST_SLOT, WS_ACT, WS_Y = range(8)

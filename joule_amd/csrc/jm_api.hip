@@ -51,6 +51,8 @@ int check_group_shape(int d, int m, int group) {
     const int lpr = d / group;
     if (lpr != 16 && lpr != 32 && lpr != 64)
         return fail(JM_ERR_SHAPE, "d / group must be 16, 32 or 64 (got %d)", lpr);
+    if (d % 512 || (d / 512 != 1 && d / 512 != 2 && d / 512 != 3 && d / 512 != 4 && d / 512 != 6 && d / 512 != 8))
+        return fail(JM_ERR_SHAPE, "d must be 512, 1024, 1536, 2048, 3072 or 4096 (got %d)", d);
     if (m / group > 64) return fail(JM_ERR_SHAPE, "intermediate / group must be <= 64 (got %d)", m / group);
     if (m % 64) return fail(JM_ERR_SHAPE, "intermediate must be a multiple of 64 (got %d)", m);
     if (d % 128) return fail(JM_ERR_SHAPE, "d must be a multiple of 128 (got %d)", d);
@@ -64,8 +66,7 @@ struct jm_store {
     const uint8_t* blob;
     uint64_t blob_bytes;
     uint64_t* off_dev;          // [3][L*E][2]
-    const void* router;         // [L][E][d]
-    int router_bf16;
+    float* wt;                  // [L][E][8][d/8] residue-major copy of the router table
     int device;
     // workspace, sized for cap_B tokens; last_B = B of the last call
     int cap_B;
@@ -82,7 +83,12 @@ struct jm_store {
     int* n_active;
     int* first_slot;
     int* rank;
+    int* comb;
+    jm::ExpertWork* work;
     float* act;
+    // optional per-stage events (jm_store_profile)
+    int prof;
+    hipEvent_t ev[JM_STAGES + 1];
     uint32_t* adig;
     float* ascale;
     float* y;
@@ -96,7 +102,7 @@ int reserve(jm_store* s, int B) {
     const size_t nslot = (size_t)B * k;
     const size_t words_d = (size_t)(d / G) * JM_NDIG * (G / 8);
     const size_t words_m = (size_t)(m / G) * JM_NDIG * (G / 8);
-    size_t sz[15] = {
+    size_t sz[19] = {
         (size_t)B * E * 4,            // logits
         nslot * 4,                    // top
         nslot * 4,                    // tw
@@ -108,6 +114,9 @@ int reserve(jm_store* s, int B) {
         4,                            // n_active
         (size_t)E * 4,                // first_slot
         nslot * 4,                    // rank
+        nslot * 4,                    // comb
+        (size_t)E * sizeof(jm::ExpertWork),   // work table
+        0, 0,
         nslot * m * 4,                // act
         nslot * words_m * 4,          // adig
         nslot * (m / G) * 4,          // ascale
@@ -122,15 +131,18 @@ int reserve(jm_store* s, int B) {
     if (s->ws) (void)hipFree(s->ws);
     s->ws = mem;
     char* p = (char*)mem;
-    void** slots[15] = {(void**)&s->logits, (void**)&s->top, (void**)&s->tw, (void**)&s->xdig,
+    void** slots[19] = {(void**)&s->logits, (void**)&s->top, (void**)&s->tw, (void**)&s->xdig,
                         (void**)&s->xscale, (void**)&s->seg_off, (void**)&s->seg_slot,
                         (void**)&s->active, (void**)&s->n_active, (void**)&s->first_slot,
-                        (void**)&s->rank, (void**)&s->act, (void**)&s->adig,
+                        (void**)&s->rank, (void**)&s->comb, (void**)&s->work, nullptr,
+                        nullptr, (void**)&s->act, (void**)&s->adig,
                         (void**)&s->ascale, (void**)&s->y};
-    for (int i = 0; i < 15; i++) {
-        *slots[i] = p;
+    for (int i = 0; i < 19; i++) {
+        if (slots[i]) *slots[i] = p;
         p += align256(sz[i]);
     }
+    JM_HIP(hipMemset(mem, 0, total), "hipMemset workspace");
+    JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize after workspace clear");
     s->cap_B = B;
     return 0;
 }
@@ -211,7 +223,10 @@ int jm_store_destroy(jm_store* s) {
     (void)hipSetDevice(s->device);
     (void)hipDeviceSynchronize();
     if (s->off_dev) (void)hipFree(s->off_dev);
+    if (s->wt) (void)hipFree(s->wt);
     if (s->ws) (void)hipFree(s->ws);
+    if (s->prof)
+        for (int i = 0; i <= JM_STAGES; i++) (void)hipEventDestroy(s->ev[i]);
     delete s;
     return 0;
 }
@@ -221,8 +236,12 @@ int jm_store_set_router(jm_store* s, const void* gate_w, int dtype) {
     if (!gate_w) return fail(JM_ERR_ARG, "router weights are NULL");
     if (dtype != JM_DTYPE_F32 && dtype != JM_DTYPE_BF16) return fail(JM_ERR_ARG, "router dtype must be f32 or bf16");
     if (!aligned(gate_w, 4)) return fail(JM_ERR_ARG, "router weights must be 4-byte aligned");
-    s->router = gate_w;
-    s->router_bf16 = dtype == JM_DTYPE_BF16;
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    const size_t n = (size_t)s->L * s->E * s->d;
+    if (!s->wt) JM_HIP(hipMalloc(&s->wt, n * sizeof(float)), "hipMalloc router copy");
+    JM_HIP(jm::launch_router_transpose(gate_w, dtype == JM_DTYPE_BF16, s->wt, (long long)s->L * s->E, s->d,
+                                       nullptr), "router transpose launch");
+    JM_HIP(hipDeviceSynchronize(), "router transpose");
     return 0;
 }
 
@@ -246,7 +265,7 @@ int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, 
 int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out,
                        int32_t* topk_idx, float* topk_w, void* stream) {
     if (int rc = check_store(s)) return rc;
-    if (!s->router) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
+    if (!s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
     if (layer < 0 || layer >= s->L) return fail(JM_ERR_ARG, "layer %d outside [0, %d)", layer, s->L);
     if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
     if (B == 0) return 0;
@@ -256,26 +275,58 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     if (int rc = reserve(s, B)) return rc;
     hipStream_t st = (hipStream_t)stream;
     const int E = s->E, d = s->d, k = s->topk, G = s->group;
-    const size_t rstride = (size_t)E * d * (s->router_bf16 ? 2 : 4);
-    const void* gw = (const char*)s->router + (size_t)layer * rstride;
     JM_HIP(hipSetDevice(s->device), "hipSetDevice");
-    JM_HIP(jm::launch_router(gw, s->router_bf16, x, s->logits, B, E, d, st), "router launch");
-    JM_HIP(jm::launch_topk(s->logits, B, E, k, s->renorm, s->top, s->tw, st), "top-k launch");
-    JM_HIP(jm::launch_dispatch(s->top, B * k, E, s->seg_off, s->seg_slot, s->active, s->n_active,
-                               s->first_slot, s->rank, st), "dispatch launch");
-    JM_HIP(jm::launch_prep_digits(x, d, B, d, G, s->xdig, s->xscale, st), "digit prep launch");
-    jm::ExpertArgs a;
-    a.blob = s->blob; a.off = s->off_dev; a.LE = s->L * E;
-    a.layer = layer; a.E = E; a.d = d; a.m = s->m; a.topk = k; a.group = G;
-    a.n_active = s->n_active; a.active = s->active; a.seg_off = s->seg_off; a.seg_slot = s->seg_slot;
-    a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
-    a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y;
     const int umax = std::min(E, B * k);
-    JM_HIP(jm::launch_experts(a, umax, st), "expert launch");
-    JM_HIP(jm::launch_combine(s->y, s->top, s->first_slot, B, k, d, out, st), "combine launch");
+    jm::RouteArgs r;
+    r.wt = s->wt + (size_t)layer * E * d;
+    r.x = x; r.B = B; r.E = E; r.d = d; r.topk = k; r.renorm = s->renorm; r.group = G;
+    r.logits = s->logits; r.xdig = s->xdig; r.xscale = s->xscale; r.top = s->top; r.tw = s->tw;
+    r.seg_off = s->seg_off; r.seg_slot = s->seg_slot; r.active = s->active; r.n_active = s->n_active;
+    r.first_slot = s->first_slot; r.comb = s->comb; r.rank_scratch = s->rank;
+    r.work = s->work; r.umax = umax; r.rec_off = (const unsigned long long*)s->off_dev;
+    r.LE = (long long)s->L * E; r.key0 = (long long)layer * E;
+    jm::ExpertArgs a;
+    a.blob = s->blob; a.work = s->work; a.d = d; a.m = s->m; a.topk = k; a.group = G;
+    a.seg_slot = s->seg_slot; a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
+    a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y;
+#define JM_MARK(i) if (s->prof) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
+    JM_MARK(0);
+    JM_HIP(jm::launch_route(r, st), "route launch");
+    JM_MARK(1);
+    JM_HIP(jm::launch_gateup(a, umax, st), "gate/up launch");
+    JM_MARK(2);
+    JM_HIP(jm::launch_down(a, umax, st), "down launch");
+    JM_MARK(3);
+    JM_HIP(jm::launch_combine(s->y, s->comb, B, k, d, out, st), "combine launch");
+    JM_MARK(4);
+#undef JM_MARK
     s->last_B = B;
     if (topk_idx) JM_HIP(hipMemcpyAsync(topk_idx, s->top, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k");
     if (topk_w) JM_HIP(hipMemcpyAsync(topk_w, s->tw, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k weights");
+    return 0;
+}
+
+int jm_store_profile(jm_store* s, int enable) {
+    if (int rc = check_store(s)) return rc;
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    if (enable && !s->prof) {
+        for (int i = 0; i <= JM_STAGES; i++) JM_HIP(hipEventCreate(&s->ev[i]), "hipEventCreate");
+        s->prof = 1;
+    } else if (!enable && s->prof) {
+        JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        for (int i = 0; i <= JM_STAGES; i++) (void)hipEventDestroy(s->ev[i]);
+        s->prof = 0;
+    }
+    return 0;
+}
+
+int jm_store_stage_ms(jm_store* s, float* ms, int n) {
+    if (int rc = check_store(s)) return rc;
+    if (!s->prof) return fail(JM_ERR_ARG, "profiling is off (jm_store_profile)");
+    if (!ms || n < JM_STAGES) return fail(JM_ERR_ARG, "need room for %d stage times", JM_STAGES);
+    JM_HIP(hipEventSynchronize(s->ev[JM_STAGES]), "hipEventSynchronize");
+    for (int i = 0; i < JM_STAGES; i++)
+        JM_HIP(hipEventElapsedTime(&ms[i], s->ev[i], s->ev[i + 1]), "hipEventElapsedTime");
     return 0;
 }
 
@@ -314,17 +365,19 @@ int jm_router(const void* gate_w, int dtype, const float* x, int B, int E, int d
     return 0;
 }
 
-int jm_dispatch(const int32_t* top, int nslot, int E, int32_t* seg_off, int32_t* seg_slot,
-                int32_t* active, int32_t* n_active, int32_t* first_slot, void* stream) {
-    if (!top || !seg_off || !seg_slot || !active || !n_active || !first_slot)
+int jm_dispatch(const int32_t* top, int nslot, int E, int topk, int32_t* seg_off, int32_t* seg_slot,
+                int32_t* active, int32_t* n_active, int32_t* first_slot, int32_t* comb, void* stream) {
+    if (!top || !seg_off || !seg_slot || !active || !n_active || !first_slot || !comb)
         return fail(JM_ERR_ARG, "NULL argument to jm_dispatch");
-    if (nslot < 0 || nslot > JM_MAX_SLOTS || E <= 0 || E > JM_MAX_E)
-        return fail(JM_ERR_SHAPE, "need 0 <= nslot <= %d and 0 < E <= %d", JM_MAX_SLOTS, JM_MAX_E);
+    if (nslot < 0 || nslot > JM_MAX_SLOTS || E <= 0 || E > JM_MAX_E || topk <= 0 || topk > JM_MAX_TOPK ||
+        nslot % topk)
+        return fail(JM_ERR_SHAPE, "need 0 <= nslot <= %d (a multiple of topk <= %d) and 0 < E <= %d",
+                    JM_MAX_SLOTS, JM_MAX_TOPK, JM_MAX_E);
     hipStream_t st = (hipStream_t)stream;
     void* scratch = nullptr;
     JM_HIP(hipMallocAsync(&scratch, align256((size_t)nslot * 4 + 4), st), "hipMallocAsync dispatch scratch");
-    hipError_t e = jm::launch_dispatch(top, nslot, E, seg_off, seg_slot, active, n_active, first_slot,
-                                       (int*)scratch, st);
+    hipError_t e = jm::launch_dispatch(top, nslot, E, topk, seg_off, seg_slot, active, n_active, first_slot,
+                                       comb, (int*)scratch, st);
     hipError_t f = hipFreeAsync(scratch, st);
     if (e != hipSuccess) return hip_fail(e, "dispatch launch");
     if (f != hipSuccess) return hip_fail(f, "hipFreeAsync");

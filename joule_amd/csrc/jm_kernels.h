@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "jm_device.h"
+
 // Signed base-16 digits per activation value in the Q4 dot (see jm_device.h).
 #ifndef JM_NDIG
 #define JM_NDIG 4
@@ -23,12 +25,8 @@ namespace jm {
 
 struct ExpertArgs {
     const uint8_t* blob;      // HBM copy of experts_q4.bin
-    const uint64_t* off;      // [3][L*E][2] (scales offset, packed offset)
-    int LE;                   // L * E
-    int layer, E, d, m, topk, group;
-    const int* n_active;      // number of experts with a non-empty segment
-    const int* active;        // their ids, ascending
-    const int* seg_off;       // [E+1] segment starts in seg_slot
+    const ExpertWork* work;   // [umax] per active expert: segment + record offsets
+    int d, m, topk;
     const int* seg_slot;      // [B*k] slot ids (b*k+i) grouped by expert, stable
     const float* tw;          // [B*k] routing weight of each slot
     const uint32_t* xdig;     // [B][d/G][NDIG][G/8] token digits
@@ -37,7 +35,34 @@ struct ExpertArgs {
     uint32_t* adig;           // [B*k][m/G][NDIG][G/8]
     float* ascale;            // [B*k][m/G]
     float* y;                 // [B*k][d]   weighted expert output per slot
+    int group;
 };
+
+// Routing front (router + x digits + top-k + dispatch) in one launch.
+struct RouteArgs {
+    const float* wt;          // [E][8][d/8] residue-major router table of the layer
+    const float* x;           // [B][d]
+    int B, E, d, topk, renorm, group;
+    float* logits;            // [B][E]
+    uint32_t* xdig;           // [B][d/G][NDIG][G/8]
+    float* xscale;            // [B][d/G]
+    int* top;                 // [B*k]
+    float* tw;                // [B*k]
+    int* seg_off;             // [E+1]
+    int* seg_slot;            // [B*k]
+    int* active;              // [E]
+    int* n_active;            // [1]
+    int* first_slot;          // [E]
+    int* comb;                // [B*k] each token's slots in union order, -1 padded
+    int* rank_scratch;        // [B*k]
+    ExpertWork* work;         // [umax] expert work table
+    int umax;                 // min(E, B*k)
+    const unsigned long long* rec_off;   // store offsets [3][L*E][2]
+    long long LE, key0;       // L*E and layer*E
+};
+hipError_t launch_route(const RouteArgs& a, hipStream_t st);
+hipError_t launch_router_transpose(const void* in, int bf16, float* out, long long rows, int d,
+                                   hipStream_t st);
 
 hipError_t launch_router(const void* gate_w, int bf16, const float* x, float* logits,
                          int B, int E, int d, hipStream_t st);
@@ -46,12 +71,13 @@ hipError_t launch_prep_digits(const float* src, int stride, int rows, int cols, 
 hipError_t launch_topk(const float* logits, int B, int E, int k, int renorm, int* top, float* tw,
                        hipStream_t st);
 // E <= JM_MAX_E, nslot <= JM_MAX_SLOTS
-hipError_t launch_dispatch(const int* top, int nslot, int E, int* seg_off, int* seg_slot,
-                           int* active, int* n_active, int* first_slot, int* rank_scratch,
+hipError_t launch_dispatch(const int* top, int nslot, int E, int k, int* seg_off, int* seg_slot,
+                           int* active, int* n_active, int* first_slot, int* comb, int* rank_scratch,
                            hipStream_t st);
-hipError_t launch_experts(const ExpertArgs& a, int umax, hipStream_t st);
-hipError_t launch_combine(const float* y, const int* top, const int* first_slot, int B, int k, int d,
-                          float* out, hipStream_t st);
+hipError_t launch_gateup(const ExpertArgs& a, int umax, hipStream_t st);
+hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st);
+// out[b] = sum of the token's slots of y in the order comb gives
+hipError_t launch_combine(const float* y, const int* comb, int B, int k, int d, float* out, hipStream_t st);
 hipError_t launch_dequant(const uint8_t* packed, const uint16_t* scales, long long numel, int group,
                           float* out, hipStream_t st);
 hipError_t launch_q4_rows(const uint8_t* packed, const uint16_t* scales, int rows, int cols, int group,

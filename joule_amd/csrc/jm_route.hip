@@ -1,0 +1,225 @@
+// Routing front of the MoE block (gfx950):
+//
+//   k_router   router scores in the reference's 8-chain order
+//              (decode_kernel.c:234-256, 693-718) and the x digits for the
+//              expert dots
+//   k_select   top-k of every token (decode_kernel.c:1425-1448), then the
+//              dispatch of all slots (:1449-1485) and the expert work table,
+//              in one block (B <= 64); larger batches run the multi-block
+//              top-k and the single-block dispatch as two launches
+//
+// Blocks never wait for or read data written by other blocks of the same
+// launch: on MI355X each XCD has its own L2, and a device-scope handoff
+// inside a kernel costs an L2 write-back and invalidate, while the kernel
+// boundary does that once.
+//
+// k_router: grid (ceil(E/8), ceil(B/4)), 256 threads.  Wave w of block
+// (eg, g) owns token b = 4g + w; lane (e_local = lane/8, r = lane%8) runs
+// the FMA chain r of expert 8*eg + e_local: the 8 lanes of an expert hold
+// the 8 partial sums that the reference keeps in the 8 lanes of an AVX2
+// register.  The router table is read from a copy laid out residue-major,
+// wt[e][r][t] = gate_w[e][8t + r], so a lane's chain is contiguous (64
+// float4 for d = 2048) and loads as wide vectors; the token is staged in LDS
+// in the same order.
+#include <algorithm>
+
+#include "jm_device.h"
+#include "jm_kernels.h"
+
+namespace jm {
+
+// residue-major copy of one router table: out[e][r][t] = in[e][8t + r]
+template <bool BF16>
+__global__ void __launch_bounds__(256)
+k_router_transpose(const void* __restrict__ in, float* __restrict__ out, long long rows, int d) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * d) return;
+    const long long e = i / d;
+    const int j = (int)(i % d);
+    const float v = BF16 ? bf16_bits_to_f32(((const uint16_t*)in)[i]) : ((const float*)in)[i];
+    const int T = d / 8;
+    out[e * d + (long long)(j & 7) * T + (j >> 3)] = v;
+}
+
+hipError_t launch_router_transpose(const void* in, int bf16, float* out, long long rows, int d,
+                                   hipStream_t st) {
+    const long long n = rows * d;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (bf16) hipLaunchKernelGGL(k_router_transpose<true>, grid, dim3(256), 0, st, in, out, rows, d);
+    else hipLaunchKernelGGL(k_router_transpose<false>, grid, dim3(256), 0, st, in, out, rows, d);
+    return hipGetLastError();
+}
+
+constexpr int ROUTE_TOK = 4;         // tokens per block (one per wave)
+constexpr int ROUTE_EXP = 8;         // experts per block
+constexpr int CH = 16;               // float4 per chain chunk (64 values)
+
+// DV = d / 512: chain chunks of 64 values per lane, and 2*DV float4 of the
+// token per lane for the staging.  The token's loads are issued first and
+// every loop is unrolled, so each wait covers exactly the loads it needs
+// (the memory counter retires loads in issue order).
+template <int G, int NDIG, int DV>
+__global__ void __launch_bounds__(256)
+k_router(RouteArgs a) {
+    extern __shared__ float lds[];
+    constexpr int d = DV * 512;
+    constexpr int T = d / 8;                 // chain length
+    constexpr int TP = T + 4;                // padded LDS row: the 8 residues fall in different banks
+    constexpr int XV = d / 256;              // float4 of the token per lane
+    float* xT = lds;
+    const int eg = blockIdx.x, g = blockIdx.y;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = lane & 7, el = lane >> 3;
+    const int e = eg * ROUTE_EXP + el;
+    const int b = g * ROUTE_TOK + w;
+    const bool tok = b < a.B;
+    const bool live = tok && e < a.E;
+
+    float4 xv4[XV];
+    if (tok) {
+        const float4* xb = (const float4*)(a.x + (size_t)b * d);
+#pragma unroll
+        for (int i = 0; i < XV; i++) xv4[i] = xb[lane + 64 * i];
+    }
+    const float4* wp = (const float4*)(a.wt + ((size_t)(live ? e : 0) * 8 + r) * T);
+    float4 A[CH], Bv[CH];
+    if (live) {
+#pragma unroll
+        for (int i = 0; i < CH; i++) A[i] = wp[i];
+        if (DV > 1) {
+#pragma unroll
+            for (int i = 0; i < CH; i++) Bv[i] = wp[CH + i];
+        }
+    }
+    if (tok) {
+        float* dst = xT + (size_t)w * 8 * TP;
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const int j = 4 * (lane + 64 * i);
+            dst[((j + 0) & 7) * TP + ((j + 0) >> 3)] = xv4[i].x;
+            dst[((j + 1) & 7) * TP + ((j + 1) >> 3)] = xv4[i].y;
+            dst[((j + 2) & 7) * TP + ((j + 2) >> 3)] = xv4[i].z;
+            dst[((j + 3) & 7) * TP + ((j + 3) >> 3)] = xv4[i].w;
+        }
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    if (live) {
+        const float4* xr = (const float4*)(xT + (size_t)w * 8 * TP + (size_t)r * TP);
+#pragma unroll
+        for (int c = 0; c < DV; c += 2) {
+#pragma unroll
+            for (int i = 0; i < CH; i++) {
+                const float4 xv = xr[c * CH + i];
+                acc = __builtin_fmaf(A[i].x, xv.x, acc);
+                acc = __builtin_fmaf(A[i].y, xv.y, acc);
+                acc = __builtin_fmaf(A[i].z, xv.z, acc);
+                acc = __builtin_fmaf(A[i].w, xv.w, acc);
+            }
+            if (c + 2 < DV) {
+#pragma unroll
+                for (int i = 0; i < CH; i++) A[i] = wp[(c + 2) * CH + i];
+            }
+            if (c + 1 < DV) {
+#pragma unroll
+                for (int i = 0; i < CH; i++) {
+                    const float4 xv = xr[(c + 1) * CH + i];
+                    acc = __builtin_fmaf(Bv[i].x, xv.x, acc);
+                    acc = __builtin_fmaf(Bv[i].y, xv.y, acc);
+                    acc = __builtin_fmaf(Bv[i].z, xv.z, acc);
+                    acc = __builtin_fmaf(Bv[i].w, xv.w, acc);
+                }
+                if (c + 3 < DV) {
+#pragma unroll
+                    for (int i = 0; i < CH; i++) Bv[i] = wp[(c + 3) * CH + i];
+                }
+            }
+        }
+    }
+    // horizontal sum in the AVX2 order: (r, r^4), then ^2, then ^1
+    acc = __fadd_rn(acc, __shfl_xor(acc, 4, JM_WAVE));
+    acc = __fadd_rn(acc, __shfl_xor(acc, 2, JM_WAVE));
+    acc = __fadd_rn(acc, __shfl_xor(acc, 1, JM_WAVE));
+    if (live && r == 0) a.logits[(size_t)b * a.E + e] = acc;
+
+    // x digits: this block's share of the token group's (token, group) pairs
+    constexpr int ng = d / G;
+    const int ntok = min(ROUTE_TOK, a.B - g * ROUTE_TOK);
+    const int npairs = ntok * ng;
+    const int nblk = gridDim.x;
+    constexpr int PPW = JM_WAVE / G;
+    const int sub = lane / G;
+    for (int base = (eg + nblk * w) * PPW; base < npairs; base += nblk * 4 * PPW) {
+        const int p = base + sub;
+        const bool ok = p < npairs;
+        const int bt = g * ROUTE_TOK + (ok ? p / ng : 0);
+        const int gg = ok ? p % ng : 0;
+        const float v = ok ? a.x[(size_t)bt * d + (size_t)gg * G + (lane & (G - 1))] : 0.0f;
+        encode_group_wave<G, NDIG>(v, ok, a.xdig + ((size_t)bt * ng + gg) * (NDIG * (G / 8)),
+                                   a.xscale + (size_t)bt * ng + gg);
+    }
+}
+
+// Top-k of every token (wave w takes tokens w, w + 16, ...) into LDS, then
+// the dispatch of all slots and the work table; one block of 1024 threads.
+template <int EPL>
+__global__ void __launch_bounds__(1024)
+k_select(RouteArgs a) {
+    extern __shared__ int lds_i[];
+    const int w = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const int nslot = a.B * a.topk;
+    int* top_l = lds_i;                                  // [nslot]
+    float* tw_l = (float*)(top_l + nslot);               // [nslot]
+    int* rest = (int*)(tw_l + nslot);
+    float* p_lds = (float*)rest + (size_t)w * 64 * EPL;
+    for (int b = w; b < a.B; b += nw)
+        topk_wave<EPL>(a.logits + (size_t)b * a.E, a.E, a.topk, a.renorm, p_lds,
+                       top_l + b * a.topk, tw_l + b * a.topk);
+    __syncthreads();
+    for (int i = threadIdx.x; i < nslot; i += blockDim.x) {
+        a.top[i] = top_l[i];
+        a.tw[i] = tw_l[i];
+    }
+    dispatch_block(top_l, nslot, a.E, a.topk, rest, a.seg_off, a.seg_slot, a.active, a.n_active,
+                   a.first_slot, a.comb, a.rank_scratch, a.work, a.umax, a.rec_off, a.LE, a.key0);
+}
+
+// Dispatch and work table alone, after the multi-block top-k (large B).
+__global__ void __launch_bounds__(1024)
+k_dispatch_work(RouteArgs a) {
+    extern __shared__ int lds_i[];
+    dispatch_block(a.top, a.B * a.topk, a.E, a.topk, lds_i, a.seg_off, a.seg_slot, a.active,
+                   a.n_active, a.first_slot, a.comb, a.rank_scratch, a.work, a.umax, a.rec_off, a.LE,
+                   a.key0);
+}
+
+static size_t dispatch_lds_bytes(int E) { return (size_t)dispatch_lds_ints(E) * 4; }
+
+hipError_t launch_route(const RouteArgs& a, hipStream_t st) {
+    const dim3 grid((unsigned)((a.E + ROUTE_EXP - 1) / ROUTE_EXP), (unsigned)((a.B + ROUTE_TOK - 1) / ROUTE_TOK));
+    const size_t xl = (size_t)ROUTE_TOK * 8 * (a.d / 8 + 4) * 4;
+#define JM_RT(GG, DVV) hipLaunchKernelGGL((k_router<GG, JM_NDIG, DVV>), grid, dim3(256), xl, st, a)
+#define JM_RTD(GG) switch (a.d / 512) { case 1: JM_RT(GG, 1); break; case 2: JM_RT(GG, 2); break; \
+        case 3: JM_RT(GG, 3); break; case 4: JM_RT(GG, 4); break; case 6: JM_RT(GG, 6); break; \
+        case 8: JM_RT(GG, 8); break; default: return hipErrorInvalidValue; }
+    if (a.group == 64) { JM_RTD(64) } else { JM_RTD(32) }
+#undef JM_RTD
+#undef JM_RT
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int epl = a.E <= 64 ? 1 : a.E <= 128 ? 2 : a.E <= 256 ? 4 : 8;
+    if (a.B <= 64) {
+        const size_t lds = (size_t)2 * a.B * a.topk * 4 + std::max((size_t)16 * 64 * epl * 4, dispatch_lds_bytes(a.E));
+#define JM_SEL(EPL) hipLaunchKernelGGL(k_select<EPL>, dim3(1), dim3(1024), lds, st, a)
+        if (epl == 1) JM_SEL(1); else if (epl == 2) JM_SEL(2); else if (epl == 4) JM_SEL(4); else JM_SEL(8);
+#undef JM_SEL
+    } else {
+        e = launch_topk(a.logits, a.B, a.E, a.topk, a.renorm, a.top, a.tw, st);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_dispatch_work, dim3(1), dim3(1024), dispatch_lds_bytes(a.E), st, a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace jm

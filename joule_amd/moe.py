@@ -187,6 +187,16 @@ class HbmExpertStore:
                                                  _lib.stream_handle(stream)), "jm_layer_ffn_batch")
         return out
 
+    def profile(self, enable: bool = True) -> None:
+        """Record HIP events around each kernel of later calls."""
+        _lib.check(_lib.lib().jm_store_profile(self._h, int(bool(enable))), "jm_store_profile")
+
+    def stage_ms(self) -> dict:
+        """Milliseconds per stage of the last call (waits for it)."""
+        ms = (ctypes.c_float * len(_lib.STAGES))()
+        _lib.check(_lib.lib().jm_store_stage_ms(self._h, ms, len(_lib.STAGES)), "jm_store_stage_ms")
+        return dict(zip(_lib.STAGES, [float(v) for v in ms]))
+
     def read_workspace(self, B: int, stream=None) -> dict:
         """Host copies of the last call's dispatch and per-slot intermediates."""
         s = self.shape

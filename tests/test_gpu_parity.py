@@ -178,11 +178,11 @@ def test_dispatch_stable_sort(gpu, B, E, k):
     if B >= 8:
         top[1, 2] = -1                         # a slot without an expert (NaN scores)
     t = torch.from_numpy(top.ravel()).cuda()
-    outs = [torch.full((n,), -7, dtype=torch.int32, device="cuda") for n in (E + 1, B * k, E, 1, E)]
-    _lib.check(_lib.lib().jm_dispatch(_lib.ptr(t), B * k, E, *[_lib.ptr(o) for o in outs],
+    outs = [torch.full((n,), -7, dtype=torch.int32, device="cuda") for n in (E + 1, B * k, E, 1, E, B * k)]
+    _lib.check(_lib.lib().jm_dispatch(_lib.ptr(t), B * k, E, k, *[_lib.ptr(o) for o in outs],
                                       _lib.stream_handle()))
     torch.cuda.synchronize()
-    seg_off, seg_slot, active, n_active, first_slot = (o.cpu().numpy() for o in outs)
+    seg_off, seg_slot, active, n_active, first_slot, comb = (o.cpu().numpy() for o in outs)
     flat = top.ravel()
     valid = np.where(flat >= 0)[0]
     order = valid[np.argsort(flat[valid], kind="stable")]
@@ -193,6 +193,15 @@ def test_dispatch_stable_sort(gpu, B, E, k):
     assert n_active[0] == len(act) and np.array_equal(active[:len(act)], act)
     for e in act:
         assert first_slot[e] == order[seg_off[e]]
+    # union order of the reference: experts in order of first appearance over (b, i)
+    first = {}
+    for s_, e in enumerate(flat):
+        if e >= 0 and e not in first:
+            first[e] = s_
+    for b in range(B):
+        slots = [b * k + i for i in range(k) if flat[b * k + i] >= 0]
+        want = sorted(slots, key=lambda s_: first[flat[s_]]) + [-1] * (k - len(slots))
+        assert comb[b * k:(b + 1) * k].tolist() == want
 
 
 # ------------------------------------------------------------------- block
@@ -259,6 +268,25 @@ def test_block_zipf_large_segments(qwen64):
     err = _rel(out, rout)
     print(f"  max rel err zipf B=512: {err:.3e}", flush=True)
     assert err <= TOL
+
+
+def test_block_nan_tokens(qwen64):
+    """A NaN token has NaN scores: every probability is NaN, no expert beats
+    -1e30, its k slots get index -1 and it contributes nothing (the
+    reference would index expert -1; here the slot is skipped)."""
+    banner("block NaN tokens")
+    x = activations(8, QWEN3.d)
+    x[3, 100] = np.nan
+    out, top, tw = _run_block(qwen64, 0, x)
+    rout, rtop, rtw = qwen64.oracle(0).forward(x)
+    assert np.all(top[3] == -1) and np.array_equal(top, rtop)
+    assert np.array_equal(tw.view(np.uint32), rtw.view(np.uint32))
+    assert np.all(out[3] == 0.0)
+    keep = [b for b in range(8) if b != 3]
+    assert _rel(out[keep], rout[keep]) <= TOL
+    xa = np.full((2, QWEN3.d), np.nan, np.float32)
+    out2, top2, _ = _run_block(qwen64, 0, xa)
+    assert np.all(top2 == -1) and np.all(out2 == 0.0)
 
 
 def test_block_empty_and_errors(qwen64):
