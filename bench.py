@@ -106,14 +106,14 @@ def measure(store, gw, x, steps, warmup, n_layers, stage_steps=None):
     return ms, stages, U
 
 
-def block_numbers(shape, group, B, ms, stages, U, steps, n_layers):
+def block_numbers(shape, group, B, ms, stages, U, steps, n_layers, router_bytes=4):
     from joule_amd.moe import algorithmic_bytes
     from joule_amd.q4_store import record_sizes
 
     # average routed experts over the timed steps' layer sequence
     seq = [U[i % n_layers] for i in range(steps)]
     u_avg = sum(seq) / len(seq)
-    bytes_block = algorithmic_bytes(shape, group, B, 0) + u_avg * sum(
+    bytes_block = algorithmic_bytes(shape, group, B, 0, router_bytes) + u_avg * sum(
         sum(record_sizes(r, c, group)) for r, c in ((shape.m, shape.d), (shape.m, shape.d), (shape.d, shape.m)))
     gate_up = u_avg * 2 * sum(record_sizes(shape.m, shape.d, group))
     down = u_avg * sum(record_sizes(shape.d, shape.m, group))
@@ -206,7 +206,8 @@ def main() -> int:
     x = torch.from_numpy(x_np).cuda()
     log(f"timing B={B}: {args.warmup} warm-up + {args.steps} steps")
     ms, stages, U = measure(store, gw, x, args.steps, args.warmup, NL)
-    main_res = block_numbers(shape, G, B, ms, stages, U, args.steps, NL)
+    rb = store.router_bytes_per_weight()
+    main_res = block_numbers(shape, G, B, ms, stages, U, args.steps, NL, rb)
     log(f"B={B}: {main_res['tok_per_s']:.0f} tok/s, {ms * 1e3:.1f} us/step, block "
         f"{main_res['block_GBs']:.0f} GB/s, gate/up {main_res['gateup_GBs']:.0f} GB/s, stages {stages}")
 
@@ -215,7 +216,7 @@ def main() -> int:
         for b in (1, 32):
             xb = torch.from_numpy(activations(b, shape.d)).cuda()
             m2, st2, U2 = measure(store, gw, xb, max(args.steps // 2, 50), 10, NL)
-            r = block_numbers(shape, G, b, m2, st2, U2, max(args.steps // 2, 50), NL)
+            r = block_numbers(shape, G, b, m2, st2, U2, max(args.steps // 2, 50), NL, rb)
             sweep[f"qwen3_B{b}"] = {k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac",
                                                       "gateup_GBs", "experts_routed_avg")}
             log(f"sweep qwen3 B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s")
@@ -233,7 +234,8 @@ def main() -> int:
         for b in (1, 8):
             xb = torch.from_numpy(activations(b, OLMOE.d)).cuda()
             m2, st2, U2 = measure(ostore, ogw, xb, max(args.steps // 2, 50), 10, NL)
-            r = block_numbers(OLMOE, G, b, m2, st2, U2, max(args.steps // 2, 50), NL)
+            r = block_numbers(OLMOE, G, b, m2, st2, U2, max(args.steps // 2, 50), NL,
+                              ostore.router_bytes_per_weight())
             sweep[f"olmoe_B{b}"] = {k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac",
                                                       "gateup_GBs", "experts_routed_avg")}
             log(f"sweep olmoe B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s")

@@ -95,6 +95,11 @@ int jm_store_destroy(jm_store* s);
  * table may be freed after the call.  Synchronises the device. */
 int jm_store_set_router(jm_store* s, const void* gate_w, int dtype);
 
+/* The element type the store's router copy holds: JM_DTYPE_BF16 when every
+ * weight is exactly a bf16 value (always for a bf16 table), else
+ * JM_DTYPE_F32.  Each call reads E*d elements of it. */
+int jm_store_router_dtype(const jm_store* s, int* dtype);
+
 /* Size the workspace for batches of up to max_B tokens now, so that later
  * calls with B <= max_B allocate nothing. */
 int jm_store_reserve(jm_store* s, int max_B);

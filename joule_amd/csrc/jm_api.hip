@@ -66,7 +66,8 @@ struct jm_store {
     const uint8_t* blob;
     uint64_t blob_bytes;
     uint64_t* off_dev;          // [3][L*E][2]
-    float* wt;                  // [L][E][8][d/8] residue-major copy of the router table
+    void* wt;                   // [L][E][8][d/8] residue-major copy of the router table
+    int wt_bf16;                // the copy holds bf16 (the table is exactly bf16-valued)
     int device;
     // workspace, sized for cap_B tokens; last_B = B of the last call
     int cap_B;
@@ -238,9 +239,26 @@ int jm_store_set_router(jm_store* s, const void* gate_w, int dtype) {
     if (!aligned(gate_w, 4)) return fail(JM_ERR_ARG, "router weights must be 4-byte aligned");
     JM_HIP(hipSetDevice(s->device), "hipSetDevice");
     const size_t n = (size_t)s->L * s->E * s->d;
-    if (!s->wt) JM_HIP(hipMalloc(&s->wt, n * sizeof(float)), "hipMalloc router copy");
-    JM_HIP(jm::launch_router_transpose(gate_w, dtype == JM_DTYPE_BF16, s->wt, (long long)s->L * s->E, s->d,
-                                       nullptr), "router transpose launch");
+    int exact = 1;
+    if (dtype == JM_DTYPE_F32) {
+        unsigned* flag = nullptr;
+        JM_HIP(hipMalloc(&flag, sizeof(unsigned)), "hipMalloc flag");
+        unsigned h = 0;
+        hipError_t e = hipMemset(flag, 0, sizeof(unsigned));
+        if (e == hipSuccess) e = jm::launch_bf16_exact((const float*)gate_w, (long long)n, flag, nullptr);
+        if (e == hipSuccess) e = hipMemcpy(&h, flag, sizeof(unsigned), hipMemcpyDeviceToHost);
+        (void)hipFree(flag);
+        if (e != hipSuccess) return hip_fail(e, "router bf16 check");
+        exact = h == 0;
+    }
+    if (s->wt && s->wt_bf16 != exact) {
+        (void)hipFree(s->wt);
+        s->wt = nullptr;
+    }
+    if (!s->wt) JM_HIP(hipMalloc(&s->wt, n * (exact ? 2 : 4)), "hipMalloc router copy");
+    s->wt_bf16 = exact;
+    JM_HIP(jm::launch_router_transpose(gate_w, dtype == JM_DTYPE_BF16, s->wt, exact, (long long)s->L * s->E,
+                                       s->d, nullptr), "router transpose launch");
     JM_HIP(hipDeviceSynchronize(), "router transpose");
     return 0;
 }
@@ -262,6 +280,13 @@ int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, 
     return 0;
 }
 
+int jm_store_router_dtype(const jm_store* s, int* dtype) {
+    if (int rc = check_store(s)) return rc;
+    if (!s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
+    if (dtype) *dtype = s->wt_bf16 ? JM_DTYPE_BF16 : JM_DTYPE_F32;
+    return 0;
+}
+
 int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out,
                        int32_t* topk_idx, float* topk_w, void* stream) {
     if (int rc = check_store(s)) return rc;
@@ -278,7 +303,8 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     JM_HIP(hipSetDevice(s->device), "hipSetDevice");
     const int umax = std::min(E, B * k);
     jm::RouteArgs r;
-    r.wt = s->wt + (size_t)layer * E * d;
+    r.wt = (const char*)s->wt + (size_t)layer * E * d * (s->wt_bf16 ? 2 : 4);
+    r.wt_bf16 = s->wt_bf16;
     r.x = x; r.B = B; r.E = E; r.d = d; r.topk = k; r.renorm = s->renorm; r.group = G;
     r.logits = s->logits; r.xdig = s->xdig; r.xscale = s->xscale; r.top = s->top; r.tw = s->tw;
     r.seg_off = s->seg_off; r.seg_slot = s->seg_slot; r.active = s->active; r.n_active = s->n_active;

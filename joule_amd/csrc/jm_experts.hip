@@ -35,10 +35,10 @@ __device__ __forceinline__ uint4 flip_nibbles(uint4 v) {
 
 // ------------------------------------------------------------------ gate/up
 
-template <int G, int NDIG, int LPR>
-__global__ void __launch_bounds__(512)
+template <int G, int NDIG, int LPR, int WAVES = 8>
+__global__ void __launch_bounds__(WAVES * 64)
 k_gateup(ExpertArgs a) {
-    constexpr int RB = 64, WAVES = 8;
+    constexpr int RB = 64;
     constexpr int ROWS_PER_WAVE = RB / WAVES;
     constexpr int RPW = JM_WAVE / LPR;
     constexpr int STEPS = ROWS_PER_WAVE / RPW;
@@ -57,11 +57,16 @@ k_gateup(ExpertArgs a) {
     const uint16_t* sc_u = (const uint16_t*)(a.blob + wk.sc[1]);
     const int row0 = rb * RB + wave * ROWS_PER_WAVE + rsub;
 
-    // every weight load of this wave's rows, issued up front
+    // every weight load of this wave's rows is issued before any arithmetic;
+    // the token's digits are requested between the two halves so that the
+    // first steps can start while the later rows are still in flight
     uint4 wg[STEPS][Q], wu[STEPS][Q];
     uint16_t hg[STEPS], hu[STEPS];
+    TokDigits<G, NDIG> td;
 #pragma unroll
     for (int s = 0; s < STEPS; s++) {
+        if (s == STEPS / 2)
+            load_digits<G, NDIG>(td, a.xdig, a.xscale, (size_t)(slot / a.topk) * ngroups + g, true);
         const int row = row0 + s * RPW;
         const uint4* pg = (const uint4*)(pk_g + (size_t)row * (a.d / 2) + (size_t)g * (G / 2));
         const uint4* pu = (const uint4*)(pk_u + (size_t)row * (a.d / 2) + (size_t)g * (G / 2));
@@ -70,12 +75,7 @@ k_gateup(ExpertArgs a) {
         hg[s] = sc_g[(size_t)row * ngroups + g];
         hu[s] = sc_u[(size_t)row * ngroups + g];
     }
-    TokDigits<G, NDIG> td;
-    load_digits<G, NDIG>(td, a.xdig, a.xscale, (size_t)(slot / a.topk) * ngroups + g, true);
-#pragma unroll
-    for (int s = 0; s < STEPS; s++)
-#pragma unroll
-        for (int q = 0; q < Q; q++) { wg[s][q] = flip_nibbles(wg[s][q]); wu[s][q] = flip_nibbles(wu[s][q]); }
+    if (STEPS == 1) load_digits<G, NDIG>(td, a.xdig, a.xscale, (size_t)(slot / a.topk) * ngroups + g, true);
 
     __shared__ float act_lds[RB];
     for (int t = 0; t < wk.n; t++) {
@@ -83,8 +83,11 @@ k_gateup(ExpertArgs a) {
 #pragma unroll
         for (int s = 0; s < STEPS; s++) {
             const float sg = fp16_hw(hg[s]), su = fp16_hw(hu[s]);
-            const int ig = group_dot_flipped<G, NDIG>(wg[s], td);
-            const int iu = group_dot_flipped<G, NDIG>(wu[s], td);
+            uint4 fg[Q], fu[Q];
+#pragma unroll
+            for (int q = 0; q < Q; q++) { fg[q] = flip_nibbles(wg[s][q]); fu[q] = flip_nibbles(wu[s][q]); }
+            const int ig = group_dot_flipped<G, NDIG>(fg, td);
+            const int iu = group_dot_flipped<G, NDIG>(fu, td);
             const float vg = seg_sum<LPR>(__fmul_rn((float)ig, __fmul_rn(td.s, sg)));
             const float vu = seg_sum<LPR>(__fmul_rn((float)iu, __fmul_rn(td.s, su)));
             if (g == 0) {
@@ -116,10 +119,9 @@ k_gateup(ExpertArgs a) {
 
 // -------------------------------------------------------------------- down
 
-template <int G, int NDIG, int LPR>
-__global__ void __launch_bounds__(512)
+template <int G, int NDIG, int LPR, int WAVES = 8, int RBD = 128>
+__global__ void __launch_bounds__(WAVES * 64)
 k_down(ExpertArgs a) {
-    constexpr int RBD = 128, WAVES = 8;
     constexpr int ROWS_PER_WAVE = RBD / WAVES;
     constexpr int RPW = JM_WAVE / LPR;
     constexpr int STEPS = ROWS_PER_WAVE / RPW;
@@ -139,8 +141,14 @@ k_down(ExpertArgs a) {
 
     uint4 wd[STEPS][Q];
     uint16_t hd[STEPS];
+    float wt = 0.0f;
+    TokDigits<G, NDIG> td;
 #pragma unroll
     for (int s = 0; s < STEPS; s++) {
+        if (s == STEPS / 2) {
+            wt = a.tw[slot];
+            load_digits<G, NDIG>(td, a.adig, a.ascale, (size_t)slot * ngroups + g, glive);
+        }
         const int row = row0 + s * RPW;
         if (glive) {
             const uint4* p = (const uint4*)(pk_d + (size_t)row * (a.m / 2) + (size_t)g * (G / 2));
@@ -153,19 +161,19 @@ k_down(ExpertArgs a) {
             hd[s] = 0;
         }
     }
-    float wt = a.tw[slot];
-    TokDigits<G, NDIG> td;
-    load_digits<G, NDIG>(td, a.adig, a.ascale, (size_t)slot * ngroups + g, glive);
-#pragma unroll
-    for (int s = 0; s < STEPS; s++)
-#pragma unroll
-        for (int q = 0; q < Q; q++) wd[s][q] = flip_nibbles(wd[s][q]);
+    if (STEPS == 1) {
+        wt = a.tw[slot];
+        load_digits<G, NDIG>(td, a.adig, a.ascale, (size_t)slot * ngroups + g, glive);
+    }
 
     for (int t = 0; t < wk.n; t++) {
         const int next = t + 1 < wk.n ? a.seg_slot[wk.s0 + t + 1] : 0;
 #pragma unroll
         for (int s = 0; s < STEPS; s++) {
-            const int iv = group_dot_flipped<G, NDIG>(wd[s], td);
+            uint4 f[Q];
+#pragma unroll
+            for (int q = 0; q < Q; q++) f[q] = flip_nibbles(wd[s][q]);
+            const int iv = group_dot_flipped<G, NDIG>(f, td);
             const float v = seg_sum<LPR>(glive ? __fmul_rn((float)iv, __fmul_rn(td.s, fp16_hw(hd[s]))) : 0.0f);
             if (g == 0) a.y[(size_t)slot * a.d + row0 + s * RPW] = __fmul_rn(wt, v);
         }

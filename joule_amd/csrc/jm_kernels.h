@@ -40,7 +40,8 @@ struct ExpertArgs {
 
 // Routing front (router + x digits + top-k + dispatch) in one launch.
 struct RouteArgs {
-    const float* wt;          // [E][8][d/8] residue-major router table of the layer
+    const void* wt;           // [E][8][d/8] residue-major router table of the layer
+    int wt_bf16;              // 1: wt holds bf16 bits, 0: float32
     const float* x;           // [B][d]
     int B, E, d, topk, renorm, group;
     float* logits;            // [B][E]
@@ -61,8 +62,9 @@ struct RouteArgs {
     long long LE, key0;       // L*E and layer*E
 };
 hipError_t launch_route(const RouteArgs& a, hipStream_t st);
-hipError_t launch_router_transpose(const void* in, int bf16, float* out, long long rows, int d,
-                                   hipStream_t st);
+hipError_t launch_router_transpose(const void* in, int in_bf16, void* out, int out_bf16, long long rows,
+                                   int d, hipStream_t st);
+hipError_t launch_bf16_exact(const float* in, long long n, unsigned* flag, hipStream_t st);
 
 hipError_t launch_router(const void* gate_w, int bf16, const float* x, float* logits,
                          int B, int E, int d, hipStream_t st);

@@ -28,25 +28,44 @@
 
 namespace jm {
 
-// residue-major copy of one router table: out[e][r][t] = in[e][8t + r]
-template <bool BF16>
+// Residue-major copy of the router tables: out[e][r][t] = in[e][8t + r],
+// as float32 or, when every value is exactly a bf16 (the reference's own
+// table type), as bf16 bits.
+template <bool IN_BF16, bool OUT_BF16>
 __global__ void __launch_bounds__(256)
-k_router_transpose(const void* __restrict__ in, float* __restrict__ out, long long rows, int d) {
+k_router_transpose(const void* __restrict__ in, void* __restrict__ out, long long rows, int d) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows * d) return;
     const long long e = i / d;
     const int j = (int)(i % d);
-    const float v = BF16 ? bf16_bits_to_f32(((const uint16_t*)in)[i]) : ((const float*)in)[i];
-    const int T = d / 8;
-    out[e * d + (long long)(j & 7) * T + (j >> 3)] = v;
+    const float v = IN_BF16 ? bf16_bits_to_f32(((const uint16_t*)in)[i]) : ((const float*)in)[i];
+    const long long o = e * d + (long long)(j & 7) * (d / 8) + (j >> 3);
+    if (OUT_BF16) ((uint16_t*)out)[o] = (uint16_t)(__float_as_uint(v) >> 16);
+    else ((float*)out)[o] = v;
 }
 
-hipError_t launch_router_transpose(const void* in, int bf16, float* out, long long rows, int d,
-                                   hipStream_t st) {
+// ORs the low 16 bits of every float32 value into *flag (0: all bf16-exact)
+__global__ void __launch_bounds__(256)
+k_bf16_exact(const float* __restrict__ in, long long n, unsigned* __restrict__ flag) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    unsigned low = i < n ? (__float_as_uint(in[i]) & 0xFFFFu) : 0u;
+    low = (unsigned)seg_or<64>((int)(low != 0));
+    if ((threadIdx.x & 63) == 0 && low) atomicOr(flag, 1u);
+}
+
+hipError_t launch_router_transpose(const void* in, int in_bf16, void* out, int out_bf16, long long rows,
+                                   int d, hipStream_t st) {
     const long long n = rows * d;
     const dim3 grid((unsigned)((n + 255) / 256));
-    if (bf16) hipLaunchKernelGGL(k_router_transpose<true>, grid, dim3(256), 0, st, in, out, rows, d);
-    else hipLaunchKernelGGL(k_router_transpose<false>, grid, dim3(256), 0, st, in, out, rows, d);
+    if (in_bf16 && out_bf16) hipLaunchKernelGGL((k_router_transpose<true, true>), grid, dim3(256), 0, st, in, out, rows, d);
+    else if (in_bf16) hipLaunchKernelGGL((k_router_transpose<true, false>), grid, dim3(256), 0, st, in, out, rows, d);
+    else if (out_bf16) hipLaunchKernelGGL((k_router_transpose<false, true>), grid, dim3(256), 0, st, in, out, rows, d);
+    else hipLaunchKernelGGL((k_router_transpose<false, false>), grid, dim3(256), 0, st, in, out, rows, d);
+    return hipGetLastError();
+}
+
+hipError_t launch_bf16_exact(const float* in, long long n, unsigned* flag, hipStream_t st) {
+    hipLaunchKernelGGL(k_bf16_exact, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, in, n, flag);
     return hipGetLastError();
 }
 
@@ -54,18 +73,118 @@ constexpr int ROUTE_TOK = 4;         // tokens per block (one per wave)
 constexpr int ROUTE_EXP = 8;         // experts per block
 constexpr int CH = 16;               // float4 per chain chunk (64 values)
 
-// DV = d / 512: chain chunks of 64 values per lane, and 2*DV float4 of the
-// token per lane for the staging.  The token's loads are issued first and
-// every loop is unrolled, so each wait covers exactly the loads it needs
-// (the memory counter retires loads in issue order).
-template <int G, int NDIG, int DV>
+// DV = d / 512.  A lane's chain is T = d/8 values: with a bf16 table it is
+// T/8 uint4 (32 for d = 2048), all loaded at once; with a float32 table it
+// is T/4 float4, loaded in chunks of 64 values, two chunks in flight.  The
+// token's loads are issued first and every loop is unrolled, so each wait
+// covers exactly the loads it needs (the memory counter retires loads in
+// issue order).
+template <int DV, bool WBF16>
+__device__ __forceinline__ float router_chain(const void* wt_base, int e, int r, const float* xr, bool live,
+                                              float4 (&xv4)[DV * 2], float* dst, bool tok, int lane) {
+    constexpr int T = DV * 64;
+    constexpr int TP = T + 4;
+    float acc = 0.0f;
+    if (WBF16) {
+        constexpr int NW = T / 8;                      // uint4 per chain
+        const uint4* wp = (const uint4*)((const uint16_t*)wt_base + ((size_t)e * 8 + r) * T);
+        uint4 W[NW];
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < NW; i++) W[i] = wp[i];
+        }
+        if (tok) {
+#pragma unroll
+            for (int i = 0; i < DV * 2; i++) {
+                const int j = 4 * (lane + 64 * i);
+                dst[((j + 0) & 7) * TP + ((j + 0) >> 3)] = xv4[i].x;
+                dst[((j + 1) & 7) * TP + ((j + 1) >> 3)] = xv4[i].y;
+                dst[((j + 2) & 7) * TP + ((j + 2) >> 3)] = xv4[i].z;
+                dst[((j + 3) & 7) * TP + ((j + 3) >> 3)] = xv4[i].w;
+            }
+        }
+        __syncthreads();
+        if (live) {
+            const float4* xq = (const float4*)xr;
+#pragma unroll
+            for (int i = 0; i < NW; i++) {
+                const float4 x0 = xq[2 * i], x1 = xq[2 * i + 1];
+                const unsigned w[4] = {W[i].x, W[i].y, W[i].z, W[i].w};
+                acc = __builtin_fmaf(__uint_as_float(w[0] << 16), x0.x, acc);
+                acc = __builtin_fmaf(__uint_as_float(w[0] & 0xFFFF0000u), x0.y, acc);
+                acc = __builtin_fmaf(__uint_as_float(w[1] << 16), x0.z, acc);
+                acc = __builtin_fmaf(__uint_as_float(w[1] & 0xFFFF0000u), x0.w, acc);
+                acc = __builtin_fmaf(__uint_as_float(w[2] << 16), x1.x, acc);
+                acc = __builtin_fmaf(__uint_as_float(w[2] & 0xFFFF0000u), x1.y, acc);
+                acc = __builtin_fmaf(__uint_as_float(w[3] << 16), x1.z, acc);
+                acc = __builtin_fmaf(__uint_as_float(w[3] & 0xFFFF0000u), x1.w, acc);
+            }
+        }
+    } else {
+        const float4* wp = (const float4*)((const float*)wt_base + ((size_t)e * 8 + r) * T);
+        float4 A[CH], Bv[CH];
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < CH; i++) A[i] = wp[i];
+            if (DV > 1) {
+#pragma unroll
+                for (int i = 0; i < CH; i++) Bv[i] = wp[CH + i];
+            }
+        }
+        if (tok) {
+#pragma unroll
+            for (int i = 0; i < DV * 2; i++) {
+                const int j = 4 * (lane + 64 * i);
+                dst[((j + 0) & 7) * TP + ((j + 0) >> 3)] = xv4[i].x;
+                dst[((j + 1) & 7) * TP + ((j + 1) >> 3)] = xv4[i].y;
+                dst[((j + 2) & 7) * TP + ((j + 2) >> 3)] = xv4[i].z;
+                dst[((j + 3) & 7) * TP + ((j + 3) >> 3)] = xv4[i].w;
+            }
+        }
+        __syncthreads();
+        if (live) {
+            const float4* xq = (const float4*)xr;
+#pragma unroll
+            for (int c = 0; c < DV; c += 2) {
+#pragma unroll
+                for (int i = 0; i < CH; i++) {
+                    const float4 xv = xq[c * CH + i];
+                    acc = __builtin_fmaf(A[i].x, xv.x, acc);
+                    acc = __builtin_fmaf(A[i].y, xv.y, acc);
+                    acc = __builtin_fmaf(A[i].z, xv.z, acc);
+                    acc = __builtin_fmaf(A[i].w, xv.w, acc);
+                }
+                if (c + 2 < DV) {
+#pragma unroll
+                    for (int i = 0; i < CH; i++) A[i] = wp[(c + 2) * CH + i];
+                }
+                if (c + 1 < DV) {
+#pragma unroll
+                    for (int i = 0; i < CH; i++) {
+                        const float4 xv = xq[(c + 1) * CH + i];
+                        acc = __builtin_fmaf(Bv[i].x, xv.x, acc);
+                        acc = __builtin_fmaf(Bv[i].y, xv.y, acc);
+                        acc = __builtin_fmaf(Bv[i].z, xv.z, acc);
+                        acc = __builtin_fmaf(Bv[i].w, xv.w, acc);
+                    }
+                    if (c + 3 < DV) {
+#pragma unroll
+                        for (int i = 0; i < CH; i++) Bv[i] = wp[(c + 3) * CH + i];
+                    }
+                }
+            }
+        }
+    }
+    return acc;
+}
+
+template <int G, int NDIG, int DV, bool WBF16>
 __global__ void __launch_bounds__(256)
 k_router(RouteArgs a) {
     extern __shared__ float lds[];
     constexpr int d = DV * 512;
     constexpr int T = d / 8;                 // chain length
     constexpr int TP = T + 4;                // padded LDS row: the 8 residues fall in different banks
-    constexpr int XV = d / 256;              // float4 of the token per lane
     float* xT = lds;
     const int eg = blockIdx.x, g = blockIdx.y;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -75,74 +194,23 @@ k_router(RouteArgs a) {
     const bool tok = b < a.B;
     const bool live = tok && e < a.E;
 
-    float4 xv4[XV];
+    float4 xv4[DV * 2];
     if (tok) {
         const float4* xb = (const float4*)(a.x + (size_t)b * d);
 #pragma unroll
-        for (int i = 0; i < XV; i++) xv4[i] = xb[lane + 64 * i];
+        for (int i = 0; i < DV * 2; i++) xv4[i] = xb[lane + 64 * i];
     }
-    const float4* wp = (const float4*)(a.wt + ((size_t)(live ? e : 0) * 8 + r) * T);
-    float4 A[CH], Bv[CH];
-    if (live) {
-#pragma unroll
-        for (int i = 0; i < CH; i++) A[i] = wp[i];
-        if (DV > 1) {
-#pragma unroll
-            for (int i = 0; i < CH; i++) Bv[i] = wp[CH + i];
-        }
-    }
-    if (tok) {
-        float* dst = xT + (size_t)w * 8 * TP;
-#pragma unroll
-        for (int i = 0; i < XV; i++) {
-            const int j = 4 * (lane + 64 * i);
-            dst[((j + 0) & 7) * TP + ((j + 0) >> 3)] = xv4[i].x;
-            dst[((j + 1) & 7) * TP + ((j + 1) >> 3)] = xv4[i].y;
-            dst[((j + 2) & 7) * TP + ((j + 2) >> 3)] = xv4[i].z;
-            dst[((j + 3) & 7) * TP + ((j + 3) >> 3)] = xv4[i].w;
-        }
-    }
-    __syncthreads();
-    float acc = 0.0f;
-    if (live) {
-        const float4* xr = (const float4*)(xT + (size_t)w * 8 * TP + (size_t)r * TP);
-#pragma unroll
-        for (int c = 0; c < DV; c += 2) {
-#pragma unroll
-            for (int i = 0; i < CH; i++) {
-                const float4 xv = xr[c * CH + i];
-                acc = __builtin_fmaf(A[i].x, xv.x, acc);
-                acc = __builtin_fmaf(A[i].y, xv.y, acc);
-                acc = __builtin_fmaf(A[i].z, xv.z, acc);
-                acc = __builtin_fmaf(A[i].w, xv.w, acc);
-            }
-            if (c + 2 < DV) {
-#pragma unroll
-                for (int i = 0; i < CH; i++) A[i] = wp[(c + 2) * CH + i];
-            }
-            if (c + 1 < DV) {
-#pragma unroll
-                for (int i = 0; i < CH; i++) {
-                    const float4 xv = xr[(c + 1) * CH + i];
-                    acc = __builtin_fmaf(Bv[i].x, xv.x, acc);
-                    acc = __builtin_fmaf(Bv[i].y, xv.y, acc);
-                    acc = __builtin_fmaf(Bv[i].z, xv.z, acc);
-                    acc = __builtin_fmaf(Bv[i].w, xv.w, acc);
-                }
-                if (c + 3 < DV) {
-#pragma unroll
-                    for (int i = 0; i < CH; i++) Bv[i] = wp[(c + 3) * CH + i];
-                }
-            }
-        }
-    }
+    float* dst = xT + (size_t)w * 8 * TP;
+    const float* xr = xT + (size_t)w * 8 * TP + (size_t)r * TP;
+    float acc = router_chain<DV, WBF16>(a.wt, live ? e : 0, r, xr, live, xv4, dst, tok, lane);
     // horizontal sum in the AVX2 order: (r, r^4), then ^2, then ^1
     acc = __fadd_rn(acc, __shfl_xor(acc, 4, JM_WAVE));
     acc = __fadd_rn(acc, __shfl_xor(acc, 2, JM_WAVE));
     acc = __fadd_rn(acc, __shfl_xor(acc, 1, JM_WAVE));
     if (live && r == 0) a.logits[(size_t)b * a.E + e] = acc;
 
-    // x digits: this block's share of the token group's (token, group) pairs
+    // x digits of this block's share of the token group's (token, group)
+    // pairs, read from the staged copy: x[bt][j] = xT[bt%4][j%8][j/8]
     constexpr int ng = d / G;
     const int ntok = min(ROUTE_TOK, a.B - g * ROUTE_TOK);
     const int npairs = ntok * ng;
@@ -152,9 +220,11 @@ k_router(RouteArgs a) {
     for (int base = (eg + nblk * w) * PPW; base < npairs; base += nblk * 4 * PPW) {
         const int p = base + sub;
         const bool ok = p < npairs;
-        const int bt = g * ROUTE_TOK + (ok ? p / ng : 0);
+        const int tl = ok ? p / ng : 0;
         const int gg = ok ? p % ng : 0;
-        const float v = ok ? a.x[(size_t)bt * d + (size_t)gg * G + (lane & (G - 1))] : 0.0f;
+        const int j = gg * G + (lane & (G - 1));
+        const float v = ok ? xT[(size_t)tl * 8 * TP + (size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
+        const int bt = g * ROUTE_TOK + tl;
         encode_group_wave<G, NDIG>(v, ok, a.xdig + ((size_t)bt * ng + gg) * (NDIG * (G / 8)),
                                    a.xscale + (size_t)bt * ng + gg);
     }
@@ -199,7 +269,8 @@ static size_t dispatch_lds_bytes(int E) { return (size_t)dispatch_lds_ints(E) * 
 hipError_t launch_route(const RouteArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)((a.E + ROUTE_EXP - 1) / ROUTE_EXP), (unsigned)((a.B + ROUTE_TOK - 1) / ROUTE_TOK));
     const size_t xl = (size_t)ROUTE_TOK * 8 * (a.d / 8 + 4) * 4;
-#define JM_RT(GG, DVV) hipLaunchKernelGGL((k_router<GG, JM_NDIG, DVV>), grid, dim3(256), xl, st, a)
+#define JM_RT(GG, DVV) do { if (a.wt_bf16) hipLaunchKernelGGL((k_router<GG, JM_NDIG, DVV, true>), grid, dim3(256), xl, st, a); \
+                           else hipLaunchKernelGGL((k_router<GG, JM_NDIG, DVV, false>), grid, dim3(256), xl, st, a); } while (0)
 #define JM_RTD(GG) switch (a.d / 512) { case 1: JM_RT(GG, 1); break; case 2: JM_RT(GG, 2); break; \
         case 3: JM_RT(GG, 3); break; case 4: JM_RT(GG, 4); break; case 6: JM_RT(GG, 6); break; \
         case 8: JM_RT(GG, 8); break; default: return hipErrorInvalidValue; }

@@ -134,6 +134,12 @@ class HbmExpertStore:
         _lib.check(_lib.lib().jm_store_set_router(self._h, _lib.ptr(gate_w), dt), "jm_store_set_router")
         self.router = gate_w
 
+    def router_bytes_per_weight(self) -> int:
+        """Bytes per router weight the store's copy holds (2 for bf16-exact tables)."""
+        dt = ctypes.c_int()
+        _lib.check(_lib.lib().jm_store_router_dtype(self._h, ctypes.byref(dt)), "jm_store_router_dtype")
+        return 2 if dt.value == _lib.JM_DTYPE_BF16 else 4
+
     def reserve(self, max_B: int) -> None:
         _lib.check(_lib.lib().jm_store_reserve(self._h, int(max_B)), "jm_store_reserve")
 

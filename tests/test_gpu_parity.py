@@ -237,6 +237,25 @@ def test_block_second_layer_and_determinism(qwen64):
     assert not np.array_equal(a[1], c[1])
 
 
+def test_block_fp32_router_table(qwen64):
+    """A router table that is not bf16-exact is kept in float32 (the other
+    chain path); results stay bit-exact against the oracle."""
+    banner("block fp32 router table")
+    rng = np.random.default_rng(77)
+    gw = rng.normal(0, 0.02, qwen64.gw.shape).astype(np.float32)
+    qwen64.store.set_router(torch.from_numpy(gw).cuda())
+    try:
+        assert qwen64.store.router_bytes_per_weight() == 4
+        x = activations(8, QWEN3.d)
+        out, top, tw = _run_block(qwen64, 1, x)
+        rout, rtop, rtw = qwen64.oracle(1, gw=gw[1]).forward(x)
+        assert np.array_equal(top, rtop) and np.array_equal(tw.view(np.uint32), rtw.view(np.uint32))
+        assert _rel(out, rout) <= TOL
+    finally:
+        qwen64.store.set_router(torch.from_numpy(qwen64.gw).cuda())
+    assert qwen64.store.router_bytes_per_weight() == 2
+
+
 def test_block_batch_invariance(qwen64):
     banner("block batch invariance")
     x = activations(8, QWEN3.d)
