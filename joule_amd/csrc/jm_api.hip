@@ -66,7 +66,7 @@ struct jm_store {
     const uint8_t* blob;
     uint64_t blob_bytes;
     uint64_t* off_dev;          // [3][L*E][2]
-    void* wt;                   // [L][E][8][d/8] residue-major copy of the router table
+    void* wt;                   // [L][Ep/8][d/8/P][64][P] interleaved copy of the router table
     int wt_bf16;                // the copy holds bf16 (the table is exactly bf16-valued)
     int device;
     // workspace, sized for cap_B tokens; last_B = B of the last call
@@ -102,7 +102,7 @@ int reserve(jm_store* s, int B) {
     const int E = s->E, d = s->d, m = s->m, k = s->topk, G = s->group;
     const size_t nslot = (size_t)B * k;
     const size_t words_d = (size_t)(d / G) * JM_NDIG * (G / 8);
-    const size_t words_m = (size_t)(m / G) * JM_NDIG * (G / 8);
+    const size_t words_m = (size_t)(m / 8) * JM_NDIG;
     size_t sz[19] = {
         (size_t)B * E * 4,            // logits
         nslot * 4,                    // top
@@ -120,7 +120,7 @@ int reserve(jm_store* s, int B) {
         0, 0,
         nslot * m * 4,                // act
         nslot * words_m * 4,          // adig
-        nslot * (m / G) * 4,          // ascale
+        nslot * (m / 8) * 4,          // ascale
         nslot * d * 4,                // y
     };
     size_t total = 0;
@@ -255,10 +255,12 @@ int jm_store_set_router(jm_store* s, const void* gate_w, int dtype) {
         (void)hipFree(s->wt);
         s->wt = nullptr;
     }
-    if (!s->wt) JM_HIP(hipMalloc(&s->wt, n * (exact ? 2 : 4)), "hipMalloc router copy");
+    const size_t ncopy = (size_t)s->L * jm::router_experts_padded(s->E) * s->d;
+    if (!s->wt) JM_HIP(hipMalloc(&s->wt, ncopy * (exact ? 2 : 4)), "hipMalloc router copy");
     s->wt_bf16 = exact;
+    JM_HIP(hipMemset(s->wt, 0, ncopy * (exact ? 2 : 4)), "router copy clear");
     JM_HIP(jm::launch_router_transpose(gate_w, dtype == JM_DTYPE_BF16, s->wt, exact, (long long)s->L * s->E,
-                                       s->d, nullptr), "router transpose launch");
+                                       s->E, s->d, nullptr), "router transpose launch");
     JM_HIP(hipDeviceSynchronize(), "router transpose");
     return 0;
 }
@@ -303,7 +305,7 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     JM_HIP(hipSetDevice(s->device), "hipSetDevice");
     const int umax = std::min(E, B * k);
     jm::RouteArgs r;
-    r.wt = (const char*)s->wt + (size_t)layer * E * d * (s->wt_bf16 ? 2 : 4);
+    r.wt = (const char*)s->wt + (size_t)layer * jm::router_experts_padded(E) * d * (s->wt_bf16 ? 2 : 4);
     r.wt_bf16 = s->wt_bf16;
     r.x = x; r.B = B; r.E = E; r.d = d; r.topk = k; r.renorm = s->renorm; r.group = G;
     r.logits = s->logits; r.xdig = s->xdig; r.xscale = s->xscale; r.top = s->top; r.tw = s->tw;
@@ -312,7 +314,7 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     r.work = s->work; r.umax = umax; r.rec_off = (const unsigned long long*)s->off_dev;
     r.LE = (long long)s->L * E; r.key0 = (long long)layer * E;
     jm::ExpertArgs a;
-    a.blob = s->blob; a.work = s->work; a.d = d; a.m = s->m; a.topk = k; a.group = G;
+    a.blob = s->blob; a.work = s->work; a.umax = umax; a.d = d; a.m = s->m; a.topk = k; a.group = G;
     a.seg_slot = s->seg_slot; a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
     a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y;
 #define JM_MARK(i) if (s->prof) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")

@@ -54,9 +54,10 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
 // to int gives INT_MIN, whose biased exponent is negative (the GPU's own
 // conversion would give 0 and let the NaN through).
 __device__ __forceinline__ float expf_fast(float v) {
-    if (v != v) return 0.0f;
-    if (v < -17.0f) return 0.0f;
-    if (v > 88.0f) v = 88.0f;
+    // written without branches: every path is computed and the early-out
+    // cases select 0 at the end
+    const bool zero = (v != v) || (v < -17.0f);
+    v = v > 88.0f ? 88.0f : v;
     const float y = __fmul_rn(v, 1.4426950408889634f);
     const int k = (int)(y >= 0.0f ? __fadd_rn(y, 0.5f) : __fsub_rn(y, 0.5f));
     const float f = __fsub_rn(y, (float)k);
@@ -65,10 +66,10 @@ __device__ __forceinline__ float expf_fast(float v) {
     p = __builtin_fmaf(f, p, 0.2402265f);
     p = __builtin_fmaf(f, p, 0.6931472f);
     p = __builtin_fmaf(f, p, 1.0f);
-    int biased = k + 127;
-    if (biased < 0) return 0.0f;
-    if (biased > 254) biased = 254;
-    return __fmul_rn(p, __uint_as_float((uint32_t)biased << 23));
+    const int biased = k + 127;
+    const int bc = biased < 0 ? 0 : biased > 254 ? 254 : biased;
+    const float r = __fmul_rn(p, __uint_as_float((uint32_t)bc << 23));
+    return (zero || biased < 0) ? 0.0f : r;
 }
 
 // SiLU(g) * u exactly as the reference writes it: (g / (1 + e^-g)) * u.
@@ -125,6 +126,8 @@ constexpr int DPP_XOR1 = 0xB1;          // quad_perm(1,0,3,2)
 constexpr int DPP_XOR2 = 0x4E;          // quad_perm(2,3,0,1)
 constexpr int DPP_ROW_MIRROR = 0x140;   // lane i <- 15 - i within a row
 constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <- 7 - i within 8 lanes
+constexpr int DPP_ROL4 = 0x12C;         // lane i <- i + 4 (mod 16) within a row (row_ror:12)
+constexpr int DPP_ROR8 = 0x128;         // lane i <- i ^ 8 within a row (row_ror:8)
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
@@ -152,6 +155,56 @@ __device__ __forceinline__ float seg_sum(float v) {
     if (W >= 32) v = __fadd_rn(v, swz_xor16_f(v));
     if (W >= 64) v = __fadd_rn(v, __shfl_xor(v, 32, JM_WAVE));
     return v;
+}
+
+// One level of a transposing butterfly at lane distance D (32, 16, 8, 4):
+// the N values of a lane become N/2, each lane keeping the half selected by
+// its lane bit D and adding its partner's copy of that half.  Partners are
+// l ^ D for D = 32, 16, 8 and 7 - l within 8 lanes for D = 4.
+template <int D, int N>
+__device__ __forceinline__ void transpose_level(float* v) {
+    const bool hi = (threadIdx.x & D) != 0;
+#pragma unroll
+    for (int j = 0; j < N / 2; j++) {
+        const float a = v[j], b = v[j + N / 2];
+        if constexpr (D == 32) {
+            const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+            v[j] = __fadd_rn(__uint_as_float(p[0]), __uint_as_float(p[1]));
+        } else if constexpr (D == 16) {
+            const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+            v[j] = __fadd_rn(__uint_as_float(p[0]), __uint_as_float(p[1]));
+        } else {
+            const float keep = hi ? b : a, send = hi ? a : b;
+            v[j] = __fadd_rn(keep, dpp_f<D == 8 ? DPP_ROR8 : DPP_HALF_MIRROR>(send));
+        }
+    }
+}
+
+// Totals of N = W/4 partial sums per lane over aligned segments of W lanes
+// (W = 16, 32, 64), all at once: transposing levels at distances W/2 .. 4,
+// then plain sums at distances 2 and 1.  Value v (bits of v = lane bits
+// log2(W)-1 .. 2) ends in lanes W*seg + 4*v + {0, 1, 2, 3}; returned.
+template <int W>
+__device__ __forceinline__ float transpose_sum(float (&v)[W / 4]) {
+    constexpr int N = W / 4;
+    if constexpr (W == 64) {
+        transpose_level<32, N>(v);
+        transpose_level<16, N / 2>(v);
+        transpose_level<8, N / 4>(v);
+        transpose_level<4, N / 8>(v);
+    } else if constexpr (W == 32) {
+        transpose_level<16, N>(v);
+        transpose_level<8, N / 2>(v);
+        transpose_level<4, N / 4>(v);
+    } else {
+        static_assert(W == 16, "segments of 16, 32 or 64 lanes");
+        transpose_level<8, N>(v);
+        transpose_level<4, N / 2>(v);
+    }
+    float t = v[0];
+    t = __fadd_rn(t, dpp_f<DPP_XOR2>(t));
+    t = __fadd_rn(t, dpp_f<DPP_XOR1>(t));
+    return t;
 }
 
 template <int W>
@@ -204,30 +257,19 @@ __device__ __forceinline__ void encode_group_wave(float v, bool store, uint32_t*
 
 // ---------------------------------------------------------- router top-k
 
-// 64-bit max over the whole wave; every lane gets the result.  Rows of 16
-// lanes reduce with DPP, then the four row maxima are read as scalars.
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-#define JM_STEP(CTRL)                                                            \
-    {                                                                            \
-        const unsigned lo = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)v, CTRL, 0xF, 0xF, false); \
-        const unsigned hi = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)(v >> 32), CTRL, 0xF, 0xF, false); \
-        const unsigned long long o = ((unsigned long long)hi << 32) | lo;        \
-        v = o > v ? o : v;                                                       \
-    }
-    JM_STEP(DPP_XOR1)
-    JM_STEP(DPP_XOR2)
-    JM_STEP(DPP_HALF_MIRROR)
-    JM_STEP(DPP_ROW_MIRROR)
-#undef JM_STEP
-    unsigned long long m = 0;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, 16 * r);
-        const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), 16 * r);
-        const unsigned long long o = ((unsigned long long)hi << 32) | lo;
-        m = o > m ? o : m;
-    }
-    return m;
+// Float max over the whole wave; every lane gets the result (non-NaN
+// inputs).  Rows of 16 lanes reduce with DPP, then the four row maxima are
+// read as scalars.
+__device__ __forceinline__ float wave_max_f(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 // Softmax over the E scores of one token and top-k selection, one wave
@@ -235,11 +277,11 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
 // a sequential sum over e = 0..E-1 by lane 0, p /= sum, k rounds of argmax
 // with ties to the lowest index, optional renormalisation by the sequential
 // sum of the k weights.
-// Argmax key of a candidate: (bits(p) << 32) | ~e.  Probabilities are >= 0,
-// so their bit patterns order like their values, and ~e puts the lower index
-// first among equal values; NaN and used entries get key 0, i.e. they are
-// never chosen, and a round whose maximum is 0 yields index -1 and weight
-// -1e30, the reference's values when nothing beats its -1e30 start.
+// A round takes the largest candidate p (an exact float max; candidates are
+// the p >= 0 not taken yet, so NaN never wins) and, among the entries equal
+// to it, the lowest index (first set bit of a ballot, lower e first).  A
+// round without candidates yields index -1 and weight -1e30, the reference's
+// values when nothing beats its -1e30 start.
 // p_lds holds 64*EPL floats.  Lane i < k writes top[i] and tw[i].
 template <int EPL>
 __device__ __forceinline__ void topk_wave(const float* __restrict__ s, int E, int k, int renorm,
@@ -253,52 +295,65 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ s, int E, in
         v[j] = e < E ? s[e] : __int_as_float(0x7FC00000);
         if (v[j] > mx) mx = v[j];
     }
-    mx = seg_max<64>(mx);                      // fmaxf ignores NaN, like the strict > scan
+    mx = wave_max_f(mx);                       // lane values are >= -1e30, never NaN
+    float ex[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
         const int e = lane + 64 * j;
-        if (e < E) p_lds[e] = expf_fast(__fsub_rn(v[j], mx));
+        ex[j] = expf_fast(__fsub_rn(v[j], mx));
+        if (e < E) p_lds[e] = ex[j];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float sum = 0.0f;
     if (lane == 0) {
+        // the reads of 32 values are issued together, the adds stay in order
         int e = 0;
-        for (; e + 4 <= E; e += 4) {
-            const float4 q = *(const float4*)(p_lds + e);
-            sum = __fadd_rn(sum, q.x); sum = __fadd_rn(sum, q.y);
-            sum = __fadd_rn(sum, q.z); sum = __fadd_rn(sum, q.w);
+        for (; e + 32 <= E; e += 32) {
+            float4 q[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) q[c] = *(const float4*)(p_lds + e + 4 * c);
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                sum = __fadd_rn(sum, q[c].x); sum = __fadd_rn(sum, q[c].y);
+                sum = __fadd_rn(sum, q[c].z); sum = __fadd_rn(sum, q[c].w);
+            }
         }
         for (; e < E; e++) sum = __fadd_rn(sum, p_lds[e]);
     }
-    sum = __shfl(sum, 0, JM_WAVE);
-    unsigned long long key[EPL];
+    sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sum), 0));
+    float cand[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
         const int e = lane + 64 * j;
-        const float p = e < E ? __fdiv_rn(p_lds[e], sum) : __int_as_float(0x7FC00000);
-        key[j] = (p >= 0.0f) ? (((unsigned long long)__float_as_uint(p) << 32) | (unsigned)~e) : 0ull;
+        const float p = __fdiv_rn(ex[j], sum);
+        cand[j] = (e < E && p >= 0.0f) ? p : -1.0f;
     }
-    float my_w = 0.0f;
+    float my_w = 0.0f, ss = 0.0f;
     int my_e = -1;
     for (int i = 0; i < k; i++) {
-        unsigned long long best = 0;
+        float best = cand[0];
 #pragma unroll
-        for (int j = 0; j < EPL; j++) best = key[j] > best ? key[j] : best;
-        best = wave_max_u64(best);
-        const int bi = best ? (int)~(unsigned)best : -1;
-        const float bv = best ? __uint_as_float((unsigned)(best >> 32)) : -1e30f;
+        for (int j = 1; j < EPL; j++) best = fmaxf(best, cand[j]);
+        best = wave_max_f(best);
+        int bi = -1;
+        float bv = -1e30f;
+        if (best >= 0.0f) {
+            bv = best;
 #pragma unroll
-        for (int j = 0; j < EPL; j++)
-            if (key[j] == best) key[j] = 0;
+            for (int j = 0; j < EPL; j++) {
+                const unsigned long long m = __ballot(cand[j] == best);
+                if (bi < 0 && m) bi = 64 * j + (int)__builtin_ctzll(m);
+            }
+#pragma unroll
+            for (int j = 0; j < EPL; j++)
+                if (lane + 64 * j == bi) cand[j] = -2.0f;
+        }
+        ss = __fadd_rn(ss, bv);
         if (lane == i) { my_w = bv; my_e = bi; }
     }
-    if (renorm) {
-        float ss = 0.0f;
-        for (int i = 0; i < k; i++) ss = __fadd_rn(ss, __shfl(my_w, i, JM_WAVE));
-        my_w = __fdiv_rn(my_w, ss);
-    }
+    if (renorm) my_w = __fdiv_rn(my_w, ss);
     if (lane < k) {
         top[lane] = my_e;
         tw[lane] = my_w;
@@ -309,150 +364,189 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ s, int E, in
 
 constexpr int DISP_CHUNKS_C = 16;
 
-// Exclusive prefix sum over the block (blockDim.x <= 1024); every thread
-// must call it.  wsum is LDS scratch of 16 ints; *total receives the sum.
-__device__ __forceinline__ int block_exclusive_scan(int v, int* wsum, int* total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, JM_WAVE);
-        if (lane >= o) x += y;
-    }
-    if (lane == 63) wsum[w] = x;
-    __syncthreads();
-    int off = 0, all = 0;
-    for (int j = 0; j < nw; j++) {
-        const int t = wsum[j];
-        off += j < w ? t : 0;
-        all += t;
-    }
-    *total = all;
-    __syncthreads();
-    return off + x - v;
-}
-
 // Work table entry of one active expert for the expert kernels: its
 // segment and the byte offsets of its gate/up/down records, so that an
-// expert block needs one load to know everything it streams.
+// expert wave needs one load to know everything it streams.
 struct ExpertWork {
     int e, s0, n, pad;
     unsigned long long sc[3], pk[3];
 };
 
+// Inclusive prefix sum over the wave with DPP: shifts of 1, 2, 4, 8 within
+// rows of 16 lanes, then row 0's total into row 1, rows 0-1's into 2-3.
+__device__ __forceinline__ unsigned wave_inclusive_scan(unsigned x) {
+    x += (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, true);   // row_shr:1
+    x += (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, true);   // row_shr:2
+    x += (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, true);   // row_shr:4
+    x += (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, true);   // row_shr:8
+    x += (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    x += (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return x;
+}
+
+// Exclusive prefix sums of two 32-bit fields over the block (blockDim.x <=
+// 1024); every thread must call it.  wsum is LDS scratch of 32 unsigned;
+// tot receives both totals.
+__device__ __forceinline__ uint2 block_exclusive_scan2(uint2 v, unsigned* wsum, uint2* tot) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const unsigned a = wave_inclusive_scan(v.x), b = wave_inclusive_scan(v.y);
+    if (lane == 63) { wsum[w] = a; wsum[16 + w] = b; }
+    __syncthreads();
+    unsigned offa = 0, offb = 0, alla = 0, allb = 0;
+    for (int j = 0; j < nw; j++) {
+        const unsigned ta = wsum[j], tb = wsum[16 + j];
+        offa += j < w ? ta : 0u;
+        offb += j < w ? tb : 0u;
+        alla += ta;
+        allb += tb;
+    }
+    *tot = make_uint2(alla, allb);
+    __syncthreads();
+    return make_uint2(offa + a - v.x, offb + b - v.y);
+}
+
+// Record offsets of expert e (one per part: scales, packed) from the store's
+// [3][L*E][2] table at key0 = layer * E; loaded by the expert's own thread at
+// the start of a dispatch so that they are in registers when its work entry
+// is written.
+struct ExpertRec {
+    unsigned long long sc[3], pk[3];
+};
+
+__device__ __forceinline__ ExpertRec load_expert_rec(const unsigned long long* __restrict__ rec_off,
+                                                     long long LE, long long key0, int e) {
+    ExpertRec r;
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        r.sc[p] = rec_off[((long long)p * LE + key0 + e) * 2 + 0];
+        r.pk[p] = rec_off[((long long)p * LE + key0 + e) * 2 + 1];
+    }
+    return r;
+}
+
 // LDS of dispatch_block, in ints
-__host__ __device__ constexpr int dispatch_lds_ints(int E) { return DISP_CHUNKS_C * E + 3 * E + 1 + 16; }
+__host__ __device__ constexpr int dispatch_lds_ints(int E) { return DISP_CHUNKS_C * E + 2 * E + 1 + 32; }
 
 // Stable counting sort of nslot slots by expert id, run by one whole block
 // (decode_kernel.c:1449-1485 builds the same segments in first-appearance
 // order; here they are in expert-id order, slots within a segment in
-// increasing b*k+i order).  `top` should point to LDS.  Writes
-// seg_off[E+1], seg_slot, active[U], *n_active = U, first_slot[e], and
+// increasing b*k+i order).  `top` should point to LDS; `rank` is nslot ints
+// of scratch (LDS when it fits).  E <= blockDim.x.  Writes seg_off[E+1],
+// seg_slot, active[U] (expert-id order), *n_active = U, first_slot[e], and
 // comb[b*k + j] = the token's slots in the reference's union order
-// (ascending first appearance of their expert), -1 padded; with `work`,
-// also the expert work table for the first umax active experts (n = 0 past
-// U), from the store's [3][L*E][2] record offsets at key0 = layer * E.
+// (ascending first appearance of their expert), -1 padded.  With `work`,
+// also the expert work table for umax entries: the experts with two or more
+// slots first, then those with one (each group in expert-id order), so that
+// the longest segments start first; entries past U have n = 0.  `rec` holds
+// the record offsets of expert tid (tid < E).
 __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E, int k, int* lds,
                                                int* __restrict__ seg_off, int* __restrict__ seg_slot,
                                                int* __restrict__ active, int* __restrict__ n_active,
                                                int* __restrict__ first_slot, int* __restrict__ comb,
-                                               int* __restrict__ rank_scratch,
-                                               ExpertWork* __restrict__ work = nullptr, int umax = 0,
-                                               const unsigned long long* __restrict__ rec_off = nullptr,
-                                               long long LE = 0, long long key0 = 0) {
+                                               int* rank, ExpertWork* __restrict__ work = nullptr,
+                                               int umax = 0, const ExpertRec* rec = nullptr) {
     int* cnt = lds;                              // [DISP_CHUNKS][E]
     int* off = cnt + DISP_CHUNKS_C * E;          // [E + 1]
     int* fs = off + E + 1;                       // [E]
-    int* act = fs + E;                           // [E]
-    int* wsum = act + E;                         // [16]
+    unsigned* wsum = (unsigned*)(fs + E);        // [32]
     const int tid = threadIdx.x, nth = blockDim.x;
     const int chunk = (nslot + DISP_CHUNKS_C - 1) / DISP_CHUNKS_C;
     for (int i = tid; i < DISP_CHUNKS_C * E; i += nth) cnt[i] = 0;
     __syncthreads();
     for (int s = tid; s < nslot; s += nth) {
         const int e = top[s];
-        if (e < 0 || e >= E) { rank_scratch[s] = -1; continue; }
+        if (e < 0 || e >= E) { rank[s] = -1; continue; }
         const int c = s / chunk;
-        int rank = 0;
-        for (int q = c * chunk; q < s; q++) rank += (top[q] == e);
-        rank_scratch[s] = rank;
+        int r = 0;
+        for (int q = c * chunk; q < s; q++) r += (top[q] == e);
+        rank[s] = r;
         atomicAdd(&cnt[c * E + e], 1);
     }
     __syncthreads();
     // per expert: exclusive prefix over chunks, then one block scan of
-    // (active flag << 20 | count) gives segment starts and active indices
+    // (count, multi << 16 | single) gives segment starts and the work-table
+    // positions of both groups
     int total_e = 0;
-    for (int e = tid; e < E; e += nth) {
-        int run = 0;
-        for (int c = 0; c < DISP_CHUNKS_C; c++) {
-            const int n = cnt[c * E + e];
-            cnt[c * E + e] = run;
-            run += n;
-        }
-        total_e = run;                           // E <= nth: one expert per thread
-    }
-    const int packed = tid < E ? (((total_e > 0) << 20) | total_e) : 0;
-    int tot;
-    const int excl = block_exclusive_scan(packed, wsum, &tot);
-    const int U = tot >> 20;
     if (tid < E) {
-        off[tid] = excl & 0xFFFFF;
-        seg_off[tid] = excl & 0xFFFFF;
-        if (total_e > 0) {
-            active[excl >> 20] = tid;
-            act[excl >> 20] = tid;
+        int n[DISP_CHUNKS_C];
+#pragma unroll
+        for (int c = 0; c < DISP_CHUNKS_C; c++) n[c] = cnt[c * E + tid];
+        int run = 0;
+#pragma unroll
+        for (int c = 0; c < DISP_CHUNKS_C; c++) {
+            cnt[c * E + tid] = run;
+            run += n[c];
         }
+        total_e = run;
+    }
+    uint2 tot;
+    const uint2 excl = block_exclusive_scan2(
+        make_uint2((unsigned)total_e, ((unsigned)(total_e > 1) << 16) | (unsigned)(total_e == 1)), wsum, &tot);
+    const int n_multi = (int)(tot.y >> 16), n_single = (int)(tot.y & 0xFFFFu);
+    const int U = n_multi + n_single;
+    const int my_off = (int)excl.x;
+    if (tid < E) {
+        off[tid] = my_off;
+        seg_off[tid] = my_off;
     }
     if (tid == 0) {
-        off[E] = tot & 0xFFFFF;
-        seg_off[E] = tot & 0xFFFFF;
+        off[E] = (int)tot.x;
+        seg_off[E] = (int)tot.x;
         *n_active = U;
+    }
+    if (tid < E && total_e > 0) {
+        const int im = (int)(excl.y >> 16), is = (int)(excl.y & 0xFFFFu);
+        // expert-id order over both groups: experts below tid with any slot
+        active[im + is] = tid;
+        if (work) {
+            ExpertWork wk;
+            wk.e = tid;
+            wk.s0 = my_off;
+            wk.n = total_e;
+            wk.pad = 0;
+#pragma unroll
+            for (int p = 0; p < 3; p++) { wk.sc[p] = rec->sc[p]; wk.pk[p] = rec->pk[p]; }
+            const int u = total_e > 1 ? im : n_multi + is;
+            if (u < umax) work[u] = wk;
+        }
+    }
+    if (work) {
+        for (int u = U + tid; u < umax; u += nth) {
+            ExpertWork wk;
+            wk.e = -1; wk.s0 = 0; wk.n = 0; wk.pad = 0;
+#pragma unroll
+            for (int p = 0; p < 3; p++) { wk.sc[p] = 0; wk.pk[p] = 0; }
+            work[u] = wk;
+        }
     }
     __syncthreads();
     for (int s = tid; s < nslot; s += nth) {
-        const int rank = rank_scratch[s];
-        if (rank < 0) continue;
+        const int r = rank[s];
+        if (r < 0) continue;
         const int e = top[s];
-        const int pos = off[e] + cnt[(s / chunk) * E + e] + rank;
+        const int pos = off[e] + cnt[(s / chunk) * E + e] + r;
         seg_slot[pos] = s;
         if (pos == off[e]) { first_slot[e] = s; fs[e] = s; }
     }
     __syncthreads();
     // union order per token: its slots ranked by the first slot of their
     // expert (distinct experts -> distinct keys); slots without an expert go
-    // last and are stored as -1
+    // last and are stored as -1.  Each slot's key goes to `rank` first.
+    for (int bi = tid; bi < nslot; bi += nth) {
+        const int e = top[bi];
+        rank[bi] = (e >= 0 && e < E) ? fs[e] : 0x7FFFFFFF;
+    }
+    __syncthreads();
     for (int bi = tid; bi < nslot; bi += nth) {
         const int b = bi / k, i = bi % k;
-        const int e = top[bi];
-        const bool ok = e >= 0 && e < E;
-        const int key = ok ? fs[e] : 0x7FFFFFFF;
-        int rank = 0;
+        const int key = rank[bi];
+        int r = 0;
+#pragma unroll 8
         for (int j = 0; j < k; j++) {
-            const int ej = top[b * k + j];
-            const int kj = (ej >= 0 && ej < E) ? fs[ej] : 0x7FFFFFFF;
-            rank += (kj < key) || (kj == key && j < i);
+            const int kj = rank[b * k + j];
+            r += (kj < key) || (kj == key && j < i);
         }
-        comb[b * k + rank] = ok ? bi : -1;
-    }
-    if (work) {
-        for (int u = tid; u < umax; u += nth) {
-            ExpertWork wk;
-            wk.pad = 0;
-            if (u < U) {
-                const int e = act[u];
-                wk.e = e;
-                wk.s0 = off[e];
-                wk.n = off[e + 1] - off[e];
-                for (int p = 0; p < 3; p++) {
-                    wk.sc[p] = rec_off[((long long)p * LE + key0 + e) * 2 + 0];
-                    wk.pk[p] = rec_off[((long long)p * LE + key0 + e) * 2 + 1];
-                }
-            } else {
-                wk.e = -1; wk.s0 = 0; wk.n = 0;
-                for (int p = 0; p < 3; p++) { wk.sc[p] = 0; wk.pk[p] = 0; }
-            }
-            work[u] = wk;
-        }
+        comb[b * k + r] = key != 0x7FFFFFFF ? bi : -1;
     }
 }
 

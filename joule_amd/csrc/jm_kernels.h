@@ -26,14 +26,15 @@ namespace jm {
 struct ExpertArgs {
     const uint8_t* blob;      // HBM copy of experts_q4.bin
     const ExpertWork* work;   // [umax] per active expert: segment + record offsets
+    int umax;                 // work table entries
     int d, m, topk;
     const int* seg_slot;      // [B*k] slot ids (b*k+i) grouped by expert, stable
     const float* tw;          // [B*k] routing weight of each slot
     const uint32_t* xdig;     // [B][d/G][NDIG][G/8] token digits
     const float* xscale;      // [B][d/G]
     float* act;               // [B*k][m]   SiLU(gate)*up per slot
-    uint32_t* adig;           // [B*k][m/G][NDIG][G/8]
-    float* ascale;            // [B*k][m/G]
+    uint32_t* adig;           // [B*k][m/8][NDIG] act digits, 8 values per group
+    float* ascale;            // [B*k][m/8]
     float* y;                 // [B*k][d]   weighted expert output per slot
     int group;
 };
@@ -62,8 +63,10 @@ struct RouteArgs {
     long long LE, key0;       // L*E and layer*E
 };
 hipError_t launch_route(const RouteArgs& a, hipStream_t st);
+// experts per layer in the router copy: E rounded up to whole groups of 8
+__host__ __device__ constexpr int router_experts_padded(int E) { return (E + 7) / 8 * 8; }
 hipError_t launch_router_transpose(const void* in, int in_bf16, void* out, int out_bf16, long long rows,
-                                   int d, hipStream_t st);
+                                   int E, int d, hipStream_t st);
 hipError_t launch_bf16_exact(const float* in, long long n, unsigned* flag, hipStream_t st);
 
 hipError_t launch_router(const void* gate_w, int bf16, const float* x, float* logits,

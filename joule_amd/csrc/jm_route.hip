@@ -14,13 +14,14 @@
 // boundary does that once.
 //
 // k_router: grid (ceil(E/8), ceil(B/4)), 256 threads.  Wave w of block
-// (eg, g) owns token b = 4g + w; lane (e_local = lane/8, r = lane%8) runs
-// the FMA chain r of expert 8*eg + e_local: the 8 lanes of an expert hold
-// the 8 partial sums that the reference keeps in the 8 lanes of an AVX2
-// register.  The router table is read from a copy laid out residue-major,
-// wt[e][r][t] = gate_w[e][8t + r], so a lane's chain is contiguous (64
-// float4 for d = 2048) and loads as wide vectors; the token is staged in LDS
-// in the same order.
+// (eg, g) owns token b = 4g + w; lane L = 8 * e_local + r runs the FMA
+// chain r of expert 8*eg + e_local: the 8 lanes of an expert hold the 8
+// partial sums that the reference keeps in the 8 lanes of an AVX2 register.
+// The router table is read from a copy in which the 64 chains of an expert
+// group are interleaved in 16-byte pieces: piece i of lane L's chain
+// (values 8t + r for t in the piece) sits at [eg][i][L], so each load
+// instruction of a wave reads 1 KiB of contiguous memory.  The token is
+// staged in LDS in the chains' order.
 #include <algorithm>
 
 #include "jm_device.h"
@@ -28,18 +29,28 @@
 
 namespace jm {
 
-// Residue-major copy of the router tables: out[e][r][t] = in[e][8t + r],
+// Interleaved copy of the router tables (L layers of E experts; E padded
+// to Ep = a multiple of 8 per layer, the padding left as the caller cleared
+// it).  Value j of expert e is value t = j / 8 of chain r = j % 8; with P
+// values per 16-byte piece (8 bf16 or 4 float32) it goes to piece t / P of
+// lane 8 * (e % 8) + r in expert group e / 8:
+//   out[l][e/8][t/P][8*(e%8) + r][t%P] = in[l][e][j]
 // as float32 or, when every value is exactly a bf16 (the reference's own
 // table type), as bf16 bits.
 template <bool IN_BF16, bool OUT_BF16>
 __global__ void __launch_bounds__(256)
-k_router_transpose(const void* __restrict__ in, void* __restrict__ out, long long rows, int d) {
+k_router_transpose(const void* __restrict__ in, void* __restrict__ out, long long rows, int E, int Ep,
+                   int d) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows * d) return;
-    const long long e = i / d;
+    const long long row = i / d;
     const int j = (int)(i % d);
+    const long long l = row / E;
+    const int e = (int)(row % E);
     const float v = IN_BF16 ? bf16_bits_to_f32(((const uint16_t*)in)[i]) : ((const float*)in)[i];
-    const long long o = e * d + (long long)(j & 7) * (d / 8) + (j >> 3);
+    constexpr int P = OUT_BF16 ? 8 : 4;
+    const int t = j >> 3, lane = ((e & 7) << 3) | (j & 7);
+    const long long o = l * Ep * d + ((((long long)(e >> 3) * (d / 8 / P) + t / P) * 64 + lane) * P + t % P);
     if (OUT_BF16) ((uint16_t*)out)[o] = (uint16_t)(__float_as_uint(v) >> 16);
     else ((float*)out)[o] = v;
 }
@@ -54,13 +65,16 @@ k_bf16_exact(const float* __restrict__ in, long long n, unsigned* __restrict__ f
 }
 
 hipError_t launch_router_transpose(const void* in, int in_bf16, void* out, int out_bf16, long long rows,
-                                   int d, hipStream_t st) {
+                                   int E, int d, hipStream_t st) {
     const long long n = rows * d;
+    const int Ep = router_experts_padded(E);
     const dim3 grid((unsigned)((n + 255) / 256));
-    if (in_bf16 && out_bf16) hipLaunchKernelGGL((k_router_transpose<true, true>), grid, dim3(256), 0, st, in, out, rows, d);
-    else if (in_bf16) hipLaunchKernelGGL((k_router_transpose<true, false>), grid, dim3(256), 0, st, in, out, rows, d);
-    else if (out_bf16) hipLaunchKernelGGL((k_router_transpose<false, true>), grid, dim3(256), 0, st, in, out, rows, d);
-    else hipLaunchKernelGGL((k_router_transpose<false, false>), grid, dim3(256), 0, st, in, out, rows, d);
+#define JM_TR(A, B) hipLaunchKernelGGL((k_router_transpose<A, B>), grid, dim3(256), 0, st, in, out, rows, E, Ep, d)
+    if (in_bf16 && out_bf16) JM_TR(true, true);
+    else if (in_bf16) JM_TR(true, false);
+    else if (out_bf16) JM_TR(false, true);
+    else JM_TR(false, false);
+#undef JM_TR
     return hipGetLastError();
 }
 
@@ -87,11 +101,11 @@ __device__ __forceinline__ float router_chain(const void* wt_base, int e, int r,
     float acc = 0.0f;
     if (WBF16) {
         constexpr int NW = T / 8;                      // uint4 per chain
-        const uint4* wp = (const uint4*)((const uint16_t*)wt_base + ((size_t)e * 8 + r) * T);
+        const uint4* wp = (const uint4*)wt_base + (size_t)(e >> 3) * NW * 64 + (((e & 7) << 3) | r);
         uint4 W[NW];
         if (live) {
 #pragma unroll
-            for (int i = 0; i < NW; i++) W[i] = wp[i];
+            for (int i = 0; i < NW; i++) W[i] = wp[(size_t)i * 64];
         }
         if (tok) {
 #pragma unroll
@@ -121,14 +135,14 @@ __device__ __forceinline__ float router_chain(const void* wt_base, int e, int r,
             }
         }
     } else {
-        const float4* wp = (const float4*)((const float*)wt_base + ((size_t)e * 8 + r) * T);
+        const float4* wp = (const float4*)wt_base + (size_t)(e >> 3) * (T / 4) * 64 + (((e & 7) << 3) | r);
         float4 A[CH], Bv[CH];
         if (live) {
 #pragma unroll
-            for (int i = 0; i < CH; i++) A[i] = wp[i];
+            for (int i = 0; i < CH; i++) A[i] = wp[(size_t)i * 64];
             if (DV > 1) {
 #pragma unroll
-                for (int i = 0; i < CH; i++) Bv[i] = wp[CH + i];
+                for (int i = 0; i < CH; i++) Bv[i] = wp[(size_t)(CH + i) * 64];
             }
         }
         if (tok) {
@@ -156,7 +170,7 @@ __device__ __forceinline__ float router_chain(const void* wt_base, int e, int r,
                 }
                 if (c + 2 < DV) {
 #pragma unroll
-                    for (int i = 0; i < CH; i++) A[i] = wp[(c + 2) * CH + i];
+                    for (int i = 0; i < CH; i++) A[i] = wp[(size_t)((c + 2) * CH + i) * 64];
                 }
                 if (c + 1 < DV) {
 #pragma unroll
@@ -169,7 +183,7 @@ __device__ __forceinline__ float router_chain(const void* wt_base, int e, int r,
                     }
                     if (c + 3 < DV) {
 #pragma unroll
-                        for (int i = 0; i < CH; i++) Bv[i] = wp[(c + 3) * CH + i];
+                        for (int i = 0; i < CH; i++) Bv[i] = wp[(size_t)((c + 3) * CH + i) * 64];
                     }
                 }
             }
@@ -232,16 +246,21 @@ k_router(RouteArgs a) {
 
 // Top-k of every token (wave w takes tokens w, w + 16, ...) into LDS, then
 // the dispatch of all slots and the work table; one block of 1024 threads.
+// The record offsets of expert tid are requested first so that they arrive
+// while the top-k runs.
 template <int EPL>
 __global__ void __launch_bounds__(1024)
 k_select(RouteArgs a) {
     extern __shared__ int lds_i[];
+    ExpertRec rec;
+    if ((int)threadIdx.x < a.E) rec = load_expert_rec(a.rec_off, a.LE, a.key0, threadIdx.x);
     const int w = threadIdx.x >> 6;
     const int nw = blockDim.x >> 6;
     const int nslot = a.B * a.topk;
     int* top_l = lds_i;                                  // [nslot]
     float* tw_l = (float*)(top_l + nslot);               // [nslot]
-    int* rest = (int*)(tw_l + nslot);
+    int* rank_l = (int*)(tw_l + nslot);                  // [nslot]
+    int* rest = lds_i + (3 * nslot + 3) / 4 * 4;          // 16-byte aligned
     float* p_lds = (float*)rest + (size_t)w * 64 * EPL;
     for (int b = w; b < a.B; b += nw)
         topk_wave<EPL>(a.logits + (size_t)b * a.E, a.E, a.topk, a.renorm, p_lds,
@@ -252,16 +271,17 @@ k_select(RouteArgs a) {
         a.tw[i] = tw_l[i];
     }
     dispatch_block(top_l, nslot, a.E, a.topk, rest, a.seg_off, a.seg_slot, a.active, a.n_active,
-                   a.first_slot, a.comb, a.rank_scratch, a.work, a.umax, a.rec_off, a.LE, a.key0);
+                   a.first_slot, a.comb, rank_l, a.work, a.umax, &rec);
 }
 
 // Dispatch and work table alone, after the multi-block top-k (large B).
 __global__ void __launch_bounds__(1024)
 k_dispatch_work(RouteArgs a) {
     extern __shared__ int lds_i[];
+    ExpertRec rec;
+    if ((int)threadIdx.x < a.E) rec = load_expert_rec(a.rec_off, a.LE, a.key0, threadIdx.x);
     dispatch_block(a.top, a.B * a.topk, a.E, a.topk, lds_i, a.seg_off, a.seg_slot, a.active,
-                   a.n_active, a.first_slot, a.comb, a.rank_scratch, a.work, a.umax, a.rec_off, a.LE,
-                   a.key0);
+                   a.n_active, a.first_slot, a.comb, a.rank_scratch, a.work, a.umax, &rec);
 }
 
 static size_t dispatch_lds_bytes(int E) { return (size_t)dispatch_lds_ints(E) * 4; }
@@ -281,7 +301,7 @@ hipError_t launch_route(const RouteArgs& a, hipStream_t st) {
     if (e != hipSuccess) return e;
     const int epl = a.E <= 64 ? 1 : a.E <= 128 ? 2 : a.E <= 256 ? 4 : 8;
     if (a.B <= 64) {
-        const size_t lds = (size_t)2 * a.B * a.topk * 4 + std::max((size_t)16 * 64 * epl * 4, dispatch_lds_bytes(a.E));
+        const size_t lds = (size_t)(3 * a.B * a.topk + 3) / 4 * 16 + std::max((size_t)16 * 64 * epl * 4, dispatch_lds_bytes(a.E));
 #define JM_SEL(EPL) hipLaunchKernelGGL(k_select<EPL>, dim3(1), dim3(1024), lds, st, a)
         if (epl == 1) JM_SEL(1); else if (epl == 2) JM_SEL(2); else if (epl == 4) JM_SEL(4); else JM_SEL(8);
 #undef JM_SEL
