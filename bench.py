@@ -37,6 +37,17 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
 
+# HBM traffic of one k_gateup launch on the default workload (B=8, group 64,
+# 16 rotating layers), measured by two rocprofv3 --pmc runs of this script
+# (FETCH_SIZE, then WRITE_SIZE; --steps 48 --warmup 16 --calib-copy-mib 256),
+# averaged over every k_gateup dispatch.  Each counter is scaled by what it
+# reads for the 256 MiB copy in the same run: FETCH_SIZE reports half of the
+# copied bytes (factor 2.0), WRITE_SIZE all of them (factor 1.0).
+GATEUP_PMC = {"batch": 8, "group": 64, "layers": 16,
+              "fetch_kib": 42098.2, "fetch_factor": 2.0,
+              "write_kib": 336.1, "write_factor": 1.0,
+              "source": "profiles/pmc_traffic_qwen3_b8.md"}
+
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -182,6 +193,9 @@ def main() -> int:
     ap.add_argument("--group", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after timing, run 8 torch copies of this many MiB (a known-size kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -210,6 +224,16 @@ def main() -> int:
     main_res = block_numbers(shape, G, B, ms, stages, U, args.steps, NL, rb)
     log(f"B={B}: {main_res['tok_per_s']:.0f} tok/s, {ms * 1e3:.1f} us/step, block "
         f"{main_res['block_GBs']:.0f} GB/s, gate/up {main_res['gateup_GBs']:.0f} GB/s, stages {stages}")
+
+    if args.calib_copy_mib > 0:
+        n = args.calib_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log(f"ran 8 copies of {args.calib_copy_mib} MiB for counter calibration")
 
     sweep = {}
     if not args.no_sweep:
@@ -241,6 +265,10 @@ def main() -> int:
             log(f"sweep olmoe B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s")
 
     gu_ms = stages["gateup"]
+    traffic = None
+    if (B, G, NL) == (GATEUP_PMC["batch"], GATEUP_PMC["group"], GATEUP_PMC["layers"]):
+        traffic = 1024.0 * (GATEUP_PMC["fetch_kib"] * GATEUP_PMC["fetch_factor"]
+                            + GATEUP_PMC["write_kib"] * GATEUP_PMC["write_factor"])
     res = {
         "metric": "MoE decode tok/s + achieved HBM GB/s, Qwen3-30B-A3B-shape Q4, B=1 and B=8",
         "value": main_res["tok_per_s"],
@@ -260,7 +288,8 @@ def main() -> int:
                    "intermediate": shape.m, "group": G, "layers_rotated": NL},
         "roofline": {"bound": "hbm", "kernel": "k_gateup",
                      "achieved": main_res["gateup_GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": main_res["gateup_GBs"] / PEAK_HBM_GBS, "traffic": None,
+                     "frac": main_res["gateup_GBs"] / PEAK_HBM_GBS, "traffic": traffic,
+                     "traffic_source": GATEUP_PMC["source"] if traffic else None,
                      "bytes_per_launch": main_res["gateup_bytes"], "avg_launch_ms": gu_ms},
         "block": {k: main_res[k] for k in ("bytes_alg", "block_GBs", "block_frac", "experts_routed_avg",
                                            "down_GBs")},

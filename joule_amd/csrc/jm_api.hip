@@ -338,7 +338,10 @@ int jm_store_profile(jm_store* s, int enable) {
     if (int rc = check_store(s)) return rc;
     JM_HIP(hipSetDevice(s->device), "hipSetDevice");
     if (enable && !s->prof) {
-        for (int i = 0; i <= JM_STAGES; i++) JM_HIP(hipEventCreate(&s->ev[i]), "hipEventCreate");
+        // no system-scope fence: the marks then cost the stream little more
+        // than the kernels' own boundaries
+        for (int i = 0; i <= JM_STAGES; i++)
+            JM_HIP(hipEventCreateWithFlags(&s->ev[i], hipEventDisableSystemFence), "hipEventCreate");
         s->prof = 1;
     } else if (!enable && s->prof) {
         JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
