@@ -68,7 +68,8 @@ int jm_version(void);
 const char* jm_last_error(void);
 
 /* sizeof(jm_kernel_cfg) and the compile-time kernel parameters: digits per
- * activation value in the Q4 dot, tokens per pass over an expert. */
+ * activation value in the Q4 dot, and rows per gate/up work item (the
+ * number of act values that share one digit scale). */
 int jm_abi_sizes(int* kernel_cfg_bytes, int* ndig, int* nt);
 
 /*
@@ -90,9 +91,11 @@ int jm_store_destroy(jm_store* s);
 
 /* Router weights, the reference's KernelW.gate_w [L][E][d]
  * (decode_kernel.c:303).  dtype JM_DTYPE_BF16 takes the reference's bf16
- * table as is; JM_DTYPE_F32 takes float32.  The store keeps its own float32
- * copy laid out residue-major (w[e][r][t] = gate_w[e][8t + r]); the caller's
- * table may be freed after the call.  Synchronises the device. */
+ * table as is; JM_DTYPE_F32 takes float32.  The store keeps its own copy,
+ * in bf16 when every weight is exactly a bf16 value and in float32
+ * otherwise, with the 8 FMA chains of 8 experts interleaved for coalesced
+ * loads; the caller's table may be freed after the call.  Synchronises the
+ * device. */
 int jm_store_set_router(jm_store* s, const void* gate_w, int dtype);
 
 /* The element type the store's router copy holds: JM_DTYPE_BF16 when every

@@ -164,7 +164,7 @@ const char* jm_last_error(void) { return g_err; }
 int jm_abi_sizes(int* kernel_cfg_bytes, int* ndig, int* nt) {
     if (kernel_cfg_bytes) *kernel_cfg_bytes = (int)sizeof(jm_kernel_cfg);
     if (ndig) *ndig = JM_NDIG;
-    if (nt) *nt = JM_NT;
+    if (nt) *nt = 8;
     return 0;
 }
 

@@ -10,10 +10,6 @@
 #ifndef JM_NDIG
 #define JM_NDIG 4
 #endif
-// Tokens of one expert segment processed per pass over the expert's rows.
-#ifndef JM_NT
-#define JM_NT 4
-#endif
 
 // Limits of the kernels: experts per layer (top-k keeps E/64 values per lane,
 // dispatch keeps per-expert counts in LDS) and slots (B*topk) per call.
