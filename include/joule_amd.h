@@ -122,16 +122,20 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
                        int32_t* topk_idx, float* topk_w, void* stream);
 
 /* Per-stage timing.  With profiling on, jm_layer_ffn_batch records a HIP
- * event around each of its JM_STAGES stages (route: router scores + digits,
- * then top-k + dispatch; gate/up; down; combine); jm_store_stage_ms waits
- * for the last call and returns the elapsed milliseconds of each stage. */
-#define JM_STAGES 4
+ * event around each of its JM_STAGES stages (route: router scores, top-k and
+ * x digits, plus the dispatch when B * topk > 256; gate/up; down with the
+ * combine); jm_store_stage_ms waits for the last call and returns the
+ * elapsed milliseconds of each stage. */
+#define JM_STAGES 3
 int jm_store_profile(jm_store* s, int enable);
 int jm_store_stage_ms(jm_store* s, float* ms, int n);
 
 /* Copy an intermediate of the last jm_layer_ffn_batch call out of the
  * store's workspace into caller device memory (stream-ordered), for tests and
- * profiling.  `bytes` must not exceed the field's size at the last call's B:
+ * profiling.  `bytes` must not exceed the field's size at the last call's B.
+ * Calls with B * topk <= 256 write only JM_WS_LOGITS and JM_WS_ACT (their
+ * dispatch is a ballot inside the expert kernels and their combine runs in
+ * the down kernel); the other fields are then an error:
  *   JM_WS_LOGITS     float [B][E] router scores
  *   JM_WS_SEG_OFF    int32 [E+1] segment starts (slots grouped by expert)
  *   JM_WS_SEG_SLOT   int32 [B*topk] slot ids b*topk+i grouped by expert

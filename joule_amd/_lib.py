@@ -49,7 +49,7 @@ class KernelCfg(ctypes.Structure):
                 ("norm_topk_prob", _i), ("expert_i8", _i), ("expert_bf16", _i)]
 
 
-STAGES = ("route", "gateup", "down", "combine")
+STAGES = ("route", "gateup", "down")
 
 # jm_store_copy_workspace fields
 WS_LOGITS, WS_SEG_OFF, WS_SEG_SLOT, WS_ACTIVE, WS_N_ACTIVE, WS_FIRST_SLOT, WS_ACT, WS_Y = range(8)

@@ -66,6 +66,10 @@ struct jm_store {
     const uint8_t* blob;
     uint64_t blob_bytes;
     uint64_t* off_dev;          // [3][L*E][2]
+    jm::RecLoc rec;             // record locator (the table, or the affine formula)
+    int dec_last;               // the last call took the decode path
+    int n_cu;                   // compute units of the device (persistent grids)
+    int lds_max;                // LDS bytes one block may use
     void* wt;                   // [L][Ep/8][d/8/P][64][P] interleaved copy of the router table
     int wt_bf16;                // the copy holds bf16 (the table is exactly bf16-valued)
     int device;
@@ -208,12 +212,41 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
     s->device = attr.device;
     const size_t ob = (size_t)3 * L * E * 2 * sizeof(uint64_t);
     hipError_t e = hipSetDevice(s->device);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&s->n_cu, hipDeviceAttributeMultiprocessorCount, s->device);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&s->lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, s->device);
     if (e == hipSuccess) e = hipMalloc(&s->off_dev, ob);
     if (e == hipSuccess) e = hipMemcpy(s->off_dev, offsets, ob, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         if (s->off_dev) (void)hipFree(s->off_dev);
         delete s;
         return hip_fail(e, "jm_store_create offset table");
+    }
+    // records at base + key * stride + a per-part offset (the reference's
+    // converter writes (layer, expert, part) in order): locate them by formula
+    s->rec.table = (const unsigned long long*)s->off_dev;
+    s->rec.LE = (long long)L * E;
+    s->rec.affine = 0;
+    {
+        const uint64_t* o = offsets;
+        const size_t LE = (size_t)L * E;
+        const uint64_t base = o[0];
+        const uint64_t stride = LE > 1 ? o[2] - o[0] : 0;
+        bool affine = LE == 1 || o[2] > o[0];
+        uint64_t so[3], po[3];
+        for (int p = 0; p < 3 && affine; p++) {
+            so[p] = o[(size_t)p * LE * 2 + 0] - base;
+            po[p] = o[(size_t)p * LE * 2 + 1] - base;
+            for (size_t i = 0; i < LE && affine; i++) {
+                const uint64_t b = base + i * stride;
+                affine = o[((size_t)p * LE + i) * 2 + 0] == b + so[p] && o[((size_t)p * LE + i) * 2 + 1] == b + po[p];
+            }
+        }
+        if (affine) {
+            s->rec.affine = 1;
+            s->rec.base = base;
+            s->rec.stride = stride;
+            for (int p = 0; p < 3; p++) { s->rec.so[p] = so[p]; s->rec.po[p] = po[p]; }
+        }
     }
     *out = s;
     return 0;
@@ -304,6 +337,8 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     const int E = s->E, d = s->d, k = s->topk, G = s->group;
     JM_HIP(hipSetDevice(s->device), "hipSetDevice");
     const int umax = std::min(E, B * k);
+    const int nslot = B * k;
+    const bool dec = nslot <= JM_DEC_SLOTS;
     jm::RouteArgs r;
     r.wt = (const char*)s->wt + (size_t)layer * jm::router_experts_padded(E) * d * (s->wt_bf16 ? 2 : 4);
     r.wt_bf16 = s->wt_bf16;
@@ -311,23 +346,32 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     r.logits = s->logits; r.xdig = s->xdig; r.xscale = s->xscale; r.top = s->top; r.tw = s->tw;
     r.seg_off = s->seg_off; r.seg_slot = s->seg_slot; r.active = s->active; r.n_active = s->n_active;
     r.first_slot = s->first_slot; r.comb = s->comb; r.rank_scratch = s->rank;
-    r.work = s->work; r.umax = umax; r.rec_off = (const unsigned long long*)s->off_dev;
-    r.LE = (long long)s->L * E; r.key0 = (long long)layer * E;
+    r.work = s->work; r.umax = umax; r.rec = s->rec;
+    r.key0 = (long long)layer * E;
     jm::ExpertArgs a;
-    a.blob = s->blob; a.work = s->work; a.umax = umax; a.d = d; a.m = s->m; a.topk = k; a.group = G;
-    a.seg_slot = s->seg_slot; a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
-    a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y;
+    a.blob = s->blob; a.rec = s->rec; a.key0 = (long long)layer * E; a.E = E;
+    a.work = s->work; a.umax = umax; a.seg_slot = s->seg_slot;
+    a.top = s->top; a.nslot = nslot; a.B = B;
+    a.d = d; a.m = s->m; a.topk = k; a.group = G;
+    a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
+    a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y; a.out = out;
 #define JM_MARK(i) if (s->prof) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
     JM_MARK(0);
-    JM_HIP(jm::launch_route(r, st), "route launch");
+    JM_HIP(jm::launch_route_tok(r, st), "route launch");
+    if (!dec) JM_HIP(jm::launch_dispatch_work(r, st), "dispatch launch");
     JM_MARK(1);
-    JM_HIP(jm::launch_gateup(a, umax, st), "gate/up launch");
+    if (dec) JM_HIP(jm::launch_gateup_dec(a, st), "gate/up launch");
+    else JM_HIP(jm::launch_gateup(a, umax, st), "gate/up launch");
     JM_MARK(2);
-    JM_HIP(jm::launch_down(a, umax, st), "down launch");
+    if (dec) {
+        JM_HIP(jm::launch_down_comb(a, st), "down/combine launch");
+    } else {
+        JM_HIP(jm::launch_down(a, umax, st), "down launch");
+        JM_HIP(jm::launch_combine(s->y, s->comb, B, k, d, out, st), "combine launch");
+    }
     JM_MARK(3);
-    JM_HIP(jm::launch_combine(s->y, s->comb, B, k, d, out, st), "combine launch");
-    JM_MARK(4);
 #undef JM_MARK
+    s->dec_last = dec;
     s->last_B = B;
     if (topk_idx) JM_HIP(hipMemcpyAsync(topk_idx, s->top, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k");
     if (topk_w) JM_HIP(hipMemcpyAsync(topk_w, s->tw, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k weights");
@@ -379,6 +423,8 @@ int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t by
         default: return fail(JM_ERR_ARG, "unknown workspace field %d", field);
     }
     if (!src || s->last_B == 0) return fail(JM_ERR_ARG, "no call has run on this store yet");
+    if (s->dec_last && field != JM_WS_LOGITS && field != JM_WS_ACT)
+        return fail(JM_ERR_ARG, "field %d is written only by the dispatch path (B * topk > %d)", field, JM_DEC_SLOTS);
     if (bytes > cap) return fail(JM_ERR_ARG, "%llu bytes requested, field holds %zu", (unsigned long long)bytes, cap);
     JM_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "workspace copy");
     return 0;

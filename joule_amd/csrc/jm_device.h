@@ -207,6 +207,20 @@ __device__ __forceinline__ float transpose_sum(float (&v)[W / 4]) {
     return t;
 }
 
+// Totals of N partial sums per lane over aligned segments of W lanes
+// (N = 1 .. W/4): transposing levels at distances W/2 .. W/N, then plain sums
+// over the W/N lanes that share a value.  Value v ends in the lanes with
+// (lane % W) / (W / N) == v; returned.
+template <int W, int N>
+__device__ __forceinline__ float transpose_reduce(float (&v)[N]) {
+    static_assert(N >= 1 && W / N >= 4 && (N & (N - 1)) == 0, "N a power of two, at most W/4");
+    if constexpr (N >= 2) transpose_level<W / 2, N>(v);
+    if constexpr (N >= 4) transpose_level<W / 4, N / 2>(v);
+    if constexpr (N >= 8) transpose_level<W / 8, N / 4>(v);
+    if constexpr (N >= 16) transpose_level<W / 16, N / 8>(v);
+    return seg_sum<W / N>(v[0]);
+}
+
 template <int W>
 __device__ __forceinline__ float seg_max(float v) {
     if (W >= 2) v = fmaxf(v, dpp_f<DPP_XOR1>(v));
@@ -405,24 +419,162 @@ __device__ __forceinline__ uint2 block_exclusive_scan2(uint2 v, unsigned* wsum, 
     return make_uint2(offa + a - v.x, offb + b - v.y);
 }
 
-// Record offsets of expert e (one per part: scales, packed) from the store's
-// [3][L*E][2] table at key0 = layer * E; loaded by the expert's own thread at
-// the start of a dispatch so that they are in registers when its work entry
-// is written.
+// Where the records of (part p, key l*E+e) lie in the store blob: the
+// store's [3][L*E][2] table of (scales, packed) offsets or, when every
+// record sits at base + key * stride + a per-part offset (a store written in
+// (layer, expert, part) order, as the reference's converter writes it), that
+// formula, which costs no load.
+struct RecLoc {
+    const unsigned long long* table;   // [3][LE][2]
+    long long LE;
+    int affine;
+    unsigned long long base, stride, so[3], po[3];
+
+    __device__ __forceinline__ void get(int p, long long key, unsigned long long& sc,
+                                        unsigned long long& pk) const {
+        if (affine) {
+            const unsigned long long o = base + (unsigned long long)key * stride;
+            sc = o + so[p];
+            pk = o + po[p];
+        } else {
+            sc = table[((long long)p * LE + key) * 2 + 0];
+            pk = table[((long long)p * LE + key) * 2 + 1];
+        }
+    }
+};
+
+// Record offsets of expert e (one per part: scales, packed) at key0 =
+// layer * E; loaded by the expert's own thread at the start of a dispatch so
+// that they are in registers when its work entry is written.
 struct ExpertRec {
     unsigned long long sc[3], pk[3];
 };
 
-__device__ __forceinline__ ExpertRec load_expert_rec(const unsigned long long* __restrict__ rec_off,
-                                                     long long LE, long long key0, int e) {
+__device__ __forceinline__ ExpertRec load_expert_rec(const RecLoc& rl, long long key0, int e) {
     ExpertRec r;
 #pragma unroll
-    for (int p = 0; p < 3; p++) {
-        r.sc[p] = rec_off[((long long)p * LE + key0 + e) * 2 + 0];
-        r.pk[p] = rec_off[((long long)p * LE + key0 + e) * 2 + 1];
-    }
+    for (int p = 0; p < 3; p++) rl.get(p, key0 + e, r.sc[p], r.pk[p]);
     return r;
 }
+
+// The slots of one expert on the decode path (B * topk <= 256 slots): a
+// ballot over the top-k table of every slot.  Slots come out in increasing
+// order, the order of the reference's slot lists (decode_kernel.c:1459-1485).
+struct BallotSlots {
+    unsigned long long m0, m1, m2, m3;
+    int n;
+
+    // Loads top[0..nslot) (lane l holds slots l, l + 64, ...) and ballots
+    // the slots routed to the expert of slot s.  False when slot s has no
+    // expert or an earlier slot has the same expert: then another wave item
+    // (that of the expert's first slot) covers it.  *e receives the expert.
+    __device__ __forceinline__ bool init(const int* __restrict__ top, int nslot, int E, int s, int* e) {
+        const int lane = threadIdx.x & 63;
+        const int t0 = lane < nslot ? top[lane] : -1;
+        const int t1 = nslot > 64 && lane + 64 < nslot ? top[lane + 64] : -1;
+        const int t2 = nslot > 128 && lane + 128 < nslot ? top[lane + 128] : -1;
+        const int t3 = nslot > 192 && lane + 192 < nslot ? top[lane + 192] : -1;
+        const int j = s >> 6;
+        const int tj = j == 0 ? t0 : j == 1 ? t1 : j == 2 ? t2 : t3;
+        const int ex = __builtin_amdgcn_readlane(tj, s & 63);
+        *e = ex;
+        if (ex < 0 || ex >= E) return false;
+        set(t0, t1, t2, t3, ex);
+        const int lowest = m0 ? __builtin_ctzll(m0) : m1 ? 64 + __builtin_ctzll(m1)
+                         : m2 ? 128 + __builtin_ctzll(m2) : 192 + __builtin_ctzll(m3);
+        return lowest == s;
+    }
+
+    // The slots of expert e from a top-k table in LDS.
+    __device__ __forceinline__ void init_lds(const int* top_lds, int nslot, int e) {
+        const int lane = threadIdx.x & 63;
+        const int t0 = lane < nslot ? top_lds[lane] : -1;
+        const int t1 = lane + 64 < nslot ? top_lds[lane + 64] : -1;
+        const int t2 = lane + 128 < nslot ? top_lds[lane + 128] : -1;
+        const int t3 = lane + 192 < nslot ? top_lds[lane + 192] : -1;
+        set(t0, t1, t2, t3, e);
+    }
+
+    __device__ __forceinline__ void set(int t0, int t1, int t2, int t3, int e) {
+        m0 = __ballot(t0 == e);
+        m1 = __ballot(t1 == e);
+        m2 = __ballot(t2 == e);
+        m3 = __ballot(t3 == e);
+        n = __popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3);
+    }
+
+    // The next slot in increasing order (n calls in all).
+    __device__ __forceinline__ int next() {
+        if (m0) { const int s = __builtin_ctzll(m0); m0 &= m0 - 1; return s; }
+        if (m1) { const int s = __builtin_ctzll(m1); m1 &= m1 - 1; return 64 + s; }
+        if (m2) { const int s = __builtin_ctzll(m2); m2 &= m2 - 1; return 128 + s; }
+        const int s = __builtin_ctzll(m3);
+        m3 &= m3 - 1;
+        return 192 + s;
+    }
+};
+
+// Decode-path routing summary in LDS, computed by a whole block of at least
+// JM_DEC_SLOTS threads (nslot <= JM_DEC_SLOTS): the top-k table (top_l),
+// each expert's first slot (first_l, INT_MAX for unrouted experts) and the
+// union list (ulist: the slots that are their expert's first, in slot order:
+// the reference's union order, decode_kernel.c:1449-1485).  wcnt is LDS
+// scratch of JM_DEC_SLOTS / 64 ints.  Returns the union length U.  Every
+// thread must call it; it ends with a barrier.
+template <int NSLOTS>
+__device__ __forceinline__ int decode_union(const int* __restrict__ top, int nslot, int E, int* top_l,
+                                            int* first_l, int* ulist, int* wcnt, int* e_out = nullptr) {
+    constexpr int NSW = NSLOTS / 64;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (tid < nslot) top_l[tid] = top[tid];
+    for (int i = tid; i < E; i += blockDim.x) first_l[i] = 0x7FFFFFFF;
+    __syncthreads();
+    int e_me = -1;
+    if (tid < nslot) {
+        const int e = top_l[tid];
+        if (e >= 0 && e < E) {
+            e_me = e;
+            atomicMin(&first_l[e], tid);
+        }
+    }
+    __syncthreads();
+    const bool first = e_me >= 0 && first_l[e_me] == tid;
+    const unsigned long long fm = __ballot(first);
+    if (w < NSW && lane == 0) wcnt[w] = __popcll(fm);
+    __syncthreads();
+    int U = 0, before = 0;
+#pragma unroll
+    for (int j = 0; j < NSW; j++) {
+        const int cj = wcnt[j];
+        before += j < w ? cj : 0;
+        U += cj;
+    }
+    if (first) ulist[before + __popcll(fm & ((1ull << lane) - 1ull))] = tid;
+    if (e_out) *e_out = e_me;
+    __syncthreads();
+    return U;
+}
+
+// The slots of one work-table entry (dispatch path): seg_slot[s0 .. s0+n),
+// the first 64 held one per lane.
+struct TableSlots {
+    const int* seg_slot;
+    int s0, n, slotv, t;
+
+    __device__ __forceinline__ void init(const int* __restrict__ ss, int start, int count) {
+        const int lane = threadIdx.x & 63;
+        seg_slot = ss;
+        s0 = start;
+        n = count;
+        slotv = lane < count ? ss[start + lane] : 0;
+        t = 0;
+    }
+
+    __device__ __forceinline__ int next() {
+        const int i = t++;
+        return i < 64 ? __builtin_amdgcn_readlane(slotv, i) : seg_slot[s0 + i];
+    }
+};
 
 // LDS of dispatch_block, in ints
 __host__ __device__ constexpr int dispatch_lds_ints(int E) { return DISP_CHUNKS_C * E + 2 * E + 1 + 32; }

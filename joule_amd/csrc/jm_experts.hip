@@ -1,24 +1,29 @@
-// Grouped Q4 expert product of the MoE block (gfx950), three launches:
+// Grouped Q4 expert product of the MoE block (gfx950).
 //
-//   k_gateup   per (active expert, 8 intermediate rows), one wave:
-//              g = gate_row . x, u = up_row . x for every token routed to the
-//              expert, act = (g / (1 + expf_fast(-g))) * u
-//              (decode_kernel.c:1365-1375), and the 8 act values re-encoded
-//              as digits with one scale for the down pass
-//   k_down     per (active expert, 16 hidden rows), one wave:
-//              y[slot][r] = w_slot * (down_row . act_slot) (:1376-1383)
-//   k_combine  out[b] = the token's k expert rows summed in the reference's
-//              union order (:1502-1507)
+// Decode path (B * topk <= 256 slots), two launches after the routing:
+//   k_gateup<BALLOT>  per (slot, 8 intermediate rows), one wave; the wave of
+//                     an expert's first slot finds all its slots by a ballot
+//                     over the top-k table (others exit) and computes
+//                     g = gate_row . x, u = up_row . x for each of them,
+//                     act = (g / (1 + expf_fast(-g))) * u
+//                     (decode_kernel.c:1365-1375), and the 8 act values
+//                     re-encoded as digits with one scale for the down pass
+//   k_down_comb       per chunk of 8 hidden rows, one block: every routed
+//                     expert's rows against the act of each of its slots,
+//                     y = w_slot * (down_row . act) (:1376-1383) into LDS,
+//                     then out[b][rows] = the token's k values summed in the
+//                     reference's union order (:1502-1507)
+// Dispatch path (more slots): the same gate/up over the work table the
+// dispatch kernel writes, k_down per (expert, 16 hidden rows) into y, and
+// k_combine.
 //
 // Lane layout: a row of C columns is read as C/32 chunks of 16 bytes (32
 // packed weights); lane col of an LPR-lane row segment holds chunks col,
 // col + LPR, ... so that each load instruction of a wave covers whole rows
 // of contiguous memory (one 1 KiB row per instruction for C = 2048).  A wave
 // item issues every weight load of its rows before any arithmetic; the
-// registers then serve each token of the expert's segment in turn while the
-// next token's digits load.  Waves are independent: no barriers, no LDS.
-// The work table (written by the dispatch, longest segments first) gives a
-// wave its expert, segment and record offsets in one scalar load.
+// registers then serve each token of the expert in turn while the next
+// token's digits load.
 //
 // The chunk dot runs on v_dot8_i32_i4: the packed nibbles XOR 0x8 are the
 // signed values q - 8, and each activation value is given as NDIG signed
@@ -58,7 +63,7 @@ constexpr int DN_ROWS = 16;    // down rows per wave item
 
 // ------------------------------------------------------------------ gate/up
 
-template <int G, int NDIG, int LPR, int QC>
+template <int G, int NDIG, int LPR, int QC, bool BALLOT>
 __global__ void __launch_bounds__(256)
 k_gateup(ExpertArgs a) {
     constexpr int RPI = JM_WAVE / LPR;
@@ -67,17 +72,35 @@ k_gateup(ExpertArgs a) {
     const int item = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nchunk = a.m / GU_ROWS;
     const int u = item / nchunk, c = item % nchunk;
-    if (u >= a.umax) return;
-    const ExpertWork wk = a.work[u];
-    if (wk.n == 0) return;
-    const int slotv = lane < wk.n ? a.seg_slot[wk.s0 + lane] : 0;   // slots of the first 64 tokens
+    // the expert, its record offsets and its slots
+    unsigned long long so_g, po_g, so_u, po_u;
+    int n;
+    BallotSlots bs;
+    TableSlots ts;
+    if constexpr (BALLOT) {
+        if (u >= a.nslot) return;
+        int e;
+        if (!bs.init(a.top, a.nslot, a.E, u, &e)) return;
+        n = bs.n;
+        a.rec.get(0, a.key0 + e, so_g, po_g);
+        a.rec.get(1, a.key0 + e, so_u, po_u);
+    } else {
+        if (u >= a.umax) return;
+        const ExpertWork wk = a.work[u];
+        if (wk.n == 0) return;
+        n = wk.n;
+        ts.init(a.seg_slot, wk.s0, wk.n);
+        so_g = wk.sc[0]; po_g = wk.pk[0];
+        so_u = wk.sc[1]; po_u = wk.pk[1];
+    }
+    auto next_slot = [&]() { if constexpr (BALLOT) return bs.next(); else return ts.next(); };
     const int col = lane & (LPR - 1), rsub = lane / LPR;
     const int cpr = a.d / 32, ngroups = a.d / G;
     const int row0 = c * GU_ROWS + rsub;
-    const uint8_t* pk_g = a.blob + wk.pk[0];
-    const uint16_t* sc_g = (const uint16_t*)(a.blob + wk.sc[0]);
-    const uint8_t* pk_u = a.blob + wk.pk[1];
-    const uint16_t* sc_u = (const uint16_t*)(a.blob + wk.sc[1]);
+    const uint8_t* pk_g = a.blob + po_g;
+    const uint16_t* sc_g = (const uint16_t*)(a.blob + so_g);
+    const uint8_t* pk_u = a.blob + po_u;
+    const uint16_t* sc_u = (const uint16_t*)(a.blob + so_u);
 
     // chunks past the row (lanes beyond C/32) read chunk 0 and count zero:
     // every load is unconditional, so the loads of all steps are in flight
@@ -124,7 +147,7 @@ k_gateup(ExpertArgs a) {
     // (the memory counter retires loads in order), but nothing is issued late
     __builtin_amdgcn_sched_barrier(0);
     ChunkDigits<NDIG> cur[QC], nxt[QC];
-    int slot = __builtin_amdgcn_readlane(slotv, 0);
+    int slot = next_slot();
     load_tok(cur, slot);
     __builtin_amdgcn_sched_barrier(0);
     // signed nibbles once, for every token
@@ -137,10 +160,10 @@ k_gateup(ExpertArgs a) {
     // LPR * r + 8 * s (gate) and + 4 (up)
     const int i8 = lane & 7;
     const int src = LPR * (i8 % RPI) + 8 * (i8 / RPI);
-    for (int t = 0; t < wk.n; t++) {
+    for (int t = 0; t < n; t++) {
         int nslot = 0;
-        if (t + 1 < wk.n) {
-            nslot = t + 1 < 64 ? __builtin_amdgcn_readlane(slotv, t + 1) : a.seg_slot[wk.s0 + t + 1];
+        if (t + 1 < n) {
+            nslot = next_slot();
             load_tok(nxt, nslot);
         }
         float part[2 * S];                   // value 2s + m: step s, m = 0 gate, 1 up
@@ -172,7 +195,7 @@ k_gateup(ExpertArgs a) {
         if (lane < 8) a.act[(size_t)slot * a.m + c * GU_ROWS + lane] = mine;
         const size_t ai = (size_t)slot * (a.m / 8) + c;
         encode_group_wave<8, NDIG>(mine, lane < 8, a.adig + ai * NDIG, a.ascale + ai);
-        if (t + 1 < wk.n) {
+        if (t + 1 < n) {
             slot = nslot;
 #pragma unroll
             for (int q = 0; q < QC; q++) cur[q] = nxt[q];
@@ -194,7 +217,8 @@ k_down(ExpertArgs a) {
     if (u >= a.umax) return;
     const ExpertWork wk = a.work[u];
     if (wk.n == 0) return;
-    const int slotv = lane < wk.n ? a.seg_slot[wk.s0 + lane] : 0;
+    TableSlots ts;
+    ts.init(a.seg_slot, wk.s0, wk.n);
     const int col = lane & (LPR - 1), rsub = lane / LPR;
     const int cpr = a.m / 32, ngroups = a.m / G;
     const int row0 = c * DN_ROWS + rsub;
@@ -242,7 +266,7 @@ k_down(ExpertArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     uint32_t cd[QC][4][NDIG], nd[QC][4][NDIG];
     float4 cs[QC], ns[QC];
-    int slot = __builtin_amdgcn_readlane(slotv, 0);
+    int slot = ts.next();
     float wt = a.tw[slot];
     load_act(cd, cs, slot);
     __builtin_amdgcn_sched_barrier(0);
@@ -255,7 +279,7 @@ k_down(ExpertArgs a) {
         int nslot = 0;
         float nwt = 0.0f;
         if (t + 1 < wk.n) {
-            nslot = t + 1 < 64 ? __builtin_amdgcn_readlane(slotv, t + 1) : a.seg_slot[wk.s0 + t + 1];
+            nslot = ts.next();
             nwt = a.tw[nslot];
             load_act(nd, ns, nslot);
         }
@@ -299,6 +323,183 @@ k_down(ExpertArgs a) {
     }
 }
 
+// ---------------------------------------------------------- down + combine
+
+constexpr int DC_ROWS = 8;             // hidden rows per block
+constexpr int DC_THREADS = 512;
+constexpr int DC_WAVES = DC_THREADS / 64;
+
+// Decode path: block c owns hidden rows [c * DC_ROWS, (c + 1) * DC_ROWS) of
+// every token.  It lists the routed experts in the reference's union order
+// (first appearance over the slots); wave w takes experts w, w + 8, ...,
+// keeping NR of them in flight (each expert's rows, and the act digits of
+// its first slot, requested in that order), writes w_slot * (rows . act_slot)
+// for each slot into LDS, and finally sums each token's values in union
+// order.  Every block streams the same bytes: the rows of all routed
+// experts.
+template <int G, int NDIG, int LPR, int QC>
+__global__ void __launch_bounds__(DC_THREADS)
+k_down_comb(ExpertArgs a) {
+    constexpr int R = DC_ROWS;
+    constexpr int RPI = JM_WAVE / LPR;          // rows per load instruction
+    constexpr int S = R / RPI;                  // load steps per expert
+    static_assert(S >= 1 && S * RPI == R, "whole rows per step");
+    constexpr int NR = S * QC <= 4 ? 4 : 2;     // experts in flight per wave
+    static_assert(JM_DEC_SLOTS <= DC_THREADS, "a slot per thread");
+    __shared__ int top_l[JM_DEC_SLOTS], ulist[JM_DEC_SLOTS], comb_l[JM_DEC_SLOTS];
+    __shared__ int first_l[JM_MAX_E];
+    __shared__ float tw_l[JM_DEC_SLOTS];
+    __shared__ float ypart[JM_DEC_SLOTS * R];
+    __shared__ int wcnt[JM_DEC_SLOTS / 64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = blockIdx.x;
+    const int nslot = a.nslot, E = a.E, k = a.topk;
+
+    if (tid < nslot) tw_l[tid] = a.tw[tid];
+    int e_me;
+    const int U = decode_union<JM_DEC_SLOTS>(a.top, nslot, E, top_l, first_l, ulist, wcnt, &e_me);
+    // each token's slots ranked by the first slot of their expert (distinct
+    // experts -> distinct keys); slots without an expert last, as -1
+    if (tid < nslot) {
+        const int b = tid / k, i = tid % k;
+        const int key = e_me >= 0 ? first_l[e_me] : 0x7FFFFFFF;
+        int rnk = 0;
+        for (int j = 0; j < k; j++) {
+            const int ej = top_l[b * k + j];
+            const int kj = (ej >= 0 && ej < E) ? first_l[ej] : 0x7FFFFFFF;
+            rnk += (kj < key) || (kj == key && j < i);
+        }
+        comb_l[b * k + rnk] = e_me >= 0 ? tid : -1;
+    }
+    __syncthreads();
+
+    const int col = lane & (LPR - 1), rsub = lane / LPR;
+    const int cpr = a.m / 32, ngroups = a.m / G;
+    // chunks past the row read chunk 0 and count zero (unconditional loads)
+    bool live[QC];
+    int chk[QC], grp[QC];
+#pragma unroll
+    for (int q = 0; q < QC; q++) {
+        const int ch = col + LPR * q;
+        live[q] = ch < cpr;
+        chk[q] = live[q] ? ch : 0;
+        grp[q] = chk[q] * 32 / G;
+    }
+    // act digits of a chunk: 4 groups of 8 values, NDIG words each, 4 scales
+    struct Act {
+        uint32_t dg[QC][4][NDIG];
+        float4 sc[QC];
+    };
+    auto load_act = [&](Act& ad, int slot) {
+#pragma unroll
+        for (int q = 0; q < QC; q++) {
+            const size_t ai = (size_t)slot * (a.m / 8) + (size_t)chk[q] * 4;
+            const uint4* p = (const uint4*)(a.adig + ai * NDIG);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                static_assert(NDIG == 4, "act digit loads assume 4 digits (one uint4 per 8 values)");
+                const uint4 v = p[j];
+                ad.dg[q][j][0] = v.x; ad.dg[q][j][1] = v.y; ad.dg[q][j][2] = v.z; ad.dg[q][j][3] = v.w;
+            }
+            ad.sc[q] = *(const float4*)(a.ascale + ai);
+        }
+    };
+    struct Rows {
+        uint4 wd[S][QC];
+        uint16_t hd[S][QC];
+    };
+    // expert u: the act digits of its first slot, then its rows
+    auto issue = [&](Rows& rw, Act& ad, int u) {
+        const int s0 = ulist[u];
+        const int e = top_l[s0];
+        load_act(ad, s0);
+        unsigned long long so, po;
+        a.rec.get(2, a.key0 + e, so, po);
+        const uint8_t* pk = a.blob + po;
+        const uint16_t* scl = (const uint16_t*)(a.blob + so);
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const int row = c * R + rsub + s * RPI;
+#pragma unroll
+            for (int q = 0; q < QC; q++) {
+                rw.wd[s][q] = *(const uint4*)(pk + (size_t)row * (a.m / 2) + (size_t)chk[q] * 16);
+                rw.hd[s][q] = scl[(size_t)row * ngroups + grp[q]];
+            }
+        }
+    };
+    auto slot_dot = [&](const Rows& rw, const Act& ad, int slot) {
+        float part[S];
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            float ps = 0.0f;
+#pragma unroll
+            for (int q = 0; q < QC; q++) {
+                const uint4 f = flip_nibbles(rw.wd[s][q]);
+                const uint32_t fw[4] = {f.x, f.y, f.z, f.w};
+                const float sj[4] = {ad.sc[q].x, ad.sc[q].y, ad.sc[q].z, ad.sc[q].w};
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    int iv = 0;
+#pragma unroll
+                    for (int kk = NDIG - 1; kk >= 0; kk--) iv = dot8(fw[j], ad.dg[q][j][kk], iv << 4);
+                    acc = __fadd_rn(acc, __fmul_rn((float)iv, sj[j]));
+                }
+                ps = __fadd_rn(ps, live[q] ? __fmul_rn(acc, fp16_hw(rw.hd[s][q])) : 0.0f);
+            }
+            part[s] = ps;
+        }
+        // row s * RPI + rsub of the block's rows ends in the lanes with
+        // (lane % LPR) / (LPR / S) == s
+        const float v = transpose_reduce<LPR, S>(part);
+        if ((lane & (LPR / S - 1)) == 0) {
+            const int s_idx = (lane & (LPR - 1)) / (LPR / S);
+            ypart[slot * R + s_idx * RPI + rsub] = __fmul_rn(tw_l[slot], v);
+        }
+    };
+    // all slots of expert u; the later slots' digits are requested on demand
+    auto expert = [&](const Rows& rw, const Act& ad, int u) {
+        const int s0 = ulist[u];
+        BallotSlots bs;
+        bs.init_lds(top_l, nslot, top_l[s0]);
+        (void)bs.next();                      // s0
+        slot_dot(rw, ad, s0);
+        for (int t = 1; t < bs.n; t++) {
+            const int slot = bs.next();
+            Act more;
+            load_act(more, slot);
+            slot_dot(rw, more, slot);
+        }
+    };
+    const int nj = U > w ? (U - w + DC_WAVES - 1) / DC_WAVES : 0;   // this wave's experts
+    Rows rw[NR];
+    Act ad[NR];
+#pragma unroll
+    for (int q = 0; q < NR; q++)
+        if (q < nj) issue(rw[q], ad[q], w + q * DC_WAVES);
+    for (int j0 = 0; j0 < nj; j0 += NR) {
+#pragma unroll
+        for (int q = 0; q < NR; q++) {
+            const int j = j0 + q;
+            if (j < nj) {
+                expert(rw[q], ad[q], w + j * DC_WAVES);
+                if (j + NR < nj) issue(rw[q], ad[q], w + (j + NR) * DC_WAVES);
+            }
+        }
+    }
+    __syncthreads();
+    for (int o = tid; o < a.B * R; o += DC_THREADS) {
+        const int b = o / R, rr = o % R;
+        float acc = 0.0f;
+        for (int j = 0; j < k; j++) {
+            const int sl = comb_l[b * k + j];
+            if (sl >= 0) acc = __fadd_rn(acc, ypart[sl * R + rr]);
+        }
+        a.out[(size_t)b * a.d + (size_t)c * R + rr] = acc;
+    }
+}
+
 // ----------------------------------------------------------------- combine
 
 __global__ void __launch_bounds__(256)
@@ -330,19 +531,45 @@ static inline void row_lanes(int C, int* lpr, int* qc) {
     *lpr = raw <= 16 ? 16 : raw <= 32 ? 32 : 64;
 }
 
-hipError_t launch_gateup(const ExpertArgs& a, int umax, hipStream_t st) {
-    const long long waves = (long long)umax * (a.m / GU_ROWS);
+template <bool BALLOT>
+static hipError_t gateup_launch(const ExpertArgs& a, long long items, hipStream_t st) {
+    const long long waves = items * (a.m / GU_ROWS);
     if (waves == 0) return hipSuccess;
     const dim3 grid((unsigned)((waves + 3) / 4));
     int lpr, qc;
     row_lanes(a.d, &lpr, &qc);
-#define JM_GU(GG, L, Q) hipLaunchKernelGGL((k_gateup<GG, JM_NDIG, L, Q>), grid, dim3(256), 0, st, a)
+#define JM_GU(GG, L, Q) hipLaunchKernelGGL((k_gateup<GG, JM_NDIG, L, Q, BALLOT>), grid, dim3(256), 0, st, a)
 #define JM_GUG(GG) if (qc == 2) JM_GU(GG, 64, 2); else if (lpr == 64) JM_GU(GG, 64, 1); \
                    else if (lpr == 32) JM_GU(GG, 32, 1); else JM_GU(GG, 16, 1);
     if (qc > 2) return hipErrorInvalidValue;
     if (a.group == 64) { JM_GUG(64) } else { JM_GUG(32) }
 #undef JM_GUG
 #undef JM_GU
+    return hipGetLastError();
+}
+
+hipError_t launch_gateup(const ExpertArgs& a, int umax, hipStream_t st) {
+    return gateup_launch<false>(a, umax, st);
+}
+
+hipError_t launch_gateup_dec(const ExpertArgs& a, hipStream_t st) {
+    if (a.nslot > JM_DEC_SLOTS) return hipErrorInvalidValue;
+    return gateup_launch<true>(a, a.nslot, st);
+}
+
+hipError_t launch_down_comb(const ExpertArgs& a, hipStream_t st) {
+    if (a.nslot > JM_DEC_SLOTS || a.E > JM_MAX_E || a.d % DC_ROWS) return hipErrorInvalidValue;
+    if (a.nslot == 0) return hipSuccess;
+    const dim3 grid((unsigned)(a.d / DC_ROWS));
+    int lpr, qc;
+    row_lanes(a.m, &lpr, &qc);
+#define JM_DC(GG, L, Q) hipLaunchKernelGGL((k_down_comb<GG, JM_NDIG, L, Q>), grid, dim3(DC_THREADS), 0, st, a)
+#define JM_DCG(GG) if (qc == 2) JM_DC(GG, 64, 2); else if (lpr == 64) JM_DC(GG, 64, 1); \
+                   else if (lpr == 32) JM_DC(GG, 32, 1); else JM_DC(GG, 16, 1);
+    if (qc > 2) return hipErrorInvalidValue;
+    if (a.group == 64) { JM_DCG(64) } else { JM_DCG(32) }
+#undef JM_DCG
+#undef JM_DC
     return hipGetLastError();
 }
 

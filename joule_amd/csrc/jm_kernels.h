@@ -16,28 +16,42 @@
 #define JM_MAX_E 512
 #define JM_MAX_SLOTS 65536
 #define JM_MAX_TOPK 32
+// Calls with B*topk up to this many slots take the decode path: three
+// launches, the experts' slots found by ballots over the top-k table and the
+// combine done in the down kernel.  Larger calls take the dispatch path.
+#define JM_DEC_SLOTS 256
 
 namespace jm {
 
 struct ExpertArgs {
     const uint8_t* blob;      // HBM copy of experts_q4.bin
+    RecLoc rec;               // record offsets within blob
+    long long key0;           // layer * E
+    int E;
+    // dispatch path: the work table and its segments
     const ExpertWork* work;   // [umax] per active expert: segment + record offsets
     int umax;                 // work table entries
-    int d, m, topk;
     const int* seg_slot;      // [B*k] slot ids (b*k+i) grouped by expert, stable
+    // decode path: the top-k table
+    const int* top;           // [B*k] expert of each slot (-1: none)
+    int nslot;                // B*k
+    int B;
+    int d, m, topk;
     const float* tw;          // [B*k] routing weight of each slot
     const uint32_t* xdig;     // [B][d/G][NDIG][G/8] token digits
     const float* xscale;      // [B][d/G]
     float* act;               // [B*k][m]   SiLU(gate)*up per slot
     uint32_t* adig;           // [B*k][m/8][NDIG] act digits, 8 values per group
     float* ascale;            // [B*k][m/8]
-    float* y;                 // [B*k][d]   weighted expert output per slot
+    float* y;                 // [B*k][d]   weighted expert output per slot (dispatch path)
+    float* out;               // [B][d]     block output (decode path)
     int group;
 };
 
-// Routing front (router + x digits + top-k + dispatch) in one launch.
+// Routing front: router scores, top-k, x digits and (dispatch path) the
+// dispatch and work table.
 struct RouteArgs {
-    const void* wt;           // [E][8][d/8] residue-major router table of the layer
+    const void* wt;           // interleaved router copy of the layer
     int wt_bf16;              // 1: wt holds bf16 bits, 0: float32
     const float* x;           // [B][d]
     int B, E, d, topk, renorm, group;
@@ -55,10 +69,14 @@ struct RouteArgs {
     int* rank_scratch;        // [B*k]
     ExpertWork* work;         // [umax] expert work table
     int umax;                 // min(E, B*k)
-    const unsigned long long* rec_off;   // store offsets [3][L*E][2]
-    long long LE, key0;       // L*E and layer*E
+    RecLoc rec;               // store record offsets
+    long long key0;           // layer*E
 };
-hipError_t launch_route(const RouteArgs& a, hipStream_t st);
+// router scores + x digits (one wave per expert group and token), then the
+// top-k of every token
+hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st);
+// dispatch + work table from a.top (dispatch path)
+hipError_t launch_dispatch_work(const RouteArgs& a, hipStream_t st);
 // experts per layer in the router copy: E rounded up to whole groups of 8
 __host__ __device__ constexpr int router_experts_padded(int E) { return (E + 7) / 8 * 8; }
 hipError_t launch_router_transpose(const void* in, int in_bf16, void* out, int out_bf16, long long rows,
@@ -75,6 +93,11 @@ hipError_t launch_topk(const float* logits, int B, int E, int k, int renorm, int
 hipError_t launch_dispatch(const int* top, int nslot, int E, int k, int* seg_off, int* seg_slot,
                            int* active, int* n_active, int* first_slot, int* comb, int* rank_scratch,
                            hipStream_t st);
+// decode path (nslot <= JM_DEC_SLOTS): gate/up over ballot-found slots, then
+// down + combine into a.out
+hipError_t launch_gateup_dec(const ExpertArgs& a, hipStream_t st);
+hipError_t launch_down_comb(const ExpertArgs& a, hipStream_t st);
+// dispatch path: gate/up and down over the work table, then the combine
 hipError_t launch_gateup(const ExpertArgs& a, int umax, hipStream_t st);
 hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st);
 // out[b] = sum of the token's slots of y in the order comb gives
