@@ -326,12 +326,12 @@ k_down(ExpertArgs a) {
 // ---------------------------------------------------------- down + combine
 
 constexpr int DC_ROWS = 8;             // hidden rows per block
-constexpr int DC_THREADS = 512;
+constexpr int DC_THREADS = 768;
 constexpr int DC_WAVES = DC_THREADS / 64;
 
 // Decode path: block c owns hidden rows [c * DC_ROWS, (c + 1) * DC_ROWS) of
 // every token.  It lists the routed experts in the reference's union order
-// (first appearance over the slots); wave w takes experts w, w + 8, ...,
+// (first appearance over the slots); wave w takes experts w, w + 12, ...,
 // keeping NR of them in flight (each expert's rows, and the act digits of
 // its first slot, requested in that order), writes w_slot * (rows . act_slot)
 // for each slot into LDS, and finally sums each token's values in union
@@ -344,7 +344,7 @@ k_down_comb(ExpertArgs a) {
     constexpr int RPI = JM_WAVE / LPR;          // rows per load instruction
     constexpr int S = R / RPI;                  // load steps per expert
     static_assert(S >= 1 && S * RPI == R, "whole rows per step");
-    constexpr int NR = S * QC <= 4 ? 4 : 2;     // experts in flight per wave
+    constexpr int NR = 2;                       // experts in flight per wave
     static_assert(JM_DEC_SLOTS <= DC_THREADS, "a slot per thread");
     __shared__ int top_l[JM_DEC_SLOTS], ulist[JM_DEC_SLOTS], comb_l[JM_DEC_SLOTS];
     __shared__ int first_l[JM_MAX_E];
@@ -444,9 +444,9 @@ k_down_comb(ExpertArgs a) {
                     int iv = 0;
 #pragma unroll
                     for (int kk = NDIG - 1; kk >= 0; kk--) iv = dot8(fw[j], ad.dg[q][j][kk], iv << 4);
-                    acc = __fadd_rn(acc, __fmul_rn((float)iv, sj[j]));
+                    acc = __builtin_fmaf((float)iv, sj[j], acc);
                 }
-                ps = __fadd_rn(ps, live[q] ? __fmul_rn(acc, fp16_hw(rw.hd[s][q])) : 0.0f);
+                ps = __builtin_fmaf(acc, live[q] ? fp16_hw(rw.hd[s][q]) : 0.0f, ps);
             }
             part[s] = ps;
         }
