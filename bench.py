@@ -17,7 +17,9 @@ Reported (one JSON line):
   block        the same ratio for the whole block (all algorithmic bytes:
                routed experts, router table, x in/out) over ms_per_step
   stages       average milliseconds of each kernel
-  sweep        the same measurement at B=1 and B=32 (Qwen3) and OLMoE B=1/8
+  sweep        the same measurement at B=1 and B=32 (Qwen3), OLMoE B=1/8, and
+               the prefill-style Qwen3 block: 512 tokens with Zipf(1.1)-biased
+               routing, whose large segments take the MFMA branch
   cpu_baseline the C restatement of the reference block (oracle/) on this
                host's cores, 8 workers + caller as the reference runs B>1,
                on a bounded sample of the same workload
@@ -36,6 +38,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
+PEAK_MFMA_TFLOPS = 2500.0      # dense bf16/fp16 MFMA
+ZIPF_ALPHA = 0.28              # Zipf(1.1) bias strength: per-expert counts about 5..200 over 512 tokens
 
 # HBM traffic of one k_gateup launch on the default workload (B=8, group 64,
 # 16 rotating layers), measured by two rocprofv3 --pmc runs of this script
@@ -204,6 +208,7 @@ def main() -> int:
               f"(--gpus {args.gpus}, WORLD_SIZE {world}); run with --gpus 1.", file=sys.stderr)
         return 2
 
+    import numpy as np
     import torch
 
     from joule_amd.moe import OLMOE, QWEN3
@@ -244,6 +249,38 @@ def main() -> int:
             sweep[f"qwen3_B{b}"] = {k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac",
                                                       "gateup_GBs", "experts_routed_avg")}
             log(f"sweep qwen3 B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s")
+
+    if not args.no_sweep:
+        # prefill-style batch: 512 tokens with Zipf(1.1)-biased routing (per-expert
+        # counts about 5..200); the MFMA branch takes the experts with >= 8 slots
+        from joule_amd.synth import apply_logit_bias, zipf_bias
+
+        bz = 512
+        bias = zipf_bias(shape.E, s=1.1, alpha=ZIPF_ALPHA)
+        xz_np = activations(bz, shape.d)
+        gz = np.stack([apply_logit_bias(gw[l], xz_np, bias)[0] for l in range(NL)])
+        xz = torch.from_numpy(apply_logit_bias(gw[0], xz_np, bias)[1]).cuda()
+        store.set_router(torch.from_numpy(gz).cuda())
+        nz = max(args.steps // 8, 20)
+        m2, st2, U2 = measure(store, gz, xz, nz, 5, NL)
+        r = block_numbers(shape, G, bz, m2, st2, U2, nz, NL, rb)
+        top = torch.empty((bz, shape.topk), dtype=torch.int32, device="cuda")
+        store.layer_ffn_batch(0, xz, topk_idx=top)
+        tiles = store.dense_tiles()
+        counts = np.bincount(top.cpu().numpy().ravel(), minlength=shape.E)
+        flops = 2.0 * bz * shape.topk * 3 * shape.d * shape.m
+        sweep["qwen3_zipf512"] = {
+            **{k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac", "experts_routed_avg")},
+            "tflops": flops / (m2 * 1e-3) / 1e12,
+            "mfma_frac_of_bf16_peak": flops / (m2 * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS,
+            "zipf_alpha": ZIPF_ALPHA, "count_max": int(counts.max()), "count_min": int(counts.min()),
+            "dense_experts": int((counts >= 8).sum()), "dense_tiles": tiles,
+            "stages_ms": st2,
+        }
+        log(f"sweep qwen3 zipf B={bz}: {r['tok_per_s']:.0f} tok/s, {m2 * 1e3:.1f} us/step, "
+            f"{flops / (m2 * 1e-3) / 1e12:.1f} TFLOP/s, counts {counts.min()}..{counts.max()}, "
+            f"dense tiles {tiles}, stages {st2}")
+        store.set_router(torch.from_numpy(gw).cuda())
 
     cpu = None
     if args.cpu_seconds > 0:

@@ -109,6 +109,14 @@ int jm_store_reserve(jm_store* s, int max_B);
 
 int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, int* group);
 
+/* Batches with B * topk > 256 slots: an expert routed at least min_tokens
+ * slots takes the MFMA branch (64-token tiles of fp16 products on
+ * LDS-dequantized weights), the others the wave-item GEMV kernels.
+ * 0 restores the default (8); a value above B * topk keeps every expert on
+ * the GEMV kernels.  No counterpart in the reference, whose batch is at most
+ * 16 tokens (decode_kernel.c:1522). */
+int jm_store_set_dense_min(jm_store* s, int min_tokens);
+
 /*
  * The MoE block of one layer: layer_ffn_batch(cfg, W, l, x, B, out)
  * (decode_kernel.c:1387-1508), for any B >= 0 (the reference clamps B to 16
@@ -143,7 +151,8 @@ int jm_store_stage_ms(jm_store* s, float* ms, int n);
  *   JM_WS_N_ACTIVE   int32 [1] how many of them
  *   JM_WS_FIRST_SLOT int32 [E] first slot of each active expert
  *   JM_WS_ACT        float [B*topk][intermediate] SiLU(gate)*up per slot
- *   JM_WS_Y          float [B*topk][d] weighted expert output per slot */
+ *   JM_WS_Y          float [B*topk][d] weighted expert output per slot
+ *   JM_WS_N_DENSE_TILES int32 [1] 64-token tiles the MFMA branch computed */
 #define JM_WS_LOGITS 0
 #define JM_WS_SEG_OFF 1
 #define JM_WS_SEG_SLOT 2
@@ -152,6 +161,7 @@ int jm_store_stage_ms(jm_store* s, float* ms, int n);
 #define JM_WS_FIRST_SLOT 5
 #define JM_WS_ACT 6
 #define JM_WS_Y 7
+#define JM_WS_N_DENSE_TILES 8
 int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t bytes, void* stream);
 
 /* ---- stage entry points (the steps of layer_ffn_batch, for tests) ---- */

@@ -97,6 +97,13 @@ struct jm_store {
     uint32_t* adig;
     float* ascale;
     float* y;
+    int2* tiles;                // dense tiles (dispatch path)
+    int* n_tiles;
+    _Float16* act_h;            // act split for the MFMA down
+    _Float16* act_l;
+    _Float16* xsh;              // tokens split for the MFMA gate/up
+    _Float16* xsl;
+    int dense_min;              // segment size from which an expert takes the MFMA branch
 };
 
 namespace {
@@ -107,7 +114,8 @@ int reserve(jm_store* s, int B) {
     const size_t nslot = (size_t)B * k;
     const size_t words_d = (size_t)(d / G) * JM_NDIG * (G / 8);
     const size_t words_m = (size_t)(m / 8) * JM_NDIG;
-    size_t sz[19] = {
+    const size_t max_tiles = nslot / JM_DENSE_TILE + E;
+    const size_t sz[] = {
         (size_t)B * E * 4,            // logits
         nslot * 4,                    // top
         nslot * 4,                    // tw
@@ -121,12 +129,18 @@ int reserve(jm_store* s, int B) {
         nslot * 4,                    // rank
         nslot * 4,                    // comb
         (size_t)E * sizeof(jm::ExpertWork),   // work table
-        0, 0,
+        max_tiles * 8,                // dense tiles
+        4,                            // n_tiles
         nslot * m * 4,                // act
         nslot * words_m * 4,          // adig
         nslot * (m / 8) * 4,          // ascale
         nslot * d * 4,                // y
+        nslot * m * 2,                // act_h
+        nslot * m * 2,                // act_l
+        (size_t)B * d * 2,            // xsh
+        (size_t)B * d * 2,            // xsl
     };
+    constexpr int NF = sizeof(sz) / sizeof(sz[0]);
     size_t total = 0;
     for (size_t v : sz) total += align256(v);
     void* mem = nullptr;
@@ -136,14 +150,15 @@ int reserve(jm_store* s, int B) {
     if (s->ws) (void)hipFree(s->ws);
     s->ws = mem;
     char* p = (char*)mem;
-    void** slots[19] = {(void**)&s->logits, (void**)&s->top, (void**)&s->tw, (void**)&s->xdig,
+    void** slots[NF] = {(void**)&s->logits, (void**)&s->top, (void**)&s->tw, (void**)&s->xdig,
                         (void**)&s->xscale, (void**)&s->seg_off, (void**)&s->seg_slot,
                         (void**)&s->active, (void**)&s->n_active, (void**)&s->first_slot,
-                        (void**)&s->rank, (void**)&s->comb, (void**)&s->work, nullptr,
-                        nullptr, (void**)&s->act, (void**)&s->adig,
-                        (void**)&s->ascale, (void**)&s->y};
-    for (int i = 0; i < 19; i++) {
-        if (slots[i]) *slots[i] = p;
+                        (void**)&s->rank, (void**)&s->comb, (void**)&s->work, (void**)&s->tiles,
+                        (void**)&s->n_tiles, (void**)&s->act, (void**)&s->adig,
+                        (void**)&s->ascale, (void**)&s->y, (void**)&s->act_h, (void**)&s->act_l,
+                        (void**)&s->xsh, (void**)&s->xsl};
+    for (int i = 0; i < NF; i++) {
+        *slots[i] = p;
         p += align256(sz[i]);
     }
     JM_HIP(hipMemset(mem, 0, total), "hipMemset workspace");
@@ -207,6 +222,7 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
     s->L = L; s->E = E; s->d = d; s->m = m; s->topk = k;
     s->renorm = cfg->norm_topk_prob ? 1 : 0;
     s->group = group;
+    s->dense_min = JM_DENSE_MIN_DEFAULT;
     s->blob = (const uint8_t*)blob;
     s->blob_bytes = blob_bytes;
     s->device = attr.device;
@@ -304,6 +320,13 @@ int jm_store_reserve(jm_store* s, int max_B) {
     return reserve(s, max_B);
 }
 
+int jm_store_set_dense_min(jm_store* s, int min_tokens) {
+    if (int rc = check_store(s)) return rc;
+    if (min_tokens < 0) return fail(JM_ERR_ARG, "min_tokens must be >= 0 (0 = default)");
+    s->dense_min = min_tokens == 0 ? JM_DENSE_MIN_DEFAULT : min_tokens;
+    return 0;
+}
+
 int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, int* group) {
     if (int rc = check_store(s)) return rc;
     if (L) *L = s->L;
@@ -332,6 +355,8 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     if (!x || !out) return fail(JM_ERR_ARG, "x and out must be non-NULL");
     if (!aligned(x, 16) || !aligned(out, 16)) return fail(JM_ERR_ARG, "x and out must be 16-byte aligned");
     if ((long long)B * s->topk > JM_MAX_SLOTS) return fail(JM_ERR_SHAPE, "B * topk must be <= %d", JM_MAX_SLOTS);
+    if (B * s->topk > JM_DEC_SLOTS && (size_t)jm::dispatch_lds_ints(B * s->topk, s->E) * 4 > (size_t)s->lds_max)
+        return fail(JM_ERR_SHAPE, "B * topk = %d slots over %d experts exceed the dispatch's LDS", B * s->topk, s->E);
     if (int rc = reserve(s, B)) return rc;
     hipStream_t st = (hipStream_t)stream;
     const int E = s->E, d = s->d, k = s->topk, G = s->group;
@@ -348,6 +373,7 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     r.first_slot = s->first_slot; r.comb = s->comb; r.rank_scratch = s->rank;
     r.work = s->work; r.umax = umax; r.rec = s->rec;
     r.key0 = (long long)layer * E;
+    r.dense_min = s->dense_min; r.tiles = s->tiles; r.n_tiles = s->n_tiles;
     jm::ExpertArgs a;
     a.blob = s->blob; a.rec = s->rec; a.key0 = (long long)layer * E; a.E = E;
     a.work = s->work; a.umax = umax; a.seg_slot = s->seg_slot;
@@ -355,18 +381,30 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     a.d = d; a.m = s->m; a.topk = k; a.group = G;
     a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
     a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y; a.out = out;
+    a.dense_min = jm::mfma_shape_ok(d, s->m) ? s->dense_min : 0x7FFFFFFF;
+    r.dense_min = a.dense_min;
+    a.tiles = s->tiles; a.n_tiles = s->n_tiles;
+    r.xsh = dec ? nullptr : s->xsh; r.xsl = dec ? nullptr : s->xsl;
+    a.xsh = s->xsh; a.xsl = s->xsl;
+    a.act_h = s->act_h; a.act_l = s->act_l;
+    const int max_tiles = nslot / JM_DENSE_TILE + E;
 #define JM_MARK(i) if (s->prof) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
     JM_MARK(0);
     JM_HIP(jm::launch_route_tok(r, st), "route launch");
     if (!dec) JM_HIP(jm::launch_dispatch_work(r, st), "dispatch launch");
     JM_MARK(1);
-    if (dec) JM_HIP(jm::launch_gateup_dec(a, st), "gate/up launch");
-    else JM_HIP(jm::launch_gateup(a, umax, st), "gate/up launch");
+    if (dec) {
+        JM_HIP(jm::launch_gateup_dec(a, st), "gate/up launch");
+    } else {
+        JM_HIP(jm::launch_gateup(a, umax, st), "gate/up launch");
+        JM_HIP(jm::launch_gateup_mfma(a, max_tiles, st), "gate/up MFMA launch");
+    }
     JM_MARK(2);
     if (dec) {
         JM_HIP(jm::launch_down_comb(a, st), "down/combine launch");
     } else {
         JM_HIP(jm::launch_down(a, umax, st), "down launch");
+        JM_HIP(jm::launch_down_mfma(a, max_tiles, st), "down MFMA launch");
         JM_HIP(jm::launch_combine(s->y, s->comb, B, k, d, out, st), "combine launch");
     }
     JM_MARK(3);
@@ -420,6 +458,7 @@ int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t by
         case JM_WS_FIRST_SLOT: src = s->first_slot; cap = (size_t)s->E * 4; break;
         case JM_WS_ACT: src = s->act; cap = nslot * s->m * 4; break;
         case JM_WS_Y: src = s->y; cap = nslot * s->d * 4; break;
+        case JM_WS_N_DENSE_TILES: src = s->n_tiles; cap = 4; break;
         default: return fail(JM_ERR_ARG, "unknown workspace field %d", field);
     }
     if (!src || s->last_B == 0) return fail(JM_ERR_ARG, "no call has run on this store yet");
@@ -450,6 +489,11 @@ int jm_dispatch(const int32_t* top, int nslot, int E, int topk, int32_t* seg_off
         nslot % topk)
         return fail(JM_ERR_SHAPE, "need 0 <= nslot <= %d (a multiple of topk <= %d) and 0 < E <= %d",
                     JM_MAX_SLOTS, JM_MAX_TOPK, JM_MAX_E);
+    int dev = 0, lds_max = 0;
+    JM_HIP(hipGetDevice(&dev), "hipGetDevice");
+    JM_HIP(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev), "hipDeviceGetAttribute");
+    if ((size_t)jm::dispatch_lds_ints(nslot, E) * 4 > (size_t)lds_max)
+        return fail(JM_ERR_SHAPE, "%d slots over %d experts exceed the dispatch's LDS", nslot, E);
     hipStream_t st = (hipStream_t)stream;
     void* scratch = nullptr;
     JM_HIP(hipMallocAsync(&scratch, align256((size_t)nslot * 4 + 4), st), "hipMallocAsync dispatch scratch");

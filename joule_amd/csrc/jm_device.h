@@ -376,7 +376,6 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ s, int E, in
 
 // ------------------------------------------------------------- dispatch
 
-constexpr int DISP_CHUNKS_C = 16;
 
 // Work table entry of one active expert for the expert kernels: its
 // segment and the byte offsets of its gate/up/down records, so that an
@@ -576,43 +575,58 @@ struct TableSlots {
     }
 };
 
-// LDS of dispatch_block, in ints
-__host__ __device__ constexpr int dispatch_lds_ints(int E) { return DISP_CHUNKS_C * E + 2 * E + 1 + 32; }
+// Dispatch chunks: 64 consecutive slots, one wave's worth.
+constexpr int DISP_CHUNK = 64;
+
+// LDS of dispatch_block, in ints: per-chunk expert counts, segment starts,
+// first slots, scan scratch.
+__host__ __device__ constexpr int dispatch_lds_ints(int nslot, int E) {
+    return (nslot + DISP_CHUNK - 1) / DISP_CHUNK * E + 2 * E + 1 + 32;
+}
 
 // Stable counting sort of nslot slots by expert id, run by one whole block
 // (decode_kernel.c:1449-1485 builds the same segments in first-appearance
 // order; here they are in expert-id order, slots within a segment in
-// increasing b*k+i order).  `top` should point to LDS; `rank` is nslot ints
-// of scratch (LDS when it fits).  E <= blockDim.x.  Writes seg_off[E+1],
-// seg_slot, active[U] (expert-id order), *n_active = U, first_slot[e], and
-// comb[b*k + j] = the token's slots in the reference's union order
-// (ascending first appearance of their expert), -1 padded.  With `work`,
-// also the expert work table for umax entries: the experts with two or more
-// slots first, then those with one (each group in expert-id order), so that
-// the longest segments start first; entries past U have n = 0.  `rec` holds
-// the record offsets of expert tid (tid < E).
+// increasing b*k+i order).  `rank` is nslot ints of scratch.  E <=
+// blockDim.x.  Writes seg_off[E+1], seg_slot, active[U] (expert-id order),
+// *n_active = U, first_slot[e], and comb[b*k + j] = the token's slots in the
+// reference's union order (ascending first appearance of their expert), -1
+// padded.  With `work`, also the expert work table for umax entries: the
+// experts with two or more slots first, then those with one (each group in
+// expert-id order), so that the longest segments start first; entries past U
+// have n = 0.  `rec` holds the record offsets of expert tid (tid < E).
+// A slot's rank among the earlier slots of its chunk with the same expert
+// comes from ballots over the bits of the expert id (lanes with equal ids
+// agree on every bit).
 __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E, int k, int* lds,
                                                int* __restrict__ seg_off, int* __restrict__ seg_slot,
                                                int* __restrict__ active, int* __restrict__ n_active,
                                                int* __restrict__ first_slot, int* __restrict__ comb,
                                                int* rank, ExpertWork* __restrict__ work = nullptr,
                                                int umax = 0, const ExpertRec* rec = nullptr) {
-    int* cnt = lds;                              // [DISP_CHUNKS][E]
-    int* off = cnt + DISP_CHUNKS_C * E;          // [E + 1]
+    const int nchunk = (nslot + DISP_CHUNK - 1) / DISP_CHUNK;
+    int* cnt = lds;                              // [nchunk][E]
+    int* off = cnt + nchunk * E;                 // [E + 1]
     int* fs = off + E + 1;                       // [E]
     unsigned* wsum = (unsigned*)(fs + E);        // [32]
-    const int tid = threadIdx.x, nth = blockDim.x;
-    const int chunk = (nslot + DISP_CHUNKS_C - 1) / DISP_CHUNKS_C;
-    for (int i = tid; i < DISP_CHUNKS_C * E; i += nth) cnt[i] = 0;
+    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63;
+    for (int i = tid; i < nchunk * E; i += nth) cnt[i] = 0;
     __syncthreads();
-    for (int s = tid; s < nslot; s += nth) {
-        const int e = top[s];
-        if (e < 0 || e >= E) { rank[s] = -1; continue; }
-        const int c = s / chunk;
-        int r = 0;
-        for (int q = c * chunk; q < s; q++) r += (top[q] == e);
-        rank[s] = r;
-        atomicAdd(&cnt[c * E + e], 1);
+    int nbits = 1;
+    while ((1 << nbits) < E) nbits++;
+    for (int c = tid >> 6; c < nchunk; c += nth >> 6) {
+        const int s = c * DISP_CHUNK + lane;
+        const int e0 = s < nslot ? top[s] : -1;
+        const bool ok = e0 >= 0 && e0 < E;
+        const int e = ok ? e0 : 0;
+        unsigned long long same = __ballot(ok);
+        for (int b = 0; b < nbits; b++) {
+            const unsigned long long bb = __ballot(ok && ((e >> b) & 1));
+            same &= ((e >> b) & 1) ? bb : ~bb;
+        }
+        const int r = __popcll(same & ((1ull << lane) - 1ull));
+        if (s < nslot) rank[s] = ok ? r : -1;
+        if (ok && r == 0) cnt[c * E + e] = __popcll(same);
     }
     __syncthreads();
     // per expert: exclusive prefix over chunks, then one block scan of
@@ -620,14 +634,11 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
     // positions of both groups
     int total_e = 0;
     if (tid < E) {
-        int n[DISP_CHUNKS_C];
-#pragma unroll
-        for (int c = 0; c < DISP_CHUNKS_C; c++) n[c] = cnt[c * E + tid];
         int run = 0;
-#pragma unroll
-        for (int c = 0; c < DISP_CHUNKS_C; c++) {
+        for (int c = 0; c < nchunk; c++) {
+            const int v = cnt[c * E + tid];
             cnt[c * E + tid] = run;
-            run += n[c];
+            run += v;
         }
         total_e = run;
     }
@@ -676,7 +687,7 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
         const int r = rank[s];
         if (r < 0) continue;
         const int e = top[s];
-        const int pos = off[e] + cnt[(s / chunk) * E + e] + r;
+        const int pos = off[e] + cnt[(s / DISP_CHUNK) * E + e] + r;
         seg_slot[pos] = s;
         if (pos == off[e]) { first_slot[e] = s; fs[e] = s; }
     }

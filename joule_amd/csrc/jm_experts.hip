@@ -15,7 +15,8 @@
 //                     reference's union order (:1502-1507)
 // Dispatch path (more slots): the same gate/up over the work table the
 // dispatch kernel writes, k_down per (expert, 16 hidden rows) into y, and
-// k_combine.
+// k_combine; experts with dense_min or more slots are left to the MFMA
+// kernels (jm_mfma.hip).
 //
 // Lane layout: a row of C columns is read as C/32 chunks of 16 bytes (32
 // packed weights); lane col of an LPR-lane row segment holds chunks col,
@@ -87,7 +88,7 @@ k_gateup(ExpertArgs a) {
     } else {
         if (u >= a.umax) return;
         const ExpertWork wk = a.work[u];
-        if (wk.n == 0) return;
+        if (wk.n == 0 || wk.n >= a.dense_min) return;     // none, or the MFMA branch's
         n = wk.n;
         ts.init(a.seg_slot, wk.s0, wk.n);
         so_g = wk.sc[0]; po_g = wk.pk[0];
@@ -216,7 +217,7 @@ k_down(ExpertArgs a) {
     const int u = item / nchunk, c = item % nchunk;
     if (u >= a.umax) return;
     const ExpertWork wk = a.work[u];
-    if (wk.n == 0) return;
+    if (wk.n == 0 || wk.n >= a.dense_min) return;         // none, or the MFMA branch's
     TableSlots ts;
     ts.init(a.seg_slot, wk.s0, wk.n);
     const int col = lane & (LPR - 1), rsub = lane / LPR;

@@ -20,8 +20,16 @@
 // launches, the experts' slots found by ballots over the top-k table and the
 // combine done in the down kernel.  Larger calls take the dispatch path.
 #define JM_DEC_SLOTS 256
+// Dispatch path: experts with at least dense_min slots take the MFMA branch,
+// in tiles of this many tokens.  Its fp16 operands store each group of 8
+// columns in the order 0 4 1 5 2 6 3 7 (the order the nibble dequantisation
+// produces): column c sits at 8 (c / 8) + mfma_slot(c % 8).
+#define JM_DENSE_TILE 64
+#define JM_DENSE_MIN_DEFAULT 8
 
 namespace jm {
+
+__host__ __device__ constexpr int mfma_slot(int i) { return (i & 3) * 2 + (i >> 2); }
 
 struct ExpertArgs {
     const uint8_t* blob;      // HBM copy of experts_q4.bin
@@ -38,6 +46,8 @@ struct ExpertArgs {
     int B;
     int d, m, topk;
     const float* tw;          // [B*k] routing weight of each slot
+    const _Float16* xsh;      // [B][d] tokens split hi/lo in MFMA column order (MFMA branch)
+    const _Float16* xsl;
     const uint32_t* xdig;     // [B][d/G][NDIG][G/8] token digits
     const float* xscale;      // [B][d/G]
     float* act;               // [B*k][m]   SiLU(gate)*up per slot
@@ -46,6 +56,12 @@ struct ExpertArgs {
     float* y;                 // [B*k][d]   weighted expert output per slot (dispatch path)
     float* out;               // [B][d]     block output (decode path)
     int group;
+    // dispatch path, dense branch
+    int dense_min;            // experts with at least this many slots take the MFMA kernels
+    const int2* tiles;        // [max tiles] (work entry, 64-token tile) of the dense experts
+    const int* n_tiles;       // [1] how many
+    _Float16* act_h;          // [B*k][m] act split into fp16 hi + lo for the MFMA down
+    _Float16* act_l;
 };
 
 // Routing front: router scores, top-k, x digits and (dispatch path) the
@@ -58,6 +74,8 @@ struct RouteArgs {
     float* logits;            // [B][E]
     uint32_t* xdig;           // [B][d/G][NDIG][G/8]
     float* xscale;            // [B][d/G]
+    _Float16* xsh;            // [B][d] token split hi/lo in MFMA column order (NULL: not needed)
+    _Float16* xsl;
     int* top;                 // [B*k]
     float* tw;                // [B*k]
     int* seg_off;             // [E+1]
@@ -71,6 +89,9 @@ struct RouteArgs {
     int umax;                 // min(E, B*k)
     RecLoc rec;               // store record offsets
     long long key0;           // layer*E
+    int dense_min;            // dispatch path: slots from which an expert takes the MFMA kernels
+    int2* tiles;              // dense tiles (work entry, token tile), in work-table order
+    int* n_tiles;             // [1]
 };
 // router scores + x digits (one wave per expert group and token), then the
 // top-k of every token
@@ -100,6 +121,12 @@ hipError_t launch_down_comb(const ExpertArgs& a, hipStream_t st);
 // dispatch path: gate/up and down over the work table, then the combine
 hipError_t launch_gateup(const ExpertArgs& a, int umax, hipStream_t st);
 hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st);
+// dense branch: grids of max_tiles x (row tiles); blocks past *n_tiles exit.
+// mfma_shape_ok: d and intermediate are multiples of 128 (else the GEMV
+// kernels take every expert)
+bool mfma_shape_ok(int d, int m);
+hipError_t launch_gateup_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st);
+hipError_t launch_down_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st);
 // out[b] = sum of the token's slots of y in the order comb gives
 hipError_t launch_combine(const float* y, const int* comb, int B, int k, int d, float* out, hipStream_t st);
 hipError_t launch_dequant(const uint8_t* packed, const uint16_t* scales, long long numel, int group,

@@ -159,7 +159,7 @@ hipError_t launch_topk(const float* logits, int B, int E, int k, int renorm, int
 hipError_t launch_dispatch(const int* top, int nslot, int E, int k, int* seg_off, int* seg_slot,
                            int* active, int* n_active, int* first_slot, int* comb, int* rank_scratch,
                            hipStream_t st) {
-    const size_t lds = (size_t)dispatch_lds_ints(E) * 4;
+    const size_t lds = (size_t)dispatch_lds_ints(nslot, E) * 4;
     hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), lds, st, top, nslot, E, k, seg_off, seg_slot,
                        active, n_active, first_slot, comb, rank_scratch);
     return hipGetLastError();

@@ -7,7 +7,9 @@
 //   k_topk           (jm_kernels.hip) one wave per token: softmax + top-k +
 //                    renormalisation (:1425-1448)
 //   k_dispatch_work  dispatch path only (more than 256 slots): the counting
-//                    sort of all slots (:1449-1485) and the expert work table
+//                    sort of all slots (:1449-1485), the expert work table
+//                    and the token tiles of the experts that take the MFMA
+//                    branch
 //
 // No block waits for or reads data written by another block of the same
 // launch: on MI355X each XCD has its own L2, and a device-scope handoff
@@ -28,6 +30,8 @@
 #include "jm_kernels.h"
 
 namespace jm {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 // Interleaved copy of the router tables (L layers of E experts; E padded
 // to Ep = a multiple of 8 per layer, the padding left as the caller cleared
@@ -203,6 +207,23 @@ k_router_grp(RouteArgs a) {
         encode_group_wave<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + (ok ? p : 0)) * (NDIG * (G / 8)),
                                    a.xscale + (size_t)b * ng + (ok ? p : 0));
     }
+    // the token split into fp16 hi + lo for the MFMA branch, columns in its
+    // order: this block's share of 8-column groups
+    if (a.xsh) {
+        for (int c = (eg * 64 + lane) * 8; c < d; c += ngrp * 64 * 8) {
+            half8 h, l;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int j = c + i;
+                const float v = xT[(size_t)(j & 7) * TP + (j >> 3)];
+                const _Float16 hh = (_Float16)v;
+                h[mfma_slot(i)] = hh;
+                l[mfma_slot(i)] = (_Float16)(v - (float)hh);
+            }
+            *(half8*)(a.xsh + (size_t)b * d + c) = h;
+            *(half8*)(a.xsl + (size_t)b * d + c) = l;
+        }
+    }
 }
 
 // Dispatch and work table of all slots from the top-k table (dispatch path).
@@ -213,6 +234,18 @@ k_dispatch_work(RouteArgs a) {
     if ((int)threadIdx.x < a.E) rec = load_expert_rec(a.rec, a.key0, threadIdx.x);
     dispatch_block(a.top, a.B * a.topk, a.E, a.topk, lds_i, a.seg_off, a.seg_slot, a.active,
                    a.n_active, a.first_slot, a.comb, a.rank_scratch, a.work, a.umax, &rec);
+    // the dense experts' token tiles, in work-table order
+    __syncthreads();
+    const int u = threadIdx.x;
+    int ct = 0;
+    if (u < a.umax) {
+        const int n = a.work[u].n;
+        ct = n >= a.dense_min ? (n + JM_DENSE_TILE - 1) / JM_DENSE_TILE : 0;
+    }
+    uint2 tot;
+    const uint2 ex = block_exclusive_scan2(make_uint2((unsigned)ct, 0u), (unsigned*)lds_i, &tot);
+    for (int j = 0; j < ct; j++) a.tiles[ex.x + j] = make_int2(u, j);
+    if (threadIdx.x == 0) *a.n_tiles = (int)tot.x;
 }
 
 hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {
@@ -233,7 +266,7 @@ hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_dispatch_work(const RouteArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL(k_dispatch_work, dim3(1), dim3(1024), (size_t)dispatch_lds_ints(a.E) * 4, st, a);
+    hipLaunchKernelGGL(k_dispatch_work, dim3(1), dim3(1024), (size_t)dispatch_lds_ints(a.B * a.topk, a.E) * 4, st, a);
     return hipGetLastError();
 }
 

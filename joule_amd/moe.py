@@ -140,6 +140,18 @@ class HbmExpertStore:
         _lib.check(_lib.lib().jm_store_router_dtype(self._h, ctypes.byref(dt)), "jm_store_router_dtype")
         return 2 if dt.value == _lib.JM_DTYPE_BF16 else 4
 
+    def set_dense_min(self, min_tokens: int) -> None:
+        """Segment size from which an expert takes the MFMA branch (batches
+        with more than 256 slots); 0 restores the default."""
+        _lib.check(_lib.lib().jm_store_set_dense_min(self._h, int(min_tokens)), "jm_store_set_dense_min")
+
+    def dense_tiles(self, stream=None) -> int:
+        """64-token tiles the MFMA branch computed in the last call."""
+        t = torch.zeros(1, dtype=torch.int32, device=self.blob.device)
+        _lib.check(_lib.lib().jm_store_copy_workspace(self._h, _lib.WS_N_DENSE_TILES, _lib.ptr(t), 4,
+                                                      _lib.stream_handle(stream)), "jm_store_copy_workspace")
+        return int(t.item())
+
     def reserve(self, max_B: int) -> None:
         _lib.check(_lib.lib().jm_store_reserve(self._h, int(max_B)), "jm_store_reserve")
 

@@ -277,15 +277,42 @@ def test_block_zipf_large_segments(qwen64):
     qwen64.store.set_router(w)
     try:
         out, top, tw = _run_block(qwen64, 0, x)
+        tiles = qwen64.store.dense_tiles()
     finally:
         qwen64.store.set_router(torch.from_numpy(qwen64.gw).cuda())
     counts = np.bincount(top.ravel(), minlength=s.E)
-    print(f"  segment sizes: max {counts.max()} nonzero {np.count_nonzero(counts)}", flush=True)
+    print(f"  segment sizes: max {counts.max()} nonzero {np.count_nonzero(counts)}, "
+          f"dense tiles {tiles}", flush=True)
     assert counts.max() >= 64
+    assert tiles == int(sum((c + 63) // 64 for c in counts if c >= 8))    # the default threshold
     rout, rtop, rtw = qwen64.oracle(0, gw=gw).forward(x)
     assert np.array_equal(top, rtop)
     err = _rel(out, rout)
     print(f"  max rel err zipf B=512: {err:.3e}", flush=True)
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("dense_min", [1, 1 << 30])
+def test_block_dispatch_path_branches(qwen64, dense_min):
+    """B=64 (512 slots, the dispatch path) with every expert forced onto the
+    MFMA branch (dense_min=1) or onto the wave-item GEMV kernels."""
+    banner(f"block B=64 dense_min={dense_min}")
+    x = activations(64, QWEN3.d)
+    qwen64.store.set_dense_min(dense_min)
+    try:
+        out, top, tw = _run_block(qwen64, 0, x)
+        tiles = qwen64.store.dense_tiles()
+    finally:
+        qwen64.store.set_dense_min(0)
+    counts = np.bincount(top.ravel(), minlength=QWEN3.E)
+    if dense_min == 1:
+        assert tiles == int(sum((c + 63) // 64 for c in counts if c > 0))
+    else:
+        assert tiles == 0
+    rout, rtop, rtw = qwen64.oracle(0).forward(x)
+    assert np.array_equal(top, rtop) and np.array_equal(tw.view(np.uint32), rtw.view(np.uint32))
+    err = _rel(out, rout)
+    print(f"  max rel err B=64 dense_min={dense_min}: {err:.3e}", flush=True)
     assert err <= TOL
 
 
