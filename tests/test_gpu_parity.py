@@ -335,6 +335,55 @@ def test_block_nan_tokens(qwen64):
     assert np.all(top2 == -1) and np.all(out2 == 0.0)
 
 
+def _shuffled_store(layer: "Layer"):
+    """The same records in another order (parts and experts interleaved
+    out of (layer, expert, part) order, with gaps), and its offset table:
+    the kernels must then locate records through the table."""
+    s = layer.shape
+    host = layer.host
+    offs = layer.offsets
+    LE = offs.shape[1]
+    recs = []
+    for p in range(3):
+        for key in range(LE):
+            so, po = (int(v) for v in offs[p, key])
+            sb, pb = po - so, Q.record_sizes(*((s.m, s.d) if p < 2 else (s.d, s.m)), layer.group)[1]
+            recs.append((p, key, so, sb, pb))
+    rng = np.random.default_rng(5)
+    order = rng.permutation(len(recs))
+    parts, new = [], np.zeros_like(offs)
+    pos = 0
+    for i in order:
+        p, key, so, sb, pb = recs[i]
+        pos += 256                                   # a gap before every record
+        parts.append((pos, host[so:so + sb + pb]))
+        new[p, key] = (pos, pos + sb)
+        pos = (pos + sb + pb + 15) // 16 * 16
+    blob = np.zeros(pos, np.uint8)
+    for at, data in parts:
+        blob[at:at + len(data)] = data
+    st = HbmExpertStore(s, layer.L, torch.from_numpy(blob).cuda(), new, layer.group)
+    st.set_router(torch.from_numpy(layer.gw).cuda())
+    return st
+
+
+def test_block_record_table_layout(qwen64):
+    """A store whose records are not in (layer, expert, part) order gives the
+    bit-identical block on the decode path, the GEMV dispatch path and the
+    MFMA branch."""
+    banner("block shuffled record layout")
+    shuffled = _shuffled_store(qwen64)
+    for B, dense_min in ((8, 0), (64, 1 << 30), (64, 1)):
+        x = torch.from_numpy(activations(B, QWEN3.d)).cuda()
+        outs = []
+        for st in (qwen64.store, shuffled):
+            st.set_dense_min(dense_min)
+            outs.append(st.layer_ffn_batch(1, x).cpu().numpy())
+            st.set_dense_min(0)
+        assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), (B, dense_min)
+    shuffled.close()
+
+
 def test_block_empty_and_errors(qwen64):
     banner("block B=0 and argument errors")
     s = QWEN3
