@@ -164,6 +164,86 @@ int jm_store_stage_ms(jm_store* s, float* ms, int n);
 #define JM_WS_N_DENSE_TILES 8
 int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t bytes, void* stream);
 
+/* ---- batch decode over all layers (decode_layers_batch) ---- */
+
+/* One sequence's cache of one layer, the reference's KVCache
+ * (decode_kernel.c:328-331): k and v [maxT][n_kv][hd], here bfloat16 device
+ * memory (the reference's is float32). */
+typedef struct jm_kv_cache {
+    void* k;
+    void* v;
+} jm_kv_cache;
+
+/* The reference's KernelW (decode_kernel.c:288-325; ctypes mirror
+ * decoder3.py:49-69) field for field, with device pointers.  Read here:
+ * final_norm, norm1, norm2 [L][d], wq [L][H*hd][d], wk/wv [L][KH*hd][d],
+ * wo [L][d][H*hd] (all bf16), bq/bk/bv (float32, when bias_qkv), qn/kn
+ * [L][hd] (bf16, when qk_norm_type = 1), cos/sin [maxT][hd] (float32).
+ * gate_w and the expert tables are the store's (jm_store_set_router, the
+ * blob); embed and lm_head are not read by jm_decode_layers_batch; w1/w2/w3
+ * and the int8 fields must be NULL and use_i8 0. */
+typedef struct jm_kernel_w {
+    const uint16_t* embed;
+    const void* lm_head;
+    const uint16_t* final_norm;
+    const uint16_t* norm1;
+    const uint16_t* norm2;
+    const uint16_t* wq;
+    const uint16_t* wk;
+    const uint16_t* wv;
+    const uint16_t* wo;
+    const float* bq;
+    const float* bk;
+    const float* bv;
+    const uint16_t* qn;
+    const uint16_t* kn;
+    const uint16_t* gate_w;
+    const uint16_t* w1;
+    const uint16_t* w2;
+    const uint16_t* w3;
+    const uint8_t* wq_i8;
+    const float* wq_i8s;
+    const uint8_t* wk_i8;
+    const float* wk_i8s;
+    const uint8_t* wv_i8;
+    const float* wv_i8s;
+    const uint8_t* wo_i8;
+    const float* wo_i8s;
+    const uint8_t* lm_i8;
+    const float* lm_i8s;
+    const uint8_t* const* expert_pk[3];
+    const uint16_t* const* expert_sc[3];
+    const float* cos;
+    const float* sin;
+    int use_i8;
+} jm_kernel_w;
+
+/*
+ * decode_layers_batch(cfg, W, kv, positions, xin, B, logits)
+ * (decode_kernel.c:1518-1556) over the store's layers: per layer RMSNorm,
+ * attention (QKV, per-head QK-norm, RoPE, KV append at positions[b], SDPA,
+ * o_proj) and residual, RMSNorm, the store's MoE block and residual; then
+ * the final RMSNorm into hidden [B][d] float32.
+ *   cfg        L, d, E, topk, intermediate, norm_topk_prob as the store's;
+ *              n_heads, n_kv (n_heads / n_kv in 1, 2, 4, 8), hd = 128, eps,
+ *              maxT, qk_norm_type (0 or 1), bias_qkv
+ *   kv         HOST array of B * L caches, entry b * L + l (as the reference)
+ *   positions  HOST int32 [B]: the cache row each token writes; attention
+ *              covers rows 0 .. positions[b] (the others must be filled)
+ *   xin        [B][d] float32 (device)
+ *   logits     must be NULL: the lm_head is applied to hidden by the caller
+ * Any B >= 0 (the reference clamps B to 16, decode_kernel.c:1522).  With
+ * jm_store_profile on, jm_store_decode_ms splits the call's time.
+ */
+int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* cfg, const jm_kernel_w* W, const jm_kv_cache* kv,
+                           const int32_t* positions, const float* xin, int B, float* logits, float* hidden,
+                           void* stream);
+
+/* Milliseconds of the last profiled jm_decode_layers_batch call: its
+ * attention parts (norm1 to the o_proj residual, summed over layers), its
+ * MoE blocks (norm2 to the residual) and the whole call (waits for it). */
+int jm_store_decode_ms(jm_store* s, float* attn_ms, float* moe_ms, float* total_ms);
+
 /* ---- stage entry points (the steps of layer_ffn_batch, for tests) ---- */
 
 /* Router scores, softmax, top-k and renormalisation

@@ -15,10 +15,9 @@
 #include <mutex>
 #include <vector>
 
-#include "../../include/joule_amd.h"
-#include "jm_kernels.h"
+#include "jm_store.h"
 
-namespace {
+namespace jm {
 
 thread_local char g_err[512] = "";
 
@@ -34,15 +33,14 @@ int hip_fail(hipError_t e, const char* what) {
     return fail(JM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-#define JM_HIP(expr, what)                              \
-    do {                                                \
-        hipError_t _e = (expr);                         \
-        if (_e != hipSuccess) return hip_fail(_e, what); \
-    } while (0)
+}  // namespace jm
 
-inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+namespace {
 
-bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+using jm::aligned;
+using jm::align256;
+using jm::fail;
+using jm::hip_fail;
 
 int check_group_shape(int d, int m, int group) {
     if (group != 32 && group != 64) return fail(JM_ERR_SHAPE, "group must be 32 or 64, got %d", group);
@@ -61,54 +59,7 @@ int check_group_shape(int d, int m, int group) {
 
 }  // namespace
 
-struct jm_store {
-    int L, E, d, m, topk, renorm, group;
-    const uint8_t* blob;
-    uint64_t blob_bytes;
-    uint64_t* off_dev;          // [3][L*E][2]
-    jm::RecLoc rec;             // record locator (the table, or the affine formula)
-    int dec_last;               // the last call took the decode path
-    int n_cu;                   // compute units of the device (persistent grids)
-    int lds_max;                // LDS bytes one block may use
-    void* wt;                   // [L][Ep/8][d/8/P][64][P] interleaved copy of the router table
-    int wt_bf16;                // the copy holds bf16 (the table is exactly bf16-valued)
-    int device;
-    // workspace, sized for cap_B tokens; last_B = B of the last call
-    int cap_B;
-    int last_B;
-    void* ws;
-    float* logits;
-    int* top;
-    float* tw;
-    uint32_t* xdig;
-    float* xscale;
-    int* seg_off;
-    int* seg_slot;
-    int* active;
-    int* n_active;
-    int* first_slot;
-    int* rank;
-    int* comb;
-    jm::ExpertWork* work;
-    float* act;
-    // optional per-stage events (jm_store_profile)
-    int prof;
-    hipEvent_t ev[JM_STAGES + 1];
-    uint32_t* adig;
-    float* ascale;
-    float* y;
-    int2* tiles;                // dense tiles (dispatch path)
-    int* n_tiles;
-    _Float16* act_h;            // act split for the MFMA down
-    _Float16* act_l;
-    _Float16* xsh;              // tokens split for the MFMA gate/up
-    _Float16* xsl;
-    int dense_min;              // segment size from which an expert takes the MFMA branch
-};
-
-namespace {
-
-int reserve(jm_store* s, int B) {
+int jm::store_reserve(jm_store* s, int B) {
     if (B <= s->cap_B) return 0;
     const int E = s->E, d = s->d, m = s->m, k = s->topk, G = s->group;
     const size_t nslot = (size_t)B * k;
@@ -167,6 +118,8 @@ int reserve(jm_store* s, int B) {
     return 0;
 }
 
+namespace {
+
 int check_store(const jm_store* s) {
     if (!s) return fail(JM_ERR_ARG, "store is NULL");
     return 0;
@@ -174,11 +127,76 @@ int check_store(const jm_store* s) {
 
 }  // namespace
 
+namespace jm {
+
+int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const uint16_t* norm_w,
+                float eps, const float* resid, bool stage_marks, hipStream_t st) {
+    if ((long long)B * s->topk > JM_MAX_SLOTS) return fail(JM_ERR_SHAPE, "B * topk must be <= %d", JM_MAX_SLOTS);
+    if (B * s->topk > JM_DEC_SLOTS && (size_t)jm::dispatch_lds_ints(B * s->topk, s->E) * 4 > (size_t)s->lds_max)
+        return fail(JM_ERR_SHAPE, "B * topk = %d slots over %d experts exceed the dispatch's LDS", B * s->topk, s->E);
+    if (int rc = store_reserve(s, B)) return rc;
+    const int E = s->E, d = s->d, k = s->topk, G = s->group;
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    const int umax = std::min(E, B * k);
+    const int nslot = B * k;
+    const bool dec = nslot <= JM_DEC_SLOTS;
+    jm::RouteArgs r;
+    r.wt = (const char*)s->wt + (size_t)layer * jm::router_experts_padded(E) * d * (s->wt_bf16 ? 2 : 4);
+    r.wt_bf16 = s->wt_bf16;
+    r.x = x; r.norm_w = norm_w; r.eps = eps; r.B = B; r.E = E; r.d = d; r.topk = k; r.renorm = s->renorm; r.group = G;
+    r.logits = s->logits; r.xdig = s->xdig; r.xscale = s->xscale; r.top = s->top; r.tw = s->tw;
+    r.seg_off = s->seg_off; r.seg_slot = s->seg_slot; r.active = s->active; r.n_active = s->n_active;
+    r.first_slot = s->first_slot; r.comb = s->comb; r.rank_scratch = s->rank;
+    r.work = s->work; r.umax = umax; r.rec = s->rec;
+    r.key0 = (long long)layer * E;
+    r.dense_min = s->dense_min; r.tiles = s->tiles; r.n_tiles = s->n_tiles;
+    jm::ExpertArgs a;
+    a.blob = s->blob; a.rec = s->rec; a.key0 = (long long)layer * E; a.E = E;
+    a.work = s->work; a.umax = umax; a.seg_slot = s->seg_slot;
+    a.top = s->top; a.nslot = nslot; a.B = B;
+    a.d = d; a.m = s->m; a.topk = k; a.group = G;
+    a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
+    a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y; a.out = out; a.resid = resid;
+    a.dense_min = jm::mfma_shape_ok(d, s->m) ? s->dense_min : 0x7FFFFFFF;
+    r.dense_min = a.dense_min;
+    a.tiles = s->tiles; a.n_tiles = s->n_tiles;
+    r.xsh = dec ? nullptr : s->xsh; r.xsl = dec ? nullptr : s->xsl;
+    a.xsh = s->xsh; a.xsl = s->xsl;
+    a.act_h = s->act_h; a.act_l = s->act_l;
+    const int max_tiles = nslot / JM_DENSE_TILE + E;
+#define JM_MARK(i) if (s->prof && stage_marks) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
+    JM_MARK(0);
+    JM_HIP(jm::launch_route_tok(r, st), "route launch");
+    if (!dec) JM_HIP(jm::launch_dispatch_work(r, st), "dispatch launch");
+    JM_MARK(1);
+    if (dec) {
+        JM_HIP(jm::launch_gateup_dec(a, st), "gate/up launch");
+    } else {
+        JM_HIP(jm::launch_gateup(a, umax, st), "gate/up launch");
+        JM_HIP(jm::launch_gateup_mfma(a, max_tiles, st), "gate/up MFMA launch");
+    }
+    JM_MARK(2);
+    if (dec) {
+        JM_HIP(jm::launch_down_comb(a, st), "down/combine launch");
+    } else {
+        JM_HIP(jm::launch_down(a, umax, st), "down launch");
+        JM_HIP(jm::launch_down_mfma(a, max_tiles, st), "down MFMA launch");
+        JM_HIP(jm::launch_combine(s->y, s->comb, B, k, d, resid, out, st), "combine launch");
+    }
+    JM_MARK(3);
+#undef JM_MARK
+    s->dec_last = dec;
+    s->last_B = B;
+    return 0;
+}
+
+}  // namespace jm
+
 extern "C" {
 
 int jm_version(void) { return JM_ABI_VERSION; }
 
-const char* jm_last_error(void) { return g_err; }
+const char* jm_last_error(void) { return jm::g_err; }
 
 int jm_abi_sizes(int* kernel_cfg_bytes, int* ndig, int* nt) {
     if (kernel_cfg_bytes) *kernel_cfg_bytes = (int)sizeof(jm_kernel_cfg);
@@ -277,6 +295,7 @@ int jm_store_destroy(jm_store* s) {
     if (s->ws) (void)hipFree(s->ws);
     if (s->prof)
         for (int i = 0; i <= JM_STAGES; i++) (void)hipEventDestroy(s->ev[i]);
+    jm::decode_free_all(s);
     delete s;
     return 0;
 }
@@ -317,7 +336,7 @@ int jm_store_set_router(jm_store* s, const void* gate_w, int dtype) {
 int jm_store_reserve(jm_store* s, int max_B) {
     if (int rc = check_store(s)) return rc;
     if (max_B < 0) return fail(JM_ERR_ARG, "max_B must be >= 0");
-    return reserve(s, max_B);
+    return jm::store_reserve(s, max_B);
 }
 
 int jm_store_set_dense_min(jm_store* s, int min_tokens) {
@@ -354,63 +373,9 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     if (B == 0) return 0;
     if (!x || !out) return fail(JM_ERR_ARG, "x and out must be non-NULL");
     if (!aligned(x, 16) || !aligned(out, 16)) return fail(JM_ERR_ARG, "x and out must be 16-byte aligned");
-    if ((long long)B * s->topk > JM_MAX_SLOTS) return fail(JM_ERR_SHAPE, "B * topk must be <= %d", JM_MAX_SLOTS);
-    if (B * s->topk > JM_DEC_SLOTS && (size_t)jm::dispatch_lds_ints(B * s->topk, s->E) * 4 > (size_t)s->lds_max)
-        return fail(JM_ERR_SHAPE, "B * topk = %d slots over %d experts exceed the dispatch's LDS", B * s->topk, s->E);
-    if (int rc = reserve(s, B)) return rc;
     hipStream_t st = (hipStream_t)stream;
-    const int E = s->E, d = s->d, k = s->topk, G = s->group;
-    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
-    const int umax = std::min(E, B * k);
-    const int nslot = B * k;
-    const bool dec = nslot <= JM_DEC_SLOTS;
-    jm::RouteArgs r;
-    r.wt = (const char*)s->wt + (size_t)layer * jm::router_experts_padded(E) * d * (s->wt_bf16 ? 2 : 4);
-    r.wt_bf16 = s->wt_bf16;
-    r.x = x; r.B = B; r.E = E; r.d = d; r.topk = k; r.renorm = s->renorm; r.group = G;
-    r.logits = s->logits; r.xdig = s->xdig; r.xscale = s->xscale; r.top = s->top; r.tw = s->tw;
-    r.seg_off = s->seg_off; r.seg_slot = s->seg_slot; r.active = s->active; r.n_active = s->n_active;
-    r.first_slot = s->first_slot; r.comb = s->comb; r.rank_scratch = s->rank;
-    r.work = s->work; r.umax = umax; r.rec = s->rec;
-    r.key0 = (long long)layer * E;
-    r.dense_min = s->dense_min; r.tiles = s->tiles; r.n_tiles = s->n_tiles;
-    jm::ExpertArgs a;
-    a.blob = s->blob; a.rec = s->rec; a.key0 = (long long)layer * E; a.E = E;
-    a.work = s->work; a.umax = umax; a.seg_slot = s->seg_slot;
-    a.top = s->top; a.nslot = nslot; a.B = B;
-    a.d = d; a.m = s->m; a.topk = k; a.group = G;
-    a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
-    a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y; a.out = out;
-    a.dense_min = jm::mfma_shape_ok(d, s->m) ? s->dense_min : 0x7FFFFFFF;
-    r.dense_min = a.dense_min;
-    a.tiles = s->tiles; a.n_tiles = s->n_tiles;
-    r.xsh = dec ? nullptr : s->xsh; r.xsl = dec ? nullptr : s->xsl;
-    a.xsh = s->xsh; a.xsl = s->xsl;
-    a.act_h = s->act_h; a.act_l = s->act_l;
-    const int max_tiles = nslot / JM_DENSE_TILE + E;
-#define JM_MARK(i) if (s->prof) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
-    JM_MARK(0);
-    JM_HIP(jm::launch_route_tok(r, st), "route launch");
-    if (!dec) JM_HIP(jm::launch_dispatch_work(r, st), "dispatch launch");
-    JM_MARK(1);
-    if (dec) {
-        JM_HIP(jm::launch_gateup_dec(a, st), "gate/up launch");
-    } else {
-        JM_HIP(jm::launch_gateup(a, umax, st), "gate/up launch");
-        JM_HIP(jm::launch_gateup_mfma(a, max_tiles, st), "gate/up MFMA launch");
-    }
-    JM_MARK(2);
-    if (dec) {
-        JM_HIP(jm::launch_down_comb(a, st), "down/combine launch");
-    } else {
-        JM_HIP(jm::launch_down(a, umax, st), "down launch");
-        JM_HIP(jm::launch_down_mfma(a, max_tiles, st), "down MFMA launch");
-        JM_HIP(jm::launch_combine(s->y, s->comb, B, k, d, out, st), "combine launch");
-    }
-    JM_MARK(3);
-#undef JM_MARK
-    s->dec_last = dec;
-    s->last_B = B;
+    if (int rc = jm::ffn_enqueue(s, layer, x, B, out, nullptr, 0.0f, nullptr, true, st)) return rc;
+    const int k = s->topk;
     if (topk_idx) JM_HIP(hipMemcpyAsync(topk_idx, s->top, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k");
     if (topk_w) JM_HIP(hipMemcpyAsync(topk_w, s->tw, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k weights");
     return 0;

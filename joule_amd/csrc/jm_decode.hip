@@ -1,0 +1,272 @@
+// Batch decode over all layers: decode_layers_batch(cfg, W, kv, positions,
+// xin, B, logits) (decode_kernel.c:1518-1556) on the GPU, with the MoE block
+// of each layer from the store.  Per layer, five launches around the MoE
+// block's own:
+//
+//   qkv      = [Wq; Wk; Wv] . RMSNorm1(h) (+ bias)            k_gemv_bf16
+//   partials = attention over 128-position splits of the cache  k_attn_part
+//   att      = the splits merged                               k_attn_comb
+//   h       += Wo . att                                        k_gemv_bf16
+//   h       += MoE(RMSNorm2(h))    the norm inside the router, the add inside
+//                                  the down/combine kernel
+//
+// then hidden = RMSNorm_final(h).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cstring>
+
+#include "jm_store.h"
+
+using jm::align256;
+using jm::aligned;
+using jm::fail;
+using jm::hip_fail;
+
+namespace {
+
+constexpr int HD = 128;     // head dimension the attention kernels take
+constexpr int PSPLIT = 128; // positions per attention split
+
+void free_decode(jm_store* s) {
+    if (s->dws) (void)hipFree(s->dws);
+    s->dws = nullptr;
+    s->dec_B = s->dec_S = s->dec_nqkv = s->dec_hq = 0;
+}
+
+int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq) {
+    const size_t tab_bytes = align256((size_t)B * s->L * 16 + (size_t)B * 4);
+    if (tab_bytes > s->tab_cap) {
+        if (s->tab_pending) JM_HIP(hipEventSynchronize(s->tab_ev), "hipEventSynchronize staging");
+        s->tab_pending = 0;
+        if (s->tab_host) (void)hipHostFree(s->tab_host);
+        s->tab_host = nullptr;
+        JM_HIP(hipHostMalloc((void**)&s->tab_host, tab_bytes, hipHostMallocDefault), "hipHostMalloc staging");
+        s->tab_cap = tab_bytes;
+        s->dec_B = 0;   // the device table lives in the workspace: regrow it too
+    }
+    if (!s->tab_ev) JM_HIP(hipEventCreateWithFlags(&s->tab_ev, hipEventDisableTiming), "hipEventCreate");
+    if (B <= s->dec_B && S <= s->dec_S && nqkv <= s->dec_nqkv && hq <= s->dec_hq) return 0;
+    B = std::max(B, s->dec_B);
+    S = std::max(S, s->dec_S);
+    nqkv = std::max(nqkv, s->dec_nqkv);
+    hq = std::max(hq, s->dec_hq);
+    const int d = s->d;
+    const size_t sz[] = {
+        (size_t)B * d * 4,                        // h
+        (size_t)B * nqkv * 4,                     // qkv
+        (size_t)B * S * hq * 4,                   // part_o: H heads x hd per split
+        (size_t)B * S * (hq / HD) * 2 * 4,        // part_ml
+        (size_t)B * hq * 4,                       // att
+        s->tab_cap,                               // KV pointers + positions
+    };
+    size_t total = 0;
+    for (size_t v : sz) total += align256(v);
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize before decode workspace growth");
+    free_decode(s);
+    JM_HIP(hipMalloc(&s->dws, total), "hipMalloc decode workspace");
+    char* p = (char*)s->dws;
+    void** slots[] = {(void**)&s->h, (void**)&s->qkv, (void**)&s->part_o, (void**)&s->part_ml,
+                      (void**)&s->att, (void**)&s->tab};
+    for (size_t i = 0; i < sizeof sz / sizeof sz[0]; i++) {
+        *slots[i] = p;
+        p += align256(sz[i]);
+    }
+    JM_HIP(hipMemset(s->dws, 0, total), "hipMemset decode workspace");
+    JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize after decode workspace clear");
+    s->dec_B = B; s->dec_S = S; s->dec_nqkv = nqkv; s->dec_hq = hq;
+    return 0;
+}
+
+int check_decode_args(const jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, int* qpk) {
+    if (c->L != s->L || c->d != s->d || c->E != s->E || c->topk != s->topk || c->intermediate != s->m)
+        return fail(JM_ERR_SHAPE, "cfg (L=%d d=%d E=%d topk=%d m=%d) does not match the store (L=%d d=%d E=%d topk=%d m=%d)",
+                    c->L, c->d, c->E, c->topk, c->intermediate, s->L, s->d, s->E, s->topk, s->m);
+    if ((c->norm_topk_prob ? 1 : 0) != s->renorm) return fail(JM_ERR_SHAPE, "cfg norm_topk_prob differs from the store's");
+    if (c->hd != HD) return fail(JM_ERR_SHAPE, "head dim must be %d (got %d)", HD, c->hd);
+    if (c->n_heads <= 0 || c->n_kv <= 0 || c->n_heads % c->n_kv)
+        return fail(JM_ERR_SHAPE, "n_heads=%d must be a positive multiple of n_kv=%d", c->n_heads, c->n_kv);
+    *qpk = c->n_heads / c->n_kv;
+    if (*qpk != 1 && *qpk != 2 && *qpk != 4 && *qpk != 8)
+        return fail(JM_ERR_SHAPE, "n_heads / n_kv must be 1, 2, 4 or 8 (got %d)", *qpk);
+    if (!jm::gemv_shape_ok(c->d) || !jm::gemv_shape_ok(c->n_heads * HD))
+        return fail(JM_ERR_SHAPE, "d=%d and n_heads*hd=%d must each be 1024, 2048 or 4096", c->d, c->n_heads * HD);
+    if (c->qk_norm_type != 0 && c->qk_norm_type != 1)
+        return fail(JM_ERR_SHAPE, "qk_norm_type %d: only 0 (none) and 1 (per head) are supported", c->qk_norm_type);
+    if (c->maxT <= 0) return fail(JM_ERR_SHAPE, "maxT must be positive");
+    if (!(c->eps >= 0.0f)) return fail(JM_ERR_SHAPE, "eps must be >= 0");
+    if (!W) return fail(JM_ERR_ARG, "weights are NULL");
+    if (!W->final_norm || !W->norm1 || !W->norm2 || !W->wq || !W->wk || !W->wv || !W->wo || !W->cos || !W->sin)
+        return fail(JM_ERR_ARG, "final_norm, norm1, norm2, wq, wk, wv, wo, cos and sin must be set");
+    if (c->qk_norm_type == 1 && (!W->qn || !W->kn)) return fail(JM_ERR_ARG, "qk_norm_type 1 needs qn and kn");
+    if (c->bias_qkv && (!W->bq || !W->bk || !W->bv)) return fail(JM_ERR_ARG, "bias_qkv needs bq, bk and bv");
+    if (W->use_i8 || W->wq_i8 || W->wk_i8 || W->wv_i8 || W->wo_i8 || W->lm_i8)
+        return fail(JM_ERR_ARG, "the int8 attention weights are not supported (use_i8 = 0, *_i8 = NULL)");
+    if (W->w1 || W->w2 || W->w3) return fail(JM_ERR_ARG, "dense FFN layers (w1/w2/w3) are not supported: the FFN is the store's MoE");
+    const void* al[] = {W->final_norm, W->norm1, W->norm2, W->wq, W->wk, W->wv, W->wo, W->cos, W->sin,
+                        c->qk_norm_type == 1 ? (const void*)W->qn : nullptr,
+                        c->qk_norm_type == 1 ? (const void*)W->kn : nullptr};
+    for (const void* p : al)
+        if (p && !aligned(p, 16)) return fail(JM_ERR_ARG, "weight tensors must be 16-byte aligned");
+    return 0;
+}
+
+}  // namespace
+
+namespace jm {
+
+void decode_free_all(jm_store* s) {
+    free_decode(s);
+    if (s->tab_pending) (void)hipEventSynchronize(s->tab_ev);
+    if (s->tab_host) (void)hipHostFree(s->tab_host);
+    if (s->tab_ev) (void)hipEventDestroy(s->tab_ev);
+    if (s->dev_marks) {
+        for (int i = 0; i < s->dprof_n; i++) (void)hipEventDestroy(s->dev_marks[i]);
+        delete[] s->dev_marks;
+    }
+    s->tab_host = nullptr;
+    s->tab_ev = nullptr;
+    s->dev_marks = nullptr;
+    s->dprof_n = 0;
+}
+
+}  // namespace jm
+
+extern "C" {
+
+int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const jm_kv_cache* kv,
+                           const int32_t* positions, const float* xin, int B, float* logits, float* hidden,
+                           void* stream) {
+    if (!s || !c) return fail(JM_ERR_ARG, "store and cfg must be non-NULL");
+    if (!s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
+    int qpk = 0;
+    if (int rc = check_decode_args(s, c, W, &qpk)) return rc;
+    if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
+    if (B == 0) return 0;
+    if (!kv || !positions || !xin || !hidden) return fail(JM_ERR_ARG, "kv, positions, xin and hidden must be non-NULL");
+    if (logits) return fail(JM_ERR_ARG, "logits: the lm_head is not part of this call; pass NULL and apply it to hidden");
+    if (!aligned(xin, 16) || !aligned(hidden, 16)) return fail(JM_ERR_ARG, "xin and hidden must be 16-byte aligned");
+    const int L = c->L, d = c->d, H = c->n_heads, KH = c->n_kv;
+    int maxT = 0;
+    for (int b = 0; b < B; b++) {
+        if (positions[b] < 0 || positions[b] >= c->maxT)
+            return fail(JM_ERR_ARG, "positions[%d] = %d outside [0, maxT=%d)", b, positions[b], c->maxT);
+        maxT = std::max(maxT, positions[b] + 1);
+    }
+    for (long long i = 0; i < (long long)B * L; i++)
+        if (!kv[i].k || !kv[i].v || !aligned(kv[i].k, 16) || !aligned(kv[i].v, 16))
+            return fail(JM_ERR_ARG, "kv[%lld]: k and v must be non-NULL and 16-byte aligned", i);
+    const int nqkv = (H + 2 * KH) * HD;
+    const int S = (maxT + PSPLIT - 1) / PSPLIT;
+    const int S_cap = (c->maxT + PSPLIT - 1) / PSPLIT;
+    if (int rc = jm::store_reserve(s, B)) return rc;
+    if (int rc = decode_reserve(s, B, S_cap, nqkv, H * HD)) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+
+    // KV pointer table and positions to the device through pinned staging
+    if (s->tab_pending) JM_HIP(hipEventSynchronize(s->tab_ev), "hipEventSynchronize staging");
+    for (long long i = 0; i < (long long)B * L; i++) {
+        s->tab_host[2 * i] = (unsigned long long)(uintptr_t)kv[i].k;
+        s->tab_host[2 * i + 1] = (unsigned long long)(uintptr_t)kv[i].v;
+    }
+    int* pos_host = (int*)(s->tab_host + (size_t)2 * B * L);
+    memcpy(pos_host, positions, (size_t)B * 4);
+    const size_t tab_bytes = (size_t)B * L * 16 + (size_t)B * 4;
+    JM_HIP(hipMemcpyAsync(s->tab, s->tab_host, tab_bytes, hipMemcpyHostToDevice, st), "staging copy");
+    JM_HIP(hipEventRecord(s->tab_ev, st), "hipEventRecord staging");
+    s->tab_pending = 1;
+    const int* pos_dev = (const int*)(s->tab + (size_t)2 * B * L);
+
+    // per-layer split of the time (jm_store_profile)
+    const int nmarks = 2 * L + 3;
+    if (s->prof && s->dprof_n != nmarks) {
+        if (s->dev_marks) {
+            JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+            for (int i = 0; i < s->dprof_n; i++) (void)hipEventDestroy(s->dev_marks[i]);
+            delete[] s->dev_marks;
+        }
+        s->dev_marks = new hipEvent_t[nmarks];
+        s->dprof_n = 0;
+        for (int i = 0; i < nmarks; i++) {
+            JM_HIP(hipEventCreateWithFlags(&s->dev_marks[i], hipEventDisableSystemFence), "hipEventCreate");
+            s->dprof_n = i + 1;
+        }
+    }
+#define JM_DMARK(i) if (s->prof) JM_HIP(hipEventRecord(s->dev_marks[i], st), "hipEventRecord")
+
+    JM_DMARK(0);
+    JM_HIP(hipMemcpyAsync(s->h, xin, (size_t)B * d * 4, hipMemcpyDeviceToDevice, st), "copy xin");
+    const float sdiv = jm::sqrtf_fast((float)HD);
+    for (int l = 0; l < L; l++) {
+        JM_DMARK(2 * l + 1);
+        jm::GemvArgs g{};
+        g.x = s->h;
+        g.norm_w = W->norm1 + (size_t)l * d;
+        g.eps = c->eps;
+        g.w[0] = W->wq + (size_t)l * H * HD * d;
+        g.w[1] = W->wk + (size_t)l * KH * HD * d;
+        g.w[2] = W->wv + (size_t)l * KH * HD * d;
+        if (c->bias_qkv) {
+            g.bias[0] = W->bq + (size_t)l * H * HD;
+            g.bias[1] = W->bk + (size_t)l * KH * HD;
+            g.bias[2] = W->bv + (size_t)l * KH * HD;
+        }
+        g.rows[0] = H * HD; g.rows[1] = KH * HD; g.rows[2] = KH * HD;
+        g.K = d; g.N = nqkv; g.B = B;
+        g.out = s->qkv;
+        JM_HIP(jm::launch_gemv_bf16(g, 4, st), "qkv launch");
+
+        jm::AttnArgs at{};
+        at.qkv = s->qkv; at.nqkv = nqkv; at.H = H; at.KH = KH; at.B = B;
+        at.qn = c->qk_norm_type == 1 ? W->qn + (size_t)l * HD : nullptr;
+        at.kn = c->qk_norm_type == 1 ? W->kn + (size_t)l * HD : nullptr;
+        at.eps = c->eps; at.sdiv = sdiv;
+        at.cos = W->cos; at.sin = W->sin;
+        at.pos = pos_dev; at.kv = s->tab; at.L = L; at.layer = l;
+        at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;
+        // the grid covers the longest token's splits; the buffers hold S_cap
+        // per (token, KV head), indexed with the call's S
+        JM_HIP(jm::launch_attn(at, qpk, s->att, st), "attention launch");
+
+        jm::GemvArgs o{};
+        o.x = s->att;
+        o.w[0] = W->wo + (size_t)l * d * H * HD;
+        o.rows[0] = d;
+        o.K = H * HD; o.N = d; o.B = B;
+        o.resid = s->h; o.out = s->h;
+        JM_HIP(jm::launch_gemv_bf16(o, 2, st), "o_proj launch");
+
+        JM_DMARK(2 * l + 2);
+        if (int rc = jm::ffn_enqueue(s, l, s->h, B, s->h, W->norm2 + (size_t)l * d, c->eps, s->h, false, st))
+            return rc;
+    }
+    JM_DMARK(2 * L + 1);
+    JM_HIP(jm::launch_rms_rows(s->h, W->final_norm, B, d, c->eps, hidden, st), "final norm launch");
+    JM_DMARK(2 * L + 2);
+#undef JM_DMARK
+    return 0;
+}
+
+int jm_store_decode_ms(jm_store* s, float* attn_ms, float* moe_ms, float* total_ms) {
+    if (!s) return fail(JM_ERR_ARG, "store is NULL");
+    if (!s->prof || !s->dev_marks) return fail(JM_ERR_ARG, "no profiled decode call (jm_store_profile, then jm_decode_layers_batch)");
+    const int L = (s->dprof_n - 3) / 2;
+    JM_HIP(hipEventSynchronize(s->dev_marks[s->dprof_n - 1]), "hipEventSynchronize");
+    float at = 0.0f, mo = 0.0f, tot = 0.0f, v = 0.0f;
+    for (int l = 0; l < L; l++) {
+        JM_HIP(hipEventElapsedTime(&v, s->dev_marks[2 * l + 1], s->dev_marks[2 * l + 2]), "hipEventElapsedTime");
+        at += v;
+        JM_HIP(hipEventElapsedTime(&v, s->dev_marks[2 * l + 2], s->dev_marks[2 * l + 3]), "hipEventElapsedTime");
+        mo += v;
+    }
+    JM_HIP(hipEventElapsedTime(&tot, s->dev_marks[0], s->dev_marks[s->dprof_n - 1]), "hipEventElapsedTime");
+    if (attn_ms) *attn_ms = at;
+    if (moe_ms) *moe_ms = mo;
+    if (total_ms) *total_ms = tot;
+    return 0;
+}
+
+}  // extern "C"

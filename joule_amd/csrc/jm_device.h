@@ -72,6 +72,31 @@ __device__ __forceinline__ float expf_fast(float v) {
     return (zero || biased < 0) ? 0.0f : r;
 }
 
+// The reference's square root, decode_kernel.c:88-93: a bit-level first
+// guess (exponent halved) refined by one Newton step; relative error below
+// 2e-3, exact at powers of 4.
+__host__ __device__ __forceinline__ float sqrtf_fast(float x) {
+    union { float f; uint32_t u; } v = {x};
+    v.u = (v.u + 0x3F800000u) >> 1;
+#ifdef __HIP_DEVICE_COMPILE__
+    return __fmul_rn(0.5f, __fadd_rn(v.f, __fdiv_rn(x, v.f)));
+#else
+    return 0.5f * (v.f + x / v.f);
+#endif
+}
+
+// RMSNorm scale of a row with sum of squares ss over n values, as
+// rms_norm computes it (decode_kernel.c:224-230): 1 / sqrtf_fast(ss / n + eps).
+__device__ __forceinline__ float rms_inv(float ss, int n, float eps) {
+    return __fdiv_rn(1.0f, sqrtf_fast(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
+}
+
+// float -> bfloat16 bits, round to nearest even (finite values).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
 // SiLU(g) * u exactly as the reference writes it: (g / (1 + e^-g)) * u.
 __device__ __forceinline__ float swiglu(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_fast(-g))), u);

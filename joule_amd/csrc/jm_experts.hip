@@ -497,7 +497,9 @@ k_down_comb(ExpertArgs a) {
             const int sl = comb_l[b * k + j];
             if (sl >= 0) acc = __fadd_rn(acc, ypart[sl * R + rr]);
         }
-        a.out[(size_t)b * a.d + (size_t)c * R + rr] = acc;
+        const size_t oi = (size_t)b * a.d + (size_t)c * R + rr;
+        // the residual add h + block of the decoder layer (resid may be out)
+        a.out[oi] = a.resid ? __fadd_rn(a.resid[oi], acc) : acc;
     }
 }
 
@@ -505,7 +507,7 @@ k_down_comb(ExpertArgs a) {
 
 __global__ void __launch_bounds__(256)
 k_combine(const float* __restrict__ y, const int* __restrict__ comb, int B, int k, int d,
-          float* __restrict__ out) {
+          const float* resid, float* out) {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     const int d4 = d / 4;
     if (idx >= B * d4) return;
@@ -520,6 +522,10 @@ k_combine(const float* __restrict__ y, const int* __restrict__ comb, int B, int 
             acc.x = __fadd_rn(acc.x, v.x); acc.y = __fadd_rn(acc.y, v.y);
             acc.z = __fadd_rn(acc.z, v.z); acc.w = __fadd_rn(acc.w, v.w);
         }
+    }
+    if (resid) {   // the residual add h + block of the decoder layer
+        const float4 h = *(const float4*)(resid + (size_t)b * d + r);
+        acc = make_float4(__fadd_rn(h.x, acc.x), __fadd_rn(h.y, acc.y), __fadd_rn(h.z, acc.z), __fadd_rn(h.w, acc.w));
     }
     *(float4*)(out + (size_t)b * d + r) = acc;
 }
@@ -590,10 +596,12 @@ hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_combine(const float* y, const int* comb, int B, int k, int d, float* out, hipStream_t st) {
+hipError_t launch_combine(const float* y, const int* comb, int B, int k, int d, const float* resid,
+                          float* out, hipStream_t st) {
     const long long n = (long long)B * (d / 4);
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, comb, B, k, d, out);
+    hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, comb, B, k, d,
+                       resid, out);
     return hipGetLastError();
 }
 

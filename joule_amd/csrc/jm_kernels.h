@@ -54,7 +54,8 @@ struct ExpertArgs {
     uint32_t* adig;           // [B*k][m/8][NDIG] act digits, 8 values per group
     float* ascale;            // [B*k][m/8]
     float* y;                 // [B*k][d]   weighted expert output per slot (dispatch path)
-    float* out;               // [B][d]     block output (decode path)
+    float* out;               // [B][d]     block output
+    const float* resid;       // [B][d]     added to the block output (NULL: none); may alias out
     int group;
     // dispatch path, dense branch
     int dense_min;            // experts with at least this many slots take the MFMA kernels
@@ -70,6 +71,8 @@ struct RouteArgs {
     const void* wt;           // interleaved router copy of the layer
     int wt_bf16;              // 1: wt holds bf16 bits, 0: float32
     const float* x;           // [B][d]
+    const uint16_t* norm_w;   // [d] bf16 RMSNorm weight applied to x first (NULL: x as given)
+    float eps;
     int B, E, d, topk, renorm, group;
     float* logits;            // [B][E]
     uint32_t* xdig;           // [B][d/G][NDIG][G/8]
@@ -127,8 +130,51 @@ hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st);
 bool mfma_shape_ok(int d, int m);
 hipError_t launch_gateup_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st);
 hipError_t launch_down_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st);
-// out[b] = sum of the token's slots of y in the order comb gives
-hipError_t launch_combine(const float* y, const int* comb, int B, int k, int d, float* out, hipStream_t st);
+// out[b] = (resid[b] +) sum of the token's slots of y in the order comb gives
+hipError_t launch_combine(const float* y, const int* comb, int B, int k, int d, const float* resid,
+                          float* out, hipStream_t st);
+// ---- decoder layer around the MoE block (jm_attn.hip)
+
+// out[b][row] = (resid +) (bias +) W[row] . xn[b] over the rows of up to three
+// stacked bf16 matrices [rows_i][K]; xn = x or RMSNorm(x) * norm_w.
+struct GemvArgs {
+    const float* x;           // [B][K]
+    const uint16_t* norm_w;   // [K] bf16, or NULL
+    float eps;
+    const uint16_t* w[3];     // bf16 [rows[i]][K]
+    const float* bias[3];     // fp32 [rows[i]] or NULL
+    int rows[3];
+    int K, N, B;              // N = rows[0] + rows[1] + rows[2] (the out row stride)
+    const float* resid;       // [B][N] or NULL; may alias out
+    float* out;               // [B][N]
+};
+// K in {1024, 2048, 4096}; rows_per_wave 2 or 4 (4 waves per block)
+bool gemv_shape_ok(int K);
+hipError_t launch_gemv_bf16(const GemvArgs& a, int rows_per_wave, hipStream_t st);
+
+// Decode attention of one layer for B tokens, head dim 128, H / KH query
+// heads per KV head (1, 2, 4 or 8), in splits of 128 positions.
+struct AttnArgs {
+    const float* qkv;         // [B][nqkv]: H q heads, KH k heads, KH v heads
+    int nqkv, H, KH, B;
+    const uint16_t* qn;       // [128] bf16 per-head q norm of the layer, or NULL
+    const uint16_t* kn;       // [128] bf16 per-head k norm, or NULL
+    float eps;
+    float sdiv;               // score divisor sqrtf_fast(128)
+    const float* cos;         // [maxT][128]
+    const float* sin;
+    const int* pos;           // [B] position each token writes (T = pos + 1)
+    const unsigned long long* kv;   // [B*L][2] bf16 k, v caches [maxT][KH][128]
+    int L, layer;
+    int S;                    // splits the partial buffers hold per (token, KV head)
+    float* part_o;            // [B][KH][S][H/KH][128]
+    float* part_ml;           // [B][KH][S][H/KH][2]
+};
+// partial attention, then the merge into att [B][H*128]
+hipError_t launch_attn(const AttnArgs& a, int qpk, float* att, hipStream_t st);
+hipError_t launch_rms_rows(const float* x, const uint16_t* w, int B, int d, float eps, float* out,
+                           hipStream_t st);
+
 hipError_t launch_dequant(const uint8_t* packed, const uint16_t* scales, long long numel, int group,
                           float* out, hipStream_t st);
 hipError_t launch_q4_rows(const uint8_t* packed, const uint16_t* scales, int rows, int cols, int group,

@@ -166,6 +166,28 @@ k_router_grp(RouteArgs a) {
     uint4 buf[NB][C::CP];
 #pragma unroll
     for (int c = 0; c < NB; c++) C::load(buf[c], wt, eg, c, lane);
+    if (a.norm_w) {
+        // the decoder layer's RMSNorm of the token first (decode_kernel.c:224-230,
+        // applied at :1549): x * (1 / sqrtf_fast(sum x^2 / d + eps)) * w
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            ss = __builtin_fmaf(xv[i].x, xv[i].x, ss);
+            ss = __builtin_fmaf(xv[i].y, xv[i].y, ss);
+            ss = __builtin_fmaf(xv[i].z, xv[i].z, ss);
+            ss = __builtin_fmaf(xv[i].w, xv[i].w, ss);
+        }
+        const float inv = rms_inv(seg_sum<64>(ss), d, a.eps);
+        const uint2* nw = (const uint2*)a.norm_w;
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const uint2 w = nw[lane + 64 * i];
+            xv[i].x = __fmul_rn(__fmul_rn(xv[i].x, inv), bf16_bits_to_f32(w.x & 0xFFFFu));
+            xv[i].y = __fmul_rn(__fmul_rn(xv[i].y, inv), bf16_bits_to_f32(w.x >> 16));
+            xv[i].z = __fmul_rn(__fmul_rn(xv[i].z, inv), bf16_bits_to_f32(w.y & 0xFFFFu));
+            xv[i].w = __fmul_rn(__fmul_rn(xv[i].w, inv), bf16_bits_to_f32(w.y >> 16));
+        }
+    }
 #pragma unroll
     for (int i = 0; i < XV; i++) {
         const int j = 4 * (lane + 64 * i);

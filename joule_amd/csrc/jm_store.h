@@ -1,0 +1,101 @@
+// The store handle behind the C ABI and the helpers its entry points share
+// (jm_api.hip: the MoE block and the stage entry points; jm_decode.hip: the
+// batch-decode driver around it).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/joule_amd.h"
+#include "jm_kernels.h"
+
+struct jm_store {
+    int L, E, d, m, topk, renorm, group;
+    const uint8_t* blob;
+    uint64_t blob_bytes;
+    uint64_t* off_dev;          // [3][L*E][2]
+    jm::RecLoc rec;             // record locator (the table, or the affine formula)
+    int dec_last;               // the last call took the decode path
+    int n_cu;                   // compute units of the device (persistent grids)
+    int lds_max;                // LDS bytes one block may use
+    void* wt;                   // [L][Ep/8][d/8/P][64][P] interleaved copy of the router table
+    int wt_bf16;                // the copy holds bf16 (the table is exactly bf16-valued)
+    int device;
+    // workspace, sized for cap_B tokens; last_B = B of the last call
+    int cap_B;
+    int last_B;
+    void* ws;
+    float* logits;
+    int* top;
+    float* tw;
+    uint32_t* xdig;
+    float* xscale;
+    int* seg_off;
+    int* seg_slot;
+    int* active;
+    int* n_active;
+    int* first_slot;
+    int* rank;
+    int* comb;
+    jm::ExpertWork* work;
+    float* act;
+    // optional per-stage events (jm_store_profile)
+    int prof;
+    hipEvent_t ev[JM_STAGES + 1];
+    uint32_t* adig;
+    float* ascale;
+    float* y;
+    int2* tiles;                // dense tiles (dispatch path)
+    int* n_tiles;
+    _Float16* act_h;            // act split for the MFMA down
+    _Float16* act_l;
+    _Float16* xsh;              // tokens split for the MFMA gate/up
+    _Float16* xsl;
+    int dense_min;              // segment size from which an expert takes the MFMA branch
+    // ---- batch decode (jm_decode_layers_batch) ----
+    int dec_B, dec_S, dec_nqkv, dec_hq;   // sizes the decode workspace holds
+    void* dws;                  // decode workspace
+    float* h;                   // [B][d] residual stream
+    float* qkv;                 // [B][(H + 2 KH) hd] projections
+    float* part_o;              // [B][KH][S][H/KH][hd] attention partials per position split
+    float* part_ml;             // [B][KH][S][H/KH][2] their (max, sum)
+    float* att;                 // [B][H hd] attention output
+    unsigned long long* tab;    // [B*L][2] KV pointers, then [B] positions (device)
+    unsigned long long* tab_host;   // pinned staging of tab
+    size_t tab_cap;             // bytes of tab / tab_host
+    hipEvent_t tab_ev;          // the last staging copy
+    int tab_pending;
+    // per-layer attention / MoE split of the last decode call (jm_store_profile)
+    int dprof_n;
+    hipEvent_t* dev_marks;      // [2 L + 2]
+};
+
+namespace jm {
+
+// Record a message for jm_last_error() (per calling thread) and return code.
+int fail(int code, const char* fmt, ...);
+int hip_fail(hipError_t e, const char* what);
+
+inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// MoE workspace for batches of up to B tokens.
+int store_reserve(jm_store* s, int B);
+
+// Enqueue the MoE block of one layer on x [B][d] into out [B][d].  With
+// norm_w, x is RMS-normalised with it first (in the router); with resid,
+// out = resid + block (resid may alias out).  stage_marks: record the
+// store's stage events.
+int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const uint16_t* norm_w,
+                float eps, const float* resid, bool stage_marks, hipStream_t st);
+
+// Release the batch-decode workspace, staging and events.
+void decode_free_all(jm_store* s);
+
+}  // namespace jm
+
+#define JM_HIP(expr, what)                                  \
+    do {                                                    \
+        hipError_t _e = (expr);                             \
+        if (_e != hipSuccess) return jm::hip_fail(_e, what); \
+    } while (0)

@@ -1,0 +1,208 @@
+"""Batch decode over all layers on the GPU: the reference's
+``decode_layers_batch`` (src/jouleai/native/decode_kernel.c:1518-1556).
+
+Host-side mirror of the reference's native decoder surface
+(src/jouleai/native/decoder3.py:35-69, 402-415, 453-490):
+
+* ``KernelW`` / ``KVCache`` are the reference's ctypes structures, filled
+  with device pointers of torch tensors;
+* ``rope_tables`` builds the cos/sin tables as ``NativeDecoder._rope_tables``
+  does (rotate-half layout, ``emb = cat(freqs, freqs)``);
+* ``KVCacheSet`` holds the bf16 caches of B sequences x L layers and the
+  ``KVCache[B*L]`` array (entry b*L + l) the call takes;
+* ``HipDecoder.decode_layers_batch(x, positions, kv)`` runs every layer
+  (attention, then the store's MoE block) and returns the final-normed hidden
+  state [B, d].  The lm_head is applied by the caller.
+
+The arithmetic is in libjoule_amd.so; PyTorch holds device memory.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from .moe import HbmExpertStore, MoEShape
+
+_vp = ctypes.c_void_p
+
+
+class KernelW(ctypes.Structure):
+    """KernelW (decode_kernel.c:288-325; decoder3.py:49-69), field for field."""
+    _fields_ = [
+        ("embed", _vp), ("lm_head", _vp), ("final_norm", _vp),
+        ("norm1", _vp), ("norm2", _vp),
+        ("wq", _vp), ("wk", _vp), ("wv", _vp), ("wo", _vp),
+        ("bq", _vp), ("bk", _vp), ("bv", _vp),
+        ("qn", _vp), ("kn", _vp), ("gate_w", _vp),
+        ("w1", _vp), ("w2", _vp), ("w3", _vp),
+        ("wq_i8", _vp), ("wq_i8s", _vp), ("wk_i8", _vp), ("wk_i8s", _vp),
+        ("wv_i8", _vp), ("wv_i8s", _vp), ("wo_i8", _vp), ("wo_i8s", _vp),
+        ("lm_i8", _vp), ("lm_i8s", _vp),
+        ("expert_pk", _vp * 3), ("expert_sc", _vp * 3),
+        ("cos", _vp), ("sin", _vp),
+        ("use_i8", ctypes.c_int),
+    ]
+
+
+class KVCache(ctypes.Structure):
+    """KVCache (decode_kernel.c:328-331): one sequence's k, v of one layer."""
+    _fields_ = [("k", _vp), ("v", _vp)]
+
+
+@dataclass(frozen=True)
+class DecoderShape:
+    """Attention shape of the decoder around an MoE block."""
+
+    n_layers: int
+    moe: MoEShape
+    n_heads: int
+    n_kv: int
+    hd: int = 128
+    eps: float = 1e-6
+    theta: float = 1e6
+    maxT: int = 4096
+    qk_norm_type: int = 1        # 1: per-head RMSNorm on q and k (Qwen3)
+    bias_qkv: bool = False
+    name: str = ""
+
+    @property
+    def d(self) -> int:
+        return self.moe.d
+
+    def kernel_cfg(self) -> _lib.KernelCfg:
+        c = self.moe.kernel_cfg(self.n_layers)
+        c.n_heads, c.n_kv, c.hd = self.n_heads, self.n_kv, self.hd
+        c.eps, c.maxT = float(self.eps), int(self.maxT)
+        c.qk_norm_type, c.bias_qkv = int(self.qk_norm_type), int(bool(self.bias_qkv))
+        return c
+
+
+def qwen3_30b_a3b(n_layers: int = 48, maxT: int = 4096) -> DecoderShape:
+    """Qwen3-30B-A3B: 48 layers, d 2048, GQA 32 / 4 heads of 128, per-head
+    QK-norm, RoPE theta 1e6, eps 1e-6, and the Qwen3 MoE block."""
+    from .moe import QWEN3
+    return DecoderShape(n_layers=n_layers, moe=QWEN3, n_heads=32, n_kv=4, hd=128, eps=1e-6,
+                        theta=1e6, maxT=maxT, qk_norm_type=1, name="qwen3-30b-a3b")
+
+
+def rope_tables(maxT: int, hd: int, theta: float) -> tuple[np.ndarray, np.ndarray]:
+    """cos, sin [maxT, hd] float32 as NativeDecoder._rope_tables
+    (decoder3.py:402-415): inv = 1 / theta^(2i/hd) in float64, angles
+    pos * inv, emb = cat(angles, angles) rounded to float32, then cos/sin."""
+    inv = 1.0 / (theta ** (np.arange(0, hd, 2).astype(np.float64) / hd))
+    pos = np.arange(maxT).astype(np.float64)[:, None]
+    fr = pos * inv[None, :]
+    emb = np.concatenate([fr, fr], axis=-1).astype(np.float32)
+    return np.cos(emb), np.sin(emb)
+
+
+def _bf16_dev(t: torch.Tensor, shape, name: str, device) -> torch.Tensor:
+    if t.dtype != torch.bfloat16 or tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must be bfloat16 {tuple(shape)}, got {t.dtype} {tuple(t.shape)}")
+    return t.to(device).contiguous()
+
+
+class DecoderWeights:
+    """The dense (non-expert) weights of every layer, on the device.
+
+    bf16 tensors: norm1/norm2 [L, d], final_norm [d], wq [L, H*hd, d],
+    wk/wv [L, KH*hd, d], wo [L, d, H*hd], qn/kn [L, hd]; float32 biases
+    bq [L, H*hd], bk/bv [L, KH*hd] when the shape has bias_qkv.  The rope
+    tables are built from the shape.
+    """
+
+    def __init__(self, shape: DecoderShape, device="cuda", **t: torch.Tensor):
+        L, d, H, KH, hd = shape.n_layers, shape.d, shape.n_heads, shape.n_kv, shape.hd
+        self.shape = shape
+        want = {"norm1": (L, d), "norm2": (L, d), "final_norm": (d,), "wq": (L, H * hd, d),
+                "wk": (L, KH * hd, d), "wv": (L, KH * hd, d), "wo": (L, d, H * hd)}
+        if shape.qk_norm_type == 1:
+            want.update(qn=(L, hd), kn=(L, hd))
+        self.t: dict[str, torch.Tensor] = {}
+        for k, shp in want.items():
+            if k not in t:
+                raise ValueError(f"missing weight {k}")
+            self.t[k] = _bf16_dev(t[k], shp, k, device)
+        if shape.bias_qkv:
+            for k, shp in (("bq", (L, H * hd)), ("bk", (L, KH * hd)), ("bv", (L, KH * hd))):
+                self.t[k] = t[k].to(device=device, dtype=torch.float32).contiguous()
+        cos, sin = rope_tables(shape.maxT, hd, shape.theta)
+        self.t["cos"] = torch.from_numpy(cos).to(device)
+        self.t["sin"] = torch.from_numpy(sin).to(device)
+
+    def kernel_w(self) -> KernelW:
+        w = KernelW()
+        for k, v in self.t.items():
+            setattr(w, k, v.data_ptr())
+        return w
+
+
+class KVCacheSet:
+    """bf16 caches for B sequences x L layers: one tensor [B, L, 2, maxT, KH, hd]
+    and the KVCache[B*L] array (entry b*L + l) that points into it."""
+
+    def __init__(self, shape: DecoderShape, B: int, device="cuda", data: torch.Tensor | None = None):
+        L, KH, hd, T = shape.n_layers, shape.n_kv, shape.hd, shape.maxT
+        full = (B, L, 2, T, KH, hd)
+        if data is None:
+            data = torch.zeros(full, dtype=torch.bfloat16, device=device)
+        if data.dtype != torch.bfloat16 or tuple(data.shape) != full or not data.is_contiguous():
+            raise ValueError(f"cache must be a contiguous bfloat16 tensor {full}")
+        self.shape, self.B, self.data = shape, B, data
+        self.table = (KVCache * (B * L))()
+        for b in range(B):
+            for l in range(L):
+                self.table[b * L + l].k = data[b, l, 0].data_ptr()
+                self.table[b * L + l].v = data[b, l, 1].data_ptr()
+
+    def k(self, b: int, l: int) -> torch.Tensor:
+        return self.data[b, l, 0]
+
+    def v(self, b: int, l: int) -> torch.Tensor:
+        return self.data[b, l, 1]
+
+
+class HipDecoder:
+    """decode_layers_batch over an HBM expert store and dense weights."""
+
+    def __init__(self, store: HbmExpertStore, weights: DecoderWeights):
+        shape = weights.shape
+        if store.shape != shape.moe or store.n_layers != shape.n_layers:
+            raise ValueError("store and decoder shapes differ")
+        self.store, self.weights, self.shape = store, weights, shape
+        self._cfg = shape.kernel_cfg()
+        self._w = weights.kernel_w()
+
+    def decode_layers_batch(self, x: torch.Tensor, positions, kv: KVCacheSet,
+                            hidden: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """hidden [B, d] = final RMSNorm of the residual stream after every
+        layer, for tokens x [B, d] (float32) writing cache rows positions[b]."""
+        if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or x.dim() != 2:
+            raise ValueError("x must be a contiguous float32 CUDA tensor [B, d]")
+        B = x.shape[0]
+        if kv.B < B:
+            raise ValueError(f"cache set holds {kv.B} sequences, batch has {B}")
+        pos = np.ascontiguousarray(np.asarray(positions, dtype=np.int32).reshape(-1))
+        if pos.size != B:
+            raise ValueError("one position per token")
+        if hidden is None:
+            hidden = torch.empty_like(x)
+        table = kv.table if kv.B == B else (KVCache * (B * self.shape.n_layers)).from_buffer(kv.table)
+        _lib.check(_lib.lib().jm_decode_layers_batch(
+            self.store._h, ctypes.byref(self._cfg), ctypes.byref(self._w), ctypes.cast(table, _vp),
+            pos.ctypes.data_as(ctypes.c_void_p), _lib.ptr(x), B, None, _lib.ptr(hidden),
+            _lib.stream_handle(stream)), "jm_decode_layers_batch")
+        return hidden
+
+    def split_ms(self) -> dict:
+        """Attention / MoE / total milliseconds of the last call made with
+        profiling on (store.profile(True)); waits for it."""
+        a, m, t = ctypes.c_float(), ctypes.c_float(), ctypes.c_float()
+        _lib.check(_lib.lib().jm_store_decode_ms(self.store._h, ctypes.byref(a), ctypes.byref(m),
+                                                 ctypes.byref(t)), "jm_store_decode_ms")
+        return {"attention": a.value, "moe": m.value, "total": t.value}

@@ -137,3 +137,58 @@ def torch_store(shape: MoEShape, n_layers: int, group: int = 64, seed: int = 100
         if progress:
             progress(l)
     return blob, offsets
+
+
+# ------------------------------------------------------------ decoder
+
+
+def decoder_weights(shape, seed: int = 6000, device: str | torch.device = "cuda",
+                    norm_jitter: float = 0.0) -> dict:
+    """Dense weights of a decoder (joule_amd.decoder.DecoderShape) as bf16
+    tensors on ``device``: projections N(0, 0.02); RMSNorm / QK-norm weights
+    1.0, or 1 + N(0, norm_jitter) when norm_jitter > 0 (tests use it so
+    that a weight applied to the wrong element shows); float32 biases
+    N(0, 0.02) when the shape has bias_qkv.  One torch generator seeded with
+    ``seed`` draws them in a fixed order."""
+    L, d, H, KH, hd = shape.n_layers, shape.d, shape.n_heads, shape.n_kv, shape.hd
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+
+    def normal(*shp, std=0.02):
+        return (torch.randn(shp, generator=gen, device=device, dtype=torch.float32) * std)
+
+    def norm_w(*shp):
+        w = torch.ones(shp, device=device, dtype=torch.float32)
+        if norm_jitter > 0:
+            w += normal(*shp, std=norm_jitter)
+        return w.to(torch.bfloat16)
+
+    t = {
+        "wq": normal(L, H * hd, d).to(torch.bfloat16),
+        "wk": normal(L, KH * hd, d).to(torch.bfloat16),
+        "wv": normal(L, KH * hd, d).to(torch.bfloat16),
+        "wo": normal(L, d, H * hd).to(torch.bfloat16),
+        "norm1": norm_w(L, d),
+        "norm2": norm_w(L, d),
+        "final_norm": norm_w(d),
+    }
+    if shape.qk_norm_type == 1:
+        t["qn"] = norm_w(L, hd)
+        t["kn"] = norm_w(L, hd)
+    if shape.bias_qkv:
+        t["bq"] = normal(L, H * hd)
+        t["bk"] = normal(L, KH * hd)
+        t["bv"] = normal(L, KH * hd)
+    return t
+
+
+def fill_kv(data: torch.Tensor, seed: int = 5000) -> torch.Tensor:
+    """Fill a cache tensor [B, L, 2, T, KH, hd] (bf16) with N(0, 1): one
+    generator per layer, seeded seed + layer, drawing [B, 2, T, KH, hd]."""
+    B, L = data.shape[0], data.shape[1]
+    for l in range(L):
+        gen = torch.Generator(device=data.device)
+        gen.manual_seed(seed + l)
+        data[:, l].copy_(torch.randn(data[:, l].shape, generator=gen, device=data.device,
+                                     dtype=torch.float32).to(torch.bfloat16))
+    return data

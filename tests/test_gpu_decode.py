@@ -1,0 +1,145 @@
+"""GPU parity of the batch decode (jm_decode_layers_batch) with the CPU
+restatement of decode_layers_batch (oracle/decoder.py, decode_kernel.c:1518-1556).
+
+Each case builds a small model on the GPU (Q4 expert store, bf16 attention
+weights with jittered norm weights, a bf16 KV cache filled with N(0, 1)),
+runs the decode for a batch with ragged positions, and checks:
+  * the final hidden state within 1e-3 max relative error per token;
+  * the cache rows written at the positions against the oracle's (bf16
+    values; at most one bf16 unit apart, nearly all identical);
+  * a second step at the next positions, which reads the rows the first
+    step appended.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from joule_amd import _lib
+from joule_amd.decoder import DecoderShape, DecoderWeights, HipDecoder, KVCacheSet, qwen3_30b_a3b
+from joule_amd.moe import HbmExpertStore, MoEShape
+from joule_amd.synth import activations, decoder_weights, fill_kv, router_weights, torch_store
+from oracle import decoder as D
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _model(shape: DecoderShape, group: int, B: int):
+    L, moe = shape.n_layers, shape.moe
+    blob, offsets = torch_store(moe, L, group)
+    store = HbmExpertStore(moe, L, blob, offsets, group)
+    gw = np.stack([router_weights(moe, l) for l in range(L)])
+    store.set_router(torch.from_numpy(gw).cuda())
+    t = decoder_weights(shape, norm_jitter=0.1)
+    weights = DecoderWeights(shape, **t)
+    kv = KVCacheSet(shape, B)
+    fill_kv(kv.data)
+    torch.cuda.synchronize()
+    # the oracle's copies
+    w = {k: v.float().cpu().numpy() for k, v in weights.t.items()}
+    blob_h = blob.cpu().numpy()
+    moe_o = [O.OracleMoE(moe.d, moe.m, moe.E, moe.topk, moe.renorm, group, gw[l], blob_h,
+                         offsets[:, l * moe.E:(l + 1) * moe.E]) for l in range(L)]
+    oracle = D.OracleDecoder(L, moe.d, shape.n_heads, shape.n_kv, shape.hd, shape.eps, shape.qk_norm_type,
+                             shape.bias_qkv, w, moe_o)
+    return HipDecoder(store, weights), oracle, kv
+
+
+def _kv_host(kv: KVCacheSet, B: int, L: int):
+    d = kv.data.float().cpu().numpy()
+    return [[(d[b, l, 0].copy(), d[b, l, 1].copy()) for l in range(L)] for b in range(B)]
+
+
+def _check_step(dec, oracle, kv, kv_h, x, positions, label):
+    B, L = x.shape[0], dec.shape.n_layers
+    print(f"[decode] {label} B={B} L={L} positions={list(positions)}", flush=True)
+    hid = dec.decode_layers_batch(torch.from_numpy(x).cuda(), positions, kv)
+    torch.cuda.synchronize()
+    got = hid.cpu().numpy()
+    want = oracle.decode_layers_batch(x, positions, kv_h)
+    rel = np.abs(got - want).max(axis=1) / np.abs(want).max(axis=1)
+    assert np.isfinite(got).all()
+    assert rel.max() <= TOL, f"{label}: per-token max rel error {rel}"
+    # cache rows appended at the positions
+    data = kv.data
+    n_same = n_all = 0
+    for b, p in enumerate(positions):
+        for l in range(L):
+            for j in (0, 1):
+                g = data[b, l, j, p].float().cpu().numpy()
+                r = kv_h[b][l][j][p]
+                # one bf16 unit, plus the upstream float32 differences, which
+                # scale with the row (not with elements near zero)
+                lim = np.abs(r) * 2.0 ** -7 + 1e-4 * np.abs(r).max()
+                bad = int((np.abs(g - r) > lim).sum())
+                assert bad == 0, f"{label}: cache row b={b} l={l} {'kv'[j]}: {bad} values off by more than a bf16 unit"
+                n_same += int((g == r).sum())
+                n_all += g.size
+    assert n_same >= 0.98 * n_all, f"{label}: {n_all - n_same} of {n_all} cache values differ"
+    return rel.max()
+
+
+CASES = {
+    # Qwen3-30B-A3B layers (GQA 32/4, per-head QK-norm), ragged positions
+    # across split boundaries (128) and up to 2048
+    "qwen3_l2_b8": (qwen3_30b_a3b(n_layers=2, maxT=2176), 64, [0, 1, 127, 128, 129, 700, 2047, 2048]),
+    # no GQA, no QK-norm, QKV bias, 16 experts top-4 without renormalisation
+    "mha_bias_l2_b3": (DecoderShape(n_layers=2, moe=MoEShape(d=1024, m=256, E=16, topk=4, renorm=False),
+                                    n_heads=8, n_kv=8, maxT=300, qk_norm_type=0, bias_qkv=True), 64, [5, 0, 299]),
+    # 4 query heads per KV head, group 32
+    "gqa4_l1_b2": (DecoderShape(n_layers=1, moe=MoEShape(d=1024, m=512, E=32, topk=8, renorm=True),
+                                n_heads=8, n_kv=2, maxT=520), 32, [511, 256]),
+    # 2 query heads per KV head, d 2048
+    "gqa2_l1_b5": (DecoderShape(n_layers=1, moe=MoEShape(d=2048, m=768, E=64, topk=4, renorm=True),
+                                n_heads=16, n_kv=8, maxT=260), 64, [3, 130, 255, 64, 200]),
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_decode_layers_batch_matches_oracle(case):
+    shape, group, positions = CASES[case]
+    B = len(positions)
+    dec, oracle, kv = _model(shape, group, B)
+    kv_h = _kv_host(kv, B, shape.n_layers)
+    x = activations(B, shape.d)
+    _check_step(dec, oracle, kv, kv_h, x, positions, case)
+    # next step: one position further, reading the rows just appended
+    nxt = [min(p + 1, shape.maxT - 1) for p in positions]
+    x2 = activations(B, shape.d, seed=3100)
+    _check_step(dec, oracle, kv, kv_h, x2, nxt, case + " step 2")
+    dec.store.close()
+
+
+def test_decode_split_profile_and_errors():
+    shape = DecoderShape(n_layers=1, moe=MoEShape(d=1024, m=256, E=16, topk=4, renorm=True),
+                         n_heads=8, n_kv=2, maxT=256)
+    dec, _, kv = _model(shape, 64, 2)
+    x = torch.from_numpy(activations(2, shape.d)).cuda()
+    L = _lib.lib()
+    st = _lib.stream_handle()
+    cfg, w = dec._cfg, dec._w
+    pos = np.array([3, 256], np.int32)            # 256 >= maxT
+    rc = L.jm_decode_layers_batch(dec.store._h, ctypes.byref(cfg), ctypes.byref(w), ctypes.cast(kv.table, ctypes.c_void_p),
+                                  pos.ctypes.data_as(ctypes.c_void_p), _lib.ptr(x), 2, None, _lib.ptr(x), st)
+    assert rc == -1 and b"positions" in L.jm_last_error()
+    pos = np.array([3, 4], np.int32)
+    rc = L.jm_decode_layers_batch(dec.store._h, ctypes.byref(cfg), ctypes.byref(w), ctypes.cast(kv.table, ctypes.c_void_p),
+                                  pos.ctypes.data_as(ctypes.c_void_p), _lib.ptr(x), 2, _lib.ptr(x), _lib.ptr(x), st)
+    assert rc == -1 and b"lm_head" in L.jm_last_error()
+    bad = shape.kernel_cfg()
+    bad.hd = 64
+    rc = L.jm_decode_layers_batch(dec.store._h, ctypes.byref(bad), ctypes.byref(w), ctypes.cast(kv.table, ctypes.c_void_p),
+                                  pos.ctypes.data_as(ctypes.c_void_p), _lib.ptr(x), 2, None, _lib.ptr(x), st)
+    assert rc == -2
+    # profiled call: attention + MoE parts within the whole
+    dec.store.profile(True)
+    dec.decode_layers_batch(x, [3, 4], kv)
+    ms = dec.split_ms()
+    assert ms["attention"] > 0 and ms["moe"] > 0 and ms["attention"] + ms["moe"] <= ms["total"] * 1.001
+    dec.store.profile(False)
+    dec.store.close()
