@@ -17,9 +17,12 @@ Reported (one JSON line):
   block        the same ratio for the whole block (all algorithmic bytes:
                routed experts, router table, x in/out) over ms_per_step
   stages       average milliseconds of each kernel
-  sweep        the same measurement at B=1 and B=32 (Qwen3), OLMoE B=1/8, and
-               the prefill-style Qwen3 block: 512 tokens with Zipf(1.1)-biased
-               routing, whose large segments take the MFMA branch
+  sweep        the same measurement at B=1 and B=32 (Qwen3), OLMoE B=1/8, the
+               prefill-style Qwen3 block: 512 tokens with Zipf(1.1)-biased
+               routing, whose large segments take the MFMA branch, and the
+               full 48-layer Qwen3-30B-A3B decode step at B=8 (attention over
+               2049 cached positions + the MoE block per layer), with the MoE
+               share of the step isolated
   cpu_baseline the C restatement of the reference block (oracle/) on this
                host's cores, 8 workers + caller as the reference runs B>1,
                on a bounded sample of the same workload
@@ -187,6 +190,88 @@ def cpu_baseline(store, gw, x_np, n_layers, budget_s):
     }
 
 
+def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
+    """The full Qwen3-30B-A3B-shaped decode step: n_layers x (attention + MoE
+    block) at batch B, every token at cache position `position` (attention
+    over position + 1 rows of a bf16 cache filled with N(0, 1)).  Returns
+    tokens/s, the attention / MoE split of a profiled step, and the
+    algorithmic HBM bytes of a step (routed experts counted per layer)."""
+    import numpy as np
+    import torch
+
+    from joule_amd.decoder import DecoderWeights, HipDecoder, KVCacheSet, qwen3_30b_a3b
+    from joule_amd.moe import QWEN3
+    from joule_amd.q4_store import record_sizes
+    from joule_amd.synth import activations, decoder_weights, fill_kv
+
+    shape = qwen3_30b_a3b(n_layers, maxT)
+    log(f"decode: building {n_layers} Qwen3-30B-A3B layers (store, attention weights, KV cache)")
+    store, _ = build_layers(QWEN3, n_layers, group, seed=1000)
+    weights = DecoderWeights(shape, **decoder_weights(shape))
+    kv = KVCacheSet(shape, B)
+    fill_kv(kv.data)
+    dec = HipDecoder(store, weights)
+    x = torch.from_numpy(activations(B, shape.d)).cuda()
+    hid = torch.empty_like(x)
+    pos = [position] * B
+    store.reserve(B)
+    for _ in range(warmup):
+        dec.decode_layers_batch(x, pos, kv, hid)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(steps):
+        dec.decode_layers_batch(x, pos, kv, hid)
+    e1.record(st)
+    host_ms = (time.perf_counter() - t0) * 1e3 / steps      # enqueue time per step
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    # attention / MoE split (events at every layer's boundaries)
+    store.profile(True)
+    split = {"attention": 0.0, "moe": 0.0, "total": 0.0}
+    for _ in range(3):
+        dec.decode_layers_batch(x, pos, kv, hid)
+        for k, v in dec.split_ms().items():
+            split[k] += v / 3
+    store.profile(False)
+    # routed experts per layer, from a traced step
+    k = QWEN3.topk
+    tr = torch.empty((n_layers, B, k), dtype=torch.int32, device="cuda")
+    dec.trace_topk(tr)
+    dec.decode_layers_batch(x, pos, kv, hid)
+    dec.trace_topk(None)
+    t = tr.cpu().numpy()
+    U = [len(np.unique(t[l])) for l in range(n_layers)]
+    eb = sum(sum(record_sizes(r, c, group)) for r, c in ((QWEN3.m, QWEN3.d), (QWEN3.m, QWEN3.d), (QWEN3.d, QWEN3.m)))
+    H, KH, hd, d = shape.n_heads, shape.n_kv, shape.hd, shape.d
+    T = position + 1
+    moe_bytes = sum(U) * eb + n_layers * (QWEN3.E * d * store.router_bytes_per_weight() + 2 * B * d * 4)
+    attn_w = n_layers * 2 * (H * hd * d + 2 * KH * hd * d + d * H * hd)
+    kv_bytes = n_layers * B * T * KH * hd * 2 * 2
+    total = moe_bytes + attn_w + kv_bytes
+    ok = bool(torch.isfinite(hid).all().item())
+    res = {
+        "tok_per_s": B / (ms * 1e-3), "ms_per_step": ms, "host_enqueue_ms_per_step": host_ms,
+        "layers": n_layers, "batch": B, "position": position,
+        "attention_ms_profiled": split["attention"], "moe_ms_profiled": split["moe"],
+        "step_ms_profiled": split["total"],
+        "moe_share": split["moe"] / split["total"] if split["total"] > 0 else None,
+        "experts_routed_avg": sum(U) / len(U),
+        "bytes_alg": total, "bytes_moe": moe_bytes, "bytes_attn_weights": attn_w, "bytes_kv": kv_bytes,
+        "GBs": total / (ms * 1e-3) / 1e9, "hbm_frac": total / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "hidden_finite": ok,
+    }
+    log(f"decode {n_layers} layers B={B}: {res['tok_per_s']:.0f} tok/s, {ms:.3f} ms/step "
+        f"(host enqueue {host_ms:.3f} ms), attention {split['attention']:.3f} ms, MoE {split['moe']:.3f} ms, "
+        f"{res['GBs']:.0f} GB/s over {total / 1e9:.2f} GB")
+    store.close()
+    del dec, weights, kv, store
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,6 +282,8 @@ def main() -> int:
     ap.add_argument("--group", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the 48-layer decode step (B=--batch, --steps timed steps); prints its JSON")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after timing, run 8 torch copies of this many MiB (a known-size kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -218,6 +305,10 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     torch.cuda.set_device(0)
+    if args.decode_only:
+        r = decode_step(args.batch, args.steps, args.warmup, args.group)
+        print(json.dumps({"decode_step": r}), flush=True)
+        return 0
     shape, G, B, NL = QWEN3, args.group, args.batch, args.layers
     log(f"building {NL} Qwen3-shaped layers (G={G}) on the GPU")
     store, gw = build_layers(shape, NL, G, seed=1000)
@@ -300,6 +391,11 @@ def main() -> int:
             sweep[f"olmoe_B{b}"] = {k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac",
                                                       "gateup_GBs", "experts_routed_avg")}
             log(f"sweep olmoe B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s")
+
+    if not args.no_sweep:
+        del ostore
+        torch.cuda.empty_cache()
+        sweep["qwen3_decode48_B8"] = decode_step(8, max(args.steps // 20, 10), 3, G)
 
     gu_ms = stages["gateup"]
     traffic = None

@@ -239,6 +239,12 @@ int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* cfg, const jm_kerne
                            const int32_t* positions, const float* xin, int B, float* logits, float* hidden,
                            void* stream);
 
+/* With buf set (device int32, `bytes` long), each later
+ * jm_decode_layers_batch also copies every layer's selected experts into
+ * buf[l][B][topk], for accounting and tests; NULL turns it off.  No
+ * counterpart in the reference. */
+int jm_store_trace_topk(jm_store* s, int32_t* buf, uint64_t bytes);
+
 /* Milliseconds of the last profiled jm_decode_layers_batch call: its
  * attention parts (norm1 to the o_proj residual, summed over layers), its
  * MoE blocks (norm2 to the residual) and the whole call (waits for it). */

@@ -129,8 +129,8 @@ int check_store(const jm_store* s) {
 
 namespace jm {
 
-int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const uint16_t* norm_w,
-                float eps, const float* resid, bool stage_marks, hipStream_t st) {
+int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const FfnIo& io,
+                bool stage_marks, hipStream_t st) {
     if ((long long)B * s->topk > JM_MAX_SLOTS) return fail(JM_ERR_SHAPE, "B * topk must be <= %d", JM_MAX_SLOTS);
     if (B * s->topk > JM_DEC_SLOTS && (size_t)jm::dispatch_lds_ints(B * s->topk, s->E) * 4 > (size_t)s->lds_max)
         return fail(JM_ERR_SHAPE, "B * topk = %d slots over %d experts exceed the dispatch's LDS", B * s->topk, s->E);
@@ -143,7 +143,8 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     jm::RouteArgs r;
     r.wt = (const char*)s->wt + (size_t)layer * jm::router_experts_padded(E) * d * (s->wt_bf16 ? 2 : 4);
     r.wt_bf16 = s->wt_bf16;
-    r.x = x; r.norm_w = norm_w; r.eps = eps; r.B = B; r.E = E; r.d = d; r.topk = k; r.renorm = s->renorm; r.group = G;
+    r.x = x; r.xpart = io.xpart; r.nxpart = io.nxpart; r.xmid = io.xmid;
+    r.norm_w = io.norm_w; r.eps = io.eps; r.B = B; r.E = E; r.d = d; r.topk = k; r.renorm = s->renorm; r.group = G;
     r.logits = s->logits; r.xdig = s->xdig; r.xscale = s->xscale; r.top = s->top; r.tw = s->tw;
     r.seg_off = s->seg_off; r.seg_slot = s->seg_slot; r.active = s->active; r.n_active = s->n_active;
     r.first_slot = s->first_slot; r.comb = s->comb; r.rank_scratch = s->rank;
@@ -156,7 +157,7 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     a.top = s->top; a.nslot = nslot; a.B = B;
     a.d = d; a.m = s->m; a.topk = k; a.group = G;
     a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
-    a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y; a.out = out; a.resid = resid;
+    a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y; a.out = out; a.resid = io.resid;
     a.dense_min = jm::mfma_shape_ok(d, s->m) ? s->dense_min : 0x7FFFFFFF;
     r.dense_min = a.dense_min;
     a.tiles = s->tiles; a.n_tiles = s->n_tiles;
@@ -181,7 +182,7 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     } else {
         JM_HIP(jm::launch_down(a, umax, st), "down launch");
         JM_HIP(jm::launch_down_mfma(a, max_tiles, st), "down MFMA launch");
-        JM_HIP(jm::launch_combine(s->y, s->comb, B, k, d, resid, out, st), "combine launch");
+        JM_HIP(jm::launch_combine(s->y, s->comb, B, k, d, io.resid, out, st), "combine launch");
     }
     JM_MARK(3);
 #undef JM_MARK
@@ -374,7 +375,7 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     if (!x || !out) return fail(JM_ERR_ARG, "x and out must be non-NULL");
     if (!aligned(x, 16) || !aligned(out, 16)) return fail(JM_ERR_ARG, "x and out must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
-    if (int rc = jm::ffn_enqueue(s, layer, x, B, out, nullptr, 0.0f, nullptr, true, st)) return rc;
+    if (int rc = jm::ffn_enqueue(s, layer, x, B, out, jm::FfnIo{}, true, st)) return rc;
     const int k = s->topk;
     if (topk_idx) JM_HIP(hipMemcpyAsync(topk_idx, s->top, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k");
     if (topk_w) JM_HIP(hipMemcpyAsync(topk_w, s->tw, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k weights");

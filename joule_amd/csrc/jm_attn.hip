@@ -5,18 +5,24 @@
 // (decode_kernel.c:1120-1234, 1518-1556) step for step, regrouped into few
 // launches:
 //
-//   k_gemv_bf16   norm1 + Wq/Wk/Wv (+ bias)  -> qkv        (:224-230, :1126-1145)
-//   k_attn_part   per-head QK-norm, RoPE, KV append, scores, softmax and
-//                 P.V over one 128-position split of the cache  (:1165-1222)
+//   k_gemv_part   Wq/Wk/Wv . (h * norm1 weight), per 512-column slice
+//                                                             (:224-230, :1126-1145)
+//   k_qkv_fin     the slices summed, RMSNorm row scale, bias, per-head
+//                 QK-norm, RoPE; q out, k and v appended to the cache
+//                                                               (:1146-1199)
+//   k_attn_part   scores, softmax and P.V over one 128-position split of
+//                 the cache                                     (:1200-1222)
 //   k_attn_comb   the splits merged per head                   (flash-decoding merge)
-//   k_gemv_bf16   Wo . att + residual -> h                     (:1225-1232, :1546-1547)
+//   k_gemv_part   Wo . att per slice; the MoE router sums the slices into
+//                 the residual                                  (:1225-1232, :1546-1547)
 //   k_rms_rows    the final RMSNorm                            (:1556)
 //
-// The projections are HBM-bound GEMVs: every 16-byte weight load of a lane
-// serves all the batch's tokens, whose rows sit in LDS.  Attention streams
-// the cache once: one block per (position split, KV head, token) reads 128
-// positions of K and V (256 bytes each per head) and serves every query head
-// of that KV head.
+// The projections are HBM-bound GEMVs split over 512-column slices: every
+// 16-byte weight load of a lane serves all the batch's tokens, whose slice
+// (16 KiB at 8 tokens) sits in LDS, and the consumer adds the slices.
+// Attention streams the cache once: one block per (position split, KV head,
+// token) reads 128 positions of K and V (256 bytes each per head) and serves
+// every query head of that KV head.
 #include "jm_device.h"
 #include "jm_kernels.h"
 
@@ -24,122 +30,81 @@ namespace jm {
 
 // ------------------------------------------------------------------ GEMV
 
-// out[b][row] = (resid[b][row] +) (bias[row] +) W[row] . xn[b], rows of the
-// stacked matrices w[0..2]; xn = x, or RMSNorm(x) * norm_w.  Block: 4 waves
-// of R rows each; every lane holds 8 consecutive columns of each of its rows
-// per 512-column pass, all passes' weights requested up front.  Tokens in
-// groups of BT (grid.y); their rows staged in LDS in chunks of KC columns.
-template <int BT, int NP, int R>
-__global__ void __launch_bounds__(256)
-k_gemv_bf16(GemvArgs a) {
-    constexpr int K = NP * 512;
-    constexpr int KC0 = 16384 / BT;                  // 64 KiB of fp32 rows
-    constexpr int KC = K < KC0 ? K : KC0 / 512 * 512;
-    constexpr int PPC = KC / 512;                    // passes per chunk
-    static_assert(KC >= 512 && K % KC == 0, "chunking");
-    __shared__ __align__(16) float xs[BT * KC];
-    __shared__ float invl[BT];
+// Partial products of 512-column slices: part[s][b][row] = sum over columns
+// k of slice s of W[row][k] * x[b][k] (* norm_w[k]), rows of the stacked
+// matrices w[0..2].  Block (row group, slice, token group): 8 waves of 8 rows,
+// each lane holding 8 consecutive columns of its rows; the slice of every
+// token of the group staged in LDS (16 KiB at 8 tokens).  The consumer sums
+// the slices (and applies the RMSNorm row scale), so that each block moves
+// few activation bytes and a projection spreads over hundreds of blocks.
+template <int BT>
+__global__ void __launch_bounds__(512)
+k_gemv_part(GemvArgs a) {
+    constexpr int R = 8;
+    __shared__ __align__(16) float xs[BT * 512];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int tb0 = blockIdx.y * BT;
-    const int row0 = (blockIdx.x * 4 + w) * R;
+    const int slice = blockIdx.y, tb0 = blockIdx.z * BT;
+    const int row0 = blockIdx.x * 64 + w * R;
+    const int k0 = slice * 512;
 
-    // this wave's rows: every pass's 8 columns, requested first
-    uint4 wq[NP][R];
+    // this wave's rows, 16 bytes per lane each, requested first
+    uint4 wq[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         int row = row0 + r;
         row = row < a.N ? row : a.N - 1;
         const uint16_t* wr;
-        if (row < a.rows[0]) wr = a.w[0] + (size_t)row * K;
-        else if (row < a.rows[0] + a.rows[1]) wr = a.w[1] + (size_t)(row - a.rows[0]) * K;
-        else wr = a.w[2] + (size_t)(row - a.rows[0] - a.rows[1]) * K;
-        const uint4* p = (const uint4*)wr + lane;
-#pragma unroll
-        for (int pg = 0; pg < NP; pg++) wq[pg][r] = p[pg * 64];
+        if (row < a.rows[0]) wr = a.w[0] + (size_t)row * a.K;
+        else if (row < a.rows[0] + a.rows[1]) wr = a.w[1] + (size_t)(row - a.rows[0]) * a.K;
+        else wr = a.w[2] + (size_t)(row - a.rows[0] - a.rows[1]) * a.K;
+        wq[r] = *((const uint4*)(wr + k0) + lane);
     }
-    // RMSNorm scales of the group's tokens (one wave per token)
-    if (a.norm_w) {
-        for (int b = w; b < BT; b += 4) {
-            float ss = 0.0f;
-            if (tb0 + b < a.B) {
-                const float4* xr = (const float4*)(a.x + (size_t)(tb0 + b) * K);
+    // the tokens' slice (times the norm weight)
 #pragma unroll
-                for (int i = 0; i < K / 256; i++) {
-                    const float4 v = xr[lane + 64 * i];
-                    ss = __builtin_fmaf(v.x, v.x, ss);
-                    ss = __builtin_fmaf(v.y, v.y, ss);
-                    ss = __builtin_fmaf(v.z, v.z, ss);
-                    ss = __builtin_fmaf(v.w, v.w, ss);
-                }
+    for (int i = tid; i < BT * 128; i += 512) {
+        const int b = i >> 7, c = 4 * (i & 127);
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (tb0 + b < a.B) {
+            v = *(const float4*)(a.x + (size_t)(tb0 + b) * a.K + k0 + c);
+            if (a.norm_w) {
+                const uint2 nw = *(const uint2*)(a.norm_w + k0 + c);
+                v.x = __fmul_rn(v.x, bf16_bits_to_f32(nw.x & 0xFFFFu));
+                v.y = __fmul_rn(v.y, bf16_bits_to_f32(nw.x >> 16));
+                v.z = __fmul_rn(v.z, bf16_bits_to_f32(nw.y & 0xFFFFu));
+                v.w = __fmul_rn(v.w, bf16_bits_to_f32(nw.y >> 16));
             }
-            ss = seg_sum<64>(ss);
-            if (lane == 0) invl[b] = rms_inv(ss, K, a.eps);
+        }
+        *(float4*)(xs + b * 512 + c) = v;
+    }
+    __syncthreads();
+
+    float wf[R][8];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t ww[4] = {wq[r].x, wq[r].y, wq[r].z, wq[r].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            wf[r][2 * i] = __uint_as_float(ww[i] << 16);
+            wf[r][2 * i + 1] = __uint_as_float(ww[i] & 0xFFFF0000u);
         }
     }
     float acc[R][BT];
 #pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int b = 0; b < BT; b++) acc[r][b] = 0.0f;
-
-#pragma unroll
-    for (int pg = 0; pg < NP; pg++) {
-        if (pg % PPC == 0) {
-            // stage columns [kc0, kc0 + KC) of the group's tokens
-            const int kc0 = pg * 512;
-            __syncthreads();
-#pragma unroll 4
-            for (int i = tid; i < BT * KC / 4; i += 256) {
-                const int b = i / (KC / 4), c = 4 * (i % (KC / 4));
-                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if (tb0 + b < a.B) {
-                    v = *(const float4*)(a.x + (size_t)(tb0 + b) * K + kc0 + c);
-                    if (a.norm_w) {
-                        const float inv = invl[b];
-                        const uint2 nw = *(const uint2*)(a.norm_w + kc0 + c);
-                        v.x = __fmul_rn(__fmul_rn(v.x, inv), bf16_bits_to_f32(nw.x & 0xFFFFu));
-                        v.y = __fmul_rn(__fmul_rn(v.y, inv), bf16_bits_to_f32(nw.x >> 16));
-                        v.z = __fmul_rn(__fmul_rn(v.z, inv), bf16_bits_to_f32(nw.y & 0xFFFFu));
-                        v.w = __fmul_rn(__fmul_rn(v.w, inv), bf16_bits_to_f32(nw.y >> 16));
-                    }
-                }
-                *(float4*)(xs + b * KC + c) = v;
-            }
-            __syncthreads();
-        }
-        const int kl = (pg % PPC) * 512 + lane * 8;
-        // this pass's weights as floats, once for all tokens; the empty asm
-        // keeps the conversion (and the wait for the load) at this pass
-        float wf[R][8];
+    for (int b = 0; b < BT; b++) {
+        const float4 x0 = *(const float4*)(xs + b * 512 + lane * 8);
+        const float4 x1 = *(const float4*)(xs + b * 512 + lane * 8 + 4);
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            uint32_t ww[4] = {wq[pg][r].x, wq[pg][r].y, wq[pg][r].z, wq[pg][r].w};
-            __asm__ volatile("" : "+v"(ww[0]), "+v"(ww[1]), "+v"(ww[2]), "+v"(ww[3]));
+            float s = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                wf[r][2 * i] = __uint_as_float(ww[i] << 16);
-                wf[r][2 * i + 1] = __uint_as_float(ww[i] & 0xFFFF0000u);
-            }
+            for (int i = 0; i < 8; i++) s = __builtin_fmaf(wf[r][i], xv[i], s);
+            acc[r][b] = s;
         }
+        // one token at a time: the empty asm takes the sums and fences
+        // memory, so later tokens' LDS reads are not hoisted into registers
 #pragma unroll
-        for (int b = 0; b < BT; b++) {
-            const float4 x0 = *(const float4*)(xs + b * KC + kl);
-            const float4 x1 = *(const float4*)(xs + b * KC + kl + 4);
-            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float s = acc[r][b];
-#pragma unroll
-                for (int i = 0; i < 8; i++) s = __builtin_fmaf(wf[r][i], xv[i], s);
-                acc[r][b] = s;
-            }
-            // one token's columns at a time: the empty asm takes the running
-            // sums and fences memory, so neither are later tokens' LDS reads
-            // hoisted nor this token's multiply-adds sunk (either would hold
-            // many tokens' columns in registers)
-#pragma unroll
-            for (int r = 0; r < R; r++) __asm__ volatile("" : "+v"(acc[r][b]) : : "memory");
-        }
+        for (int r = 0; r < R; r++) __asm__ volatile("" : "+v"(acc[r][b]) : : "memory");
     }
     // row totals: groups of up to 16 partial sums transposed across the wave
     constexpr int NV = R * BT;
@@ -156,40 +121,23 @@ k_gemv_bf16(GemvArgs a) {
             const int vi = g0 + lane / LPV;
             const int r = vi / BT, b = vi % BT;
             const int row = row0 + r;
-            if (row < a.N && tb0 + b < a.B) {
-                float y = tot;
-                if (row < a.rows[0]) { if (a.bias[0]) y = __fadd_rn(y, a.bias[0][row]); }
-                else if (row < a.rows[0] + a.rows[1]) { if (a.bias[1]) y = __fadd_rn(y, a.bias[1][row - a.rows[0]]); }
-                else if (a.bias[2]) y = __fadd_rn(y, a.bias[2][row - a.rows[0] - a.rows[1]]);
-                const size_t o = (size_t)(tb0 + b) * a.N + row;
-                if (a.resid) y = __fadd_rn(a.resid[o], y);
-                a.out[o] = y;
-            }
+            if (row < a.N && tb0 + b < a.B) a.part[((size_t)slice * a.B + tb0 + b) * a.N + row] = tot;
         }
     }
 }
 
-bool gemv_shape_ok(int K) { return K == 1024 || K == 2048 || K == 4096; }
+bool gemv_shape_ok(int K) { return K > 0 && K % 512 == 0 && K <= 8192; }
 
-hipError_t launch_gemv_bf16(const GemvArgs& a, int rows_per_wave, hipStream_t st) {
+hipError_t launch_gemv_part(const GemvArgs& a, hipStream_t st) {
     if (a.B == 0 || a.N == 0) return hipSuccess;
-    const int BT = a.B <= 1 ? 1 : a.B <= 2 ? 2 : a.B <= 4 ? 4 : a.B <= 8 ? 8 : 16;
-    const int R = rows_per_wave == 2 ? 2 : 4;
-    const dim3 grid((unsigned)((a.N + 4 * R - 1) / (4 * R)), (unsigned)((a.B + BT - 1) / BT));
-#define JM_GV(BB, NN, RR) hipLaunchKernelGGL((k_gemv_bf16<BB, NN, RR>), grid, dim3(256), 0, st, a)
-#define JM_GVR(BB, NN) if (R == 2) JM_GV(BB, NN, 2); else JM_GV(BB, NN, 4)
-#define JM_GVN(BB) switch (a.K) { case 1024: JM_GVR(BB, 2); break; case 2048: JM_GVR(BB, 4); break; \
-        case 4096: JM_GVR(BB, 8); break; default: return hipErrorInvalidValue; }
+    const int BT = a.B <= 1 ? 1 : a.B <= 2 ? 2 : a.B <= 4 ? 4 : 8;
+    const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)(a.K / 512), (unsigned)((a.B + BT - 1) / BT));
     switch (BT) {
-        case 1: JM_GVN(1) break;
-        case 2: JM_GVN(2) break;
-        case 4: JM_GVN(4) break;
-        case 8: JM_GVN(8) break;
-        default: JM_GVN(16) break;
+        case 1: hipLaunchKernelGGL(k_gemv_part<1>, grid, dim3(512), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(k_gemv_part<2>, grid, dim3(512), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(k_gemv_part<4>, grid, dim3(512), 0, st, a); break;
+        default: hipLaunchKernelGGL(k_gemv_part<8>, grid, dim3(512), 0, st, a); break;
     }
-#undef JM_GVN
-#undef JM_GVR
-#undef JM_GV
     return hipGetLastError();
 }
 
@@ -213,16 +161,83 @@ __device__ __forceinline__ float head_reduce16(float (&v)[QPK]) {
 
 __device__ __forceinline__ float bf16_round(float f) { return __uint_as_float(f32_to_bf16_rne(f) << 16); }
 
+// The projections of one head of one token finished: the column slices
+// summed, times the RMSNorm row scale of h, plus the bias (:1126-1145); for
+// q and k heads the per-head RMSNorm (:1174-1189) and RoPE rotate-half at
+// the token's position (:1190-1194, :259-266).  q heads go to qout; k and v
+// heads are appended to the bf16 cache at the position (:1195-1199).
+// Block (head in q.., k.., v.., token), one thread per dimension.
+__global__ void __launch_bounds__(128)
+k_qkv_fin(AttnArgs a) {
+    constexpr int HD = 128;
+    __shared__ float vals[HD];
+    __shared__ float red[2];
+    const int hh = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    const int pos = a.pos[b];
+    // RMSNorm row scale of the layer input (the projections were taken of
+    // h * norm weight)
+    const float* hb = a.h + (size_t)b * a.d;
+    float ss = 0.0f;
+    for (int i = t; i < a.d / 4; i += HD) {
+        const float4 v = *(const float4*)(hb + 4 * i);
+        ss = __builtin_fmaf(v.x, v.x, ss);
+        ss = __builtin_fmaf(v.y, v.y, ss);
+        ss = __builtin_fmaf(v.z, v.z, ss);
+        ss = __builtin_fmaf(v.w, v.w, ss);
+    }
+    ss = seg_sum<64>(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const float inv = rms_inv(__fadd_rn(red[0], red[1]), a.d, a.eps);
+    const int row = hh * HD + t;
+    float v = a.qkv[(size_t)b * a.nqkv + row];
+    for (int sl = 1; sl < a.nslice; sl++) v = __fadd_rn(v, a.qkv[((size_t)sl * a.B + b) * a.nqkv + row]);
+    v = __fmul_rn(v, inv);
+    const bool isq = hh < a.H, isk = !isq && hh < a.H + a.KH;
+    const float* bias = isq ? a.bq : isk ? a.bk : a.bv;
+    const int brow = isq ? row : isk ? row - a.H * HD : row - (a.H + a.KH) * HD;
+    if (bias) v = __fadd_rn(v, bias[brow]);
+    const unsigned long long* kvp = a.kv + ((size_t)b * a.L + a.layer) * 2;
+    if (!isq && !isk) {                  // v head: to the cache
+        uint16_t* vc = (uint16_t*)kvp[1];
+        vc[((size_t)pos * a.KH + (hh - a.H - a.KH)) * HD + t] = (uint16_t)f32_to_bf16_rne(v);
+        return;
+    }
+    const uint16_t* nw = isq ? a.qn : a.kn;
+    if (nw) {
+        float sq = seg_sum<64>(__fmul_rn(v, v));
+        __syncthreads();                 // red[] reused
+        if ((t & 63) == 0) red[t >> 6] = sq;
+        __syncthreads();
+        const float hinv = rms_inv(__fadd_rn(red[0], red[1]), HD, a.eps);
+        v = __fmul_rn(__fmul_rn(v, hinv), bf16_bits_to_f32(nw[t]));
+    }
+    // rotate-half: dim i pairs with i + 64 (first half: a cos - b sin,
+    // second half: a sin + b cos, with a = dim i, b = dim i + 64)
+    vals[t] = v;
+    __syncthreads();
+    const float other = vals[t ^ 64];
+    const bool lo = t < HD / 2;
+    const int ci = lo ? t : t - HD / 2;
+    const float c = a.cos[(size_t)pos * HD + ci], sn = a.sin[(size_t)pos * HD + ci];
+    const float o = lo ? __builtin_fmaf(v, c, -__fmul_rn(other, sn)) : __builtin_fmaf(other, sn, __fmul_rn(v, c));
+    if (isq) {
+        a.qout[((size_t)b * a.H + hh) * HD + t] = o;
+    } else {
+        uint16_t* kc = (uint16_t*)kvp[0];
+        kc[((size_t)pos * a.KH + (hh - a.H)) * HD + t] = (uint16_t)f32_to_bf16_rne(o);
+    }
+}
+
 // One (position split, KV head, token): QPK query heads over positions
-// [128 s, 128 s + 128) of the token's T = pos + 1.  256 threads; lane
-// (g, j) of wave w takes positions 128 s + 32 w + 4 st + g (st < 8) and
-// head dimensions 8 j .. 8 j + 7.
+// [128 s, 128 s + 128) of the token's T = pos + 1 cache rows (the row at pos
+// appended by k_qkv_fin).  256 threads; lane (g, j) of wave w takes
+// positions 128 s + 32 w + 4 st + g (st < 8) and head dimensions 8 j ..
+// 8 j + 7.
 template <int QPK>
 __global__ void __launch_bounds__(256)
 k_attn_part(AttnArgs a) {
     constexpr int HD = 128, P = 128, SP = P + 4;
-    __shared__ __align__(16) float qs[QPK][HD];        // the query heads, normalised and rotated
-    __shared__ __align__(16) float kvn[2][HD];         // the new k and v, as the bf16 cache holds them
     __shared__ __align__(16) float sc[QPK][SP];        // scores, then exp(score - max)
     __shared__ __align__(16) float red[4][QPK * HD];   // per-wave partial outputs
     const int s = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
@@ -231,105 +246,39 @@ k_attn_part(AttnArgs a) {
     const int t0 = s * P;
     if (t0 >= T) return;                 // past this token's positions (block-uniform)
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const float* qb = a.qkv + (size_t)b * a.nqkv;
     const unsigned long long* kvp = a.kv + ((size_t)b * a.L + a.layer) * 2;
-    uint16_t* kc = (uint16_t*)kvp[0];
-    uint16_t* vc = (uint16_t*)kvp[1];
-
-    // ---- the query heads and the new k: per-head RMSNorm (:1174-1189),
-    // then RoPE rotate-half at pos (:1190-1194, :259-266); dims i and i + 64
-    // are 16 lanes apart in a 32-thread group of 4 dims per thread
-    {
-        const int grp = tid >> 5, li = tid & 31, dim = 4 * li;
-        const bool lo = dim < HD / 2;
-        const int ci = lo ? dim : dim - HD / 2;
-        const float4 cs = *(const float4*)(a.cos + (size_t)pos * HD + ci);
-        const float4 sn = *(const float4*)(a.sin + (size_t)pos * HD + ci);
-        for (int it = grp; it <= QPK; it += 8) {
-            const bool isk = it == QPK;
-            const float* src = qb + (size_t)(isk ? a.H + kh : kh * QPK + it) * HD;
-            float v[4];
-            {
-                const float4 t = *(const float4*)(src + dim);
-                v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-            }
-            const uint16_t* nw = isk ? a.kn : a.qn;
-            if (nw) {
-                float ss = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 4; i++) ss = __builtin_fmaf(v[i], v[i], ss);
-                const float inv = rms_inv(seg_sum<32>(ss), HD, a.eps);
-                const uint2 wv = *(const uint2*)(nw + dim);
-                const uint32_t wb[4] = {wv.x & 0xFFFFu, wv.x >> 16, wv.y & 0xFFFFu, wv.y >> 16};
-#pragma unroll
-                for (int i = 0; i < 4; i++) v[i] = __fmul_rn(__fmul_rn(v[i], inv), bf16_bits_to_f32(wb[i]));
-            }
-            const float c4[4] = {cs.x, cs.y, cs.z, cs.w}, s4[4] = {sn.x, sn.y, sn.z, sn.w};
-            float o[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float other = __shfl_xor(v[i], 16, JM_WAVE);
-                // first half: a cos - b sin; second half: a sin + b cos
-                // (a = dim i, b = dim i + 64)
-                o[i] = lo ? __builtin_fmaf(v[i], c4[i], -__fmul_rn(other, s4[i]))
-                          : __builtin_fmaf(other, s4[i], __fmul_rn(v[i], c4[i]));
-            }
-            if (!isk) {
-                *(float4*)(&qs[it][dim]) = make_float4(o[0], o[1], o[2], o[3]);
-            } else {
-                *(float4*)(&kvn[0][dim]) = make_float4(bf16_round(o[0]), bf16_round(o[1]), bf16_round(o[2]),
-                                                       bf16_round(o[3]));
-            }
-        }
-        if (tid < 32) {
-            const float4 t = *(const float4*)(qb + (size_t)(a.H + a.KH + kh) * HD + dim);
-            *(float4*)(&kvn[1][dim]) = make_float4(bf16_round(t.x), bf16_round(t.y), bf16_round(t.z), bf16_round(t.w));
-        }
-    }
-    __syncthreads();
-    // the split holding pos appends the new k and v (:1195-1199)
-    if (pos - t0 < P && tid < 64) {
-        const int which = tid >> 5, dim = 4 * (tid & 31);
-        const float* src = kvn[which];
-        const uint2 bits = make_uint2(f32_to_bf16_rne(src[dim]) | (f32_to_bf16_rne(src[dim + 1]) << 16),
-                                      f32_to_bf16_rne(src[dim + 2]) | (f32_to_bf16_rne(src[dim + 3]) << 16));
-        uint16_t* dst = which ? vc : kc;
-        *(uint2*)(dst + ((size_t)pos * a.KH + kh) * HD + dim) = bits;
-    }
-
-    // ---- scores (:1205-1211): q . k / sqrtf_fast(hd)
+    const uint16_t* kc = (const uint16_t*)kvp[0];
+    const uint16_t* vc = (const uint16_t*)kvp[1];
     const int g = lane >> 4, j = lane & 15;
+    // the rows: unconditional loads (row 0 past the end)
     uint4 kr[8], vr[8];
 #pragma unroll
     for (int st = 0; st < 8; st++) {
         const int t = t0 + 32 * w + 4 * st + g;
-        const int ta = (t < T && t != pos) ? t : 0;     // unconditional loads; pos and the tail replaced below
-        const size_t off = ((size_t)ta * a.KH + kh) * HD + 8 * j;
+        const size_t off = ((size_t)(t < T ? t : 0) * a.KH + kh) * HD + 8 * j;
         kr[st] = *(const uint4*)(kc + off);
         vr[st] = *(const uint4*)(vc + off);
     }
     float q[QPK][8];
 #pragma unroll
     for (int h = 0; h < QPK; h++) {
-        const float4 q0 = *(const float4*)(&qs[h][8 * j]), q1 = *(const float4*)(&qs[h][8 * j + 4]);
+        const float4* qp = (const float4*)(a.qout + ((size_t)b * a.H + kh * QPK + h) * HD + 8 * j);
+        const float4 q0 = qp[0], q1 = qp[1];
         q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
         q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
     }
+
+    // ---- scores (:1205-1211): q . k / sqrtf_fast(hd)
     constexpr int LPH = 16 / QPK;
 #pragma unroll
     for (int st = 0; st < 8; st++) {
         const int t = t0 + 32 * w + 4 * st + g;
+        const uint32_t kw[4] = {kr[st].x, kr[st].y, kr[st].z, kr[st].w};
         float kf[8];
-        if (t == pos) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) kf[i] = kvn[0][8 * j + i];
-        } else {
-            const uint32_t kw[4] = {kr[st].x, kr[st].y, kr[st].z, kr[st].w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                kf[2 * i] = __uint_as_float(kw[i] << 16);
-                kf[2 * i + 1] = __uint_as_float(kw[i] & 0xFFFF0000u);
-            }
+        for (int i = 0; i < 4; i++) {
+            kf[2 * i] = __uint_as_float(kw[i] << 16);
+            kf[2 * i + 1] = __uint_as_float(kw[i] & 0xFFFF0000u);
         }
         float dots[QPK];
 #pragma unroll
@@ -379,18 +328,13 @@ k_attn_part(AttnArgs a) {
 #pragma unroll
     for (int st = 0; st < 8; st++) {
         const int t = t0 + 32 * w + 4 * st + g;
+        const uint32_t vw[4] = {vr[st].x, vr[st].y, vr[st].z, vr[st].w};
+        const bool ok = t < T;
         float vf[8];
-        if (t == pos) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) vf[i] = kvn[1][8 * j + i];
-        } else {
-            const uint32_t vw[4] = {vr[st].x, vr[st].y, vr[st].z, vr[st].w};
-            const bool ok = t < T;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                vf[2 * i] = ok ? __uint_as_float(vw[i] << 16) : 0.0f;
-                vf[2 * i + 1] = ok ? __uint_as_float(vw[i] & 0xFFFF0000u) : 0.0f;
-            }
+        for (int i = 0; i < 4; i++) {
+            vf[2 * i] = ok ? __uint_as_float(vw[i] << 16) : 0.0f;
+            vf[2 * i + 1] = ok ? __uint_as_float(vw[i] & 0xFFFF0000u) : 0.0f;
         }
 #pragma unroll
         for (int h = 0; h < QPK; h++) {
@@ -400,8 +344,7 @@ k_attn_part(AttnArgs a) {
         }
     }
     // sum over the 4 lane groups g: two transposing levels leave lane group
-    // g with values [g' N/4, (g' + 1) N/4) of the flat (head, dim) list,
-    // g' = 2 (g >> 1) + (g & 1) = g
+    // g with values [g N/4, (g + 1) N/4) of the flat (head, dim) list
     constexpr int N = QPK * 8;
     transpose_level<32, N>(acc);
     transpose_level<16, N / 2>(acc);
@@ -417,28 +360,52 @@ k_attn_part(AttnArgs a) {
 }
 
 // Merge of the splits of one (query head, token): out = sum_s o_s e^(m_s - M)
-// / sum_s l_s e^(m_s - M), M the max over the splits.
+// / sum_s l_s e^(m_s - M), M the max over the splits.  The splits' weights
+// are computed in parallel (128 at a time) and staged in LDS; each thread
+// then sums its dimension over them with independent loads.
 __global__ void __launch_bounds__(128)
 k_attn_comb(AttnArgs a, int qpk, float* __restrict__ att) {
-    const int h = blockIdx.x, b = blockIdx.y, dim = threadIdx.x;
+    __shared__ float fs[128];
+    __shared__ float red[2];
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
     const int kh = h / qpk, hq = h % qpk;
-    const int T = a.pos[b] + 1;
-    const int ns = (T + 127) / 128;
+    const int ns = (a.pos[b] + 128) / 128;          // splits of T = pos + 1 positions
     const size_t base = ((size_t)b * a.KH + kh) * a.S;
-    float M = -INFINITY;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, a.part_ml[((base + s) * qpk + hq) * 2]);
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < ns; s++) {
-        const float* ml = a.part_ml + ((base + s) * qpk + hq) * 2;
-        const float f = expf_fast(__fsub_rn(ml[0], M));
-        L = __builtin_fmaf(ml[1], f, L);
-        O = __builtin_fmaf(a.part_o[((base + s) * qpk + hq) * 128 + dim], f, O);
+    const float* ml = a.part_ml + (base * qpk + hq) * 2;      // split s at ml[2 qpk s]
+    float mx = -INFINITY;
+    for (int s = t; s < ns; s += 128) mx = fmaxf(mx, ml[(size_t)2 * qpk * s]);
+    mx = seg_max<64>(mx);
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    const float M = fmaxf(red[0], red[1]);
+    float lsum = 0.0f, O = 0.0f;
+    const float* po = a.part_o + (base * qpk + hq) * 128 + t;  // split s at po[128 qpk s]
+    for (int c0 = 0; c0 < ns; c0 += 128) {
+        const int s = c0 + t;
+        float f = 0.0f;
+        if (s < ns) {
+            f = expf_fast(__fsub_rn(ml[(size_t)2 * qpk * s], M));
+            lsum = __builtin_fmaf(ml[(size_t)2 * qpk * s + 1], f, lsum);
+        }
+        __syncthreads();
+        fs[t] = f;
+        __syncthreads();
+        const int n = ns - c0 < 128 ? ns - c0 : 128;
+#pragma unroll 8
+        for (int i = 0; i < n; i++) O = __builtin_fmaf(po[(size_t)128 * qpk * (c0 + i)], fs[i], O);
     }
-    att[((size_t)b * a.H + h) * 128 + dim] = __fdiv_rn(O, L);
+    lsum = seg_sum<64>(lsum);
+    __syncthreads();
+    if ((t & 63) == 0) red[t >> 6] = lsum;
+    __syncthreads();
+    att[((size_t)b * a.H + h) * 128 + t] = __fdiv_rn(O, __fadd_rn(red[0], red[1]));
 }
 
 hipError_t launch_attn(const AttnArgs& a, int qpk, float* att, hipStream_t st) {
     if (a.B == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_qkv_fin, dim3((unsigned)(a.H + 2 * a.KH), (unsigned)a.B), dim3(128), 0, st, a);
+    hipError_t e0 = hipGetLastError();
+    if (e0 != hipSuccess) return e0;
     const dim3 grid((unsigned)a.S, (unsigned)a.KH, (unsigned)a.B);
     switch (qpk) {
         case 1: hipLaunchKernelGGL(k_attn_part<1>, grid, dim3(256), 0, st, a); break;

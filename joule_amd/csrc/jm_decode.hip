@@ -3,12 +3,13 @@
 // of each layer from the store.  Per layer, five launches around the MoE
 // block's own:
 //
-//   qkv      = [Wq; Wk; Wv] . RMSNorm1(h) (+ bias)            k_gemv_bf16
-//   partials = attention over 128-position splits of the cache  k_attn_part
+//   qkv      = [Wq; Wk; Wv] . (h * norm1 w), per column slice  k_gemv_part
+//   partials = RMSNorm row scale + bias, QK-norm, RoPE, KV append,
+//              attention over 128-position splits of the cache  k_attn_part
 //   att      = the splits merged                               k_attn_comb
-//   h       += Wo . att                                        k_gemv_bf16
-//   h       += MoE(RMSNorm2(h))    the norm inside the router, the add inside
-//                                  the down/combine kernel
+//   opart    = Wo . att, per column slice                      k_gemv_part
+//   h2 = h + sum(opart); h = h2 + MoE(RMSNorm2(h2))   the sum and the norm
+//              inside the router, the add inside the down/combine kernel
 //
 // then hidden = RMSNorm_final(h).
 #include <hip/hip_runtime.h>
@@ -55,10 +56,13 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq) {
     const int d = s->d;
     const size_t sz[] = {
         (size_t)B * d * 4,                        // h
-        (size_t)B * nqkv * 4,                     // qkv
+        (size_t)B * d * 4,                        // h2
+        (size_t)(d / 512) * B * nqkv * 4,         // qkv slices
+        (size_t)(hq / 512) * B * d * 4,           // o_proj slices
         (size_t)B * S * hq * 4,                   // part_o: H heads x hd per split
         (size_t)B * S * (hq / HD) * 2 * 4,        // part_ml
         (size_t)B * hq * 4,                       // att
+        (size_t)B * hq * 4,                       // qout
         s->tab_cap,                               // KV pointers + positions
     };
     size_t total = 0;
@@ -68,8 +72,8 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq) {
     free_decode(s);
     JM_HIP(hipMalloc(&s->dws, total), "hipMalloc decode workspace");
     char* p = (char*)s->dws;
-    void** slots[] = {(void**)&s->h, (void**)&s->qkv, (void**)&s->part_o, (void**)&s->part_ml,
-                      (void**)&s->att, (void**)&s->tab};
+    void** slots[] = {(void**)&s->h, (void**)&s->h2, (void**)&s->qkv, (void**)&s->opart, (void**)&s->part_o,
+                      (void**)&s->part_ml, (void**)&s->att, (void**)&s->qout, (void**)&s->tab};
     for (size_t i = 0; i < sizeof sz / sizeof sz[0]; i++) {
         *slots[i] = p;
         p += align256(sz[i]);
@@ -92,7 +96,7 @@ int check_decode_args(const jm_store* s, const jm_kernel_cfg* c, const jm_kernel
     if (*qpk != 1 && *qpk != 2 && *qpk != 4 && *qpk != 8)
         return fail(JM_ERR_SHAPE, "n_heads / n_kv must be 1, 2, 4 or 8 (got %d)", *qpk);
     if (!jm::gemv_shape_ok(c->d) || !jm::gemv_shape_ok(c->n_heads * HD))
-        return fail(JM_ERR_SHAPE, "d=%d and n_heads*hd=%d must each be 1024, 2048 or 4096", c->d, c->n_heads * HD);
+        return fail(JM_ERR_SHAPE, "d=%d and n_heads*hd=%d must be multiples of 512 up to 8192", c->d, c->n_heads * HD);
     if (c->qk_norm_type != 0 && c->qk_norm_type != 1)
         return fail(JM_ERR_SHAPE, "qk_norm_type %d: only 0 (none) and 1 (per head) are supported", c->qk_norm_type);
     if (c->maxT <= 0) return fail(JM_ERR_SHAPE, "maxT must be positive");
@@ -205,28 +209,28 @@ int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_
         jm::GemvArgs g{};
         g.x = s->h;
         g.norm_w = W->norm1 + (size_t)l * d;
-        g.eps = c->eps;
         g.w[0] = W->wq + (size_t)l * H * HD * d;
         g.w[1] = W->wk + (size_t)l * KH * HD * d;
         g.w[2] = W->wv + (size_t)l * KH * HD * d;
-        if (c->bias_qkv) {
-            g.bias[0] = W->bq + (size_t)l * H * HD;
-            g.bias[1] = W->bk + (size_t)l * KH * HD;
-            g.bias[2] = W->bv + (size_t)l * KH * HD;
-        }
         g.rows[0] = H * HD; g.rows[1] = KH * HD; g.rows[2] = KH * HD;
         g.K = d; g.N = nqkv; g.B = B;
-        g.out = s->qkv;
-        JM_HIP(jm::launch_gemv_bf16(g, 4, st), "qkv launch");
+        g.part = s->qkv;
+        JM_HIP(jm::launch_gemv_part(g, st), "qkv launch");
 
         jm::AttnArgs at{};
-        at.qkv = s->qkv; at.nqkv = nqkv; at.H = H; at.KH = KH; at.B = B;
+        at.qkv = s->qkv; at.nslice = d / 512; at.h = s->h; at.d = d;
+        if (c->bias_qkv) {
+            at.bq = W->bq + (size_t)l * H * HD;
+            at.bk = W->bk + (size_t)l * KH * HD;
+            at.bv = W->bv + (size_t)l * KH * HD;
+        }
+        at.nqkv = nqkv; at.H = H; at.KH = KH; at.B = B;
         at.qn = c->qk_norm_type == 1 ? W->qn + (size_t)l * HD : nullptr;
         at.kn = c->qk_norm_type == 1 ? W->kn + (size_t)l * HD : nullptr;
         at.eps = c->eps; at.sdiv = sdiv;
         at.cos = W->cos; at.sin = W->sin;
         at.pos = pos_dev; at.kv = s->tab; at.L = L; at.layer = l;
-        at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;
+        at.qout = s->qout; at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;
         // the grid covers the longest token's splits; the buffers hold S_cap
         // per (token, KV head), indexed with the call's S
         JM_HIP(jm::launch_attn(at, qpk, s->att, st), "attention launch");
@@ -236,17 +240,33 @@ int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_
         o.w[0] = W->wo + (size_t)l * d * H * HD;
         o.rows[0] = d;
         o.K = H * HD; o.N = d; o.B = B;
-        o.resid = s->h; o.out = s->h;
-        JM_HIP(jm::launch_gemv_bf16(o, 2, st), "o_proj launch");
+        o.part = s->opart;
+        JM_HIP(jm::launch_gemv_part(o, st), "o_proj launch");
 
         JM_DMARK(2 * l + 2);
-        if (int rc = jm::ffn_enqueue(s, l, s->h, B, s->h, W->norm2 + (size_t)l * d, c->eps, s->h, false, st))
-            return rc;
+        // h2 = h + attention (summed from the o_proj slices in the router),
+        // then h = h2 + MoE(RMSNorm(h2))
+        jm::FfnIo io;
+        io.xpart = s->opart; io.nxpart = H * HD / 512; io.xmid = s->h2;
+        io.norm_w = W->norm2 + (size_t)l * d; io.eps = c->eps;
+        io.resid = s->h2;
+        if (int rc = jm::ffn_enqueue(s, l, s->h, B, s->h, io, false, st)) return rc;
+        const size_t tk = (size_t)B * c->topk * 4;
+        if (s->trace && (l + 1) * tk <= s->trace_bytes)
+            JM_HIP(hipMemcpyAsync((char*)s->trace + l * tk, s->top, tk, hipMemcpyDeviceToDevice, st), "top-k trace");
     }
     JM_DMARK(2 * L + 1);
     JM_HIP(jm::launch_rms_rows(s->h, W->final_norm, B, d, c->eps, hidden, st), "final norm launch");
     JM_DMARK(2 * L + 2);
 #undef JM_DMARK
+    return 0;
+}
+
+int jm_store_trace_topk(jm_store* s, int32_t* buf, uint64_t bytes) {
+    if (!s) return fail(JM_ERR_ARG, "store is NULL");
+    if (buf && !aligned(buf, 4)) return fail(JM_ERR_ARG, "trace buffer must be 4-byte aligned");
+    s->trace = buf;
+    s->trace_bytes = buf ? bytes : 0;
     return 0;
 }
 

@@ -71,6 +71,9 @@ struct RouteArgs {
     const void* wt;           // interleaved router copy of the layer
     int wt_bf16;              // 1: wt holds bf16 bits, 0: float32
     const float* x;           // [B][d]
+    const float* xpart;       // [nxpart][B][d] slices added to x first (NULL: none)
+    int nxpart;
+    float* xmid;              // [B][d] receives x + the slices (NULL: not kept)
     const uint16_t* norm_w;   // [d] bf16 RMSNorm weight applied to x first (NULL: x as given)
     float eps;
     int B, E, d, topk, renorm, group;
@@ -135,27 +138,32 @@ hipError_t launch_combine(const float* y, const int* comb, int B, int k, int d, 
                           float* out, hipStream_t st);
 // ---- decoder layer around the MoE block (jm_attn.hip)
 
-// out[b][row] = (resid +) (bias +) W[row] . xn[b] over the rows of up to three
-// stacked bf16 matrices [rows_i][K]; xn = x or RMSNorm(x) * norm_w.
+// part[s][b][row] = sum over the columns k of 512-column slice s of
+// W[row][k] * x[b][k] (* norm_w[k]), rows of up to three stacked bf16
+// matrices [rows_i][K]; the consumer sums the K / 512 slices.
 struct GemvArgs {
     const float* x;           // [B][K]
-    const uint16_t* norm_w;   // [K] bf16, or NULL
-    float eps;
+    const uint16_t* norm_w;   // [K] bf16 weight multiplied into x, or NULL
     const uint16_t* w[3];     // bf16 [rows[i]][K]
-    const float* bias[3];     // fp32 [rows[i]] or NULL
     int rows[3];
-    int K, N, B;              // N = rows[0] + rows[1] + rows[2] (the out row stride)
-    const float* resid;       // [B][N] or NULL; may alias out
-    float* out;               // [B][N]
+    int K, N, B;              // N = rows[0] + rows[1] + rows[2]
+    float* part;              // [K / 512][B][N]
 };
-// K in {1024, 2048, 4096}; rows_per_wave 2 or 4 (4 waves per block)
+// K a multiple of 512 (at most 8192)
 bool gemv_shape_ok(int K);
-hipError_t launch_gemv_bf16(const GemvArgs& a, int rows_per_wave, hipStream_t st);
+hipError_t launch_gemv_part(const GemvArgs& a, hipStream_t st);
 
 // Decode attention of one layer for B tokens, head dim 128, H / KH query
 // heads per KV head (1, 2, 4 or 8), in splits of 128 positions.
 struct AttnArgs {
-    const float* qkv;         // [B][nqkv]: H q heads, KH k heads, KH v heads
+    const float* qkv;         // [nslice][B][nqkv] slices of the projections of h * norm1 weight:
+                              // H q heads, KH k heads, KH v heads
+    int nslice;
+    const float* h;           // [B][d] the layer input (its RMSNorm row scale)
+    int d;
+    const float* bq;          // [H*128] / [KH*128] biases of the layer, or NULL
+    const float* bk;
+    const float* bv;
     int nqkv, H, KH, B;
     const uint16_t* qn;       // [128] bf16 per-head q norm of the layer, or NULL
     const uint16_t* kn;       // [128] bf16 per-head k norm, or NULL
@@ -166,11 +174,13 @@ struct AttnArgs {
     const int* pos;           // [B] position each token writes (T = pos + 1)
     const unsigned long long* kv;   // [B*L][2] bf16 k, v caches [maxT][KH][128]
     int L, layer;
+    float* qout;              // [B][H][128] the finished query heads
     int S;                    // splits the partial buffers hold per (token, KV head)
     float* part_o;            // [B][KH][S][H/KH][128]
     float* part_ml;           // [B][KH][S][H/KH][2]
 };
-// partial attention, then the merge into att [B][H*128]
+// the projections finished (q out, k and v appended), partial attention,
+// then the merge into att [B][H*128]
 hipError_t launch_attn(const AttnArgs& a, int qpk, float* att, hipStream_t st);
 hipError_t launch_rms_rows(const float* x, const uint16_t* w, int B, int d, float eps, float* out,
                            hipStream_t st);

@@ -166,6 +166,33 @@ k_router_grp(RouteArgs a) {
     uint4 buf[NB][C::CP];
 #pragma unroll
     for (int c = 0; c < NB; c++) C::load(buf[c], wt, eg, c, lane);
+    if (a.xpart) {
+        // the decoder layer's residual add before the MoE block
+        // (decode_kernel.c:1546-1547): x + the attention output, which comes
+        // as the o_proj's column slices
+        const float4* xp = (const float4*)(a.xpart + (size_t)b * d);
+        const size_t sstride = (size_t)a.B * d / 4;
+        float4 ps[XV];
+#pragma unroll
+        for (int i = 0; i < XV; i++) ps[i] = xp[lane + 64 * i];
+        for (int sl = 1; sl < a.nxpart; sl++) {
+#pragma unroll
+            for (int i = 0; i < XV; i++) {
+                const float4 u = xp[sl * sstride + lane + 64 * i];
+                ps[i] = make_float4(__fadd_rn(ps[i].x, u.x), __fadd_rn(ps[i].y, u.y), __fadd_rn(ps[i].z, u.z),
+                                    __fadd_rn(ps[i].w, u.w));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < XV; i++)
+            xv[i] = make_float4(__fadd_rn(xv[i].x, ps[i].x), __fadd_rn(xv[i].y, ps[i].y), __fadd_rn(xv[i].z, ps[i].z),
+                                __fadd_rn(xv[i].w, ps[i].w));
+        if (eg == 0 && a.xmid) {
+            float4* xm = (float4*)(a.xmid + (size_t)b * d);
+#pragma unroll
+            for (int i = 0; i < XV; i++) xm[lane + 64 * i] = xv[i];
+        }
+    }
     if (a.norm_w) {
         // the decoder layer's RMSNorm of the token first (decode_kernel.c:224-230,
         // applied at :1549): x * (1 / sqrtf_fast(sum x^2 / d + eps)) * w

@@ -56,15 +56,20 @@ struct jm_store {
     int dec_B, dec_S, dec_nqkv, dec_hq;   // sizes the decode workspace holds
     void* dws;                  // decode workspace
     float* h;                   // [B][d] residual stream
-    float* qkv;                 // [B][(H + 2 KH) hd] projections
+    float* h2;                  // [B][d] residual stream after attention
+    float* qkv;                 // [d/512][B][(H + 2 KH) hd] projection slices
+    float* opart;               // [H hd/512][B][d] o_proj slices
     float* part_o;              // [B][KH][S][H/KH][hd] attention partials per position split
     float* part_ml;             // [B][KH][S][H/KH][2] their (max, sum)
     float* att;                 // [B][H hd] attention output
+    float* qout;                // [B][H hd] finished query heads
     unsigned long long* tab;    // [B*L][2] KV pointers, then [B] positions (device)
     unsigned long long* tab_host;   // pinned staging of tab
     size_t tab_cap;             // bytes of tab / tab_host
     hipEvent_t tab_ev;          // the last staging copy
     int tab_pending;
+    int32_t* trace;             // [L][B][topk] selected experts per layer (jm_store_trace_topk)
+    uint64_t trace_bytes;
     // per-layer attention / MoE split of the last decode call (jm_store_profile)
     int dprof_n;
     hipEvent_t* dev_marks;      // [2 L + 2]
@@ -82,12 +87,20 @@ inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 // MoE workspace for batches of up to B tokens.
 int store_reserve(jm_store* s, int B);
 
-// Enqueue the MoE block of one layer on x [B][d] into out [B][d].  With
-// norm_w, x is RMS-normalised with it first (in the router); with resid,
-// out = resid + block (resid may alias out).  stage_marks: record the
-// store's stage events.
-int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const uint16_t* norm_w,
-                float eps, const float* resid, bool stage_marks, hipStream_t st);
+// Decoder-layer extras of the MoE block around its input and output.
+struct FfnIo {
+    const float* xpart = nullptr;   // [nxpart][B][d] added to x first (the o_proj slices)
+    int nxpart = 0;
+    float* xmid = nullptr;          // receives x + the slices
+    const uint16_t* norm_w = nullptr;   // RMSNorm weight applied next (in the router)
+    float eps = 0.0f;
+    const float* resid = nullptr;   // out = resid + block (resid may alias out)
+};
+
+// Enqueue the MoE block of one layer on x [B][d] into out [B][d].
+// stage_marks: record the store's stage events.
+int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const FfnIo& io,
+                bool stage_marks, hipStream_t st);
 
 // Release the batch-decode workspace, staging and events.
 void decode_free_all(jm_store* s);

@@ -199,6 +199,15 @@ class HipDecoder:
             _lib.stream_handle(stream)), "jm_decode_layers_batch")
         return hidden
 
+    def trace_topk(self, buf: torch.Tensor | None) -> None:
+        """Copy each layer's selected experts into buf [L, B, topk] (int32,
+        CUDA) during later calls; None stops it."""
+        if buf is not None and (buf.dtype != torch.int32 or not buf.is_cuda or not buf.is_contiguous()):
+            raise ValueError("trace buffer must be a contiguous int32 CUDA tensor")
+        _lib.check(_lib.lib().jm_store_trace_topk(self.store._h, _lib.ptr(buf),
+                                                  0 if buf is None else buf.numel() * 4),
+                   "jm_store_trace_topk")
+
     def split_ms(self) -> dict:
         """Attention / MoE / total milliseconds of the last call made with
         profiling on (store.profile(True)); waits for it."""
