@@ -239,6 +239,14 @@ int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* cfg, const jm_kerne
                            const int32_t* positions, const float* xin, int B, float* logits, float* hidden,
                            void* stream);
 
+/* With enable set, jm_decode_layers_batch records its launches once into a
+ * HIP graph and replays it, re-recording when the arguments, the batch size
+ * or the number of 128-position attention splits change; calls with
+ * profiling on run eagerly.  The KV table and positions are still copied
+ * from the host on every call.  Off by default.  No counterpart in the
+ * reference. */
+int jm_store_decode_graph(jm_store* s, int enable);
+
 /* With buf set (device int32, `bytes` long), each later
  * jm_decode_layers_batch also copies every layer's selected experts into
  * buf[l][B][topk], for accounting and tests; NULL turns it off.  No

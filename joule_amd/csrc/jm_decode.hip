@@ -31,6 +31,8 @@ constexpr int HD = 128;     // head dimension the attention kernels take
 constexpr int PSPLIT = 128; // positions per attention split
 
 void free_decode(jm_store* s) {
+    if (s->gexec) (void)hipGraphExecDestroy(s->gexec);
+    s->gexec = nullptr;
     if (s->dws) (void)hipFree(s->dws);
     s->dws = nullptr;
     s->dec_B = s->dec_S = s->dec_nqkv = s->dec_hq = 0;
@@ -117,11 +119,84 @@ int check_decode_args(const jm_store* s, const jm_kernel_cfg* c, const jm_kernel
     return 0;
 }
 
+// Every launch of one decode step on st (after the staging copy).
+int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const float* xin, int B,
+                 float* hidden, int S, int qpk, bool capturing, hipStream_t st) {
+    const int L = c->L, d = c->d, H = c->n_heads, KH = c->n_kv;
+    const int nqkv = (H + 2 * KH) * HD;
+    const int* pos_dev = (const int*)(s->tab + (size_t)2 * B * L);
+    const bool marks = s->prof && !capturing;
+#define JM_DMARK(i) if (marks) JM_HIP(hipEventRecord(s->dev_marks[i], st), "hipEventRecord")
+    JM_DMARK(0);
+    JM_HIP(hipMemcpyAsync(s->h, xin, (size_t)B * d * 4, hipMemcpyDeviceToDevice, st), "copy xin");
+    const float sdiv = jm::sqrtf_fast((float)HD);
+    for (int l = 0; l < L; l++) {
+        JM_DMARK(2 * l + 1);
+        jm::GemvArgs g{};
+        g.x = s->h;
+        g.norm_w = W->norm1 + (size_t)l * d;
+        g.w[0] = W->wq + (size_t)l * H * HD * d;
+        g.w[1] = W->wk + (size_t)l * KH * HD * d;
+        g.w[2] = W->wv + (size_t)l * KH * HD * d;
+        g.rows[0] = H * HD; g.rows[1] = KH * HD; g.rows[2] = KH * HD;
+        g.K = d; g.N = nqkv; g.B = B;
+        g.part = s->qkv;
+        JM_HIP(jm::launch_gemv_part(g, st), "qkv launch");
+
+        jm::AttnArgs at{};
+        at.qkv = s->qkv; at.nslice = d / 512; at.h = s->h; at.d = d;
+        if (c->bias_qkv) {
+            at.bq = W->bq + (size_t)l * H * HD;
+            at.bk = W->bk + (size_t)l * KH * HD;
+            at.bv = W->bv + (size_t)l * KH * HD;
+        }
+        at.nqkv = nqkv; at.H = H; at.KH = KH; at.B = B;
+        at.qn = c->qk_norm_type == 1 ? W->qn + (size_t)l * HD : nullptr;
+        at.kn = c->qk_norm_type == 1 ? W->kn + (size_t)l * HD : nullptr;
+        at.eps = c->eps; at.sdiv = sdiv;
+        at.cos = W->cos; at.sin = W->sin;
+        at.pos = pos_dev; at.kv = s->tab; at.L = L; at.layer = l;
+        at.qout = s->qout; at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;
+        // the grid covers the longest token's splits; the buffers hold S_cap
+        // per (token, KV head), indexed with the call's S
+        JM_HIP(jm::launch_attn(at, qpk, s->att, st), "attention launch");
+
+        jm::GemvArgs o{};
+        o.x = s->att;
+        o.w[0] = W->wo + (size_t)l * d * H * HD;
+        o.rows[0] = d;
+        o.K = H * HD; o.N = d; o.B = B;
+        o.part = s->opart;
+        JM_HIP(jm::launch_gemv_part(o, st), "o_proj launch");
+
+        JM_DMARK(2 * l + 2);
+        // h2 = h + attention (summed from the o_proj slices in the router),
+        // then h = h2 + MoE(RMSNorm(h2))
+        jm::FfnIo io;
+        io.xpart = s->opart; io.nxpart = H * HD / 512; io.xmid = s->h2;
+        io.norm_w = W->norm2 + (size_t)l * d; io.eps = c->eps;
+        io.resid = s->h2;
+        if (int rc = jm::ffn_enqueue(s, l, s->h, B, s->h, io, false, st)) return rc;
+        const size_t tk = (size_t)B * c->topk * 4;
+        if (s->trace && (l + 1) * tk <= s->trace_bytes)
+            JM_HIP(hipMemcpyAsync((char*)s->trace + l * tk, s->top, tk, hipMemcpyDeviceToDevice, st), "top-k trace");
+    }
+    JM_DMARK(2 * L + 1);
+    JM_HIP(jm::launch_rms_rows(s->h, W->final_norm, B, d, c->eps, hidden, st), "final norm launch");
+    JM_DMARK(2 * L + 2);
+#undef JM_DMARK
+    return 0;
+}
+
 }  // namespace
 
 namespace jm {
 
 void decode_free_all(jm_store* s) {
+    if (s->gexec) (void)hipGraphExecDestroy(s->gexec);
+    if (s->cap_st) (void)hipStreamDestroy(s->cap_st);
+    s->gexec = nullptr;
+    s->cap_st = nullptr;
     free_decode(s);
     if (s->tab_pending) (void)hipEventSynchronize(s->tab_ev);
     if (s->tab_host) (void)hipHostFree(s->tab_host);
@@ -182,9 +257,7 @@ int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_
     JM_HIP(hipMemcpyAsync(s->tab, s->tab_host, tab_bytes, hipMemcpyHostToDevice, st), "staging copy");
     JM_HIP(hipEventRecord(s->tab_ev, st), "hipEventRecord staging");
     s->tab_pending = 1;
-    const int* pos_dev = (const int*)(s->tab + (size_t)2 * B * L);
-
-    // per-layer split of the time (jm_store_profile)
+    // per-layer split of the time (jm_store_profile): eager calls only
     const int nmarks = 2 * L + 3;
     if (s->prof && s->dprof_n != nmarks) {
         if (s->dev_marks) {
@@ -199,66 +272,50 @@ int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_
             s->dprof_n = i + 1;
         }
     }
-#define JM_DMARK(i) if (s->prof) JM_HIP(hipEventRecord(s->dev_marks[i], st), "hipEventRecord")
 
-    JM_DMARK(0);
-    JM_HIP(hipMemcpyAsync(s->h, xin, (size_t)B * d * 4, hipMemcpyDeviceToDevice, st), "copy xin");
-    const float sdiv = jm::sqrtf_fast((float)HD);
-    for (int l = 0; l < L; l++) {
-        JM_DMARK(2 * l + 1);
-        jm::GemvArgs g{};
-        g.x = s->h;
-        g.norm_w = W->norm1 + (size_t)l * d;
-        g.w[0] = W->wq + (size_t)l * H * HD * d;
-        g.w[1] = W->wk + (size_t)l * KH * HD * d;
-        g.w[2] = W->wv + (size_t)l * KH * HD * d;
-        g.rows[0] = H * HD; g.rows[1] = KH * HD; g.rows[2] = KH * HD;
-        g.K = d; g.N = nqkv; g.B = B;
-        g.part = s->qkv;
-        JM_HIP(jm::launch_gemv_part(g, st), "qkv launch");
-
-        jm::AttnArgs at{};
-        at.qkv = s->qkv; at.nslice = d / 512; at.h = s->h; at.d = d;
-        if (c->bias_qkv) {
-            at.bq = W->bq + (size_t)l * H * HD;
-            at.bk = W->bk + (size_t)l * KH * HD;
-            at.bv = W->bv + (size_t)l * KH * HD;
+    if (s->dgraph && !s->prof) {
+        // replay the step from a captured graph: kernel arguments are baked
+        // in, so the capture is keyed by everything they depend on
+        DecKey key;
+        memset(&key, 0, sizeof key);
+        memcpy(&key.cfg, c, sizeof *c);
+        memcpy(&key.W, W, sizeof *W);
+        key.xin = xin; key.hidden = hidden; key.B = B; key.S = S;
+        key.trace = s->trace; key.trace_bytes = s->trace_bytes; key.ws = s->ws; key.dws = s->dws;
+        key.wt = s->wt; key.dense_min = s->dense_min;
+        if (!s->gexec || memcmp(&key, &s->gkey, sizeof key) != 0) {
+            if (s->gexec) {
+                JM_HIP(hipStreamSynchronize(st), "hipStreamSynchronize before recapture");
+                (void)hipGraphExecDestroy(s->gexec);
+                s->gexec = nullptr;
+            }
+            if (!s->cap_st) JM_HIP(hipStreamCreateWithFlags(&s->cap_st, hipStreamNonBlocking), "hipStreamCreate");
+            JM_HIP(hipStreamBeginCapture(s->cap_st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+            const int rc = enqueue_step(s, c, W, xin, B, hidden, S, qpk, true, s->cap_st);
+            hipGraph_t graph = nullptr;
+            const hipError_t ec = hipStreamEndCapture(s->cap_st, &graph);
+            if (rc) {
+                if (graph) (void)hipGraphDestroy(graph);
+                return rc;
+            }
+            if (ec != hipSuccess) return hip_fail(ec, "hipStreamEndCapture");
+            const hipError_t ei = hipGraphInstantiate(&s->gexec, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            if (ei != hipSuccess) {
+                s->gexec = nullptr;
+                return hip_fail(ei, "hipGraphInstantiate");
+            }
+            memcpy(&s->gkey, &key, sizeof key);
         }
-        at.nqkv = nqkv; at.H = H; at.KH = KH; at.B = B;
-        at.qn = c->qk_norm_type == 1 ? W->qn + (size_t)l * HD : nullptr;
-        at.kn = c->qk_norm_type == 1 ? W->kn + (size_t)l * HD : nullptr;
-        at.eps = c->eps; at.sdiv = sdiv;
-        at.cos = W->cos; at.sin = W->sin;
-        at.pos = pos_dev; at.kv = s->tab; at.L = L; at.layer = l;
-        at.qout = s->qout; at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;
-        // the grid covers the longest token's splits; the buffers hold S_cap
-        // per (token, KV head), indexed with the call's S
-        JM_HIP(jm::launch_attn(at, qpk, s->att, st), "attention launch");
-
-        jm::GemvArgs o{};
-        o.x = s->att;
-        o.w[0] = W->wo + (size_t)l * d * H * HD;
-        o.rows[0] = d;
-        o.K = H * HD; o.N = d; o.B = B;
-        o.part = s->opart;
-        JM_HIP(jm::launch_gemv_part(o, st), "o_proj launch");
-
-        JM_DMARK(2 * l + 2);
-        // h2 = h + attention (summed from the o_proj slices in the router),
-        // then h = h2 + MoE(RMSNorm(h2))
-        jm::FfnIo io;
-        io.xpart = s->opart; io.nxpart = H * HD / 512; io.xmid = s->h2;
-        io.norm_w = W->norm2 + (size_t)l * d; io.eps = c->eps;
-        io.resid = s->h2;
-        if (int rc = jm::ffn_enqueue(s, l, s->h, B, s->h, io, false, st)) return rc;
-        const size_t tk = (size_t)B * c->topk * 4;
-        if (s->trace && (l + 1) * tk <= s->trace_bytes)
-            JM_HIP(hipMemcpyAsync((char*)s->trace + l * tk, s->top, tk, hipMemcpyDeviceToDevice, st), "top-k trace");
+        JM_HIP(hipGraphLaunch(s->gexec, st), "hipGraphLaunch");
+        return 0;
     }
-    JM_DMARK(2 * L + 1);
-    JM_HIP(jm::launch_rms_rows(s->h, W->final_norm, B, d, c->eps, hidden, st), "final norm launch");
-    JM_DMARK(2 * L + 2);
-#undef JM_DMARK
+    return enqueue_step(s, c, W, xin, B, hidden, S, qpk, false, st);
+}
+
+int jm_store_decode_graph(jm_store* s, int enable) {
+    if (!s) return fail(JM_ERR_ARG, "store is NULL");
+    s->dgraph = enable ? 1 : 0;      // a recorded step is kept for later replays
     return 0;
 }
 

@@ -9,6 +9,22 @@
 #include "../../include/joule_amd.h"
 #include "jm_kernels.h"
 
+// What a captured decode step depends on (the graph bakes in kernel
+// arguments): compared bytewise, built from a zeroed struct.
+struct DecKey {
+    jm_kernel_cfg cfg;
+    jm_kernel_w W;
+    const float* xin;
+    float* hidden;
+    int B, S;
+    int32_t* trace;
+    uint64_t trace_bytes;
+    void* ws;
+    void* dws;
+    void* wt;
+    int dense_min;
+};
+
 struct jm_store {
     int L, E, d, m, topk, renorm, group;
     const uint8_t* blob;
@@ -70,6 +86,11 @@ struct jm_store {
     int tab_pending;
     int32_t* trace;             // [L][B][topk] selected experts per layer (jm_store_trace_topk)
     uint64_t trace_bytes;
+    // decode step replayed from a captured HIP graph (jm_store_decode_graph)
+    int dgraph;
+    hipStream_t cap_st;
+    hipGraphExec_t gexec;
+    DecKey gkey;
     // per-layer attention / MoE split of the last decode call (jm_store_profile)
     int dprof_n;
     hipEvent_t* dev_marks;      // [2 L + 2]

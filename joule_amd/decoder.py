@@ -170,13 +170,19 @@ class KVCacheSet:
 class HipDecoder:
     """decode_layers_batch over an HBM expert store and dense weights."""
 
-    def __init__(self, store: HbmExpertStore, weights: DecoderWeights):
+    def __init__(self, store: HbmExpertStore, weights: DecoderWeights, graph: bool = True):
         shape = weights.shape
         if store.shape != shape.moe or store.n_layers != shape.n_layers:
             raise ValueError("store and decoder shapes differ")
         self.store, self.weights, self.shape = store, weights, shape
         self._cfg = shape.kernel_cfg()
         self._w = weights.kernel_w()
+        self.set_graph(graph)
+
+    def set_graph(self, enable: bool) -> None:
+        """Replay each step from a captured HIP graph (re-recorded when the
+        buffers, batch size or attention split count change)."""
+        _lib.check(_lib.lib().jm_store_decode_graph(self.store._h, int(bool(enable))), "jm_store_decode_graph")
 
     def decode_layers_batch(self, x: torch.Tensor, positions, kv: KVCacheSet,
                             hidden: torch.Tensor | None = None, stream=None) -> torch.Tensor:

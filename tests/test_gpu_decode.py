@@ -143,3 +143,32 @@ def test_decode_split_profile_and_errors():
     assert ms["attention"] > 0 and ms["moe"] > 0 and ms["attention"] + ms["moe"] <= ms["total"] * 1.001
     dec.store.profile(False)
     dec.store.close()
+
+
+def test_decode_graph_replays_match_eager():
+    """The step replayed from a captured HIP graph gives the eager step's bits,
+    replay after replay, with eager work and synchronisation in between; new
+    positions within the same split count replay the same graph, a new split
+    count records a new one."""
+    shape = qwen3_30b_a3b(n_layers=2, maxT=400)
+    dec, _, kv = _model(shape, 64, 4)
+    x = torch.from_numpy(activations(4, shape.d)).cuda()
+    hid = torch.empty_like(x)
+    for pos in ([10, 130, 257, 300], [11, 131, 258, 301], [11, 131, 258, 399]):
+        print(f"[decode] graph replays at positions {pos}", flush=True)
+        dec.set_graph(False)
+        want = dec.decode_layers_batch(x, pos, kv, torch.empty_like(x)).clone()
+        torch.cuda.synchronize()
+        dec.set_graph(True)
+        for i in range(3):
+            got = dec.decode_layers_batch(x, pos, kv, hid)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"positions {pos}: replay {i} differs from the eager step"
+            # eager work in between: torch reductions and an eager decode step
+            assert float((x * 2).abs().sum().item()) > 0
+            dec.set_graph(False)
+            again = dec.decode_layers_batch(x, pos, kv, torch.empty_like(x))
+            torch.cuda.synchronize()
+            assert torch.equal(again, want)
+            dec.set_graph(True)
+    dec.store.close()
