@@ -142,7 +142,10 @@ struct Chain {
 // staged token.  The top-k then runs per token in k_topk once every score
 // is written: a per-token block would have to pull the whole table through
 // one CU.
-template <int G, int NDIG, int DV, bool WBF16>
+// LAYER: the decoder-layer variant, which first adds the o_proj slices to x
+// and applies the RMSNorm (a separate instance, so that the plain block's
+// router keeps its register budget).
+template <int G, int NDIG, int DV, bool WBF16, bool LAYER>
 __global__ void __launch_bounds__(64)
 k_router_grp(RouteArgs a) {
     using C = Chain<DV, WBF16>;
@@ -166,7 +169,7 @@ k_router_grp(RouteArgs a) {
     uint4 buf[NB][C::CP];
 #pragma unroll
     for (int c = 0; c < NB; c++) C::load(buf[c], wt, eg, c, lane);
-    if (a.xpart) {
+    if (LAYER && a.xpart) {
         // the decoder layer's residual add before the MoE block
         // (decode_kernel.c:1546-1547): x + the attention output, which comes
         // as the o_proj's column slices
@@ -193,7 +196,7 @@ k_router_grp(RouteArgs a) {
             for (int i = 0; i < XV; i++) xm[lane + 64 * i] = xv[i];
         }
     }
-    if (a.norm_w) {
+    if (LAYER && a.norm_w) {
         // the decoder layer's RMSNorm of the token first (decode_kernel.c:224-230,
         // applied at :1549): x * (1 / sqrtf_fast(sum x^2 / d + eps)) * w
         float ss = 0.0f;
@@ -300,7 +303,9 @@ k_dispatch_work(RouteArgs a) {
 hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {
     if (a.B == 0) return hipSuccess;
     const dim3 grid((unsigned)((a.E + 7) / 8), (unsigned)a.B);
-#define JM_RT(GG, DVV, BF) hipLaunchKernelGGL((k_router_grp<GG, JM_NDIG, DVV, BF>), grid, dim3(64), 0, st, a)
+#define JM_RT(GG, DVV, BF)                                                                                 \
+    if (a.xpart || a.norm_w) hipLaunchKernelGGL((k_router_grp<GG, JM_NDIG, DVV, BF, true>), grid, dim3(64), 0, st, a); \
+    else hipLaunchKernelGGL((k_router_grp<GG, JM_NDIG, DVV, BF, false>), grid, dim3(64), 0, st, a)
 #define JM_RTB(GG, DVV) if (a.wt_bf16) { JM_RT(GG, DVV, true); } else { JM_RT(GG, DVV, false); }
 #define JM_RTD(GG) switch (a.d / 512) { case 1: JM_RTB(GG, 1); break; case 2: JM_RTB(GG, 2); break; \
         case 3: JM_RTB(GG, 3); break; case 4: JM_RTB(GG, 4); break; case 6: JM_RTB(GG, 6); break; \
