@@ -252,6 +252,32 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
     kv_bytes = n_layers * B * T * KH * hd * 2 * 2
     total = moe_bytes + attn_w + kv_bytes
     ok = bool(torch.isfinite(hid).all().item())
+    # the serve path: the same step ending in the lm_head (vocabulary 151936,
+    # bf16 N(0, 0.02)) and its argmax, tokens out
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7000)
+    lm = (torch.randn((shape.V, shape.d), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    dec.set_lm_head(lm)
+    del lm
+    tok = torch.empty(B, dtype=torch.int32, device="cuda")
+    for _ in range(warmup):
+        dec.decode_layers_batch_argmax(x, pos, kv, tok)
+    torch.cuda.synchronize()
+    e0.record(st)
+    for _ in range(steps):
+        dec.decode_layers_batch_argmax(x, pos, kv, tok)
+    e1.record(st)
+    torch.cuda.synchronize()
+    ms_lm = e0.elapsed_time(e1) / steps
+    # the lm_head + argmax alone, on the step's hidden state
+    n_lm = 20
+    e0.record(st)
+    for _ in range(n_lm):
+        dec.lm_head(hid, None, tok)
+    e1.record(st)
+    torch.cuda.synchronize()
+    lm_ms = e0.elapsed_time(e1) / n_lm
+    lm_bytes = shape.V * shape.d * 2
     res = {
         "tok_per_s": B / (ms * 1e-3), "ms_per_step": ms, "host_enqueue_ms_per_step": host_ms,
         "layers": n_layers, "batch": B, "position": position,
@@ -262,10 +288,18 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
         "bytes_alg": total, "bytes_moe": moe_bytes, "bytes_attn_weights": attn_w, "bytes_kv": kv_bytes,
         "GBs": total / (ms * 1e-3) / 1e9, "hbm_frac": total / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
         "hidden_finite": ok,
+        "with_lm_head_argmax": {
+            "tok_per_s": B / (ms_lm * 1e-3), "ms_per_step": ms_lm, "vocab": shape.V,
+            "lm_head_argmax_ms": lm_ms, "lm_head_bytes": lm_bytes,
+            "lm_head_GBs": lm_bytes / (lm_ms * 1e-3) / 1e9,
+            "bytes_alg": total + lm_bytes,
+            "GBs": (total + lm_bytes) / (ms_lm * 1e-3) / 1e9,
+        },
     }
     log(f"decode {n_layers} layers B={B}: {res['tok_per_s']:.0f} tok/s, {ms:.3f} ms/step "
         f"(host enqueue {host_ms:.3f} ms), attention {split['attention']:.3f} ms, MoE {split['moe']:.3f} ms, "
-        f"{res['GBs']:.0f} GB/s over {total / 1e9:.2f} GB")
+        f"{res['GBs']:.0f} GB/s over {total / 1e9:.2f} GB; with lm_head + argmax {B / (ms_lm * 1e-3):.0f} tok/s "
+        f"({ms_lm:.3f} ms/step; lm_head {lm_ms * 1e3:.1f} us, {lm_bytes / (lm_ms * 1e-3) / 1e9:.0f} GB/s)")
     store.close()
     del dec, weights, kv, store
     torch.cuda.empty_cache()

@@ -223,7 +223,7 @@ typedef struct jm_kernel_w {
  * (decode_kernel.c:1518-1556) over the store's layers: per layer RMSNorm,
  * attention (QKV, per-head QK-norm, RoPE, KV append at positions[b], SDPA,
  * o_proj) and residual, RMSNorm, the store's MoE block and residual; then
- * the final RMSNorm into hidden [B][d] float32.
+ * the final RMSNorm into hidden [B][d] float32, and the lm_head into logits.
  *   cfg        L, d, E, topk, intermediate, norm_topk_prob as the store's;
  *              n_heads, n_kv (n_heads / n_kv in 1, 2, 4, 8), hd = 128, eps,
  *              maxT, qk_norm_type (0 or 1), bias_qkv
@@ -231,13 +231,43 @@ typedef struct jm_kernel_w {
  *   positions  HOST int32 [B]: the cache row each token writes; attention
  *              covers rows 0 .. positions[b] (the others must be filled)
  *   xin        [B][d] float32 (device)
- *   logits     must be NULL: the lm_head is applied to hidden by the caller
+ *   logits     optional [B][V] float32 (device): lm_head(hidden), as
+ *              lm_head_B (:964-1000); needs jm_store_set_lm_head
+ *   hidden     optional [B][d] float32 (device): the final-normed state
  * Any B >= 0 (the reference clamps B to 16, decode_kernel.c:1522).  With
  * jm_store_profile on, jm_store_decode_ms splits the call's time.
  */
 int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* cfg, const jm_kernel_w* W, const jm_kv_cache* kv,
                            const int32_t* positions, const float* xin, int B, float* logits, float* hidden,
                            void* stream);
+
+/* decode_layers_batch_argmax (decode_kernel.c:1560-1590): the same step,
+ * then out_tok[b] = the row of the largest logit of token b, as lm_head_A
+ * (:1008-1062) picks it: a row wins only with a strictly larger value
+ * (initial -1e30 at row 0), so ties go to the lowest row and NaN never wins.
+ * out_tok is int32 [B] in DEVICE memory (the reference's is host memory);
+ * no [B][V] logits are written.  hidden is optional as above. */
+int jm_decode_layers_batch_argmax(jm_store* s, const jm_kernel_cfg* cfg, const jm_kernel_w* W, const jm_kv_cache* kv,
+                                  const int32_t* positions, const float* xin, int B, int32_t* out_tok,
+                                  float* hidden, void* stream);
+
+/* The lm_head, KernelW.lm_head (decode_kernel.c:291; float32 [V][d] in the
+ * reference, widened from the checkpoint's bf16 by decoder3.py:226-230).
+ * JM_DTYPE_F32 values must be exactly bf16 (an error otherwise);
+ * JM_DTYPE_BF16 is taken as is.  The store keeps a bf16 copy [V][d]; d must
+ * be 1024, 2048 or 4096.  Synchronises the device. */
+int jm_store_set_lm_head(jm_store* s, const void* lm_head, int dtype, int V);
+
+/* The store's lm_head on x [B][d] (device float32): logits [B][V] and/or
+ * out_tok [B] (the argmax of jm_decode_layers_batch_argmax); either may be
+ * NULL but not both.  The stage entry point of the decode's last step. */
+int jm_lm_head(jm_store* s, const float* x, int B, float* logits, int32_t* out_tok, void* stream);
+
+/* embed_lookup (decode_kernel.c:1597-1600) for B tokens: out[b][i] =
+ * bf16 embed[tokens[b]][i] (W->embed [V][d], device).  tokens is int32 [B]
+ * in DEVICE memory; a token outside [0, V) gives a row of NaN. */
+int jm_embed_lookup(const jm_kernel_w* W, const jm_kernel_cfg* cfg, const int32_t* tokens, int B, float* out,
+                    void* stream);
 
 /* With enable set, jm_decode_layers_batch records its launches once into a
  * HIP graph and replays it, re-recording when the arguments, the batch size

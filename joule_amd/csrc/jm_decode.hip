@@ -35,10 +35,10 @@ void free_decode(jm_store* s) {
     s->gexec = nullptr;
     if (s->dws) (void)hipFree(s->dws);
     s->dws = nullptr;
-    s->dec_B = s->dec_S = s->dec_nqkv = s->dec_hq = 0;
+    s->dec_B = s->dec_S = s->dec_nqkv = s->dec_hq = s->dec_V = 0;
 }
 
-int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq) {
+int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     const size_t tab_bytes = align256((size_t)B * s->L * 16 + (size_t)B * 4);
     if (tab_bytes > s->tab_cap) {
         if (s->tab_pending) JM_HIP(hipEventSynchronize(s->tab_ev), "hipEventSynchronize staging");
@@ -50,11 +50,12 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq) {
         s->dec_B = 0;   // the device table lives in the workspace: regrow it too
     }
     if (!s->tab_ev) JM_HIP(hipEventCreateWithFlags(&s->tab_ev, hipEventDisableTiming), "hipEventCreate");
-    if (B <= s->dec_B && S <= s->dec_S && nqkv <= s->dec_nqkv && hq <= s->dec_hq) return 0;
+    if (B <= s->dec_B && S <= s->dec_S && nqkv <= s->dec_nqkv && hq <= s->dec_hq && V <= s->dec_V) return 0;
     B = std::max(B, s->dec_B);
     S = std::max(S, s->dec_S);
     nqkv = std::max(nqkv, s->dec_nqkv);
     hq = std::max(hq, s->dec_hq);
+    V = std::max(V, s->dec_V);
     const int d = s->d;
     const size_t sz[] = {
         (size_t)B * d * 4,                        // h
@@ -65,6 +66,9 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq) {
         (size_t)B * S * (hq / HD) * 2 * 4,        // part_ml
         (size_t)B * hq * 4,                       // att
         (size_t)B * hq * 4,                       // qout
+        (size_t)B * d * 4,                        // hid
+        (size_t)jm::lm_blocks(V) * B * 4,         // lmv
+        (size_t)jm::lm_blocks(V) * B * 4,         // lmi
         s->tab_cap,                               // KV pointers + positions
     };
     size_t total = 0;
@@ -75,14 +79,15 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq) {
     JM_HIP(hipMalloc(&s->dws, total), "hipMalloc decode workspace");
     char* p = (char*)s->dws;
     void** slots[] = {(void**)&s->h, (void**)&s->h2, (void**)&s->qkv, (void**)&s->opart, (void**)&s->part_o,
-                      (void**)&s->part_ml, (void**)&s->att, (void**)&s->qout, (void**)&s->tab};
+                      (void**)&s->part_ml, (void**)&s->att, (void**)&s->qout, (void**)&s->hid, (void**)&s->lmv,
+                      (void**)&s->lmi, (void**)&s->tab};
     for (size_t i = 0; i < sizeof sz / sizeof sz[0]; i++) {
         *slots[i] = p;
         p += align256(sz[i]);
     }
     JM_HIP(hipMemset(s->dws, 0, total), "hipMemset decode workspace");
     JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize after decode workspace clear");
-    s->dec_B = B; s->dec_S = S; s->dec_nqkv = nqkv; s->dec_hq = hq;
+    s->dec_B = B; s->dec_S = S; s->dec_nqkv = nqkv; s->dec_hq = hq; s->dec_V = V;
     return 0;
 }
 
@@ -121,7 +126,7 @@ int check_decode_args(const jm_store* s, const jm_kernel_cfg* c, const jm_kernel
 
 // Every launch of one decode step on st (after the staging copy).
 int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const float* xin, int B,
-                 float* hidden, int S, int qpk, bool capturing, hipStream_t st) {
+                 float* hidden, float* logits, int* out_tok, int S, int qpk, bool capturing, hipStream_t st) {
     const int L = c->L, d = c->d, H = c->n_heads, KH = c->n_kv;
     const int nqkv = (H + 2 * KH) * HD;
     const int* pos_dev = (const int*)(s->tab + (size_t)2 * B * L);
@@ -183,6 +188,14 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
     }
     JM_DMARK(2 * L + 1);
     JM_HIP(jm::launch_rms_rows(s->h, W->final_norm, B, d, c->eps, hidden, st), "final norm launch");
+    if (logits || out_tok) {
+        jm::LmArgs la{};
+        la.w = s->lm; la.x = hidden; la.V = s->lm_V; la.d = d; la.B = B;
+        la.logits = logits;
+        la.best_v = out_tok ? s->lmv : nullptr;
+        la.best_i = s->lmi;
+        JM_HIP(jm::launch_lm_head(la, out_tok, st), "lm_head launch");
+    }
     JM_DMARK(2 * L + 2);
 #undef JM_DMARK
     return 0;
@@ -205,6 +218,8 @@ void decode_free_all(jm_store* s) {
         for (int i = 0; i < s->dprof_n; i++) (void)hipEventDestroy(s->dev_marks[i]);
         delete[] s->dev_marks;
     }
+    if (s->lm) (void)hipFree(s->lm);
+    s->lm = nullptr;
     s->tab_host = nullptr;
     s->tab_ev = nullptr;
     s->dev_marks = nullptr;
@@ -213,20 +228,25 @@ void decode_free_all(jm_store* s) {
 
 }  // namespace jm
 
-extern "C" {
+namespace {
 
-int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const jm_kv_cache* kv,
-                           const int32_t* positions, const float* xin, int B, float* logits, float* hidden,
-                           void* stream) {
+int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const jm_kv_cache* kv,
+                const int32_t* positions, const float* xin, int B, float* logits, int32_t* out_tok,
+                float* hidden, void* stream) {
     if (!s || !c) return fail(JM_ERR_ARG, "store and cfg must be non-NULL");
     if (!s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
     int qpk = 0;
     if (int rc = check_decode_args(s, c, W, &qpk)) return rc;
     if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
     if (B == 0) return 0;
-    if (!kv || !positions || !xin || !hidden) return fail(JM_ERR_ARG, "kv, positions, xin and hidden must be non-NULL");
-    if (logits) return fail(JM_ERR_ARG, "logits: the lm_head is not part of this call; pass NULL and apply it to hidden");
-    if (!aligned(xin, 16) || !aligned(hidden, 16)) return fail(JM_ERR_ARG, "xin and hidden must be 16-byte aligned");
+    if (!kv || !positions || !xin) return fail(JM_ERR_ARG, "kv, positions and xin must be non-NULL");
+    if (!aligned(xin, 16) || (hidden && !aligned(hidden, 16))) return fail(JM_ERR_ARG, "xin and hidden must be 16-byte aligned");
+    if (logits || out_tok) {
+        if (!s->lm) return fail(JM_ERR_ARG, "lm_head not set (jm_store_set_lm_head)");
+        if (s->lm_V != c->V) return fail(JM_ERR_SHAPE, "cfg V=%d differs from the lm_head's %d rows", c->V, s->lm_V);
+        if (!jm::lm_shape_ok(c->d)) return fail(JM_ERR_SHAPE, "the lm_head takes d = 1024, 2048 or 4096 (got %d)", c->d);
+        if (out_tok && !aligned(out_tok, 4)) return fail(JM_ERR_ARG, "out_tok must be 4-byte aligned");
+    }
     const int L = c->L, d = c->d, H = c->n_heads, KH = c->n_kv;
     int maxT = 0;
     for (int b = 0; b < B; b++) {
@@ -241,7 +261,8 @@ int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_
     const int S = (maxT + PSPLIT - 1) / PSPLIT;
     const int S_cap = (c->maxT + PSPLIT - 1) / PSPLIT;
     if (int rc = jm::store_reserve(s, B)) return rc;
-    if (int rc = decode_reserve(s, B, S_cap, nqkv, H * HD)) return rc;
+    if (int rc = decode_reserve(s, B, S_cap, nqkv, H * HD, (logits || out_tok) ? c->V : 0)) return rc;
+    if (!hidden) hidden = s->hid;
     hipStream_t st = (hipStream_t)stream;
     JM_HIP(hipSetDevice(s->device), "hipSetDevice");
 
@@ -280,7 +301,8 @@ int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_
         memset(&key, 0, sizeof key);
         memcpy(&key.cfg, c, sizeof *c);
         memcpy(&key.W, W, sizeof *W);
-        key.xin = xin; key.hidden = hidden; key.B = B; key.S = S;
+        key.xin = xin; key.hidden = hidden; key.logits = logits; key.out_tok = out_tok; key.lm = s->lm;
+        key.B = B; key.S = S;
         key.trace = s->trace; key.trace_bytes = s->trace_bytes; key.ws = s->ws; key.dws = s->dws;
         key.wt = s->wt; key.dense_min = s->dense_min;
         if (!s->gexec || memcmp(&key, &s->gkey, sizeof key) != 0) {
@@ -291,7 +313,7 @@ int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_
             }
             if (!s->cap_st) JM_HIP(hipStreamCreateWithFlags(&s->cap_st, hipStreamNonBlocking), "hipStreamCreate");
             JM_HIP(hipStreamBeginCapture(s->cap_st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-            const int rc = enqueue_step(s, c, W, xin, B, hidden, S, qpk, true, s->cap_st);
+            const int rc = enqueue_step(s, c, W, xin, B, hidden, logits, out_tok, S, qpk, true, s->cap_st);
             hipGraph_t graph = nullptr;
             const hipError_t ec = hipStreamEndCapture(s->cap_st, &graph);
             if (rc) {
@@ -310,7 +332,91 @@ int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_
         JM_HIP(hipGraphLaunch(s->gexec, st), "hipGraphLaunch");
         return 0;
     }
-    return enqueue_step(s, c, W, xin, B, hidden, S, qpk, false, st);
+    return enqueue_step(s, c, W, xin, B, hidden, logits, out_tok, S, qpk, false, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int jm_decode_layers_batch(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const jm_kv_cache* kv,
+                           const int32_t* positions, const float* xin, int B, float* logits, float* hidden,
+                           void* stream) {
+    return decode_impl(s, c, W, kv, positions, xin, B, logits, nullptr, hidden, stream);
+}
+
+int jm_decode_layers_batch_argmax(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const jm_kv_cache* kv,
+                                  const int32_t* positions, const float* xin, int B, int32_t* out_tok,
+                                  float* hidden, void* stream) {
+    if (!out_tok && B > 0) return fail(JM_ERR_ARG, "out_tok must be non-NULL");
+    return decode_impl(s, c, W, kv, positions, xin, B, nullptr, out_tok, hidden, stream);
+}
+
+int jm_store_set_lm_head(jm_store* s, const void* w, int dtype, int V) {
+    if (!s) return fail(JM_ERR_ARG, "store is NULL");
+    if (!w) return fail(JM_ERR_ARG, "lm_head is NULL");
+    if (V <= 0) return fail(JM_ERR_SHAPE, "V must be positive");
+    if (dtype != JM_DTYPE_F32 && dtype != JM_DTYPE_BF16) return fail(JM_ERR_ARG, "lm_head dtype must be f32 or bf16");
+    if (!aligned(w, 4)) return fail(JM_ERR_ARG, "lm_head must be 4-byte aligned");
+    if (!jm::lm_shape_ok(s->d)) return fail(JM_ERR_SHAPE, "the lm_head takes d = 1024, 2048 or 4096 (got %d)", s->d);
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    const long long n = (long long)V * s->d;
+    if (dtype == JM_DTYPE_F32) {
+        // the reference's lm_head is float32 widened from the checkpoint's
+        // bf16 (decoder3.py:226-230): keep it as bf16 when it is exactly that
+        unsigned* flag = nullptr;
+        JM_HIP(hipMalloc(&flag, sizeof(unsigned)), "hipMalloc flag");
+        unsigned h = 0;
+        hipError_t e = hipMemset(flag, 0, sizeof(unsigned));
+        if (e == hipSuccess) e = jm::launch_bf16_exact((const float*)w, n, flag, nullptr);
+        if (e == hipSuccess) e = hipMemcpy(&h, flag, sizeof(unsigned), hipMemcpyDeviceToHost);
+        (void)hipFree(flag);
+        if (e != hipSuccess) return hip_fail(e, "lm_head bf16 check");
+        if (h) return fail(JM_ERR_ARG, "lm_head values must be bf16-representable (float32 widened from bf16)");
+    }
+    JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    if (s->lm && s->lm_V != V) {
+        (void)hipFree(s->lm);
+        s->lm = nullptr;
+    }
+    if (!s->lm) JM_HIP(hipMalloc((void**)&s->lm, (size_t)n * 2), "hipMalloc lm_head copy");
+    s->lm_V = V;
+    if (dtype == JM_DTYPE_BF16)
+        JM_HIP(hipMemcpy(s->lm, w, (size_t)n * 2, hipMemcpyDeviceToDevice), "lm_head copy");
+    else
+        JM_HIP(jm::launch_f32_bf16_bits((const float*)w, n, s->lm, nullptr), "lm_head conversion");
+    JM_HIP(hipDeviceSynchronize(), "lm_head copy");
+    return 0;
+}
+
+int jm_lm_head(jm_store* s, const float* x, int B, float* logits, int32_t* out_tok, void* stream) {
+    if (!s) return fail(JM_ERR_ARG, "store is NULL");
+    if (!s->lm) return fail(JM_ERR_ARG, "lm_head not set (jm_store_set_lm_head)");
+    if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
+    if (B == 0) return 0;
+    if (!x || (!logits && !out_tok)) return fail(JM_ERR_ARG, "x and one of logits, out_tok must be non-NULL");
+    if (!aligned(x, 16)) return fail(JM_ERR_ARG, "x must be 16-byte aligned");
+    if (int rc = decode_reserve(s, B, std::max(s->dec_S, 1), std::max(s->dec_nqkv, 512), std::max(s->dec_hq, 512), s->lm_V))
+        return rc;
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    jm::LmArgs la{};
+    la.w = s->lm; la.x = x; la.V = s->lm_V; la.d = s->d; la.B = B;
+    la.logits = logits;
+    la.best_v = out_tok ? s->lmv : nullptr;
+    la.best_i = s->lmi;
+    JM_HIP(jm::launch_lm_head(la, out_tok, (hipStream_t)stream), "lm_head launch");
+    return 0;
+}
+
+int jm_embed_lookup(const jm_kernel_w* W, const jm_kernel_cfg* c, const int32_t* tokens, int B, float* out,
+                    void* stream) {
+    if (!W || !c || !W->embed) return fail(JM_ERR_ARG, "weights, cfg and embed must be non-NULL");
+    if (c->V <= 0 || c->d <= 0) return fail(JM_ERR_SHAPE, "cfg V and d must be positive");
+    if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
+    if (B == 0) return 0;
+    if (!tokens || !out) return fail(JM_ERR_ARG, "tokens and out must be non-NULL");
+    JM_HIP(jm::launch_embed(W->embed, c->V, c->d, tokens, B, out, (hipStream_t)stream), "embedding launch");
+    return 0;
 }
 
 int jm_store_decode_graph(jm_store* s, int enable) {

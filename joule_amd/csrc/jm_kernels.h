@@ -182,6 +182,23 @@ struct AttnArgs {
 // the projections finished (q out, k and v appended), partial attention,
 // then the merge into att [B][H*128]
 hipError_t launch_attn(const AttnArgs& a, int qpk, float* att, hipStream_t st);
+// lm_head: logits[b][v] = w[v] . x[b] (bf16 rows of d columns), with the
+// per-block best row of each token for the argmax.
+struct LmArgs {
+    const uint16_t* w;        // [V][d] bf16
+    const float* x;           // [B][d]
+    int V, d, B;
+    float* logits;            // [B][V] or NULL
+    float* best_v;            // [lm_blocks(V)][B] or NULL (no argmax)
+    int* best_i;
+};
+int lm_blocks(int V);
+bool lm_shape_ok(int d);      // d in {1024, 2048, 4096}
+// the lm_head, then (out_tok non-NULL) the argmax merge into out_tok [B]
+hipError_t launch_lm_head(const LmArgs& a, int* out_tok, hipStream_t st);
+hipError_t launch_embed(const uint16_t* embed, int V, int d, const int* tokens, int B, float* out,
+                        hipStream_t st);
+hipError_t launch_f32_bf16_bits(const float* in, long long n, uint16_t* out, hipStream_t st);
 hipError_t launch_rms_rows(const float* x, const uint16_t* w, int B, int d, float eps, float* out,
                            hipStream_t st);
 

@@ -16,6 +16,9 @@ struct DecKey {
     jm_kernel_w W;
     const float* xin;
     float* hidden;
+    float* logits;
+    int* out_tok;
+    const void* lm;
     int B, S;
     int32_t* trace;
     uint64_t trace_bytes;
@@ -69,7 +72,9 @@ struct jm_store {
     _Float16* xsl;
     int dense_min;              // segment size from which an expert takes the MFMA branch
     // ---- batch decode (jm_decode_layers_batch) ----
-    int dec_B, dec_S, dec_nqkv, dec_hq;   // sizes the decode workspace holds
+    int dec_B, dec_S, dec_nqkv, dec_hq, dec_V;   // sizes the decode workspace holds
+    uint16_t* lm;               // [V][d] bf16 copy of the lm_head (jm_store_set_lm_head)
+    int lm_V;
     void* dws;                  // decode workspace
     float* h;                   // [B][d] residual stream
     float* h2;                  // [B][d] residual stream after attention
@@ -79,6 +84,9 @@ struct jm_store {
     float* part_ml;             // [B][KH][S][H/KH][2] their (max, sum)
     float* att;                 // [B][H hd] attention output
     float* qout;                // [B][H hd] finished query heads
+    float* hid;                 // [B][d] final-normed hidden state (when the caller passes none)
+    float* lmv;                 // [lm blocks][B] per-block best logit (argmax)
+    int* lmi;                   // [lm blocks][B] its row
     unsigned long long* tab;    // [B*L][2] KV pointers, then [B] positions (device)
     unsigned long long* tab_host;   // pinned staging of tab
     size_t tab_cap;             // bytes of tab / tab_host

@@ -68,6 +68,7 @@ class DecoderShape:
     maxT: int = 4096
     qk_norm_type: int = 1        # 1: per-head RMSNorm on q and k (Qwen3)
     bias_qkv: bool = False
+    V: int = 0                   # vocabulary (embedding / lm_head rows); 0: none
     name: str = ""
 
     @property
@@ -79,15 +80,17 @@ class DecoderShape:
         c.n_heads, c.n_kv, c.hd = self.n_heads, self.n_kv, self.hd
         c.eps, c.maxT = float(self.eps), int(self.maxT)
         c.qk_norm_type, c.bias_qkv = int(self.qk_norm_type), int(bool(self.bias_qkv))
+        c.V = int(self.V)
         return c
 
 
-def qwen3_30b_a3b(n_layers: int = 48, maxT: int = 4096) -> DecoderShape:
+def qwen3_30b_a3b(n_layers: int = 48, maxT: int = 4096, V: int = 151936) -> DecoderShape:
     """Qwen3-30B-A3B: 48 layers, d 2048, GQA 32 / 4 heads of 128, per-head
-    QK-norm, RoPE theta 1e6, eps 1e-6, and the Qwen3 MoE block."""
+    QK-norm, RoPE theta 1e6, eps 1e-6, vocabulary 151936, and the Qwen3 MoE
+    block."""
     from .moe import QWEN3
     return DecoderShape(n_layers=n_layers, moe=QWEN3, n_heads=32, n_kv=4, hd=128, eps=1e-6,
-                        theta=1e6, maxT=maxT, qk_norm_type=1, name="qwen3-30b-a3b")
+                        theta=1e6, maxT=maxT, qk_norm_type=1, V=V, name="qwen3-30b-a3b")
 
 
 def rope_tables(maxT: int, hd: int, theta: float) -> tuple[np.ndarray, np.ndarray]:
@@ -112,8 +115,9 @@ class DecoderWeights:
 
     bf16 tensors: norm1/norm2 [L, d], final_norm [d], wq [L, H*hd, d],
     wk/wv [L, KH*hd, d], wo [L, d, H*hd], qn/kn [L, hd]; float32 biases
-    bq [L, H*hd], bk/bv [L, KH*hd] when the shape has bias_qkv.  The rope
-    tables are built from the shape.
+    bq [L, H*hd], bk/bv [L, KH*hd] when the shape has bias_qkv; optional
+    embed [V, d] (bf16).  The rope tables are built from the shape.  The
+    lm_head goes to the store (HipDecoder.set_lm_head).
     """
 
     def __init__(self, shape: DecoderShape, device="cuda", **t: torch.Tensor):
@@ -131,6 +135,8 @@ class DecoderWeights:
         if shape.bias_qkv:
             for k, shp in (("bq", (L, H * hd)), ("bk", (L, KH * hd)), ("bv", (L, KH * hd))):
                 self.t[k] = t[k].to(device=device, dtype=torch.float32).contiguous()
+        if "embed" in t:
+            self.t["embed"] = _bf16_dev(t["embed"], (shape.V, d), "embed", device)
         cos, sin = rope_tables(shape.maxT, hd, shape.theta)
         self.t["cos"] = torch.from_numpy(cos).to(device)
         self.t["sin"] = torch.from_numpy(sin).to(device)
@@ -185,25 +191,96 @@ class HipDecoder:
         _lib.check(_lib.lib().jm_store_decode_graph(self.store._h, int(bool(enable))), "jm_store_decode_graph")
 
     def decode_layers_batch(self, x: torch.Tensor, positions, kv: KVCacheSet,
-                            hidden: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+                            hidden: torch.Tensor | None = None, logits: torch.Tensor | None = None,
+                            stream=None) -> torch.Tensor:
         """hidden [B, d] = final RMSNorm of the residual stream after every
-        layer, for tokens x [B, d] (float32) writing cache rows positions[b]."""
+        layer, for tokens x [B, d] (float32) writing cache rows positions[b];
+        with logits [B, V] (float32, CUDA) also the lm_head of it."""
         if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or x.dim() != 2:
             raise ValueError("x must be a contiguous float32 CUDA tensor [B, d]")
         B = x.shape[0]
-        if kv.B < B:
-            raise ValueError(f"cache set holds {kv.B} sequences, batch has {B}")
+        pos = self._positions(positions, B)
+        if hidden is None:
+            hidden = torch.empty_like(x)
+        if logits is not None and (logits.dtype != torch.float32 or tuple(logits.shape) != (B, self.shape.V)
+                                   or not logits.is_contiguous()):
+            raise ValueError(f"logits must be a contiguous float32 tensor [{B}, {self.shape.V}]")
+        _lib.check(_lib.lib().jm_decode_layers_batch(
+            self.store._h, ctypes.byref(self._cfg), ctypes.byref(self._w), self._table(kv, B),
+            pos.ctypes.data_as(ctypes.c_void_p), _lib.ptr(x), B, _lib.ptr(logits), _lib.ptr(hidden),
+            _lib.stream_handle(stream)), "jm_decode_layers_batch")
+        return hidden
+
+    def lm_head(self, x: torch.Tensor, logits: torch.Tensor | None = None,
+                out_tok: torch.Tensor | None = None, stream=None):
+        """The store's lm_head on x [B, d]: (logits [B, V], out_tok [B])."""
+        B = x.shape[0]
+        _lib.check(_lib.lib().jm_lm_head(self.store._h, _lib.ptr(x), B, _lib.ptr(logits), _lib.ptr(out_tok),
+                                         _lib.stream_handle(stream)), "jm_lm_head")
+        return logits, out_tok
+
+    def set_lm_head(self, lm_head: torch.Tensor) -> None:
+        """The lm_head [V, d]: bfloat16, or float32 holding bf16 values (as
+        the reference widens it); the store keeps a bf16 copy."""
+        V, d = self.shape.V, self.shape.d
+        if tuple(lm_head.shape) != (V, d) or not lm_head.is_cuda or not lm_head.is_contiguous():
+            raise ValueError(f"lm_head must be a contiguous CUDA tensor [{V}, {d}]")
+        if lm_head.dtype == torch.bfloat16:
+            dt = _lib.JM_DTYPE_BF16
+        elif lm_head.dtype == torch.float32:
+            dt = _lib.JM_DTYPE_F32
+        else:
+            raise ValueError("lm_head dtype must be bfloat16 or float32")
+        _lib.check(_lib.lib().jm_store_set_lm_head(self.store._h, _lib.ptr(lm_head), dt, V), "jm_store_set_lm_head")
+
+    def _positions(self, positions, B):
         pos = np.ascontiguousarray(np.asarray(positions, dtype=np.int32).reshape(-1))
         if pos.size != B:
             raise ValueError("one position per token")
-        if hidden is None:
-            hidden = torch.empty_like(x)
+        return pos
+
+    def _table(self, kv: KVCacheSet, B: int):
+        if kv.B < B:
+            raise ValueError(f"cache set holds {kv.B} sequences, batch has {B}")
         table = kv.table if kv.B == B else (KVCache * (B * self.shape.n_layers)).from_buffer(kv.table)
-        _lib.check(_lib.lib().jm_decode_layers_batch(
-            self.store._h, ctypes.byref(self._cfg), ctypes.byref(self._w), ctypes.cast(table, _vp),
-            pos.ctypes.data_as(ctypes.c_void_p), _lib.ptr(x), B, None, _lib.ptr(hidden),
-            _lib.stream_handle(stream)), "jm_decode_layers_batch")
-        return hidden
+        return ctypes.cast(table, _vp)
+
+    def decode_layers_batch_argmax(self, x: torch.Tensor, positions, kv: KVCacheSet,
+                                   out_tok: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """out_tok [B] (int32, CUDA): the argmax token of every sequence, as
+        decode_layers_batch_argmax (decode_kernel.c:1560-1590)."""
+        if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or x.dim() != 2:
+            raise ValueError("x must be a contiguous float32 CUDA tensor [B, d]")
+        B = x.shape[0]
+        pos = self._positions(positions, B)
+        if out_tok is None:
+            out_tok = torch.empty(B, dtype=torch.int32, device=x.device)
+        _lib.check(_lib.lib().jm_decode_layers_batch_argmax(
+            self.store._h, ctypes.byref(self._cfg), ctypes.byref(self._w), self._table(kv, B),
+            pos.ctypes.data_as(ctypes.c_void_p), _lib.ptr(x), B, _lib.ptr(out_tok), None,
+            _lib.stream_handle(stream)), "jm_decode_layers_batch_argmax")
+        return out_tok
+
+    def embed(self, tokens: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """out [B, d] float32 = bf16 embedding rows of tokens [B] (int32, CUDA),
+        as embed_lookup (decode_kernel.c:1597-1600)."""
+        if tokens.dtype != torch.int32 or not tokens.is_cuda or not tokens.is_contiguous():
+            raise ValueError("tokens must be a contiguous int32 CUDA tensor")
+        B = tokens.numel()
+        if out is None:
+            out = torch.empty((B, self.shape.d), dtype=torch.float32, device=tokens.device)
+        _lib.check(_lib.lib().jm_embed_lookup(ctypes.byref(self._w), ctypes.byref(self._cfg), _lib.ptr(tokens), B,
+                                              _lib.ptr(out), _lib.stream_handle(stream)), "jm_embed_lookup")
+        return out
+
+    def decode_batch_argmax(self, tokens, positions, kv: KVCacheSet) -> list[int]:
+        """NativeDecoder.decode_batch_argmax (decoder3.py:607-629): embed the
+        tokens, run every layer, return the argmax next token per sequence."""
+        dev = self.store.blob.device
+        tok = torch.as_tensor(np.asarray(tokens, dtype=np.int32), device=dev)
+        x = self.embed(tok)
+        out = self.decode_layers_batch_argmax(x, positions, kv)
+        return [int(v) for v in out.cpu().tolist()]
 
     def trace_topk(self, buf: torch.Tensor | None) -> None:
         """Copy each layer's selected experts into buf [L, B, topk] (int32,

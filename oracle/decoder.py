@@ -16,6 +16,11 @@ Follows src/jouleai/native/decode_kernel.c:
   decode_layers_batch   :1518-1556  norm1 -> attention -> residual -> norm2
                           -> MoE (OracleMoE, the C restatement of
                           layer_ffn_batch) -> residual; final norm
+  lm_head_B             :964-1000  logits = lm_head . x (float64 dot, rounded)
+  lm_head_A             :1008-1062  argmax: per-worker strict-> scans from
+                          (-1e30, row 0) over contiguous row ranges, merged
+                          in worker order with strict >
+  embed_lookup          :1597-1600  bf16 embedding row
 
 Two deliberate differences from the reference, both matching the GPU path:
 the KV cache holds bfloat16 values (the reference's is float32,
@@ -146,3 +151,29 @@ class OracleDecoder:
             out, _, _ = self.moe[l].forward(t)
             h = (h + out).astype(F32)
         return rms_norm(h, w["final_norm"], self.eps)
+
+
+def lm_head(W: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """logits [B, V] of rows W [V, d] (float32 holding bf16 values)."""
+    return matvec(W, x)
+
+
+def argmax_strict(logits: np.ndarray) -> np.ndarray:
+    """Per row of logits [B, V]: the row lm_head_A picks.  Its answer is the
+    first index of the largest value above -1e30 (NaN excluded), or 0 when no
+    value exceeds -1e30; the worker split of the scan does not change it
+    (its merge is in worker order with strict >)."""
+    lg = np.asarray(logits, np.float32)
+    out = np.zeros(lg.shape[0], np.int64)
+    for b in range(lg.shape[0]):
+        v = lg[b]
+        ok = (v > np.float32(-1e30)) & ~np.isnan(v)
+        if ok.any():
+            m = v[ok].max()
+            out[b] = int(np.flatnonzero(ok & (v == m))[0])
+    return out
+
+
+def embed_lookup(E: np.ndarray, tokens) -> np.ndarray:
+    """Rows of the embedding E [V, d] (float32 holding bf16 values)."""
+    return np.asarray(E, np.float32)[np.asarray(tokens, np.int64)].copy()

@@ -172,3 +172,97 @@ def test_decode_graph_replays_match_eager():
             assert torch.equal(again, want)
             dec.set_graph(True)
     dec.store.close()
+
+
+def _lm_model(V=5003, d=2048, seed=21):
+    """A one-layer Qwen3-shaped decoder with a vocabulary of V rows: embedding
+    and lm_head bf16 N(0, 0.02)."""
+    shape = DecoderShape(n_layers=1, moe=MoEShape(d=d, m=768, E=128, topk=8, renorm=True),
+                         n_heads=16, n_kv=4, maxT=300, V=V)
+    dec, oracle, kv = _model(shape, 64, 8)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    lm = (torch.randn((V, d), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    emb = (torch.randn((V, d), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    return shape, dec, oracle, kv, lm, emb
+
+
+@pytest.mark.parametrize("B", [1, 3, 8])
+def test_lm_head_logits_and_argmax(B):
+    """jm_lm_head against float64 logits of the same bf16 rows (1e-5), and its
+    argmax against lm_head_A's choice on the GPU's own logits (exact):
+    duplicated rows tie and the lower one wins, NaN rows never win."""
+    shape, dec, _, _, lm, _ = _lm_model()
+    V, d = shape.V, shape.d
+    lm = lm.clone()
+    lm[4000] = lm[17] = lm[17] * 0                  # two identical rows ...
+    lm[17, :8] = 1.0                                # ... made the largest for token 0
+    lm[4000] = lm[17]
+    lm[100] = float("nan")                          # a NaN row: NaN logits never win
+    dec.set_lm_head(lm.float())                     # float32 holding bf16 values, as the reference's
+    x = torch.from_numpy(activations(B, d)).cuda()
+    x[0, :8] = 5.0
+    logits = torch.empty((B, V), dtype=torch.float32, device="cuda")
+    tok = torch.empty(B, dtype=torch.int32, device="cuda")
+    print(f"[lm_head] B={B} V={V}", flush=True)
+    dec.lm_head(x, logits, tok)
+    torch.cuda.synchronize()
+    got = logits.cpu().numpy()
+    want = (x.double() @ lm.double().T).cpu().numpy()
+    ok = ~np.isnan(want)
+    assert np.isnan(got[:, 100]).all() and np.array_equal(np.isnan(got), ~ok)
+    rel = np.abs(got - want)[ok].max() / np.abs(want[ok]).max()
+    assert rel < 1e-5, rel
+    t = tok.cpu().numpy()
+    assert np.array_equal(t, D.argmax_strict(got))
+    assert t[0] == 17 and got[0, 17] == got[0, 4000]
+    # argmax alone (no logits) gives the same rows
+    tok2 = torch.full((B,), -1, dtype=torch.int32, device="cuda")
+    dec.lm_head(x, None, tok2)
+    assert torch.equal(tok, tok2)
+    dec.store.close()
+
+
+def test_decode_argmax_and_embedding():
+    """Tokens in, tokens out: embedding rows, one decode step with the
+    lm_head, the argmax decode, against the oracle (logits within 1e-3; the
+    argmax equal wherever the oracle's top two logits are apart by more than
+    the tolerance), and a second step that reads the appended rows."""
+    shape, dec, oracle, kv, lm, emb = _lm_model()
+    t = dict(dec.weights.t)
+    dec.weights.t["embed"] = emb
+    dec._w = dec.weights.kernel_w()
+    dec.set_lm_head(lm)
+    V, B = shape.V, 8
+    kv_h = _kv_host(kv, B, shape.n_layers)
+    E = emb.float().cpu().numpy()
+    W = lm.float().cpu().numpy()
+    tokens = np.array([0, 1, 17, 4095, 5002, 777, 3, 2500], np.int32)
+    pos = [0, 5, 130, 200, 250, 299, 128, 127]
+    for step in range(2):
+        print(f"[decode argmax] step {step} tokens {tokens.tolist()}", flush=True)
+        x = dec.embed(torch.from_numpy(tokens).cuda())
+        torch.cuda.synchronize()
+        xh = D.embed_lookup(E, tokens)
+        assert np.array_equal(x.cpu().numpy(), xh)
+        got_tok = dec.decode_layers_batch_argmax(x, pos, kv).cpu().numpy()
+        # the same step again with logits (the cache rows are rewritten with the same values)
+        logits = torch.empty((B, V), dtype=torch.float32, device="cuda")
+        dec.decode_layers_batch(x, pos, kv, logits=logits)
+        torch.cuda.synchronize()
+        gl = logits.cpu().numpy()
+        assert np.array_equal(got_tok, D.argmax_strict(gl))
+        hid = oracle.decode_layers_batch(xh, pos, kv_h)
+        wl = D.lm_head(W, hid)
+        rel = np.abs(gl - wl).max(axis=1) / np.abs(wl).max(axis=1)
+        assert rel.max() < TOL, rel
+        want_tok = D.argmax_strict(wl)
+        top2 = np.sort(wl, axis=1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > TOL * np.abs(top2[:, 1])
+        assert np.array_equal(got_tok[clear], want_tok[clear])
+        tokens = got_tok.astype(np.int32)
+        pos = [p + 1 if p + 1 < shape.maxT else p for p in pos]
+    # a token outside the vocabulary embeds as NaN
+    bad = dec.embed(torch.tensor([V, -1, 5], dtype=torch.int32, device="cuda")).cpu().numpy()
+    assert np.isnan(bad[:2]).all() and np.array_equal(bad[2], E[5])
+    dec.store.close()

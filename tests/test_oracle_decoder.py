@@ -217,3 +217,44 @@ def test_gqa_head_mapping():
         assert np.all(seg > 0) and np.all(seg < kh + 1.0 + 1e-6)
         assert np.all(np.abs(seg - seg[0]) < 1e-6)
     assert o[:hd].max() < o[2 * hd:3 * hd].min()  # heads 0-1 read KV head 0, heads 2-3 KV head 1
+
+
+def _lm_head_A_scan(logits, n_workers):
+    """The reference's argmax (decode_kernel.c:1008-1062) step by step:
+    participants take contiguous row ranges span*id/np, each keeps its best
+    from (-1e30, 0) with strict >, and the merge walks them in order with
+    strict >."""
+    V = len(logits)
+    bv, bi = np.float32(-1e30), 0
+    for w in range(n_workers):
+        lo, hi = V * w // n_workers, V * (w + 1) // n_workers
+        ov, oi = np.float32(-1e30), 0
+        for i in range(lo, hi):
+            if logits[i] > ov:
+                ov, oi = logits[i], i
+        if ov > bv:
+            bv, bi = ov, oi
+    return bi
+
+
+def test_argmax_strict_matches_the_reference_scan():
+    rng = np.random.default_rng(11)
+    cases = []
+    for _ in range(20):
+        v = rng.standard_normal(997).astype(np.float32)
+        top = v.max()
+        for j in rng.choice(997, size=3, replace=False):   # planted ties at the max
+            v[j] = top
+        cases.append(v)
+    v = rng.standard_normal(500).astype(np.float32)
+    v[[3, 400]] = np.nan
+    v[250] = 9.0
+    v[499] = 9.0
+    cases.append(v)                                          # NaN never wins, the lower 9.0 does
+    cases.append(np.full(64, -1e30, np.float32))             # nothing beats -1e30: row 0
+    cases.append(np.concatenate([np.full(10, np.nan, np.float32), np.full(5, -2e30, np.float32)]))
+    cases.append(np.array([-1e30, -1e30, -0.5, -0.5], np.float32))
+    for v in cases:
+        want = [_lm_head_A_scan(v, n) for n in (1, 3, 9, 17)]
+        assert len(set(want)) == 1                               # the worker split does not matter
+        assert D.argmax_strict(v[None])[0] == want[0]
