@@ -1,0 +1,96 @@
+"""A Qwen3-MoE checkpoint (config.json + safetensors, written here at a small
+size) loaded into the GPU decoder and decoded token by token, against the
+oracle built from the same tensors and the converted store."""
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from joule_amd.checkpoint import HipNativeDecoder
+from joule_amd.decoder import rope_tables
+from joule_amd.q4_store import BIN_NAME, INDEX_NAME, Q4Index
+from oracle import decoder as D
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+CFG = {"model_type": "qwen3_moe", "num_hidden_layers": 2, "hidden_size": 1024, "num_attention_heads": 8,
+       "num_key_value_heads": 2, "head_dim": 128, "num_experts": 16, "num_experts_per_tok": 4,
+       "moe_intermediate_size": 256, "vocab_size": 1000, "rope_theta": 1000000.0, "rms_norm_eps": 1e-06,
+       "norm_topk_prob": True, "tie_word_embeddings": False}
+
+
+def _write_checkpoint(path):
+    from safetensors.torch import save_file
+
+    g = torch.Generator().manual_seed(31)
+    c = CFG
+    L, d, H, KH, hd, E, m, V = (c["num_hidden_layers"], c["hidden_size"], c["num_attention_heads"],
+                                c["num_key_value_heads"], c["head_dim"], c["num_experts"],
+                                c["moe_intermediate_size"], c["vocab_size"])
+    r = lambda *s, std=0.02: (torch.randn(s, generator=g) * std).to(torch.bfloat16)
+    nw = lambda *s: (1.0 + 0.1 * torch.randn(s, generator=g)).to(torch.bfloat16)
+    t = {"model.embed_tokens.weight": r(V, d, std=0.5), "lm_head.weight": r(V, d), "model.norm.weight": nw(d)}
+    for l in range(L):
+        p = f"model.layers.{l}"
+        t.update({f"{p}.input_layernorm.weight": nw(d), f"{p}.post_attention_layernorm.weight": nw(d),
+                  f"{p}.self_attn.q_proj.weight": r(H * hd, d), f"{p}.self_attn.k_proj.weight": r(KH * hd, d),
+                  f"{p}.self_attn.v_proj.weight": r(KH * hd, d), f"{p}.self_attn.o_proj.weight": r(d, H * hd),
+                  f"{p}.self_attn.q_norm.weight": nw(hd), f"{p}.self_attn.k_norm.weight": nw(hd),
+                  f"{p}.mlp.gate.weight": r(E, d)})
+        for e in range(E):
+            t[f"{p}.mlp.experts.{e}.gate_proj.weight"] = r(m, d)
+            t[f"{p}.mlp.experts.{e}.up_proj.weight"] = r(m, d)
+            t[f"{p}.mlp.experts.{e}.down_proj.weight"] = r(d, m)
+    path.mkdir(parents=True, exist_ok=True)
+    save_file(t, str(path / "model.safetensors"))
+    (path / "config.json").write_text(json.dumps(CFG))
+    return {k: v.float().numpy() for k, v in t.items()}
+
+
+def test_checkpoint_decode_matches_oracle(tmp_path):
+    model = tmp_path / "qwen3-moe-tiny"
+    T = _write_checkpoint(model)
+    print("[checkpoint] loading", flush=True)
+    nd = HipNativeDecoder(model, max_tokens=64, max_batch=4)
+    c = CFG
+    L, d, H, KH, hd, E, k = (c["num_hidden_layers"], c["hidden_size"], c["num_attention_heads"],
+                             c["num_key_value_heads"], c["head_dim"], c["num_experts"], c["num_experts_per_tok"])
+    lay = [f"model.layers.{l}" for l in range(L)]
+    w = {"norm1": np.stack([T[f"{p}.input_layernorm.weight"] for p in lay]),
+         "norm2": np.stack([T[f"{p}.post_attention_layernorm.weight"] for p in lay]),
+         "final_norm": T["model.norm.weight"],
+         "wq": np.stack([T[f"{p}.self_attn.q_proj.weight"] for p in lay]),
+         "wk": np.stack([T[f"{p}.self_attn.k_proj.weight"] for p in lay]),
+         "wv": np.stack([T[f"{p}.self_attn.v_proj.weight"] for p in lay]),
+         "wo": np.stack([T[f"{p}.self_attn.o_proj.weight"] for p in lay]),
+         "qn": np.stack([T[f"{p}.self_attn.q_norm.weight"] for p in lay]),
+         "kn": np.stack([T[f"{p}.self_attn.k_norm.weight"] for p in lay])}
+    w["cos"], w["sin"] = rope_tables(64, hd, c["rope_theta"])
+    conv = model / "joule_q4"
+    blob = np.fromfile(conv / BIN_NAME, dtype=np.uint8)
+    offsets = Q4Index.load(conv / INDEX_NAME).offset_table(L, E)
+    moe = [O.OracleMoE(d, c["moe_intermediate_size"], E, k, True, 64, T[f"{p}.mlp.gate.weight"], blob,
+                       offsets[:, l * E:(l + 1) * E]) for l, p in enumerate(lay)]
+    oracle = D.OracleDecoder(L, d, H, KH, hd, c["rms_norm_eps"], 1, False, w, moe)
+    kv = [[(np.zeros((64, KH, hd), np.float32), np.zeros((64, KH, hd), np.float32)) for _ in range(L)]
+          for _ in range(4)]
+    tokens, pos = [5, 999, 0, 123], [0, 0, 0, 0]
+    for step in range(4):
+        print(f"[checkpoint] step {step} tokens {tokens}", flush=True)
+        got = nd.decode_batch_argmax(tokens, pos)
+        x = D.embed_lookup(T["model.embed_tokens.weight"], tokens)
+        lg = D.lm_head(T["lm_head.weight"], oracle.decode_layers_batch(x, pos, kv))
+        want = D.argmax_strict(lg)
+        top2 = np.sort(lg, axis=1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 1e-3 * np.abs(top2[:, 1])
+        assert np.array_equal(np.asarray(got)[clear], want[clear]), (got, want)
+        tokens = [int(v) for v in want]          # follow the oracle's sequence
+        pos = [p + 1 for p in pos]
+    # the logits path (numpy argmax of the rows) agrees on the same step
+    a = nd.decode_batch(tokens, pos)
+    b = nd.decode_batch_argmax(tokens, pos)
+    assert a == b
+    nd.dec.store.close()
