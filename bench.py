@@ -278,6 +278,35 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
     torch.cuda.synchronize()
     lm_ms = e0.elapsed_time(e1) / n_lm
     lm_bytes = shape.V * shape.d * 2
+    # prefill: one 512-token prompt through every layer in one pass per
+    # layer (jm_prefill_layers), against the reference's loop of one decode
+    # step per position, estimated from B=1 decode steps on these kernels
+    Tp = 512
+    dec.weights.t["embed"] = (torch.randn((shape.V, shape.d), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    dec._w = dec.weights.kernel_w()
+    prompt = torch.randint(0, shape.V, (Tp,), generator=g, device="cuda", dtype=torch.int32)
+    kvp = KVCacheSet(shape, 1)
+    plog = torch.empty(shape.V, dtype=torch.float32, device="cuda")
+    dec.prefill_layers(prompt, kvp, 0, plog)
+    torch.cuda.synchronize()
+    n_pf = 3
+    e0.record(st)
+    for _ in range(n_pf):
+        dec.prefill_layers(prompt, kvp, 0, plog)
+    e1.record(st)
+    torch.cuda.synchronize()
+    pf_ms = e0.elapsed_time(e1) / n_pf
+    x1 = x[:1].contiguous()
+    for _ in range(warmup):
+        dec.decode_layers_batch(x1, [Tp - 1], kvp, hid[:1])
+    torch.cuda.synchronize()
+    e0.record(st)
+    for _ in range(steps):
+        dec.decode_layers_batch(x1, [Tp - 1], kvp, hid[:1])
+    e1.record(st)
+    torch.cuda.synchronize()
+    b1_ms = e0.elapsed_time(e1) / steps
+    del kvp
     res = {
         "tok_per_s": B / (ms * 1e-3), "ms_per_step": ms, "host_enqueue_ms_per_step": host_ms,
         "layers": n_layers, "batch": B, "position": position,
@@ -288,6 +317,12 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
         "bytes_alg": total, "bytes_moe": moe_bytes, "bytes_attn_weights": attn_w, "bytes_kv": kv_bytes,
         "GBs": total / (ms * 1e-3) / 1e9, "hbm_frac": total / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
         "hidden_finite": ok,
+        "prefill_512": {
+            "prompt_tokens": Tp, "ms": pf_ms, "tok_per_s": Tp / (pf_ms * 1e-3),
+            "decode_B1_ms_per_step": b1_ms,
+            "per_position_loop_ms_estimate": Tp * b1_ms,
+            "speedup_vs_per_position_loop": Tp * b1_ms / pf_ms,
+        },
         "with_lm_head_argmax": {
             "tok_per_s": B / (ms_lm * 1e-3), "ms_per_step": ms_lm, "vocab": shape.V,
             "lm_head_argmax_ms": lm_ms, "lm_head_bytes": lm_bytes,
@@ -299,7 +334,9 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
     log(f"decode {n_layers} layers B={B}: {res['tok_per_s']:.0f} tok/s, {ms:.3f} ms/step "
         f"(host enqueue {host_ms:.3f} ms), attention {split['attention']:.3f} ms, MoE {split['moe']:.3f} ms, "
         f"{res['GBs']:.0f} GB/s over {total / 1e9:.2f} GB; with lm_head + argmax {B / (ms_lm * 1e-3):.0f} tok/s "
-        f"({ms_lm:.3f} ms/step; lm_head {lm_ms * 1e3:.1f} us, {lm_bytes / (lm_ms * 1e-3) / 1e9:.0f} GB/s)")
+        f"({ms_lm:.3f} ms/step; lm_head {lm_ms * 1e3:.1f} us, {lm_bytes / (lm_ms * 1e-3) / 1e9:.0f} GB/s); "
+        f"prefill {Tp} tokens {pf_ms:.1f} ms ({Tp / (pf_ms * 1e-3):.0f} tok/s) vs {Tp * b1_ms:.0f} ms "
+        f"for {Tp} B=1 decode steps")
     store.close()
     del dec, weights, kv, store
     torch.cuda.empty_cache()

@@ -251,6 +251,21 @@ int jm_decode_layers_batch_argmax(jm_store* s, const jm_kernel_cfg* cfg, const j
                                   const int32_t* positions, const float* xin, int B, int32_t* out_tok,
                                   float* hidden, void* stream);
 
+/* prefill_layers(cfg, W, kv, tokens, T, logits) (decode_kernel.c:1606-1615):
+ * a prompt of T tokens through every layer.  The reference runs
+ * decode_layers_batch once per position; here all T positions go through
+ * each layer together, as one batch whose token t sits at position t (the
+ * attention of position t covers cache rows 0..t, so the result is the same
+ * computation).  Writes cache rows 0..T-1 of the one sequence and, with
+ * logits non-NULL, the last position's logits [V] (device).
+ *   kv      HOST array of the sequence's L caches (entry l)
+ *   tokens  DEVICE int32 [T]; needs W->embed (and the lm_head for logits)
+ * T <= cfg->maxT; prompts longer than 512 positions go through in chunks
+ * of 512 (each chunk's attention reads the rows the earlier chunks wrote).
+ * Runs eagerly (no graph replay). */
+int jm_prefill_layers(jm_store* s, const jm_kernel_cfg* cfg, const jm_kernel_w* W, const jm_kv_cache* kv,
+                      const int32_t* tokens, int T, float* logits, void* stream);
+
 /* The lm_head, KernelW.lm_head (decode_kernel.c:291; float32 [V][d] in the
  * reference, widened from the checkpoint's bf16 by decoder3.py:226-230).
  * JM_DTYPE_F32 values must be exactly bf16 (an error otherwise);

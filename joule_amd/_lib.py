@@ -42,6 +42,7 @@ SIGNATURES = {
     "jm_store_set_lm_head": ([_vp, _vp, _i, _i], _i),
     "jm_lm_head": ([_vp, _vp, _i, _vp, _vp, _vp], _i),
     "jm_embed_lookup": ([_vp, _vp, _vp, _i, _vp, _vp], _i),
+    "jm_prefill_layers": ([_vp] * 5 + [_i, _vp, _vp], _i),
     "jm_router": ([_vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp], _i),
     "jm_dispatch": ([_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "jm_q4_dequant": ([_vp, _vp, _vp, _i64, _i, _vp], _i),

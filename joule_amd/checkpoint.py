@@ -178,3 +178,45 @@ class HipNativeDecoder:
             self._seq_pos[f"seq{b}"] = p + 1
         lg = logits.cpu().numpy()
         return [int(lg[b].argmax()) for b in range(B)]
+
+    def prefill(self, tokens: list[int]) -> np.ndarray:
+        """NativeDecoder.prefill (decoder3.py:490-509): one prompt into seq0's
+        caches; the first-token logits [V]."""
+        dev = self.kv.data.device
+        logits = torch.empty(self.shape.V, dtype=torch.float32, device=dev)
+        self.dec.prefill_layers(torch.as_tensor(np.asarray(tokens, dtype=np.int32), device=dev), self.kv, 0, logits)
+        self._seq_pos = {"seq0": len(tokens)}
+        return logits.cpu().numpy()
+
+    def prefill_batch(self, prompts: list[list[int]], chunk: int = 512) -> list[np.ndarray]:
+        """NativeDecoder.prefill_batch (decoder3.py:512-571): B prompts into
+        seq0..seqB-1; the logits [V] after each prompt's last token.  All
+        positions of all prompts go through each layer together, in chunks of
+        `chunk` tokens taken in position order, where the reference runs one
+        decode_layers_batch per position."""
+        dev = self.kv.data.device
+        B = len(prompts)
+        if B > self.kv.B:
+            raise ValueError(f"{B} prompts, the cache set holds {self.kv.B} sequences")
+        items = sorted(((t, b) for b in range(B) for t in range(len(prompts[b]))))   # position-major
+        last = np.zeros((B, self.shape.d), np.float32)
+        graph = self.dec.graph
+        self.dec.set_graph(False)          # every chunk differs: run eagerly
+        try:
+            for c0 in range(0, len(items), chunk):
+                part = items[c0:c0 + chunk]
+                tok = torch.as_tensor(np.asarray([prompts[b][t] for t, b in part], np.int32), device=dev)
+                x = self.dec.embed(tok)
+                hid = self.dec.decode_layers_batch(x, [t for t, _ in part], self.kv, seqs=[b for _, b in part])
+                rows = [i for i, (t, b) in enumerate(part) if t == len(prompts[b]) - 1]
+                if rows:
+                    h = hid[torch.as_tensor(rows, device=dev)].cpu().numpy()
+                    for r, i in enumerate(rows):
+                        last[part[i][1]] = h[r]
+        finally:
+            self.dec.set_graph(graph)
+        logits = torch.empty((B, self.shape.V), dtype=torch.float32, device=dev)
+        self.dec.lm_head(torch.from_numpy(last).to(dev), logits, None)
+        self._seq_pos = {f"seq{b}": len(prompts[b]) for b in range(B)}
+        lg = logits.cpu().numpy()
+        return [lg[b] for b in range(B)]

@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <climits>
 #include <cstring>
+#include <vector>
 
 #include "jm_store.h"
 
@@ -29,6 +30,7 @@ namespace {
 
 constexpr int HD = 128;     // head dimension the attention kernels take
 constexpr int PSPLIT = 128; // positions per attention split
+constexpr int PREFILL_CHUNK = 512;  // prompt positions per pass of jm_prefill_layers
 
 void free_decode(jm_store* s) {
     if (s->gexec) (void)hipGraphExecDestroy(s->gexec);
@@ -67,6 +69,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
         (size_t)B * hq * 4,                       // att
         (size_t)B * hq * 4,                       // qout
         (size_t)B * d * 4,                        // hid
+        (size_t)B * d * 4,                        // xemb: embedded prompt tokens (prefill)
         (size_t)jm::lm_blocks(V) * B * 4,         // lmv
         (size_t)jm::lm_blocks(V) * B * 4,         // lmi
         s->tab_cap,                               // KV pointers + positions
@@ -79,7 +82,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     JM_HIP(hipMalloc(&s->dws, total), "hipMalloc decode workspace");
     char* p = (char*)s->dws;
     void** slots[] = {(void**)&s->h, (void**)&s->h2, (void**)&s->qkv, (void**)&s->opart, (void**)&s->part_o,
-                      (void**)&s->part_ml, (void**)&s->att, (void**)&s->qout, (void**)&s->hid, (void**)&s->lmv,
+                      (void**)&s->part_ml, (void**)&s->att, (void**)&s->qout, (void**)&s->hid, (void**)&s->xemb, (void**)&s->lmv,
                       (void**)&s->lmi, (void**)&s->tab};
     for (size_t i = 0; i < sizeof sz / sizeof sz[0]; i++) {
         *slots[i] = p;
@@ -232,7 +235,7 @@ namespace {
 
 int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const jm_kv_cache* kv,
                 const int32_t* positions, const float* xin, int B, float* logits, int32_t* out_tok,
-                float* hidden, void* stream) {
+                float* hidden, void* stream, bool allow_graph = true) {
     if (!s || !c) return fail(JM_ERR_ARG, "store and cfg must be non-NULL");
     if (!s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
     int qpk = 0;
@@ -294,7 +297,7 @@ int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const
         }
     }
 
-    if (s->dgraph && !s->prof) {
+    if (s->dgraph && !s->prof && allow_graph) {
         // replay the step from a captured graph: kernel arguments are baked
         // in, so the capture is keyed by everything they depend on
         DecKey key;
@@ -350,6 +353,51 @@ int jm_decode_layers_batch_argmax(jm_store* s, const jm_kernel_cfg* c, const jm_
                                   float* hidden, void* stream) {
     if (!out_tok && B > 0) return fail(JM_ERR_ARG, "out_tok must be non-NULL");
     return decode_impl(s, c, W, kv, positions, xin, B, nullptr, out_tok, hidden, stream);
+}
+
+int jm_prefill_layers(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const jm_kv_cache* kv,
+                      const int32_t* tokens, int T, float* logits, void* stream) {
+    if (!s || !c || !W) return fail(JM_ERR_ARG, "store, cfg and weights must be non-NULL");
+    if (T <= 0) return fail(JM_ERR_ARG, "T must be positive");
+    if (T > c->maxT) return fail(JM_ERR_ARG, "T=%d exceeds maxT=%d", T, c->maxT);
+    if (!kv || !tokens) return fail(JM_ERR_ARG, "kv and tokens must be non-NULL");
+    if (!W->embed) return fail(JM_ERR_ARG, "the embedding (W->embed) must be set");
+    if (logits && !s->lm) return fail(JM_ERR_ARG, "lm_head not set (jm_store_set_lm_head)");
+    if (logits && s->lm_V != c->V) return fail(JM_ERR_SHAPE, "cfg V=%d differs from the lm_head's %d rows", c->V, s->lm_V);
+    // every position of the prompt is one token of the batch: position t,
+    // the sequence's caches for each of them; in chunks of PREFILL_CHUNK
+    // positions (each chunk's attention reads the rows the earlier chunks
+    // wrote), which bounds the MoE dispatch and the workspace
+    const int TC = T < PREFILL_CHUNK ? T : PREFILL_CHUNK;
+    std::vector<int32_t> pos((size_t)TC);
+    std::vector<jm_kv_cache> tab((size_t)TC * c->L);
+    for (int t = 0; t < TC; t++)
+        for (int l = 0; l < c->L; l++) tab[(size_t)t * c->L + l] = kv[l];
+    int qpk = 0;
+    if (int rc = check_decode_args(s, c, W, &qpk)) return rc;
+    if (int rc = jm::store_reserve(s, TC)) return rc;
+    const int nqkv = (c->n_heads + 2 * c->n_kv) * HD;
+    if (int rc = decode_reserve(s, TC, (c->maxT + PSPLIT - 1) / PSPLIT, nqkv, c->n_heads * HD, logits ? c->V : 0))
+        return rc;
+    hipStream_t st = (hipStream_t)stream;
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    int n = 0;
+    for (int t0 = 0; t0 < T; t0 += n) {
+        n = T - t0 < TC ? T - t0 : TC;
+        for (int t = 0; t < n; t++) pos[t] = t0 + t;
+        JM_HIP(jm::launch_embed(W->embed, c->V, c->d, tokens + t0, n, s->xemb, st), "embedding launch");
+        if (int rc = decode_impl(s, c, W, tab.data(), pos.data(), s->xemb, n, nullptr, nullptr, s->hid, stream, false))
+            return rc;
+    }
+    if (logits) {
+        // the lm_head at the last position only (prefill_layers, :1606-1615)
+        jm::LmArgs la{};
+        la.w = s->lm; la.x = s->hid + (size_t)(n - 1) * c->d; la.V = s->lm_V; la.d = c->d; la.B = 1;
+        la.logits = logits;
+        la.best_i = s->lmi;
+        JM_HIP(jm::launch_lm_head(la, nullptr, st), "lm_head launch");
+    }
+    return 0;
 }
 
 int jm_store_set_lm_head(jm_store* s, const void* w, int dtype, int V) {

@@ -85,6 +85,7 @@ struct jm_store {
     float* att;                 // [B][H hd] attention output
     float* qout;                // [B][H hd] finished query heads
     float* hid;                 // [B][d] final-normed hidden state (when the caller passes none)
+    float* xemb;                // [B][d] embedded prompt tokens (jm_prefill_layers)
     float* lmv;                 // [lm blocks][B] per-block best logit (argmax)
     int* lmi;                   // [lm blocks][B] its row
     unsigned long long* tab;    // [B*L][2] KV pointers, then [B] positions (device)

@@ -189,13 +189,15 @@ class HipDecoder:
         """Replay each step from a captured HIP graph (re-recorded when the
         buffers, batch size or attention split count change)."""
         _lib.check(_lib.lib().jm_store_decode_graph(self.store._h, int(bool(enable))), "jm_store_decode_graph")
+        self.graph = bool(enable)
 
     def decode_layers_batch(self, x: torch.Tensor, positions, kv: KVCacheSet,
                             hidden: torch.Tensor | None = None, logits: torch.Tensor | None = None,
-                            stream=None) -> torch.Tensor:
+                            stream=None, seqs=None) -> torch.Tensor:
         """hidden [B, d] = final RMSNorm of the residual stream after every
         layer, for tokens x [B, d] (float32) writing cache rows positions[b];
-        with logits [B, V] (float32, CUDA) also the lm_head of it."""
+        with logits [B, V] (float32, CUDA) also the lm_head of it.  Token b
+        uses sequence b's caches, or sequence seqs[b]'s."""
         if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or x.dim() != 2:
             raise ValueError("x must be a contiguous float32 CUDA tensor [B, d]")
         B = x.shape[0]
@@ -206,7 +208,7 @@ class HipDecoder:
                                    or not logits.is_contiguous()):
             raise ValueError(f"logits must be a contiguous float32 tensor [{B}, {self.shape.V}]")
         _lib.check(_lib.lib().jm_decode_layers_batch(
-            self.store._h, ctypes.byref(self._cfg), ctypes.byref(self._w), self._table(kv, B),
+            self.store._h, ctypes.byref(self._cfg), ctypes.byref(self._w), self._table(kv, B, seqs),
             pos.ctypes.data_as(ctypes.c_void_p), _lib.ptr(x), B, _lib.ptr(logits), _lib.ptr(hidden),
             _lib.stream_handle(stream)), "jm_decode_layers_batch")
         return hidden
@@ -239,11 +241,40 @@ class HipDecoder:
             raise ValueError("one position per token")
         return pos
 
-    def _table(self, kv: KVCacheSet, B: int):
+    def _table(self, kv: KVCacheSet, B: int, seqs=None):
+        """The KVCache[B*L] argument: sequence b's caches for token b, or
+        sequence seqs[b]'s (several tokens of one sequence in a prefill)."""
+        L = self.shape.n_layers
+        if seqs is not None:
+            seqs = [int(q) for q in seqs]
+            if len(seqs) != B or min(seqs) < 0 or max(seqs) >= kv.B:
+                raise ValueError("seqs: one sequence index per token, each below the cache set's size")
+            table = (KVCache * (B * L))()
+            for b, q in enumerate(seqs):
+                for l in range(L):
+                    table[b * L + l] = kv.table[q * L + l]
+            self._table_keep = table        # alive until the call has staged it
+            return ctypes.cast(table, _vp)
         if kv.B < B:
             raise ValueError(f"cache set holds {kv.B} sequences, batch has {B}")
-        table = kv.table if kv.B == B else (KVCache * (B * self.shape.n_layers)).from_buffer(kv.table)
+        table = kv.table if kv.B == B else (KVCache * (B * L)).from_buffer(kv.table)
         return ctypes.cast(table, _vp)
+
+    def prefill_layers(self, tokens: torch.Tensor, kv: KVCacheSet, seq: int = 0,
+                       logits: torch.Tensor | None = None, stream=None) -> torch.Tensor | None:
+        """prefill_layers (decode_kernel.c:1606-1615): a prompt (int32 CUDA
+        tokens [T]) through every layer into sequence seq's caches, rows
+        0..T-1; returns the last position's logits [V] when given a tensor."""
+        if tokens.dtype != torch.int32 or not tokens.is_cuda or not tokens.is_contiguous():
+            raise ValueError("tokens must be a contiguous int32 CUDA tensor")
+        L = self.shape.n_layers
+        if not 0 <= seq < kv.B:
+            raise ValueError("seq outside the cache set")
+        table = (KVCache * L).from_buffer(kv.table, seq * L * ctypes.sizeof(KVCache))
+        _lib.check(_lib.lib().jm_prefill_layers(
+            self.store._h, ctypes.byref(self._cfg), ctypes.byref(self._w), ctypes.cast(table, _vp),
+            _lib.ptr(tokens), tokens.numel(), _lib.ptr(logits), _lib.stream_handle(stream)), "jm_prefill_layers")
+        return logits
 
     def decode_layers_batch_argmax(self, x: torch.Tensor, positions, kv: KVCacheSet,
                                    out_tok: torch.Tensor | None = None, stream=None) -> torch.Tensor:

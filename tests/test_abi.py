@@ -93,3 +93,14 @@ def test_null_arguments_are_errors():
     assert L.jm_store_destroy(None) == 0
     with pytest.raises(_lib.JouleError):
         _lib.check(L.jm_store_reserve(None, 4), "reserve")
+
+
+def test_ctypes_argument_counts_match_the_header():
+    """Each ctypes signature has as many arguments as the C prototype."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    protos = dict(re.findall(r"\b(jm_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S))
+    assert set(protos) == set(_lib.SIGNATURES)
+    for name, params in protos.items():
+        params = params.strip()
+        n = 0 if params in ("", "void") else params.count(",") + 1
+        assert n == len(_lib.SIGNATURES[name][0]), (name, n, len(_lib.SIGNATURES[name][0]))
