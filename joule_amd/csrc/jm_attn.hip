@@ -30,25 +30,26 @@ namespace jm {
 
 // ------------------------------------------------------------------ GEMV
 
-// Partial products of 512-column slices: part[s][b][row] = sum over columns
-// k of slice s of W[row][k] * x[b][k] (* norm_w[k]), rows of the stacked
-// matrices w[0..2].  Block (row group, slice, token group): 8 waves of 8 rows,
-// each lane holding 8 consecutive columns of its rows; the slice of every
-// token of the group staged in LDS (16 KiB at 8 tokens).  The consumer sums
-// the slices (and applies the RMSNorm row scale), so that each block moves
-// few activation bytes and a projection spreads over hundreds of blocks.
-template <int BT>
-__global__ void __launch_bounds__(512)
+// Partial products of column slices: part[s][b][row] = sum over the
+// columns k of slice s of W[row][k] * x[b][k] (* norm_w[k]), rows of the
+// stacked matrices w[0..2].  Block (row group, slice, token group): WV waves
+// of R rows, each lane holding 8 consecutive columns of its rows per
+// 512-column pass (NPS passes per slice); the slice of every token of the
+// group staged in LDS.  The consumer sums the slices (and applies the
+// RMSNorm row scale), so that each block moves few activation bytes and a
+// projection spreads over hundreds of blocks.
+template <int BT, int R, int WV, int NPS>
+__global__ void __launch_bounds__(WV * 64)
 k_gemv_part(GemvArgs a) {
-    constexpr int R = 8;
-    __shared__ __align__(16) float xs[BT * 512];
+    constexpr int SW = NPS * 512;
+    __shared__ __align__(16) float xs[BT * SW];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int slice = blockIdx.y, tb0 = blockIdx.z * BT;
-    const int row0 = blockIdx.x * 64 + w * R;
-    const int k0 = slice * 512;
+    const int row0 = blockIdx.x * (WV * R) + w * R;
+    const int k0 = slice * SW;
 
-    // this wave's rows, 16 bytes per lane each, requested first
-    uint4 wq[R];
+    // this wave's rows, 16 bytes per lane per pass, requested first
+    uint4 wq[R][NPS];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         int row = row0 + r;
@@ -57,12 +58,13 @@ k_gemv_part(GemvArgs a) {
         if (row < a.rows[0]) wr = a.w[0] + (size_t)row * a.K;
         else if (row < a.rows[0] + a.rows[1]) wr = a.w[1] + (size_t)(row - a.rows[0]) * a.K;
         else wr = a.w[2] + (size_t)(row - a.rows[0] - a.rows[1]) * a.K;
-        wq[r] = *((const uint4*)(wr + k0) + lane);
+        const uint4* p = (const uint4*)(wr + k0) + lane;
+#pragma unroll
+        for (int j = 0; j < NPS; j++) wq[r][j] = p[j * 64];
     }
     // the tokens' slice (times the norm weight)
-#pragma unroll
-    for (int i = tid; i < BT * 128; i += 512) {
-        const int b = i >> 7, c = 4 * (i & 127);
+    for (int i = tid; i < BT * SW / 4; i += WV * 64) {
+        const int b = i / (SW / 4), c = 4 * (i % (SW / 4));
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (tb0 + b < a.B) {
             v = *(const float4*)(a.x + (size_t)(tb0 + b) * a.K + k0 + c);
@@ -74,37 +76,44 @@ k_gemv_part(GemvArgs a) {
                 v.w = __fmul_rn(v.w, bf16_bits_to_f32(nw.y >> 16));
             }
         }
-        *(float4*)(xs + b * 512 + c) = v;
+        *(float4*)(xs + b * SW + c) = v;
     }
     __syncthreads();
 
-    float wf[R][8];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const uint32_t ww[4] = {wq[r].x, wq[r].y, wq[r].z, wq[r].w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            wf[r][2 * i] = __uint_as_float(ww[i] << 16);
-            wf[r][2 * i + 1] = __uint_as_float(ww[i] & 0xFFFF0000u);
-        }
-    }
     float acc[R][BT];
 #pragma unroll
-    for (int b = 0; b < BT; b++) {
-        const float4 x0 = *(const float4*)(xs + b * 512 + lane * 8);
-        const float4 x1 = *(const float4*)(xs + b * 512 + lane * 8 + 4);
-        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < BT; b++) acc[r][b] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPS; j++) {
+        float wf[R][8];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            float s = 0.0f;
+            const uint32_t ww[4] = {wq[r][j].x, wq[r][j].y, wq[r][j].z, wq[r][j].w};
 #pragma unroll
-            for (int i = 0; i < 8; i++) s = __builtin_fmaf(wf[r][i], xv[i], s);
-            acc[r][b] = s;
+            for (int i = 0; i < 4; i++) {
+                wf[r][2 * i] = __uint_as_float(ww[i] << 16);
+                wf[r][2 * i + 1] = __uint_as_float(ww[i] & 0xFFFF0000u);
+            }
         }
-        // one token at a time: the empty asm takes the sums and fences
-        // memory, so later tokens' LDS reads are not hoisted into registers
 #pragma unroll
-        for (int r = 0; r < R; r++) __asm__ volatile("" : "+v"(acc[r][b]) : : "memory");
+        for (int b = 0; b < BT; b++) {
+            const float4 x0 = *(const float4*)(xs + b * SW + j * 512 + lane * 8);
+            const float4 x1 = *(const float4*)(xs + b * SW + j * 512 + lane * 8 + 4);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float s = acc[r][b];
+#pragma unroll
+                for (int i = 0; i < 8; i++) s = __builtin_fmaf(wf[r][i], xv[i], s);
+                acc[r][b] = s;
+            }
+            // one token at a time: the empty asm takes the sums and fences
+            // memory, so later tokens' LDS reads are not hoisted into registers
+#pragma unroll
+            for (int r = 0; r < R; r++) __asm__ volatile("" : "+v"(acc[r][b]) : : "memory");
+        }
     }
     // row totals: groups of up to 16 partial sums transposed across the wave
     constexpr int NV = R * BT;
@@ -126,18 +135,29 @@ k_gemv_part(GemvArgs a) {
     }
 }
 
-bool gemv_shape_ok(int K) { return K > 0 && K % 512 == 0 && K <= 8192; }
+bool gemv_shape_ok(int K) { return K > 0 && K % 1024 == 0 && K <= 8192; }
+
+int gemv_slice_cols(int K) { return K >= 4096 ? 1024 : 512; }
 
 hipError_t launch_gemv_part(const GemvArgs& a, hipStream_t st) {
     if (a.B == 0 || a.N == 0) return hipSuccess;
     const int BT = a.B <= 1 ? 1 : a.B <= 2 ? 2 : a.B <= 4 ? 4 : 8;
-    const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)(a.K / 512), (unsigned)((a.B + BT - 1) / BT));
+    // shapes from a sweep at 8 tokens: 512-column slices with 8 waves of 4
+    // rows for K = 2048 (2.5 TB/s on the qkv projection), 1024-column slices
+    // with 16 waves of 2 rows for K = 4096 (o_proj)
+    const bool wide = gemv_slice_cols(a.K) == 1024;
+    const int R = wide ? 2 : 4, WV = wide ? 16 : 8;
+    const dim3 grid((unsigned)((a.N + WV * R - 1) / (WV * R)), (unsigned)(a.K / gemv_slice_cols(a.K)),
+                    (unsigned)((a.B + BT - 1) / BT));
+#define JM_GP(BB) if (wide) hipLaunchKernelGGL((k_gemv_part<BB, 2, 16, 2>), grid, dim3(1024), 0, st, a); \
+                  else hipLaunchKernelGGL((k_gemv_part<BB, 4, 8, 1>), grid, dim3(512), 0, st, a)
     switch (BT) {
-        case 1: hipLaunchKernelGGL(k_gemv_part<1>, grid, dim3(512), 0, st, a); break;
-        case 2: hipLaunchKernelGGL(k_gemv_part<2>, grid, dim3(512), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(k_gemv_part<4>, grid, dim3(512), 0, st, a); break;
-        default: hipLaunchKernelGGL(k_gemv_part<8>, grid, dim3(512), 0, st, a); break;
+        case 1: JM_GP(1); break;
+        case 2: JM_GP(2); break;
+        case 4: JM_GP(4); break;
+        default: JM_GP(8); break;
     }
+#undef JM_GP
     return hipGetLastError();
 }
 

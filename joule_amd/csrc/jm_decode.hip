@@ -62,7 +62,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     const size_t sz[] = {
         (size_t)B * d * 4,                        // h
         (size_t)B * d * 4,                        // h2
-        (size_t)(d / 512) * B * nqkv * 4,         // qkv slices
+        (size_t)(d / 512) * B * nqkv * 4,         // qkv slices (at most d / 512 of them)
         (size_t)(hq / 512) * B * d * 4,           // o_proj slices
         (size_t)B * S * hq * 4,                   // part_o: H heads x hd per split
         (size_t)B * S * (hq / HD) * 2 * 4,        // part_ml
@@ -106,7 +106,7 @@ int check_decode_args(const jm_store* s, const jm_kernel_cfg* c, const jm_kernel
     if (*qpk != 1 && *qpk != 2 && *qpk != 4 && *qpk != 8)
         return fail(JM_ERR_SHAPE, "n_heads / n_kv must be 1, 2, 4 or 8 (got %d)", *qpk);
     if (!jm::gemv_shape_ok(c->d) || !jm::gemv_shape_ok(c->n_heads * HD))
-        return fail(JM_ERR_SHAPE, "d=%d and n_heads*hd=%d must be multiples of 512 up to 8192", c->d, c->n_heads * HD);
+        return fail(JM_ERR_SHAPE, "d=%d and n_heads*hd=%d must be multiples of 1024 up to 8192", c->d, c->n_heads * HD);
     if (c->qk_norm_type != 0 && c->qk_norm_type != 1)
         return fail(JM_ERR_SHAPE, "qk_norm_type %d: only 0 (none) and 1 (per head) are supported", c->qk_norm_type);
     if (c->maxT <= 0) return fail(JM_ERR_SHAPE, "maxT must be positive");
@@ -152,7 +152,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         JM_HIP(jm::launch_gemv_part(g, st), "qkv launch");
 
         jm::AttnArgs at{};
-        at.qkv = s->qkv; at.nslice = d / 512; at.h = s->h; at.d = d;
+        at.qkv = s->qkv; at.nslice = d / jm::gemv_slice_cols(d); at.h = s->h; at.d = d;
         if (c->bias_qkv) {
             at.bq = W->bq + (size_t)l * H * HD;
             at.bk = W->bk + (size_t)l * KH * HD;
@@ -181,7 +181,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         // h2 = h + attention (summed from the o_proj slices in the router),
         // then h = h2 + MoE(RMSNorm(h2))
         jm::FfnIo io;
-        io.xpart = s->opart; io.nxpart = H * HD / 512; io.xmid = s->h2;
+        io.xpart = s->opart; io.nxpart = H * HD / jm::gemv_slice_cols(H * HD); io.xmid = s->h2;
         io.norm_w = W->norm2 + (size_t)l * d; io.eps = c->eps;
         io.resid = s->h2;
         if (int rc = jm::ffn_enqueue(s, l, s->h, B, s->h, io, false, st)) return rc;

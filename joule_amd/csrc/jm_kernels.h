@@ -138,19 +138,20 @@ hipError_t launch_combine(const float* y, const int* comb, int B, int k, int d, 
                           float* out, hipStream_t st);
 // ---- decoder layer around the MoE block (jm_attn.hip)
 
-// part[s][b][row] = sum over the columns k of 512-column slice s of
+// part[s][b][row] = sum over the columns k of column slice s of
 // W[row][k] * x[b][k] (* norm_w[k]), rows of up to three stacked bf16
-// matrices [rows_i][K]; the consumer sums the K / 512 slices.
+// matrices [rows_i][K]; the consumer sums the K / gemv_slice_cols(K) slices.
 struct GemvArgs {
     const float* x;           // [B][K]
     const uint16_t* norm_w;   // [K] bf16 weight multiplied into x, or NULL
     const uint16_t* w[3];     // bf16 [rows[i]][K]
     int rows[3];
     int K, N, B;              // N = rows[0] + rows[1] + rows[2]
-    float* part;              // [K / 512][B][N]
+    float* part;              // [K / gemv_slice_cols(K)][B][N]
 };
-// K a multiple of 512 (at most 8192)
+// K a multiple of 1024 (at most 8192); slices of 512 columns, 1024 from K = 4096
 bool gemv_shape_ok(int K);
+int gemv_slice_cols(int K);
 hipError_t launch_gemv_part(const GemvArgs& a, hipStream_t st);
 
 // Decode attention of one layer for B tokens, head dim 128, H / KH query
