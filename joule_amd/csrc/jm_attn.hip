@@ -32,107 +32,86 @@ namespace jm {
 
 // Partial products of column slices: part[s][b][row] = sum over the
 // columns k of slice s of W[row][k] * x[b][k] (* norm_w[k]), rows of the
-// stacked matrices w[0..2].  Block (row group, slice, token group): WV waves
-// of R rows, each lane holding 8 consecutive columns of its rows per
-// 512-column pass (NPS passes per slice); the slice of every token of the
-// group staged in LDS.  The consumer sums the slices (and applies the
-// RMSNorm row scale), so that each block moves few activation bytes and a
-// projection spreads over hundreds of blocks.
-template <int BT, int R, int WV, int NPS>
+// stacked matrices w[0..2], on the matrix cores.  Block (row group, slice,
+// group of 8 tokens): WV waves of 16 rows.  v_mfma_f32_16x16x32_bf16 with
+// the weight rows as the A operand straight from memory (lane l: row
+// row0 + l % 16, columns 32 ks + 8 (l / 16) .. + 7, one 16-byte load per
+// k-step, all requested first) and the tokens as B columns: column n < 8
+// holds bf16(x) of token n, column n + 8 the rest bf16(x - bf16(x)); the
+// block stages them in LDS in operand order.  Columns n and n ^ 8 of the
+// product (one DPP move) add up to the token's dot product at float32-level
+// accuracy.  The consumer sums the slices (and applies the RMSNorm row
+// scale), so that a projection spreads over hundreds of waves.
+template <int SW, int WV>
 __global__ void __launch_bounds__(WV * 64)
 k_gemv_part(GemvArgs a) {
-    constexpr int SW = NPS * 512;
-    __shared__ __align__(16) float xs[BT * SW];
+    constexpr int NK = SW / 32;                    // k-steps
+    __shared__ __align__(16) uint4 xb[NK][64];     // B operands, [k-step][lane]
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int slice = blockIdx.y, tb0 = blockIdx.z * BT;
-    const int row0 = blockIdx.x * (WV * R) + w * R;
+    const int g = lane >> 4, n = lane & 15;
+    const int slice = blockIdx.y, tb0 = blockIdx.z * 8;
+    const int row0 = (blockIdx.x * WV + w) * 16;
     const int k0 = slice * SW;
-
-    // this wave's rows, 16 bytes per lane per pass, requested first
-    uint4 wq[R][NPS];
+    const bool live = row0 < a.N;                  // wave-uniform
+    // this wave's rows (a 16-row tile lies in one matrix: rows[i] % 16 == 0)
+    const int row = live ? row0 + n : 0;
+    const uint16_t* wr;
+    if (row < a.rows[0]) wr = a.w[0] + (size_t)row * a.K;
+    else if (row < a.rows[0] + a.rows[1]) wr = a.w[1] + (size_t)(row - a.rows[0]) * a.K;
+    else wr = a.w[2] + (size_t)(row - a.rows[0] - a.rows[1]) * a.K;
+    const uint16_t* wp = wr + k0 + 8 * g;
+    uint4 wa[NK];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        int row = row0 + r;
-        row = row < a.N ? row : a.N - 1;
-        const uint16_t* wr;
-        if (row < a.rows[0]) wr = a.w[0] + (size_t)row * a.K;
-        else if (row < a.rows[0] + a.rows[1]) wr = a.w[1] + (size_t)(row - a.rows[0]) * a.K;
-        else wr = a.w[2] + (size_t)(row - a.rows[0] - a.rows[1]) * a.K;
-        const uint4* p = (const uint4*)(wr + k0) + lane;
-#pragma unroll
-        for (int j = 0; j < NPS; j++) wq[r][j] = p[j * 64];
-    }
-    // the tokens' slice (times the norm weight)
-    for (int i = tid; i < BT * SW / 4; i += WV * 64) {
-        const int b = i / (SW / 4), c = 4 * (i % (SW / 4));
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (tb0 + b < a.B) {
-            v = *(const float4*)(a.x + (size_t)(tb0 + b) * a.K + k0 + c);
+    for (int ks = 0; ks < NK; ks++) wa[ks] = *(const uint4*)(wp + 32 * ks);
+    // the tokens' slice (times the norm weight), split into hi and lo columns
+    for (int i = tid; i < NK * 32; i += WV * 64) {
+        const int ks = i >> 5, gg = (i >> 3) & 3, t = i & 7;
+        const int c = k0 + 32 * ks + 8 * gg;
+        float v[8];
+        if (tb0 + t < a.B) {
+            const float4* xp = (const float4*)(a.x + (size_t)(tb0 + t) * a.K + c);
+            const float4 x0 = xp[0], x1 = xp[1];
+            v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+            v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
             if (a.norm_w) {
-                const uint2 nw = *(const uint2*)(a.norm_w + k0 + c);
-                v.x = __fmul_rn(v.x, bf16_bits_to_f32(nw.x & 0xFFFFu));
-                v.y = __fmul_rn(v.y, bf16_bits_to_f32(nw.x >> 16));
-                v.z = __fmul_rn(v.z, bf16_bits_to_f32(nw.y & 0xFFFFu));
-                v.w = __fmul_rn(v.w, bf16_bits_to_f32(nw.y >> 16));
+                const uint4 nw = *(const uint4*)(a.norm_w + c);
+                const uint32_t nn[4] = {nw.x, nw.y, nw.z, nw.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    v[2 * e] = __fmul_rn(v[2 * e], bf16_bits_to_f32(nn[e] & 0xFFFFu));
+                    v[2 * e + 1] = __fmul_rn(v[2 * e + 1], bf16_bits_to_f32(nn[e] >> 16));
+                }
             }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = 0.0f;
         }
-        *(float4*)(xs + b * SW + c) = v;
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) split_bf16x2(v[2 * e], v[2 * e + 1], hi[e], lo[e]);
+        xb[ks][16 * gg + t] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        xb[ks][16 * gg + 8 + t] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
     }
     __syncthreads();
+    if (!live) return;
 
-    float acc[R][BT];
+    // two accumulators break the dependence chain of the k-steps
+    floatx4 acc[2] = {floatx4{0.0f, 0.0f, 0.0f, 0.0f}, floatx4{0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-    for (int r = 0; r < R; r++)
+    for (int ks = 0; ks < NK; ks++)
+        acc[ks & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wa[ks]),
+                                                              __builtin_bit_cast(bf16x8, xb[ks][lane]),
+                                                              acc[ks & 1], 0, 0, 0);
+    // lane (g, n): rows row0 + 4 g + i of column n; token n = hi + lo columns
+    float tot[4];
 #pragma unroll
-        for (int b = 0; b < BT; b++) acc[r][b] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NPS; j++) {
-        float wf[R][8];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint32_t ww[4] = {wq[r][j].x, wq[r][j].y, wq[r][j].z, wq[r][j].w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                wf[r][2 * i] = __uint_as_float(ww[i] << 16);
-                wf[r][2 * i + 1] = __uint_as_float(ww[i] & 0xFFFF0000u);
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < BT; b++) {
-            const float4 x0 = *(const float4*)(xs + b * SW + j * 512 + lane * 8);
-            const float4 x1 = *(const float4*)(xs + b * SW + j * 512 + lane * 8 + 4);
-            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float s = acc[r][b];
-#pragma unroll
-                for (int i = 0; i < 8; i++) s = __builtin_fmaf(wf[r][i], xv[i], s);
-                acc[r][b] = s;
-            }
-            // one token at a time: the empty asm takes the sums and fences
-            // memory, so later tokens' LDS reads are not hoisted into registers
-#pragma unroll
-            for (int r = 0; r < R; r++) __asm__ volatile("" : "+v"(acc[r][b]) : : "memory");
-        }
+    for (int i = 0; i < 4; i++) {
+        const float c = __fadd_rn(acc[0][i], acc[1][i]);
+        tot[i] = __fadd_rn(c, dpp_f<DPP_ROR8>(c));
     }
-    // row totals: groups of up to 16 partial sums transposed across the wave
-    constexpr int NV = R * BT;
-    constexpr int NG = NV < 16 ? NV : 16;
-    float* flat = &acc[0][0];
-#pragma unroll
-    for (int g0 = 0; g0 < NV; g0 += NG) {
-        float v[NG];
-#pragma unroll
-        for (int i = 0; i < NG; i++) v[i] = flat[g0 + i];
-        const float tot = transpose_reduce<64, NG>(v);
-        constexpr int LPV = 64 / NG;                  // lanes holding each value
-        if (lane % LPV == 0) {
-            const int vi = g0 + lane / LPV;
-            const int r = vi / BT, b = vi % BT;
-            const int row = row0 + r;
-            if (row < a.N && tb0 + b < a.B) a.part[((size_t)slice * a.B + tb0 + b) * a.N + row] = tot;
-        }
-    }
+    if (n < 8 && tb0 + n < a.B)
+        *(float4*)(a.part + ((size_t)slice * a.B + tb0 + n) * a.N + row0 + 4 * g) =
+            make_float4(tot[0], tot[1], tot[2], tot[3]);
 }
 
 bool gemv_shape_ok(int K) { return K > 0 && K % 1024 == 0 && K <= 8192; }
@@ -141,23 +120,12 @@ int gemv_slice_cols(int K) { return K >= 4096 ? 1024 : 512; }
 
 hipError_t launch_gemv_part(const GemvArgs& a, hipStream_t st) {
     if (a.B == 0 || a.N == 0) return hipSuccess;
-    const int BT = a.B <= 1 ? 1 : a.B <= 2 ? 2 : a.B <= 4 ? 4 : 8;
-    // shapes from a sweep at 8 tokens: 512-column slices with 8 waves of 4
-    // rows for K = 2048 (2.5 TB/s on the qkv projection), 1024-column slices
-    // with 16 waves of 2 rows for K = 4096 (o_proj)
-    const bool wide = gemv_slice_cols(a.K) == 1024;
-    const int R = wide ? 2 : 4, WV = wide ? 16 : 8;
-    const dim3 grid((unsigned)((a.N + WV * R - 1) / (WV * R)), (unsigned)(a.K / gemv_slice_cols(a.K)),
-                    (unsigned)((a.B + BT - 1) / BT));
-#define JM_GP(BB) if (wide) hipLaunchKernelGGL((k_gemv_part<BB, 2, 16, 2>), grid, dim3(1024), 0, st, a); \
-                  else hipLaunchKernelGGL((k_gemv_part<BB, 4, 8, 1>), grid, dim3(512), 0, st, a)
-    switch (BT) {
-        case 1: JM_GP(1); break;
-        case 2: JM_GP(2); break;
-        case 4: JM_GP(4); break;
-        default: JM_GP(8); break;
-    }
-#undef JM_GP
+    if (a.rows[0] % 16 || a.rows[1] % 16 || a.rows[2] % 16) return hipErrorInvalidValue;
+    constexpr int WV = 4;
+    const int sw = gemv_slice_cols(a.K);
+    const dim3 grid((unsigned)((a.N + 16 * WV - 1) / (16 * WV)), (unsigned)(a.K / sw), (unsigned)((a.B + 7) / 8));
+    if (sw == 1024) hipLaunchKernelGGL((k_gemv_part<1024, WV>), grid, dim3(WV * 64), 0, st, a);
+    else hipLaunchKernelGGL((k_gemv_part<512, WV>), grid, dim3(WV * 64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -219,7 +187,7 @@ k_qkv_fin(AttnArgs a) {
     if (bias) v = __fadd_rn(v, bias[brow]);
     const unsigned long long* kvp = a.kv + ((size_t)b * a.L + a.layer) * 2;
     if (!isq && !isk) {                  // v head: to the cache
-        uint16_t* vc = (uint16_t*)kvp[1];
+        const gptr<uint16_t> vc = (gptr<uint16_t>)kvp[1];
         vc[((size_t)pos * a.KH + (hh - a.H - a.KH)) * HD + t] = (uint16_t)f32_to_bf16_rne(v);
         return;
     }
@@ -244,139 +212,206 @@ k_qkv_fin(AttnArgs a) {
     if (isq) {
         a.qout[((size_t)b * a.H + hh) * HD + t] = o;
     } else {
-        uint16_t* kc = (uint16_t*)kvp[0];
+        const gptr<uint16_t> kc = (gptr<uint16_t>)kvp[0];
         kc[((size_t)pos * a.KH + (hh - a.H)) * HD + t] = (uint16_t)f32_to_bf16_rne(o);
     }
 }
 
 // One (position split, KV head, token): QPK query heads over positions
 // [128 s, 128 s + 128) of the token's T = pos + 1 cache rows (the row at pos
-// appended by k_qkv_fin).  256 threads; lane (g, j) of wave w takes
-// positions 128 s + 32 w + 4 st + g (st < 8) and head dimensions 8 j ..
-// 8 j + 7.
+// appended by k_qkv_fin), on the matrix cores.  Wave w takes 32 positions
+// tw = 128 s + 32 w .. tw + 31 and all 128 head dimensions.
+//
+// Scores (:1205-1211) by v_mfma_f32_16x16x32_bf16 with the cached K rows
+// as the A operand straight from memory (lane l: row tw + 16 mt + l % 16,
+// dimensions 32 kk + 8 (l / 16) .. + 7, one 16-byte load) and the query
+// heads as B columns: column n < 8 holds bf16(q) of head n, column n + 8 the
+// rest bf16(q - bf16(q)), so the two columns' sum carries 16 significant
+// bits of q against the exact bf16 keys, accumulated in fp32.  The sum of
+// columns n and n ^ 8 (one DPP move) is the score of head n % 8 at the 4
+// positions tw + 16 mt + 4 (l / 16) + i of the lane's accumulator.
+//
+// Softmax numerators over the wave's 32 positions with the wave's own max
+// (:1212-1214), then P . V (:1215-1221) with P as the A operand: row n holds
+// head n % 8's weights split the same way (bf16(p) for n < 8, the rest for
+// n >= 8), already in the lanes that computed them; the contraction index
+// j of lane group g is position 16 (j / 4) + 4 g + j % 4.  V goes through
+// LDS (one row per position, 264 bytes, so that the 4 lane groups' reads
+// fall in different banks) and is read back per column as the B operand.
+// Rows m and m + 8 of the product (lanes l and l ^ 32) are added by one
+// transposing step.  The 4 waves' partial outputs are merged with the
+// split's max, as the split merge does across splits.
 template <int QPK>
 __global__ void __launch_bounds__(256)
 k_attn_part(AttnArgs a) {
-    constexpr int HD = 128, P = 128, SP = P + 4;
-    __shared__ __align__(16) float sc[QPK][SP];        // scores, then exp(score - max)
-    __shared__ __align__(16) float red[4][QPK * HD];   // per-wave partial outputs
+    constexpr int HD = 128, P = 128, PW = 32, VR = 132;
+    __shared__ __align__(16) uint16_t vt[4][PW * VR];   // each wave's V rows
+    __shared__ __align__(16) float red[4][QPK * HD];    // each wave's outputs
+    __shared__ float mls[4][QPK][2];                    // each wave's (max, sum)
     const int s = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int pos = a.pos[b];
     const int T = pos + 1;
     const int t0 = s * P;
     if (t0 >= T) return;                 // past this token's positions (block-uniform)
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, n = lane & 15;
+    const int tw = t0 + PW * w;
     const unsigned long long* kvp = a.kv + ((size_t)b * a.L + a.layer) * 2;
-    const uint16_t* kc = (const uint16_t*)kvp[0];
-    const uint16_t* vc = (const uint16_t*)kvp[1];
-    const int g = lane >> 4, j = lane & 15;
-    // the rows: unconditional loads (row 0 past the end)
-    uint4 kr[8], vr[8];
+    const gptr<const uint16_t> kc = (gptr<const uint16_t>)kvp[0];
+    const gptr<const uint16_t> vc = (gptr<const uint16_t>)kvp[1];
+    // requests in the order of use: the query columns (head n % 8, zero for
+    // heads >= QPK), the K rows, the V rows (unconditional: row 0 past the end)
+    const int hq = n & 7;
+    const bool lo_col = n >= 8;
+    float4 qr[4][2];
 #pragma unroll
-    for (int st = 0; st < 8; st++) {
-        const int t = t0 + 32 * w + 4 * st + g;
-        const size_t off = ((size_t)(t < T ? t : 0) * a.KH + kh) * HD + 8 * j;
-        kr[st] = *(const uint4*)(kc + off);
-        vr[st] = *(const uint4*)(vc + off);
+    for (int kk = 0; kk < 4; kk++) {
+        if (hq < QPK) {
+            const float4* qp = (const float4*)(a.qout + ((size_t)b * a.H + kh * QPK + hq) * HD + 32 * kk + 8 * g);
+            qr[kk][0] = qp[0];
+            qr[kk][1] = qp[1];
+        } else {
+            qr[kk][0] = qr[kk][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
     }
-    float q[QPK][8];
+    uint4 kr[2][4], vr[8];
 #pragma unroll
-    for (int h = 0; h < QPK; h++) {
-        const float4* qp = (const float4*)(a.qout + ((size_t)b * a.H + kh * QPK + h) * HD + 8 * j);
-        const float4 q0 = qp[0], q1 = qp[1];
-        q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
-        q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
+    for (int mt = 0; mt < 2; mt++) {
+        const int t = tw + 16 * mt + n;
+        const gptr<const uint16_t> row = kc + ((size_t)(t < T ? t : 0) * a.KH + kh) * HD + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) kr[mt][kk] = load_g16(row + 32 * kk);
     }
-
-    // ---- scores (:1205-1211): q . k / sqrtf_fast(hd)
-    constexpr int LPH = 16 / QPK;
 #pragma unroll
-    for (int st = 0; st < 8; st++) {
-        const int t = t0 + 32 * w + 4 * st + g;
-        const uint32_t kw[4] = {kr[st].x, kr[st].y, kr[st].z, kr[st].w};
-        float kf[8];
+    for (int j = 0; j < 8; j++) {
+        const int t = tw + 4 * j + g;
+        vr[j] = load_g16(vc + ((size_t)(t < T ? t : 0) * a.KH + kh) * HD + 8 * n);
+    }
+    __builtin_amdgcn_sched_barrier(0);      // keep every request ahead of the arithmetic
+    bf16x8 qb[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+        const float qv[8] = {qr[kk][0].x, qr[kk][0].y, qr[kk][0].z, qr[kk][0].w,
+                             qr[kk][1].x, qr[kk][1].y, qr[kk][1].z, qr[kk][1].w};
+        uint32_t pk[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            kf[2 * i] = __uint_as_float(kw[i] << 16);
-            kf[2 * i + 1] = __uint_as_float(kw[i] & 0xFFFF0000u);
+            uint32_t hi, lo;
+            split_bf16x2(qv[2 * i], qv[2 * i + 1], hi, lo);
+            pk[i] = lo_col ? lo : hi;
         }
-        float dots[QPK];
+        qb[kk] = __builtin_bit_cast(bf16x8, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+    }
+
+    // ---- scores: q . k / sqrtf_fast(hd)
+    floatx4 sacc[2];
 #pragma unroll
-        for (int h = 0; h < QPK; h++) {
-            float d = 0.0f;
+    for (int mt = 0; mt < 2; mt++) {
+        sacc[mt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int i = 0; i < 8; i++) d = __builtin_fmaf(q[h][i], kf[i], d);
-            dots[h] = d;
+        for (int kk = 0; kk < 4; kk++)
+            sacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[mt][kk]), qb[kk],
+                                                               sacc[mt], 0, 0, 0);
+    }
+    float sv[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float c = sacc[mt][i];
+            const float tot = __fadd_rn(c, dpp_f<DPP_ROR8>(c));
+            const int t = tw + 16 * mt + 4 * g + i;
+            const float sc = t < T ? __fdiv_rn(tot, a.sdiv) : -INFINITY;
+            sv[4 * mt + i] = sc;
+            mx = fmaxf(mx, sc);
         }
-        const float tot = head_reduce16<QPK>(dots);
-        if (j % LPH == 0) sc[j / LPH][t - t0] = t < T ? __fdiv_rn(tot, a.sdiv) : -INFINITY;
+    // over the lane groups (positions) of the column
+    mx = fmaxf(mx, swz_xor16_f(mx));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, JM_WAVE));
+    const float mref = mx == -INFINITY ? 0.0f : mx;     // a wave wholly past T
+    float l = 0.0f;
+    uint32_t pp[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float p0 = expf_fast(__fsub_rn(sv[2 * i], mref));
+        const float p1 = expf_fast(__fsub_rn(sv[2 * i + 1], mref));
+        l = __fadd_rn(__fadd_rn(l, p0), p1);
+        uint32_t hi, lo;
+        split_bf16x2(p0, p1, hi, lo);
+        pp[i] = lo_col ? lo : hi;
+    }
+    l = __fadd_rn(l, swz_xor16_f(l));
+    l = __fadd_rn(l, __shfl_xor(l, 32, JM_WAVE));
+    const bf16x8 pa = __builtin_bit_cast(bf16x8, make_uint4(pp[0], pp[1], pp[2], pp[3]));
+
+    // ---- V rows through this wave's LDS rows, read back per column
+    uint16_t* vw = vt[w];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        uint2* dst = (uint2*)(vw + (4 * j + g) * VR + 8 * n);
+        dst[0] = make_uint2(vr[j].x, vr[j].y);
+        dst[1] = make_uint2(vr[j].z, vr[j].w);
+    }
+    // LDS operations of one wave complete in order; this keeps the compiler
+    // from moving the reads above the writes
+    __asm__ volatile("" : : : "memory");
+    floatx4 oacc[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; nt++) {
+        uint32_t vb[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int j0 = 2 * i, j1 = 2 * i + 1;
+            const uint32_t e0 = vw[(16 * (j0 >> 2) + 4 * g + (j0 & 3)) * VR + 16 * nt + n];
+            const uint32_t e1 = vw[(16 * (j1 >> 2) + 4 * g + (j1 & 3)) * VR + 16 * nt + n];
+            vb[i] = e0 | (e1 << 16);
+        }
+        oacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            pa, __builtin_bit_cast(bf16x8, make_uint4(vb[0], vb[1], vb[2], vb[3])),
+            floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    }
+    // rows m (hi) and m + 8 (lo) of a head: lanes l and l ^ 32
+    float o[32];
+#pragma unroll
+    for (int nt = 0; nt < 8; nt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[4 * nt + i] = oacc[nt][i];
+    transpose_level<32, 32>(o);
+    // now o[4 nt + i] = head 4 (g % 2) + i, dimension 16 (nt + 4 (g / 2)) + n
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int hh = 4 * (g & 1) + i;
+            if (hh < QPK) red[w][hh * HD + 16 * (nt + 4 * (g >> 1)) + n] = o[4 * nt + i];
+        }
+    if (g == 0 && n < QPK) {
+        mls[w][n][0] = mx;
+        mls[w][n][1] = l;
     }
     __syncthreads();
 
-    // ---- softmax numerators over the split (:1212-1214) with the split's
-    // own max; the merge rescales by the global one
-    if (tid < QPK * 32) {
-        const int h = tid >> 5, li = tid & 31;
-        float v[4];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            v[i] = sc[h][li + 32 * i];
-            mx = fmaxf(mx, v[i]);
-        }
-        mx = seg_max<32>(mx);
-        float l = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float p = expf_fast(__fsub_rn(v[i], mx));
-            sc[h][li + 32 * i] = p;
-            l = __fadd_rn(l, p);
-        }
-        l = seg_sum<32>(l);
-        if (li == 0) {
-            float* ml = a.part_ml + ((((size_t)b * a.KH + kh) * a.S + s) * QPK + h) * 2;
-            ml[0] = mx;
-            ml[1] = l;
-        }
-    }
-    __syncthreads();
-
-    // ---- P . V (:1215-1221) over this lane's positions
-    float acc[QPK * 8];
-#pragma unroll
-    for (int i = 0; i < QPK * 8; i++) acc[i] = 0.0f;
-#pragma unroll
-    for (int st = 0; st < 8; st++) {
-        const int t = t0 + 32 * w + 4 * st + g;
-        const uint32_t vw[4] = {vr[st].x, vr[st].y, vr[st].z, vr[st].w};
-        const bool ok = t < T;
-        float vf[8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            vf[2 * i] = ok ? __uint_as_float(vw[i] << 16) : 0.0f;
-            vf[2 * i + 1] = ok ? __uint_as_float(vw[i] & 0xFFFF0000u) : 0.0f;
-        }
-#pragma unroll
-        for (int h = 0; h < QPK; h++) {
-            const float p = sc[h][t - t0];
-#pragma unroll
-            for (int i = 0; i < 8; i++) acc[h * 8 + i] = __builtin_fmaf(p, vf[i], acc[h * 8 + i]);
-        }
-    }
-    // sum over the 4 lane groups g: two transposing levels leave lane group
-    // g with values [g N/4, (g + 1) N/4) of the flat (head, dim) list
-    constexpr int N = QPK * 8;
-    transpose_level<32, N>(acc);
-    transpose_level<16, N / 2>(acc);
-#pragma unroll
-    for (int i = 0; i < N / 4; i++) {
-        const int idx = g * (N / 4) + i;
-        red[w][(idx >> 3) * HD + 8 * j + (idx & 7)] = acc[i];
-    }
-    __syncthreads();
+    // ---- the waves merged with the split's max
     float* po = a.part_o + (((size_t)b * a.KH + kh) * a.S + s) * QPK * HD;
-    for (int o = tid; o < QPK * HD; o += 256)
-        po[o] = __fadd_rn(__fadd_rn(red[0][o], red[1][o]), __fadd_rn(red[2][o], red[3][o]));
+    for (int oi = tid; oi < QPK * HD; oi += 256) {
+        const int h = oi / HD;
+        const float M = fmaxf(fmaxf(mls[0][h][0], mls[1][h][0]), fmaxf(mls[2][h][0], mls[3][h][0]));
+        float O = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) {
+            const float m = mls[ww][h][0];
+            const float f = m == -INFINITY ? 0.0f : expf_fast(__fsub_rn(m, M));
+            O = __builtin_fmaf(red[ww][oi], f, O);
+            L = __builtin_fmaf(mls[ww][h][1], f, L);
+        }
+        po[oi] = O;
+        if (oi % HD == 0) {
+            float* ml = a.part_ml + ((((size_t)b * a.KH + kh) * a.S + s) * QPK + h) * 2;
+            ml[0] = M;
+            ml[1] = L;
+        }
+    }
 }
 
 // Merge of the splits of one (query head, token): out = sum_s o_s e^(m_s - M)

@@ -97,6 +97,43 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// A device address read from memory (a table of cache addresses) is a
+// generic pointer to the compiler, which then emits flat loads: these also
+// count against the LDS counter, so that every LDS wait waits for them.  As
+// global pointers they become global loads.
+template <typename T>
+using gptr = T __attribute__((address_space(1)))*;
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16 bytes at a global address (16-byte aligned)
+__device__ __forceinline__ uint4 load_g16(gptr<const uint16_t> p) {
+    const u32x4_t v = *(gptr<const u32x4_t>)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ------------------------------------------------- bf16 matrix-core operands
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Two floats as packed bf16, rounded to nearest even (v_cvt_pk_bf16_f32;
+// a and b finite).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    const bf16x2_t h = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// The two-term bf16 split of a and b: hi = bf16(v), lo = bf16(v - hi), each
+// packed (a in the low half).  hi + lo is within 2^-18 |v| of v, so a product
+// taken as hi*w + lo*w with exact bf16 w and fp32 accumulation keeps
+// float32-level accuracy.
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t& hi, uint32_t& lo) {
+    hi = pack_bf16x2(a, b);
+    lo = pack_bf16x2(__fsub_rn(a, __uint_as_float(hi << 16)), __fsub_rn(b, __uint_as_float(hi & 0xFFFF0000u)));
+}
+
 // SiLU(g) * u exactly as the reference writes it: (g / (1 + e^-g)) * u.
 __device__ __forceinline__ float swiglu(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_fast(-g))), u);
