@@ -84,7 +84,7 @@ int jm::store_reserve(jm_store* s, int B) {
         4,                            // n_tiles
         nslot * m * 4,                // act
         nslot * words_m * 4,          // adig
-        nslot * (m / 8) * 4,          // ascale
+        nslot * (m / 32) * 4,         // ascale
         nslot * d * 4,                // y
         nslot * m * 2,                // act_h
         nslot * m * 2,                // act_l

@@ -331,6 +331,24 @@ __device__ __forceinline__ void encode_group_wave(float v, bool store, uint32_t*
     if (store && i == 0) *scale = s;
 }
 
+// Digits of the 8 values in lanes 0..7 of the wave with the digit scale of
+// a larger group, whose max |value| is mx (nf: the group holds a non-finite
+// value, whose scale is NaN).  Digit plane k's word of these 8 values goes
+// to dig[4 k]: the caller offsets dig by the word's place in the group.
+template <int NDIG>
+__device__ __forceinline__ void encode_digits_shared(float v, float mx, bool nf, bool store,
+                                                     uint32_t* __restrict__ dig) {
+    const int i = threadIdx.x & 7;
+    const float inv = (mx > 0.0f && !nf) ? __fdiv_rn((float)Digits<NDIG>::R, mx) : 0.0f;
+    int dg[NDIG];
+    split_digits<NDIG>((int)rintf(__fmul_rn(v, inv)), dg);
+#pragma unroll
+    for (int k = 0; k < NDIG; k++) {
+        const int word = seg_or<8>((dg[k] & 15) << (4 * i));
+        if (store && i == 0) dig[4 * k] = (uint32_t)word;
+    }
+}
+
 // ---------------------------------------------------------- router top-k
 
 // Float max over the whole wave; every lane gets the result (non-NaN

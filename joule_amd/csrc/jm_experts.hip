@@ -31,7 +31,8 @@
 // base-16 digits of an exact integer a = rint(x / s), so sum (q - 8) * a is
 // exact; it is scaled by s * (fp16 weight scale) in fp32.  Token digits come
 // in groups of G values (one scale per weight group); act digits in groups
-// of 8 (one scale per gate/up wave item).
+// of 32 (one scale per chunk of a down row: the 4 gate/up wave items of a
+// block, which hold 32 consecutive rows of one slot, share it).
 #include "jm_device.h"
 #include "jm_kernels.h"
 #include "jm_q4dot.h"
@@ -59,7 +60,18 @@ struct ChunkDigits {
     float s;
 };
 
-constexpr int GU_ROWS = 8;     // gate/up rows per wave item = act values per act scale
+// Exact sum over a 32-value chunk of (q - 8) * a for weights f (signed
+// nibbles) and one token's digits of the chunk (Horner over the digit
+// planes: v_dot8 accumulates in place, so one chain needs one zero).
+template <int NDIG>
+__device__ __forceinline__ int chunk_dot(const uint4& f, const ChunkDigits<NDIG>& cd) {
+    int iv = 0;
+#pragma unroll
+    for (int k = NDIG - 1; k >= 0; k--) iv = chunk_digit(f, cd.d[k], iv);
+    return iv;
+}
+
+constexpr int GU_ROWS = 8;     // gate/up rows per wave item (a block's 4 items share an act scale)
 constexpr int DN_ROWS = 16;    // down rows per wave item
 
 // ------------------------------------------------------------------ gate/up
@@ -69,6 +81,8 @@ __global__ void __launch_bounds__(256)
 k_gateup(ExpertArgs a) {
     constexpr int RPI = JM_WAVE / LPR;
     constexpr int S = GU_ROWS / RPI;
+    __shared__ float gmax[2][4];       // per token parity: each wave's max |act|
+    __shared__ int gbad[2][4];         // and whether it saw a non-finite value
     const int lane = threadIdx.x & 63;
     const int item = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nchunk = a.m / GU_ROWS;
@@ -116,6 +130,26 @@ k_gateup(ExpertArgs a) {
         grp[q] = chk[q] * 32 / G;
         half[q] = (chk[q] * 32 % G) / 32;
     }
+    auto load_tok = [&](ChunkDigits<NDIG> (&td)[QC], int slot) {
+        const size_t b = (size_t)(slot / a.topk);
+#pragma unroll
+        for (int q = 0; q < QC; q++) {
+            const size_t gi = b * ngroups + grp[q];
+            const uint4* p = (const uint4*)(a.xdig + gi * (NDIG * (G / 8))) + half[q];
+#pragma unroll
+            for (int k = 0; k < NDIG; k++) td[q].d[k] = p[k * (G / 32)];
+            td[q].s = a.xscale[gi];
+        }
+    };
+
+    // requests in the order of use: the first token's digits, then the
+    // weight rows step by step.  The memory counter retires loads in order,
+    // so the first token's arithmetic on step s waits only for the loads up
+    // to step s while the later steps' rows are still arriving.
+    ChunkDigits<NDIG> cur[QC], nxt[QC];
+    int slot = next_slot();
+    load_tok(cur, slot);
+    __builtin_amdgcn_sched_barrier(0);
     uint4 wg[S][QC], wu[S][QC];
     uint16_t hg[S][QC], hu[S][QC];
 #pragma unroll
@@ -130,77 +164,90 @@ k_gateup(ExpertArgs a) {
             hu[s][q] = sc_u[(size_t)row * ngroups + grp[q]];
         }
     }
-
-    auto load_tok = [&](ChunkDigits<NDIG> (&td)[QC], int slot) {
-        const size_t b = (size_t)(slot / a.topk);
-#pragma unroll
-        for (int q = 0; q < QC; q++) {
-            const size_t gi = b * ngroups + grp[q];
-            const uint4* p = (const uint4*)(a.xdig + gi * (NDIG * (G / 8))) + half[q];
-#pragma unroll
-            for (int k = 0; k < NDIG; k++) td[q].d[k] = p[k * (G / 32)];
-            td[q].s = a.xscale[gi];
-        }
-    };
-
-    // keep every weight load ahead of the first token's digits and of all
-    // arithmetic: waiting for the digits then also waits for the weights
-    // (the memory counter retires loads in order), but nothing is issued late
     __builtin_amdgcn_sched_barrier(0);
-    ChunkDigits<NDIG> cur[QC], nxt[QC];
-    int slot = next_slot();
-    load_tok(cur, slot);
-    __builtin_amdgcn_sched_barrier(0);
-    // signed nibbles once, for every token
-#pragma unroll
-    for (int s = 0; s < S; s++)
-#pragma unroll
-        for (int q = 0; q < QC; q++) { wg[s][q] = flip_nibbles(wg[s][q]); wu[s][q] = flip_nibbles(wu[s][q]); }
 
     // after transpose_sum, row i = s * RPI + r of the item is in lanes
     // LPR * r + 8 * s (gate) and + 4 (up)
     const int i8 = lane & 7;
     const int src = LPR * (i8 % RPI) + 8 * (i8 / RPI);
-    for (int t = 0; t < n; t++) {
-        int nslot = 0;
-        if (t + 1 < n) {
-            nslot = next_slot();
-            load_tok(nxt, nslot);
-        }
-        float part[2 * S];                   // value 2s + m: step s, m = 0 gate, 1 up
+    // the item's gate and up partial sums (value 2s + m: step s, m = 0 gate,
+    // 1 up) for one token.  The first token takes the steps in order with a
+    // scheduling barrier after each, turning each step's rows into signed
+    // nibbles (q - 8) in place, so that its arithmetic on step s waits only
+    // for the loads up to step s; the later tokens reuse the signed rows.
+    auto parts = [&](const ChunkDigits<NDIG> (&cd)[QC], float (&part)[2 * S], auto first) {
 #pragma unroll
         for (int s = 0; s < S; s++) {
             float pg = 0.0f, pu = 0.0f;
 #pragma unroll
             for (int q = 0; q < QC; q++) {
+                if constexpr (decltype(first)::value) {
+                    wg[s][q] = flip_nibbles(wg[s][q]);
+                    wu[s][q] = flip_nibbles(wu[s][q]);
+                }
                 int ig = 0, iu = 0;
 #pragma unroll
                 for (int k = NDIG - 1; k >= 0; k--) {
-                    ig = chunk_digit(wg[s][q], cur[q].d[k], ig);
-                    iu = chunk_digit(wu[s][q], cur[q].d[k], iu);
+                    ig = chunk_digit(wg[s][q], cd[q].d[k], ig);
+                    iu = chunk_digit(wu[s][q], cd[q].d[k], iu);
                 }
-                const float xs = live[q] ? cur[q].s : 0.0f;
+                const float xs = live[q] ? cd[q].s : 0.0f;
                 pg = __fadd_rn(pg, __fmul_rn((float)ig, __fmul_rn(xs, fp16_hw(hg[s][q]))));
                 pu = __fadd_rn(pu, __fmul_rn((float)iu, __fmul_rn(xs, fp16_hw(hu[s][q]))));
             }
             part[2 * s] = pg;
             part[2 * s + 1] = pu;
+            if constexpr (decltype(first)::value) __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    // SwiGLU of the item's 8 rows for the token of slot sl: the 8 act values
+    // to lanes 0..7, then fp32 act and their digits.  The 4 waves of the
+    // block hold rows 32 cb .. 32 cb + 31 of the same slot (items 4 cb ..
+    // 4 cb + 3) and share one digit scale: the maxima meet in LDS (a
+    // block-uniform barrier: the waves have the same slot and token count).
+    const int wib = c & 3, cb = c >> 2;
+    auto finish = [&](float (&part)[2 * S], int sl, int t) {
         static_assert(2 * S == LPR / 4, "one transposed value per 4 lanes");
         const float tot = transpose_sum<LPR>(part);
         const float up = dpp_f<DPP_ROL4>(tot);          // lanes with bit 2 clear: gate here, up 4 lanes on
         const float av = swiglu(tot, up);
-        // the item's 8 act values to lanes 0..7, then fp32 act and one
-        // 8-value digit group
         const float mine = __shfl(av, src, JM_WAVE);
-        if (lane < 8) a.act[(size_t)slot * a.m + c * GU_ROWS + lane] = mine;
-        const size_t ai = (size_t)slot * (a.m / 8) + c;
-        encode_group_wave<8, NDIG>(mine, lane < 8, a.adig + ai * NDIG, a.ascale + ai);
-        if (t + 1 < n) {
-            slot = nslot;
-#pragma unroll
-            for (int q = 0; q < QC; q++) cur[q] = nxt[q];
+        if (lane < 8) a.act[(size_t)sl * a.m + c * GU_ROWS + lane] = mine;
+        const float am = lane < 8 ? fabsf(mine) : 0.0f;
+        const int bad = seg_or<8>(!(am <= 3.4028235e38f) ? 1 : 0);
+        const float mx8 = seg_max<8>(am);
+        if (lane == 0) {
+            gmax[t & 1][wib] = mx8;
+            gbad[t & 1][wib] = bad;
         }
+        __syncthreads();
+        const float mx = fmaxf(fmaxf(gmax[t & 1][0], gmax[t & 1][1]), fmaxf(gmax[t & 1][2], gmax[t & 1][3]));
+        const bool nf = (gbad[t & 1][0] | gbad[t & 1][1] | gbad[t & 1][2] | gbad[t & 1][3]) != 0;
+        const size_t gi = (size_t)sl * (a.m / 32) + cb;
+        encode_digits_shared<NDIG>(mine, mx, nf, lane < 8, a.adig + gi * (NDIG * 4) + wib);
+        if (wib == 0 && lane == 0) a.ascale[gi] = digit_scale<NDIG>(mx, nf);
+    };
+    int nslot = 0;
+    if (n > 1) {
+        nslot = next_slot();
+        load_tok(nxt, nslot);
+    }
+    {
+        float part[2 * S];
+        parts(cur, part, std::true_type{});
+        finish(part, slot, 0);
+    }
+    for (int t = 1; t < n; t++) {
+        slot = nslot;
+#pragma unroll
+        for (int q = 0; q < QC; q++) cur[q] = nxt[q];
+        if (t + 1 < n) {
+            nslot = next_slot();
+            load_tok(nxt, nslot);
+        }
+        float part[2 * S];
+        parts(cur, part, std::false_type{});
+        finish(part, slot, t);
     }
 }
 
@@ -248,28 +295,23 @@ k_down(ExpertArgs a) {
         }
     }
 
-    // act digits of a chunk: 4 groups of 8 values, NDIG words each, 4 scales
-    auto load_act = [&](uint32_t (&dg)[QC][4][NDIG], float4 (&sc)[QC], int slot) {
+    // act digits of a chunk (32 values, one scale)
+    auto load_act = [&](ChunkDigits<NDIG> (&ad)[QC], int slot) {
 #pragma unroll
         for (int q = 0; q < QC; q++) {
-            const size_t ai = (size_t)slot * (a.m / 8) + (size_t)chk[q] * 4;
-            const uint4* p = (const uint4*)(a.adig + ai * NDIG);
+            const size_t gi = (size_t)slot * (a.m / 32) + chk[q];
+            const uint4* p = (const uint4*)(a.adig + gi * (NDIG * 4));
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                static_assert(NDIG == 4, "act digit loads assume 4 digits (one uint4 per 8 values)");
-                const uint4 v = p[j];
-                dg[q][j][0] = v.x; dg[q][j][1] = v.y; dg[q][j][2] = v.z; dg[q][j][3] = v.w;
-            }
-            sc[q] = *(const float4*)(a.ascale + ai);
+            for (int k = 0; k < NDIG; k++) ad[q].d[k] = p[k];
+            ad[q].s = a.ascale[gi];
         }
     };
 
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t cd[QC][4][NDIG], nd[QC][4][NDIG];
-    float4 cs[QC], ns[QC];
+    ChunkDigits<NDIG> cd[QC], nd[QC];
     int slot = ts.next();
     float wt = a.tw[slot];
-    load_act(cd, cs, slot);
+    load_act(cd, slot);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < S; s++)
@@ -282,7 +324,7 @@ k_down(ExpertArgs a) {
         if (t + 1 < wk.n) {
             nslot = ts.next();
             nwt = a.tw[nslot];
-            load_act(nd, ns, nslot);
+            load_act(nd, nslot);
         }
         float part[S];
 #pragma unroll
@@ -290,17 +332,8 @@ k_down(ExpertArgs a) {
             float ps = 0.0f;
 #pragma unroll
             for (int q = 0; q < QC; q++) {
-                const uint32_t fw[4] = {wd[s][q].x, wd[s][q].y, wd[s][q].z, wd[s][q].w};
-                const float sj[4] = {cs[q].x, cs[q].y, cs[q].z, cs[q].w};
-                float acc = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    int iv = 0;
-#pragma unroll
-                    for (int k = NDIG - 1; k >= 0; k--) iv = dot8(fw[j], cd[q][j][k], iv << 4);
-                    acc = __fadd_rn(acc, __fmul_rn((float)iv, sj[j]));
-                }
-                ps = __fadd_rn(ps, live[q] ? __fmul_rn(acc, fp16_hw(hd[s][q])) : 0.0f);
+                const int iv = chunk_dot(wd[s][q], cd[q]);
+                ps = __builtin_fmaf((float)iv, live[q] ? __fmul_rn(cd[q].s, fp16_hw(hd[s][q])) : 0.0f, ps);
             }
             part[s] = ps;
         }
@@ -313,13 +346,7 @@ k_down(ExpertArgs a) {
             slot = nslot;
             wt = nwt;
 #pragma unroll
-            for (int q = 0; q < QC; q++) {
-                cs[q] = ns[q];
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-#pragma unroll
-                    for (int k = 0; k < NDIG; k++) cd[q][j][k] = nd[q][j][k];
-            }
+            for (int q = 0; q < QC; q++) cd[q] = nd[q];
         }
     }
 }
@@ -387,23 +414,18 @@ k_down_comb(ExpertArgs a) {
         chk[q] = live[q] ? ch : 0;
         grp[q] = chk[q] * 32 / G;
     }
-    // act digits of a chunk: 4 groups of 8 values, NDIG words each, 4 scales
+    // act digits of a chunk (32 values, one scale)
     struct Act {
-        uint32_t dg[QC][4][NDIG];
-        float4 sc[QC];
+        ChunkDigits<NDIG> c[QC];
     };
     auto load_act = [&](Act& ad, int slot) {
 #pragma unroll
         for (int q = 0; q < QC; q++) {
-            const size_t ai = (size_t)slot * (a.m / 8) + (size_t)chk[q] * 4;
-            const uint4* p = (const uint4*)(a.adig + ai * NDIG);
+            const size_t gi = (size_t)slot * (a.m / 32) + chk[q];
+            const uint4* p = (const uint4*)(a.adig + gi * (NDIG * 4));
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                static_assert(NDIG == 4, "act digit loads assume 4 digits (one uint4 per 8 values)");
-                const uint4 v = p[j];
-                ad.dg[q][j][0] = v.x; ad.dg[q][j][1] = v.y; ad.dg[q][j][2] = v.z; ad.dg[q][j][3] = v.w;
-            }
-            ad.sc[q] = *(const float4*)(a.ascale + ai);
+            for (int k = 0; k < NDIG; k++) ad.c[q].d[k] = p[k];
+            ad.c[q].s = a.ascale[gi];
         }
     };
     struct Rows {
@@ -436,18 +458,8 @@ k_down_comb(ExpertArgs a) {
             float ps = 0.0f;
 #pragma unroll
             for (int q = 0; q < QC; q++) {
-                const uint4 f = flip_nibbles(rw.wd[s][q]);
-                const uint32_t fw[4] = {f.x, f.y, f.z, f.w};
-                const float sj[4] = {ad.sc[q].x, ad.sc[q].y, ad.sc[q].z, ad.sc[q].w};
-                float acc = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    int iv = 0;
-#pragma unroll
-                    for (int kk = NDIG - 1; kk >= 0; kk--) iv = dot8(fw[j], ad.dg[q][j][kk], iv << 4);
-                    acc = __builtin_fmaf((float)iv, sj[j], acc);
-                }
-                ps = __builtin_fmaf(acc, live[q] ? fp16_hw(rw.hd[s][q]) : 0.0f, ps);
+                const int iv = chunk_dot(flip_nibbles(rw.wd[s][q]), ad.c[q]);
+                ps = __builtin_fmaf((float)iv, live[q] ? __fmul_rn(ad.c[q].s, fp16_hw(rw.hd[s][q])) : 0.0f, ps);
             }
             part[s] = ps;
         }

@@ -51,8 +51,8 @@ struct ExpertArgs {
     const uint32_t* xdig;     // [B][d/G][NDIG][G/8] token digits
     const float* xscale;      // [B][d/G]
     float* act;               // [B*k][m]   SiLU(gate)*up per slot
-    uint32_t* adig;           // [B*k][m/8][NDIG] act digits, 8 values per group
-    float* ascale;            // [B*k][m/8]
+    uint32_t* adig;           // [B*k][m/32][NDIG][4] act digits, 32 values per group (word j: values 8j..8j+7)
+    float* ascale;            // [B*k][m/32]
     float* y;                 // [B*k][d]   weighted expert output per slot (dispatch path)
     float* out;               // [B][d]     block output
     const float* resid;       // [B][d]     added to the block output (NULL: none); may alias out
