@@ -152,7 +152,7 @@ __device__ __forceinline__ float bf16_round(float f) { return __uint_as_float(f3
 // The projections of one head of one token finished: the column slices
 // summed, times the RMSNorm row scale of h, plus the bias (:1126-1145); for
 // q and k heads the per-head RMSNorm (:1174-1189) and RoPE rotate-half at
-// the token's position (:1190-1194, :259-266).  q heads go to qout; k and v
+// the token's position (:1190-1194, :259-266).  q heads go to qsplit; k and v
 // heads are appended to the bf16 cache at the position (:1195-1199).
 // Block (head in q.., k.., v.., token), one thread per dimension.
 __global__ void __launch_bounds__(128)
@@ -210,7 +210,12 @@ k_qkv_fin(AttnArgs a) {
     const float c = a.cos[(size_t)pos * HD + ci], sn = a.sin[(size_t)pos * HD + ci];
     const float o = lo ? __builtin_fmaf(v, c, -__fmul_rn(other, sn)) : __builtin_fmaf(other, sn, __fmul_rn(v, c));
     if (isq) {
-        a.qout[((size_t)b * a.H + hh) * HD + t] = o;
+        // split for the attention's matrix cores: hi = bf16(q), lo = bf16(q - hi)
+        const uint32_t hi = f32_to_bf16_rne(o);
+        const uint32_t lo = f32_to_bf16_rne(__fsub_rn(o, __uint_as_float(hi << 16)));
+        uint16_t* qs = a.qsplit + ((size_t)b * a.H + hh) * 2 * HD;
+        qs[t] = (uint16_t)hi;
+        qs[HD + t] = (uint16_t)lo;
     } else {
         const gptr<uint16_t> kc = (gptr<uint16_t>)kvp[0];
         kc[((size_t)pos * a.KH + (hh - a.H)) * HD + t] = (uint16_t)f32_to_bf16_rne(o);
@@ -226,8 +231,9 @@ k_qkv_fin(AttnArgs a) {
 // as the A operand straight from memory (lane l: row tw + 16 mt + l % 16,
 // dimensions 32 kk + 8 (l / 16) .. + 7, one 16-byte load) and the query
 // heads as B columns: column n < 8 holds bf16(q) of head n, column n + 8 the
-// rest bf16(q - bf16(q)), so the two columns' sum carries 16 significant
-// bits of q against the exact bf16 keys, accumulated in fp32.  The sum of
+// rest bf16(q - bf16(q)) (split by k_qkv_fin), so the two columns' sum
+// carries 16 significant bits of q against the exact bf16 keys, accumulated
+// in fp32.  The sum of
 // columns n and n ^ 8 (one DPP move) is the score of head n % 8 at the 4
 // positions tw + 16 mt + 4 (l / 16) + i of the lane's accumulator.
 //
@@ -260,19 +266,16 @@ k_attn_part(AttnArgs a) {
     const gptr<const uint16_t> kc = (gptr<const uint16_t>)kvp[0];
     const gptr<const uint16_t> vc = (gptr<const uint16_t>)kvp[1];
     // requests in the order of use: the query columns (head n % 8, zero for
-    // heads >= QPK), the K rows, the V rows (unconditional: row 0 past the end)
+    // heads >= QPK; the hi half of the split for n < 8, the lo half above),
+    // the K rows, the V rows (unconditional: row 0 past the end)
     const int hq = n & 7;
     const bool lo_col = n >= 8;
-    float4 qr[4][2];
+    uint4 qr[4];
+    {
+        const uint16_t* qp = a.qsplit + (((size_t)b * a.H + kh * QPK + (hq < QPK ? hq : 0)) * 2 + (lo_col ? 1 : 0)) * HD + 8 * g;
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++) {
-        if (hq < QPK) {
-            const float4* qp = (const float4*)(a.qout + ((size_t)b * a.H + kh * QPK + hq) * HD + 32 * kk + 8 * g);
-            qr[kk][0] = qp[0];
-            qr[kk][1] = qp[1];
-        } else {
-            qr[kk][0] = qr[kk][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
+        for (int kk = 0; kk < 4; kk++)
+            qr[kk] = hq < QPK ? *(const uint4*)(qp + 32 * kk) : make_uint4(0u, 0u, 0u, 0u);
     }
     uint4 kr[2][4], vr[8];
 #pragma unroll
@@ -290,18 +293,7 @@ k_attn_part(AttnArgs a) {
     __builtin_amdgcn_sched_barrier(0);      // keep every request ahead of the arithmetic
     bf16x8 qb[4];
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++) {
-        const float qv[8] = {qr[kk][0].x, qr[kk][0].y, qr[kk][0].z, qr[kk][0].w,
-                             qr[kk][1].x, qr[kk][1].y, qr[kk][1].z, qr[kk][1].w};
-        uint32_t pk[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint32_t hi, lo;
-            split_bf16x2(qv[2 * i], qv[2 * i + 1], hi, lo);
-            pk[i] = lo_col ? lo : hi;
-        }
-        qb[kk] = __builtin_bit_cast(bf16x8, make_uint4(pk[0], pk[1], pk[2], pk[3]));
-    }
+    for (int kk = 0; kk < 4; kk++) qb[kk] = __builtin_bit_cast(bf16x8, qr[kk]);
 
     // ---- scores: q . k / sqrtf_fast(hd)
     floatx4 sacc[2];

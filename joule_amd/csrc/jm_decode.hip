@@ -67,7 +67,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
         (size_t)B * S * hq * 4,                   // part_o: H heads x hd per split
         (size_t)B * S * (hq / HD) * 2 * 4,        // part_ml
         (size_t)B * hq * 4,                       // att
-        (size_t)B * hq * 4,                       // qout
+        (size_t)B * hq * 2 * 2,                   // qsplit
         (size_t)B * d * 4,                        // hid
         (size_t)B * d * 4,                        // xemb: embedded prompt tokens (prefill)
         (size_t)jm::lm_blocks(V) * B * 4,         // lmv
@@ -82,7 +82,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     JM_HIP(hipMalloc(&s->dws, total), "hipMalloc decode workspace");
     char* p = (char*)s->dws;
     void** slots[] = {(void**)&s->h, (void**)&s->h2, (void**)&s->qkv, (void**)&s->opart, (void**)&s->part_o,
-                      (void**)&s->part_ml, (void**)&s->att, (void**)&s->qout, (void**)&s->hid, (void**)&s->xemb, (void**)&s->lmv,
+                      (void**)&s->part_ml, (void**)&s->att, (void**)&s->qsplit, (void**)&s->hid, (void**)&s->xemb, (void**)&s->lmv,
                       (void**)&s->lmi, (void**)&s->tab};
     for (size_t i = 0; i < sizeof sz / sizeof sz[0]; i++) {
         *slots[i] = p;
@@ -164,7 +164,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         at.eps = c->eps; at.sdiv = sdiv;
         at.cos = W->cos; at.sin = W->sin;
         at.pos = pos_dev; at.kv = s->tab; at.L = L; at.layer = l;
-        at.qout = s->qout; at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;
+        at.qsplit = s->qsplit; at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;
         // the grid covers the longest token's splits; the buffers hold S_cap
         // per (token, KV head), indexed with the call's S
         JM_HIP(jm::launch_attn(at, qpk, s->att, st), "attention launch");

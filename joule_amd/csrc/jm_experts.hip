@@ -354,7 +354,13 @@ k_down(ExpertArgs a) {
 // ---------------------------------------------------------- down + combine
 
 constexpr int DC_ROWS = 8;             // hidden rows per block
-constexpr int DC_THREADS = 768;
+#ifndef JM_DC_THREADS
+#define JM_DC_THREADS 768
+#endif
+#ifndef JM_DC_NR
+#define JM_DC_NR 2
+#endif
+constexpr int DC_THREADS = JM_DC_THREADS;
 constexpr int DC_WAVES = DC_THREADS / 64;
 
 // Decode path: block c owns hidden rows [c * DC_ROWS, (c + 1) * DC_ROWS) of
@@ -372,7 +378,7 @@ k_down_comb(ExpertArgs a) {
     constexpr int RPI = JM_WAVE / LPR;          // rows per load instruction
     constexpr int S = R / RPI;                  // load steps per expert
     static_assert(S >= 1 && S * RPI == R, "whole rows per step");
-    constexpr int NR = 2;                       // experts in flight per wave
+    constexpr int NR = JM_DC_NR;                // experts in flight per wave
     static_assert(JM_DEC_SLOTS <= DC_THREADS, "a slot per thread");
     __shared__ int top_l[JM_DEC_SLOTS], ulist[JM_DEC_SLOTS], comb_l[JM_DEC_SLOTS];
     __shared__ int first_l[JM_MAX_E];

@@ -175,7 +175,7 @@ struct AttnArgs {
     const int* pos;           // [B] position each token writes (T = pos + 1)
     const unsigned long long* kv;   // [B*L][2] bf16 k, v caches [maxT][KH][128]
     int L, layer;
-    float* qout;              // [B][H][128] the finished query heads
+    uint16_t* qsplit;         // [B][H][2][128] bf16 the finished query heads: hi = bf16(q), lo = bf16(q - hi)
     int S;                    // splits the partial buffers hold per (token, KV head)
     float* part_o;            // [B][KH][S][H/KH][128]
     float* part_ml;           // [B][KH][S][H/KH][2]

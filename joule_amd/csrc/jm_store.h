@@ -83,7 +83,7 @@ struct jm_store {
     float* part_o;              // [B][KH][S][H/KH][hd] attention partials per position split
     float* part_ml;             // [B][KH][S][H/KH][2] their (max, sum)
     float* att;                 // [B][H hd] attention output
-    float* qout;                // [B][H hd] finished query heads
+    uint16_t* qsplit;           // [B][H][2][hd] finished query heads, bf16 hi and lo
     float* hid;                 // [B][d] final-normed hidden state (when the caller passes none)
     float* xemb;                // [B][d] embedded prompt tokens (jm_prefill_layers)
     float* lmv;                 // [lm blocks][B] per-block best logit (argmax)
