@@ -2,7 +2,8 @@
 
     python -m joule_amd.build
 
-compiles joule_amd/csrc/*.hip into joule_amd/libjoule_amd.so with hipcc.
+compiles joule_amd/csrc/*.hip (objects under joule_amd/_build/) into
+joule_amd/libjoule_amd.so with hipcc.
 Flags: -ffp-contract=off (fused multiply-adds are written explicitly where
 the reference arithmetic has them) and packed FP32 instructions disabled.
 """
@@ -13,6 +14,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -36,9 +38,7 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP library cannot be built")
 
 
-def build(verbose: bool = False) -> Path:
-    tmp = OUT.with_suffix(".so.tmp")
-    cmd = [hipcc(), *FLAGS, *map(str, SRC), "-o", str(tmp)]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -48,6 +48,22 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError("hipcc failed:\n" + "\n".join(noise))
     if noise and verbose:
         print("\n".join(noise), file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile each source to an object in parallel (one process per file),
+    then link the shared library."""
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    objs = [objdir / (src.stem + ".o") for src in SRC]
+    jobs = [[hipcc(), *compile_flags, "-c", str(src), "-o", str(obj)] for src, obj in zip(SRC, objs)]
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        for fut in [ex.submit(_run, cmd, verbose) for cmd in jobs]:
+            fut.result()
+    tmp = OUT.with_suffix(".so.tmp")
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, OUT)
     return OUT
 

@@ -151,6 +151,7 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     r.work = s->work; r.umax = umax; r.rec = s->rec;
     r.key0 = (long long)layer * E;
     r.dense_min = s->dense_min; r.tiles = s->tiles; r.n_tiles = s->n_tiles;
+    r.skip_topk = dec && jm::gateup_topk(B, E);
     jm::ExpertArgs a;
     a.blob = s->blob; a.rec = s->rec; a.key0 = (long long)layer * E; a.E = E;
     a.work = s->work; a.umax = umax; a.seg_slot = s->seg_slot;
@@ -164,6 +165,7 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     r.xsh = dec ? nullptr : s->xsh; r.xsl = dec ? nullptr : s->xsl;
     a.xsh = s->xsh; a.xsl = s->xsl;
     a.act_h = s->act_h; a.act_l = s->act_l;
+    a.logits = s->logits; a.renorm = s->renorm; a.top_w = s->top; a.tw_w = s->tw;
     const int max_tiles = nslot / JM_DENSE_TILE + E;
 #define JM_MARK(i) if (s->prof && stage_marks) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
     JM_MARK(0);

@@ -1,7 +1,9 @@
 // Grouped Q4 expert product of the MoE block (gfx950).
 //
 // Decode path (B * topk <= 256 slots), two launches after the routing:
-//   k_gateup<BALLOT>  per (slot, 8 intermediate rows), one wave; the wave of
+//   k_gateup<BALLOT>  per (slot, 8 intermediate rows), one wave (for batches
+//                     of up to JM_GU_TOPK_MAX_B tokens each block of 4 waves
+//                     first computes the top-k of every token); the wave of
 //                     an expert's first slot finds all its slots by a ballot
 //                     over the top-k table (others exit) and computes
 //                     g = gate_row . x, u = up_row . x for each of them,
@@ -76,7 +78,12 @@ constexpr int DN_ROWS = 16;    // down rows per wave item
 
 // ------------------------------------------------------------------ gate/up
 
-template <int G, int NDIG, int LPR, int QC, bool BALLOT>
+// EPL > 0 (decode path, small batches): the block first computes the top-k
+// of every token from the router scores itself (softmax, top-k and renorm as
+// k_topk: decode_kernel.c:1425-1448, topk_wave), its 4 waves taking tokens
+// w, w + 4, ...; block 0 also writes the table for the down kernel and the
+// caller.  This replaces the top-k launch.
+template <int G, int NDIG, int LPR, int QC, bool BALLOT, int EPL>
 __global__ void __launch_bounds__(256)
 k_gateup(ExpertArgs a) {
     constexpr int RPI = JM_WAVE / LPR;
@@ -84,7 +91,8 @@ k_gateup(ExpertArgs a) {
     __shared__ float gmax[2][4];       // per token parity: each wave's max |act|
     __shared__ int gbad[2][4];         // and whether it saw a non-finite value
     const int lane = threadIdx.x & 63;
-    const int item = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int item = blockIdx.x * 4 + wave;
     const int nchunk = a.m / GU_ROWS;
     const int u = item / nchunk, c = item % nchunk;
     // the expert, its record offsets and its slots
@@ -92,10 +100,27 @@ k_gateup(ExpertArgs a) {
     int n;
     BallotSlots bs;
     TableSlots ts;
+    const int* top = a.top;
+    if constexpr (BALLOT && EPL > 0) {
+        constexpr int EP = EPL > 0 ? EPL : 1;
+        __shared__ int top_s[JM_DEC_SLOTS];
+        __shared__ float tw_s[JM_DEC_SLOTS];
+        __shared__ float p_s[4][64 * EP];
+        for (int b = wave; b < a.B; b += 4)
+            topk_wave<EP>(a.logits + (size_t)b * a.E, a.E, a.topk, a.renorm, p_s[wave],
+                          top_s + b * a.topk, tw_s + b * a.topk);
+        __syncthreads();
+        if (blockIdx.x == 0)
+            for (int i = threadIdx.x; i < a.nslot; i += 256) {
+                a.top_w[i] = top_s[i];
+                a.tw_w[i] = tw_s[i];
+            }
+        top = top_s;
+    }
     if constexpr (BALLOT) {
         if (u >= a.nslot) return;
         int e;
-        if (!bs.init(a.top, a.nslot, a.E, u, &e)) return;
+        if (!bs.init(top, a.nslot, a.E, u, &e)) return;
         n = bs.n;
         a.rec.get(0, a.key0 + e, so_g, po_g);
         a.rec.get(1, a.key0 + e, so_u, po_u);
@@ -556,14 +581,14 @@ static inline void row_lanes(int C, int* lpr, int* qc) {
     *lpr = raw <= 16 ? 16 : raw <= 32 ? 32 : 64;
 }
 
-template <bool BALLOT>
+template <bool BALLOT, int EPL>
 static hipError_t gateup_launch(const ExpertArgs& a, long long items, hipStream_t st) {
     const long long waves = items * (a.m / GU_ROWS);
     if (waves == 0) return hipSuccess;
     const dim3 grid((unsigned)((waves + 3) / 4));
     int lpr, qc;
     row_lanes(a.d, &lpr, &qc);
-#define JM_GU(GG, L, Q) hipLaunchKernelGGL((k_gateup<GG, JM_NDIG, L, Q, BALLOT>), grid, dim3(256), 0, st, a)
+#define JM_GU(GG, L, Q) hipLaunchKernelGGL((k_gateup<GG, JM_NDIG, L, Q, BALLOT, EPL>), grid, dim3(256), 0, st, a)
 #define JM_GUG(GG) if (qc == 2) JM_GU(GG, 64, 2); else if (lpr == 64) JM_GU(GG, 64, 1); \
                    else if (lpr == 32) JM_GU(GG, 32, 1); else JM_GU(GG, 16, 1);
     if (qc > 2) return hipErrorInvalidValue;
@@ -574,12 +599,16 @@ static hipError_t gateup_launch(const ExpertArgs& a, long long items, hipStream_
 }
 
 hipError_t launch_gateup(const ExpertArgs& a, int umax, hipStream_t st) {
-    return gateup_launch<false>(a, umax, st);
+    return gateup_launch<false, 0>(a, umax, st);
 }
+
+bool gateup_topk(int B, int E) { return B <= JM_GU_TOPK_MAX_B && E <= JM_MAX_E; }
 
 hipError_t launch_gateup_dec(const ExpertArgs& a, hipStream_t st) {
     if (a.nslot > JM_DEC_SLOTS) return hipErrorInvalidValue;
-    return gateup_launch<true>(a, a.nslot, st);
+    if (!gateup_topk(a.B, a.E)) return gateup_launch<true, 0>(a, a.nslot, st);
+    if (!a.logits || !a.top_w || !a.tw_w) return hipErrorInvalidValue;
+    return a.E <= 128 ? gateup_launch<true, 2>(a, a.nslot, st) : gateup_launch<true, 8>(a, a.nslot, st);
 }
 
 hipError_t launch_down_comb(const ExpertArgs& a, hipStream_t st) {

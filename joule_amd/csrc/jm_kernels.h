@@ -63,6 +63,12 @@ struct ExpertArgs {
     const int* n_tiles;       // [1] how many
     _Float16* act_h;          // [B*k][m] act split into fp16 hi + lo for the MFMA down
     _Float16* act_l;
+    // decode path with the top-k in the gate/up kernel (gateup_topk): the
+    // router scores, and where the table is written
+    const float* logits;      // [B][E]
+    int renorm;
+    int* top_w;               // [B*k] (the same memory as top)
+    float* tw_w;              // [B*k] (the same memory as tw)
 };
 
 // Routing front: router scores, top-k, x digits and (dispatch path) the
@@ -98,9 +104,10 @@ struct RouteArgs {
     int dense_min;            // dispatch path: slots from which an expert takes the MFMA kernels
     int2* tiles;              // dense tiles (work entry, token tile), in work-table order
     int* n_tiles;             // [1]
+    int skip_topk;            // 1: the top-k runs in the gate/up kernel
 };
 // router scores + x digits (one wave per expert group and token), then the
-// top-k of every token
+// top-k of every token (unless skip_topk)
 hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st);
 // dispatch + work table from a.top (dispatch path)
 hipError_t launch_dispatch_work(const RouteArgs& a, hipStream_t st);
@@ -121,7 +128,10 @@ hipError_t launch_dispatch(const int* top, int nslot, int E, int k, int* seg_off
                            int* active, int* n_active, int* first_slot, int* comb, int* rank_scratch,
                            hipStream_t st);
 // decode path (nslot <= JM_DEC_SLOTS): gate/up over ballot-found slots, then
-// down + combine into a.out
+// down + combine into a.out.  For gateup_topk(B, E) the gate/up kernel
+// computes the top-k itself (from a.logits; no top-k launch before it).
+#define JM_GU_TOPK_MAX_B 4
+bool gateup_topk(int B, int E);
 hipError_t launch_gateup_dec(const ExpertArgs& a, hipStream_t st);
 hipError_t launch_down_comb(const ExpertArgs& a, hipStream_t st);
 // dispatch path: gate/up and down over the work table, then the combine

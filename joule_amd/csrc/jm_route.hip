@@ -315,7 +315,7 @@ hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {
 #undef JM_RTB
 #undef JM_RT
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || a.skip_topk) return e;
     return launch_topk(a.logits, a.B, a.E, a.topk, a.renorm, a.top, a.tw, st);
 }
 

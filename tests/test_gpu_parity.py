@@ -224,6 +224,32 @@ def test_block_parity(request, which, B):
     assert err <= TOL
 
 
+# Decode-path shapes beyond the two model shapes: rows of 16 lanes
+# (d = 1024, m = 512), gate/up rows of two chunks per lane (d = 4096) and
+# down rows of 64 lanes (m > 1024).
+SHAPES = [MoEShape(1024, 512, 16, 4, True, "d1024-m512"),
+          MoEShape(4096, 1536, 32, 8, False, "d4096-m1536"),
+          MoEShape(1024, 2048, 8, 2, True, "d1024-m2048")]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: s.name)
+@pytest.mark.parametrize("B", [1, 7])
+def test_block_decode_launch_shapes(gpu, oracle_lib, shape, B):
+    banner(f"block {shape.name} B={B}")
+    layer = Layer(shape, 64, 1, oracle_lib)
+    try:
+        x = activations(B, shape.d)
+        out, top, tw = _run_block(layer, 0, x)
+        rout, rtop, rtw = layer.oracle(0).forward(x)
+        assert np.array_equal(top, rtop)
+        assert np.array_equal(tw.view(np.uint32), rtw.view(np.uint32))
+        err = _rel(out, rout)
+        print(f"  max rel err {shape.name} B={B}: {err:.3e}", flush=True)
+        assert err <= TOL
+    finally:
+        layer.store.close()
+
+
 def test_block_second_layer_and_determinism(qwen64):
     banner("block layer 1, determinism")
     x = activations(8, QWEN3.d)
