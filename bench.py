@@ -51,8 +51,8 @@ ZIPF_ALPHA = 0.28              # Zipf(1.1) bias strength: per-expert counts abou
 # reads for the 256 MiB copy in the same run: FETCH_SIZE reports half of the
 # copied bytes (factor 2.0), WRITE_SIZE all of them (factor 1.0).
 GATEUP_PMC = {"batch": 8, "group": 64, "layers": 16,
-              "fetch_kib": 42067.4, "fetch_factor": 2.0,
-              "write_kib": 336.1, "write_factor": 1.0,
+              "fetch_kib": 42100.9, "fetch_factor": 2.0,
+              "write_kib": 338.8, "write_factor": 1.0,
               "source": "profiles/pmc_traffic_qwen3_b8.md"}
 
 
