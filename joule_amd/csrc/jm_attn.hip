@@ -114,6 +114,135 @@ k_gemv_part(GemvArgs a) {
             make_float4(tot[0], tot[1], tot[2], tot[3]);
 }
 
+// ------------------------------------------------------------------ GEMM
+//
+// The same product for many tokens at once (a prefill chunk): part[0][b][row]
+// = sum over all K columns of W[row][k] * x[b][k] (* norm_w[k]), one output
+// slice.  Block (128-row tile, 64-token tile), 8 waves: 2 token halves x 4
+// row quarters of 32, each wave a 32 x 32 tile by v_mfma_f32_32x32x16_bf16
+// with the tokens on the A side (split into bf16 hi and lo, two products
+// per k-step, as the GEMV splits them) and the weight rows on the B side.
+// Operands go through LDS in 64-column stages, two stages streaming into
+// registers while the stage in LDS is multiplied.  Lane layout as the dense
+// expert branch's: A[i][k] at lane i % 32, k = 8 (l / 32) + j; B[k][n] at
+// lane n % 32, k = 8 (l / 32) + j; D register v of lane l = (i = 8 (v / 4)
+// + 4 (l / 32) + v % 4, n = l % 32).  Each weight byte crosses HBM once per
+// token tile instead of once per 8 tokens.
+constexpr int GM_T = 64;            // tokens per block
+constexpr int GM_R = 128;           // weight rows per block
+constexpr int GM_KS = 64;           // columns per stage
+constexpr int GM_KP = GM_KS + 8;    // padded LDS row, in bf16 (144 bytes: 16-byte aligned, bank-spread)
+
+struct GmStage {
+    float4 x0, x1;                  // 8 columns of one token
+    uint4 nw;                       // their norm weights (bf16)
+    uint4 w[2];                     // 2 x 8 columns of weight rows
+};
+
+__global__ void __launch_bounds__(512, 1)
+k_gemm_bf16(GemvArgs a) {
+    typedef float floatx16 __attribute__((ext_vector_type(16)));
+    __shared__ __align__(16) uint16_t xh[2][GM_T * GM_KP], xl[2][GM_T * GM_KP], wl[2][GM_R * GM_KP];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int row0 = blockIdx.x * GM_R, tb0 = blockIdx.y * GM_T;
+    const int K = a.K, nstage = K / GM_KS;
+    // the 128-row tile lies in one matrix (row counts are multiples of 128)
+    const uint16_t* wm;
+    int wr0;
+    if (row0 < a.rows[0]) { wm = a.w[0]; wr0 = row0; }
+    else if (row0 < a.rows[0] + a.rows[1]) { wm = a.w[1]; wr0 = row0 - a.rows[0]; }
+    else { wm = a.w[2]; wr0 = row0 - a.rows[0] - a.rows[1]; }
+    // staging: token xt, columns 8 xp .. 8 xp + 7; weight rows wrw and
+    // wrw + 64, columns 8 wp .. 8 wp + 7
+    const int xt = tid >> 3, xp = tid & 7;
+    const int wrw = tid >> 3, wp = tid & 7;
+    const bool xlive = tb0 + xt < a.B;
+    const float* xrow = a.x + (size_t)(xlive ? tb0 + xt : 0) * K + 8 * xp;
+    const uint16_t* wp0 = wm + (size_t)(wr0 + wrw) * K + 8 * wp;
+    const uint16_t* wp1 = wp0 + (size_t)64 * K;
+
+    // every load is unconditional (past the last stage: the last stage again)
+    auto load_stage = [&](GmStage& r, int s) __attribute__((always_inline)) {
+        s = s < nstage ? s : nstage - 1;
+        const float4* xs = (const float4*)(xrow + s * GM_KS);
+        r.x0 = xs[0];
+        r.x1 = xs[1];
+        if (a.norm_w) r.nw = *(const uint4*)(a.norm_w + s * GM_KS + 8 * xp);
+        r.w[0] = *(const uint4*)(wp0 + s * GM_KS);
+        r.w[1] = *(const uint4*)(wp1 + s * GM_KS);
+    };
+    auto store_stage = [&](const GmStage& r, int buf) __attribute__((always_inline)) {
+        float v[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
+        if (a.norm_w) {
+            const uint32_t nn[4] = {r.nw.x, r.nw.y, r.nw.z, r.nw.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v[2 * e] = __fmul_rn(v[2 * e], bf16_bits_to_f32(nn[e] & 0xFFFFu));
+                v[2 * e + 1] = __fmul_rn(v[2 * e + 1], bf16_bits_to_f32(nn[e] >> 16));
+            }
+        }
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) split_bf16x2(v[2 * e], v[2 * e + 1], hi[e], lo[e]);
+        const unsigned keep = xlive ? 0xFFFFFFFFu : 0u;     // tokens past B stage zeros
+        *(uint4*)&xh[buf][xt * GM_KP + 8 * xp] = make_uint4(hi[0] & keep, hi[1] & keep, hi[2] & keep, hi[3] & keep);
+        *(uint4*)&xl[buf][xt * GM_KP + 8 * xp] = make_uint4(lo[0] & keep, lo[1] & keep, lo[2] & keep, lo[3] & keep);
+        *(uint4*)&wl[buf][wrw * GM_KP + 8 * wp] = r.w[0];
+        *(uint4*)&wl[buf][(wrw + 64) * GM_KP + 8 * wp] = r.w[1];
+    };
+
+    const int th = w & 1, rq = w >> 1;            // this wave's token half and row quarter
+    const int ai = th * 32 + (lane & 31), bn = rq * 32 + (lane & 31), kq = 8 * (lane >> 5);
+    floatx16 acc = {};
+    auto mfma_stage = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k2 = 0; k2 < GM_KS / 16; k2++) {
+            const int k0 = k2 * 16 + kq;
+            const bf16x8 a_h = *(const bf16x8*)&xh[buf][ai * GM_KP + k0];
+            const bf16x8 a_l = *(const bf16x8*)&xl[buf][ai * GM_KP + k0];
+            const bf16x8 b = *(const bf16x8*)&wl[buf][bn * GM_KP + k0];
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, b, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, b, acc, 0, 0, 0);
+        }
+    };
+    // stages s + 1 and s + 2 stream into registers while stage s (in LDS) is
+    // multiplied; nstage is even
+    GmStage r0, r1;
+    load_stage(r0, 0);
+    load_stage(r1, 1);
+    store_stage(r0, 0);
+    load_stage(r0, 2);
+    __syncthreads();
+    for (int s = 0; s < nstage; s += 2) {
+        mfma_stage(0);
+        store_stage(r1, 1);
+        load_stage(r1, s + 3);
+        __syncthreads();
+        mfma_stage(1);
+        store_stage(r0, 0);
+        load_stage(r0, s + 4);
+        __syncthreads();
+    }
+    const int n = row0 + bn;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int t = tb0 + th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+        if (t < a.B) a.part[(size_t)t * a.N + n] = acc[v];
+    }
+}
+
+bool gemm_shape_ok(const GemvArgs& a) {
+    return a.K % (2 * GM_KS) == 0 && a.rows[0] % GM_R == 0 && a.rows[1] % GM_R == 0 && a.rows[2] % GM_R == 0;
+}
+
+hipError_t launch_gemm_bf16(const GemvArgs& a, hipStream_t st) {
+    if (a.B == 0 || a.N == 0) return hipSuccess;
+    if (!gemm_shape_ok(a)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(a.N / GM_R), (unsigned)((a.B + GM_T - 1) / GM_T));
+    hipLaunchKernelGGL(k_gemm_bf16, grid, dim3(512), 0, st, a);
+    return hipGetLastError();
+}
+
 bool gemv_shape_ok(int K) { return K > 0 && K % 1024 == 0 && K <= 8192; }
 
 int gemv_slice_cols(int K) { return K >= 4096 ? 1024 : 512; }

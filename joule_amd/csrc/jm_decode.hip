@@ -149,10 +149,13 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         g.rows[0] = H * HD; g.rows[1] = KH * HD; g.rows[2] = KH * HD;
         g.K = d; g.N = nqkv; g.B = B;
         g.part = s->qkv;
-        JM_HIP(jm::launch_gemv_part(g, st), "qkv launch");
+        // a prefill chunk takes the GEMM: one slice instead of d / 512
+        const bool gq = B >= JM_GEMM_MIN_B && jm::gemm_shape_ok(g);
+        if (gq) JM_HIP(jm::launch_gemm_bf16(g, st), "qkv GEMM launch");
+        else JM_HIP(jm::launch_gemv_part(g, st), "qkv launch");
 
         jm::AttnArgs at{};
-        at.qkv = s->qkv; at.nslice = d / jm::gemv_slice_cols(d); at.h = s->h; at.d = d;
+        at.qkv = s->qkv; at.nslice = gq ? 1 : d / jm::gemv_slice_cols(d); at.h = s->h; at.d = d;
         if (c->bias_qkv) {
             at.bq = W->bq + (size_t)l * H * HD;
             at.bk = W->bk + (size_t)l * KH * HD;
@@ -175,13 +178,15 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         o.rows[0] = d;
         o.K = H * HD; o.N = d; o.B = B;
         o.part = s->opart;
-        JM_HIP(jm::launch_gemv_part(o, st), "o_proj launch");
+        const bool go = B >= JM_GEMM_MIN_B && jm::gemm_shape_ok(o);
+        if (go) JM_HIP(jm::launch_gemm_bf16(o, st), "o_proj GEMM launch");
+        else JM_HIP(jm::launch_gemv_part(o, st), "o_proj launch");
 
         JM_DMARK(2 * l + 2);
         // h2 = h + attention (summed from the o_proj slices in the router),
         // then h = h2 + MoE(RMSNorm(h2))
         jm::FfnIo io;
-        io.xpart = s->opart; io.nxpart = H * HD / jm::gemv_slice_cols(H * HD); io.xmid = s->h2;
+        io.xpart = s->opart; io.nxpart = go ? 1 : H * HD / jm::gemv_slice_cols(H * HD); io.xmid = s->h2;
         io.norm_w = W->norm2 + (size_t)l * d; io.eps = c->eps;
         io.resid = s->h2;
         if (int rc = jm::ffn_enqueue(s, l, s->h, B, s->h, io, false, st)) return rc;

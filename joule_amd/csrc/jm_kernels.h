@@ -163,6 +163,12 @@ struct GemvArgs {
 bool gemv_shape_ok(int K);
 int gemv_slice_cols(int K);
 hipError_t launch_gemv_part(const GemvArgs& a, hipStream_t st);
+// many tokens (a prefill chunk): the whole sum into part[0] (one slice);
+// every row count a multiple of 128, K a multiple of 128
+bool gemm_shape_ok(const GemvArgs& a);
+hipError_t launch_gemm_bf16(const GemvArgs& a, hipStream_t st);
+// from this many tokens the projections take the GEMM
+#define JM_GEMM_MIN_B 33
 
 // Decode attention of one layer for B tokens, head dim 128, H / KH query
 // heads per KV head (1, 2, 4 or 8), in splits of 128 positions.

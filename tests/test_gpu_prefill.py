@@ -75,6 +75,7 @@ def test_prefill_layers_matches_per_position_decode(L, T):
     got = logits.cpu().numpy()
     want = _oracle_prefill(oracle, w, W_lm, prompt, kv_seq)
     rel = np.abs(got - want).max() / np.abs(want).max()
+    print(f"  prefill L={L} T={T}: last-position logits max rel err {rel:.2e}", flush=True)
     assert rel < TOL, rel
     _check_rows(kv, 0, kv_seq, T, L, f"T={T}")
     dec.store.close()
