@@ -137,13 +137,19 @@ struct GmStage {
     float4 x0, x1;                  // 8 columns of one token
     uint4 nw;                       // their norm weights (bf16)
     uint4 w[2];                     // 2 x 8 columns of weight rows
+    int s;                          // the stage (before clamping to the last one)
 };
 
 __global__ void __launch_bounds__(512, 1)
 k_gemm_bf16(GemvArgs a) {
     typedef float floatx16 __attribute__((ext_vector_type(16)));
     __shared__ __align__(16) uint16_t xh[2][GM_T * GM_KP], xl[2][GM_T * GM_KP], wl[2][GM_R * GM_KP];
+    __shared__ float ss_l[GM_T][8];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // the first row tile also sums each token's squares (the RMSNorm of the
+    // layer input, for the consumer) from the values it stages
+    const bool want_ss = a.rss && blockIdx.x == 0;
+    float ss = 0.0f;
     const int row0 = blockIdx.x * GM_R, tb0 = blockIdx.y * GM_T;
     const int K = a.K, nstage = K / GM_KS;
     // the 128-row tile lies in one matrix (row counts are multiples of 128)
@@ -163,6 +169,7 @@ k_gemm_bf16(GemvArgs a) {
 
     // every load is unconditional (past the last stage: the last stage again)
     auto load_stage = [&](GmStage& r, int s) __attribute__((always_inline)) {
+        r.s = s;
         s = s < nstage ? s : nstage - 1;
         const float4* xs = (const float4*)(xrow + s * GM_KS);
         r.x0 = xs[0];
@@ -173,6 +180,10 @@ k_gemm_bf16(GemvArgs a) {
     };
     auto store_stage = [&](const GmStage& r, int buf) __attribute__((always_inline)) {
         float v[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
+        if (want_ss && r.s < nstage) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[e], v[e], ss);
+        }
         if (a.norm_w) {
             const uint32_t nn[4] = {r.nw.x, r.nw.y, r.nw.z, r.nw.w};
 #pragma unroll
@@ -228,6 +239,16 @@ k_gemm_bf16(GemvArgs a) {
     for (int v = 0; v < 16; v++) {
         const int t = tb0 + th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
         if (t < a.B) a.part[(size_t)t * a.N + n] = acc[v];
+    }
+    if (want_ss) {
+        ss_l[xt][xp] = ss;
+        __syncthreads();
+        if (tid < GM_T && tb0 + tid < a.B) {
+            float t = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) t = __fadd_rn(t, ss_l[tid][i]);
+            a.rss[tb0 + tid] = t;
+        }
     }
 }
 
@@ -293,19 +314,24 @@ k_qkv_fin(AttnArgs a) {
     const int pos = a.pos[b];
     // RMSNorm row scale of the layer input (the projections were taken of
     // h * norm weight)
-    const float* hb = a.h + (size_t)b * a.d;
-    float ss = 0.0f;
-    for (int i = t; i < a.d / 4; i += HD) {
-        const float4 v = *(const float4*)(hb + 4 * i);
-        ss = __builtin_fmaf(v.x, v.x, ss);
-        ss = __builtin_fmaf(v.y, v.y, ss);
-        ss = __builtin_fmaf(v.z, v.z, ss);
-        ss = __builtin_fmaf(v.w, v.w, ss);
+    float inv;
+    if (a.rss) {
+        inv = rms_inv(a.rss[b], a.d, a.eps);        // summed by the projection GEMM
+    } else {
+        const float* hb = a.h + (size_t)b * a.d;
+        float ss = 0.0f;
+        for (int i = t; i < a.d / 4; i += HD) {
+            const float4 v = *(const float4*)(hb + 4 * i);
+            ss = __builtin_fmaf(v.x, v.x, ss);
+            ss = __builtin_fmaf(v.y, v.y, ss);
+            ss = __builtin_fmaf(v.z, v.z, ss);
+            ss = __builtin_fmaf(v.w, v.w, ss);
+        }
+        ss = seg_sum<64>(ss);
+        if ((t & 63) == 0) red[t >> 6] = ss;
+        __syncthreads();
+        inv = rms_inv(__fadd_rn(red[0], red[1]), a.d, a.eps);
     }
-    ss = seg_sum<64>(ss);
-    if ((t & 63) == 0) red[t >> 6] = ss;
-    __syncthreads();
-    const float inv = rms_inv(__fadd_rn(red[0], red[1]), a.d, a.eps);
     const int row = hh * HD + t;
     float v = a.qkv[(size_t)b * a.nqkv + row];
     for (int sl = 1; sl < a.nslice; sl++) v = __fadd_rn(v, a.qkv[((size_t)sl * a.B + b) * a.nqkv + row]);

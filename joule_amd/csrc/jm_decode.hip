@@ -72,6 +72,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
         (size_t)B * d * 4,                        // xemb: embedded prompt tokens (prefill)
         (size_t)jm::lm_blocks(V) * B * 4,         // lmv
         (size_t)jm::lm_blocks(V) * B * 4,         // lmi
+        (size_t)B * 4,                            // rss: sums of squares of h (projection GEMM)
         s->tab_cap,                               // KV pointers + positions
     };
     size_t total = 0;
@@ -83,7 +84,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     char* p = (char*)s->dws;
     void** slots[] = {(void**)&s->h, (void**)&s->h2, (void**)&s->qkv, (void**)&s->opart, (void**)&s->part_o,
                       (void**)&s->part_ml, (void**)&s->att, (void**)&s->qsplit, (void**)&s->hid, (void**)&s->xemb, (void**)&s->lmv,
-                      (void**)&s->lmi, (void**)&s->tab};
+                      (void**)&s->lmi, (void**)&s->rss, (void**)&s->tab};
     for (size_t i = 0; i < sizeof sz / sizeof sz[0]; i++) {
         *slots[i] = p;
         p += align256(sz[i]);
@@ -149,13 +150,16 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         g.rows[0] = H * HD; g.rows[1] = KH * HD; g.rows[2] = KH * HD;
         g.K = d; g.N = nqkv; g.B = B;
         g.part = s->qkv;
-        // a prefill chunk takes the GEMM: one slice instead of d / 512
+        // a prefill chunk takes the GEMM: one slice instead of d / 512, and
+        // the sums of squares of h for the RMSNorm scale
         const bool gq = B >= JM_GEMM_MIN_B && jm::gemm_shape_ok(g);
+        g.rss = gq ? s->rss : nullptr;
         if (gq) JM_HIP(jm::launch_gemm_bf16(g, st), "qkv GEMM launch");
         else JM_HIP(jm::launch_gemv_part(g, st), "qkv launch");
 
         jm::AttnArgs at{};
         at.qkv = s->qkv; at.nslice = gq ? 1 : d / jm::gemv_slice_cols(d); at.h = s->h; at.d = d;
+        at.rss = g.rss;
         if (c->bias_qkv) {
             at.bq = W->bq + (size_t)l * H * HD;
             at.bk = W->bk + (size_t)l * KH * HD;

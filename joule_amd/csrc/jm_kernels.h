@@ -158,6 +158,7 @@ struct GemvArgs {
     int rows[3];
     int K, N, B;              // N = rows[0] + rows[1] + rows[2]
     float* part;              // [K / gemv_slice_cols(K)][B][N]
+    float* rss;               // GEMM only: [B] receives sum x[b][k]^2 over all k (NULL: not wanted)
 };
 // K a multiple of 1024 (at most 8192); slices of 512 columns, 1024 from K = 4096
 bool gemv_shape_ok(int K);
@@ -178,6 +179,7 @@ struct AttnArgs {
     int nslice;
     const float* h;           // [B][d] the layer input (its RMSNorm row scale)
     int d;
+    const float* rss;         // [B] sum of h^2 over d when the projection computed it (NULL: from h)
     const float* bq;          // [H*128] / [KH*128] biases of the layer, or NULL
     const float* bk;
     const float* bv;

@@ -88,6 +88,7 @@ struct jm_store {
     float* xemb;                // [B][d] embedded prompt tokens (jm_prefill_layers)
     float* lmv;                 // [lm blocks][B] per-block best logit (argmax)
     int* lmi;                   // [lm blocks][B] its row
+    float* rss;                 // [B] sums of squares of h from the projection GEMM (prefill chunks)
     unsigned long long* tab;    // [B*L][2] KV pointers, then [B] positions (device)
     unsigned long long* tab_host;   // pinned staging of tab
     size_t tab_cap;             // bytes of tab / tab_host
