@@ -106,6 +106,9 @@ struct RouteArgs {
     int* n_tiles;             // [1]
     int skip_topk;            // 1: the top-k runs in the gate/up kernel
 };
+// from this many tokens the router serves 4 tokens per block from one read
+// of each group's table (k_router_quad)
+#define JM_ROUTER_QUAD_MIN_B 64
 // router scores + x digits (one wave per expert group and token), then the
 // top-k of every token (unless skip_topk)
 hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st);

@@ -278,6 +278,166 @@ k_router_grp(RouteArgs a) {
     }
 }
 
+// The same for batches of many tokens: block (4 expert groups, 4 tokens),
+// one wave per group.  Wave w first stages token 4 * blockIdx.y + w in LDS
+// (with the decoder layer's slice sum and RMSNorm, LAYER); then each wave
+// runs its group's chains for the 4 tokens from one read of its table
+// chunks, each token's chain in the same order as k_router_grp's, so the
+// scores are the same bits.  The table is read once per 4 tokens instead of
+// once per token.  The x digits and the MFMA-branch split of the 4 tokens
+// are shared out over the grid's waves as k_router_grp shares them.
+constexpr int RQ_T = 4;             // tokens per block
+template <int G, int NDIG, int DV, bool WBF16, bool LAYER>
+__global__ void __launch_bounds__(256)
+k_router_quad(RouteArgs a) {
+    using C = Chain<DV, WBF16>;
+    constexpr int d = DV * 512;
+    constexpr int T = d / 8;
+    constexpr int TP = T + 4;
+    __shared__ float xT[RQ_T][8 * TP];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int eg = blockIdx.x * 4 + w;           // this wave's expert group
+    const int ngrp = (a.E + 7) / 8, nvg = gridDim.x * 4;
+    const int b0 = blockIdx.y * RQ_T;
+    const int r = lane & 7, el = lane >> 3;
+    const uint4* wt = (const uint4*)a.wt;
+    const bool chains = eg < ngrp;
+
+    constexpr int XV = d / 4 / 64;
+    constexpr int NB = C::NC < 16 ? C::NC : 16;
+    uint4 buf[NB][C::CP];
+    if (chains) {
+#pragma unroll
+        for (int c = 0; c < NB; c++) C::load(buf[c], wt, eg, c, lane);
+    }
+    // wave w stages token b0 + w
+    {
+        const int b = b0 + w;
+        float4 xv[XV];
+        if (b < a.B) {
+            const float4* xb = (const float4*)(a.x + (size_t)b * d);
+#pragma unroll
+            for (int i = 0; i < XV; i++) xv[i] = xb[lane + 64 * i];
+            if (LAYER && a.xpart) {
+                const float4* xp = (const float4*)(a.xpart + (size_t)b * d);
+                const size_t sstride = (size_t)a.B * d / 4;
+                float4 ps[XV];
+#pragma unroll
+                for (int i = 0; i < XV; i++) ps[i] = xp[lane + 64 * i];
+                for (int sl = 1; sl < a.nxpart; sl++) {
+#pragma unroll
+                    for (int i = 0; i < XV; i++) {
+                        const float4 u = xp[sl * sstride + lane + 64 * i];
+                        ps[i] = make_float4(__fadd_rn(ps[i].x, u.x), __fadd_rn(ps[i].y, u.y), __fadd_rn(ps[i].z, u.z),
+                                            __fadd_rn(ps[i].w, u.w));
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < XV; i++)
+                    xv[i] = make_float4(__fadd_rn(xv[i].x, ps[i].x), __fadd_rn(xv[i].y, ps[i].y),
+                                        __fadd_rn(xv[i].z, ps[i].z), __fadd_rn(xv[i].w, ps[i].w));
+                if (blockIdx.x == 0 && a.xmid) {
+                    float4* xm = (float4*)(a.xmid + (size_t)b * d);
+#pragma unroll
+                    for (int i = 0; i < XV; i++) xm[lane + 64 * i] = xv[i];
+                }
+            }
+            if (LAYER && a.norm_w) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int i = 0; i < XV; i++) {
+                    ss = __builtin_fmaf(xv[i].x, xv[i].x, ss);
+                    ss = __builtin_fmaf(xv[i].y, xv[i].y, ss);
+                    ss = __builtin_fmaf(xv[i].z, xv[i].z, ss);
+                    ss = __builtin_fmaf(xv[i].w, xv[i].w, ss);
+                }
+                const float inv = rms_inv(seg_sum<64>(ss), d, a.eps);
+                const uint2* nw = (const uint2*)a.norm_w;
+#pragma unroll
+                for (int i = 0; i < XV; i++) {
+                    const uint2 wv = nw[lane + 64 * i];
+                    xv[i].x = __fmul_rn(__fmul_rn(xv[i].x, inv), bf16_bits_to_f32(wv.x & 0xFFFFu));
+                    xv[i].y = __fmul_rn(__fmul_rn(xv[i].y, inv), bf16_bits_to_f32(wv.x >> 16));
+                    xv[i].z = __fmul_rn(__fmul_rn(xv[i].z, inv), bf16_bits_to_f32(wv.y & 0xFFFFu));
+                    xv[i].w = __fmul_rn(__fmul_rn(xv[i].w, inv), bf16_bits_to_f32(wv.y >> 16));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < XV; i++) xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        float* xw = xT[w];
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const int j = 4 * (lane + 64 * i);
+            xw[((j + 0) & 7) * TP + ((j + 0) >> 3)] = xv[i].x;
+            xw[((j + 1) & 7) * TP + ((j + 1) >> 3)] = xv[i].y;
+            xw[((j + 2) & 7) * TP + ((j + 2) >> 3)] = xv[i].z;
+            xw[((j + 3) & 7) * TP + ((j + 3) >> 3)] = xv[i].w;
+        }
+    }
+    __syncthreads();
+    const int nt = min(RQ_T, a.B - b0);           // tokens of this block (>= 1)
+    if (chains) {
+        float acc[RQ_T];
+#pragma unroll
+        for (int t = 0; t < RQ_T; t++) acc[t] = 0.0f;
+        // each token's chain in k_router_grp's order: chunk c's fused
+        // multiply-adds, pinned before the loads of chunk c + NB
+#pragma unroll
+        for (int c = 0; c < C::NC; c++) {
+#pragma unroll
+            for (int t = 0; t < RQ_T; t++) {
+                acc[t] = C::fma_chunk(buf[c % NB], xT[t] + (size_t)r * TP, c, acc[t]);
+                __asm__ volatile("" : "+v"(acc[t]) : : "memory");
+            }
+            if (c + NB < C::NC) C::load(buf[c % NB], wt, eg, c + NB, lane);
+        }
+        const int e = 8 * eg + el;
+#pragma unroll
+        for (int t = 0; t < RQ_T; t++) {
+            float v = acc[t];
+            v = __fadd_rn(v, __shfl_xor(v, 4, JM_WAVE));
+            v = __fadd_rn(v, __shfl_xor(v, 2, JM_WAVE));
+            v = __fadd_rn(v, __shfl_xor(v, 1, JM_WAVE));
+            if (r == 0 && e < a.E && t < nt) a.logits[(size_t)(b0 + t) * a.E + e] = v;
+        }
+    }
+    // x digits (one G-value group per G-lane segment) and the MFMA split of
+    // the block's tokens: this wave's share, over the grid's nvg waves
+    constexpr int ng = d / G;
+    constexpr int PPW = JM_WAVE / G;
+    const int sub = lane / G;
+    for (int t = 0; t < nt; t++) {
+        const int b = b0 + t;
+        const float* xw = xT[t];
+        for (int base = eg * PPW; base < ng; base += nvg * PPW) {
+            const int p = base + sub;
+            const bool ok = p < ng;
+            const int j = (ok ? p : 0) * G + (lane & (G - 1));
+            const float v = ok ? xw[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
+            encode_group_wave<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + (ok ? p : 0)) * (NDIG * (G / 8)),
+                                       a.xscale + (size_t)b * ng + (ok ? p : 0));
+        }
+        if (a.xsh) {
+            for (int c = (eg * 64 + lane) * 8; c < d; c += nvg * 64 * 8) {
+                half8 h, l;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int j = c + i;
+                    const float v = xw[(size_t)(j & 7) * TP + (j >> 3)];
+                    const _Float16 hh = (_Float16)v;
+                    h[mfma_slot(i)] = hh;
+                    l[mfma_slot(i)] = (_Float16)(v - (float)hh);
+                }
+                *(half8*)(a.xsh + (size_t)b * d + c) = h;
+                *(half8*)(a.xsl + (size_t)b * d + c) = l;
+            }
+        }
+    }
+}
+
 // Dispatch and work table of all slots from the top-k table (dispatch path).
 __global__ void __launch_bounds__(1024)
 k_dispatch_work(RouteArgs a) {
@@ -302,10 +462,14 @@ k_dispatch_work(RouteArgs a) {
 
 hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {
     if (a.B == 0) return hipSuccess;
-    const dim3 grid((unsigned)((a.E + 7) / 8), (unsigned)a.B);
-#define JM_RT(GG, DVV, BF)                                                                                 \
-    if (a.xpart || a.norm_w) hipLaunchKernelGGL((k_router_grp<GG, JM_NDIG, DVV, BF, true>), grid, dim3(64), 0, st, a); \
-    else hipLaunchKernelGGL((k_router_grp<GG, JM_NDIG, DVV, BF, false>), grid, dim3(64), 0, st, a)
+    const int ngrp = (a.E + 7) / 8;
+    const bool quad = a.B >= JM_ROUTER_QUAD_MIN_B;
+    const dim3 grid((unsigned)ngrp, (unsigned)a.B);
+    const dim3 gridq((unsigned)((ngrp + 3) / 4), (unsigned)((a.B + RQ_T - 1) / RQ_T));
+#define JM_RT1(GG, DVV, BF, LY)                                                                          \
+    if (quad) hipLaunchKernelGGL((k_router_quad<GG, JM_NDIG, DVV, BF, LY>), gridq, dim3(256), 0, st, a); \
+    else hipLaunchKernelGGL((k_router_grp<GG, JM_NDIG, DVV, BF, LY>), grid, dim3(64), 0, st, a)
+#define JM_RT(GG, DVV, BF) if (a.xpart || a.norm_w) { JM_RT1(GG, DVV, BF, true); } else { JM_RT1(GG, DVV, BF, false); }
 #define JM_RTB(GG, DVV) if (a.wt_bf16) { JM_RT(GG, DVV, true); } else { JM_RT(GG, DVV, false); }
 #define JM_RTD(GG) switch (a.d / 512) { case 1: JM_RTB(GG, 1); break; case 2: JM_RTB(GG, 2); break; \
         case 3: JM_RTB(GG, 3); break; case 4: JM_RTB(GG, 4); break; case 6: JM_RTB(GG, 6); break; \
@@ -314,6 +478,7 @@ hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {
 #undef JM_RTD
 #undef JM_RTB
 #undef JM_RT
+#undef JM_RT1
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.skip_topk) return e;
     return launch_topk(a.logits, a.B, a.E, a.topk, a.renorm, a.top, a.tw, st);
