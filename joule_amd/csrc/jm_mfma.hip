@@ -6,10 +6,12 @@
 //   k_gateup_mfma  per (expert, 64-token tile, 128 intermediate rows):
 //                  G = X . Wg^T and U = X . Wu^T over d, then
 //                  act = (G / (1 + expf_fast(-G))) * U
-//   k_down_mfma    per (expert, 64-token tile, 128 hidden rows):
+//   k_down_mfma    per (expert, 64-token tile, 128 hidden rows; 256 for a
+//                  tile of up to 32 tokens):
 //                  y[slot] = w_slot * (act . Wd^T) over the intermediate
 //
-// Operands, per 64-column stage of the contraction, staged in LDS:
+// Operands, per 64-column (narrow down tiles: 32-column) stage of the
+// contraction, staged in LDS:
 //   weights  the signed nibbles q - 8 as fp16 (exact), one fp32 scale per
 //            row and Q4 group applied to the fp32 accumulator of that group;
 //   tokens   each fp32 value split into hi = fp16(v) and lo = fp16(v - hi)
@@ -35,9 +37,7 @@ namespace jm {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int MT = JM_DENSE_TILE;   // tokens per tile
-constexpr int KS = 64;              // contraction columns per stage
-constexpr int KP = KS + 8;          // padded LDS row, in halves (144 bytes: 16-byte aligned, bank-spread)
+constexpr int MT = JM_DENSE_TILE;   // tokens per tile of the tile list
 
 __device__ __forceinline__ void split_hi_lo(float v, _Float16& h, _Float16& l) {
     h = (_Float16)v;
@@ -85,119 +85,169 @@ __device__ __forceinline__ bool tile_info(const ExpertArgs& a, int t, TileInfo* 
     return true;
 }
 
-constexpr int MTHREADS = 512;       // 8 waves: 2 token halves x 4 row quarters of the 128-row tile
-constexpr int MROWS = 128;          // weight rows per block
+constexpr int MTHREADS = 512;       // 8 waves per block
+constexpr int MROWS = 128;          // weight rows of one block column (blockIdx.y)
+
+// Tile shapes.  A wide tile (33..64 tokens, and every gate/up tile) is
+// multiplied by one block per 128 weight rows: 8 waves of 32 tokens x 32
+// rows (2 token halves x 4 row quarters), 64-column stages.  A narrow down
+// tile (up to 32 tokens: most experts of a skewed prefill batch) is
+// multiplied by one block per 256 rows, the even block of each pair of
+// block columns (the odd one exits): 8 waves of the same 32 tokens x 32
+// rows each, 32-column stages.  Both shapes issue the same MFMAs per wave
+// and stream the same bytes per block; the narrow one halves the blocks of
+// a narrow tile and multiplies no padding half.
+template <bool NARROW>
+struct Shape {
+    static constexpr int TOK = NARROW ? 32 : 64;      // tokens per tile
+    static constexpr int ROWS = NARROW ? 256 : 128;   // weight rows per block
+    static constexpr int KS = NARROW ? 32 : 64;       // contraction columns per stage
+    static constexpr int KP = KS + 8;                 // padded LDS row in halves (80 / 144 bytes: 16-byte aligned, bank-spread)
+    static constexpr int XPC = KS / 8;                // 8-value token pieces per token and stage
+    static constexpr int XTHR = TOK * XPC;            // threads staging tokens (128 / 512)
+    static constexpr int WPR = KS / 32;               // 16-byte weight pieces per row and stage
+};
+
+// Scale groups of a stage: NGS scale values per row, each over KSG MFMA
+// k-steps; a 64-value group spans SPG = 2 narrow stages, and its two halves'
+// partial sums are summed before the scale is applied.
+template <int G, int KS_>
+struct Groups {
+    static constexpr int NGS = KS_ >= G ? KS_ / G : 1;
+    static constexpr int KSG = (KS_ >= G ? G : KS_) / 16;
+    static constexpr int SPG = KS_ >= G ? 1 : G / KS_;
+    static_assert(SPG == 1 || SPG == 2, "a scale group spans one or two stages");
+};
+
+// narrow tiles need whole 256-row blocks
+__device__ __forceinline__ bool narrow_rows_ok(int rows) { return rows % (2 * MROWS) == 0; }
 
 // ------------------------------------------------------------------ gate/up
 
-// Stage registers of one thread: 8 token values, one 16-byte piece of one
-// row of one matrix, that row's scales for the stage.
+template <int G, bool NARROW>
+struct GuLds {
+    using S = Shape<NARROW>;
+    _Float16 xh[2][S::TOK * S::KP], xl[2][S::TOK * S::KP];
+    _Float16 wl[2][2][S::ROWS * S::KP];
+    float scl[2][2][S::ROWS][Groups<G, S::KS>::NGS];
+    int tok[S::TOK];
+};
+
 // Stage registers of one thread: 8 token values (hi and lo), one 16-byte
 // piece of one row of one matrix, that row's scales for the stage.
 template <int NGS>
-struct GuStage {
+struct StageRegs {
     uint4 h, l;
     uint4 w;
     uint16_t sc[NGS];
 };
 
-template <int G>
-__global__ void __launch_bounds__(MTHREADS, 1)
-k_gateup_mfma(ExpertArgs a) {
-    TileInfo ti;
-    if (!tile_info(a, blockIdx.x, &ti)) return;
-    constexpr int NGS = KS / G;                   // scale groups per stage
-    constexpr int KSG = G / 16;                   // MFMA k-steps per scale group
-    __shared__ __align__(16) _Float16 xh[2][MT * KP], xl[2][MT * KP], wl[2][2][MROWS * KP];
-    __shared__ float scl[2][2][MROWS][NGS];
-    __shared__ int tok_b[MT];
+template <int G, bool NARROW>
+__device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo& ti, unsigned char* sm) {
+    using S = Shape<NARROW>;
+    using Q = Groups<G, S::KS>;
+    GuLds<G, NARROW>& L = *reinterpret_cast<GuLds<G, NARROW>*>(sm);
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = tid >> 6;
-    const int rt = blockIdx.y;                    // 128-row tile of the intermediate
-    const int d = a.d, ng = d / G, nstage = d / KS;
-    if (tid < MT) tok_b[tid] = tid < ti.nt ? a.seg_slot[ti.slot0 + tid] / a.topk : -1;
+    const int row0 = blockIdx.y * MROWS;          // first intermediate row of the block
+    const int d = a.d, ng = d / G, nstage = d / S::KS;
+    if (tid < S::TOK) L.tok[tid] = tid < ti.nt ? a.seg_slot[ti.slot0 + tid] / a.topk : -1;
     unsigned long long so[2], po[2];
     a.rec.get(0, a.key0 + ti.e, so[0], po[0]);
     a.rec.get(1, a.key0 + ti.e, so[1], po[1]);
     __syncthreads();
 
-    // staging assignment: tokens (8 threads x 8 values each), weights (one
-    // 16-byte piece of one row of one matrix)
-    const int xt = tid >> 3, xpart = tid & 7;
-    const int wm = tid >> 8, wrow = (tid & 255) >> 1, wpiece = tid & 1;
-    const int xb = tok_b[xt];
+    // staging assignment: tokens (threads < XTHR, 8 values each of one
+    // token), weights (every thread one 16-byte piece of one row of one
+    // matrix)
+    const bool xthr = S::XTHR == MTHREADS || tid < S::XTHR;   // wave-uniform
+    const int xt = (tid / S::XPC) % S::TOK, xpart = tid % S::XPC;
+    const int wm = tid >> 8, widx = tid & 255;
+    const int wrow = widx / S::WPR, wpiece = widx % S::WPR;
+    const int xb = L.tok[xt];
     const size_t xo = (size_t)(xb >= 0 ? xb : 0) * d + xpart * 8;
-    const uint8_t* wpk = a.blob + po[wm] + (size_t)(rt * MROWS + wrow) * (d / 2) + wpiece * 16;
-    const uint16_t* wsc = (const uint16_t*)(a.blob + so[wm]) + (size_t)(rt * MROWS + wrow) * ng;
+    const uint8_t* wpk = a.blob + po[wm] + (size_t)(row0 + wrow) * (d / 2) + wpiece * 16;
+    const uint16_t* wsc = (const uint16_t*)(a.blob + so[wm]) + (size_t)(row0 + wrow) * ng;
 
-    // every load is unconditional (past the last stage: the last stage again),
-    // so that each wait counts exactly the loads it needs
-    auto load_stage = [&](GuStage<NGS>& r, int s) __attribute__((always_inline)) {
+    // every load is unconditional (past the last stage: the last stage again)
+    auto load_stage = [&](StageRegs<Q::NGS>& r, int s) __attribute__((always_inline)) {
         s = s < nstage ? s : nstage - 1;
-        r.h = *(const uint4*)(a.xsh + xo + s * KS);
-        r.l = *(const uint4*)(a.xsl + xo + s * KS);
-        r.w = *(const uint4*)(wpk + s * (KS / 2));
+        if (xthr) {
+            r.h = *(const uint4*)(a.xsh + xo + s * S::KS);
+            r.l = *(const uint4*)(a.xsl + xo + s * S::KS);
+        }
+        r.w = *(const uint4*)(wpk + s * (S::KS / 2));
 #pragma unroll
-        for (int j = 0; j < NGS; j++) r.sc[j] = wsc[s * NGS + j];
+        for (int j = 0; j < Q::NGS; j++) r.sc[j] = wsc[(s * S::KS) / G + j];
     };
-    auto store_stage = [&](const GuStage<NGS>& r, int buf) __attribute__((always_inline)) {
-        const unsigned keep = xb >= 0 ? 0xFFFFFFFFu : 0u;     // padding tokens stage zeros
-        *(uint4*)&xh[buf][xt * KP + xpart * 8] = make_uint4(r.h.x & keep, r.h.y & keep, r.h.z & keep, r.h.w & keep);
-        *(uint4*)&xl[buf][xt * KP + xpart * 8] = make_uint4(r.l.x & keep, r.l.y & keep, r.l.z & keep, r.l.w & keep);
-        nibbles_to_lds(r.w, &wl[buf][wm][wrow * KP + wpiece * 32]);
+    auto store_stage = [&](const StageRegs<Q::NGS>& r, int buf) __attribute__((always_inline)) {
+        if (xthr) {
+            const unsigned keep = xb >= 0 ? 0xFFFFFFFFu : 0u;     // padding tokens stage zeros
+            *(uint4*)&L.xh[buf][xt * S::KP + xpart * 8] = make_uint4(r.h.x & keep, r.h.y & keep, r.h.z & keep, r.h.w & keep);
+            *(uint4*)&L.xl[buf][xt * S::KP + xpart * 8] = make_uint4(r.l.x & keep, r.l.y & keep, r.l.z & keep, r.l.w & keep);
+        }
+        nibbles_to_lds(r.w, &L.wl[buf][wm][wrow * S::KP + wpiece * 32]);
         if (wpiece == 0) {
 #pragma unroll
-            for (int j = 0; j < NGS; j++) scl[buf][wm][wrow][j] = fp16_hw(r.sc[j]);
+            for (int j = 0; j < Q::NGS; j++) L.scl[buf][wm][wrow][j] = fp16_hw(r.sc[j]);
         }
     };
 
-    const int th = w & 1, rq = w >> 1;            // this wave's token half and row quarter
+    // this wave's token half and 32-row slice
+    const int th = NARROW ? 0 : (w & 1), rq = NARROW ? w : (w >> 1);
     const int ai = th * 32 + (lane & 31), bn = rq * 32 + (lane & 31), kq = 8 * (lane >> 5);
     floatx16 tg = {}, tu = {};
-    auto mfma_stage = [&](int buf) __attribute__((always_inline)) {
+    floatx16 cg = {}, cu = {};                    // partial sums carried into a group's second stage
+    // fresh: the stage starts a scale group; apply: it ends one
+    auto mfma_stage = [&](int buf, bool fresh, bool apply) __attribute__((always_inline)) {
 #pragma unroll
-        for (int gs = 0; gs < NGS; gs++) {
-            floatx16 ag = {}, au = {};
+        for (int gs = 0; gs < Q::NGS; gs++) {
+            floatx16 ag = fresh ? floatx16{} : cg, au = fresh ? floatx16{} : cu;
 #pragma unroll
-            for (int k2 = 0; k2 < KSG; k2++) {
-                const int k0 = (gs * KSG + k2) * 16 + kq;
-                const half8 a_h = *(const half8*)&xh[buf][ai * KP + k0];
-                const half8 a_l = *(const half8*)&xl[buf][ai * KP + k0];
-                const half8 b_g = *(const half8*)&wl[buf][0][bn * KP + k0];
-                const half8 b_u = *(const half8*)&wl[buf][1][bn * KP + k0];
+            for (int k2 = 0; k2 < Q::KSG; k2++) {
+                const int k0 = (gs * Q::KSG + k2) * 16 + kq;
+                const half8 a_h = *(const half8*)&L.xh[buf][ai * S::KP + k0];
+                const half8 a_l = *(const half8*)&L.xl[buf][ai * S::KP + k0];
+                const half8 b_g = *(const half8*)&L.wl[buf][0][bn * S::KP + k0];
+                const half8 b_u = *(const half8*)&L.wl[buf][1][bn * S::KP + k0];
                 ag = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, b_g, ag, 0, 0, 0);
                 ag = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, b_g, ag, 0, 0, 0);
                 au = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, b_u, au, 0, 0, 0);
                 au = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, b_u, au, 0, 0, 0);
             }
-            const float sg = scl[buf][0][bn][gs], su = scl[buf][1][bn][gs];
+            if (apply) {
+                const float sg = L.scl[buf][0][bn][gs], su = L.scl[buf][1][bn][gs];
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                tg[v] = __builtin_fmaf(sg, ag[v], tg[v]);
-                tu[v] = __builtin_fmaf(su, au[v], tu[v]);
+                for (int v = 0; v < 16; v++) {
+                    tg[v] = __builtin_fmaf(sg, ag[v], tg[v]);
+                    tu[v] = __builtin_fmaf(su, au[v], tu[v]);
+                }
+            } else {
+                cg = ag;
+                cu = au;
             }
         }
     };
     // stages s + 1 and s + 2 stream into registers while stage s (in LDS) is
-    // multiplied; nstage is even
-    GuStage<NGS> r0, r1;
+    // multiplied; nstage is even, so buffer 0 always holds an even stage
+    StageRegs<Q::NGS> r0, r1;
     load_stage(r0, 0);
     load_stage(r1, 1);
     store_stage(r0, 0);
     load_stage(r0, 2);
     __syncthreads();
     for (int s = 0; s < nstage; s += 2) {
-        mfma_stage(0);                            // stage s; r1 = s + 1, r0 = s + 2 in flight
+        mfma_stage(0, true, Q::SPG == 1);         // stage s; r1 = s + 1, r0 = s + 2 in flight
         store_stage(r1, 1);
         load_stage(r1, s + 3);
         __syncthreads();
-        mfma_stage(1);                            // stage s + 1; r0 = s + 2, r1 = s + 3
+        mfma_stage(1, Q::SPG == 1, true);         // stage s + 1; r0 = s + 2, r1 = s + 3
         store_stage(r0, 0);
         load_stage(r0, s + 4);
         __syncthreads();
     }
     // act = SiLU(g) * u for this lane's row and 16 tokens
-    const int r = rt * MROWS + bn;
+    const int r = row0 + bn;
 #pragma unroll
     for (int v = 0; v < 16; v++) {
         const int i = th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
@@ -214,114 +264,156 @@ k_gateup_mfma(ExpertArgs a) {
     }
 }
 
-// --------------------------------------------------------------------- down
-
-template <int NGS>
-struct DnStage {
-    uint4 h, l;
-    uint4 w;
-    uint16_t sc[NGS];
-};
-
+// Gate/up takes every tile in the wide shape: with narrow tiles in 256-row
+// blocks the 512-token Zipf-routed block's gate/up took 167 us instead of
+// 160 (twice the stages of half the MFMA work each, and the per-stage
+// latency is what bounds it), while the down product, with a third of the
+// contraction, gains from the halved block count.
 template <int G>
 __global__ void __launch_bounds__(MTHREADS, 1)
-k_down_mfma(ExpertArgs a) {
+k_gateup_mfma(ExpertArgs a) {
     TileInfo ti;
     if (!tile_info(a, blockIdx.x, &ti)) return;
-    constexpr int NGS = KS / G;
-    constexpr int KSG = G / 16;
-    __shared__ __align__(16) _Float16 xh[2][MT * KP], xl[2][MT * KP], wl[2][MROWS * KP];
-    __shared__ float scl[2][MROWS][NGS];
-    __shared__ int tok_s[MT];
+    __shared__ __align__(16) unsigned char sm[sizeof(GuLds<G, false>)];
+    gateup_tile<G, false>(a, ti, sm);
+}
+
+// --------------------------------------------------------------------- down
+
+template <int G, bool NARROW>
+struct DnLds {
+    using S = Shape<NARROW>;
+    _Float16 xh[2][S::TOK * S::KP], xl[2][S::TOK * S::KP];
+    _Float16 wl[2][S::ROWS * S::KP];
+    float scl[2][S::ROWS][Groups<G, S::KS>::NGS];
+    int tok[S::TOK];
+};
+
+template <int G, bool NARROW>
+__device__ __forceinline__ void down_tile(const ExpertArgs& a, const TileInfo& ti, unsigned char* sm) {
+    using S = Shape<NARROW>;
+    using Q = Groups<G, S::KS>;
+    DnLds<G, NARROW>& L = *reinterpret_cast<DnLds<G, NARROW>*>(sm);
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = tid >> 6;
-    const int rt = blockIdx.y;                    // 128-row tile of the hidden dimension
-    const int m = a.m, ng = m / G, nstage = m / KS;
-    if (tid < MT) tok_s[tid] = tid < ti.nt ? a.seg_slot[ti.slot0 + tid] : -1;
+    const int row0 = blockIdx.y * MROWS;          // first hidden row of the block
+    const int m = a.m, ng = m / G, nstage = m / S::KS;
+    if (tid < S::TOK) L.tok[tid] = tid < ti.nt ? a.seg_slot[ti.slot0 + tid] : -1;
     unsigned long long so, po;
     a.rec.get(2, a.key0 + ti.e, so, po);
     __syncthreads();
 
-    const int xt = tid >> 3, xpart = tid & 7;     // act: 8 threads x 8 columns per token
-    const int wrow = (tid & 255) >> 1, wpiece = tid & 1;   // threads 0..255 stage the weights
-    const bool wthr = tid < 2 * MROWS;
-    const int xs = tok_s[xt];
+    // staging: act (threads < XTHR, 8 columns of one token each), weights
+    // (threads 0..255, one 16-byte piece of one row each)
+    const bool xthr = S::XTHR == MTHREADS || tid < S::XTHR;   // wave-uniform
+    const bool wthr = tid < 256;                               // wave-uniform
+    const int xt = (tid / S::XPC) % S::TOK, xpart = tid % S::XPC;
+    const int widx = tid & 255;
+    const int wrow = widx / S::WPR, wpiece = widx % S::WPR;
+    const int xs = L.tok[xt];
     const size_t xo = (size_t)(xs >= 0 ? xs : 0) * m + xpart * 8;
-    const uint8_t* wpk = a.blob + po + (size_t)(rt * MROWS + wrow) * (m / 2) + wpiece * 16;
-    const uint16_t* wsc = (const uint16_t*)(a.blob + so) + (size_t)(rt * MROWS + wrow) * ng;
+    const uint8_t* wpk = a.blob + po + (size_t)(row0 + wrow) * (m / 2) + wpiece * 16;
+    const uint16_t* wsc = (const uint16_t*)(a.blob + so) + (size_t)(row0 + wrow) * ng;
 
-    auto load_stage = [&](DnStage<NGS>& r, int s) __attribute__((always_inline)) {
+    auto load_stage = [&](StageRegs<Q::NGS>& r, int s) __attribute__((always_inline)) {
         s = s < nstage ? s : nstage - 1;
-        r.h = *(const uint4*)(a.act_h + xo + s * KS);
-        r.l = *(const uint4*)(a.act_l + xo + s * KS);
-        r.w = *(const uint4*)(wpk + s * (KS / 2));
-#pragma unroll
-        for (int j = 0; j < NGS; j++) r.sc[j] = wsc[s * NGS + j];
-    };
-    auto store_stage = [&](const DnStage<NGS>& r, int buf) __attribute__((always_inline)) {
-        const unsigned keep = xs >= 0 ? 0xFFFFFFFFu : 0u;     // padding tokens stage zeros
-        *(uint4*)&xh[buf][xt * KP + xpart * 8] = make_uint4(r.h.x & keep, r.h.y & keep, r.h.z & keep, r.h.w & keep);
-        *(uint4*)&xl[buf][xt * KP + xpart * 8] = make_uint4(r.l.x & keep, r.l.y & keep, r.l.z & keep, r.l.w & keep);
+        if (xthr) {
+            r.h = *(const uint4*)(a.act_h + xo + s * S::KS);
+            r.l = *(const uint4*)(a.act_l + xo + s * S::KS);
+        }
         if (wthr) {
-            nibbles_to_lds(r.w, &wl[buf][wrow * KP + wpiece * 32]);
+            r.w = *(const uint4*)(wpk + s * (S::KS / 2));
+#pragma unroll
+            for (int j = 0; j < Q::NGS; j++) r.sc[j] = wsc[(s * S::KS) / G + j];
+        }
+    };
+    auto store_stage = [&](const StageRegs<Q::NGS>& r, int buf) __attribute__((always_inline)) {
+        if (xthr) {
+            const unsigned keep = xs >= 0 ? 0xFFFFFFFFu : 0u;     // padding tokens stage zeros
+            *(uint4*)&L.xh[buf][xt * S::KP + xpart * 8] = make_uint4(r.h.x & keep, r.h.y & keep, r.h.z & keep, r.h.w & keep);
+            *(uint4*)&L.xl[buf][xt * S::KP + xpart * 8] = make_uint4(r.l.x & keep, r.l.y & keep, r.l.z & keep, r.l.w & keep);
+        }
+        if (wthr) {
+            nibbles_to_lds(r.w, &L.wl[buf][wrow * S::KP + wpiece * 32]);
             if (wpiece == 0) {
 #pragma unroll
-                for (int j = 0; j < NGS; j++) scl[buf][wrow][j] = fp16_hw(r.sc[j]);
+                for (int j = 0; j < Q::NGS; j++) L.scl[buf][wrow][j] = fp16_hw(r.sc[j]);
             }
         }
     };
 
-    const int th = w & 1, rq = w >> 1;
+    const int th = NARROW ? 0 : (w & 1), rq = NARROW ? w : (w >> 1);
     const int ai = th * 32 + (lane & 31), bn = rq * 32 + (lane & 31), kq = 8 * (lane >> 5);
     floatx16 tot = {};
-    auto mfma_stage = [&](int buf) __attribute__((always_inline)) {
+    floatx16 carry = {};                          // partial sum carried into a group's second stage
+    auto mfma_stage = [&](int buf, bool fresh, bool apply) __attribute__((always_inline)) {
 #pragma unroll
-        for (int gs = 0; gs < NGS; gs++) {
-            floatx16 acc = {};
+        for (int gs = 0; gs < Q::NGS; gs++) {
+            floatx16 acc = fresh ? floatx16{} : carry;
 #pragma unroll
-            for (int k2 = 0; k2 < KSG; k2++) {
-                const int k0 = (gs * KSG + k2) * 16 + kq;
-                const half8 a_h = *(const half8*)&xh[buf][ai * KP + k0];
-                const half8 a_l = *(const half8*)&xl[buf][ai * KP + k0];
-                const half8 b = *(const half8*)&wl[buf][bn * KP + k0];
+            for (int k2 = 0; k2 < Q::KSG; k2++) {
+                const int k0 = (gs * Q::KSG + k2) * 16 + kq;
+                const half8 a_h = *(const half8*)&L.xh[buf][ai * S::KP + k0];
+                const half8 a_l = *(const half8*)&L.xl[buf][ai * S::KP + k0];
+                const half8 b = *(const half8*)&L.wl[buf][bn * S::KP + k0];
                 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, b, acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, b, acc, 0, 0, 0);
             }
-            const float sc = scl[buf][bn][gs];
+            if (apply) {
+                const float sc = L.scl[buf][bn][gs];
 #pragma unroll
-            for (int v = 0; v < 16; v++) tot[v] = __builtin_fmaf(sc, acc[v], tot[v]);
+                for (int v = 0; v < 16; v++) tot[v] = __builtin_fmaf(sc, acc[v], tot[v]);
+            } else {
+                carry = acc;
+            }
         }
     };
-    DnStage<NGS> r0, r1;
+    StageRegs<Q::NGS> r0, r1;
     load_stage(r0, 0);
     load_stage(r1, 1);
     store_stage(r0, 0);
     load_stage(r0, 2);
     __syncthreads();
     for (int s = 0; s < nstage; s += 2) {
-        mfma_stage(0);
+        mfma_stage(0, true, Q::SPG == 1);
         store_stage(r1, 1);
         load_stage(r1, s + 3);
         __syncthreads();
-        mfma_stage(1);
+        mfma_stage(1, Q::SPG == 1, true);
         store_stage(r0, 0);
         load_stage(r0, s + 4);
         __syncthreads();
     }
-    const int r = rt * MROWS + bn;
+    const int r = row0 + bn;
 #pragma unroll
     for (int v = 0; v < 16; v++) {
         const int i = th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
         if (i < ti.nt) {
-            const int slot = tok_s[i];
+            const int slot = L.tok[i];
             a.y[(size_t)slot * a.d + r] = __fmul_rn(a.tw[slot], tot[v]);
         }
     }
 }
 
+template <int G>
+__global__ void __launch_bounds__(MTHREADS, 1)
+k_down_mfma(ExpertArgs a) {
+    TileInfo ti;
+    if (!tile_info(a, blockIdx.x, &ti)) return;
+    constexpr size_t W = sizeof(DnLds<G, false>), N = sizeof(DnLds<G, true>);
+    __shared__ __align__(16) unsigned char sm[W > N ? W : N];
+    if (ti.nt <= 32 && narrow_rows_ok(a.d)) {
+        if (blockIdx.y & 1) return;               // the even block of the pair takes all 256 rows
+        down_tile<G, true>(a, ti, sm);
+    } else {
+        down_tile<G, false>(a, ti, sm);
+    }
+}
+
 // the MFMA branch needs whole 128-row tiles and an even number of 64-column
-// stages on both products
-bool mfma_shape_ok(int d, int m) { return d % MROWS == 0 && m % MROWS == 0 && (d / KS) % 2 == 0 && (m / KS) % 2 == 0; }
+// stages on both products (narrow tiles also take 256-row blocks where the
+// rows allow)
+bool mfma_shape_ok(int d, int m) { return d % MROWS == 0 && m % MROWS == 0 && (d / 64) % 2 == 0 && (m / 64) % 2 == 0; }
 
 hipError_t launch_gateup_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st) {
     if (max_tiles == 0) return hipSuccess;

@@ -293,28 +293,36 @@ def test_block_batch_invariance(qwen64):
         assert np.abs(one[0][0] - full[0][t]).max() <= 1e-6 * np.abs(one[0][0]).max()
 
 
-def test_block_zipf_large_segments(qwen64):
-    """512 tokens with Zipf-biased routing: segments of 0 to ~200 tokens."""
-    banner("block zipf B=512")
-    s = QWEN3
+@pytest.mark.parametrize("which", ["qwen64", "qwen32", "olmoe64"])
+def test_block_zipf_large_segments(request, which):
+    """512 tokens with Zipf-biased routing: segments of 0 to ~200 tokens, so
+    the MFMA branch runs beside the wave-item kernels and its down kernel
+    gets both tile shapes (33..64 tokens: 128-row blocks, up to 32 tokens:
+    256-row blocks)."""
+    layer = request.getfixturevalue(which)
+    banner(f"block zipf {which} B=512")
+    s = layer.shape
     B = 512
-    gw, x = apply_logit_bias(qwen64.gw[0], activations(B, s.d), zipf_bias(s.E, alpha=1.0))
-    w = torch.from_numpy(np.stack([gw, qwen64.gw[1]])).cuda()
-    qwen64.store.set_router(w)
+    gw, x = apply_logit_bias(layer.gw[0], activations(B, s.d), zipf_bias(s.E, alpha=1.0))
+    w = torch.from_numpy(np.stack([gw] + [layer.gw[l] for l in range(1, layer.L)])).cuda()
+    layer.store.set_router(w)
     try:
-        out, top, tw = _run_block(qwen64, 0, x)
-        tiles = qwen64.store.dense_tiles()
+        out, top, tw = _run_block(layer, 0, x)
+        tiles = layer.store.dense_tiles()
     finally:
-        qwen64.store.set_router(torch.from_numpy(qwen64.gw).cuda())
+        layer.store.set_router(torch.from_numpy(layer.gw).cuda())
     counts = np.bincount(top.ravel(), minlength=s.E)
+    dense = [c for c in counts if c >= 8]                                   # the default threshold
+    narrow = sum(1 for c in dense for j in range((c + 63) // 64) if c - 64 * j <= 32)
     print(f"  segment sizes: max {counts.max()} nonzero {np.count_nonzero(counts)}, "
-          f"dense tiles {tiles}", flush=True)
+          f"dense tiles {tiles} ({narrow} of up to 32 tokens)", flush=True)
     assert counts.max() >= 64
-    assert tiles == int(sum((c + 63) // 64 for c in counts if c >= 8))    # the default threshold
-    rout, rtop, rtw = qwen64.oracle(0, gw=gw).forward(x)
+    assert tiles == int(sum((c + 63) // 64 for c in dense))
+    assert 0 < narrow < tiles
+    rout, rtop, rtw = layer.oracle(0, gw=gw).forward(x)
     assert np.array_equal(top, rtop)
     err = _rel(out, rout)
-    print(f"  max rel err zipf B=512: {err:.3e}", flush=True)
+    print(f"  max rel err zipf {which} B=512: {err:.3e}", flush=True)
     assert err <= TOL
 
 
