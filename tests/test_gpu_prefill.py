@@ -62,7 +62,7 @@ def _check_rows(kv, b, kv_seq, T, L, label):
             assert bad == 0, f"{label}: layer {l} {'kv'[j]}: {bad} cache values off by more than a bf16 unit"
 
 
-@pytest.mark.parametrize("L,T", [(2, 200), (1, 600)])
+@pytest.mark.parametrize("L,T", [(2, 200), (1, 600), (1, 77)])
 def test_prefill_layers_matches_per_position_decode(L, T):
     dec, oracle, kv, w, W_lm = _model(L, maxT=640, B=1)
     rng = np.random.default_rng(T)
