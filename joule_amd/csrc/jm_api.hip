@@ -175,15 +175,22 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     if (dec) {
         JM_HIP(jm::launch_gateup_dec(a, st), "gate/up launch");
     } else {
-        JM_HIP(jm::launch_gateup(a, umax, st), "gate/up launch");
+        // the experts under dense_min (wave-item kernels: act digits, y rows
+        // of their slots) on the side stream, the MFMA experts (act hi/lo,
+        // their own y rows) here: disjoint slots and buffers
+        JM_HIP(hipEventRecord(s->fork_ev, st), "hipEventRecord fork");
+        JM_HIP(hipStreamWaitEvent(s->side_st, s->fork_ev, 0), "hipStreamWaitEvent fork");
+        JM_HIP(jm::launch_gateup(a, umax, s->side_st), "gate/up launch");
+        JM_HIP(jm::launch_down(a, umax, s->side_st), "down launch");
+        JM_HIP(hipEventRecord(s->join_ev, s->side_st), "hipEventRecord join");
         JM_HIP(jm::launch_gateup_mfma(a, max_tiles, st), "gate/up MFMA launch");
     }
     JM_MARK(2);
     if (dec) {
         JM_HIP(jm::launch_down_comb(a, st), "down/combine launch");
     } else {
-        JM_HIP(jm::launch_down(a, umax, st), "down launch");
         JM_HIP(jm::launch_down_mfma(a, max_tiles, st), "down MFMA launch");
+        JM_HIP(hipStreamWaitEvent(st, s->join_ev, 0), "hipStreamWaitEvent join");
         JM_HIP(jm::launch_combine(s->y, s->comb, B, k, d, io.resid, out, st), "combine launch");
     }
     JM_MARK(3);
@@ -285,6 +292,13 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
             for (int p = 0; p < 3; p++) { s->rec.so[p] = so[p]; s->rec.po[p] = po[p]; }
         }
     }
+    e = hipStreamCreateWithFlags(&s->side_st, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s->fork_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s->join_ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        jm_store_destroy(s);
+        return hip_fail(e, "jm_store_create side stream");
+    }
     *out = s;
     return 0;
 }
@@ -298,6 +312,9 @@ int jm_store_destroy(jm_store* s) {
     if (s->ws) (void)hipFree(s->ws);
     if (s->prof)
         for (int i = 0; i <= JM_STAGES; i++) (void)hipEventDestroy(s->ev[i]);
+    if (s->side_st) (void)hipStreamDestroy(s->side_st);
+    if (s->fork_ev) (void)hipEventDestroy(s->fork_ev);
+    if (s->join_ev) (void)hipEventDestroy(s->join_ev);
     jm::decode_free_all(s);
     delete s;
     return 0;

@@ -104,6 +104,11 @@ struct jm_store {
     // per-layer attention / MoE split of the last decode call (jm_store_profile)
     int dprof_n;
     hipEvent_t* dev_marks;      // [2 L + 2]
+    // dispatch path: the small experts' wave-item chain (gate/up, down) runs
+    // on side_st beside the MFMA chain, forked after the dispatch and joined
+    // before the combine (default priority, like every stream here)
+    hipStream_t side_st;
+    hipEvent_t fork_ev, join_ev;
 };
 
 namespace jm {

@@ -145,16 +145,23 @@ def test_decode_split_profile_and_errors():
     dec.store.close()
 
 
-def test_decode_graph_replays_match_eager():
+@pytest.mark.parametrize("B", [4, 40])
+def test_decode_graph_replays_match_eager(B):
     """The step replayed from a captured HIP graph gives the eager step's bits,
     replay after replay, with eager work and synchronisation in between; new
     positions within the same split count replay the same graph, a new split
-    count records a new one."""
+    count records a new one.  B=40 (320 slots) takes the MoE dispatch path,
+    whose small-expert chain runs on a second stream inside the graph."""
     shape = qwen3_30b_a3b(n_layers=2, maxT=400)
-    dec, _, kv = _model(shape, 64, 4)
-    x = torch.from_numpy(activations(4, shape.d)).cuda()
+    dec, _, kv = _model(shape, 64, B)
+    x = torch.from_numpy(activations(B, shape.d)).cuda()
     hid = torch.empty_like(x)
-    for pos in ([10, 130, 257, 300], [11, 131, 258, 301], [11, 131, 258, 399]):
+    if B == 4:
+        sets = ([10, 130, 257, 300], [11, 131, 258, 301], [11, 131, 258, 399])
+    else:
+        p1 = [10 + 7 * i for i in range(B)]
+        sets = (p1, [p + 1 for p in p1], [p + 1 for p in p1[:-1]] + [399])
+    for pos in sets:
         print(f"[decode] graph replays at positions {pos}", flush=True)
         dec.set_graph(False)
         want = dec.decode_layers_batch(x, pos, kv, torch.empty_like(x)).clone()
