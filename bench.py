@@ -343,6 +343,43 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
     return res
 
 
+def prefill_only(group, reps, n_layers=48, maxT=2176, Tp=512):
+    """Only the 512-token prefill of decode_step's model (for kernel
+    profiles): one warm-up pass, then `reps` timed passes of
+    jm_prefill_layers with the lm_head at the last position."""
+    import torch
+
+    from joule_amd.decoder import DecoderWeights, HipDecoder, KVCacheSet, qwen3_30b_a3b
+    from joule_amd.moe import QWEN3
+    from joule_amd.synth import decoder_weights
+
+    shape = qwen3_30b_a3b(n_layers, maxT)
+    log(f"prefill: building {n_layers} Qwen3-30B-A3B layers")
+    store, _ = build_layers(QWEN3, n_layers, group, seed=1000)
+    dec = HipDecoder(store, DecoderWeights(shape, **decoder_weights(shape)))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7000)
+    dec.set_lm_head((torch.randn((shape.V, shape.d), generator=g, device="cuda") * 0.02).to(torch.bfloat16))
+    dec.weights.t["embed"] = (torch.randn((shape.V, shape.d), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    dec._w = dec.weights.kernel_w()
+    prompt = torch.randint(0, shape.V, (Tp,), generator=g, device="cuda", dtype=torch.int32)
+    kvp = KVCacheSet(shape, 1)
+    plog = torch.empty(shape.V, dtype=torch.float32, device="cuda")
+    dec.prefill_layers(prompt, kvp, 0, plog)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        dec.prefill_layers(prompt, kvp, 0, plog)
+    e1.record(st)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    store.close()
+    return {"prompt_tokens": Tp, "layers": n_layers, "reps": reps, "ms": ms, "tok_per_s": Tp / (ms * 1e-3),
+            "logits_finite": bool(torch.isfinite(plog).all().item())}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -355,6 +392,8 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the 48-layer decode step (B=--batch, --steps timed steps); prints its JSON")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the 48-layer 512-token prefill (--steps timed passes); prints its JSON")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after timing, run 8 torch copies of this many MiB (a known-size kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -379,6 +418,10 @@ def main() -> int:
     if args.decode_only:
         r = decode_step(args.batch, args.steps, args.warmup, args.group)
         print(json.dumps({"decode_step": r}), flush=True)
+        return 0
+    if args.prefill_only:
+        r = prefill_only(args.group, args.steps)
+        print(json.dumps({"prefill_512": r}), flush=True)
         return 0
     shape, G, B, NL = QWEN3, args.group, args.batch, args.layers
     log(f"building {NL} Qwen3-shaped layers (G={G}) on the GPU")
