@@ -18,11 +18,11 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
-def _model(L, maxT, B, V=3000, seed=41):
-    moe = MoEShape(d=2048, m=768, E=128, topk=8, renorm=True)
+def _model(L, maxT, B, V=3000, seed=41, moe=None, group=64):
+    moe = moe or MoEShape(d=2048, m=768, E=128, topk=8, renorm=True)
     shape = DecoderShape(n_layers=L, moe=moe, n_heads=16, n_kv=4, maxT=maxT, V=V)
-    blob, offsets = torch_store(moe, L, 64)
-    store = HbmExpertStore(moe, L, blob, offsets, 64)
+    blob, offsets = torch_store(moe, L, group)
+    store = HbmExpertStore(moe, L, blob, offsets, group)
     gw = np.stack([router_weights(moe, l) for l in range(L)])
     store.set_router(torch.from_numpy(gw).cuda())
     t = decoder_weights(shape, norm_jitter=0.1)
@@ -37,7 +37,8 @@ def _model(L, maxT, B, V=3000, seed=41):
     torch.cuda.synchronize()
     w = {k: v.float().cpu().numpy() for k, v in dec.weights.t.items()}
     blob_h = blob.cpu().numpy()
-    moe_o = [O.OracleMoE(2048, 768, 128, 8, True, 64, gw[l], blob_h, offsets[:, l * 128:(l + 1) * 128])
+    E = moe.E
+    moe_o = [O.OracleMoE(2048, moe.m, E, moe.topk, moe.renorm, group, gw[l], blob_h, offsets[:, l * E:(l + 1) * E])
              for l in range(L)]
     oracle = D.OracleDecoder(L, 2048, 16, 4, 128, shape.eps, 1, False, w, moe_o)
     return dec, oracle, kv, w, lm.float().cpu().numpy()
@@ -78,6 +79,30 @@ def test_prefill_layers_matches_per_position_decode(L, T):
     print(f"  prefill L={L} T={T}: last-position logits max rel err {rel:.2e}", flush=True)
     assert rel < TOL, rel
     _check_rows(kv, 0, kv_seq, T, L, f"T={T}")
+    dec.store.close()
+
+
+@pytest.mark.parametrize("moe,group", [(MoEShape(d=2048, m=1024, E=64, topk=8, renorm=False), 64),
+                                       (MoEShape(d=2048, m=768, E=128, topk=8, renorm=True), 32)],
+                         ids=["olmoe-g64", "qwen3-g32"])
+def test_prefill_moe_variants(moe, group):
+    """The prefill with the other MoE shape (64 experts, m = 1024, no
+    renormalisation) and with Q4 group 32: the dispatch path, both MFMA tile
+    shapes and the small-expert kernels at other sizes."""
+    T = 150
+    dec, oracle, kv, w, W_lm = _model(1, maxT=256, B=1, moe=moe, group=group)
+    rng = np.random.default_rng(T + group)
+    prompt = rng.integers(0, 3000, size=T).tolist()
+    kv_seq = [(kv.data[0, 0, 0].float().cpu().numpy(), kv.data[0, 0, 1].float().cpu().numpy())]
+    print(f"[prefill] E={moe.E} m={moe.m} G{group} T={T}", flush=True)
+    logits = torch.empty(3000, dtype=torch.float32, device="cuda")
+    dec.prefill_layers(torch.tensor(prompt, dtype=torch.int32, device="cuda"), kv, 0, logits)
+    torch.cuda.synchronize()
+    want = _oracle_prefill(oracle, w, W_lm, prompt, kv_seq)
+    rel = np.abs(logits.cpu().numpy() - want).max() / np.abs(want).max()
+    print(f"  prefill E={moe.E} G{group}: last-position logits max rel err {rel:.2e}", flush=True)
+    assert rel < TOL, rel
+    _check_rows(kv, 0, kv_seq, T, 1, f"E={moe.E} G{group}")
     dec.store.close()
 
 
