@@ -292,6 +292,13 @@ int jm_embed_lookup(const jm_kernel_w* W, const jm_kernel_cfg* cfg, const int32_
  * reference. */
 int jm_store_decode_graph(jm_store* s, int enable);
 
+/* set_max_layers(n) (decode_kernel.c:1617): later jm_decode_layers_batch,
+ * jm_decode_layers_batch_argmax and jm_prefill_layers calls of this store
+ * run only layers 0 .. n-1 before the final norm (and lm_head); n < 0 (the
+ * default) runs all.  The reference's setting is process-global
+ * (g_max_layers); here it is per store. */
+int jm_store_set_max_layers(jm_store* s, int n);
+
 /* With buf set (device int32, `bytes` long), each later
  * jm_decode_layers_batch also copies every layer's selected experts into
  * buf[l][B][topk], for accounting and tests; NULL turns it off.  No

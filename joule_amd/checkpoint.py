@@ -45,6 +45,22 @@ def decoder_shape(cfg: dict, max_tokens: int = 4096) -> tuple[DecoderShape, str]
     qk, naming = _MOE_TYPES[mt]
     if cfg.get("q_lora_rank") or cfg.get("kv_lora_rank"):
         raise ValueError("MLA attention (latent KV) is not supported")
+    if cfg.get("clip_qkv") is not None:
+        # the reference's native decoder does not clamp q/k/v (only its
+        # Python streamer does, generic_streamer.py:118-121): refuse rather
+        # than decode such a checkpoint differently from either
+        raise ValueError("clip_qkv is not supported by the GPU decoder")
+    rs = cfg.get("rope_scaling") or (cfg.get("rope_parameters") if isinstance(cfg.get("rope_parameters"), dict)
+                                     else None)
+    rope_scaling: tuple = ()
+    if rs:
+        rtype = rs.get("rope_type", rs.get("type", "default"))
+        if rtype == "llama3":
+            rope_scaling = tuple(sorted((k, v) for k, v in rs.items() if isinstance(v, (int, float, str))))
+        elif rtype != "default":
+            # decoder3.py:405-410 handles llama3 only; other types would decode
+            # with unscaled tables
+            raise ValueError(f"rope_scaling type '{rtype}' is not supported (llama3 only)")
     heads = cfg["num_attention_heads"]
     hd = cfg.get("head_dim") or cfg["hidden_size"] // heads
     moe = MoEShape(d=cfg["hidden_size"], m=cfg.get("moe_intermediate_size") or cfg.get("intermediate_size", 0),
@@ -54,7 +70,8 @@ def decoder_shape(cfg: dict, max_tokens: int = 4096) -> tuple[DecoderShape, str]
                          n_kv=cfg.get("num_key_value_heads", heads), hd=hd,
                          eps=cfg.get("rms_norm_eps", cfg.get("layer_norm_eps", 1e-5)),
                          theta=cfg.get("rope_theta", 1e4), maxT=max_tokens, qk_norm_type=qk,
-                         bias_qkv=bool(cfg.get("attention_bias", False)), V=cfg["vocab_size"], name=mt)
+                         bias_qkv=bool(cfg.get("attention_bias", False)), V=cfg["vocab_size"], name=mt,
+                         rope_scaling=rope_scaling)
     return shape, naming
 
 

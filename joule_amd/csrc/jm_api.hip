@@ -90,6 +90,8 @@ int jm::store_reserve(jm_store* s, int B) {
         nslot * m * 2,                // act_l
         (size_t)B * d * 2,            // xsh
         (size_t)B * d * 2,            // xsl
+        (size_t)B * 4,                // xexp
+        nslot * ((m + 127) / 128) * 4,    // aexp
     };
     constexpr int NF = sizeof(sz) / sizeof(sz[0]);
     size_t total = 0;
@@ -107,7 +109,7 @@ int jm::store_reserve(jm_store* s, int B) {
                         (void**)&s->rank, (void**)&s->comb, (void**)&s->work, (void**)&s->tiles,
                         (void**)&s->n_tiles, (void**)&s->act, (void**)&s->adig,
                         (void**)&s->ascale, (void**)&s->y, (void**)&s->act_h, (void**)&s->act_l,
-                        (void**)&s->xsh, (void**)&s->xsl};
+                        (void**)&s->xsh, (void**)&s->xsl, (void**)&s->xexp, (void**)&s->aexp};
     for (int i = 0; i < NF; i++) {
         *slots[i] = p;
         p += align256(sz[i]);
@@ -162,9 +164,9 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     a.dense_min = jm::mfma_shape_ok(d, s->m) ? s->dense_min : 0x7FFFFFFF;
     r.dense_min = a.dense_min;
     a.tiles = s->tiles; a.n_tiles = s->n_tiles;
-    r.xsh = dec ? nullptr : s->xsh; r.xsl = dec ? nullptr : s->xsl;
-    a.xsh = s->xsh; a.xsl = s->xsl;
-    a.act_h = s->act_h; a.act_l = s->act_l;
+    r.xsh = dec ? nullptr : s->xsh; r.xsl = dec ? nullptr : s->xsl; r.xexp = s->xexp;
+    a.xsh = s->xsh; a.xsl = s->xsl; a.xexp = s->xexp;
+    a.act_h = s->act_h; a.act_l = s->act_l; a.aexp = s->aexp;
     a.logits = s->logits; a.renorm = s->renorm; a.top_w = s->top; a.tw_w = s->tw;
     const int max_tiles = nslot / JM_DENSE_TILE + E;
 #define JM_MARK(i) if (s->prof && stage_marks) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
@@ -251,6 +253,7 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
     s->renorm = cfg->norm_topk_prob ? 1 : 0;
     s->group = group;
     s->dense_min = JM_DENSE_MIN_DEFAULT;
+    s->max_layers = -1;
     s->blob = (const uint8_t*)blob;
     s->blob_bytes = blob_bytes;
     s->device = attr.device;

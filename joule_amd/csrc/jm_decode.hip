@@ -128,10 +128,15 @@ int check_decode_args(const jm_store* s, const jm_kernel_cfg* c, const jm_kernel
     return 0;
 }
 
+// Layers a step runs: all L, or the first max_layers (set_max_layers,
+// decode_kernel.c:1617; the loop bound at :1527 and :1568).
+int run_layers(const jm_store* s, int L) { return s->max_layers < 0 ? L : std::min(L, s->max_layers); }
+
 // Every launch of one decode step on st (after the staging copy).
 int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const float* xin, int B,
                  float* hidden, float* logits, int* out_tok, int S, int qpk, bool capturing, hipStream_t st) {
     const int L = c->L, d = c->d, H = c->n_heads, KH = c->n_kv;
+    const int nl = run_layers(s, L);
     const int nqkv = (H + 2 * KH) * HD;
     const int* pos_dev = (const int*)(s->tab + (size_t)2 * B * L);
     const bool marks = s->prof && !capturing;
@@ -139,7 +144,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
     JM_DMARK(0);
     JM_HIP(hipMemcpyAsync(s->h, xin, (size_t)B * d * 4, hipMemcpyDeviceToDevice, st), "copy xin");
     const float sdiv = jm::sqrtf_fast((float)HD);
-    for (int l = 0; l < L; l++) {
+    for (int l = 0; l < nl; l++) {
         JM_DMARK(2 * l + 1);
         jm::GemvArgs g{};
         g.x = s->h;
@@ -198,7 +203,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         if (s->trace && (l + 1) * tk <= s->trace_bytes)
             JM_HIP(hipMemcpyAsync((char*)s->trace + l * tk, s->top, tk, hipMemcpyDeviceToDevice, st), "top-k trace");
     }
-    JM_DMARK(2 * L + 1);
+    JM_DMARK(2 * nl + 1);
     JM_HIP(jm::launch_rms_rows(s->h, W->final_norm, B, d, c->eps, hidden, st), "final norm launch");
     if (logits || out_tok) {
         jm::LmArgs la{};
@@ -208,7 +213,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         la.best_i = s->lmi;
         JM_HIP(jm::launch_lm_head(la, out_tok, st), "lm_head launch");
     }
-    JM_DMARK(2 * L + 2);
+    JM_DMARK(2 * nl + 2);
 #undef JM_DMARK
     return 0;
 }
@@ -291,7 +296,7 @@ int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const
     JM_HIP(hipEventRecord(s->tab_ev, st), "hipEventRecord staging");
     s->tab_pending = 1;
     // per-layer split of the time (jm_store_profile): eager calls only
-    const int nmarks = 2 * L + 3;
+    const int nmarks = 2 * run_layers(s, L) + 3;
     if (s->prof && s->dprof_n != nmarks) {
         if (s->dev_marks) {
             JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
@@ -316,7 +321,8 @@ int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const
         key.xin = xin; key.hidden = hidden; key.logits = logits; key.out_tok = out_tok; key.lm = s->lm;
         key.B = B; key.S = S;
         key.trace = s->trace; key.trace_bytes = s->trace_bytes; key.ws = s->ws; key.dws = s->dws;
-        key.wt = s->wt; key.dense_min = s->dense_min;
+        key.wt = s->wt; key.wt_bf16 = s->wt_bf16; key.lm_V = s->lm_V; key.nl = run_layers(s, c->L);
+        key.dense_min = s->dense_min;
         if (!s->gexec || memcmp(&key, &s->gkey, sizeof key) != 0) {
             if (s->gexec) {
                 JM_HIP(hipStreamSynchronize(st), "hipStreamSynchronize before recapture");
@@ -479,6 +485,12 @@ int jm_embed_lookup(const jm_kernel_w* W, const jm_kernel_cfg* c, const int32_t*
 int jm_store_decode_graph(jm_store* s, int enable) {
     if (!s) return fail(JM_ERR_ARG, "store is NULL");
     s->dgraph = enable ? 1 : 0;      // a recorded step is kept for later replays
+    return 0;
+}
+
+int jm_store_set_max_layers(jm_store* s, int n) {
+    if (!s) return fail(JM_ERR_ARG, "store is NULL");
+    s->max_layers = n < 0 ? -1 : n;
     return 0;
 }
 

@@ -134,6 +134,18 @@ __device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t& hi, uin
     lo = pack_bf16x2(__fsub_rn(a, __uint_as_float(hi << 16)), __fsub_rn(b, __uint_as_float(hi & 0xFFFF0000u)));
 }
 
+// Power-of-two prescale of a row before its fp16 hi + lo split: the
+// exponent p >= 0 with mx * 2^-p < 2^15 for the row's largest magnitude mx,
+// 0 when the row already fits (or mx is not finite, so that Inf and NaN
+// propagate as they would unscaled).  Scaling by 2^-p and back by 2^p is
+// exact, so the products keep their bits wherever the fp16 range sufficed.
+__device__ __forceinline__ int split_exp(float mx) {
+    if (!(mx >= 32768.0f) || !(mx <= 3.4028235e38f)) return 0;
+    return (int)((__float_as_uint(mx) >> 23) & 0xFFu) - 127 - 14;
+}
+// 2^p as a float, -126 <= p <= 127
+__device__ __forceinline__ float exp2i(int p) { return __uint_as_float((uint32_t)(127 + p) << 23); }
+
 // SiLU(g) * u exactly as the reference writes it: (g / (1 + e^-g)) * u.
 __device__ __forceinline__ float swiglu(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_fast(-g))), u);

@@ -48,6 +48,7 @@ struct ExpertArgs {
     const float* tw;          // [B*k] routing weight of each slot
     const _Float16* xsh;      // [B][d] tokens split hi/lo in MFMA column order (MFMA branch)
     const _Float16* xsl;
+    const float* xexp;        // [B] 2^p: each token was split as x * 2^-p (p > 0 only past the fp16 range)
     const uint32_t* xdig;     // [B][d/G][NDIG][G/8] token digits
     const float* xscale;      // [B][d/G]
     float* act;               // [B*k][m]   SiLU(gate)*up per slot
@@ -63,6 +64,7 @@ struct ExpertArgs {
     const int* n_tiles;       // [1] how many
     _Float16* act_h;          // [B*k][m] act split into fp16 hi + lo for the MFMA down
     _Float16* act_l;
+    float* aexp;              // [B*k][m/128] 2^p of each 128-row block of act_h/act_l (split as act * 2^-p)
     // decode path with the top-k in the gate/up kernel (gateup_topk): the
     // router scores, and where the table is written
     const float* logits;      // [B][E]
@@ -88,6 +90,7 @@ struct RouteArgs {
     float* xscale;            // [B][d/G]
     _Float16* xsh;            // [B][d] token split hi/lo in MFMA column order (NULL: not needed)
     _Float16* xsl;
+    float* xexp;              // [B] 2^p of each token's split (x * 2^-p; p > 0 only past the fp16 range)
     int* top;                 // [B*k]
     float* tw;                // [B*k]
     int* seg_off;             // [E+1]

@@ -17,7 +17,11 @@
 //   tokens   each fp32 value split into hi = fp16(v) and lo = fp16(v - hi)
 //            (by the router kernel for x, by the gate/up epilogue for act),
 //            two products per tile, so the activations keep 22 significant
-//            bits (|v| < 65504).
+//            bits.  A row whose largest magnitude reaches 2^15 (x: a token;
+//            act: a slot's 128-row block) is split as v * 2^-p instead, and
+//            its products are scaled back by 2^p (exact): the gate/up
+//            epilogue for x, the down kernel's group scales for act, so the
+//            fp16 range never clips an activation.
 // Both operands keep each 8-column group in the order 0 4 1 5 2 6 3 7 that
 // the nibble dequantisation produces; the contraction does not care.
 // v_mfma_f32_32x32x16_f16 tiles with the tokens on the A side: lane l holds
@@ -131,6 +135,8 @@ struct GuLds {
     _Float16 wl[2][2][S::ROWS * S::KP];
     float scl[2][2][S::ROWS][Groups<G, S::KS>::NGS];
     int tok[S::TOK];
+    float xf[S::TOK];              // 2^p of each token's split
+    float amx[4][S::TOK];          // max |act| of each token over each row quarter's 32 rows
 };
 
 // Stage registers of one thread: 8 token values (hi and lo), one 16-byte
@@ -151,7 +157,11 @@ __device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo&
     const int w = tid >> 6;
     const int row0 = blockIdx.y * MROWS;          // first intermediate row of the block
     const int d = a.d, ng = d / G, nstage = d / S::KS;
-    if (tid < S::TOK) L.tok[tid] = tid < ti.nt ? a.seg_slot[ti.slot0 + tid] / a.topk : -1;
+    if (tid < S::TOK) {
+        const int b = tid < ti.nt ? a.seg_slot[ti.slot0 + tid] / a.topk : -1;
+        L.tok[tid] = b;
+        L.xf[tid] = b >= 0 ? a.xexp[b] : 1.0f;
+    }
     unsigned long long so[2], po[2];
     a.rec.get(0, a.key0 + ti.e, so[0], po[0]);
     a.rec.get(1, a.key0 + ti.e, so[1], po[1]);
@@ -246,17 +256,32 @@ __device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo&
         load_stage(r0, s + 4);
         __syncthreads();
     }
-    // act = SiLU(g) * u for this lane's row and 16 tokens
+    // act = SiLU(g) * u for this lane's row and 16 tokens (the token's
+    // split prescale undone first)
     const int r = row0 + bn;
+    float av[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int i = th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+        const float f = L.xf[i];
+        av[v] = swiglu(__fmul_rn(tg[v], f), __fmul_rn(tu[v], f));
+        // the token's max |act| over this half-wave's 32 rows
+        const float mx = seg_max<32>(i < ti.nt ? fabsf(av[v]) : 0.0f);
+        if ((lane & 31) == 0) L.amx[rq][i] = mx;
+    }
+    __syncthreads();
+    const int nb = a.m / MROWS;
 #pragma unroll
     for (int v = 0; v < 16; v++) {
         const int i = th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
         if (i < ti.nt) {
             const int slot = a.seg_slot[ti.slot0 + i];
-            const float av = swiglu(tg[v], tu[v]);
+            // one prescale per (slot, this block's 128 rows)
+            const int pe = split_exp(fmaxf(fmaxf(L.amx[0][i], L.amx[1][i]), fmaxf(L.amx[2][i], L.amx[3][i])));
+            if (rq == 0 && (lane & 31) == 0) a.aexp[(size_t)slot * nb + blockIdx.y] = exp2i(pe);
             _Float16 hh, ll;
-            split_hi_lo(av, hh, ll);
-            a.act[(size_t)slot * a.m + r] = av;
+            split_hi_lo(__fmul_rn(av[v], exp2i(-pe)), hh, ll);
+            a.act[(size_t)slot * a.m + r] = av[v];
             const size_t o = (size_t)slot * a.m + (r & ~7) + mfma_slot(r & 7);
             a.act_h[o] = hh;
             a.act_l[o] = ll;
@@ -302,6 +327,15 @@ __device__ __forceinline__ void down_tile(const ExpertArgs& a, const TileInfo& t
     unsigned long long so, po;
     a.rec.get(2, a.key0 + ti.e, so, po);
     __syncthreads();
+    // act blocks split with a prescale (a magnitude past 2^15): the tile then
+    // scales each token's group products back by 2^p of its 128-column block
+    const int nb = m / MROWS;
+    int any = 0;
+    for (int q = tid; q < S::TOK * nb; q += MTHREADS) {
+        const int sl = L.tok[q / nb];
+        if (sl >= 0 && a.aexp[(size_t)sl * nb + q % nb] != 1.0f) any = 1;
+    }
+    const bool scaled = __syncthreads_or(any) != 0;
 
     // staging: act (threads < XTHR, 8 columns of one token each), weights
     // (threads 0..255, one 16-byte piece of one row each)
@@ -346,7 +380,7 @@ __device__ __forceinline__ void down_tile(const ExpertArgs& a, const TileInfo& t
     const int ai = th * 32 + (lane & 31), bn = rq * 32 + (lane & 31), kq = 8 * (lane >> 5);
     floatx16 tot = {};
     floatx16 carry = {};                          // partial sum carried into a group's second stage
-    auto mfma_stage = [&](int buf, bool fresh, bool apply) __attribute__((always_inline)) {
+    auto mfma_stage = [&](int buf, int st, bool fresh, bool apply) __attribute__((always_inline)) {
 #pragma unroll
         for (int gs = 0; gs < Q::NGS; gs++) {
             floatx16 acc = fresh ? floatx16{} : carry;
@@ -361,8 +395,19 @@ __device__ __forceinline__ void down_tile(const ExpertArgs& a, const TileInfo& t
             }
             if (apply) {
                 const float sc = L.scl[buf][bn][gs];
+                if (scaled) {
+                    // stages never straddle a 128-column block
+                    const int g128 = st * S::KS / MROWS;
 #pragma unroll
-                for (int v = 0; v < 16; v++) tot[v] = __builtin_fmaf(sc, acc[v], tot[v]);
+                    for (int v = 0; v < 16; v++) {
+                        const int sl = L.tok[th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4)];
+                        const float f = sl >= 0 ? a.aexp[(size_t)sl * nb + g128] : 1.0f;
+                        tot[v] = __builtin_fmaf(__fmul_rn(sc, f), acc[v], tot[v]);
+                    }
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 16; v++) tot[v] = __builtin_fmaf(sc, acc[v], tot[v]);
+                }
             } else {
                 carry = acc;
             }
@@ -375,11 +420,11 @@ __device__ __forceinline__ void down_tile(const ExpertArgs& a, const TileInfo& t
     load_stage(r0, 2);
     __syncthreads();
     for (int s = 0; s < nstage; s += 2) {
-        mfma_stage(0, true, Q::SPG == 1);
+        mfma_stage(0, s, true, Q::SPG == 1);
         store_stage(r1, 1);
         load_stage(r1, s + 3);
         __syncthreads();
-        mfma_stage(1, Q::SPG == 1, true);
+        mfma_stage(1, s + 1, Q::SPG == 1, true);
         store_stage(r0, 0);
         load_stage(r0, s + 4);
         __syncthreads();

@@ -218,6 +218,17 @@ k_router_grp(RouteArgs a) {
             xv[i].w = __fmul_rn(__fmul_rn(xv[i].w, inv), bf16_bits_to_f32(w.y >> 16));
         }
     }
+    // the power-of-two prescale of the token's fp16 split (MFMA branch)
+    float xf = 1.0f;
+    if (a.xsh) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XV; i++)
+            mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xv[i].x), fabsf(xv[i].y))), fmaxf(fabsf(xv[i].z), fabsf(xv[i].w)));
+        const int pe = split_exp(seg_max<64>(mx));
+        xf = exp2i(-pe);
+        if (eg == 0 && lane == 0) a.xexp[b] = exp2i(pe);
+    }
 #pragma unroll
     for (int i = 0; i < XV; i++) {
         const int j = 4 * (lane + 64 * i);
@@ -267,7 +278,7 @@ k_router_grp(RouteArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int j = c + i;
-                const float v = xT[(size_t)(j & 7) * TP + (j >> 3)];
+                const float v = __fmul_rn(xT[(size_t)(j & 7) * TP + (j >> 3)], xf);
                 const _Float16 hh = (_Float16)v;
                 h[mfma_slot(i)] = hh;
                 l[mfma_slot(i)] = (_Float16)(v - (float)hh);
@@ -295,6 +306,7 @@ k_router_quad(RouteArgs a) {
     constexpr int T = d / 8;
     constexpr int TP = T + 4;
     __shared__ float xT[RQ_T][8 * TP];
+    __shared__ float xfs[RQ_T];                  // 2^-p of each token's fp16 split
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int eg = blockIdx.x * 4 + w;           // this wave's expert group
@@ -367,6 +379,17 @@ k_router_quad(RouteArgs a) {
 #pragma unroll
             for (int i = 0; i < XV; i++) xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
+        if (a.xsh) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < XV; i++)
+                mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xv[i].x), fabsf(xv[i].y))), fmaxf(fabsf(xv[i].z), fabsf(xv[i].w)));
+            const int pe = split_exp(seg_max<64>(mx));
+            if (lane == 0) {
+                xfs[w] = exp2i(-pe);
+                if (blockIdx.x == 0 && b < a.B) a.xexp[b] = exp2i(pe);
+            }
+        }
         float* xw = xT[w];
 #pragma unroll
         for (int i = 0; i < XV; i++) {
@@ -421,12 +444,13 @@ k_router_quad(RouteArgs a) {
                                        a.xscale + (size_t)b * ng + (ok ? p : 0));
         }
         if (a.xsh) {
+            const float xf = xfs[t];
             for (int c = (eg * 64 + lane) * 8; c < d; c += nvg * 64 * 8) {
                 half8 h, l;
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
                     const int j = c + i;
-                    const float v = xw[(size_t)(j & 7) * TP + (j >> 3)];
+                    const float v = __fmul_rn(xw[(size_t)(j & 7) * TP + (j >> 3)], xf);
                     const _Float16 hh = (_Float16)v;
                     h[mfma_slot(i)] = hh;
                     l[mfma_slot(i)] = (_Float16)(v - (float)hh);

@@ -25,6 +25,9 @@ struct DecKey {
     void* ws;
     void* dws;
     void* wt;
+    int wt_bf16;                // element type of the router copy: a reallocation may return the same address
+    int lm_V;
+    int nl;                     // layers the step runs (jm_store_set_max_layers)
     int dense_min;
 };
 
@@ -70,8 +73,11 @@ struct jm_store {
     _Float16* act_l;
     _Float16* xsh;              // tokens split for the MFMA gate/up
     _Float16* xsl;
+    float* xexp;                // [B] power-of-two prescale of each token's split
+    float* aexp;                // [B*k][m/128] power-of-two prescale of each act block's split
     int dense_min;              // segment size from which an expert takes the MFMA branch
     // ---- batch decode (jm_decode_layers_batch) ----
+    int max_layers;             // jm_store_set_max_layers: < 0 runs every layer
     int dec_B, dec_S, dec_nqkv, dec_hq, dec_V;   // sizes the decode workspace holds
     uint16_t* lm;               // [V][d] bf16 copy of the lm_head (jm_store_set_lm_head)
     int lm_V;

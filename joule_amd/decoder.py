@@ -70,6 +70,9 @@ class DecoderShape:
     bias_qkv: bool = False
     V: int = 0                   # vocabulary (embedding / lm_head rows); 0: none
     name: str = ""
+    # RoPE scaling of config.json as sorted (key, value) pairs; only
+    # rope_type "llama3" changes the tables (decoder3.py:405-407)
+    rope_scaling: tuple = ()
 
     @property
     def d(self) -> int:
@@ -93,11 +96,41 @@ def qwen3_30b_a3b(n_layers: int = 48, maxT: int = 4096, V: int = 151936) -> Deco
                         theta=1e6, maxT=maxT, qk_norm_type=1, V=V, name="qwen3-30b-a3b")
 
 
-def rope_tables(maxT: int, hd: int, theta: float) -> tuple[np.ndarray, np.ndarray]:
+def llama3_inv_freq(hd: int, theta: float, scaling: dict) -> np.ndarray:
+    """Inverse frequencies of rope_type "llama3" (generic_streamer.py:21-39):
+    the float32 base frequencies 1 / theta^(2i/hd), unchanged above the
+    high-frequency wavelength bound, divided by `factor` below the
+    low-frequency one, and blended linearly in between; float32 out."""
+    inv = (np.float32(1.0) / (np.float32(theta) ** (np.arange(0, hd, 2, dtype=np.float32) / np.float32(hd))))
+    inv = inv.astype(np.float32)
+    orig_max = float(scaling.get("original_max_position_tokens", 8192))
+    factor = float(scaling.get("factor", 1.0))
+    low_f = float(scaling.get("low_freq_factor", 1.0))
+    high_f = float(scaling.get("high_freq_factor", 4.0))
+    low_w, high_w = orig_max / low_f, orig_max / high_f
+    out = inv.copy()
+    for i, f in enumerate(inv.tolist()):
+        wavelen = 2 * 3.141592653589793 / f
+        if wavelen < high_w:
+            out[i] = f
+        elif wavelen > low_w:
+            out[i] = f / factor
+        else:
+            smooth = (orig_max / wavelen - low_f) / (high_f - low_f)
+            out[i] = (1 - smooth) * (f / factor) + smooth * f
+    return out
+
+
+def rope_tables(maxT: int, hd: int, theta: float, rope_scaling=None) -> tuple[np.ndarray, np.ndarray]:
     """cos, sin [maxT, hd] float32 as NativeDecoder._rope_tables
-    (decoder3.py:402-415): inv = 1 / theta^(2i/hd) in float64, angles
-    pos * inv, emb = cat(angles, angles) rounded to float32, then cos/sin."""
-    inv = 1.0 / (theta ** (np.arange(0, hd, 2).astype(np.float64) / hd))
+    (decoder3.py:402-415): inv = 1 / theta^(2i/hd) in float64 (or the llama3
+    frequencies when rope_scaling says rope_type "llama3"), angles pos * inv,
+    emb = cat(angles, angles) rounded to float32, then cos/sin."""
+    sc = dict(rope_scaling or ())
+    if sc.get("rope_type") == "llama3":
+        inv = llama3_inv_freq(hd, theta, sc).astype(np.float64)
+    else:
+        inv = 1.0 / (theta ** (np.arange(0, hd, 2).astype(np.float64) / hd))
     pos = np.arange(maxT).astype(np.float64)[:, None]
     fr = pos * inv[None, :]
     emb = np.concatenate([fr, fr], axis=-1).astype(np.float32)
@@ -137,7 +170,7 @@ class DecoderWeights:
                 self.t[k] = t[k].to(device=device, dtype=torch.float32).contiguous()
         if "embed" in t:
             self.t["embed"] = _bf16_dev(t["embed"], (shape.V, d), "embed", device)
-        cos, sin = rope_tables(shape.maxT, hd, shape.theta)
+        cos, sin = rope_tables(shape.maxT, hd, shape.theta, shape.rope_scaling)
         self.t["cos"] = torch.from_numpy(cos).to(device)
         self.t["sin"] = torch.from_numpy(sin).to(device)
 
@@ -312,6 +345,11 @@ class HipDecoder:
         x = self.embed(tok)
         out = self.decode_layers_batch_argmax(x, positions, kv)
         return [int(v) for v in out.cpu().tolist()]
+
+    def set_max_layers(self, n: int) -> None:
+        """Run only layers 0 .. n-1 in later calls (n < 0: all), as the
+        reference's set_max_layers (decode_kernel.c:1617)."""
+        _lib.check(_lib.lib().jm_store_set_max_layers(self.store._h, int(n)), "jm_store_set_max_layers")
 
     def trace_topk(self, buf: torch.Tensor | None) -> None:
         """Copy each layer's selected experts into buf [L, B, topk] (int32,

@@ -140,16 +140,25 @@ class OracleDecoder:
                 att[b, h * hd:(h + 1) * hd] = attention(qb[h], kc[:T, kh], vc[:T, kh], self.sdiv)
         return matvec(w["wo"][l], att)
 
-    def decode_layers_batch(self, x: np.ndarray, positions, kv) -> np.ndarray:
-        """Final-normed hidden state [B, d] after all layers."""
+    def decode_layers_batch(self, x: np.ndarray, positions, kv, trace: list | None = None,
+                            n_threads: int = 1, progress=None) -> np.ndarray:
+        """Final-normed hidden state [B, d] after all layers.  With `trace`
+        (a list), each layer appends a dict: "moe_in" (the normed input of
+        its MoE block), "top" (its selected experts) and "hidden" (the final
+        norm of h after this layer: what the step returns when it stops
+        there, set_max_layers, decode_kernel.c:1617)."""
         w = self.w
         h = np.array(x, F32, copy=True)
         for l in range(self.L):
             t = rms_norm(h, w["norm1"][l], self.eps)
             h = (h + self.layer_attn(l, t, positions, kv)).astype(F32)
             t = rms_norm(h, w["norm2"][l], self.eps)
-            out, _, _ = self.moe[l].forward(t)
+            out, top, _ = self.moe[l].forward(t, n_threads=n_threads)
             h = (h + out).astype(F32)
+            if trace is not None:
+                trace.append({"moe_in": t, "top": top, "hidden": rms_norm(h, w["final_norm"], self.eps)})
+            if progress:
+                progress(l)
         return rms_norm(h, w["final_norm"], self.eps)
 
 

@@ -558,7 +558,11 @@ JMO_API int jmo_layer_ffn_batch(const jmo_moe* p, const float* x, int B, float* 
         return -2;
     }
     const int workers = n_threads > 1 ? n_threads - 1 : 0;
-    if (B > 1 && !jmo_pool_init(workers)) return -3;
+    if (B > 1 && !jmo_pool_init(workers)) {
+        free(scores); free(sel); free(uh); free(cnt); free(pos); free(uidx); free(uw);
+        free(slot_u); free(act); free(y);
+        return -3;
+    }
 
     jmo_job job = {p, x, B, scores, sel, uh, uidx, uw, act, y, all_tokens};
     /* router scores: inline at B <= 1, pooled over experts otherwise */

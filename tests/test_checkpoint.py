@@ -40,3 +40,49 @@ def test_registry_defaults_and_families():
         decoder_shape(dict(olmoe, model_type="qwen3"))          # dense: not the MoE path
     with pytest.raises(ValueError):
         decoder_shape(dict(olmoe, model_type="deepseek", kv_lora_rank=512))   # MLA attention
+
+
+def test_clip_qkv_and_unknown_rope_scaling_are_refused():
+    # the reference keeps both fields (registry.py:76-79); the GPU decoder
+    # implements llama3 scaling and refuses what it would otherwise drop
+    with pytest.raises(ValueError, match="clip_qkv"):
+        decoder_shape(dict(QWEN3_30B, clip_qkv=8.0))
+    with pytest.raises(ValueError, match="yarn"):
+        decoder_shape(dict(QWEN3_30B, rope_scaling={"rope_type": "yarn", "factor": 4.0}))
+    s, _ = decoder_shape(dict(QWEN3_30B, rope_scaling={"rope_type": "default"}))
+    assert s.rope_scaling == ()
+    s, _ = decoder_shape(dict(QWEN3_30B, rope_parameters={"rope_type": "llama3", "factor": 8.0}))
+    assert dict(s.rope_scaling)["rope_type"] == "llama3"
+
+
+def test_llama3_rope_tables():
+    """generic_streamer.py:21-39, pinned by its three regimes: wavelengths
+    below orig_max / high_freq_factor keep the base frequency, those above
+    orig_max / low_freq_factor are divided by the factor, and in between the
+    frequency is the linear blend with smooth = (orig_max / wavelen - low) /
+    (high - low); the tables are cos/sin of pos * inv, duplicated halves."""
+    import numpy as np
+
+    from joule_amd.decoder import llama3_inv_freq, rope_tables
+
+    hd, theta = 128, 500000.0
+    sc = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_tokens": 8192}
+    base = (np.float32(1.0) / (np.float32(theta) ** (np.arange(0, hd, 2, dtype=np.float32) / np.float32(hd))))
+    inv = llama3_inv_freq(hd, theta, sc)
+    wl = 2 * np.pi / base.astype(np.float64)
+    hi, lo = wl < 8192 / 4.0, wl > 8192 / 1.0
+    mid = ~hi & ~lo
+    assert hi.any() and lo.any() and mid.any()       # all three regimes occur at this shape
+    assert np.array_equal(inv[hi], base[hi])
+    np.testing.assert_allclose(inv[lo], base[lo] / 8.0, rtol=1e-7)
+    smooth = (8192 / wl[mid] - 1.0) / 3.0
+    np.testing.assert_allclose(inv[mid], (1 - smooth) * base[mid] / 8.0 + smooth * base[mid], rtol=1e-6)
+    # blended frequencies lie between the two ends
+    assert np.all(inv[mid] <= base[mid]) and np.all(inv[mid] >= base[mid] / 8.0)
+    cos, sin = rope_tables(16, hd, theta, tuple(sorted(sc.items())))
+    ang = (np.arange(16, dtype=np.float64)[:, None] * inv.astype(np.float64)[None, :])
+    emb = np.concatenate([ang, ang], axis=1).astype(np.float32)
+    assert np.array_equal(cos, np.cos(emb)) and np.array_equal(sin, np.sin(emb))
+    c0, _ = rope_tables(16, hd, theta)
+    assert not np.array_equal(c0, cos)

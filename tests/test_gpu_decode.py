@@ -273,3 +273,53 @@ def test_decode_argmax_and_embedding():
     bad = dec.embed(torch.tensor([V, -1, 5], dtype=torch.int32, device="cuda")).cpu().numpy()
     assert np.isnan(bad[:2]).all() and np.array_equal(bad[2], E[5])
     dec.store.close()
+
+
+def test_decode_graph_follows_router_dtype_and_max_layers():
+    """A captured step is recorded again when the router copy changes element
+    type (a bf16-exact table, then a float32 one, possibly at the same
+    address) and when set_max_layers changes the layer count; the replays
+    equal the eager steps, and the step stopped after one layer equals the
+    oracle's first layer followed by the final norm."""
+    shape = qwen3_30b_a3b(n_layers=2, maxT=300)
+    B = 4
+    dec, oracle, kv = _model(shape, 64, B)
+    kv_h = _kv_host(kv, B, shape.n_layers)
+    x = torch.from_numpy(activations(B, shape.d)).cuda()
+    pos = [10, 20, 130, 299]
+    hid = torch.empty_like(x)
+    print("[decode] graph with the bf16 router copy", flush=True)
+    dec.set_graph(True)
+    a = dec.decode_layers_batch(x, pos, kv, hid).clone()
+    rng = np.random.default_rng(31)
+    gw32 = rng.normal(0, 0.02, (shape.n_layers, shape.moe.E, shape.d)).astype(np.float32)
+    dec.store.set_router(torch.from_numpy(gw32).cuda())
+    assert dec.store.router_bytes_per_weight() == 4
+    print("[decode] graph with the float32 router copy", flush=True)
+    g1 = dec.decode_layers_batch(x, pos, kv, hid).clone()
+    dec.set_graph(False)
+    e1 = dec.decode_layers_batch(x, pos, kv, torch.empty_like(x))
+    torch.cuda.synchronize()
+    assert torch.equal(g1, e1) and not torch.equal(a, g1)
+    # one layer only, graph and eager, against the oracle
+    gw = np.stack([router_weights(shape.moe, l) for l in range(shape.n_layers)])
+    dec.store.set_router(torch.from_numpy(gw).cuda())
+    print("[decode] set_max_layers(1)", flush=True)
+    dec.set_max_layers(1)
+    dec.set_graph(True)
+    one_g = dec.decode_layers_batch(x, pos, kv, hid).clone()
+    dec.set_graph(False)
+    one_e = dec.decode_layers_batch(x, pos, kv, torch.empty_like(x))
+    torch.cuda.synchronize()
+    assert torch.equal(one_g, one_e)
+    trace = []
+    oracle.decode_layers_batch(x.cpu().numpy(), pos, kv_h, trace=trace)
+    want = trace[0]["hidden"]
+    got = one_e.cpu().numpy()
+    rel = np.abs(got - want).max(axis=1) / np.abs(want).max(axis=1)
+    assert rel.max() <= TOL, rel
+    dec.set_max_layers(-1)
+    full = dec.decode_layers_batch(x, pos, kv, torch.empty_like(x)).cpu().numpy()
+    rel = np.abs(full - trace[1]["hidden"]).max(axis=1) / np.abs(trace[1]["hidden"]).max(axis=1)
+    assert rel.max() <= TOL, rel
+    dec.store.close()

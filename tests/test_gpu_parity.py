@@ -150,6 +150,24 @@ def test_router_bitexact(gpu, oracle_lib, shape, B):
     assert np.array_equal(lg2.view(np.uint32), lg.view(np.uint32)) and np.array_equal(top2, top)
 
 
+def test_router_lane_grouping_kat(gpu, oracle_lib):
+    """The lane-grouping known answer of tests/test_oracle_math.py through
+    the GPU router (float32 and bf16 tables, d = 512 and 2048): a row whose
+    products are 2^24, 1, 1, 1, -2^24 at j = 0, 8, 16, 9, 4 scores exactly 1
+    against x = ones only in the reference's chain order and sum tree."""
+    from test_oracle_math import router_kat_row
+    banner("router lane-grouping KAT")
+    for d in (512, 2048):
+        gw = router_weights(MoEShape(d=d, m=64, E=16, topk=4, renorm=True), 0)
+        gw[3] = router_kat_row(d)
+        x = np.ones((2, d), np.float32)
+        for bf16 in (False, True):
+            lg, _, _ = _gpu_router(gw, x, 4, True, bf16=bf16)
+            assert np.all(lg[:, 3] == 1.0), (d, bf16, lg[:, 3])
+            rl, _, _ = oracle_lib.route(gw, x, 4, True)
+            assert np.array_equal(lg.view(np.uint32), rl.view(np.uint32))
+
+
 def test_router_ties_lowest_index(gpu, oracle_lib):
     banner("router ties")
     E, d, k = 64, 256, 6
@@ -293,17 +311,19 @@ def test_block_batch_invariance(qwen64):
         assert np.abs(one[0][0] - full[0][t]).max() <= 1e-6 * np.abs(one[0][0]).max()
 
 
+@pytest.mark.parametrize("alpha", [1.0, 0.28])
 @pytest.mark.parametrize("which", ["qwen64", "qwen32", "olmoe64"])
-def test_block_zipf_large_segments(request, which):
-    """512 tokens with Zipf-biased routing: segments of 0 to ~200 tokens, so
-    the MFMA branch runs beside the wave-item kernels and its down kernel
-    gets both tile shapes (33..64 tokens: 128-row blocks, up to 32 tokens:
-    256-row blocks)."""
+def test_block_zipf_large_segments(request, which, alpha):
+    """512 tokens with Zipf-biased routing: segments of 0 to ~500 tokens
+    (alpha 1.0) or about 5 to 200 (alpha 0.28, the mix the benchmark
+    times), so the MFMA branch runs beside the wave-item kernels and its
+    down kernel gets both tile shapes (33..64 tokens: 128-row blocks, up to
+    32 tokens: 256-row blocks)."""
     layer = request.getfixturevalue(which)
-    banner(f"block zipf {which} B=512")
+    banner(f"block zipf {which} B=512 alpha={alpha}")
     s = layer.shape
     B = 512
-    gw, x = apply_logit_bias(layer.gw[0], activations(B, s.d), zipf_bias(s.E, alpha=1.0))
+    gw, x = apply_logit_bias(layer.gw[0], activations(B, s.d), zipf_bias(s.E, alpha=alpha))
     w = torch.from_numpy(np.stack([gw] + [layer.gw[l] for l in range(1, layer.L)])).cuda()
     layer.store.set_router(w)
     try:
@@ -319,10 +339,10 @@ def test_block_zipf_large_segments(request, which):
     assert counts.max() >= 64
     assert tiles == int(sum((c + 63) // 64 for c in dense))
     assert 0 < narrow < tiles
-    rout, rtop, rtw = layer.oracle(0, gw=gw).forward(x)
+    rout, rtop, rtw = layer.oracle(0, gw=gw).forward(x, n_threads=8)
     assert np.array_equal(top, rtop)
     err = _rel(out, rout)
-    print(f"  max rel err zipf {which} B=512: {err:.3e}", flush=True)
+    print(f"  max rel err zipf {which} B=512 alpha={alpha}: {err:.3e}", flush=True)
     assert err <= TOL
 
 

@@ -65,6 +65,51 @@ def test_router_dot_exact_and_tree(oracle_lib):
     assert abs(oracle_lib.router_dot(w, x) - exact) <= bound
 
 
+# A router row whose dot with x = ones depends on every part of the
+# reference's order (decode_kernel.c:234-256): products 2^24 at j=0, 1 at
+# j=8, 16 and 9, -2^24 at j=4, zeros elsewhere.  Lanes hold j = r (mod 8),
+# each an FMA chain in increasing j: lane 0 = (2^24 + 1) + 1 = 2^24 (each
+# 1 lost to ties-to-even), lane 1 = 1, lane 4 = -2^24; the tree
+# ((l0 + l4) + (l2 + l6)) + ((l1 + l5) + (l3 + l7)) gives 0 + 1 = 1.
+ROUTER_KAT = {0: 2.0**24, 8: 1.0, 16: 1.0, 9: 1.0, 4: -(2.0**24)}
+
+
+def router_kat_row(d):
+    w = np.zeros(d, np.float32)
+    for j, v in ROUTER_KAT.items():
+        w[j] = v
+    return w
+
+
+def test_router_lane_grouping_kat(oracle_lib):
+    """The KAT above at d = 24 and d = 2048 (zeros beyond j = 16 change no
+    rounding).  Plausible mistakes give other values, computed here in
+    float32 to show the KAT separates them: lanes over consecutive blocks of
+    j (2), one sequential sum (3), a lane chain in decreasing j (3), and the
+    j = r (mod 8) lanes summed in lane order instead of the tree (0)."""
+    f32 = np.float32
+    for d in (24, 2048):
+        w = router_kat_row(d)
+        assert oracle_lib.router_dot(w, np.ones(d, np.float32)) == 1.0
+    w = router_kat_row(24)
+
+    def tree(l):
+        return f32(f32(f32(l[0] + l[4]) + f32(l[2] + l[6])) + f32(f32(l[1] + l[5]) + f32(l[3] + l[7])))
+
+    def chain(vals):
+        acc = f32(0)
+        for v in vals:
+            acc = f32(acc + f32(v))
+        return acc
+
+    blocked = tree([chain(w[3 * r:3 * r + 3]) for r in range(8)])
+    sequential = chain(w)
+    reversed_chain = tree([chain(w[r::8][::-1]) for r in range(8)])
+    lane_order = chain([chain(w[r::8]) for r in range(8)])
+    assert tree([chain(w[r::8]) for r in range(8)]) == 1.0       # the reference's order, restated
+    assert [blocked, sequential, reversed_chain, lane_order] == [2.0, 3.0, 3.0, 0.0]
+
+
 def test_softmax_topk_ties_and_renorm(oracle_lib):
     s = np.array([1.0, 3.0, 3.0, 2.0, 3.0, -5.0], np.float32)
     p, top, tw = oracle_lib.softmax_topk(s, 4, renorm=False)
