@@ -129,6 +129,23 @@ int jm_store_set_dense_min(jm_store* s, int min_tokens);
 int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out,
                        int32_t* topk_idx, float* topk_w, void* stream);
 
+/* jm_layer_ffn_batch for callers that cannot allocate device memory: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  No counterpart in the reference.  The same kernels and
+ * results as jm_layer_ffn_batch, with the workspace in a fixed array of
+ * JM_NOALLOC_SCRATCH_BYTES on each device (reserved when the library first
+ * creates a store on that device, kept until the process ends) instead of
+ * the store's own: the call allocates nothing and fails with JM_ERR_SHAPE
+ * when B tokens of the store's shape need more workspace than the array
+ * holds (about 140 KB per token for the Qwen3-30B-A3B block: up to ~110
+ * tokens).  Every call on a device shares that device's array: calls that
+ * overlap on one GPU (other streams, other stores, other threads) race and
+ * must be serialised by the caller.  jm_store_copy_workspace does not see
+ * this workspace. */
+#define JM_NOALLOC_SCRATCH_BYTES (16u << 20)
+int jm_layer_ffn_batch_noalloc(jm_store* s, int layer, const float* x, int B, float* out,
+                               int32_t* topk_idx, float* topk_w, void* stream);
+
 /* Per-stage timing.  With profiling on, jm_layer_ffn_batch records a HIP
  * event around each of its JM_STAGES stages (route: router scores, top-k and
  * x digits, plus the dispatch when B * topk > 256; gate/up; down with the

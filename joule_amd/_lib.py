@@ -31,6 +31,7 @@ SIGNATURES = {
     "jm_store_set_dense_min": ([_vp, _i], _i),
     "jm_store_router_dtype": ([_vp, _vp], _i),
     "jm_layer_ffn_batch": ([_vp, _i, _vp, _i, _vp, _vp, _vp, _vp], _i),
+    "jm_layer_ffn_batch_noalloc": ([_vp, _i, _vp, _i, _vp, _vp, _vp, _vp], _i),
     "jm_store_copy_workspace": ([_vp, _i, _vp, _u64, _vp], _i),
     "jm_store_profile": ([_vp, _i], _i),
     "jm_store_stage_ms": ([_vp, _vp, _i], _i),

@@ -35,6 +35,34 @@ int hip_fail(hipError_t e, const char* what) {
 
 }  // namespace jm
 
+// Workspace of jm_layer_ffn_batch_noalloc: one fixed array on each device
+// the library runs on, held until the process ends.  Host code never uses
+// the array's name as an address: jm_store_create resolves the device
+// address once per device (hipGetSymbolAddress with that device current)
+// into scratch_ptr, and the calls lay the workspace out from there.
+static __device__ __align__(256) unsigned char scratch[JM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[MAX_DEVICES];
+
+// Resolve the scratch array's address on `device` (current) once.
+int resolve_scratch(int device) {
+    if (device < 0 || device >= MAX_DEVICES)
+        return jm::fail(JM_ERR_ARG, "device %d beyond the %d the no-allocation workspace tracks", device, MAX_DEVICES);
+    std::lock_guard<std::mutex> lk(scratch_mu);
+    if (scratch_ptr[device]) return 0;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return jm::hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    scratch_ptr[device] = p;
+    return 0;
+}
+
+}  // namespace
+
 namespace {
 
 using jm::aligned;
@@ -59,14 +87,17 @@ int check_group_shape(int d, int m, int group) {
 
 }  // namespace
 
-int jm::store_reserve(jm_store* s, int B) {
-    if (B <= s->cap_B) return 0;
+namespace {
+
+// Sizes of the Ws fields for B tokens, in field order.
+constexpr int WS_NF = 25;
+void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
     const int E = s->E, d = s->d, m = s->m, k = s->topk, G = s->group;
     const size_t nslot = (size_t)B * k;
     const size_t words_d = (size_t)(d / G) * JM_NDIG * (G / 8);
     const size_t words_m = (size_t)(m / 8) * JM_NDIG;
     const size_t max_tiles = nslot / JM_DENSE_TILE + E;
-    const size_t sz[] = {
+    const size_t v[WS_NF] = {
         (size_t)B * E * 4,            // logits
         nslot * 4,                    // top
         nslot * 4,                    // tw
@@ -93,27 +124,46 @@ int jm::store_reserve(jm_store* s, int B) {
         (size_t)B * 4,                // xexp
         nslot * ((m + 127) / 128) * 4,    // aexp
     };
-    constexpr int NF = sizeof(sz) / sizeof(sz[0]);
+    for (int i = 0; i < WS_NF; i++) sz[i] = v[i];
+}
+
+}  // namespace
+
+size_t jm::ws_bytes(const jm_store* s, int B) {
+    size_t sz[WS_NF];
+    ws_sizes(s, B, sz);
     size_t total = 0;
     for (size_t v : sz) total += align256(v);
+    return total;
+}
+
+void jm::ws_layout(const jm_store* s, int B, char* base, Ws* w) {
+    size_t sz[WS_NF];
+    ws_sizes(s, B, sz);
+    void** slots[WS_NF] = {(void**)&w->logits, (void**)&w->top, (void**)&w->tw, (void**)&w->xdig,
+                           (void**)&w->xscale, (void**)&w->seg_off, (void**)&w->seg_slot,
+                           (void**)&w->active, (void**)&w->n_active, (void**)&w->first_slot,
+                           (void**)&w->rank, (void**)&w->comb, (void**)&w->work, (void**)&w->tiles,
+                           (void**)&w->n_tiles, (void**)&w->act, (void**)&w->adig,
+                           (void**)&w->ascale, (void**)&w->y, (void**)&w->act_h, (void**)&w->act_l,
+                           (void**)&w->xsh, (void**)&w->xsl, (void**)&w->xexp, (void**)&w->aexp};
+    static_assert(sizeof(Ws) == WS_NF * sizeof(void*), "a size for every workspace field");
+    for (int i = 0; i < WS_NF; i++) {
+        *slots[i] = base;
+        base += align256(sz[i]);
+    }
+}
+
+int jm::store_reserve(jm_store* s, int B) {
+    if (B <= s->cap_B) return 0;
+    const size_t total = ws_bytes(s, B);
     void* mem = nullptr;
     JM_HIP(hipSetDevice(s->device), "hipSetDevice");
     JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize before workspace growth");
     JM_HIP(hipMalloc(&mem, total), "hipMalloc workspace");
     if (s->ws) (void)hipFree(s->ws);
     s->ws = mem;
-    char* p = (char*)mem;
-    void** slots[NF] = {(void**)&s->logits, (void**)&s->top, (void**)&s->tw, (void**)&s->xdig,
-                        (void**)&s->xscale, (void**)&s->seg_off, (void**)&s->seg_slot,
-                        (void**)&s->active, (void**)&s->n_active, (void**)&s->first_slot,
-                        (void**)&s->rank, (void**)&s->comb, (void**)&s->work, (void**)&s->tiles,
-                        (void**)&s->n_tiles, (void**)&s->act, (void**)&s->adig,
-                        (void**)&s->ascale, (void**)&s->y, (void**)&s->act_h, (void**)&s->act_l,
-                        (void**)&s->xsh, (void**)&s->xsl, (void**)&s->xexp, (void**)&s->aexp};
-    for (int i = 0; i < NF; i++) {
-        *slots[i] = p;
-        p += align256(sz[i]);
-    }
+    ws_layout(s, B, (char*)mem, &s->w);
     JM_HIP(hipMemset(mem, 0, total), "hipMemset workspace");
     JM_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize after workspace clear");
     s->cap_B = B;
@@ -132,11 +182,14 @@ int check_store(const jm_store* s) {
 namespace jm {
 
 int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const FfnIo& io,
-                bool stage_marks, hipStream_t st) {
+                bool stage_marks, hipStream_t st, const Ws* wsp) {
     if ((long long)B * s->topk > JM_MAX_SLOTS) return fail(JM_ERR_SHAPE, "B * topk must be <= %d", JM_MAX_SLOTS);
     if (B * s->topk > JM_DEC_SLOTS && (size_t)jm::dispatch_lds_ints(B * s->topk, s->E) * 4 > (size_t)s->lds_max)
         return fail(JM_ERR_SHAPE, "B * topk = %d slots over %d experts exceed the dispatch's LDS", B * s->topk, s->E);
-    if (int rc = store_reserve(s, B)) return rc;
+    if (!wsp) {
+        if (int rc = store_reserve(s, B)) return rc;
+    }
+    const Ws& w = wsp ? *wsp : s->w;
     const int E = s->E, d = s->d, k = s->topk, G = s->group;
     JM_HIP(hipSetDevice(s->device), "hipSetDevice");
     const int umax = std::min(E, B * k);
@@ -147,27 +200,27 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     r.wt_bf16 = s->wt_bf16;
     r.x = x; r.xpart = io.xpart; r.nxpart = io.nxpart; r.xmid = io.xmid;
     r.norm_w = io.norm_w; r.eps = io.eps; r.B = B; r.E = E; r.d = d; r.topk = k; r.renorm = s->renorm; r.group = G;
-    r.logits = s->logits; r.xdig = s->xdig; r.xscale = s->xscale; r.top = s->top; r.tw = s->tw;
-    r.seg_off = s->seg_off; r.seg_slot = s->seg_slot; r.active = s->active; r.n_active = s->n_active;
-    r.first_slot = s->first_slot; r.comb = s->comb; r.rank_scratch = s->rank;
-    r.work = s->work; r.umax = umax; r.rec = s->rec;
+    r.logits = w.logits; r.xdig = w.xdig; r.xscale = w.xscale; r.top = w.top; r.tw = w.tw;
+    r.seg_off = w.seg_off; r.seg_slot = w.seg_slot; r.active = w.active; r.n_active = w.n_active;
+    r.first_slot = w.first_slot; r.comb = w.comb; r.rank_scratch = w.rank;
+    r.work = w.work; r.umax = umax; r.rec = s->rec;
     r.key0 = (long long)layer * E;
-    r.dense_min = s->dense_min; r.tiles = s->tiles; r.n_tiles = s->n_tiles;
+    r.dense_min = s->dense_min; r.tiles = w.tiles; r.n_tiles = w.n_tiles;
     r.skip_topk = dec && jm::gateup_topk(B, E);
     jm::ExpertArgs a;
     a.blob = s->blob; a.rec = s->rec; a.key0 = (long long)layer * E; a.E = E;
-    a.work = s->work; a.umax = umax; a.seg_slot = s->seg_slot;
-    a.top = s->top; a.nslot = nslot; a.B = B;
+    a.work = w.work; a.umax = umax; a.seg_slot = w.seg_slot;
+    a.top = w.top; a.nslot = nslot; a.B = B;
     a.d = d; a.m = s->m; a.topk = k; a.group = G;
-    a.tw = s->tw; a.xdig = s->xdig; a.xscale = s->xscale;
-    a.act = s->act; a.adig = s->adig; a.ascale = s->ascale; a.y = s->y; a.out = out; a.resid = io.resid;
+    a.tw = w.tw; a.xdig = w.xdig; a.xscale = w.xscale;
+    a.act = w.act; a.adig = w.adig; a.ascale = w.ascale; a.y = w.y; a.out = out; a.resid = io.resid;
     a.dense_min = jm::mfma_shape_ok(d, s->m) ? s->dense_min : 0x7FFFFFFF;
     r.dense_min = a.dense_min;
-    a.tiles = s->tiles; a.n_tiles = s->n_tiles;
-    r.xsh = dec ? nullptr : s->xsh; r.xsl = dec ? nullptr : s->xsl; r.xexp = s->xexp;
-    a.xsh = s->xsh; a.xsl = s->xsl; a.xexp = s->xexp;
-    a.act_h = s->act_h; a.act_l = s->act_l; a.aexp = s->aexp;
-    a.logits = s->logits; a.renorm = s->renorm; a.top_w = s->top; a.tw_w = s->tw;
+    a.tiles = w.tiles; a.n_tiles = w.n_tiles;
+    r.xsh = dec ? nullptr : w.xsh; r.xsl = dec ? nullptr : w.xsl; r.xexp = w.xexp;
+    a.xsh = w.xsh; a.xsl = w.xsl; a.xexp = w.xexp;
+    a.act_h = w.act_h; a.act_l = w.act_l; a.aexp = w.aexp;
+    a.logits = w.logits; a.renorm = s->renorm; a.top_w = w.top; a.tw_w = w.tw;
     const int max_tiles = nslot / JM_DENSE_TILE + E;
 #define JM_MARK(i) if (s->prof && stage_marks) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
     JM_MARK(0);
@@ -193,12 +246,14 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     } else {
         JM_HIP(jm::launch_down_mfma(a, max_tiles, st), "down MFMA launch");
         JM_HIP(hipStreamWaitEvent(st, s->join_ev, 0), "hipStreamWaitEvent join");
-        JM_HIP(jm::launch_combine(s->y, s->comb, B, k, d, io.resid, out, st), "combine launch");
+        JM_HIP(jm::launch_combine(w.y, w.comb, B, k, d, io.resid, out, st), "combine launch");
     }
     JM_MARK(3);
 #undef JM_MARK
-    s->dec_last = dec;
-    s->last_B = B;
+    if (!wsp) {
+        s->dec_last = dec;
+        s->last_B = B;
+    }
     return 0;
 }
 
@@ -294,6 +349,11 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
             s->rec.stride = stride;
             for (int p = 0; p < 3; p++) { s->rec.so[p] = so[p]; s->rec.po[p] = po[p]; }
         }
+    }
+    if (int rc = resolve_scratch(s->device)) {
+        (void)hipFree(s->off_dev);
+        delete s;
+        return rc;
     }
     e = hipStreamCreateWithFlags(&s->side_st, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&s->fork_ev, hipEventDisableTiming);
@@ -399,8 +459,34 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
     hipStream_t st = (hipStream_t)stream;
     if (int rc = jm::ffn_enqueue(s, layer, x, B, out, jm::FfnIo{}, true, st)) return rc;
     const int k = s->topk;
-    if (topk_idx) JM_HIP(hipMemcpyAsync(topk_idx, s->top, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k");
-    if (topk_w) JM_HIP(hipMemcpyAsync(topk_w, s->tw, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k weights");
+    if (topk_idx) JM_HIP(hipMemcpyAsync(topk_idx, s->w.top, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k");
+    if (topk_w) JM_HIP(hipMemcpyAsync(topk_w, s->w.tw, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k weights");
+    return 0;
+}
+
+int jm_layer_ffn_batch_noalloc(jm_store* s, int layer, const float* x, int B, float* out,
+                               int32_t* topk_idx, float* topk_w, void* stream) {
+    if (int rc = check_store(s)) return rc;
+    if (!s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
+    if (layer < 0 || layer >= s->L) return fail(JM_ERR_ARG, "layer %d outside [0, %d)", layer, s->L);
+    if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
+    if (B == 0) return 0;
+    if (!x || !out) return fail(JM_ERR_ARG, "x and out must be non-NULL");
+    if (!aligned(x, 16) || !aligned(out, 16)) return fail(JM_ERR_ARG, "x and out must be 16-byte aligned");
+    const size_t need = jm::ws_bytes(s, B);
+    if (need > (size_t)JM_NOALLOC_SCRATCH_BYTES)
+        return fail(JM_ERR_SHAPE, "B=%d needs %zu bytes of workspace; the fixed no-allocation workspace holds %zu "
+                    "(use jm_layer_ffn_batch, or fewer tokens per call)", B, need, (size_t)JM_NOALLOC_SCRATCH_BYTES);
+    void* base = (s->device >= 0 && s->device < MAX_DEVICES) ? scratch_ptr[s->device] : nullptr;
+    if (!base) return fail(JM_ERR_ARG, "the no-allocation workspace of device %d is not resolved", s->device);
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    jm::Ws w;
+    jm::ws_layout(s, B, (char*)base, &w);
+    hipStream_t st = (hipStream_t)stream;
+    if (int rc = jm::ffn_enqueue(s, layer, x, B, out, jm::FfnIo{}, false, st, &w)) return rc;
+    const int k = s->topk;
+    if (topk_idx) JM_HIP(hipMemcpyAsync(topk_idx, w.top, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k");
+    if (topk_w) JM_HIP(hipMemcpyAsync(topk_w, w.tw, (size_t)B * k * 4, hipMemcpyDeviceToDevice, st), "copy top-k weights");
     return 0;
 }
 
@@ -438,15 +524,15 @@ int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t by
     const void* src = nullptr;
     size_t cap = 0;
     switch (field) {
-        case JM_WS_LOGITS: src = s->logits; cap = (size_t)s->last_B * s->E * 4; break;
-        case JM_WS_SEG_OFF: src = s->seg_off; cap = (size_t)(s->E + 1) * 4; break;
-        case JM_WS_SEG_SLOT: src = s->seg_slot; cap = nslot * 4; break;
-        case JM_WS_ACTIVE: src = s->active; cap = (size_t)s->E * 4; break;
-        case JM_WS_N_ACTIVE: src = s->n_active; cap = 4; break;
-        case JM_WS_FIRST_SLOT: src = s->first_slot; cap = (size_t)s->E * 4; break;
-        case JM_WS_ACT: src = s->act; cap = nslot * s->m * 4; break;
-        case JM_WS_Y: src = s->y; cap = nslot * s->d * 4; break;
-        case JM_WS_N_DENSE_TILES: src = s->n_tiles; cap = 4; break;
+        case JM_WS_LOGITS: src = s->w.logits; cap = (size_t)s->last_B * s->E * 4; break;
+        case JM_WS_SEG_OFF: src = s->w.seg_off; cap = (size_t)(s->E + 1) * 4; break;
+        case JM_WS_SEG_SLOT: src = s->w.seg_slot; cap = nslot * 4; break;
+        case JM_WS_ACTIVE: src = s->w.active; cap = (size_t)s->E * 4; break;
+        case JM_WS_N_ACTIVE: src = s->w.n_active; cap = 4; break;
+        case JM_WS_FIRST_SLOT: src = s->w.first_slot; cap = (size_t)s->E * 4; break;
+        case JM_WS_ACT: src = s->w.act; cap = nslot * s->m * 4; break;
+        case JM_WS_Y: src = s->w.y; cap = nslot * s->d * 4; break;
+        case JM_WS_N_DENSE_TILES: src = s->w.n_tiles; cap = 4; break;
         default: return fail(JM_ERR_ARG, "unknown workspace field %d", field);
     }
     if (!src || s->last_B == 0) return fail(JM_ERR_ARG, "no call has run on this store yet");

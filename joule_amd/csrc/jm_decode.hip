@@ -201,7 +201,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         if (int rc = jm::ffn_enqueue(s, l, s->h, B, s->h, io, false, st)) return rc;
         const size_t tk = (size_t)B * c->topk * 4;
         if (s->trace && (l + 1) * tk <= s->trace_bytes)
-            JM_HIP(hipMemcpyAsync((char*)s->trace + l * tk, s->top, tk, hipMemcpyDeviceToDevice, st), "top-k trace");
+            JM_HIP(hipMemcpyAsync((char*)s->trace + l * tk, s->w.top, tk, hipMemcpyDeviceToDevice, st), "top-k trace");
     }
     JM_DMARK(2 * nl + 1);
     JM_HIP(jm::launch_rms_rows(s->h, W->final_norm, B, d, c->eps, hidden, st), "final norm launch");

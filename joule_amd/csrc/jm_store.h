@@ -9,6 +9,40 @@
 #include "../../include/joule_amd.h"
 #include "jm_kernels.h"
 
+namespace jm {
+
+// The MoE block's workspace for B tokens: one device region, each field
+// 256-byte aligned, in this order (ws_layout).
+struct Ws {
+    float* logits;              // [B][E]
+    int* top;                   // [B*k]
+    float* tw;                  // [B*k]
+    uint32_t* xdig;             // [B][d/G][NDIG][G/8] token digits
+    float* xscale;              // [B][d/G]
+    int* seg_off;               // [E+1]
+    int* seg_slot;              // [B*k]
+    int* active;                // [E]
+    int* n_active;              // [1]
+    int* first_slot;            // [E]
+    int* rank;                  // [B*k]
+    int* comb;                  // [B*k]
+    ExpertWork* work;           // [E]
+    int2* tiles;                // [B*k/64 + E] dense tiles (dispatch path)
+    int* n_tiles;               // [1]
+    float* act;                 // [B*k][m]
+    uint32_t* adig;             // [B*k][m/8][NDIG] act digits
+    float* ascale;              // [B*k][m/32]
+    float* y;                   // [B*k][d]
+    _Float16* act_h;            // [B*k][m] act split for the MFMA down
+    _Float16* act_l;
+    _Float16* xsh;              // [B][d] tokens split for the MFMA gate/up
+    _Float16* xsl;
+    float* xexp;                // [B] power-of-two prescale of each token's split
+    float* aexp;                // [B*k][m/128] power-of-two prescale of each act block's split
+};
+
+}  // namespace jm
+
 // What a captured decode step depends on (the graph bakes in kernel
 // arguments): compared bytewise, built from a zeroed struct.
 struct DecKey {
@@ -47,34 +81,10 @@ struct jm_store {
     int cap_B;
     int last_B;
     void* ws;
-    float* logits;
-    int* top;
-    float* tw;
-    uint32_t* xdig;
-    float* xscale;
-    int* seg_off;
-    int* seg_slot;
-    int* active;
-    int* n_active;
-    int* first_slot;
-    int* rank;
-    int* comb;
-    jm::ExpertWork* work;
-    float* act;
+    jm::Ws w;                   // the fields of ws for cap_B tokens
     // optional per-stage events (jm_store_profile)
     int prof;
     hipEvent_t ev[JM_STAGES + 1];
-    uint32_t* adig;
-    float* ascale;
-    float* y;
-    int2* tiles;                // dense tiles (dispatch path)
-    int* n_tiles;
-    _Float16* act_h;            // act split for the MFMA down
-    _Float16* act_l;
-    _Float16* xsh;              // tokens split for the MFMA gate/up
-    _Float16* xsl;
-    float* xexp;                // [B] power-of-two prescale of each token's split
-    float* aexp;                // [B*k][m/128] power-of-two prescale of each act block's split
     int dense_min;              // segment size from which an expert takes the MFMA branch
     // ---- batch decode (jm_decode_layers_batch) ----
     int max_layers;             // jm_store_set_max_layers: < 0 runs every layer
@@ -128,6 +138,10 @@ inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 // MoE workspace for batches of up to B tokens.
 int store_reserve(jm_store* s, int B);
+// Bytes of the workspace layout for B tokens of the store's shape, and the
+// fields laid out from base (256-byte aligned).
+size_t ws_bytes(const jm_store* s, int B);
+void ws_layout(const jm_store* s, int B, char* base, Ws* w);
 
 // Decoder-layer extras of the MoE block around its input and output.
 struct FfnIo {
@@ -139,10 +153,11 @@ struct FfnIo {
     const float* resid = nullptr;   // out = resid + block (resid may alias out)
 };
 
-// Enqueue the MoE block of one layer on x [B][d] into out [B][d].
+// Enqueue the MoE block of one layer on x [B][d] into out [B][d], with the
+// workspace w (nullptr: the store's own, grown to B tokens first).
 // stage_marks: record the store's stage events.
 int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const FfnIo& io,
-                bool stage_marks, hipStream_t st);
+                bool stage_marks, hipStream_t st, const Ws* w = nullptr);
 
 // Release the batch-decode workspace, staging and events.
 void decode_free_all(jm_store* s);
