@@ -3,7 +3,9 @@
     python -m joule_amd.build
 
 compiles joule_amd/csrc/*.hip (objects under joule_amd/_build/) into
-joule_amd/libjoule_amd.so with hipcc.
+joule_amd/libjoule_amd.so with hipcc, and joule_amd/csrc/probe/jm_probe.hip
+into joule_amd/libjoule_probe.so (launch and hand-off cost probes that
+bench.py --probe runs; not part of the MoE block).
 Flags: -ffp-contract=off (fused multiply-adds are written explicitly where
 the reference arithmetic has them) and packed FP32 instructions disabled.
 """
@@ -21,6 +23,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 SRC = sorted((PKG / "csrc").glob("*.hip"))
 OUT = PKG / "libjoule_amd.so"
+PROBE_SRC = PKG / "csrc" / "probe" / "jm_probe.hip"
+PROBE_OUT = PKG / "libjoule_probe.so"
 ARCH = os.environ.get("JM_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
@@ -58,6 +62,8 @@ def build(verbose: bool = False) -> Path:
     compile_flags = [f for f in FLAGS if f != "-shared"]
     objs = [objdir / (src.stem + ".o") for src in SRC]
     jobs = [[hipcc(), *compile_flags, "-c", str(src), "-o", str(obj)] for src, obj in zip(SRC, objs)]
+    probe_tmp = PROBE_OUT.with_suffix(".so.tmp")
+    jobs.append([hipcc(), *FLAGS, str(PROBE_SRC), "-o", str(probe_tmp)])
     workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
     with ThreadPoolExecutor(max_workers=workers) as ex:
         for fut in [ex.submit(_run, cmd, verbose) for cmd in jobs]:
@@ -65,6 +71,7 @@ def build(verbose: bool = False) -> Path:
     tmp = OUT.with_suffix(".so.tmp")
     _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, OUT)
+    os.replace(probe_tmp, PROBE_OUT)
     return OUT
 
 

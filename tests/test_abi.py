@@ -41,6 +41,25 @@ def test_library_exports_header_symbols():
         assert hasattr(L, name)
 
 
+def test_probe_library_exports_header_symbols():
+    """libjoule_probe.so (bench.py --probe) exports what joule_probe.h declares."""
+    from joule_amd.build import PROBE_OUT
+
+    if not PROBE_OUT.exists():
+        pytest.skip("libjoule_probe.so not built (run python -m joule_amd.build)")
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "joule_probe.h").read_text(), flags=re.S)
+    declared = sorted(set(re.findall(r"\b(jmp_[a-z0-9_]+)\s*\(", text)))
+    assert declared == ["jmp_handoff", "jmp_last_error", "jmp_launch_chain"]
+    syms = subprocess.run(["nm", "-D", "--defined-only", str(PROBE_OUT)], capture_output=True,
+                          text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (jmp_[a-z0-9_]+)", syms))
+    assert set(declared) <= exported
+    P = ctypes.CDLL(str(PROBE_OUT))
+    f = ctypes.c_float()
+    assert P.jmp_launch_chain(0, 0, 1, ctypes.byref(f)) == -1      # argument check, no GPU work
+    assert P.jmp_handoff(0, 1, 0, 1, ctypes.byref(f), None) == -1
+
+
 def test_kernel_cfg_layout():
     # KernelCfg of decode_kernel.c:269-286: 15 ints and one float, 64 bytes,
     # eps at byte 32 and norm_topk_prob at byte 52 (decoder3.py:35-46)
