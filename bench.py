@@ -47,7 +47,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
-PEAK_MFMA_TFLOPS = 2500.0      # dense bf16/fp16 MFMA
+PEAK_MFMA_I8_TOPS = 5000.0     # dense int8 MFMA (the dense branch's operands)
 ZIPF_ALPHA = 0.28              # Zipf(1.1) bias strength: per-expert counts about 5..200 over 512 tokens
 
 # HBM traffic of the block's kernels on the default workload (B=8, group 64,
@@ -157,6 +157,47 @@ def block_numbers(shape, group, B, ms, stages, U, steps, n_layers, router_bytes=
         "down_GBs": down / (stages["down"] * 1e-3) / 1e9,
         "stages_ms": stages,
     }
+
+
+def zipf_block(store, gw, steps, n_layers, bz=512):
+    """The prefill-style Qwen3 block: bz tokens with Zipf(1.1)-biased routing
+    (per-expert counts about 5..200 at bz = 512); the experts with at least
+    dense_min (8) slots take the MFMA branch.  Returns (results, biased
+    router table, biased x)."""
+    import numpy as np
+    import torch
+
+    from joule_amd.synth import activations, apply_logit_bias, zipf_bias
+
+    shape, G = store.shape, store.group
+    rb = store.router_bytes_per_weight()
+    bias = zipf_bias(shape.E, s=1.1, alpha=ZIPF_ALPHA)
+    xz_np = activations(bz, shape.d)
+    gz = np.stack([apply_logit_bias(gw[l], xz_np, bias)[0] for l in range(n_layers)])
+    xz_np = apply_logit_bias(gw[0], xz_np, bias)[1]
+    xz = torch.from_numpy(xz_np).cuda()
+    store.set_router(torch.from_numpy(gz).cuda())
+    nz = max(steps // 8, 20)
+    m2, st2, U2 = measure(store, gz, xz, nz, 5, n_layers)
+    r = block_numbers(shape, G, bz, m2, st2, U2, nz, n_layers, rb)
+    top = torch.empty((bz, shape.topk), dtype=torch.int32, device="cuda")
+    store.layer_ffn_batch(0, xz, topk_idx=top)
+    tiles = store.dense_tiles()
+    counts = np.bincount(top.cpu().numpy().ravel(), minlength=shape.E)
+    flops = 2.0 * bz * shape.topk * 3 * shape.d * shape.m
+    res = {
+        **{k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac", "experts_routed_avg")},
+        "tflops": flops / (m2 * 1e-3) / 1e12,
+        "mfma_frac_of_int8_peak": flops / (m2 * 1e-3) / 1e12 / PEAK_MFMA_I8_TOPS,
+        "zipf_alpha": ZIPF_ALPHA, "count_max": int(counts.max()), "count_min": int(counts.min()),
+        "dense_experts": int((counts >= 8).sum()), "dense_tiles": tiles,
+        "stages_ms": st2,
+    }
+    log(f"sweep qwen3 zipf B={bz}: {r['tok_per_s']:.0f} tok/s, {m2 * 1e3:.1f} us/step, "
+        f"{flops / (m2 * 1e-3) / 1e12:.1f} TFLOP/s, counts {counts.min()}..{counts.max()}, "
+        f"dense tiles {tiles}, stages {st2}")
+    store.set_router(torch.from_numpy(gw).cuda())
+    return res, gz, xz_np
 
 
 def host_info() -> dict:
@@ -524,6 +565,8 @@ def main() -> int:
                     help="only the 48-layer decode step (B=--batch, --steps timed steps); prints its JSON")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 48-layer 512-token prefill (--steps timed passes); prints its JSON")
+    ap.add_argument("--zipf-only", action="store_true",
+                    help="only the 512-token Zipf-routed block (MFMA branch) on the 16-layer store; prints its JSON")
     ap.add_argument("--probe", action="store_true",
                     help="only the launch and hand-off cost probes (libjoule_probe.so); prints their JSON")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -561,6 +604,9 @@ def main() -> int:
     shape, G, B, NL = QWEN3, args.group, args.batch, args.layers
     log(f"building {NL} Qwen3-shaped layers (G={G}) on the GPU")
     store, gw = build_layers(shape, NL, G, seed=1000)
+    if args.zipf_only:
+        print(json.dumps({"qwen3_zipf512": zipf_block(store, gw, args.steps, NL)[0]}), flush=True)
+        return 0
     x_np = activations(B, shape.d)
     x = torch.from_numpy(x_np).cuda()
     log(f"timing B={B}: {args.warmup} warm-up + {args.steps} steps")
@@ -605,40 +651,10 @@ def main() -> int:
                 cpu_sweep[f"qwen3_B{b}"] = cpu_case(moes, xs[b], cpu_share, f"qwen3 B={b}")[0]
 
     if not args.no_sweep:
-        # prefill-style batch: 512 tokens with Zipf(1.1)-biased routing (per-expert
-        # counts about 5..200); the MFMA branch takes the experts with >= 8 slots
-        from joule_amd.synth import apply_logit_bias, zipf_bias
-
-        bz = 512
-        bias = zipf_bias(shape.E, s=1.1, alpha=ZIPF_ALPHA)
-        xz_np = activations(bz, shape.d)
-        gz = np.stack([apply_logit_bias(gw[l], xz_np, bias)[0] for l in range(NL)])
-        xz_np = apply_logit_bias(gw[0], xz_np, bias)[1]
-        xz = torch.from_numpy(xz_np).cuda()
-        store.set_router(torch.from_numpy(gz).cuda())
-        nz = max(args.steps // 8, 20)
-        m2, st2, U2 = measure(store, gz, xz, nz, 5, NL)
-        r = block_numbers(shape, G, bz, m2, st2, U2, nz, NL, rb)
-        top = torch.empty((bz, shape.topk), dtype=torch.int32, device="cuda")
-        store.layer_ffn_batch(0, xz, topk_idx=top)
-        tiles = store.dense_tiles()
-        counts = np.bincount(top.cpu().numpy().ravel(), minlength=shape.E)
-        flops = 2.0 * bz * shape.topk * 3 * shape.d * shape.m
-        sweep["qwen3_zipf512"] = {
-            **{k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac", "experts_routed_avg")},
-            "tflops": flops / (m2 * 1e-3) / 1e12,
-            "mfma_frac_of_bf16_peak": flops / (m2 * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS,
-            "zipf_alpha": ZIPF_ALPHA, "count_max": int(counts.max()), "count_min": int(counts.min()),
-            "dense_experts": int((counts >= 8).sum()), "dense_tiles": tiles,
-            "stages_ms": st2,
-        }
-        log(f"sweep qwen3 zipf B={bz}: {r['tok_per_s']:.0f} tok/s, {m2 * 1e3:.1f} us/step, "
-            f"{flops / (m2 * 1e-3) / 1e12:.1f} TFLOP/s, counts {counts.min()}..{counts.max()}, "
-            f"dense tiles {tiles}, stages {st2}")
-        store.set_router(torch.from_numpy(gw).cuda())
+        sweep["qwen3_zipf512"], gz, xz_np = zipf_block(store, gw, args.steps, NL)
         if cpu_on:
             zmoes = oracle_moes(store, gz, 1)
-            cpu_sweep["qwen3_zipf512"] = cpu_case(zmoes, xz_np, cpu_share, f"qwen3 zipf B={bz}", min_calls=1)[0]
+            cpu_sweep["qwen3_zipf512"] = cpu_case(zmoes, xz_np, cpu_share, "qwen3 zipf B=512", min_calls=1)[0]
             del zmoes
 
     cpu = None

@@ -117,12 +117,12 @@ void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
         nslot * words_m * 4,          // adig
         nslot * (m / 32) * 4,         // ascale
         nslot * d * 4,                // y
-        nslot * m * 2,                // act_h
-        nslot * m * 2,                // act_l
-        (size_t)B * d * 2,            // xsh
-        (size_t)B * d * 2,            // xsl
-        (size_t)B * 4,                // xexp
-        nslot * ((m + 127) / 128) * 4,    // aexp
+        nslot * m,                    // aqh
+        nslot * m,                    // aql
+        (size_t)B * d,                // xqh
+        (size_t)B * d,                // xql
+        (size_t)B * (d / G) * 4,      // xqs
+        nslot * (m / G) * 4,          // aqs
     };
     for (int i = 0; i < WS_NF; i++) sz[i] = v[i];
 }
@@ -145,8 +145,8 @@ void jm::ws_layout(const jm_store* s, int B, char* base, Ws* w) {
                            (void**)&w->active, (void**)&w->n_active, (void**)&w->first_slot,
                            (void**)&w->rank, (void**)&w->comb, (void**)&w->work, (void**)&w->tiles,
                            (void**)&w->n_tiles, (void**)&w->act, (void**)&w->adig,
-                           (void**)&w->ascale, (void**)&w->y, (void**)&w->act_h, (void**)&w->act_l,
-                           (void**)&w->xsh, (void**)&w->xsl, (void**)&w->xexp, (void**)&w->aexp};
+                           (void**)&w->ascale, (void**)&w->y, (void**)&w->aqh, (void**)&w->aql,
+                           (void**)&w->xqh, (void**)&w->xql, (void**)&w->xqs, (void**)&w->aqs};
     static_assert(sizeof(Ws) == WS_NF * sizeof(void*), "a size for every workspace field");
     for (int i = 0; i < WS_NF; i++) {
         *slots[i] = base;
@@ -214,12 +214,13 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     a.d = d; a.m = s->m; a.topk = k; a.group = G;
     a.tw = w.tw; a.xdig = w.xdig; a.xscale = w.xscale;
     a.act = w.act; a.adig = w.adig; a.ascale = w.ascale; a.y = w.y; a.out = out; a.resid = io.resid;
-    a.dense_min = jm::mfma_shape_ok(d, s->m) ? s->dense_min : 0x7FFFFFFF;
+    a.dense_min = s->mfma_ok ? s->dense_min : 0x7FFFFFFF;
     r.dense_min = a.dense_min;
     a.tiles = w.tiles; a.n_tiles = w.n_tiles;
-    r.xsh = dec ? nullptr : w.xsh; r.xsl = dec ? nullptr : w.xsl; r.xexp = w.xexp;
-    a.xsh = w.xsh; a.xsl = w.xsl; a.xexp = w.xexp;
-    a.act_h = w.act_h; a.act_l = w.act_l; a.aexp = w.aexp;
+    const bool mfma = !dec && a.dense_min <= nslot;
+    r.xqh = mfma ? w.xqh : nullptr; r.xql = w.xql; r.xqs = w.xqs;
+    a.xqh = w.xqh; a.xql = w.xql; a.xqs = w.xqs;
+    a.aqh = w.aqh; a.aql = w.aql; a.aqs = w.aqs;
     a.logits = w.logits; a.renorm = s->renorm; a.top_w = w.top; a.tw_w = w.tw;
     const int max_tiles = nslot / JM_DENSE_TILE + E;
 #define JM_MARK(i) if (s->prof && stage_marks) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
@@ -285,6 +286,7 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
     if (!aligned(blob, 16)) return fail(JM_ERR_ARG, "store blob must be 16-byte aligned");
     // every record must lie inside the blob, with packed rows 16-byte aligned
     const uint64_t sg = (uint64_t)m * d / group * 2, pg = (uint64_t)m * d / 2;
+    bool sc16 = true;                           // the MFMA branch reads scales in 8- and 16-byte pieces
     for (int p = 0; p < 3; p++)
         for (int i = 0; i < L * E; i++) {
             const uint64_t so = offsets[((size_t)p * L * E + i) * 2 + 0];
@@ -295,6 +297,7 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
             if (so + sg > blob_bytes || po + pg > blob_bytes || so + sg < so || po + pg < po)
                 return fail(JM_ERR_ARG, "record %d of part %d lies outside the %llu-byte blob", i, p,
                             (unsigned long long)blob_bytes);
+            sc16 = sc16 && so % 16 == 0;
         }
     hipPointerAttribute_t attr;
     hipError_t pe = hipPointerGetAttributes(&attr, blob);
@@ -308,6 +311,7 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
     s->renorm = cfg->norm_topk_prob ? 1 : 0;
     s->group = group;
     s->dense_min = JM_DENSE_MIN_DEFAULT;
+    s->mfma_ok = jm::mfma_shape_ok(d, m) && sc16;
     s->max_layers = -1;
     s->blob = (const uint8_t*)blob;
     s->blob_bytes = blob_bytes;

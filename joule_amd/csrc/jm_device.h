@@ -134,15 +134,6 @@ __device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t& hi, uin
     lo = pack_bf16x2(__fsub_rn(a, __uint_as_float(hi << 16)), __fsub_rn(b, __uint_as_float(hi & 0xFFFF0000u)));
 }
 
-// Power-of-two prescale of a row before its fp16 hi + lo split: the
-// exponent p >= 0 with mx * 2^-p < 2^15 for the row's largest magnitude mx,
-// 0 when the row already fits (or mx is not finite, so that Inf and NaN
-// propagate as they would unscaled).  Scaling by 2^-p and back by 2^p is
-// exact, so the products keep their bits wherever the fp16 range sufficed.
-__device__ __forceinline__ int split_exp(float mx) {
-    if (!(mx >= 32768.0f) || !(mx <= 3.4028235e38f)) return 0;
-    return (int)((__float_as_uint(mx) >> 23) & 0xFFu) - 127 - 14;
-}
 // 2^p as a float, -126 <= p <= 127
 __device__ __forceinline__ float exp2i(int p) { return __uint_as_float((uint32_t)(127 + p) << 23); }
 
@@ -341,6 +332,47 @@ __device__ __forceinline__ void encode_group_wave(float v, bool store, uint32_t*
         if (store && (i & 7) == 0) dig[k * (G / 8) + (i >> 3)] = (uint32_t)word;
     }
     if (store && i == 0) *scale = s;
+}
+
+// --------------------------------------- int8 digit pairs (MFMA branch)
+//
+// The MFMA branch multiplies signed int8 weights (q - 8) by activations
+// written as two int8 digits per value: over a G-value group (the columns
+// one weight-scale group covers), a_j = rint(x_j / s) with s = max|x| / 32639,
+// and a_j = 256 hi_j + lo_j with hi_j, lo_j in [-128, 127] (|a_j| <= 32639 =
+// 127 * 256 + 127 keeps hi in range).  A group's integer dot with the
+// weights is exact: |sum_j a_j (q_j - 8)| <= G * 32639 * 8 < 2^24, so its
+// conversion to float is exact as well.
+constexpr int I8_R = 32639;
+
+// Position of value u (0..7) within its aligned 8-value run in the int8
+// operand order: the even values, then the odd ones.  That is the byte
+// order in which one dword of packed nibbles (value i in bits 4i..4i+3)
+// unpacks: its low nibbles, then its high nibbles.
+__host__ __device__ constexpr int i8_pos(int u) { return (u & 1) ? 4 + (u >> 1) : (u >> 1); }
+
+// Encode one group of G floats, value i held by lane i of an aligned G-lane
+// segment (G = 32 or 64): lane i writes its two digits to hi[p] and lo[p],
+// p = its value's place in the int8 operand order; lane 0 writes the scale
+// (NaN when the group holds a non-finite value, so that it propagates).
+// Only when `store`; every lane of the segment must call this.
+template <int G>
+__device__ __forceinline__ void encode_i8_group_wave(float v, bool store, int8_t* __restrict__ hi,
+                                                     int8_t* __restrict__ lo, float* __restrict__ scale) {
+    const int i = threadIdx.x & (G - 1);
+    const float a = fabsf(v);
+    const int bad = seg_or<G>(!(a <= 3.4028235e38f) ? 1 : 0);
+    const float mx = seg_max<G>(a);
+    const float inv = (mx > 0.0f && !bad) ? __fdiv_rn((float)I8_R, mx) : 0.0f;
+    const int q = (int)rintf(__fmul_rn(v, inv));
+    const int l = ((q + 128) & 255) - 128;
+    const int h = (q - l) >> 8;
+    if (store) {
+        const int p = (i & ~7) + i8_pos(i & 7);
+        hi[p] = (int8_t)h;
+        lo[p] = (int8_t)l;
+        if (i == 0) *scale = bad ? __int_as_float(0x7FC00000) : __fdiv_rn(mx, (float)I8_R);
+    }
 }
 
 // Digits of the 8 values in lanes 0..7 of the wave with the digit scale of

@@ -21,15 +21,13 @@
 // combine done in the down kernel.  Larger calls take the dispatch path.
 #define JM_DEC_SLOTS 256
 // Dispatch path: experts with at least dense_min slots take the MFMA branch,
-// in tiles of this many tokens.  Its fp16 operands store each group of 8
-// columns in the order 0 4 1 5 2 6 3 7 (the order the nibble dequantisation
-// produces): column c sits at 8 (c / 8) + mfma_slot(c % 8).
-#define JM_DENSE_TILE 64
+// in tiles of this many tokens.  Its int8 operands (weights q - 8, and the
+// activations' two digits) store each run of 8 columns in the order
+// i8_pos gives (jm_device.h): the even columns, then the odd ones.
+#define JM_DENSE_TILE 32
 #define JM_DENSE_MIN_DEFAULT 8
 
 namespace jm {
-
-__host__ __device__ constexpr int mfma_slot(int i) { return (i & 3) * 2 + (i >> 2); }
 
 struct ExpertArgs {
     const uint8_t* blob;      // HBM copy of experts_q4.bin
@@ -46,9 +44,9 @@ struct ExpertArgs {
     int B;
     int d, m, topk;
     const float* tw;          // [B*k] routing weight of each slot
-    const _Float16* xsh;      // [B][d] tokens split hi/lo in MFMA column order (MFMA branch)
-    const _Float16* xsl;
-    const float* xexp;        // [B] 2^p: each token was split as x * 2^-p (p > 0 only past the fp16 range)
+    const int8_t* xqh;        // [B][d] tokens as int8 digit pairs (hi, lo) in int8 operand order (MFMA branch)
+    const int8_t* xql;
+    const float* xqs;         // [B][d/G] their scales
     const uint32_t* xdig;     // [B][d/G][NDIG][G/8] token digits
     const float* xscale;      // [B][d/G]
     float* act;               // [B*k][m]   SiLU(gate)*up per slot
@@ -60,11 +58,11 @@ struct ExpertArgs {
     int group;
     // dispatch path, dense branch
     int dense_min;            // experts with at least this many slots take the MFMA kernels
-    const int2* tiles;        // [max tiles] (work entry, 64-token tile) of the dense experts
+    const int2* tiles;        // [max tiles] (work entry, token tile) of the dense experts
     const int* n_tiles;       // [1] how many
-    _Float16* act_h;          // [B*k][m] act split into fp16 hi + lo for the MFMA down
-    _Float16* act_l;
-    float* aexp;              // [B*k][m/128] 2^p of each 128-row block of act_h/act_l (split as act * 2^-p)
+    int8_t* aqh;              // [B*k][m] act as int8 digit pairs for the MFMA down
+    int8_t* aql;
+    float* aqs;               // [B*k][m/G] their scales
     // decode path with the top-k in the gate/up kernel (gateup_topk): the
     // router scores, and where the table is written
     const float* logits;      // [B][E]
@@ -88,9 +86,9 @@ struct RouteArgs {
     float* logits;            // [B][E]
     uint32_t* xdig;           // [B][d/G][NDIG][G/8]
     float* xscale;            // [B][d/G]
-    _Float16* xsh;            // [B][d] token split hi/lo in MFMA column order (NULL: not needed)
-    _Float16* xsl;
-    float* xexp;              // [B] 2^p of each token's split (x * 2^-p; p > 0 only past the fp16 range)
+    int8_t* xqh;              // [B][d] tokens as int8 digit pairs for the MFMA branch (NULL: not needed)
+    int8_t* xql;
+    float* xqs;               // [B][d/G] their scales
     int* top;                 // [B*k]
     float* tw;                // [B*k]
     int* seg_off;             // [E+1]
@@ -143,9 +141,10 @@ hipError_t launch_down_comb(const ExpertArgs& a, hipStream_t st);
 // dispatch path: gate/up and down over the work table, then the combine
 hipError_t launch_gateup(const ExpertArgs& a, int umax, hipStream_t st);
 hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st);
-// dense branch: grids of max_tiles x (row tiles); blocks past *n_tiles exit.
-// mfma_shape_ok: d and intermediate are multiples of 128 (else the GEMV
-// kernels take every expert)
+// dense branch: grids of max_tiles x (row blocks); blocks past *n_tiles exit.
+// mfma_shape_ok: d and the intermediate multiples of 256, up to 2048, and at
+// most 1024 or a multiple of 1024 (the tile's token digits stay in LDS one
+// 1024-column phase at a time); otherwise the GEMV kernels take every expert
 bool mfma_shape_ok(int d, int m);
 hipError_t launch_gateup_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st);
 hipError_t launch_down_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st);

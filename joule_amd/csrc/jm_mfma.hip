@@ -1,76 +1,76 @@
-// Dense branch of the grouped Q4 expert product (gfx950 MFMA), taken by the
-// experts whose segment holds at least `dense_min` tokens (prefill-sized
+// Dense branch of the grouped Q4 expert product (gfx950 int8 MFMA), taken by
+// the experts whose segment holds at least `dense_min` tokens (prefill-sized
 // batches, skewed routing).  The same contraction as the wave-item kernels
 // in jm_experts.hip (decode_kernel.c:1365-1383), as tiled products:
 //
-//   k_gateup_mfma  per (expert, 64-token tile, 128 intermediate rows):
+//   k_gateup_mfma  per (expert, 32-token tile, 128 intermediate rows):
 //                  G = X . Wg^T and U = X . Wu^T over d, then
-//                  act = (G / (1 + expf_fast(-G))) * U
-//   k_down_mfma    per (expert, 64-token tile, 128 hidden rows; 256 for a
-//                  tile of up to 32 tokens):
+//                  act = (G / (1 + expf_fast(-G))) * U, written as int8
+//                  digit pairs for the down product (and as float)
+//   k_down_mfma    per (expert, 32-token tile, 512 hidden rows in two passes):
 //                  y[slot] = w_slot * (act . Wd^T) over the intermediate
 //
-// Operands, per 64-column (narrow down tiles: 32-column) stage of the
-// contraction, staged in LDS:
-//   weights  the signed nibbles q - 8 as fp16 (exact), one fp32 scale per
-//            row and Q4 group applied to the fp32 accumulator of that group;
-//   tokens   each fp32 value split into hi = fp16(v) and lo = fp16(v - hi)
-//            (by the router kernel for x, by the gate/up epilogue for act),
-//            two products per tile, so the activations keep 22 significant
-//            bits.  A row whose largest magnitude reaches 2^15 (x: a token;
-//            act: a slot's 128-row block) is split as v * 2^-p instead, and
-//            its products are scaled back by 2^p (exact): the gate/up
-//            epilogue for x, the down kernel's group scales for act, so the
-//            fp16 range never clips an activation.
-// Both operands keep each 8-column group in the order 0 4 1 5 2 6 3 7 that
-// the nibble dequantisation produces; the contraction does not care.
-// v_mfma_f32_32x32x16_f16 tiles with the tokens on the A side: lane l holds
-// one weight row (n = l % 32) and 16 tokens, so a group's scale is one value
-// per lane.  Lane layout (checked on the device): A[i][k] at lane i % 32,
-// k = 8 * (l / 32) + j; B[k][n] at lane n % 32, k = 8 * (l / 32) + j;
-// D register v of lane l = (i = 8 (v / 4) + 4 (l / 32) + v % 4, n = l % 32).
+// Operands:
+//   weights  the signed nibbles q - 8 as int8, unpacked in registers from
+//            the packed record (each wave streams its own rows);
+//   tokens   two int8 digits per value with one float scale per token and
+//            Q4 group (jm_device.h: encode_i8_group_wave): the router kernel
+//            writes them for x, the gate/up epilogue for act.
+// v_mfma_i32_32x32x32_i8 tiles, tokens on the A side (i), weight rows on the
+// B side (n).  Lane layout (checked on the device): A[i][k] at lane i % 32,
+// k = 16 (l / 32) + j; B[k][n] at lane n % 32, k = 16 (l / 32) + j; D
+// register v of lane l = (i = 8 (v / 4) + 4 (l / 32) + v % 4, n = l % 32).
+// So a lane holds one weight row and 16 tokens: the row's group scale is one
+// value per lane, the tokens' scales 16.
 //
-// Two stages stream into registers while the stage in LDS is multiplied;
-// the next stage goes to the other LDS buffer after the MFMAs (double
-// buffering).
+// Per Q4 group of a lane's row and its 16 tokens the two digit products are
+// exact int32 sums (hi and lo), combined as 256 hi + lo (exact, below 2^24 in
+// magnitude), converted to float and accumulated as
+//   acc += (float(256 hi + lo) * s_token) * s_row.
+//
+// The whole contraction of a tile's 32 tokens (both digit planes) stays in
+// LDS for the block's lifetime, so the main loop has no barriers: each wave
+// streams its weight rows through a ring of register stages and reads its
+// token operands from LDS.
+#include <atomic>
+#include <type_traits>
+
 #include "jm_device.h"
 #include "jm_kernels.h"
 
 namespace jm {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef int int16v __attribute__((ext_vector_type(16)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int MT = JM_DENSE_TILE;   // tokens per tile of the tile list
+constexpr int MT = JM_DENSE_TILE;   // tokens per tile (32)
+static_assert(MT == 32, "the tile's tokens are the 32 A rows of one MFMA");
+constexpr int MTHREADS = 512;       // 8 waves per block
+constexpr int NWAVE = MTHREADS / 64;
+constexpr int GU_ROWS = 128;        // intermediate rows of a gate/up block (both matrices)
+constexpr int DN_ROWS = 256;        // hidden rows of one pass of a down block (8 waves x 32)
+constexpr int DN_BLOCK_ROWS = 512;  // hidden rows of a down block: two passes over its staged act digits
+constexpr int KMAX = 2048;          // longest contraction the kernels take
+constexpr int KPAD = 16;            // bytes of padding per LDS token row (bank spread)
+constexpr int KPH_MAX = 1024;       // columns of a token phase (the tokens' LDS holds one phase)
+constexpr int SSC = 256;            // columns of a weight super-stage: 128 bytes (one cache line) per row
+constexpr int WRS = 144;            // LDS bytes per row of a wave's weight buffer (128 + bank spread)
+constexpr int WBUF = 32 * WRS;      // one super-stage of a wave's 32 rows
 
-__device__ __forceinline__ void split_hi_lo(float v, _Float16& h, _Float16& l) {
-    h = (_Float16)v;
-    l = (_Float16)(v - (float)h);
+// One dword of 8 packed nibbles (value i in bits 4i..4i+3) as two dwords of
+// int8 q - 8 in i8_pos order: values 0 2 4 6, then 1 3 5 7.  For a byte b in
+// 0..15, (b + 0x78) ^ 0x80 is b - 8 as a signed byte; no carry leaves a byte.
+__device__ __forceinline__ void nib_to_i8(uint32_t w, int& lo, int& hi) {
+    lo = (int)(((w & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
+    hi = (int)((((w >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
 }
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-// 32 nibbles (one 16-byte piece; word c holds values 8c..8c+7, value i in
-// bits 4i..4i+3) as q - 8 in fp16, to 4 x 16 bytes of LDS in the MFMA
-// column order (0 4 1 5 2 6 3 7 per 8 values): the fp16 bits 0x6400 | q
-// are 1024 + q exactly, and one packed subtraction of 1032 leaves q - 8.
-__device__ __forceinline__ void nibbles_to_lds(uint4 p, _Float16* dst) {
-    const uint32_t w[4] = {p.x, p.y, p.z, p.w};
-    const half2_t bias = {(_Float16)1032.0f, (_Float16)1032.0f};
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        uint32_t t[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) t[i] = ((w[c] >> (4 * i)) & 0x000F000Fu) | 0x64006400u;   // values (i, i + 4)
-        half8 h;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const half2_t v = __builtin_bit_cast(half2_t, t[i]) - bias;
-            h[2 * i] = v[0];
-            h[2 * i + 1] = v[1];
-        }
-        *(half8*)(dst + 8 * c) = h;
-    }
+__device__ __forceinline__ int4v wdigits(uint32_t w0, uint32_t w1) {
+    int a0, a1, a2, a3;
+    nib_to_i8(w0, a0, a1);
+    nib_to_i8(w1, a2, a3);
+    return int4v{a0, a1, a2, a3};
 }
 
 struct TileInfo {
@@ -89,392 +89,469 @@ __device__ __forceinline__ bool tile_info(const ExpertArgs& a, int t, TileInfo* 
     return true;
 }
 
-constexpr int MTHREADS = 512;       // 8 waves per block
-constexpr int MROWS = 128;          // weight rows of one block column (blockIdx.y)
-
-// Tile shapes.  A wide tile (33..64 tokens, and every gate/up tile) is
-// multiplied by one block per 128 weight rows: 8 waves of 32 tokens x 32
-// rows (2 token halves x 4 row quarters), 64-column stages.  A narrow down
-// tile (up to 32 tokens: most experts of a skewed prefill batch) is
-// multiplied by one block per 256 rows, the even block of each pair of
-// block columns (the odd one exits): 8 waves of the same 32 tokens x 32
-// rows each, 32-column stages.  Both shapes issue the same MFMAs per wave
-// and stream the same bytes per block; the narrow one halves the blocks of
-// a narrow tile and multiplies no padding half.
-template <bool NARROW>
-struct Shape {
-    static constexpr int TOK = NARROW ? 32 : 64;      // tokens per tile
-    static constexpr int ROWS = NARROW ? 256 : 128;   // weight rows per block
-    static constexpr int KS = NARROW ? 32 : 64;       // contraction columns per stage
-    static constexpr int KP = KS + 8;                 // padded LDS row in halves (80 / 144 bytes: 16-byte aligned, bank-spread)
-    static constexpr int XPC = KS / 8;                // 8-value token pieces per token and stage
-    static constexpr int XTHR = TOK * XPC;            // threads staging tokens (128 / 512)
-    static constexpr int WPR = KS / 32;               // 16-byte weight pieces per row and stage
+// LDS layout of a block with contraction length K:
+//   q    the tile's token digits of one phase (kph columns): token i's plane
+//        p (0 hi, 1 lo) at q + (p * MT + i) * (kph + KPAD), in int8 operand
+//        order; kph + KPAD = 16 mod 256 bytes puts the 16 token rows of a
+//        ds_read_b128 half-wave in distinct banks
+//   s    the tokens' scales over all of K: group g, token i at s[g * MT + i]
+//   tok  the tile's token (gate/up) or slot (down) rows, then its slot ids
+//        (gate/up) or routing weights (down)
+//   w    per wave, two super-stage buffers of its 32 weight rows (WRS bytes
+//        per row)
+struct Lay {
+    int kph;
+    size_t s, tok, w, total;
+    __host__ __device__ constexpr Lay(int K, int G)
+        : kph(K < KPH_MAX ? K : KPH_MAX),
+          s((size_t)2 * MT * ((K < KPH_MAX ? K : KPH_MAX) + KPAD)),
+          tok(s + (size_t)(K / G) * MT * 4),
+          w(tok + 2 * MT * 4),
+          total(tok + 2 * MT * 4 + (size_t)NWAVE * 2 * WBUF) {}
 };
 
-// Scale groups of a stage: NGS scale values per row, each over KSG MFMA
-// k-steps; a 64-value group spans SPG = 2 narrow stages, and its two halves'
-// partial sums are summed before the scale is applied.
-template <int G, int KS_>
-struct Groups {
-    static constexpr int NGS = KS_ >= G ? KS_ / G : 1;
-    static constexpr int KSG = (KS_ >= G ? G : KS_) / 16;
-    static constexpr int SPG = KS_ >= G ? 1 : G / KS_;
-    static_assert(SPG == 1 || SPG == 2, "a scale group spans one or two stages");
-};
-
-// narrow tiles need whole 256-row blocks
-__device__ __forceinline__ bool narrow_rows_ok(int rows) { return rows % (2 * MROWS) == 0; }
-
-// ------------------------------------------------------------------ gate/up
-
-template <int G, bool NARROW>
-struct GuLds {
-    using S = Shape<NARROW>;
-    _Float16 xh[2][S::TOK * S::KP], xl[2][S::TOK * S::KP];
-    _Float16 wl[2][2][S::ROWS * S::KP];
-    float scl[2][2][S::ROWS][Groups<G, S::KS>::NGS];
-    int tok[S::TOK];
-    float xf[S::TOK];              // 2^p of each token's split
-    float amx[4][S::TOK];          // max |act| of each token over each row quarter's 32 rows
-};
-
-// Stage registers of one thread: 8 token values (hi and lo), one 16-byte
-// piece of one row of one matrix, that row's scales for the stage.
-template <int NGS>
-struct StageRegs {
-    uint4 h, l;
-    uint4 w;
-    uint16_t sc[NGS];
-};
-
-template <int G, bool NARROW>
-__device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo& ti, unsigned char* sm) {
-    using S = Shape<NARROW>;
-    using Q = Groups<G, S::KS>;
-    GuLds<G, NARROW>& L = *reinterpret_cast<GuLds<G, NARROW>*>(sm);
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = tid >> 6;
-    const int row0 = blockIdx.y * MROWS;          // first intermediate row of the block
-    const int d = a.d, ng = d / G, nstage = d / S::KS;
-    if (tid < S::TOK) {
-        const int b = tid < ti.nt ? a.seg_slot[ti.slot0 + tid] / a.topk : -1;
-        L.tok[tid] = b;
-        L.xf[tid] = b >= 0 ? a.xexp[b] : 1.0f;
+// Stage the tile's digit planes, columns [c0, c0 + kph), into q: token i's
+// rows are row src[i] of hi/lo [.][K].  All threads; no branches, so each
+// thread's loads of a batch are all in flight together (indices past the
+// end repeat the last piece, stored again to the same place).
+__device__ __forceinline__ void stage_phase(const int8_t* __restrict__ hi, const int8_t* __restrict__ lo,
+                                            const int* src, int K, int c0, int kph, int8_t* q) {
+    constexpr int BATCH = 8;
+    // an opaque thread index: the addresses below are recomputed at each
+    // staging instead of being kept live across the caller's main loop
+    int tid = threadIdx.x;
+    __asm__ volatile("" : "+v"(tid));
+    const int KP = kph + KPAD;
+    const int pieces = kph / 16;                  // 16-byte pieces per token row
+    const int total = 2 * MT * pieces;
+    // u / pieces as a multiply-high: exact for u * pieces < 2^32
+    const unsigned magic = 0xFFFFFFFFu / (unsigned)pieces + 1u;
+    for (int base = 0; base < total; base += MTHREADS * BATCH) {
+        uint4 v[BATCH];
+        int dst[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; j++) {
+            const unsigned u = (unsigned)min(base + j * MTHREADS + tid, total - 1);
+            const int r = (int)__umulhi(u, magic);                // plane * MT + token
+            const int pc = (int)u - r * pieces;
+            v[j] = *(const uint4*)((r >= MT ? lo : hi) + (size_t)src[r & (MT - 1)] * K + c0 + pc * 16);
+            dst[j] = r * KP + pc * 16;
+        }
+#pragma unroll
+        for (int j = 0; j < BATCH; j++) *(uint4*)(q + dst[j]) = v[j];
     }
-    unsigned long long so[2], po[2];
-    a.rec.get(0, a.key0 + ti.e, so[0], po[0]);
-    a.rec.get(1, a.key0 + ti.e, so[1], po[1]);
-    __syncthreads();
+}
 
-    // staging assignment: tokens (threads < XTHR, 8 values each of one
-    // token), weights (every thread one 16-byte piece of one row of one
-    // matrix)
-    const bool xthr = S::XTHR == MTHREADS || tid < S::XTHR;   // wave-uniform
-    const int xt = (tid / S::XPC) % S::TOK, xpart = tid % S::XPC;
-    const int wm = tid >> 8, widx = tid & 255;
-    const int wrow = widx / S::WPR, wpiece = widx % S::WPR;
-    const int xb = L.tok[xt];
-    const size_t xo = (size_t)(xb >= 0 ? xb : 0) * d + xpart * 8;
-    const uint8_t* wpk = a.blob + po[wm] + (size_t)(row0 + wrow) * (d / 2) + wpiece * 16;
-    const uint16_t* wsc = (const uint16_t*)(a.blob + so[wm]) + (size_t)(row0 + wrow) * ng;
-
-    // every load is unconditional (past the last stage: the last stage again)
-    auto load_stage = [&](StageRegs<Q::NGS>& r, int s) __attribute__((always_inline)) {
-        s = s < nstage ? s : nstage - 1;
-        if (xthr) {
-            r.h = *(const uint4*)(a.xsh + xo + s * S::KS);
-            r.l = *(const uint4*)(a.xsl + xo + s * S::KS);
-        }
-        r.w = *(const uint4*)(wpk + s * (S::KS / 2));
-#pragma unroll
-        for (int j = 0; j < Q::NGS; j++) r.sc[j] = wsc[(s * S::KS) / G + j];
-    };
-    auto store_stage = [&](const StageRegs<Q::NGS>& r, int buf) __attribute__((always_inline)) {
-        if (xthr) {
-            const unsigned keep = xb >= 0 ? 0xFFFFFFFFu : 0u;     // padding tokens stage zeros
-            *(uint4*)&L.xh[buf][xt * S::KP + xpart * 8] = make_uint4(r.h.x & keep, r.h.y & keep, r.h.z & keep, r.h.w & keep);
-            *(uint4*)&L.xl[buf][xt * S::KP + xpart * 8] = make_uint4(r.l.x & keep, r.l.y & keep, r.l.z & keep, r.l.w & keep);
-        }
-        nibbles_to_lds(r.w, &L.wl[buf][wm][wrow * S::KP + wpiece * 32]);
-        if (wpiece == 0) {
-#pragma unroll
-            for (int j = 0; j < Q::NGS; j++) L.scl[buf][wm][wrow][j] = fp16_hw(r.sc[j]);
-        }
-    };
-
-    // this wave's token half and 32-row slice
-    const int th = NARROW ? 0 : (w & 1), rq = NARROW ? w : (w >> 1);
-    const int ai = th * 32 + (lane & 31), bn = rq * 32 + (lane & 31), kq = 8 * (lane >> 5);
-    floatx16 tg = {}, tu = {};
-    floatx16 cg = {}, cu = {};                    // partial sums carried into a group's second stage
-    // fresh: the stage starts a scale group; apply: it ends one
-    auto mfma_stage = [&](int buf, bool fresh, bool apply) __attribute__((always_inline)) {
-#pragma unroll
-        for (int gs = 0; gs < Q::NGS; gs++) {
-            floatx16 ag = fresh ? floatx16{} : cg, au = fresh ? floatx16{} : cu;
-#pragma unroll
-            for (int k2 = 0; k2 < Q::KSG; k2++) {
-                const int k0 = (gs * Q::KSG + k2) * 16 + kq;
-                const half8 a_h = *(const half8*)&L.xh[buf][ai * S::KP + k0];
-                const half8 a_l = *(const half8*)&L.xl[buf][ai * S::KP + k0];
-                const half8 b_g = *(const half8*)&L.wl[buf][0][bn * S::KP + k0];
-                const half8 b_u = *(const half8*)&L.wl[buf][1][bn * S::KP + k0];
-                ag = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, b_g, ag, 0, 0, 0);
-                ag = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, b_g, ag, 0, 0, 0);
-                au = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, b_u, au, 0, 0, 0);
-                au = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, b_u, au, 0, 0, 0);
-            }
-            if (apply) {
-                const float sg = L.scl[buf][0][bn][gs], su = L.scl[buf][1][bn][gs];
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    tg[v] = __builtin_fmaf(sg, ag[v], tg[v]);
-                    tu[v] = __builtin_fmaf(su, au[v], tu[v]);
-                }
-            } else {
-                cg = ag;
-                cu = au;
-            }
-        }
-    };
-    // stages s + 1 and s + 2 stream into registers while stage s (in LDS) is
-    // multiplied; nstage is even, so buffer 0 always holds an even stage
-    StageRegs<Q::NGS> r0, r1;
-    load_stage(r0, 0);
-    load_stage(r1, 1);
-    store_stage(r0, 0);
-    load_stage(r0, 2);
-    __syncthreads();
-    for (int s = 0; s < nstage; s += 2) {
-        mfma_stage(0, true, Q::SPG == 1);         // stage s; r1 = s + 1, r0 = s + 2 in flight
-        store_stage(r1, 1);
-        load_stage(r1, s + 3);
-        __syncthreads();
-        mfma_stage(1, Q::SPG == 1, true);         // stage s + 1; r0 = s + 2, r1 = s + 3
-        store_stage(r0, 0);
-        load_stage(r0, s + 4);
-        __syncthreads();
+// The tile's token scales over all of K (padding tokens, i >= nt: 0).
+__device__ __forceinline__ void stage_scales(const float* __restrict__ sc, const int* src, int nt, int ng, float* s) {
+    for (int u = threadIdx.x; u < ng * MT; u += MTHREADS) {
+        const int g = u / MT, i = u % MT;
+        s[u] = i < nt ? sc[(size_t)src[i] * ng + g] : 0.0f;
     }
-    // act = SiLU(g) * u for this lane's row and 16 tokens (the token's
-    // split prescale undone first)
-    const int r = row0 + bn;
-    float av[16];
+}
+
+// A wave's weight stream.  A super-stage is SSC columns of the wave's 32
+// rows: one 128-byte line per row, read as 4 coalesced loads per lane (load
+// k: lane L takes row 8 k + L / 8, bytes 16 (L % 8) of the line), then
+// written to the wave's own LDS buffer and read back per stage in the MFMA
+// layout (lane n % 32 its row).  Two super-stages are in flight.  With the
+// lines come this lane's row's scales of the super-stage's groups (4 stages
+// x 64 / G groups).
+template <int G>
+struct WStream {
+    static constexpr int NSC = 4 * 64 / G;        // scales per super-stage
+    typedef typename std::conditional<NSC == 4, uint2, uint4>::type ScT;
+    uint4 wb[2][4];                               // [0]: the next super-stage, [1]: the one after
+    ScT sc[2];
+    const uint8_t* wbase;                         // the wave's first row
+    const uint8_t* srow;                          // this lane's row's scales
+    size_t rowb;                                  // bytes per row
+    int nss;                                      // super-stages over K
+    __device__ __forceinline__ void load(int slot, int S) {
+        S = S < nss ? S : nss - 1;
+        const int L = threadIdx.x & 63;
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int i = th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-        const float f = L.xf[i];
-        av[v] = swiglu(__fmul_rn(tg[v], f), __fmul_rn(tu[v], f));
-        // the token's max |act| over this half-wave's 32 rows
-        const float mx = seg_max<32>(i < ti.nt ? fabsf(av[v]) : 0.0f);
-        if ((lane & 31) == 0) L.amx[rq][i] = mx;
+        for (int k = 0; k < 4; k++)
+            wb[slot][k] = *(const uint4*)(wbase + (size_t)(8 * k + L / 8) * rowb + (size_t)S * (SSC / 2) + 16 * (L % 8));
+        sc[slot] = *(const ScT*)(srow + (size_t)S * NSC * 2);
     }
-    __syncthreads();
-    const int nb = a.m / MROWS;
+    // write the next super-stage's lines to LDS buffer wl and return its
+    // scales; the one after moves up and super-stage S is requested behind it
+    __device__ __forceinline__ ScT advance(uint8_t* wl, int S) {
+        const int L = threadIdx.x & 63;
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int i = th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-        if (i < ti.nt) {
-            const int slot = a.seg_slot[ti.slot0 + i];
-            // one prescale per (slot, this block's 128 rows)
-            const int pe = split_exp(fmaxf(fmaxf(L.amx[0][i], L.amx[1][i]), fmaxf(L.amx[2][i], L.amx[3][i])));
-            if (rq == 0 && (lane & 31) == 0) a.aexp[(size_t)slot * nb + blockIdx.y] = exp2i(pe);
-            _Float16 hh, ll;
-            split_hi_lo(__fmul_rn(av[v], exp2i(-pe)), hh, ll);
-            a.act[(size_t)slot * a.m + r] = av[v];
-            const size_t o = (size_t)slot * a.m + (r & ~7) + mfma_slot(r & 7);
-            a.act_h[o] = hh;
-            a.act_l[o] = ll;
+        for (int k = 0; k < 4; k++) *(uint4*)(wl + (8 * k + L / 8) * WRS + 16 * (L % 8)) = wb[0][k];
+        const ScT r = sc[0];
+#pragma unroll
+        for (int k = 0; k < 4; k++) wb[0][k] = wb[1][k];
+        sc[0] = sc[1];
+        load(1, S);
+        return r;
+    }
+};
+
+// scale u (0..NSC-1) of a super-stage's packed fp16 scales, as float
+template <int G>
+__device__ __forceinline__ float sc_at(const typename WStream<G>::ScT& v, int u) {
+    uint32_t w;
+    if (G == 64) w = u < 2 ? ((const uint2&)v).x : ((const uint2&)v).y;
+    else w = u < 2 ? ((const uint4&)v).x : u < 4 ? ((const uint4&)v).y : u < 6 ? ((const uint4&)v).z : ((const uint4&)v).w;
+    return fp16_hw((uint16_t)(w >> (16 * (u & 1))));
+}
+
+// A wave's token operands of one stage: both sub-steps, both digit planes.
+// Stage columns (relative to the token phase) start at c; lane half h.
+//   G = 64: one group; sub-step u takes values 32 h + 16 u + 0..15.
+//   G = 32: two groups; sub-step u (= group u) takes values 32 u + 16 h + 0..15.
+struct AOps {
+    int4v ah0, ah1, al0, al1;
+};
+
+template <int G>
+__device__ __forceinline__ AOps load_aops(const int8_t* qh, const int8_t* ql, int c, int h) {
+    const int o0 = G == 64 ? c + 32 * h : c + 16 * h;
+    const int o1 = G == 64 ? o0 + 16 : o0 + 32;
+    return AOps{*(const int4v*)(qh + o0), *(const int4v*)(qh + o1), *(const int4v*)(ql + o0),
+                *(const int4v*)(ql + o1)};
+}
+
+// The weight operands of one stage from the wave's LDS buffer (row n, lane
+// half h), as int8 (q - 8): sub-step 0 and 1 (see AOps).
+template <int G>
+__device__ __forceinline__ void load_bops(const uint8_t* wl, int n, int h, int cs, int4v& b0, int4v& b1) {
+    const uint8_t* r = wl + n * WRS + 32 * cs;
+    if (G == 64) {
+        const uint4 w = *(const uint4*)(r + 16 * h);
+        b0 = wdigits(w.x, w.y);
+        b1 = wdigits(w.z, w.w);
+    } else {
+        const uint2 w0 = *(const uint2*)(r + 8 * h), w1 = *(const uint2*)(r + 16 + 8 * h);
+        b0 = wdigits(w0.x, w0.y);
+        b1 = wdigits(w1.x, w1.y);
+    }
+}
+
+// The 16 tokens' scales of one group (this lane's half h)
+struct SxOps {
+    float4 s[4];
+};
+
+__device__ __forceinline__ SxOps load_sx(const float* s, int g, int h) {
+    const float* sg = s + (size_t)g * MT + 4 * h;
+    return SxOps{{*(const float4*)(sg), *(const float4*)(sg + 8), *(const float4*)(sg + 16),
+                  *(const float4*)(sg + 24)}};
+}
+
+// The integer products of one stage: per group of the stage, hi and lo
+// digit planes.
+template <int G>
+struct IOps {
+    int16v ih[64 / G], il[64 / G];
+};
+
+template <int G>
+__device__ __forceinline__ void stage_mfma(IOps<G>& o, const AOps& a, const int4v& b0, const int4v& b1) {
+    if (G == 64) {
+        o.ih[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.ah0, b0, int16v{}, 0, 0, 0);
+        o.il[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al0, b0, int16v{}, 0, 0, 0);
+        o.ih[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.ah1, b1, o.ih[0], 0, 0, 0);
+        o.il[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al1, b1, o.il[0], 0, 0, 0);
+    } else {
+        o.ih[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.ah0, b0, int16v{}, 0, 0, 0);
+        o.il[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al0, b0, int16v{}, 0, 0, 0);
+        o.ih[G == 64 ? 0 : 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.ah1, b1, int16v{}, 0, 0, 0);
+        o.il[G == 64 ? 0 : 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al1, b1, int16v{}, 0, 0, 0);
+    }
+}
+
+// acc += 256 * ih + il of one group, times each token's scale, times the
+// row's scale
+__device__ __forceinline__ void group_acc(floatx16& acc, const int16v& ih, const int16v& il, const SxOps& sx,
+                                          float ws) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float sv[4] = {sx.s[k].x, sx.s[k].y, sx.s[k].z, sx.s[k].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int v = 4 * k + j;
+            const int iv = ih[v] * 256 + il[v];
+            acc[v] = __builtin_fmaf(__fmul_rn((float)iv, sv[j]), ws, acc[v]);
         }
     }
 }
 
-// Gate/up takes every tile in the wide shape: with narrow tiles in 256-row
-// blocks the 512-token Zipf-routed block's gate/up took 167 us instead of
-// 160 (twice the stages of half the MFMA work each, and the per-stage
-// latency is what bounds it), while the down product, with a third of the
-// contraction, gains from the halved block count.
+// Where a block's token digits come from, for the phase restaging.
+struct TokSrc {
+    const int8_t* hi;
+    const int8_t* lo;
+    const int* rows;
+    int K;
+};
+
+// The contraction of one wave: its 32 weight rows (lane n = l % 32 holds
+// row n) against the tile's 32 tokens over K columns, into acc.  The token
+// digits of the first phase and all the scales are in LDS, and the weight
+// stream's first two super-stages are in flight.  Stage c's token operands
+// are read one stage ahead; for G = 64 stage c's MFMAs are issued before
+// stage c - 1's scale epilogue (products alternate by stage parity), so
+// each wave has independent MFMA and VALU work at every point.  At each
+// token phase boundary the block restages the tokens (two barriers).
+template <int G>
+__device__ __forceinline__ void wave_product(floatx16& acc, WStream<G>& ws, uint8_t* wl, int8_t* q,
+                                             const float* s, const TokSrc& ts, const Lay& ly) {
+    constexpr int NG = 64 / G;                    // groups per stage
+    constexpr bool PIPE = G == 64;
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 31, h = lane >> 5;
+    const int KP = ly.kph + KPAD;
+    const int8_t* qh = q + (size_t)n * KP;
+    const int8_t* ql = q + (size_t)(MT + n) * KP;
+    const int sspp = ly.kph / SSC;                // super-stages per token phase
+    const int nss = ws.nss;
+    AOps ab[2];
+    IOps<G> pr[PIPE ? 2 : 1];
+    float wsp[PIPE ? 2 : 1][NG];
+    const int nph = (nss + sspp - 1) / sspp;
+#pragma unroll 1
+    for (int ph = 0; ph < nph; ph++) {
+      if (ph > 0) {
+        __syncthreads();                          // every wave is done with the previous phase
+        stage_phase(ts.hi, ts.lo, ts.rows, ts.K, ph * ly.kph, ly.kph, q);
+        __syncthreads();
+      }
+      const int s_end = min(nss, (ph + 1) * sspp);
+#pragma unroll 1
+      for (int S = ph * sspp; S < s_end; S++) {
+        const bool pstart = S % sspp == 0, pend = S + 1 == s_end;
+        uint8_t* wbuf = wl + (S & 1) * WBUF;
+        const typename WStream<G>::ScT scs = ws.advance(wbuf, S + 2);
+        const int cp = (S % sspp) * SSC;          // the super-stage's first column within the phase
+        if (PIPE && pstart) ab[0] = load_aops<G>(qh, ql, cp, h);
+#pragma unroll
+        for (int cs = 0; cs < 4; cs++) {
+            // keep each stage's instructions within the stage: the operands
+            // of the next stage are already requested explicitly, and
+            // hoisting more would cost registers
+            __builtin_amdgcn_sched_barrier(0);
+            const int c = 4 * S + cs;             // stage index over K
+            const int cur = cs & 1, prv = cur ^ 1;
+            if (!PIPE) ab[cur] = load_aops<G>(qh, ql, cp + 64 * cs, h);
+            else if (!(cs == 3 && pend)) ab[prv] = load_aops<G>(qh, ql, cp + 64 * (cs + 1), h);
+            SxOps sxp;
+            if (PIPE && c > 0) sxp = load_sx(s, c - 1, h);
+            int4v b0, b1;
+            load_bops<G>(wbuf, n, h, cs, b0, b1);
+            const int pc = PIPE ? cur : 0, pp = PIPE ? prv : 0;
+            stage_mfma<G>(pr[pc], ab[cur], b0, b1);
+#pragma unroll
+            for (int u = 0; u < NG; u++) wsp[pc][u] = sc_at<G>(scs, NG * cs + u);
+            if (PIPE) {
+                if (c > 0) group_acc(acc, pr[pp].ih[0], pr[pp].il[0], sxp, wsp[pp][0]);
+            } else {
+#pragma unroll
+                for (int u = 0; u < NG; u++)
+                    group_acc(acc, pr[0].ih[u], pr[0].il[u], load_sx(s, NG * c + u, h), wsp[0][u]);
+            }
+        }
+      }
+    }
+    if (PIPE) {
+        // the last stage's epilogue (stage 4 nss - 1 is odd: its products sit in buffer 1)
+        group_acc(acc, pr[PIPE ? 1 : 0].ih[0], pr[PIPE ? 1 : 0].il[0], load_sx(s, 4 * nss - 1, h),
+                  wsp[PIPE ? 1 : 0][0]);
+    }
+}
+
+// ------------------------------------------------------------------ gate/up
+
+template <int G>
+__device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo& ti, unsigned char* sm) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int d = a.d, m = a.m, ng = d / G;
+    const Lay ly(d, G);
+    const int mat = w & 1, rq = w >> 1;           // this wave: gate (0) or up (1), rows 32 rq .. 32 rq + 31
+    const int r0 = blockIdx.y * GU_ROWS;          // the block's first intermediate row
+    int8_t* q = (int8_t*)sm;
+    float* s = (float*)(sm + ly.s);
+    int* tok = (int*)(sm + ly.tok);
+    uint8_t* wl = sm + ly.w + (size_t)w * 2 * WBUF;
+    int* slots = tok + MT;
+    if (tid < MT) {
+        const int sl = a.seg_slot[ti.slot0 + (tid < ti.nt ? tid : 0)];   // padding: the first slot
+        slots[tid] = sl;
+        tok[tid] = sl / a.topk;
+    }
+    unsigned long long so, po;
+    a.rec.get(mat, a.key0 + ti.e, so, po);
+    const int n = lane & 31;
+    const int wrow0 = r0 + 32 * rq;               // the wave's first row
+    WStream<G> ws;
+    ws.wbase = a.blob + po + (size_t)wrow0 * (d / 2);
+    ws.srow = a.blob + so + (size_t)(wrow0 + n) * ng * 2;
+    ws.rowb = d / 2;
+    ws.nss = d / SSC;
+    ws.load(0, 0);
+    ws.load(1, 1);
+    __syncthreads();
+    stage_phase(a.xqh, a.xql, tok, d, 0, ly.kph, q);
+    stage_scales(a.xqs, tok, ti.nt, ng, s);
+    __syncthreads();
+    floatx16 acc = {};
+    wave_product<G>(acc, ws, wl, q, s, TokSrc{a.xqh, a.xql, tok, d}, ly);
+
+    // SwiGLU: both matrices' sums to LDS (over the token digits), then one
+    // wave per (token, 64-row piece) forms act, its digits and scale
+    __syncthreads();
+    const int h = lane >> 5;
+    constexpr int RP = GU_ROWS + 4;               // padded LDS row of one token's sums
+    float* gu = (float*)sm;                       // [2][MT][RP]
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int i = 8 * (v / 4) + 4 * h + (v % 4);
+        gu[((size_t)mat * MT + i) * RP + 32 * rq + n] = acc[v];
+    }
+    __syncthreads();
+    const int mg = m / G;
+    for (int it = w; it < MT * (GU_ROWS / 64); it += NWAVE) {
+        const int i = it / (GU_ROWS / 64), piece = it % (GU_ROWS / 64);
+        if (i >= ti.nt) continue;                 // wave-uniform
+        const int slot = slots[i];
+        const int rr = 64 * piece + lane;         // row within the block
+        // SiLU(g) * u with a hardware reciprocal: act is quantized to 15-bit
+        // digits next, far coarser than the reciprocal's rounding
+        const float g = gu[(size_t)i * RP + rr], u = gu[((size_t)MT + i) * RP + rr];
+        const float av = __fmul_rn(__fmul_rn(g, __builtin_amdgcn_rcpf(__fadd_rn(1.0f, expf_fast(-g)))), u);
+        const int row = r0 + rr;
+        a.act[(size_t)slot * m + row] = av;
+        const int g0 = row / G;                   // this lane's group (a G-lane segment)
+        encode_i8_group_wave<G>(av, true, a.aqh + (size_t)slot * m + (size_t)g0 * G,
+                                a.aql + (size_t)slot * m + (size_t)g0 * G, a.aqs + (size_t)slot * mg + g0);
+    }
+}
+
 template <int G>
 __global__ void __launch_bounds__(MTHREADS, 1)
 k_gateup_mfma(ExpertArgs a) {
     TileInfo ti;
     if (!tile_info(a, blockIdx.x, &ti)) return;
-    __shared__ __align__(16) unsigned char sm[sizeof(GuLds<G, false>)];
-    gateup_tile<G, false>(a, ti, sm);
+    extern __shared__ __align__(16) unsigned char sm[];
+    gateup_tile<G>(a, ti, sm);
 }
 
 // --------------------------------------------------------------------- down
-
-template <int G, bool NARROW>
-struct DnLds {
-    using S = Shape<NARROW>;
-    _Float16 xh[2][S::TOK * S::KP], xl[2][S::TOK * S::KP];
-    _Float16 wl[2][S::ROWS * S::KP];
-    float scl[2][S::ROWS][Groups<G, S::KS>::NGS];
-    int tok[S::TOK];
-};
-
-template <int G, bool NARROW>
-__device__ __forceinline__ void down_tile(const ExpertArgs& a, const TileInfo& ti, unsigned char* sm) {
-    using S = Shape<NARROW>;
-    using Q = Groups<G, S::KS>;
-    DnLds<G, NARROW>& L = *reinterpret_cast<DnLds<G, NARROW>*>(sm);
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = tid >> 6;
-    const int row0 = blockIdx.y * MROWS;          // first hidden row of the block
-    const int m = a.m, ng = m / G, nstage = m / S::KS;
-    if (tid < S::TOK) L.tok[tid] = tid < ti.nt ? a.seg_slot[ti.slot0 + tid] : -1;
-    unsigned long long so, po;
-    a.rec.get(2, a.key0 + ti.e, so, po);
-    __syncthreads();
-    // act blocks split with a prescale (a magnitude past 2^15): the tile then
-    // scales each token's group products back by 2^p of its 128-column block
-    const int nb = m / MROWS;
-    int any = 0;
-    for (int q = tid; q < S::TOK * nb; q += MTHREADS) {
-        const int sl = L.tok[q / nb];
-        if (sl >= 0 && a.aexp[(size_t)sl * nb + q % nb] != 1.0f) any = 1;
-    }
-    const bool scaled = __syncthreads_or(any) != 0;
-
-    // staging: act (threads < XTHR, 8 columns of one token each), weights
-    // (threads 0..255, one 16-byte piece of one row each)
-    const bool xthr = S::XTHR == MTHREADS || tid < S::XTHR;   // wave-uniform
-    const bool wthr = tid < 256;                               // wave-uniform
-    const int xt = (tid / S::XPC) % S::TOK, xpart = tid % S::XPC;
-    const int widx = tid & 255;
-    const int wrow = widx / S::WPR, wpiece = widx % S::WPR;
-    const int xs = L.tok[xt];
-    const size_t xo = (size_t)(xs >= 0 ? xs : 0) * m + xpart * 8;
-    const uint8_t* wpk = a.blob + po + (size_t)(row0 + wrow) * (m / 2) + wpiece * 16;
-    const uint16_t* wsc = (const uint16_t*)(a.blob + so) + (size_t)(row0 + wrow) * ng;
-
-    auto load_stage = [&](StageRegs<Q::NGS>& r, int s) __attribute__((always_inline)) {
-        s = s < nstage ? s : nstage - 1;
-        if (xthr) {
-            r.h = *(const uint4*)(a.act_h + xo + s * S::KS);
-            r.l = *(const uint4*)(a.act_l + xo + s * S::KS);
-        }
-        if (wthr) {
-            r.w = *(const uint4*)(wpk + s * (S::KS / 2));
-#pragma unroll
-            for (int j = 0; j < Q::NGS; j++) r.sc[j] = wsc[(s * S::KS) / G + j];
-        }
-    };
-    auto store_stage = [&](const StageRegs<Q::NGS>& r, int buf) __attribute__((always_inline)) {
-        if (xthr) {
-            const unsigned keep = xs >= 0 ? 0xFFFFFFFFu : 0u;     // padding tokens stage zeros
-            *(uint4*)&L.xh[buf][xt * S::KP + xpart * 8] = make_uint4(r.h.x & keep, r.h.y & keep, r.h.z & keep, r.h.w & keep);
-            *(uint4*)&L.xl[buf][xt * S::KP + xpart * 8] = make_uint4(r.l.x & keep, r.l.y & keep, r.l.z & keep, r.l.w & keep);
-        }
-        if (wthr) {
-            nibbles_to_lds(r.w, &L.wl[buf][wrow * S::KP + wpiece * 32]);
-            if (wpiece == 0) {
-#pragma unroll
-                for (int j = 0; j < Q::NGS; j++) L.scl[buf][wrow][j] = fp16_hw(r.sc[j]);
-            }
-        }
-    };
-
-    const int th = NARROW ? 0 : (w & 1), rq = NARROW ? w : (w >> 1);
-    const int ai = th * 32 + (lane & 31), bn = rq * 32 + (lane & 31), kq = 8 * (lane >> 5);
-    floatx16 tot = {};
-    floatx16 carry = {};                          // partial sum carried into a group's second stage
-    auto mfma_stage = [&](int buf, int st, bool fresh, bool apply) __attribute__((always_inline)) {
-#pragma unroll
-        for (int gs = 0; gs < Q::NGS; gs++) {
-            floatx16 acc = fresh ? floatx16{} : carry;
-#pragma unroll
-            for (int k2 = 0; k2 < Q::KSG; k2++) {
-                const int k0 = (gs * Q::KSG + k2) * 16 + kq;
-                const half8 a_h = *(const half8*)&L.xh[buf][ai * S::KP + k0];
-                const half8 a_l = *(const half8*)&L.xl[buf][ai * S::KP + k0];
-                const half8 b = *(const half8*)&L.wl[buf][bn * S::KP + k0];
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, b, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, b, acc, 0, 0, 0);
-            }
-            if (apply) {
-                const float sc = L.scl[buf][bn][gs];
-                if (scaled) {
-                    // stages never straddle a 128-column block
-                    const int g128 = st * S::KS / MROWS;
-#pragma unroll
-                    for (int v = 0; v < 16; v++) {
-                        const int sl = L.tok[th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4)];
-                        const float f = sl >= 0 ? a.aexp[(size_t)sl * nb + g128] : 1.0f;
-                        tot[v] = __builtin_fmaf(__fmul_rn(sc, f), acc[v], tot[v]);
-                    }
-                } else {
-#pragma unroll
-                    for (int v = 0; v < 16; v++) tot[v] = __builtin_fmaf(sc, acc[v], tot[v]);
-                }
-            } else {
-                carry = acc;
-            }
-        }
-    };
-    StageRegs<Q::NGS> r0, r1;
-    load_stage(r0, 0);
-    load_stage(r1, 1);
-    store_stage(r0, 0);
-    load_stage(r0, 2);
-    __syncthreads();
-    for (int s = 0; s < nstage; s += 2) {
-        mfma_stage(0, s, true, Q::SPG == 1);
-        store_stage(r1, 1);
-        load_stage(r1, s + 3);
-        __syncthreads();
-        mfma_stage(1, s + 1, Q::SPG == 1, true);
-        store_stage(r0, 0);
-        load_stage(r0, s + 4);
-        __syncthreads();
-    }
-    const int r = row0 + bn;
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int i = th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-        if (i < ti.nt) {
-            const int slot = L.tok[i];
-            a.y[(size_t)slot * a.d + r] = __fmul_rn(a.tw[slot], tot[v]);
-        }
-    }
-}
 
 template <int G>
 __global__ void __launch_bounds__(MTHREADS, 1)
 k_down_mfma(ExpertArgs a) {
     TileInfo ti;
     if (!tile_info(a, blockIdx.x, &ti)) return;
-    constexpr size_t W = sizeof(DnLds<G, false>), N = sizeof(DnLds<G, true>);
-    __shared__ __align__(16) unsigned char sm[W > N ? W : N];
-    if (ti.nt <= 32 && narrow_rows_ok(a.d)) {
-        if (blockIdx.y & 1) return;               // the even block of the pair takes all 256 rows
-        down_tile<G, true>(a, ti, sm);
-    } else {
-        down_tile<G, false>(a, ti, sm);
+    extern __shared__ __align__(16) unsigned char sm[];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int d = a.d, m = a.m, ng = m / G;
+    const Lay ly(m, G);
+    int8_t* q = (int8_t*)sm;
+    float* s = (float*)(sm + ly.s);
+    int* tok = (int*)(sm + ly.tok);
+    float* tws = (float*)(tok + MT);
+    uint8_t* wl = sm + ly.w + (size_t)w * 2 * WBUF;
+    if (tid < MT) {
+        const int sl = a.seg_slot[ti.slot0 + (tid < ti.nt ? tid : 0)];   // padding: the first slot
+        tok[tid] = sl;
+        tws[tid] = a.tw[sl];
+    }
+    unsigned long long so, po;
+    a.rec.get(2, a.key0 + ti.e, so, po);
+    const int n = lane & 31, h = lane >> 5;
+    WStream<G> ws;
+    ws.rowb = m / 2;
+    ws.nss = m / SSC;
+    auto start = [&](int pass) __attribute__((always_inline)) {
+        const int wrow0 = blockIdx.y * DN_BLOCK_ROWS + pass * DN_ROWS + 32 * w;
+        ws.wbase = a.blob + po + (size_t)wrow0 * (m / 2);
+        ws.srow = a.blob + so + (size_t)(wrow0 + n) * ng * 2;
+        ws.load(0, 0);
+        ws.load(1, 1);
+        return wrow0 + n;
+    };
+    int row = start(0);
+    __syncthreads();
+    stage_phase(a.aqh, a.aql, tok, m, 0, ly.kph, q);
+    stage_scales(a.aqs, tok, ti.nt, ng, s);
+    __syncthreads();
+    // the staged act digits serve DN_BLOCK_ROWS / DN_ROWS passes over the rows
+#pragma unroll 1
+    for (int pass = 0; pass < DN_BLOCK_ROWS / DN_ROWS; pass++) {
+        floatx16 acc = {};
+        wave_product<G>(acc, ws, wl, q, s, TokSrc{a.aqh, a.aql, tok, m}, ly);
+        const int r = row;
+        if (pass + 1 < DN_BLOCK_ROWS / DN_ROWS) row = start(pass + 1);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int i = 8 * (v / 4) + 4 * h + (v % 4);
+            if (i < ti.nt) a.y[(size_t)tok[i] * d + r] = __fmul_rn(tws[i], acc[v]);
+        }
     }
 }
 
-// the MFMA branch needs whole 128-row tiles and an even number of 64-column
-// stages on both products (narrow tiles also take 256-row blocks where the
-// rows allow)
-bool mfma_shape_ok(int d, int m) { return d % MROWS == 0 && m % MROWS == 0 && (d / 64) % 2 == 0 && (m / 64) % 2 == 0; }
+// Contractions the kernels take: multiples of the weight super-stage, and
+// one token phase or whole phases; row counts of whole blocks.
+static bool mfma_k_ok(int K) { return K % SSC == 0 && K <= KMAX && (K <= KPH_MAX || K % KPH_MAX == 0); }
+
+bool mfma_shape_ok(int d, int m) {
+    return d % DN_BLOCK_ROWS == 0 && m % GU_ROWS == 0 && mfma_k_ok(d) && mfma_k_ok(m);
+}
+
+namespace {
+
+template <int G>
+constexpr size_t gateup_lds(int d) {
+    return Lay(d, G).total > (size_t)2 * MT * (GU_ROWS + 4) * 4 ? Lay(d, G).total
+                                                                 : (size_t)2 * MT * (GU_ROWS + 4) * 4;
+}
+
+// Dynamic LDS above 64 KiB must be allowed per kernel: once per device,
+// for the largest contraction the kernels take.
+constexpr int MAX_DEV = 64;
+std::atomic<unsigned> g_lds_set[MAX_DEV];
+
+hipError_t allow_lds() {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= MAX_DEV) return hipErrorInvalidDevice;
+    if (g_lds_set[dev].load(std::memory_order_acquire)) return hipSuccess;
+    const struct { const void* f; size_t b; } k[4] = {
+        {(const void*)k_gateup_mfma<64>, gateup_lds<64>(KMAX)}, {(const void*)k_gateup_mfma<32>, gateup_lds<32>(KMAX)},
+        {(const void*)k_down_mfma<64>, Lay(KMAX, 64).total}, {(const void*)k_down_mfma<32>, Lay(KMAX, 32).total}};
+    for (const auto& x : k) {
+        e = hipFuncSetAttribute(x.f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)x.b);
+        if (e != hipSuccess) return e;
+    }
+    g_lds_set[dev].store(1u, std::memory_order_release);
+    return hipSuccess;
+}
+
+}  // namespace
 
 hipError_t launch_gateup_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st) {
     if (max_tiles == 0) return hipSuccess;
-    if (!mfma_shape_ok(a.d, a.m)) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)max_tiles, (unsigned)(a.m / MROWS));
-    if (a.group == 64) hipLaunchKernelGGL(k_gateup_mfma<64>, grid, dim3(MTHREADS), 0, st, a);
-    else hipLaunchKernelGGL(k_gateup_mfma<32>, grid, dim3(MTHREADS), 0, st, a);
+    if (!mfma_shape_ok(a.d, a.m) || (a.group != 64 && a.group != 32)) return hipErrorInvalidValue;
+    hipError_t e = allow_lds();
+    if (e != hipSuccess) return e;
+    const dim3 grid((unsigned)max_tiles, (unsigned)(a.m / GU_ROWS));
+    if (a.group == 64) hipLaunchKernelGGL(k_gateup_mfma<64>, grid, dim3(MTHREADS), gateup_lds<64>(a.d), st, a);
+    else hipLaunchKernelGGL(k_gateup_mfma<32>, grid, dim3(MTHREADS), gateup_lds<32>(a.d), st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_down_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st) {
     if (max_tiles == 0) return hipSuccess;
-    if (!mfma_shape_ok(a.d, a.m)) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)max_tiles, (unsigned)(a.d / MROWS));
-    if (a.group == 64) hipLaunchKernelGGL(k_down_mfma<64>, grid, dim3(MTHREADS), 0, st, a);
-    else hipLaunchKernelGGL(k_down_mfma<32>, grid, dim3(MTHREADS), 0, st, a);
+    if (!mfma_shape_ok(a.d, a.m) || (a.group != 64 && a.group != 32)) return hipErrorInvalidValue;
+    hipError_t e = allow_lds();
+    if (e != hipSuccess) return e;
+    const dim3 grid((unsigned)max_tiles, (unsigned)(a.d / DN_BLOCK_ROWS));
+    if (a.group == 64) hipLaunchKernelGGL(k_down_mfma<64>, grid, dim3(MTHREADS), Lay(a.m, 64).total, st, a);
+    else hipLaunchKernelGGL(k_down_mfma<32>, grid, dim3(MTHREADS), Lay(a.m, 32).total, st, a);
     return hipGetLastError();
 }
 

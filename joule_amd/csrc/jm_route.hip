@@ -31,7 +31,6 @@
 
 namespace jm {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 // Interleaved copy of the router tables (L layers of E experts; E padded
 // to Ep = a multiple of 8 per layer, the padding left as the caller cleared
@@ -218,17 +217,6 @@ k_router_grp(RouteArgs a) {
             xv[i].w = __fmul_rn(__fmul_rn(xv[i].w, inv), bf16_bits_to_f32(w.y >> 16));
         }
     }
-    // the power-of-two prescale of the token's fp16 split (MFMA branch)
-    float xf = 1.0f;
-    if (a.xsh) {
-        float mx = 0.0f;
-#pragma unroll
-        for (int i = 0; i < XV; i++)
-            mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xv[i].x), fabsf(xv[i].y))), fmaxf(fabsf(xv[i].z), fabsf(xv[i].w)));
-        const int pe = split_exp(seg_max<64>(mx));
-        xf = exp2i(-pe);
-        if (eg == 0 && lane == 0) a.xexp[b] = exp2i(pe);
-    }
 #pragma unroll
     for (int i = 0; i < XV; i++) {
         const int j = 4 * (lane + 64 * i);
@@ -269,22 +257,10 @@ k_router_grp(RouteArgs a) {
         const float v = ok ? xT[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
         encode_group_wave<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + (ok ? p : 0)) * (NDIG * (G / 8)),
                                    a.xscale + (size_t)b * ng + (ok ? p : 0));
-    }
-    // the token split into fp16 hi + lo for the MFMA branch, columns in its
-    // order: this block's share of 8-column groups
-    if (a.xsh) {
-        for (int c = (eg * 64 + lane) * 8; c < d; c += ngrp * 64 * 8) {
-            half8 h, l;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int j = c + i;
-                const float v = __fmul_rn(xT[(size_t)(j & 7) * TP + (j >> 3)], xf);
-                const _Float16 hh = (_Float16)v;
-                h[mfma_slot(i)] = hh;
-                l[mfma_slot(i)] = (_Float16)(v - (float)hh);
-            }
-            *(half8*)(a.xsh + (size_t)b * d + c) = h;
-            *(half8*)(a.xsl + (size_t)b * d + c) = l;
+        // the same group as int8 digit pairs for the MFMA branch
+        if (a.xqh) {
+            const size_t o = (size_t)b * d + (size_t)(ok ? p : 0) * G;
+            encode_i8_group_wave<G>(v, ok, a.xqh + o, a.xql + o, a.xqs + (size_t)b * ng + (ok ? p : 0));
         }
     }
 }
@@ -295,7 +271,7 @@ k_router_grp(RouteArgs a) {
 // runs its group's chains for the 4 tokens from one read of its table
 // chunks, each token's chain in the same order as k_router_grp's, so the
 // scores are the same bits.  The table is read once per 4 tokens instead of
-// once per token.  The x digits and the MFMA-branch split of the 4 tokens
+// once per token.  The x digits and the MFMA-branch digit pairs of the 4 tokens
 // are shared out over the grid's waves as k_router_grp shares them.
 constexpr int RQ_T = 4;             // tokens per block
 template <int G, int NDIG, int DV, bool WBF16, bool LAYER>
@@ -306,7 +282,6 @@ k_router_quad(RouteArgs a) {
     constexpr int T = d / 8;
     constexpr int TP = T + 4;
     __shared__ float xT[RQ_T][8 * TP];
-    __shared__ float xfs[RQ_T];                  // 2^-p of each token's fp16 split
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int eg = blockIdx.x * 4 + w;           // this wave's expert group
@@ -379,17 +354,6 @@ k_router_quad(RouteArgs a) {
 #pragma unroll
             for (int i = 0; i < XV; i++) xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
-        if (a.xsh) {
-            float mx = 0.0f;
-#pragma unroll
-            for (int i = 0; i < XV; i++)
-                mx = fmaxf(fmaxf(mx, fmaxf(fabsf(xv[i].x), fabsf(xv[i].y))), fmaxf(fabsf(xv[i].z), fabsf(xv[i].w)));
-            const int pe = split_exp(seg_max<64>(mx));
-            if (lane == 0) {
-                xfs[w] = exp2i(-pe);
-                if (blockIdx.x == 0 && b < a.B) a.xexp[b] = exp2i(pe);
-            }
-        }
         float* xw = xT[w];
 #pragma unroll
         for (int i = 0; i < XV; i++) {
@@ -427,7 +391,7 @@ k_router_quad(RouteArgs a) {
             if (r == 0 && e < a.E && t < nt) a.logits[(size_t)(b0 + t) * a.E + e] = v;
         }
     }
-    // x digits (one G-value group per G-lane segment) and the MFMA split of
+    // x digits (one G-value group per G-lane segment) and the MFMA digit pairs of
     // the block's tokens: this wave's share, over the grid's nvg waves
     constexpr int ng = d / G;
     constexpr int PPW = JM_WAVE / G;
@@ -442,21 +406,9 @@ k_router_quad(RouteArgs a) {
             const float v = ok ? xw[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
             encode_group_wave<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + (ok ? p : 0)) * (NDIG * (G / 8)),
                                        a.xscale + (size_t)b * ng + (ok ? p : 0));
-        }
-        if (a.xsh) {
-            const float xf = xfs[t];
-            for (int c = (eg * 64 + lane) * 8; c < d; c += nvg * 64 * 8) {
-                half8 h, l;
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const int j = c + i;
-                    const float v = __fmul_rn(xw[(size_t)(j & 7) * TP + (j >> 3)], xf);
-                    const _Float16 hh = (_Float16)v;
-                    h[mfma_slot(i)] = hh;
-                    l[mfma_slot(i)] = (_Float16)(v - (float)hh);
-                }
-                *(half8*)(a.xsh + (size_t)b * d + c) = h;
-                *(half8*)(a.xsl + (size_t)b * d + c) = l;
+            if (a.xqh) {
+                const size_t o = (size_t)b * d + (size_t)(ok ? p : 0) * G;
+                encode_i8_group_wave<G>(v, ok, a.xqh + o, a.xql + o, a.xqs + (size_t)b * ng + (ok ? p : 0));
             }
         }
     }

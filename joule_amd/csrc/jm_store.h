@@ -27,18 +27,18 @@ struct Ws {
     int* rank;                  // [B*k]
     int* comb;                  // [B*k]
     ExpertWork* work;           // [E]
-    int2* tiles;                // [B*k/64 + E] dense tiles (dispatch path)
+    int2* tiles;                // [B*k/32 + E] dense tiles (dispatch path)
     int* n_tiles;               // [1]
     float* act;                 // [B*k][m]
     uint32_t* adig;             // [B*k][m/8][NDIG] act digits
     float* ascale;              // [B*k][m/32]
     float* y;                   // [B*k][d]
-    _Float16* act_h;            // [B*k][m] act split for the MFMA down
-    _Float16* act_l;
-    _Float16* xsh;              // [B][d] tokens split for the MFMA gate/up
-    _Float16* xsl;
-    float* xexp;                // [B] power-of-two prescale of each token's split
-    float* aexp;                // [B*k][m/128] power-of-two prescale of each act block's split
+    int8_t* aqh;                // [B*k][m] act as int8 digit pairs for the MFMA down
+    int8_t* aql;
+    int8_t* xqh;                // [B][d] tokens as int8 digit pairs for the MFMA gate/up
+    int8_t* xql;
+    float* xqs;                 // [B][d/G] scales of the token digit pairs
+    float* aqs;                 // [B*k][m/G] scales of the act digit pairs
 };
 
 }  // namespace jm
@@ -86,6 +86,7 @@ struct jm_store {
     int prof;
     hipEvent_t ev[JM_STAGES + 1];
     int dense_min;              // segment size from which an expert takes the MFMA branch
+    bool mfma_ok;               // the shape and the records' alignment allow the MFMA branch
     // ---- batch decode (jm_decode_layers_batch) ----
     int max_layers;             // jm_store_set_max_layers: < 0 runs every layer
     int dec_B, dec_S, dec_nqkv, dec_hq, dec_V;   // sizes the decode workspace holds
