@@ -90,7 +90,7 @@ int check_group_shape(int d, int m, int group) {
 namespace {
 
 // Sizes of the Ws fields for B tokens, in field order.
-constexpr int WS_NF = 25;
+constexpr int WS_NF = 24;
 void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
     const int E = s->E, d = s->d, m = s->m, k = s->topk, G = s->group;
     const size_t nslot = (size_t)B * k;
@@ -108,7 +108,6 @@ void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
         (size_t)E * 4,                // active
         4,                            // n_active
         (size_t)E * 4,                // first_slot
-        nslot * 4,                    // rank
         nslot * 4,                    // comb
         (size_t)E * sizeof(jm::ExpertWork),   // work table
         max_tiles * 8,                // dense tiles
@@ -143,7 +142,7 @@ void jm::ws_layout(const jm_store* s, int B, char* base, Ws* w) {
     void** slots[WS_NF] = {(void**)&w->logits, (void**)&w->top, (void**)&w->tw, (void**)&w->xdig,
                            (void**)&w->xscale, (void**)&w->seg_off, (void**)&w->seg_slot,
                            (void**)&w->active, (void**)&w->n_active, (void**)&w->first_slot,
-                           (void**)&w->rank, (void**)&w->comb, (void**)&w->work, (void**)&w->tiles,
+                           (void**)&w->comb, (void**)&w->work, (void**)&w->tiles,
                            (void**)&w->n_tiles, (void**)&w->act, (void**)&w->adig,
                            (void**)&w->ascale, (void**)&w->y, (void**)&w->aqh, (void**)&w->aql,
                            (void**)&w->xqh, (void**)&w->xql, (void**)&w->xqs, (void**)&w->aqs};
@@ -202,7 +201,7 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     r.norm_w = io.norm_w; r.eps = io.eps; r.B = B; r.E = E; r.d = d; r.topk = k; r.renorm = s->renorm; r.group = G;
     r.logits = w.logits; r.xdig = w.xdig; r.xscale = w.xscale; r.top = w.top; r.tw = w.tw;
     r.seg_off = w.seg_off; r.seg_slot = w.seg_slot; r.active = w.active; r.n_active = w.n_active;
-    r.first_slot = w.first_slot; r.comb = w.comb; r.rank_scratch = w.rank;
+    r.first_slot = w.first_slot; r.comb = w.comb;
     r.work = w.work; r.umax = umax; r.rec = s->rec;
     r.key0 = (long long)layer * E;
     r.dense_min = s->dense_min; r.tiles = w.tiles; r.n_tiles = w.n_tiles;
@@ -572,14 +571,8 @@ int jm_dispatch(const int32_t* top, int nslot, int E, int topk, int32_t* seg_off
     JM_HIP(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev), "hipDeviceGetAttribute");
     if ((size_t)jm::dispatch_lds_ints(nslot, E) * 4 > (size_t)lds_max)
         return fail(JM_ERR_SHAPE, "%d slots over %d experts exceed the dispatch's LDS", nslot, E);
-    hipStream_t st = (hipStream_t)stream;
-    void* scratch = nullptr;
-    JM_HIP(hipMallocAsync(&scratch, align256((size_t)nslot * 4 + 4), st), "hipMallocAsync dispatch scratch");
-    hipError_t e = jm::launch_dispatch(top, nslot, E, topk, seg_off, seg_slot, active, n_active, first_slot,
-                                       comb, (int*)scratch, st);
-    hipError_t f = hipFreeAsync(scratch, st);
-    if (e != hipSuccess) return hip_fail(e, "dispatch launch");
-    if (f != hipSuccess) return hip_fail(f, "hipFreeAsync");
+    JM_HIP(jm::launch_dispatch(top, nslot, E, topk, seg_off, seg_slot, active, n_active, first_slot, comb,
+                               (hipStream_t)stream), "dispatch launch");
     return 0;
 }
 

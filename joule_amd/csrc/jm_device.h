@@ -702,46 +702,55 @@ struct TableSlots {
 // Dispatch chunks: 64 consecutive slots, one wave's worth.
 constexpr int DISP_CHUNK = 64;
 
-// LDS of dispatch_block, in ints: per-chunk expert counts, segment starts,
-// first slots, scan scratch.
+// LDS of dispatch_block, in ints: per-expert chunk counts [E][nchunk],
+// segment starts [E + 1], first slots [E], scan scratch [32], then 16 bits
+// per slot twice: the expert ids, and the in-chunk ranks (later the union
+// keys).
 __host__ __device__ constexpr int dispatch_lds_ints(int nslot, int E) {
-    return (nslot + DISP_CHUNK - 1) / DISP_CHUNK * E + 2 * E + 1 + 32;
+    return (nslot + DISP_CHUNK - 1) / DISP_CHUNK * E + 2 * E + 1 + 32 + 2 * ((nslot + 1) / 2);
 }
 
-// Stable counting sort of nslot slots by expert id, run by one whole block
-// (decode_kernel.c:1449-1485 builds the same segments in first-appearance
-// order; here they are in expert-id order, slots within a segment in
-// increasing b*k+i order).  `rank` is nslot ints of scratch.  E <=
-// blockDim.x.  Writes seg_off[E+1], seg_slot, active[U] (expert-id order),
-// *n_active = U, first_slot[e], and comb[b*k + j] = the token's slots in the
-// reference's union order (ascending first appearance of their expert), -1
-// padded.  With `work`, also the expert work table for umax entries: the
-// experts with two or more slots first, then those with one (each group in
-// expert-id order), so that the longest segments start first; entries past U
-// have n = 0.  `rec` holds the record offsets of expert tid (tid < E).
-// A slot's rank among the earlier slots of its chunk with the same expert
-// comes from ballots over the bits of the expert id (lanes with equal ids
-// agree on every bit).
+// Stable counting sort of nslot (< 65536) slots by expert id, run by one
+// whole block (decode_kernel.c:1449-1485 builds the same segments in
+// first-appearance order; here they are in expert-id order, slots within a
+// segment in increasing b*k+i order).  E <= blockDim.x.  Everything between
+// the top-k table and the outputs stays in LDS.  Writes seg_off[E+1],
+// seg_slot, active[U] (expert-id order), *n_active = U, first_slot[e], and
+// comb[b*k + j] = the token's slots in the reference's union order
+// (ascending first appearance of their expert), -1 padded.  With `work`,
+// also the expert work table for umax entries: the experts with two or more
+// slots first, then those with one (each group in expert-id order), so that
+// the longest segments start first; entries past U have n = 0.  `rec` holds
+// the record offsets of expert tid (tid < E).  A slot's rank among the
+// earlier slots of its chunk with the same expert comes from ballots over
+// the bits of the expert id (lanes with equal ids agree on every bit).
 __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E, int k, int* lds,
                                                int* __restrict__ seg_off, int* __restrict__ seg_slot,
                                                int* __restrict__ active, int* __restrict__ n_active,
                                                int* __restrict__ first_slot, int* __restrict__ comb,
-                                               int* rank, ExpertWork* __restrict__ work = nullptr,
+                                               ExpertWork* __restrict__ work = nullptr,
                                                int umax = 0, const ExpertRec* rec = nullptr) {
+    constexpr unsigned short NONE = 0xFFFF;
     const int nchunk = (nslot + DISP_CHUNK - 1) / DISP_CHUNK;
-    int* cnt = lds;                              // [nchunk][E]
+    int* cnt = lds;                              // [E][nchunk]
     int* off = cnt + nchunk * E;                 // [E + 1]
     int* fs = off + E + 1;                       // [E]
     unsigned* wsum = (unsigned*)(fs + E);        // [32]
-    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63;
+    unsigned short* te = (unsigned short*)(wsum + 32);   // [nslot] expert id, NONE: no expert
+    unsigned short* rk = te + 2 * ((nslot + 1) / 2);     // [nslot] in-chunk rank, then union key
+    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, w = tid >> 6, nw = nth >> 6;
     for (int i = tid; i < nchunk * E; i += nth) cnt[i] = 0;
+    for (int s = tid; s < nslot; s += nth) {
+        const int e = top[s];
+        te[s] = (e >= 0 && e < E) ? (unsigned short)e : NONE;
+    }
     __syncthreads();
     int nbits = 1;
     while ((1 << nbits) < E) nbits++;
-    for (int c = tid >> 6; c < nchunk; c += nth >> 6) {
+    for (int c = w; c < nchunk; c += nw) {
         const int s = c * DISP_CHUNK + lane;
-        const int e0 = s < nslot ? top[s] : -1;
-        const bool ok = e0 >= 0 && e0 < E;
+        const unsigned short e0 = s < nslot ? te[s] : NONE;
+        const bool ok = e0 != NONE;
         const int e = ok ? e0 : 0;
         unsigned long long same = __ballot(ok);
         for (int b = 0; b < nbits; b++) {
@@ -749,23 +758,27 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
             same &= ((e >> b) & 1) ? bb : ~bb;
         }
         const int r = __popcll(same & ((1ull << lane) - 1ull));
-        if (s < nslot) rank[s] = ok ? r : -1;
-        if (ok && r == 0) cnt[c * E + e] = __popcll(same);
+        if (s < nslot) rk[s] = ok ? (unsigned short)r : NONE;
+        if (ok && r == 0) cnt[e * nchunk + c] = __popcll(same);
     }
     __syncthreads();
-    // per expert: exclusive prefix over chunks, then one block scan of
-    // (count, multi << 16 | single) gives segment starts and the work-table
-    // positions of both groups
-    int total_e = 0;
-    if (tid < E) {
-        int run = 0;
-        for (int c = 0; c < nchunk; c++) {
-            const int v = cnt[c * E + tid];
-            cnt[c * E + tid] = run;
-            run += v;
+    // per expert: exclusive prefix over its chunks (one wave per expert, a
+    // wave scan per 64 chunks); the expert's total goes to off[e]
+    for (int e = w; e < E; e += nw) {
+        unsigned carry = 0;
+        for (int c0 = 0; c0 < nchunk; c0 += 64) {
+            const int c = c0 + lane;
+            const unsigned v = c < nchunk ? (unsigned)cnt[e * nchunk + c] : 0u;
+            const unsigned incl = wave_inclusive_scan(v);
+            if (c < nchunk) cnt[e * nchunk + c] = (int)(carry + incl - v);
+            carry += (unsigned)__shfl(incl, 63, JM_WAVE);
         }
-        total_e = run;
+        if (lane == 0) off[e] = (int)carry;
     }
+    __syncthreads();
+    // one block scan of (count, multi << 16 | single) gives segment starts
+    // and the work-table positions of both groups
+    const int total_e = tid < E ? off[tid] : 0;
     uint2 tot;
     const uint2 excl = block_exclusive_scan2(
         make_uint2((unsigned)total_e, ((unsigned)(total_e > 1) << 16) | (unsigned)(total_e == 1)), wsum, &tot);
@@ -808,32 +821,32 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
     }
     __syncthreads();
     for (int s = tid; s < nslot; s += nth) {
-        const int r = rank[s];
-        if (r < 0) continue;
-        const int e = top[s];
-        const int pos = off[e] + cnt[(s / DISP_CHUNK) * E + e] + r;
+        const unsigned short r = rk[s];
+        if (r == NONE) continue;
+        const int e = te[s];
+        const int pos = off[e] + cnt[e * nchunk + s / DISP_CHUNK] + r;
         seg_slot[pos] = s;
         if (pos == off[e]) { first_slot[e] = s; fs[e] = s; }
     }
     __syncthreads();
     // union order per token: its slots ranked by the first slot of their
     // expert (distinct experts -> distinct keys); slots without an expert go
-    // last and are stored as -1.  Each slot's key goes to `rank` first.
+    // last and are stored as -1.  Each slot's key replaces its rank.
     for (int bi = tid; bi < nslot; bi += nth) {
-        const int e = top[bi];
-        rank[bi] = (e >= 0 && e < E) ? fs[e] : 0x7FFFFFFF;
+        const unsigned short e = te[bi];
+        rk[bi] = e != NONE ? (unsigned short)fs[e] : NONE;
     }
     __syncthreads();
     for (int bi = tid; bi < nslot; bi += nth) {
         const int b = bi / k, i = bi % k;
-        const int key = rank[bi];
+        const unsigned short key = rk[bi];
         int r = 0;
 #pragma unroll 8
         for (int j = 0; j < k; j++) {
-            const int kj = rank[b * k + j];
+            const unsigned short kj = rk[b * k + j];
             r += (kj < key) || (kj == key && j < i);
         }
-        comb[b * k + r] = key != 0x7FFFFFFF ? bi : -1;
+        comb[b * k + r] = key != NONE ? bi : -1;
     }
 }
 

@@ -14,7 +14,7 @@
 // Limits of the kernels: experts per layer (top-k keeps E/64 values per lane,
 // dispatch keeps per-expert counts in LDS) and slots (B*topk) per call.
 #define JM_MAX_E 512
-#define JM_MAX_SLOTS 65536
+#define JM_MAX_SLOTS 65535       // the dispatch keeps slot indices in 16 bits
 #define JM_MAX_TOPK 32
 // Calls with B*topk up to this many slots take the decode path: three
 // launches, the experts' slots found by ballots over the top-k table and the
@@ -97,7 +97,6 @@ struct RouteArgs {
     int* n_active;            // [1]
     int* first_slot;          // [E]
     int* comb;                // [B*k] each token's slots in union order, -1 padded
-    int* rank_scratch;        // [B*k]
     ExpertWork* work;         // [umax] expert work table
     int umax;                 // min(E, B*k)
     RecLoc rec;               // store record offsets
@@ -129,8 +128,7 @@ hipError_t launch_topk(const float* logits, int B, int E, int k, int renorm, int
                        hipStream_t st);
 // E <= JM_MAX_E, nslot <= JM_MAX_SLOTS
 hipError_t launch_dispatch(const int* top, int nslot, int E, int k, int* seg_off, int* seg_slot,
-                           int* active, int* n_active, int* first_slot, int* comb, int* rank_scratch,
-                           hipStream_t st);
+                           int* active, int* n_active, int* first_slot, int* comb, hipStream_t st);
 // decode path (nslot <= JM_DEC_SLOTS): gate/up over ballot-found slots, then
 // down + combine into a.out.  For gateup_topk(B, E) the gate/up kernel
 // computes the top-k itself (from a.logits; no top-k launch before it).

@@ -65,10 +65,9 @@ k_topk(const float* __restrict__ logits, int E, int k, int renorm, int* __restri
 __global__ void __launch_bounds__(1024)
 k_dispatch(const int* __restrict__ top, int nslot, int E, int k, int* __restrict__ seg_off,
            int* __restrict__ seg_slot, int* __restrict__ active, int* __restrict__ n_active,
-           int* __restrict__ first_slot, int* __restrict__ comb, int* __restrict__ rank_scratch) {
+           int* __restrict__ first_slot, int* __restrict__ comb) {
     extern __shared__ int lds_i[];
-    dispatch_block(top, nslot, E, k, lds_i, seg_off, seg_slot, active, n_active, first_slot, comb,
-                   rank_scratch);
+    dispatch_block(top, nslot, E, k, lds_i, seg_off, seg_slot, active, n_active, first_slot, comb);
 }
 
 // Exact dequantisation (q - 8) * fp32(scale) of one tensor record.
@@ -157,11 +156,10 @@ hipError_t launch_topk(const float* logits, int B, int E, int k, int renorm, int
 }
 
 hipError_t launch_dispatch(const int* top, int nslot, int E, int k, int* seg_off, int* seg_slot,
-                           int* active, int* n_active, int* first_slot, int* comb, int* rank_scratch,
-                           hipStream_t st) {
+                           int* active, int* n_active, int* first_slot, int* comb, hipStream_t st) {
     const size_t lds = (size_t)dispatch_lds_ints(nslot, E) * 4;
     hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), lds, st, top, nslot, E, k, seg_off, seg_slot,
-                       active, n_active, first_slot, comb, rank_scratch);
+                       active, n_active, first_slot, comb);
     return hipGetLastError();
 }
 

@@ -421,7 +421,7 @@ k_dispatch_work(RouteArgs a) {
     ExpertRec rec;
     if ((int)threadIdx.x < a.E) rec = load_expert_rec(a.rec, a.key0, threadIdx.x);
     dispatch_block(a.top, a.B * a.topk, a.E, a.topk, lds_i, a.seg_off, a.seg_slot, a.active,
-                   a.n_active, a.first_slot, a.comb, a.rank_scratch, a.work, a.umax, &rec);
+                   a.n_active, a.first_slot, a.comb, a.work, a.umax, &rec);
     // the dense experts' token tiles, in work-table order
     __syncthreads();
     const int u = threadIdx.x;

@@ -24,7 +24,6 @@ struct Ws {
     int* active;                // [E]
     int* n_active;              // [1]
     int* first_slot;            // [E]
-    int* rank;                  // [B*k]
     int* comb;                  // [B*k]
     ExpertWork* work;           // [E]
     int2* tiles;                // [B*k/32 + E] dense tiles (dispatch path)
