@@ -7,11 +7,11 @@
 //
 //   k_gemv_part   Wq/Wk/Wv . (h * norm1 weight), per 512-column slice
 //                                                             (:224-230, :1126-1145)
-//   k_qkv_fin     the slices summed, RMSNorm row scale, bias, per-head
-//                 QK-norm, RoPE; q out, k and v appended to the cache
-//                                                               (:1146-1199)
-//   k_attn_part   scores, softmax and P.V over one 128-position split of
-//                 the cache                                     (:1200-1222)
+//   k_attn_part   the slices summed, RMSNorm row scale, bias, per-head
+//                 QK-norm and RoPE of the block's heads (:1146-1199; the k
+//                 and v rows appended to the cache by the split that holds
+//                 the token's position), then scores, softmax and P.V over
+//                 one 128-position split of the cache           (:1200-1222)
 //   k_attn_comb   the splits merged per head                   (flash-decoding merge)
 //   k_gemv_part   Wo . att per slice; the MoE router sums the slices into
 //                 the residual                                  (:1225-1232, :1546-1547)
@@ -63,7 +63,14 @@ k_gemv_part(GemvArgs a) {
     uint4 wa[NK];
 #pragma unroll
     for (int ks = 0; ks < NK; ks++) wa[ks] = *(const uint4*)(wp + 32 * ks);
-    // the tokens' slice (times the norm weight), split into hi and lo columns
+    // the tokens' slice (times the norm weight), split into hi and lo
+    // columns; with a.rss the first row group's blocks also sum the squares
+    // of the slice (before the norm weight) per token: thread tid serves
+    // token tb0 + tid % 8 throughout
+    static_assert((WV * 64) % 8 == 0, "token of a thread fixed over the loop");
+    __shared__ float ssw[WV][8];
+    const bool want_ss = a.rss && blockIdx.x == 0;    // block-uniform
+    float ss = 0.0f;
     for (int i = tid; i < NK * 32; i += WV * 64) {
         const int ks = i >> 5, gg = (i >> 3) & 3, t = i & 7;
         const int c = k0 + 32 * ks + 8 * gg;
@@ -73,6 +80,8 @@ k_gemv_part(GemvArgs a) {
             const float4 x0 = xp[0], x1 = xp[1];
             v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
             v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+#pragma unroll
+            for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[e], v[e], ss);
             if (a.norm_w) {
                 const uint4 nw = *(const uint4*)(a.norm_w + c);
                 const uint32_t nn[4] = {nw.x, nw.y, nw.z, nw.w};
@@ -92,7 +101,20 @@ k_gemv_part(GemvArgs a) {
         xb[ks][16 * gg + t] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
         xb[ks][16 * gg + 8 + t] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
     }
+    if (want_ss) {
+        // lanes with equal lane % 8 serve one token
+        ss = __fadd_rn(ss, __shfl_xor(ss, 8, JM_WAVE));
+        ss = __fadd_rn(ss, __shfl_xor(ss, 16, JM_WAVE));
+        ss = __fadd_rn(ss, __shfl_xor(ss, 32, JM_WAVE));
+        if (lane < 8) ssw[w][lane] = ss;
+    }
     __syncthreads();
+    if (want_ss && tid < 8 && tb0 + tid < a.B) {
+        float t = ssw[0][tid];
+#pragma unroll
+        for (int u = 1; u < WV; u++) t = __fadd_rn(t, ssw[u][tid]);
+        a.rss[(size_t)slice * a.B + tb0 + tid] = t;
+    }
     if (!live) return;
 
     // two accumulators break the dependence chain of the k-steps
@@ -299,94 +321,154 @@ __device__ __forceinline__ float head_reduce16(float (&v)[QPK]) {
 
 __device__ __forceinline__ float bf16_round(float f) { return __uint_as_float(f32_to_bf16_rne(f) << 16); }
 
-// The projections of one head of one token finished: the column slices
-// summed, times the RMSNorm row scale of h, plus the bias (:1126-1145); for
-// q and k heads the per-head RMSNorm (:1174-1189) and RoPE rotate-half at
-// the token's position (:1190-1194, :259-266).  q heads go to qsplit; k and v
-// heads are appended to the bf16 cache at the position (:1195-1199).
-// Block (head in q.., k.., v.., token), one thread per dimension.
-__global__ void __launch_bounds__(128)
-k_qkv_fin(AttnArgs a) {
+// Four consecutive projection values of one token (rows row .. row + 3 of
+// the stacked q, k, v outputs, dimensions 4 j .. 4 j + 3 of one head) with
+// everything their finish reads, requested together: the first
+// min(nslice, 4) column slices, the slices' sums of squares of h, the bias,
+// the per-head norm weight and the RoPE factors at pos.
+struct Fin4 {
+    float4 sl[4];
+    float rs[4];
+    float4 bias;
+    uint2 nw;
+    float4 c, sn;
+};
+
+__device__ __forceinline__ void fin4_load(Fin4& f, const AttnArgs& a, int b, int row, const float* bias, int brow,
+                                          const uint16_t* nw, bool rope, int pos, int j) {
     constexpr int HD = 128;
-    __shared__ float vals[HD];
-    __shared__ float red[2];
-    const int hh = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
-    const int pos = a.pos[b];
-    // RMSNorm row scale of the layer input (the projections were taken of
-    // h * norm weight)
-    float inv;
-    if (a.rss) {
-        inv = rms_inv(a.rss[b], a.d, a.eps);        // summed by the projection GEMM
-    } else {
-        const float* hb = a.h + (size_t)b * a.d;
-        float ss = 0.0f;
-        for (int i = t; i < a.d / 4; i += HD) {
-            const float4 v = *(const float4*)(hb + 4 * i);
-            ss = __builtin_fmaf(v.x, v.x, ss);
-            ss = __builtin_fmaf(v.y, v.y, ss);
-            ss = __builtin_fmaf(v.z, v.z, ss);
-            ss = __builtin_fmaf(v.w, v.w, ss);
+    const int ns = a.nslice < 4 ? a.nslice : 4;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int sl = u < ns ? u : 0;          // clamped: the select in fin4_value drops it
+        f.sl[u] = *(const float4*)(a.qkv + ((size_t)sl * a.B + b) * a.nqkv + row);
+        f.rs[u] = a.rss[(size_t)sl * a.B + b];
+    }
+    f.bias = bias ? *(const float4*)(bias + brow) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    f.nw = nw ? *(const uint2*)(nw + 4 * j) : make_uint2(0u, 0u);
+    if (rope) {
+        const size_t ci = (size_t)pos * HD + 4 * (j & 15);
+        f.c = *(const float4*)(a.cos + ci);
+        f.sn = *(const float4*)(a.sin + ci);
+    }
+}
+
+// The four values finished (decode_kernel.c:1126-1199): the column slices
+// summed in slice order, times the RMSNorm row scale of h (the projections
+// were taken of h * norm weight), plus the bias; then, for a q or k head,
+// the per-head RMSNorm with weight nw (:1174-1189) and RoPE rotate-half at
+// pos (:1190-1194, :259-266) over the aligned 32-lane segment that holds
+// the head (lane j: dimensions 4 j .. 4 j + 3; dim i pairs with i + 64,
+// i.e. lane j with j ^ 16; first half a cos - b sin, second a sin + b cos).
+__device__ __forceinline__ void fin4_value(float (&v)[4], const Fin4& f, const AttnArgs& a, int b, int row,
+                                           bool norm, bool rope, int j) {
+    constexpr int HD = 128;
+    const int ns = a.nslice < 4 ? a.nslice : 4;
+    float4 acc = f.sl[0];
+    float ss = f.rs[0];
+#pragma unroll
+    for (int u = 1; u < 4; u++) {
+        const bool in = u < ns;
+        acc.x = in ? __fadd_rn(acc.x, f.sl[u].x) : acc.x;
+        acc.y = in ? __fadd_rn(acc.y, f.sl[u].y) : acc.y;
+        acc.z = in ? __fadd_rn(acc.z, f.sl[u].z) : acc.z;
+        acc.w = in ? __fadd_rn(acc.w, f.sl[u].w) : acc.w;
+        ss = in ? __fadd_rn(ss, f.rs[u]) : ss;
+    }
+    for (int sl = 4; sl < a.nslice; sl++) {     // wider inputs (d = 3072, 8192): the rest of the slices
+        const float4 t = *(const float4*)(a.qkv + ((size_t)sl * a.B + b) * a.nqkv + row);
+        acc.x = __fadd_rn(acc.x, t.x);
+        acc.y = __fadd_rn(acc.y, t.y);
+        acc.z = __fadd_rn(acc.z, t.z);
+        acc.w = __fadd_rn(acc.w, t.w);
+        ss = __fadd_rn(ss, a.rss[(size_t)sl * a.B + b]);
+    }
+    const float inv = rms_inv(ss, a.d, a.eps);
+    v[0] = __fadd_rn(__fmul_rn(acc.x, inv), f.bias.x);
+    v[1] = __fadd_rn(__fmul_rn(acc.y, inv), f.bias.y);
+    v[2] = __fadd_rn(__fmul_rn(acc.z, inv), f.bias.z);
+    v[3] = __fadd_rn(__fmul_rn(acc.w, inv), f.bias.w);
+    if (norm) {
+        float sq = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) sq = __builtin_fmaf(v[e], v[e], sq);
+        // the reference sums the head's squares in dimension order; the
+        // tree here changes the sum by rounding only
+        const float hinv = rms_inv(seg_sum<32>(sq), HD, a.eps);
+        const uint32_t nn[4] = {f.nw.x & 0xFFFFu, f.nw.x >> 16, f.nw.y & 0xFFFFu, f.nw.y >> 16};
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = __fmul_rn(__fmul_rn(v[e], hinv), bf16_bits_to_f32(nn[e]));
+    }
+    if (rope) {
+        const bool lo = j < 16;
+        const float c[4] = {f.c.x, f.c.y, f.c.z, f.c.w}, sn[4] = {f.sn.x, f.sn.y, f.sn.z, f.sn.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float other = __shfl_xor(v[e], 16, JM_WAVE);
+            v[e] = lo ? __builtin_fmaf(v[e], c[e], -__fmul_rn(other, sn[e]))
+                      : __builtin_fmaf(other, sn[e], __fmul_rn(v[e], c[e]));
         }
-        ss = seg_sum<64>(ss);
-        if ((t & 63) == 0) red[t >> 6] = ss;
-        __syncthreads();
-        inv = rms_inv(__fadd_rn(red[0], red[1]), a.d, a.eps);
     }
-    const int row = hh * HD + t;
-    float v = a.qkv[(size_t)b * a.nqkv + row];
-    for (int sl = 1; sl < a.nslice; sl++) v = __fadd_rn(v, a.qkv[((size_t)sl * a.B + b) * a.nqkv + row]);
-    v = __fmul_rn(v, inv);
-    const bool isq = hh < a.H, isk = !isq && hh < a.H + a.KH;
-    const float* bias = isq ? a.bq : isk ? a.bk : a.bv;
-    const int brow = isq ? row : isk ? row - a.H * HD : row - (a.H + a.KH) * HD;
-    if (bias) v = __fadd_rn(v, bias[brow]);
+}
+
+// The k and v rows of one KV head of one token, for one wave: lanes 0..31
+// the k head (norm, RoPE), lanes 32..63 the v head.
+struct KvFin {
+    Fin4 f;
+    int row;
+    bool isk;
+};
+
+__device__ __forceinline__ void kv_load(KvFin& k, const AttnArgs& a, int b, int kh, int pos, int lane) {
+    constexpr int HD = 128;
+    k.isk = lane < 32;
+    const int j = lane & 31;
+    k.row = (k.isk ? a.H + kh : a.H + a.KH + kh) * HD + 4 * j;
+    fin4_load(k.f, a, b, k.row, k.isk ? a.bk : a.bv, kh * HD + 4 * j, k.isk ? a.kn : nullptr, k.isk, pos, j);
+}
+
+// Finished and appended to the token's caches kc, vc at pos (:1195-1199);
+// with kvn, also kept there (kvn[0]: k, kvn[1]: v, bf16).
+__device__ __forceinline__ void kv_store(const KvFin& k, const AttnArgs& a, int b, int kh, int pos, int lane,
+                                         gptr<uint16_t> kc, gptr<uint16_t> vc, uint16_t (*kvn)[128]) {
+    constexpr int HD = 128;
+    const int j = lane & 31;
+    float v[4];
+    fin4_value(v, k.f, a, b, k.row, k.isk && a.kn, k.isk, j);
+    uint16_t hb4[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) hb4[e] = (uint16_t)f32_to_bf16_rne(v[e]);
+    if (kvn) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) kvn[k.isk ? 0 : 1][4 * j + e] = hb4[e];
+    }
+    const gptr<uint16_t> dst = (k.isk ? kc : vc) + ((size_t)pos * a.KH + kh) * HD + 4 * j;
+    *(uint2*)dst = make_uint2(hb4[0] | ((uint32_t)hb4[1] << 16), hb4[2] | ((uint32_t)hb4[3] << 16));
+}
+
+// For a batch whose tokens may share a cache (a prefill chunk: the
+// positions of one prompt), every token's k and v rows are appended before
+// the attention reads the caches: one wave per (KV head, token).
+__global__ void __launch_bounds__(64)
+k_kv_append(AttnArgs a) {
+    const int kh = blockIdx.x, b = blockIdx.y;
+    const int pos = a.pos[b];
     const unsigned long long* kvp = a.kv + ((size_t)b * a.L + a.layer) * 2;
-    if (!isq && !isk) {                  // v head: to the cache
-        const gptr<uint16_t> vc = (gptr<uint16_t>)kvp[1];
-        vc[((size_t)pos * a.KH + (hh - a.H - a.KH)) * HD + t] = (uint16_t)f32_to_bf16_rne(v);
-        return;
-    }
-    const uint16_t* nw = isq ? a.qn : a.kn;
-    if (nw) {
-        float sq = seg_sum<64>(__fmul_rn(v, v));
-        __syncthreads();                 // red[] reused
-        if ((t & 63) == 0) red[t >> 6] = sq;
-        __syncthreads();
-        const float hinv = rms_inv(__fadd_rn(red[0], red[1]), HD, a.eps);
-        v = __fmul_rn(__fmul_rn(v, hinv), bf16_bits_to_f32(nw[t]));
-    }
-    // rotate-half: dim i pairs with i + 64 (first half: a cos - b sin,
-    // second half: a sin + b cos, with a = dim i, b = dim i + 64)
-    vals[t] = v;
-    __syncthreads();
-    const float other = vals[t ^ 64];
-    const bool lo = t < HD / 2;
-    const int ci = lo ? t : t - HD / 2;
-    const float c = a.cos[(size_t)pos * HD + ci], sn = a.sin[(size_t)pos * HD + ci];
-    const float o = lo ? __builtin_fmaf(v, c, -__fmul_rn(other, sn)) : __builtin_fmaf(other, sn, __fmul_rn(v, c));
-    if (isq) {
-        // split for the attention's matrix cores: hi = bf16(q), lo = bf16(q - hi)
-        const uint32_t hi = f32_to_bf16_rne(o);
-        const uint32_t lo = f32_to_bf16_rne(__fsub_rn(o, __uint_as_float(hi << 16)));
-        uint16_t* qs = a.qsplit + ((size_t)b * a.H + hh) * 2 * HD;
-        qs[t] = (uint16_t)hi;
-        qs[HD + t] = (uint16_t)lo;
-    } else {
-        const gptr<uint16_t> kc = (gptr<uint16_t>)kvp[0];
-        kc[((size_t)pos * a.KH + (hh - a.H)) * HD + t] = (uint16_t)f32_to_bf16_rne(o);
-    }
+    KvFin k;
+    kv_load(k, a, b, kh, pos, threadIdx.x);
+    kv_store(k, a, b, kh, pos, threadIdx.x, (gptr<uint16_t>)kvp[0], (gptr<uint16_t>)kvp[1], nullptr);
 }
 
 // One (position split, KV head, token): QPK query heads over positions
 // [128 s, 128 s + 128) of the token's T = pos + 1 cache rows (the row at pos
-// appended by k_qkv_fin), on the matrix cores.  Wave w takes 32 positions
+// finished and appended here), on the matrix cores.  Wave w takes 32 positions
 // tw = 128 s + 32 w .. tw + 31 and all 128 head dimensions.
 //
 // Scores (:1205-1211) by v_mfma_f32_16x16x32_bf16 with the cached K rows
 // as the A operand straight from memory (lane l: row tw + 16 mt + l % 16,
 // dimensions 32 kk + 8 (l / 16) .. + 7, one 16-byte load) and the query
 // heads as B columns: column n < 8 holds bf16(q) of head n, column n + 8 the
-// rest bf16(q - bf16(q)) (split by k_qkv_fin), so the two columns' sum
+// rest bf16(q - bf16(q)) (split in the prologue), so the two columns' sum
 // carries 16 significant bits of q against the exact bf16 keys, accumulated
 // in fp32.  The sum of
 // columns n and n ^ 8 (one DPP move) is the score of head n % 8 at the 4
@@ -409,29 +491,41 @@ k_attn_part(AttnArgs a) {
     __shared__ __align__(16) uint16_t vt[4][PW * VR];   // each wave's V rows
     __shared__ __align__(16) float red[4][QPK * HD];    // each wave's outputs
     __shared__ float mls[4][QPK][2];                    // each wave's (max, sum)
+    // until every wave has read them (the barrier after the query columns),
+    // red holds the finished query heads (bf16 hi, lo) and the token's own
+    // k and v row (the split that holds it): 3 blocks of 256 threads fit a CU
+    static_assert(QPK * 2 * HD * 2 + 2 * HD * 2 <= sizeof(float) * 4 * QPK * HD, "prologue fits red");
+    uint16_t (*qs)[2][HD] = (uint16_t (*)[2][HD])&red[0][0];
+    uint16_t (*kvn)[HD] = (uint16_t (*)[HD])((char*)&red[0][0] + QPK * 2 * HD * 2);
     const int s = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int pos = a.pos[b];
     const int T = pos + 1;
     const int t0 = s * P;
     if (t0 >= T) return;                 // past this token's positions (block-uniform)
+    // this split holds the token's own row and appends it (block-uniform);
+    // without a.append the rows were appended by k_kv_append
+    const bool own = a.append && pos < t0 + P;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
     const int tw = t0 + PW * w;
     const unsigned long long* kvp = a.kv + ((size_t)b * a.L + a.layer) * 2;
     const gptr<const uint16_t> kc = (gptr<const uint16_t>)kvp[0];
     const gptr<const uint16_t> vc = (gptr<const uint16_t>)kvp[1];
-    // requests in the order of use: the query columns (head n % 8, zero for
-    // heads >= QPK; the hi half of the split for n < 8, the lo half above),
-    // the K rows, the V rows (unconditional: row 0 past the end)
-    const int hq = n & 7;
-    const bool lo_col = n >= 8;
-    uint4 qr[4];
-    {
-        const uint16_t* qp = a.qsplit + (((size_t)b * a.H + kh * QPK + (hq < QPK ? hq : 0)) * 2 + (lo_col ? 1 : 0)) * HD + 8 * g;
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++)
-            qr[kk] = hq < QPK ? *(const uint4*)(qp + 32 * kk) : make_uint4(0u, 0u, 0u, 0u);
-    }
+    // requests first, in the order of use: the inputs of the block's
+    // query heads and (wave 0 of the split holding the token's row) of its
+    // k and v rows, then the K rows, then the V rows (unconditional: row 0
+    // past the end; the token's own row, not yet in the cache, is replaced
+    // below).  The projections are finished here: every split block
+    // finishes its query heads itself; with a.append the split holding the
+    // token's row also finishes its k and v, appends them to the cache and
+    // uses them in place of the cache row.
+    const int qh = tid >> 5, qj = tid & 31;          // query head qh of the block, dimensions 4 qj .. + 3
+    const int qrow = (kh * QPK + (qh < QPK ? qh : 0)) * HD + 4 * qj;
+    const bool kvw = own && w == 0;                  // wave-uniform
+    Fin4 fq;
+    fin4_load(fq, a, b, qrow, a.bq, qrow, a.qn, true, pos, qj);
+    KvFin fkv;
+    if (kvw) kv_load(fkv, a, b, kh, pos, lane);
     uint4 kr[2][4], vr[8];
 #pragma unroll
     for (int mt = 0; mt < 2; mt++) {
@@ -441,11 +535,47 @@ k_attn_part(AttnArgs a) {
         for (int kk = 0; kk < 4; kk++) kr[mt][kk] = load_g16(row + 32 * kk);
     }
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int t = tw + 4 * j + g;
-        vr[j] = load_g16(vc + ((size_t)(t < T ? t : 0) * a.KH + kh) * HD + 8 * n);
+    for (int jv = 0; jv < 8; jv++) {
+        const int t = tw + 4 * jv + g;
+        vr[jv] = load_g16(vc + ((size_t)(t < T ? t : 0) * a.KH + kh) * HD + 8 * n);
     }
     __builtin_amdgcn_sched_barrier(0);      // keep every request ahead of the arithmetic
+    {
+        float v[4];
+        fin4_value(v, fq, a, b, qrow, a.qn != nullptr, true, qj);
+        if (QPK == 8 || qh < QPK) {                 // whole 32-lane segments
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                // split for the matrix cores: hi = bf16(q), lo = bf16(q - hi)
+                const uint32_t hi = f32_to_bf16_rne(v[e]);
+                qs[qh][0][4 * qj + e] = (uint16_t)hi;
+                qs[qh][1][4 * qj + e] = (uint16_t)f32_to_bf16_rne(__fsub_rn(v[e], __uint_as_float(hi << 16)));
+            }
+        }
+        if (kvw) kv_store(fkv, a, b, kh, pos, lane, (gptr<uint16_t>)kc, (gptr<uint16_t>)vc, kvn);
+    }
+    __syncthreads();
+    // the query columns (head n % 8, zero for heads >= QPK; the hi half of
+    // the split for n < 8, the lo half above)
+    const int hq = n & 7;
+    const bool lo_col = n >= 8;
+    uint4 qr[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++)
+        qr[kk] = hq < QPK ? *(const uint4*)&qs[hq < QPK ? hq : 0][lo_col ? 1 : 0][8 * g + 32 * kk]
+                          : make_uint4(0u, 0u, 0u, 0u);
+    if (own) {
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+            if (tw + 16 * mt + n == pos) {
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) kr[mt][kk] = *(const uint4*)&kvn[0][8 * g + 32 * kk];
+            }
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (tw + 4 * j + g == pos) vr[j] = *(const uint4*)&kvn[1][8 * n];
+    }
+    __syncthreads();                        // red is free from here
     bf16x8 qb[4];
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) qb[kk] = __builtin_bit_cast(bf16x8, qr[kk]);
@@ -605,9 +735,11 @@ k_attn_comb(AttnArgs a, int qpk, float* __restrict__ att) {
 
 hipError_t launch_attn(const AttnArgs& a, int qpk, float* att, hipStream_t st) {
     if (a.B == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_qkv_fin, dim3((unsigned)(a.H + 2 * a.KH), (unsigned)a.B), dim3(128), 0, st, a);
-    hipError_t e0 = hipGetLastError();
-    if (e0 != hipSuccess) return e0;
+    if (!a.append) {
+        hipLaunchKernelGGL(k_kv_append, dim3((unsigned)a.KH, (unsigned)a.B), dim3(64), 0, st, a);
+        hipError_t e0 = hipGetLastError();
+        if (e0 != hipSuccess) return e0;
+    }
     const dim3 grid((unsigned)a.S, (unsigned)a.KH, (unsigned)a.B);
     switch (qpk) {
         case 1: hipLaunchKernelGGL(k_attn_part<1>, grid, dim3(256), 0, st, a); break;

@@ -1,11 +1,13 @@
 // Batch decode over all layers: decode_layers_batch(cfg, W, kv, positions,
 // xin, B, logits) (decode_kernel.c:1518-1556) on the GPU, with the MoE block
-// of each layer from the store.  Per layer, five launches around the MoE
+// of each layer from the store.  Per layer, four launches around the MoE
 // block's own:
 //
 //   qkv      = [Wq; Wk; Wv] . (h * norm1 w), per column slice  k_gemv_part
 //   partials = RMSNorm row scale + bias, QK-norm, RoPE, KV append,
 //              attention over 128-position splits of the cache  k_attn_part
+//              (a prefill chunk, whose positions share one cache: the KV
+//              append first, by a launch of its own         k_kv_append)
 //   att      = the splits merged                               k_attn_comb
 //   opart    = Wo . att, per column slice                      k_gemv_part
 //   h2 = h + sum(opart); h = h2 + MoE(RMSNorm2(h2))   the sum and the norm
@@ -67,12 +69,11 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
         (size_t)B * S * hq * 4,                   // part_o: H heads x hd per split
         (size_t)B * S * (hq / HD) * 2 * 4,        // part_ml
         (size_t)B * hq * 4,                       // att
-        (size_t)B * hq * 2 * 2,                   // qsplit
         (size_t)B * d * 4,                        // hid
         (size_t)B * d * 4,                        // xemb: embedded prompt tokens (prefill)
         (size_t)jm::lm_blocks(V) * B * 4,         // lmv
         (size_t)jm::lm_blocks(V) * B * 4,         // lmi
-        (size_t)B * 4,                            // rss: sums of squares of h (projection GEMM)
+        (size_t)(d / 512) * B * 4,                // rss: sums of squares of h per qkv slice
         s->tab_cap,                               // KV pointers + positions
     };
     size_t total = 0;
@@ -83,7 +84,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     JM_HIP(hipMalloc(&s->dws, total), "hipMalloc decode workspace");
     char* p = (char*)s->dws;
     void** slots[] = {(void**)&s->h, (void**)&s->h2, (void**)&s->qkv, (void**)&s->opart, (void**)&s->part_o,
-                      (void**)&s->part_ml, (void**)&s->att, (void**)&s->qsplit, (void**)&s->hid, (void**)&s->xemb, (void**)&s->lmv,
+                      (void**)&s->part_ml, (void**)&s->att, (void**)&s->hid, (void**)&s->xemb, (void**)&s->lmv,
                       (void**)&s->lmi, (void**)&s->rss, (void**)&s->tab};
     for (size_t i = 0; i < sizeof sz / sizeof sz[0]; i++) {
         *slots[i] = p;
@@ -122,9 +123,11 @@ int check_decode_args(const jm_store* s, const jm_kernel_cfg* c, const jm_kernel
     if (W->w1 || W->w2 || W->w3) return fail(JM_ERR_ARG, "dense FFN layers (w1/w2/w3) are not supported: the FFN is the store's MoE");
     const void* al[] = {W->final_norm, W->norm1, W->norm2, W->wq, W->wk, W->wv, W->wo, W->cos, W->sin,
                         c->qk_norm_type == 1 ? (const void*)W->qn : nullptr,
-                        c->qk_norm_type == 1 ? (const void*)W->kn : nullptr};
+                        c->qk_norm_type == 1 ? (const void*)W->kn : nullptr,
+                        c->bias_qkv ? (const void*)W->bq : nullptr, c->bias_qkv ? (const void*)W->bk : nullptr,
+                        c->bias_qkv ? (const void*)W->bv : nullptr};
     for (const void* p : al)
-        if (p && !aligned(p, 16)) return fail(JM_ERR_ARG, "weight tensors must be 16-byte aligned");
+        if (p && !aligned(p, 16)) return fail(JM_ERR_ARG, "weight and bias tensors must be 16-byte aligned");
     return 0;
 }
 
@@ -134,7 +137,8 @@ int run_layers(const jm_store* s, int L) { return s->max_layers < 0 ? L : std::m
 
 // Every launch of one decode step on st (after the staging copy).
 int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const float* xin, int B,
-                 float* hidden, float* logits, int* out_tok, int S, int qpk, bool capturing, hipStream_t st) {
+                 float* hidden, float* logits, int* out_tok, int S, int qpk, bool append, bool capturing,
+                 hipStream_t st) {
     const int L = c->L, d = c->d, H = c->n_heads, KH = c->n_kv;
     const int nl = run_layers(s, L);
     const int nqkv = (H + 2 * KH) * HD;
@@ -155,15 +159,15 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         g.rows[0] = H * HD; g.rows[1] = KH * HD; g.rows[2] = KH * HD;
         g.K = d; g.N = nqkv; g.B = B;
         g.part = s->qkv;
-        // a prefill chunk takes the GEMM: one slice instead of d / 512, and
-        // the sums of squares of h for the RMSNorm scale
+        // a prefill chunk takes the GEMM: one slice instead of d / 512; both
+        // also give the sums of squares of h per slice for the RMSNorm scale
         const bool gq = B >= JM_GEMM_MIN_B && jm::gemm_shape_ok(g);
-        g.rss = gq ? s->rss : nullptr;
+        g.rss = s->rss;
         if (gq) JM_HIP(jm::launch_gemm_bf16(g, st), "qkv GEMM launch");
         else JM_HIP(jm::launch_gemv_part(g, st), "qkv launch");
 
         jm::AttnArgs at{};
-        at.qkv = s->qkv; at.nslice = gq ? 1 : d / jm::gemv_slice_cols(d); at.h = s->h; at.d = d;
+        at.qkv = s->qkv; at.nslice = gq ? 1 : d / jm::gemv_slice_cols(d); at.d = d;
         at.rss = g.rss;
         if (c->bias_qkv) {
             at.bq = W->bq + (size_t)l * H * HD;
@@ -176,7 +180,8 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         at.eps = c->eps; at.sdiv = sdiv;
         at.cos = W->cos; at.sin = W->sin;
         at.pos = pos_dev; at.kv = s->tab; at.L = L; at.layer = l;
-        at.qsplit = s->qsplit; at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;
+        at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;
+        at.append = append ? 1 : 0;
         // the grid covers the longest token's splits; the buffers hold S_cap
         // per (token, KV head), indexed with the call's S
         JM_HIP(jm::launch_attn(at, qpk, s->att, st), "attention launch");
@@ -247,6 +252,25 @@ void decode_free_all(jm_store* s) {
 
 namespace {
 
+// True when the n pointers are pairwise different (open addressing over a
+// power-of-two table at most half full; pointers are nonzero).
+bool cache_pointers_distinct(const unsigned long long* p, size_t n) {
+    thread_local std::vector<unsigned long long> set;
+    size_t cap = 16;
+    while (cap < 2 * n) cap <<= 1;
+    set.assign(cap, 0ull);
+    for (size_t i = 0; i < n; i++) {
+        const unsigned long long v = p[i];
+        size_t h = (size_t)((v >> 4) * 0x9E3779B97F4A7C15ull >> 20) & (cap - 1);
+        while (set[h]) {
+            if (set[h] == v) return false;
+            h = (h + 1) & (cap - 1);
+        }
+        set[h] = v;
+    }
+    return true;
+}
+
 int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const jm_kv_cache* kv,
                 const int32_t* positions, const float* xin, int B, float* logits, int32_t* out_tok,
                 float* hidden, void* stream, bool allow_graph = true) {
@@ -289,6 +313,12 @@ int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const
         s->tab_host[2 * i] = (unsigned long long)(uintptr_t)kv[i].k;
         s->tab_host[2 * i + 1] = (unsigned long long)(uintptr_t)kv[i].v;
     }
+    // The attention kernel may append each token's k and v rows itself
+    // (inside the launch that reads the caches) only when no cache is shared
+    // by two tokens: a prompt's positions run as one batch over one cache
+    // (jm_prefill_layers), and there every row is appended by a launch of
+    // its own first.  Checked over every k and v pointer of the call.
+    const bool append = cache_pointers_distinct(s->tab_host, (size_t)2 * B * L);
     int* pos_host = (int*)(s->tab_host + (size_t)2 * B * L);
     memcpy(pos_host, positions, (size_t)B * 4);
     const size_t tab_bytes = (size_t)B * L * 16 + (size_t)B * 4;
@@ -323,6 +353,7 @@ int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const
         key.trace = s->trace; key.trace_bytes = s->trace_bytes; key.ws = s->ws; key.dws = s->dws;
         key.wt = s->wt; key.wt_bf16 = s->wt_bf16; key.lm_V = s->lm_V; key.nl = run_layers(s, c->L);
         key.dense_min = s->dense_min;
+        key.append = append ? 1 : 0;
         if (!s->gexec || memcmp(&key, &s->gkey, sizeof key) != 0) {
             if (s->gexec) {
                 JM_HIP(hipStreamSynchronize(st), "hipStreamSynchronize before recapture");
@@ -331,7 +362,7 @@ int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const
             }
             if (!s->cap_st) JM_HIP(hipStreamCreateWithFlags(&s->cap_st, hipStreamNonBlocking), "hipStreamCreate");
             JM_HIP(hipStreamBeginCapture(s->cap_st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-            const int rc = enqueue_step(s, c, W, xin, B, hidden, logits, out_tok, S, qpk, true, s->cap_st);
+            const int rc = enqueue_step(s, c, W, xin, B, hidden, logits, out_tok, S, qpk, append, true, s->cap_st);
             hipGraph_t graph = nullptr;
             const hipError_t ec = hipStreamEndCapture(s->cap_st, &graph);
             if (rc) {
@@ -350,7 +381,7 @@ int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const
         JM_HIP(hipGraphLaunch(s->gexec, st), "hipGraphLaunch");
         return 0;
     }
-    return enqueue_step(s, c, W, xin, B, hidden, logits, out_tok, S, qpk, false, st);
+    return enqueue_step(s, c, W, xin, B, hidden, logits, out_tok, S, qpk, append, false, st);
 }
 
 }  // namespace

@@ -161,7 +161,8 @@ struct GemvArgs {
     int rows[3];
     int K, N, B;              // N = rows[0] + rows[1] + rows[2]
     float* part;              // [K / gemv_slice_cols(K)][B][N]
-    float* rss;               // GEMM only: [B] receives sum x[b][k]^2 over all k (NULL: not wanted)
+    float* rss;               // [slices][B] receives the sums of x[b][k]^2 over each slice's columns
+                              // (the GEMM: one slice of all K), or NULL: not wanted
 };
 // K a multiple of 1024 (at most 8192); slices of 512 columns, 1024 from K = 4096
 bool gemv_shape_ok(int K);
@@ -180,9 +181,8 @@ struct AttnArgs {
     const float* qkv;         // [nslice][B][nqkv] slices of the projections of h * norm1 weight:
                               // H q heads, KH k heads, KH v heads
     int nslice;
-    const float* h;           // [B][d] the layer input (its RMSNorm row scale)
-    int d;
-    const float* rss;         // [B] sum of h^2 over d when the projection computed it (NULL: from h)
+    int d;                    // width of the layer input h
+    const float* rss;         // [nslice][B] sums of h^2 over the slices' columns (the RMSNorm row scale)
     const float* bq;          // [H*128] / [KH*128] biases of the layer, or NULL
     const float* bk;
     const float* bv;
@@ -196,7 +196,8 @@ struct AttnArgs {
     const int* pos;           // [B] position each token writes (T = pos + 1)
     const unsigned long long* kv;   // [B*L][2] bf16 k, v caches [maxT][KH][128]
     int L, layer;
-    uint16_t* qsplit;         // [B][H][2][128] bf16 the finished query heads: hi = bf16(q), lo = bf16(q - hi)
+    int append;               // 1: every token has its own cache; the attention appends its k and v
+                              // rows itself.  0: k_kv_append appends every row first
     int S;                    // splits the partial buffers hold per (token, KV head)
     float* part_o;            // [B][KH][S][H/KH][128]
     float* part_ml;           // [B][KH][S][H/KH][2]

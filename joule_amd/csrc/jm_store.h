@@ -62,6 +62,7 @@ struct DecKey {
     int lm_V;
     int nl;                     // layers the step runs (jm_store_set_max_layers)
     int dense_min;
+    int append;                 // the attention appends the k and v rows itself (no cache shared by two tokens)
 };
 
 struct jm_store {
@@ -99,7 +100,6 @@ struct jm_store {
     float* part_o;              // [B][KH][S][H/KH][hd] attention partials per position split
     float* part_ml;             // [B][KH][S][H/KH][2] their (max, sum)
     float* att;                 // [B][H hd] attention output
-    uint16_t* qsplit;           // [B][H][2][hd] finished query heads, bf16 hi and lo
     float* hid;                 // [B][d] final-normed hidden state (when the caller passes none)
     float* xemb;                // [B][d] embedded prompt tokens (jm_prefill_layers)
     float* lmv;                 // [lm blocks][B] per-block best logit (argmax)
