@@ -60,31 +60,44 @@ k_gemv_part(GemvArgs a) {
     else if (row < a.rows[0] + a.rows[1]) wr = a.w[1] + (size_t)(row - a.rows[0]) * a.K;
     else wr = a.w[2] + (size_t)(row - a.rows[0] - a.rows[1]) * a.K;
     const uint16_t* wp = wr + k0 + 8 * g;
+    // requests first: the tokens' slice (needed first; thread tid serves
+    // token tb0 + tid % 8 throughout), then the weight rows
+    constexpr int XI = NK * 32 / (WV * 64);        // staging items per thread
+    static_assert(NK * 32 % (WV * 64) == 0 && (WV * 64) % 8 == 0, "whole staging items, token fixed");
+    const int tx = tid & 7;
+    const bool tin = tb0 + tx < a.B;
+    float4 xv[XI][2];
+    uint4 nwv[XI];
+#pragma unroll
+    for (int it = 0; it < XI; it++) {
+        const int i = tid + it * WV * 64;
+        const int c = k0 + 32 * (i >> 5) + 8 * ((i >> 3) & 3);
+        const float4* xp = (const float4*)(a.x + (size_t)(tin ? tb0 + tx : tb0) * a.K + c);
+        xv[it][0] = xp[0];
+        xv[it][1] = xp[1];
+        if (a.norm_w) nwv[it] = *(const uint4*)(a.norm_w + c);
+    }
     uint4 wa[NK];
 #pragma unroll
     for (int ks = 0; ks < NK; ks++) wa[ks] = *(const uint4*)(wp + 32 * ks);
+    __builtin_amdgcn_sched_barrier(0);             // keep every request ahead of the staging
     // the tokens' slice (times the norm weight), split into hi and lo
     // columns; with a.rss the first row group's blocks also sum the squares
-    // of the slice (before the norm weight) per token: thread tid serves
-    // token tb0 + tid % 8 throughout
-    static_assert((WV * 64) % 8 == 0, "token of a thread fixed over the loop");
+    // of the slice (before the norm weight) per token
     __shared__ float ssw[WV][8];
     const bool want_ss = a.rss && blockIdx.x == 0;    // block-uniform
     float ss = 0.0f;
-    for (int i = tid; i < NK * 32; i += WV * 64) {
-        const int ks = i >> 5, gg = (i >> 3) & 3, t = i & 7;
-        const int c = k0 + 32 * ks + 8 * gg;
-        float v[8];
-        if (tb0 + t < a.B) {
-            const float4* xp = (const float4*)(a.x + (size_t)(tb0 + t) * a.K + c);
-            const float4 x0 = xp[0], x1 = xp[1];
-            v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-            v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+#pragma unroll
+    for (int it = 0; it < XI; it++) {
+        const int i = tid + it * WV * 64;
+        const int ks = i >> 5, gg = (i >> 3) & 3;
+        float v[8] = {xv[it][0].x, xv[it][0].y, xv[it][0].z, xv[it][0].w,
+                      xv[it][1].x, xv[it][1].y, xv[it][1].z, xv[it][1].w};
+        if (tin) {
 #pragma unroll
             for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[e], v[e], ss);
             if (a.norm_w) {
-                const uint4 nw = *(const uint4*)(a.norm_w + c);
-                const uint32_t nn[4] = {nw.x, nw.y, nw.z, nw.w};
+                const uint32_t nn[4] = {nwv[it].x, nwv[it].y, nwv[it].z, nwv[it].w};
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     v[2 * e] = __fmul_rn(v[2 * e], bf16_bits_to_f32(nn[e] & 0xFFFFu));
@@ -98,8 +111,8 @@ k_gemv_part(GemvArgs a) {
         uint32_t hi[4], lo[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) split_bf16x2(v[2 * e], v[2 * e + 1], hi[e], lo[e]);
-        xb[ks][16 * gg + t] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        xb[ks][16 * gg + 8 + t] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        xb[ks][16 * gg + tx] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        xb[ks][16 * gg + 8 + tx] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
     }
     if (want_ss) {
         // lanes with equal lane % 8 serve one token
