@@ -474,6 +474,48 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
     return res
 
 
+def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 32, 33, 36, 512), reps=200):
+    """The plugin product HipBackend.q4_gemm (jm_q4_gemm_f32, the reference's
+    q4_gemm_f32) on one Qwen3 expert matrix shape (m=768 rows of d=2048),
+    at each token count: microseconds per call on the stream (inputs and the
+    packed matrix resident on the GPU; the workspace is cached after the
+    first call) and algorithmic bytes per call.  From 33 tokens the call
+    takes the matrix cores (int8 digit pairs); below, the v_dot8 digit
+    kernel."""
+    import numpy as np
+    import torch
+
+    from joule_amd import q4_store as q4
+    from joule_amd.backend import HipBackend
+
+    rng = np.random.default_rng(7)
+    sb, pb = q4.quantize(rng.normal(0, 0.02, (m, d)).astype(np.float32), group)
+    sc = torch.from_numpy(np.frombuffer(sb, np.uint16).copy().view(np.int16)).cuda()
+    pk = torch.from_numpy(np.frombuffer(pb, np.uint8).copy()).cuda()
+    be = HipBackend()
+    st = torch.cuda.current_stream()
+    out = {}
+    for T in sizes:
+        X = torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).cuda()
+        y = torch.empty((T, m), dtype=torch.float32, device="cuda")
+        for _ in range(5):
+            be.q4_gemm(y, X, pk, sc, m, d, group)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(reps):
+            be.q4_gemm(y, X, pk, sc, m, d, group)
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = m * d // 2 + m * (d // group) * 2 + T * d * 4 + T * m * 4
+        out[f"T{T}"] = {"us_per_call": us, "bytes": nbytes, "GBs": nbytes / (us * 1e-6) / 1e9,
+                        "path": "mfma_i8" if T >= 33 else "dot8_digits",
+                        "tflops_equiv": 2.0 * T * m * d / (us * 1e-6) / 1e12}
+        log(f"plugin q4_gemm m={m} d={d} T={T}: {us:.1f} us ({out[f'T{T}']['path']})")
+    return {"m": m, "d": d, "group": group, "sizes": out}
+
+
 def prefill_only(group, reps, n_layers=48, maxT=2176, Tp=512):
     """Only the 512-token prefill of decode_step's model (for kernel
     profiles): one warm-up pass, then `reps` timed passes of
@@ -567,6 +609,8 @@ def main() -> int:
                     help="only the 48-layer 512-token prefill (--steps timed passes); prints its JSON")
     ap.add_argument("--zipf-only", action="store_true",
                     help="only the 512-token Zipf-routed block (MFMA branch) on the 16-layer store; prints its JSON")
+    ap.add_argument("--plugin-only", action="store_true",
+                    help="only the plugin product HipBackend.q4_gemm at T = 1, 32, 33, 36, 512; prints its JSON")
     ap.add_argument("--probe", action="store_true",
                     help="only the launch and hand-off cost probes (libjoule_probe.so); prints their JSON")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -600,6 +644,9 @@ def main() -> int:
     if args.prefill_only:
         r = prefill_only(args.group, args.steps)
         print(json.dumps({"prefill_512": r}), flush=True)
+        return 0
+    if args.plugin_only:
+        print(json.dumps({"plugin_q4_gemm": plugin_q4_gemm(args.group)}), flush=True)
         return 0
     shape, G, B, NL = QWEN3, args.group, args.batch, args.layers
     log(f"building {NL} Qwen3-shaped layers (G={G}) on the GPU")
@@ -687,6 +734,7 @@ def main() -> int:
         del ostore
         torch.cuda.empty_cache()
         sweep["qwen3_decode48_B8"] = decode_step(8, max(args.steps // 20, 10), 3, G)
+        sweep["plugin_q4_gemm"] = plugin_q4_gemm(G)
 
     if cpu is not None:
         cpu["sweep"] = cpu_sweep

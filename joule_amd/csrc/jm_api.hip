@@ -35,6 +35,65 @@ int hip_fail(hipError_t e, const char* what) {
 
 }  // namespace jm
 
+namespace {
+
+// Workspace of the plugin products (jm_q4_gemm_f32 / jm_q4_gemv_f32): one
+// buffer per (device, stream), grown on demand and kept until the process
+// ends.  Calls on one stream run in order, so they share it; a growth waits
+// for the stream before freeing the smaller buffer.  Under stream capture a
+// call whose buffer is too small takes a stream-ordered allocation instead
+// (freed after the call), since a capture cannot synchronise.
+struct PluginWs {
+    void* p = nullptr;
+    bool async = false;
+};
+
+struct PluginBuf {
+    int dev;
+    hipStream_t st;
+    void* p;
+    size_t bytes;
+};
+
+std::mutex g_pws_mu;
+std::vector<PluginBuf> g_pws;
+
+int plugin_ws(hipStream_t st, size_t bytes, PluginWs* out) {
+    int dev = 0;
+    JM_HIP(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_pws_mu);
+    PluginBuf* b = nullptr;
+    for (auto& x : g_pws)
+        if (x.dev == dev && x.st == st) b = &x;
+    if (b && b->bytes >= bytes) {
+        out->p = b->p;
+        return 0;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    JM_HIP(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone) {
+        JM_HIP(hipMallocAsync(&out->p, bytes, st), "hipMallocAsync plugin workspace");
+        out->async = true;
+        return 0;
+    }
+    if (b) {
+        JM_HIP(hipStreamSynchronize(st), "hipStreamSynchronize before plugin workspace growth");
+        JM_HIP(hipFree(b->p), "hipFree plugin workspace");
+        b->p = nullptr;
+        b->bytes = 0;
+    } else {
+        g_pws.push_back(PluginBuf{dev, st, nullptr, 0});
+        b = &g_pws.back();
+    }
+    const size_t grow = std::max(bytes, (size_t)1 << 20);
+    JM_HIP(hipMalloc(&b->p, grow), "hipMalloc plugin workspace");
+    b->bytes = grow;
+    out->p = b->p;
+    return 0;
+}
+
+}  // namespace
+
 // Workspace of jm_layer_ffn_batch_noalloc: one fixed array on each device
 // the library runs on, held until the process ends.  Host code never uses
 // the array's name as an address: jm_store_create resolves the device
@@ -595,16 +654,24 @@ int jm_q4_gemm_f32(float* out, const float* X, int T, const uint8_t* packed, con
     if (!aligned(packed, 16) || !aligned(X, 16)) return fail(JM_ERR_ARG, "packed and X must be 16-byte aligned");
     if (T == 0 || m == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
+    // from JM_GEMM_MIN_B tokens on the matrix cores (int8 digit pairs of X)
+    const bool mfma = T >= JM_GEMM_MIN_B && jm::q4_gemm_mfma_ok(m, d, group) && aligned(scales, 16);
     const size_t ng = (size_t)d / group;
     const size_t dig_bytes = align256((size_t)T * ng * JM_NDIG * (group / 8) * 4);
     const size_t sc_bytes = align256((size_t)T * ng * 4);
-    void* scratch = nullptr;
-    JM_HIP(hipMallocAsync(&scratch, dig_bytes + sc_bytes, st), "hipMallocAsync q4_gemm scratch");
-    uint32_t* dig = (uint32_t*)scratch;
-    float* dsc = (float*)((char*)scratch + dig_bytes);
-    hipError_t e = jm::launch_prep_digits(X, d, T, d, group, dig, dsc, st);
-    if (e == hipSuccess) e = jm::launch_q4_rows(packed, scales, m, d, group, dig, dsc, T, out, m, st);
-    hipError_t f = hipFreeAsync(scratch, st);
+    const size_t need = mfma ? jm::q4_gemm_mfma_ws(T, d, group) : dig_bytes + sc_bytes;
+    PluginWs ws;
+    if (int rc = plugin_ws(st, need, &ws)) return rc;
+    hipError_t e;
+    if (mfma) {
+        e = jm::launch_q4_gemm_mfma(packed, scales, X, T, m, d, group, ws.p, out, st);
+    } else {
+        uint32_t* dig = (uint32_t*)ws.p;
+        float* dsc = (float*)((char*)ws.p + dig_bytes);
+        e = jm::launch_prep_digits(X, d, T, d, group, dig, dsc, st);
+        if (e == hipSuccess) e = jm::launch_q4_rows(packed, scales, m, d, group, dig, dsc, T, out, m, st);
+    }
+    const hipError_t f = ws.async ? hipFreeAsync(ws.p, st) : hipSuccess;
     if (e != hipSuccess) return hip_fail(e, "q4_gemm launch");
     if (f != hipSuccess) return hip_fail(f, "hipFreeAsync");
     return 0;

@@ -146,6 +146,14 @@ hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st);
 bool mfma_shape_ok(int d, int m);
 hipError_t launch_gateup_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st);
 hipError_t launch_down_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st);
+// The plain Q4 product out[T][m] = X . dequant(W)^T on the matrix cores:
+// m a multiple of 256, d as the MFMA contraction, group 32 or 64 with each
+// row's scales a multiple of 16 (G = 32) or 8 bytes (G = 64); ws holds
+// q4_gemm_mfma_ws bytes
+bool q4_gemm_mfma_ok(int m, int d, int group);
+size_t q4_gemm_mfma_ws(int T, int d, int group);
+hipError_t launch_q4_gemm_mfma(const uint8_t* packed, const uint16_t* scales, const float* X, int T, int m, int d,
+                               int group, void* ws, float* out, hipStream_t st);
 // out[b] = (resid[b] +) sum of the token's slots of y in the order comb gives
 hipError_t launch_combine(const float* y, const int* comb, int B, int k, int d, const float* resid,
                           float* out, hipStream_t st);

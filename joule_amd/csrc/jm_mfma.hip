@@ -493,6 +493,76 @@ k_down_mfma(ExpertArgs a) {
     }
 }
 
+// ------------------------------------------------------ plain Q4 product
+
+// out[t][row] = X[t] . dequant(W[row]) for one Q4 matrix (the plugin
+// product q4_gemm_f32, expert_ffn.c:200-215, at prefill-sized T): block
+// (32-token tile, npass x 256 rows), 8 waves x 32 rows per pass over the
+// tile's staged digits, as the down kernel without routing.  The digits of X
+// come from k_prep_i8.
+template <int G>
+__global__ void __launch_bounds__(MTHREADS, 1)
+k_q4_gemm_mfma(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scales,
+               const int8_t* __restrict__ xqh, const int8_t* __restrict__ xql, const float* __restrict__ xqs,
+               int T, int m, int d, int npass, float* __restrict__ out) {
+    extern __shared__ __align__(16) unsigned char sm[];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int ng = d / G;
+    const Lay ly(d, G);
+    const int t0 = blockIdx.x * MT;
+    const int nt = min(MT, T - t0);
+    int8_t* q = (int8_t*)sm;
+    float* s = (float*)(sm + ly.s);
+    int* tok = (int*)(sm + ly.tok);
+    uint8_t* wl = sm + ly.w + (size_t)w * 2 * WBUF;
+    if (tid < MT) tok[tid] = t0 + (tid < nt ? tid : 0);   // padding: the tile's first token
+    const int n = lane & 31, h = lane >> 5;
+    WStream<G> ws;
+    ws.rowb = d / 2;
+    ws.nss = d / SSC;
+    auto start = [&](int pass) __attribute__((always_inline)) {
+        const int wrow0 = (blockIdx.y * npass + pass) * DN_ROWS + 32 * w;
+        ws.wbase = packed + (size_t)wrow0 * (d / 2);
+        ws.srow = (const uint8_t*)scales + (size_t)(wrow0 + n) * ng * 2;
+        ws.load(0, 0);
+        ws.load(1, 1);
+        return wrow0 + n;
+    };
+    int row = start(0);
+    __syncthreads();
+    stage_phase(xqh, xql, tok, d, 0, ly.kph, q);
+    stage_scales(xqs, tok, nt, ng, s);
+    __syncthreads();
+#pragma unroll 1
+    for (int pass = 0; pass < npass; pass++) {
+        floatx16 acc = {};
+        wave_product<G>(acc, ws, wl, q, s, TokSrc{xqh, xql, tok, d}, ly);
+        const int r = row;
+        if (pass + 1 < npass) row = start(pass + 1);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int i = 8 * (v / 4) + 4 * h + (v % 4);
+            if (i < nt) out[(size_t)(t0 + i) * m + r] = acc[v];
+        }
+    }
+}
+
+// Int8 digit pairs and scales of T rows of d floats, one G-lane segment per
+// Q4 group (the encoding of the block's router kernels).
+template <int G>
+__global__ void __launch_bounds__(256)
+k_prep_i8(const float* __restrict__ X, int T, int d, int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+          float* __restrict__ sc) {
+    const long long seg = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / G;
+    const int ng = d / G;
+    const bool ok = seg < (long long)T * ng;
+    const long long sg = ok ? seg : 0;
+    const int t = (int)(sg / ng), g = (int)(sg % ng);
+    const size_t o = (size_t)t * d + (size_t)g * G;
+    const float v = ok ? X[o + (threadIdx.x & (G - 1))] : 0.0f;
+    encode_i8_group_wave<G>(v, ok, hi + o, lo + o, sc + (size_t)t * ng + g);
+}
+
 // Contractions the kernels take: multiples of the weight super-stage, and
 // one token phase or whole phases; row counts of whole blocks.
 static bool mfma_k_ok(int K) { return K % SSC == 0 && K <= KMAX && (K <= KPH_MAX || K % KPH_MAX == 0); }
@@ -520,9 +590,10 @@ hipError_t allow_lds() {
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= MAX_DEV) return hipErrorInvalidDevice;
     if (g_lds_set[dev].load(std::memory_order_acquire)) return hipSuccess;
-    const struct { const void* f; size_t b; } k[4] = {
+    const struct { const void* f; size_t b; } k[6] = {
         {(const void*)k_gateup_mfma<64>, gateup_lds<64>(KMAX)}, {(const void*)k_gateup_mfma<32>, gateup_lds<32>(KMAX)},
-        {(const void*)k_down_mfma<64>, Lay(KMAX, 64).total}, {(const void*)k_down_mfma<32>, Lay(KMAX, 32).total}};
+        {(const void*)k_down_mfma<64>, Lay(KMAX, 64).total}, {(const void*)k_down_mfma<32>, Lay(KMAX, 32).total},
+        {(const void*)k_q4_gemm_mfma<64>, Lay(KMAX, 64).total}, {(const void*)k_q4_gemm_mfma<32>, Lay(KMAX, 32).total}};
     for (const auto& x : k) {
         e = hipFuncSetAttribute(x.f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)x.b);
         if (e != hipSuccess) return e;
@@ -552,6 +623,46 @@ hipError_t launch_down_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st) 
     const dim3 grid((unsigned)max_tiles, (unsigned)(a.d / DN_BLOCK_ROWS));
     if (a.group == 64) hipLaunchKernelGGL(k_down_mfma<64>, grid, dim3(MTHREADS), Lay(a.m, 64).total, st, a);
     else hipLaunchKernelGGL(k_down_mfma<32>, grid, dim3(MTHREADS), Lay(a.m, 32).total, st, a);
+    return hipGetLastError();
+}
+
+static size_t pad256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+bool q4_gemm_mfma_ok(int m, int d, int group) {
+    // whole 256-row passes; each row's scales of a super-stage in one
+    // aligned 8-byte (G = 64) or 16-byte (G = 32) load
+    return m % DN_ROWS == 0 && mfma_k_ok(d) && (group == 64 || group == 32) &&
+           ((d / group) * 2) % (group == 64 ? 8 : 16) == 0;
+}
+
+size_t q4_gemm_mfma_ws(int T, int d, int group) {
+    return pad256((size_t)T * d) * 2 + pad256((size_t)T * (d / group) * 4);
+}
+
+hipError_t launch_q4_gemm_mfma(const uint8_t* packed, const uint16_t* scales, const float* X, int T, int m, int d,
+                               int group, void* ws, float* out, hipStream_t st) {
+    if (T == 0 || m == 0) return hipSuccess;
+    if (!q4_gemm_mfma_ok(m, d, group)) return hipErrorInvalidValue;
+    hipError_t e = allow_lds();
+    if (e != hipSuccess) return e;
+    int8_t* hi = (int8_t*)ws;
+    int8_t* lo = hi + pad256((size_t)T * d);
+    float* sc = (float*)(lo + pad256((size_t)T * d));
+    const long long lanes = (long long)T * d;
+    const unsigned pblocks = (unsigned)((lanes + 255) / 256);
+    // two passes per block when the rows allow and the grid still fills the chip
+    const int tiles = (T + MT - 1) / MT;
+    const int npass = (m % (2 * DN_ROWS) == 0 && (long long)tiles * (m / (2 * DN_ROWS)) >= 256) ? 2 : 1;
+    const dim3 grid((unsigned)tiles, (unsigned)(m / (DN_ROWS * npass)));
+    if (group == 64) {
+        hipLaunchKernelGGL(k_prep_i8<64>, dim3(pblocks), dim3(256), 0, st, X, T, d, hi, lo, sc);
+        hipLaunchKernelGGL(k_q4_gemm_mfma<64>, grid, dim3(MTHREADS), Lay(d, 64).total, st, packed, scales, hi, lo, sc,
+                           T, m, d, npass, out);
+    } else {
+        hipLaunchKernelGGL(k_prep_i8<32>, dim3(pblocks), dim3(256), 0, st, X, T, d, hi, lo, sc);
+        hipLaunchKernelGGL(k_q4_gemm_mfma<32>, grid, dim3(MTHREADS), Lay(d, 32).total, st, packed, scales, hi, lo, sc,
+                           T, m, d, npass, out);
+    }
     return hipGetLastError();
 }
 

@@ -453,7 +453,12 @@ def test_block_empty_and_errors(qwen64):
 # ----------------------------------------------------------------- backend
 
 @pytest.mark.parametrize("group", [64, 32])
-@pytest.mark.parametrize("m,d,T", [(768, 2048, 1), (2048, 768, 3), (1024, 2048, 7)])
+@pytest.mark.parametrize("m,d,T", [(768, 2048, 1), (2048, 768, 3), (1024, 2048, 7),
+                                   # from 33 tokens the matrix cores (m a multiple of 256): whole and
+                                   # partial 32-token tiles, one and two 256-row passes per block
+                                   (768, 2048, 33), (2048, 768, 70), (8192, 512, 512),
+                                   # shapes the matrix-core kernel does not take: the digit kernel
+                                   (1000, 2048, 40), (768, 1536, 36)])
 def test_hip_backend_q4_gemm(gpu, oracle_lib, group, m, d, T):
     banner(f"HipBackend q4_gemm m={m} d={d} T={T} G{group}")
     rng = np.random.default_rng(m + d + T)
