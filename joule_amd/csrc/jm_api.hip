@@ -149,7 +149,7 @@ int check_group_shape(int d, int m, int group) {
 namespace {
 
 // Sizes of the Ws fields for B tokens, in field order.
-constexpr int WS_NF = 24;
+constexpr int WS_NF = 26;
 void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
     const int E = s->E, d = s->d, m = s->m, k = s->topk, G = s->group;
     const size_t nslot = (size_t)B * k;
@@ -181,6 +181,8 @@ void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
         (size_t)B * d,                // xql
         (size_t)B * (d / G) * 4,      // xqs
         nslot * (m / G) * 4,          // aqs
+        (size_t)B * (d / G) * 4,      // xqc
+        nslot * (m / G) * 4,          // aqc
     };
     for (int i = 0; i < WS_NF; i++) sz[i] = v[i];
 }
@@ -204,7 +206,8 @@ void jm::ws_layout(const jm_store* s, int B, char* base, Ws* w) {
                            (void**)&w->comb, (void**)&w->work, (void**)&w->tiles,
                            (void**)&w->n_tiles, (void**)&w->act, (void**)&w->adig,
                            (void**)&w->ascale, (void**)&w->y, (void**)&w->aqh, (void**)&w->aql,
-                           (void**)&w->xqh, (void**)&w->xql, (void**)&w->xqs, (void**)&w->aqs};
+                           (void**)&w->xqh, (void**)&w->xql, (void**)&w->xqs, (void**)&w->aqs,
+                           (void**)&w->xqc, (void**)&w->aqc};
     static_assert(sizeof(Ws) == WS_NF * sizeof(void*), "a size for every workspace field");
     for (int i = 0; i < WS_NF; i++) {
         *slots[i] = base;
@@ -276,9 +279,9 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     r.dense_min = a.dense_min;
     a.tiles = w.tiles; a.n_tiles = w.n_tiles;
     const bool mfma = !dec && a.dense_min <= nslot;
-    r.xqh = mfma ? w.xqh : nullptr; r.xql = w.xql; r.xqs = w.xqs;
-    a.xqh = w.xqh; a.xql = w.xql; a.xqs = w.xqs;
-    a.aqh = w.aqh; a.aql = w.aql; a.aqs = w.aqs;
+    r.xqh = mfma ? w.xqh : nullptr; r.xql = w.xql; r.xqs = w.xqs; r.xqc = w.xqc;
+    a.xqh = w.xqh; a.xql = w.xql; a.xqs = w.xqs; a.xqc = w.xqc;
+    a.aqh = w.aqh; a.aql = w.aql; a.aqs = w.aqs; a.aqc = w.aqc;
     a.logits = w.logits; a.renorm = s->renorm; a.top_w = w.top; a.tw_w = w.tw;
     const int max_tiles = nslot / JM_DENSE_TILE + E;
 #define JM_MARK(i) if (s->prof && stage_marks) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")

@@ -354,11 +354,14 @@ __host__ __device__ constexpr int i8_pos(int u) { return (u & 1) ? 4 + (u >> 1) 
 // Encode one group of G floats, value i held by lane i of an aligned G-lane
 // segment (G = 32 or 64): lane i writes its two digits to hi[p] and lo[p],
 // p = its value's place in the int8 operand order; lane 0 writes the scale
-// (NaN when the group holds a non-finite value, so that it propagates).
-// Only when `store`; every lane of the segment must call this.
+// (NaN when the group holds a non-finite value, so that it propagates) and
+// the sum of the group's integers q = 256 h + l (exact: below 2^24), which
+// the matrix-core kernels fold into their products with unsigned weight
+// nibbles.  Only when `store`; every lane of the segment must call this.
 template <int G>
 __device__ __forceinline__ void encode_i8_group_wave(float v, bool store, int8_t* __restrict__ hi,
-                                                     int8_t* __restrict__ lo, float* __restrict__ scale) {
+                                                     int8_t* __restrict__ lo, float* __restrict__ scale,
+                                                     int* __restrict__ qsum) {
     const int i = threadIdx.x & (G - 1);
     const float a = fabsf(v);
     const int bad = seg_or<G>(!(a <= 3.4028235e38f) ? 1 : 0);
@@ -367,11 +370,15 @@ __device__ __forceinline__ void encode_i8_group_wave(float v, bool store, int8_t
     const int q = (int)rintf(__fmul_rn(v, inv));
     const int l = ((q + 128) & 255) - 128;
     const int h = (q - l) >> 8;
+    const float qs = seg_sum<G>((float)q);
     if (store) {
         const int p = (i & ~7) + i8_pos(i & 7);
         hi[p] = (int8_t)h;
         lo[p] = (int8_t)l;
-        if (i == 0) *scale = bad ? __int_as_float(0x7FC00000) : __fdiv_rn(mx, (float)I8_R);
+        if (i == 0) {
+            *scale = bad ? __int_as_float(0x7FC00000) : __fdiv_rn(mx, (float)I8_R);
+            *qsum = (int)qs;
+        }
     }
 }
 

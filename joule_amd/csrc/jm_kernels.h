@@ -47,6 +47,7 @@ struct ExpertArgs {
     const int8_t* xqh;        // [B][d] tokens as int8 digit pairs (hi, lo) in int8 operand order (MFMA branch)
     const int8_t* xql;
     const float* xqs;         // [B][d/G] their scales
+    const int* xqc;           // [B][d/G] sums of their integers 256 h + l per group
     const uint32_t* xdig;     // [B][d/G][NDIG][G/8] token digits
     const float* xscale;      // [B][d/G]
     float* act;               // [B*k][m]   SiLU(gate)*up per slot
@@ -63,6 +64,7 @@ struct ExpertArgs {
     int8_t* aqh;              // [B*k][m] act as int8 digit pairs for the MFMA down
     int8_t* aql;
     float* aqs;               // [B*k][m/G] their scales
+    int* aqc;                 // [B*k][m/G] sums of their integers per group
     // decode path with the top-k in the gate/up kernel (gateup_topk): the
     // router scores, and where the table is written
     const float* logits;      // [B][E]
@@ -89,6 +91,7 @@ struct RouteArgs {
     int8_t* xqh;              // [B][d] tokens as int8 digit pairs for the MFMA branch (NULL: not needed)
     int8_t* xql;
     float* xqs;               // [B][d/G] their scales
+    int* xqc;                 // [B][d/G] sums of their integers per group
     int* top;                 // [B*k]
     float* tw;                // [B*k]
     int* seg_off;             // [E+1]

@@ -41,6 +41,7 @@
 namespace jm {
 
 typedef int int4v __attribute__((ext_vector_type(4)));
+typedef int int8v __attribute__((ext_vector_type(8)));
 typedef int int16v __attribute__((ext_vector_type(16)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
@@ -58,19 +59,13 @@ constexpr int SSC = 256;            // columns of a weight super-stage: 128 byte
 constexpr int WRS = 144;            // LDS bytes per row of a wave's weight buffer (128 + bank spread)
 constexpr int WBUF = 32 * WRS;      // one super-stage of a wave's 32 rows
 
-// One dword of 8 packed nibbles (value i in bits 4i..4i+3) as two dwords of
-// int8 q - 8 in i8_pos order: values 0 2 4 6, then 1 3 5 7.  For a byte b in
-// 0..15, (b + 0x78) ^ 0x80 is b - 8 as a signed byte; no carry leaves a byte.
-__device__ __forceinline__ void nib_to_i8(uint32_t w, int& lo, int& hi) {
-    lo = (int)(((w & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
-    hi = (int)((((w >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
-}
-
+// Two dwords of 8 packed nibbles each (value i in bits 4i..4i+3) as four
+// dwords of unsigned int8 q in i8_pos order: of each dword, values 0 2 4 6,
+// then 1 3 5 7.  The products take q, not q - 8: the lo plane's accumulator
+// starts at -8 times the tokens' group sums, which carries the -8.
 __device__ __forceinline__ int4v wdigits(uint32_t w0, uint32_t w1) {
-    int a0, a1, a2, a3;
-    nib_to_i8(w0, a0, a1);
-    nib_to_i8(w1, a2, a3);
-    return int4v{a0, a1, a2, a3};
+    return int4v{(int)(w0 & 0x0F0F0F0Fu), (int)((w0 >> 4) & 0x0F0F0F0Fu), (int)(w1 & 0x0F0F0F0Fu),
+                 (int)((w1 >> 4) & 0x0F0F0F0Fu)};
 }
 
 struct TileInfo {
@@ -95,17 +90,19 @@ __device__ __forceinline__ bool tile_info(const ExpertArgs& a, int t, TileInfo* 
 //        order; kph + KPAD = 16 mod 256 bytes puts the 16 token rows of a
 //        ds_read_b128 half-wave in distinct banks
 //   s    the tokens' scales over all of K: group g, token i at s[g * MT + i]
+//   c    -8 times the tokens' group sums of 256 h + l, laid out as s
 //   tok  the tile's token (gate/up) or slot (down) rows, then its slot ids
 //        (gate/up) or routing weights (down)
 //   w    per wave, two super-stage buffers of its 32 weight rows (WRS bytes
 //        per row)
 struct Lay {
     int kph;
-    size_t s, tok, w, total;
+    size_t s, c, tok, w, total;
     __host__ __device__ constexpr Lay(int K, int G)
         : kph(K < KPH_MAX ? K : KPH_MAX),
           s((size_t)2 * MT * ((K < KPH_MAX ? K : KPH_MAX) + KPAD)),
-          tok(s + (size_t)(K / G) * MT * 4),
+          c(s + (size_t)(K / G) * MT * 4),
+          tok(c + (size_t)(K / G) * MT * 4),
           w(tok + 2 * MT * 4),
           total(tok + 2 * MT * 4 + (size_t)NWAVE * 2 * WBUF) {}
 };
@@ -142,11 +139,15 @@ __device__ __forceinline__ void stage_phase(const int8_t* __restrict__ hi, const
     }
 }
 
-// The tile's token scales over all of K (padding tokens, i >= nt: 0).
-__device__ __forceinline__ void stage_scales(const float* __restrict__ sc, const int* src, int nt, int ng, float* s) {
+// The tile's token scales and group-sum corrections over all of K
+// (padding tokens, i >= nt: 0).
+__device__ __forceinline__ void stage_scales(const float* __restrict__ sc, const int* __restrict__ qc, const int* src,
+                                             int nt, int ng, float* s, int* c) {
     for (int u = threadIdx.x; u < ng * MT; u += MTHREADS) {
         const int g = u / MT, i = u % MT;
-        s[u] = i < nt ? sc[(size_t)src[i] * ng + g] : 0.0f;
+        const size_t o = (size_t)src[i] * ng + g;
+        s[u] = i < nt ? sc[o] : 0.0f;
+        c[u] = i < nt ? -8 * qc[o] : 0;
     }
 }
 
@@ -242,8 +243,19 @@ __device__ __forceinline__ SxOps load_sx(const float* s, int g, int h) {
                   *(const float4*)(sg + 24)}};
 }
 
+// The 16 tokens' corrections of one group (this lane's half h), in the
+// accumulator layout: register v holds token 8 (v / 4) + 4 h + v % 4.
+__device__ __forceinline__ int16v load_corr(const int* c, int g, int h) {
+    const int* cg = c + (size_t)g * MT + 4 * h;
+    const int8v a = __builtin_shufflevector(*(const int4v*)cg, *(const int4v*)(cg + 8), 0, 1, 2, 3, 4, 5, 6, 7);
+    const int8v b = __builtin_shufflevector(*(const int4v*)(cg + 16), *(const int4v*)(cg + 24), 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+}
+
 // The integer products of one stage: per group of the stage, hi and lo
-// digit planes.
+// digit planes.  The lo products accumulate onto o.il, which the caller sets
+// to the group's corrections: with unsigned nibbles q, 256 ih + il is then
+// the exact sum of (256 h + l) (q - 8).
 template <int G>
 struct IOps {
     int16v ih[64 / G], il[64 / G];
@@ -253,14 +265,14 @@ template <int G>
 __device__ __forceinline__ void stage_mfma(IOps<G>& o, const AOps& a, const int4v& b0, const int4v& b1) {
     if (G == 64) {
         o.ih[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.ah0, b0, int16v{}, 0, 0, 0);
-        o.il[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al0, b0, int16v{}, 0, 0, 0);
+        o.il[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al0, b0, o.il[0], 0, 0, 0);
         o.ih[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.ah1, b1, o.ih[0], 0, 0, 0);
         o.il[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al1, b1, o.il[0], 0, 0, 0);
     } else {
         o.ih[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.ah0, b0, int16v{}, 0, 0, 0);
-        o.il[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al0, b0, int16v{}, 0, 0, 0);
+        o.il[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al0, b0, o.il[0], 0, 0, 0);
         o.ih[G == 64 ? 0 : 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.ah1, b1, int16v{}, 0, 0, 0);
-        o.il[G == 64 ? 0 : 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al1, b1, int16v{}, 0, 0, 0);
+        o.il[G == 64 ? 0 : 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a.al1, b1, o.il[G == 64 ? 0 : 1], 0, 0, 0);
     }
 }
 
@@ -298,7 +310,7 @@ struct TokSrc {
 // token phase boundary the block restages the tokens (two barriers).
 template <int G>
 __device__ __forceinline__ void wave_product(floatx16& acc, WStream<G>& ws, uint8_t* wl, int8_t* q,
-                                             const float* s, const TokSrc& ts, const Lay& ly) {
+                                             const float* s, const int* cc, const TokSrc& ts, const Lay& ly) {
     constexpr int NG = 64 / G;                    // groups per stage
     constexpr bool PIPE = G == 64;
     const int lane = threadIdx.x & 63;
@@ -342,6 +354,10 @@ __device__ __forceinline__ void wave_product(floatx16& acc, WStream<G>& ws, uint
             int4v b0, b1;
             load_bops<G>(wbuf, n, h, cs, b0, b1);
             const int pc = PIPE ? cur : 0, pp = PIPE ? prv : 0;
+            // the lo accumulators start at the groups' corrections (pr[pc]'s
+            // previous products went through their epilogue already)
+#pragma unroll
+            for (int u = 0; u < NG; u++) pr[pc].il[u] = load_corr(cc, NG * c + u, h);
             stage_mfma<G>(pr[pc], ab[cur], b0, b1);
 #pragma unroll
             for (int u = 0; u < NG; u++) wsp[pc][u] = sc_at<G>(scs, NG * cs + u);
@@ -373,6 +389,7 @@ __device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo&
     const int r0 = blockIdx.y * GU_ROWS;          // the block's first intermediate row
     int8_t* q = (int8_t*)sm;
     float* s = (float*)(sm + ly.s);
+    int* cc = (int*)(sm + ly.c);
     int* tok = (int*)(sm + ly.tok);
     uint8_t* wl = sm + ly.w + (size_t)w * 2 * WBUF;
     int* slots = tok + MT;
@@ -394,10 +411,10 @@ __device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo&
     ws.load(1, 1);
     __syncthreads();
     stage_phase(a.xqh, a.xql, tok, d, 0, ly.kph, q);
-    stage_scales(a.xqs, tok, ti.nt, ng, s);
+    stage_scales(a.xqs, a.xqc, tok, ti.nt, ng, s, cc);
     __syncthreads();
     floatx16 acc = {};
-    wave_product<G>(acc, ws, wl, q, s, TokSrc{a.xqh, a.xql, tok, d}, ly);
+    wave_product<G>(acc, ws, wl, q, s, cc, TokSrc{a.xqh, a.xql, tok, d}, ly);
 
     // SwiGLU: both matrices' sums to LDS (over the token digits), then one
     // wave per (token, 64-row piece) forms act, its digits and scale
@@ -425,7 +442,8 @@ __device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo&
         a.act[(size_t)slot * m + row] = av;
         const int g0 = row / G;                   // this lane's group (a G-lane segment)
         encode_i8_group_wave<G>(av, true, a.aqh + (size_t)slot * m + (size_t)g0 * G,
-                                a.aql + (size_t)slot * m + (size_t)g0 * G, a.aqs + (size_t)slot * mg + g0);
+                                a.aql + (size_t)slot * m + (size_t)g0 * G, a.aqs + (size_t)slot * mg + g0,
+                                a.aqc + (size_t)slot * mg + g0);
     }
 }
 
@@ -451,6 +469,7 @@ k_down_mfma(ExpertArgs a) {
     const Lay ly(m, G);
     int8_t* q = (int8_t*)sm;
     float* s = (float*)(sm + ly.s);
+    int* cc = (int*)(sm + ly.c);
     int* tok = (int*)(sm + ly.tok);
     float* tws = (float*)(tok + MT);
     uint8_t* wl = sm + ly.w + (size_t)w * 2 * WBUF;
@@ -476,13 +495,13 @@ k_down_mfma(ExpertArgs a) {
     int row = start(0);
     __syncthreads();
     stage_phase(a.aqh, a.aql, tok, m, 0, ly.kph, q);
-    stage_scales(a.aqs, tok, ti.nt, ng, s);
+    stage_scales(a.aqs, a.aqc, tok, ti.nt, ng, s, cc);
     __syncthreads();
     // the staged act digits serve DN_BLOCK_ROWS / DN_ROWS passes over the rows
 #pragma unroll 1
     for (int pass = 0; pass < DN_BLOCK_ROWS / DN_ROWS; pass++) {
         floatx16 acc = {};
-        wave_product<G>(acc, ws, wl, q, s, TokSrc{a.aqh, a.aql, tok, m}, ly);
+        wave_product<G>(acc, ws, wl, q, s, cc, TokSrc{a.aqh, a.aql, tok, m}, ly);
         const int r = row;
         if (pass + 1 < DN_BLOCK_ROWS / DN_ROWS) row = start(pass + 1);
 #pragma unroll
@@ -504,7 +523,7 @@ template <int G>
 __global__ void __launch_bounds__(MTHREADS, 1)
 k_q4_gemm_mfma(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scales,
                const int8_t* __restrict__ xqh, const int8_t* __restrict__ xql, const float* __restrict__ xqs,
-               int T, int m, int d, int npass, float* __restrict__ out) {
+               const int* __restrict__ xqc, int T, int m, int d, int npass, float* __restrict__ out) {
     extern __shared__ __align__(16) unsigned char sm[];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int ng = d / G;
@@ -513,6 +532,7 @@ k_q4_gemm_mfma(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ 
     const int nt = min(MT, T - t0);
     int8_t* q = (int8_t*)sm;
     float* s = (float*)(sm + ly.s);
+    int* cc = (int*)(sm + ly.c);
     int* tok = (int*)(sm + ly.tok);
     uint8_t* wl = sm + ly.w + (size_t)w * 2 * WBUF;
     if (tid < MT) tok[tid] = t0 + (tid < nt ? tid : 0);   // padding: the tile's first token
@@ -531,12 +551,12 @@ k_q4_gemm_mfma(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ 
     int row = start(0);
     __syncthreads();
     stage_phase(xqh, xql, tok, d, 0, ly.kph, q);
-    stage_scales(xqs, tok, nt, ng, s);
+    stage_scales(xqs, xqc, tok, nt, ng, s, cc);
     __syncthreads();
 #pragma unroll 1
     for (int pass = 0; pass < npass; pass++) {
         floatx16 acc = {};
-        wave_product<G>(acc, ws, wl, q, s, TokSrc{xqh, xql, tok, d}, ly);
+        wave_product<G>(acc, ws, wl, q, s, cc, TokSrc{xqh, xql, tok, d}, ly);
         const int r = row;
         if (pass + 1 < npass) row = start(pass + 1);
 #pragma unroll
@@ -552,7 +572,7 @@ k_q4_gemm_mfma(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ 
 template <int G>
 __global__ void __launch_bounds__(256)
 k_prep_i8(const float* __restrict__ X, int T, int d, int8_t* __restrict__ hi, int8_t* __restrict__ lo,
-          float* __restrict__ sc) {
+          float* __restrict__ sc, int* __restrict__ qc) {
     const long long seg = ((long long)blockIdx.x * blockDim.x + threadIdx.x) / G;
     const int ng = d / G;
     const bool ok = seg < (long long)T * ng;
@@ -560,7 +580,7 @@ k_prep_i8(const float* __restrict__ X, int T, int d, int8_t* __restrict__ hi, in
     const int t = (int)(sg / ng), g = (int)(sg % ng);
     const size_t o = (size_t)t * d + (size_t)g * G;
     const float v = ok ? X[o + (threadIdx.x & (G - 1))] : 0.0f;
-    encode_i8_group_wave<G>(v, ok, hi + o, lo + o, sc + (size_t)t * ng + g);
+    encode_i8_group_wave<G>(v, ok, hi + o, lo + o, sc + (size_t)t * ng + g, qc + (size_t)t * ng + g);
 }
 
 // Contractions the kernels take: multiples of the weight super-stage, and
@@ -636,7 +656,7 @@ bool q4_gemm_mfma_ok(int m, int d, int group) {
 }
 
 size_t q4_gemm_mfma_ws(int T, int d, int group) {
-    return pad256((size_t)T * d) * 2 + pad256((size_t)T * (d / group) * 4);
+    return pad256((size_t)T * d) * 2 + pad256((size_t)T * (d / group) * 4) * 2;
 }
 
 hipError_t launch_q4_gemm_mfma(const uint8_t* packed, const uint16_t* scales, const float* X, int T, int m, int d,
@@ -648,6 +668,7 @@ hipError_t launch_q4_gemm_mfma(const uint8_t* packed, const uint16_t* scales, co
     int8_t* hi = (int8_t*)ws;
     int8_t* lo = hi + pad256((size_t)T * d);
     float* sc = (float*)(lo + pad256((size_t)T * d));
+    int* qc = (int*)((char*)sc + pad256((size_t)T * (d / group) * 4));
     const long long lanes = (long long)T * d;
     const unsigned pblocks = (unsigned)((lanes + 255) / 256);
     // two passes per block when the rows allow and the grid still fills the chip
@@ -655,13 +676,13 @@ hipError_t launch_q4_gemm_mfma(const uint8_t* packed, const uint16_t* scales, co
     const int npass = (m % (2 * DN_ROWS) == 0 && (long long)tiles * (m / (2 * DN_ROWS)) >= 256) ? 2 : 1;
     const dim3 grid((unsigned)tiles, (unsigned)(m / (DN_ROWS * npass)));
     if (group == 64) {
-        hipLaunchKernelGGL(k_prep_i8<64>, dim3(pblocks), dim3(256), 0, st, X, T, d, hi, lo, sc);
+        hipLaunchKernelGGL(k_prep_i8<64>, dim3(pblocks), dim3(256), 0, st, X, T, d, hi, lo, sc, qc);
         hipLaunchKernelGGL(k_q4_gemm_mfma<64>, grid, dim3(MTHREADS), Lay(d, 64).total, st, packed, scales, hi, lo, sc,
-                           T, m, d, npass, out);
+                           qc, T, m, d, npass, out);
     } else {
-        hipLaunchKernelGGL(k_prep_i8<32>, dim3(pblocks), dim3(256), 0, st, X, T, d, hi, lo, sc);
+        hipLaunchKernelGGL(k_prep_i8<32>, dim3(pblocks), dim3(256), 0, st, X, T, d, hi, lo, sc, qc);
         hipLaunchKernelGGL(k_q4_gemm_mfma<32>, grid, dim3(MTHREADS), Lay(d, 32).total, st, packed, scales, hi, lo, sc,
-                           T, m, d, npass, out);
+                           qc, T, m, d, npass, out);
     }
     return hipGetLastError();
 }

@@ -260,7 +260,8 @@ k_router_grp(RouteArgs a) {
         // the same group as int8 digit pairs for the MFMA branch
         if (a.xqh) {
             const size_t o = (size_t)b * d + (size_t)(ok ? p : 0) * G;
-            encode_i8_group_wave<G>(v, ok, a.xqh + o, a.xql + o, a.xqs + (size_t)b * ng + (ok ? p : 0));
+            encode_i8_group_wave<G>(v, ok, a.xqh + o, a.xql + o, a.xqs + (size_t)b * ng + (ok ? p : 0),
+                                    a.xqc + (size_t)b * ng + (ok ? p : 0));
         }
     }
 }
@@ -408,7 +409,8 @@ k_router_quad(RouteArgs a) {
                                        a.xscale + (size_t)b * ng + (ok ? p : 0));
             if (a.xqh) {
                 const size_t o = (size_t)b * d + (size_t)(ok ? p : 0) * G;
-                encode_i8_group_wave<G>(v, ok, a.xqh + o, a.xql + o, a.xqs + (size_t)b * ng + (ok ? p : 0));
+                encode_i8_group_wave<G>(v, ok, a.xqh + o, a.xql + o, a.xqs + (size_t)b * ng + (ok ? p : 0),
+                                    a.xqc + (size_t)b * ng + (ok ? p : 0));
             }
         }
     }

@@ -38,6 +38,8 @@ struct Ws {
     int8_t* xql;
     float* xqs;                 // [B][d/G] scales of the token digit pairs
     float* aqs;                 // [B*k][m/G] scales of the act digit pairs
+    int* xqc;                   // [B][d/G] sums of the token digit pairs' integers per group
+    int* aqc;                   // [B*k][m/G] the same for act
 };
 
 }  // namespace jm
