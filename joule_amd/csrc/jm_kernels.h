@@ -135,7 +135,9 @@ hipError_t launch_dispatch(const int* top, int nslot, int E, int k, int* seg_off
 // decode path (nslot <= JM_DEC_SLOTS): gate/up over ballot-found slots, then
 // down + combine into a.out.  For gateup_topk(B, E) the gate/up kernel
 // computes the top-k itself (from a.logits; no top-k launch before it).
+#ifndef JM_GU_TOPK_MAX_B
 #define JM_GU_TOPK_MAX_B 4
+#endif
 bool gateup_topk(int B, int E);
 hipError_t launch_gateup_dec(const ExpertArgs& a, hipStream_t st);
 hipError_t launch_down_comb(const ExpertArgs& a, hipStream_t st);
