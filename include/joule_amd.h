@@ -341,6 +341,21 @@ int jm_router(const void* gate_w, int dtype, const float* x, int B, int E, int d
 int jm_dispatch(const int32_t* top, int nslot, int E, int topk, int32_t* seg_off, int32_t* seg_slot,
                 int32_t* active, int32_t* n_active, int32_t* first_slot, int32_t* comb, void* stream);
 
+/* The expert stages of layer_ffn_batch for a given top-k table top [B][topk]
+ * (experts outside [0, E) leave their slots' rows untouched), run by the
+ * store's wave-item kernels on its workspace; slot = b * topk + i.
+ *   jm_expert_gateup: act [B*topk][m] = SwiGLU of the slot's expert's gate
+ *     and up rows against x [B][d]: (g / (1 + expf_fast(-g))) * u, the first
+ *     half of ffn_expert_worker (decode_kernel.c:1365-1375).
+ *   jm_expert_down: y [B*topk][d] = tw[slot] * (down rows . act[slot]), its
+ *     second half (:1376-1383).
+ *   jm_combine: out [B][d] = each token's y rows summed in the reference's
+ *     union order (:1502-1507). */
+int jm_expert_gateup(jm_store* s, int layer, const float* x, const int32_t* top, int B, float* act, void* stream);
+int jm_expert_down(jm_store* s, int layer, const float* act, const int32_t* top, const float* tw, int B, float* y,
+                   void* stream);
+int jm_combine(jm_store* s, const float* y, const int32_t* top, int B, float* out, void* stream);
+
 /* Exact dequantisation (q - 8) * float(scale) of one record
  * (q4_store.py:58-67 _dequantize). */
 int jm_q4_dequant(float* out, const uint8_t* packed, const uint16_t* scales, int64_t numel, int group,

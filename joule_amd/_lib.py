@@ -47,6 +47,9 @@ SIGNATURES = {
     "jm_prefill_layers": ([_vp] * 5 + [_i, _vp, _vp], _i),
     "jm_router": ([_vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp], _i),
     "jm_dispatch": ([_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
+    "jm_expert_gateup": ([_vp, _i, _vp, _vp, _i, _vp, _vp], _i),
+    "jm_expert_down": ([_vp, _i, _vp, _vp, _vp, _i, _vp, _vp], _i),
+    "jm_combine": ([_vp, _vp, _vp, _i, _vp, _vp], _i),
     "jm_q4_dequant": ([_vp, _vp, _vp, _i64, _i, _vp], _i),
     "jm_q4_gemv_f32": ([_vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
     "jm_q4_gemm_f32": ([_vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),

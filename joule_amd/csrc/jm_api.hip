@@ -238,6 +238,44 @@ int check_store(const jm_store* s) {
     return 0;
 }
 
+// Common part of the stage entry points: checks, the workspace for B
+// tokens, and the dispatch of the caller's top-k table (the counting sort,
+// the expert work table and the union order of the dispatch path) on st.
+// The stages run the dispatch path's wave-item kernels at every B.
+int stage_setup(jm_store* s, int layer, const int32_t* top, int B, const char* who, hipStream_t st,
+                jm::RouteArgs* r, jm::ExpertArgs* a) {
+    if (!s) return fail(JM_ERR_ARG, "%s: store is NULL", who);
+    if (layer < 0 || layer >= s->L) return fail(JM_ERR_ARG, "%s: layer %d outside [0, %d)", who, layer, s->L);
+    if (B < 0 || (long long)B * s->topk > JM_MAX_SLOTS)
+        return fail(JM_ERR_SHAPE, "%s: need 0 <= B and B * topk <= %d", who, JM_MAX_SLOTS);
+    if (B == 0) return 0;
+    if (!top) return fail(JM_ERR_ARG, "%s: top is NULL", who);
+    const int E = s->E, k = s->topk, nslot = B * k;
+    if ((size_t)jm::dispatch_lds_ints(nslot, E) * 4 > (size_t)s->lds_max)
+        return fail(JM_ERR_SHAPE, "%s: %d slots over %d experts exceed the dispatch's LDS", who, nslot, E);
+    if (int rc = jm::store_reserve(s, B)) return rc;
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    const jm::Ws& w = s->w;
+    r->B = B; r->E = E; r->d = s->d; r->topk = k; r->group = s->group;
+    r->top = const_cast<int*>(top);             // read only
+    r->seg_off = w.seg_off; r->seg_slot = w.seg_slot; r->active = w.active; r->n_active = w.n_active;
+    r->first_slot = w.first_slot; r->comb = w.comb;
+    r->work = w.work; r->umax = std::min(E, nslot); r->rec = s->rec;
+    r->key0 = (long long)layer * E;
+    r->dense_min = 0x7FFFFFFF;                  // no MFMA tiles
+    r->tiles = w.tiles; r->n_tiles = w.n_tiles;
+    JM_HIP(jm::launch_dispatch_work(*r, st), "dispatch launch");
+    a->blob = s->blob; a->rec = s->rec; a->key0 = r->key0; a->E = E;
+    a->work = w.work; a->umax = r->umax; a->seg_slot = w.seg_slot;
+    a->top = r->top; a->nslot = nslot; a->B = B;
+    a->d = s->d; a->m = s->m; a->topk = k; a->group = s->group;
+    a->xdig = w.xdig; a->xscale = w.xscale;
+    a->adig = w.adig; a->ascale = w.ascale;
+    a->dense_min = 0x7FFFFFFF;
+    a->tiles = w.tiles; a->n_tiles = w.n_tiles;
+    return 0;
+}
+
 }  // namespace
 
 namespace jm {
@@ -677,6 +715,55 @@ int jm_q4_gemm_f32(float* out, const float* X, int T, const uint8_t* packed, con
     const hipError_t f = ws.async ? hipFreeAsync(ws.p, st) : hipSuccess;
     if (e != hipSuccess) return hip_fail(e, "q4_gemm launch");
     if (f != hipSuccess) return hip_fail(f, "hipFreeAsync");
+    return 0;
+}
+
+// ------------------------------------------------- block stages one by one
+
+int jm_expert_gateup(jm_store* s, int layer, const float* x, const int32_t* top, int B, float* act, void* stream) {
+    jm::RouteArgs r{};
+    jm::ExpertArgs a{};
+    if (int rc = stage_setup(s, layer, top, B, "jm_expert_gateup", (hipStream_t)stream, &r, &a)) return rc;
+    if (B == 0) return 0;
+    if (!x || !act || !aligned(x, 16) || !aligned(act, 16))
+        return fail(JM_ERR_ARG, "jm_expert_gateup: x and act must be non-NULL and 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    const jm::Ws& w = s->w;
+    // the tokens' digits as the router writes them, then gate/up + SwiGLU
+    // of every slot into act (fp32) and the act digits
+    JM_HIP(jm::launch_prep_digits(x, s->d, B, s->d, s->group, w.xdig, w.xscale, st), "digits launch");
+    a.act = act;
+    JM_HIP(jm::launch_gateup(a, a.umax, st), "gate/up launch");
+    return 0;
+}
+
+int jm_expert_down(jm_store* s, int layer, const float* act, const int32_t* top, const float* tw, int B, float* y,
+                   void* stream) {
+    jm::RouteArgs r{};
+    jm::ExpertArgs a{};
+    if (int rc = stage_setup(s, layer, top, B, "jm_expert_down", (hipStream_t)stream, &r, &a)) return rc;
+    if (B == 0) return 0;
+    if (!act || !tw || !y || !aligned(act, 16) || !aligned(y, 16))
+        return fail(JM_ERR_ARG, "jm_expert_down: act, tw and y must be non-NULL, act and y 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    const jm::Ws& w = s->w;
+    // act's digits in 32-value groups, as the gate/up epilogue writes them,
+    // then y[slot] = tw[slot] * (down rows . act[slot])
+    JM_HIP(jm::launch_prep_digits(act, s->m, B * s->topk, s->m, 32, w.adig, w.ascale, st), "digits launch");
+    a.tw = tw;
+    a.y = y;
+    JM_HIP(jm::launch_down(a, a.umax, st), "down launch");
+    return 0;
+}
+
+int jm_combine(jm_store* s, const float* y, const int32_t* top, int B, float* out, void* stream) {
+    jm::RouteArgs r{};
+    jm::ExpertArgs a{};
+    if (int rc = stage_setup(s, 0, top, B, "jm_combine", (hipStream_t)stream, &r, &a)) return rc;
+    if (B == 0) return 0;
+    if (!y || !out || !aligned(y, 16) || !aligned(out, 16))
+        return fail(JM_ERR_ARG, "jm_combine: y and out must be non-NULL and 16-byte aligned");
+    JM_HIP(jm::launch_combine(y, s->w.comb, B, s->topk, s->d, nullptr, out, (hipStream_t)stream), "combine launch");
     return 0;
 }
 

@@ -205,6 +205,51 @@ class HbmExpertStore:
                                                  _lib.stream_handle(stream)), "jm_layer_ffn_batch")
         return out
 
+    # ------------------------------------------------ the block's stages
+
+    def _stage_in(self, t: torch.Tensor, name: str, shape: tuple, dtype) -> None:
+        if (t.dtype != dtype or not t.is_cuda or not t.is_contiguous() or tuple(t.shape) != shape):
+            raise ValueError(f"{name} must be a contiguous {dtype} CUDA tensor {list(shape)}")
+
+    def expert_gateup(self, l: int, x: torch.Tensor, top: torch.Tensor, stream=None) -> torch.Tensor:
+        """act[B * topk, m]: SwiGLU of each slot's expert's gate and up rows
+        against its token (ffn_expert_worker's first half,
+        decode_kernel.c:1365-1375); slot = b * topk + i of top[B, topk]."""
+        s = self.shape
+        B = x.shape[0] if x.dim() == 2 else -1
+        self._stage_in(x, "x", (B, s.d), torch.float32)
+        self._stage_in(top, "top", (B, s.topk), torch.int32)
+        act = torch.empty((B * s.topk, s.m), dtype=torch.float32, device=x.device)
+        _lib.check(_lib.lib().jm_expert_gateup(self._h, int(l), _lib.ptr(x), _lib.ptr(top), B, _lib.ptr(act),
+                                               _lib.stream_handle(stream)), "jm_expert_gateup")
+        return act
+
+    def expert_down(self, l: int, act: torch.Tensor, top: torch.Tensor, tw: torch.Tensor,
+                    stream=None) -> torch.Tensor:
+        """y[B * topk, d] = tw[slot] * (down rows of the slot's expert . act[slot])
+        (ffn_expert_worker's second half, decode_kernel.c:1376-1383)."""
+        s = self.shape
+        B = top.shape[0] if top.dim() == 2 else -1
+        self._stage_in(act, "act", (B * s.topk, s.m), torch.float32)
+        self._stage_in(top, "top", (B, s.topk), torch.int32)
+        self._stage_in(tw, "tw", (B, s.topk), torch.float32)
+        y = torch.empty((B * s.topk, s.d), dtype=torch.float32, device=act.device)
+        _lib.check(_lib.lib().jm_expert_down(self._h, int(l), _lib.ptr(act), _lib.ptr(top), _lib.ptr(tw), B,
+                                             _lib.ptr(y), _lib.stream_handle(stream)), "jm_expert_down")
+        return y
+
+    def combine(self, y: torch.Tensor, top: torch.Tensor, stream=None) -> torch.Tensor:
+        """out[B, d] = each token's y rows summed in the reference's union
+        order (decode_kernel.c:1502-1507)."""
+        s = self.shape
+        B = top.shape[0] if top.dim() == 2 else -1
+        self._stage_in(y, "y", (B * s.topk, s.d), torch.float32)
+        self._stage_in(top, "top", (B, s.topk), torch.int32)
+        out = torch.empty((B, s.d), dtype=torch.float32, device=y.device)
+        _lib.check(_lib.lib().jm_combine(self._h, _lib.ptr(y), _lib.ptr(top), B, _lib.ptr(out),
+                                         _lib.stream_handle(stream)), "jm_combine")
+        return out
+
     def profile(self, enable: bool = True) -> None:
         """Record HIP events around each kernel of later calls."""
         _lib.check(_lib.lib().jm_store_profile(self._h, int(bool(enable))), "jm_store_profile")

@@ -109,6 +109,9 @@ def test_null_arguments_are_errors():
     assert L.jm_store_create(None, 64, None, 0, None, None) == -1
     assert L.jm_layer_ffn_batch(None, 0, None, 1, None, None, None, None) == -1
     assert L.jm_q4_gemm_f32(None, None, 1, None, None, 1, 64, 64, None) == -1
+    assert L.jm_expert_gateup(None, 0, None, None, 1, None, None) == -1
+    assert L.jm_expert_down(None, 0, None, None, None, 1, None, None) == -1
+    assert L.jm_combine(None, None, None, 1, None, None) == -1
     assert L.jm_store_destroy(None) == 0
     with pytest.raises(_lib.JouleError):
         _lib.check(L.jm_store_reserve(None, 4), "reserve")

@@ -243,6 +243,78 @@ def test_block_parity(request, which, B):
     assert err <= TOL
 
 
+def _host_rec(layer: Layer, l: int, e: int, p: int):
+    """(scales u16, packed u8) of one record from the host copy of the store."""
+    s = layer.shape
+    rows, cols = ((s.m, s.d), (s.m, s.d), (s.d, s.m))[p]
+    sb, pb = Q.record_sizes(rows, cols, layer.group)
+    so, po = (int(v) for v in layer.offsets[p, l * s.E + e])
+    return layer.host[so:so + sb].view(np.uint16), layer.host[po:po + pb]
+
+
+def _union_sum(y: np.ndarray, top: np.ndarray) -> np.ndarray:
+    """Each token's y rows summed in float32 in the reference's union order:
+    experts by first appearance over the slots (decode_kernel.c:1502-1507)."""
+    B, k = top.shape
+    first = {}
+    for sl, e in enumerate(top.reshape(-1)):
+        first.setdefault(int(e), sl)
+    out = np.zeros((B, y.shape[1]), np.float32)
+    for b in range(B):
+        for i in sorted(range(k), key=lambda i: first[int(top[b, i])]):
+            out[b] = out[b] + y[b * k + i]
+    return out
+
+
+@pytest.mark.parametrize("which,B", [("qwen64", 3), ("qwen64", 40), ("qwen32", 8), ("olmoe64", 5)])
+def test_block_stages_match_oracle(request, which, B):
+    """The stage entry points against the reference's expert_job per slot
+    (expert_ffn.c:145-191: gate/up, SwiGLU, down times the routing weight):
+    act and y within the block tolerance, the union-order combine bit-exact,
+    and the three stages chained against the block."""
+    layer = request.getfixturevalue(which)
+    banner(f"stages {which} B={B}")
+    s, l = layer.shape, layer.L - 1
+    x = activations(B, s.d)
+    out_blk, top, tw = _run_block(layer, l, x)
+    O = layer.O
+    act_ref = np.empty((B * s.topk, s.m), np.float32)
+    y_ref = np.empty((B * s.topk, s.d), np.float32)
+    for b in range(B):
+        for i in range(s.topk):
+            e = int(top[b, i])
+            scr = O.expert_job(_host_rec(layer, l, e, 0), _host_rec(layer, l, e, 1), _host_rec(layer, l, e, 2),
+                               s.m, s.d, layer.group, x[b], float(tw[b, i]))
+            act_ref[b * s.topk + i] = scr[:s.m]
+            y_ref[b * s.topk + i] = scr[s.m:]
+    st = layer.store
+    top_d, tw_d = torch.from_numpy(top).cuda(), torch.from_numpy(tw).cuda()
+    act = st.expert_gateup(l, torch.from_numpy(x).cuda(), top_d)
+    y = st.expert_down(l, torch.from_numpy(act_ref).cuda(), top_d, tw_d)
+    comb = st.combine(torch.from_numpy(y_ref).cuda(), top_d)
+    chained = st.combine(st.expert_down(l, act, top_d, tw_d), top_d)
+    torch.cuda.synchronize()
+    e_act, e_y = _rel(act.cpu().numpy(), act_ref), _rel(y.cpu().numpy(), y_ref)
+    e_ch = _rel(chained.cpu().numpy(), out_blk)
+    print(f"  act {e_act:.3e}  y {e_y:.3e}  chained vs block {e_ch:.3e}", flush=True)
+    assert e_act <= TOL and e_y <= TOL and e_ch <= TOL
+    assert np.array_equal(comb.cpu().numpy().view(np.uint32), _union_sum(y_ref, top).view(np.uint32))
+
+
+def test_block_stage_errors(qwen64):
+    banner("stage entry point errors")
+    st, s = qwen64.store, qwen64.shape
+    x = torch.zeros((2, s.d), device="cuda")
+    top = torch.zeros((2, s.topk), dtype=torch.int32, device="cuda")
+    with pytest.raises(_lib.JouleError):
+        _lib.check(_lib.lib().jm_expert_gateup(st._h, qwen64.L, _lib.ptr(x), _lib.ptr(top), 2, _lib.ptr(x),
+                                               None), "gateup")
+    with pytest.raises(ValueError):
+        st.expert_down(0, torch.zeros((3, s.m), device="cuda"), top, torch.zeros((2, s.topk), device="cuda"))
+    e = torch.zeros((0, s.topk), dtype=torch.int32, device="cuda")
+    assert st.combine(torch.zeros((0, s.d), device="cuda"), e).shape == (0, s.d)
+
+
 # Decode-path shapes beyond the two model shapes: rows of 16 lanes
 # (d = 1024, m = 512), gate/up rows of two chunks per lane (d = 4096) and
 # down rows of 64 lanes (m > 1024).
