@@ -363,6 +363,30 @@ int jm_q4_dequant(float* out, const uint8_t* packed, const uint16_t* scales, int
 
 /* ---- the KernelBackend products (backend.py:45-69), device pointers ---- */
 
+/* One expert for one token, the reference's ExpertJob / expert_job
+ * (expert_ffn.c:145-191) with the same field order and meaning, on device
+ * pointers: scratch[0..m_gg) = act = SiLU(gate . x) * (up . x), then
+ * scratch[m_gg..m_gg+d_in) = prob * (down . act).  m_d must equal d_in and
+ * d_m must equal m_gg, as in the reference's callers (moe.py:32-42). */
+typedef struct jm_expert_job_t {
+    const uint8_t* pk_g;
+    const uint16_t* sc_g;
+    const uint8_t* pk_u;
+    const uint16_t* sc_u;
+    const uint8_t* pk_d;
+    const uint16_t* sc_d;
+    int m_gg;
+    int d_in;
+    int m_d;
+    int d_m;
+    int group;
+    const float* x;
+    float* scratch;
+    float prob;
+} jm_expert_job_t;
+
+int jm_expert_job(const jm_expert_job_t* job, void* stream);
+
 /* out[m] = dequant(W[m][d]) . x[d]; argument order of q4_gemv_f32
  * (quant_gemv.c:35) plus the stream. */
 int jm_q4_gemv_f32(float* out, const float* x, const uint8_t* packed, const uint16_t* scales,

@@ -51,6 +51,7 @@ SIGNATURES = {
     "jm_expert_down": ([_vp, _i, _vp, _vp, _vp, _i, _vp, _vp], _i),
     "jm_combine": ([_vp, _vp, _vp, _i, _vp, _vp], _i),
     "jm_q4_dequant": ([_vp, _vp, _vp, _i64, _i, _vp], _i),
+    "jm_expert_job": ([_vp, _vp], _i),
     "jm_q4_gemv_f32": ([_vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
     "jm_q4_gemm_f32": ([_vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
 }
@@ -62,6 +63,14 @@ class KernelCfg(ctypes.Structure):
                 ("E", _i), ("topk", _i), ("V", _i), ("eps", _c.c_float), ("maxT", _i),
                 ("intermediate", _i), ("qk_norm_type", _i), ("bias_qkv", _i),
                 ("norm_topk_prob", _i), ("expert_i8", _i), ("expert_bf16", _i)]
+
+
+class ExpertJob(ctypes.Structure):
+    """The reference's ExpertJob (expert_ffn.c:145-157, moe.py:32-42), here
+    with device pointers: jm_expert_job_t."""
+    _fields_ = [("pk_g", _vp), ("sc_g", _vp), ("pk_u", _vp), ("sc_u", _vp), ("pk_d", _vp), ("sc_d", _vp),
+                ("m_gg", _i), ("d_in", _i), ("m_d", _i), ("d_m", _i), ("group", _i),
+                ("x", _vp), ("scratch", _vp), ("prob", _c.c_float)]
 
 
 STAGES = ("route", "gateup", "down")

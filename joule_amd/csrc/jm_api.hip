@@ -767,6 +767,48 @@ int jm_combine(jm_store* s, const float* y, const int32_t* top, int B, float* ou
     return 0;
 }
 
+int jm_expert_job(const jm_expert_job_t* j, void* stream) {
+    if (!j) return fail(JM_ERR_ARG, "job is NULL");
+    if (!j->pk_g || !j->sc_g || !j->pk_u || !j->sc_u || !j->pk_d || !j->sc_d || !j->x || !j->scratch)
+        return fail(JM_ERR_ARG, "jm_expert_job: NULL pointer in the job");
+    const int m = j->m_gg, d = j->d_in, G = j->group;
+    if (G != 32 && G != 64) return fail(JM_ERR_SHAPE, "group must be 32 or 64");
+    if (m <= 0 || d <= 0 || j->m_d != d || j->d_m != m)
+        return fail(JM_ERR_SHAPE, "jm_expert_job: need m_gg, d_in > 0, m_d == d_in and d_m == m_gg (got %d %d %d %d)",
+                    m, d, j->m_d, j->d_m);
+    if (d % G || m % G || d / G > 64 || m / G > 64 || (d / 2) % 16 || (m / 2) % 16)
+        return fail(JM_ERR_SHAPE, "jm_expert_job: d_in and m_gg must be multiples of 32 and of group, at most 64 groups");
+    if (!aligned(j->pk_g, 16) || !aligned(j->pk_u, 16) || !aligned(j->pk_d, 16) || !aligned(j->x, 16))
+        return fail(JM_ERR_ARG, "jm_expert_job: packed records and x must be 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    const size_t dx = align256((size_t)(d / G) * JM_NDIG * (G / 8) * 4), sx = align256((size_t)(d / G) * 4);
+    const size_t gu = align256((size_t)2 * m * 4);
+    const size_t da = align256((size_t)(m / G) * JM_NDIG * (G / 8) * 4), sa = align256((size_t)(m / G) * 4);
+    PluginWs ws;
+    if (int rc = plugin_ws(st, dx + sx + gu + da + sa, &ws)) return rc;
+    char* p = (char*)ws.p;
+    uint32_t* dig_x = (uint32_t*)p;
+    float* sc_x = (float*)(p + dx);
+    float* gbuf = (float*)(p + dx + sx);
+    uint32_t* dig_a = (uint32_t*)(p + dx + sx + gu);
+    float* sc_a = (float*)(p + dx + sx + gu + da);
+    float* act = j->scratch;
+    float* wout = j->scratch + m;
+    // g and u rows against x, act = SiLU(g) * u (expert_ffn.c:165-172),
+    // then prob * (down rows . act) (:173-190)
+    hipError_t e = jm::launch_prep_digits(j->x, d, 1, d, G, dig_x, sc_x, st);
+    if (e == hipSuccess) e = jm::launch_q4_rows(j->pk_g, j->sc_g, m, d, G, dig_x, sc_x, 1, gbuf, m, st);
+    if (e == hipSuccess) e = jm::launch_q4_rows(j->pk_u, j->sc_u, m, d, G, dig_x, sc_x, 1, gbuf + m, m, st);
+    if (e == hipSuccess) e = jm::launch_swiglu_vec(gbuf, m, act, st);
+    if (e == hipSuccess) e = jm::launch_prep_digits(act, m, 1, m, G, dig_a, sc_a, st);
+    if (e == hipSuccess) e = jm::launch_q4_rows(j->pk_d, j->sc_d, d, m, G, dig_a, sc_a, 1, wout, d, st);
+    if (e == hipSuccess) e = jm::launch_scale_vec(wout, d, j->prob, st);
+    const hipError_t f = ws.async ? hipFreeAsync(ws.p, st) : hipSuccess;
+    if (e != hipSuccess) return hip_fail(e, "expert_job launch");
+    if (f != hipSuccess) return hip_fail(f, "hipFreeAsync");
+    return 0;
+}
+
 int jm_q4_gemv_f32(float* out, const float* x, const uint8_t* packed, const uint16_t* scales,
                    int m, int d, int group, void* stream) {
     return jm_q4_gemm_f32(out, x, 1, packed, scales, m, d, group, stream);

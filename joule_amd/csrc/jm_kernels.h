@@ -240,6 +240,10 @@ hipError_t launch_rms_rows(const float* x, const uint16_t* w, int B, int d, floa
 
 hipError_t launch_dequant(const uint8_t* packed, const uint16_t* scales, long long numel, int group,
                           float* out, hipStream_t st);
+// one expert for one token (expert_job): act = SiLU(g) * u from gu = [g; u],
+// then the down output scaled by the routing weight
+hipError_t launch_swiglu_vec(const float* gu, int m, float* act, hipStream_t st);
+hipError_t launch_scale_vec(float* v, int n, float s, hipStream_t st);
 hipError_t launch_q4_rows(const uint8_t* packed, const uint16_t* scales, int rows, int cols, int group,
                           const uint32_t* dig, const float* dscale, int T, float* out, int ostride,
                           hipStream_t st);

@@ -171,6 +171,30 @@ hipError_t launch_dequant(const uint8_t* packed, const uint16_t* scales, long lo
     return hipGetLastError();
 }
 
+// act[i] = SiLU(g[i]) * u[i] for gu = [g; u], as the reference writes it
+__global__ void __launch_bounds__(256)
+k_swiglu_vec(const float* __restrict__ gu, int m, float* __restrict__ act) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < m) act[i] = swiglu(gu[i], gu[m + i]);
+}
+
+// v[i] = v[i] * s
+__global__ void __launch_bounds__(256)
+k_scale_vec(float* __restrict__ v, int n, float s) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) v[i] = __fmul_rn(v[i], s);
+}
+
+hipError_t launch_swiglu_vec(const float* gu, int m, float* act, hipStream_t st) {
+    hipLaunchKernelGGL(k_swiglu_vec, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, gu, m, act);
+    return hipGetLastError();
+}
+
+hipError_t launch_scale_vec(float* v, int n, float s, hipStream_t st) {
+    hipLaunchKernelGGL(k_scale_vec, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, v, n, s);
+    return hipGetLastError();
+}
+
 hipError_t launch_q4_rows(const uint8_t* packed, const uint16_t* scales, int rows, int cols, int group,
                           const uint32_t* dig, const float* dscale, int T, float* out, int ostride,
                           hipStream_t st) {

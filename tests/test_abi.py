@@ -102,6 +102,14 @@ def test_store_create_rejects_bad_shapes(kw, group, code):
     assert h.value is None
 
 
+def test_expert_job_layout():
+    # ExpertJob of expert_ffn.c:145-157 / moe.py:32-42 on x86-64: six
+    # pointers, five ints, two pointers, one float
+    J = _lib.ExpertJob
+    assert J.m_gg.offset == 48 and J.group.offset == 64 and J.x.offset == 72
+    assert J.scratch.offset == 80 and J.prob.offset == 88 and ctypes.sizeof(J) == 96
+
+
 def test_null_arguments_are_errors():
     if not _lib.LIB_PATH.exists():
         pytest.skip("libjoule_amd.so not built")
@@ -112,6 +120,9 @@ def test_null_arguments_are_errors():
     assert L.jm_expert_gateup(None, 0, None, None, 1, None, None) == -1
     assert L.jm_expert_down(None, 0, None, None, None, 1, None, None) == -1
     assert L.jm_combine(None, None, None, 1, None, None) == -1
+    assert L.jm_expert_job(None, None) == -1
+    j = _lib.ExpertJob()
+    assert L.jm_expert_job(ctypes.byref(j), None) == -1
     assert L.jm_store_destroy(None) == 0
     with pytest.raises(_lib.JouleError):
         _lib.check(L.jm_store_reserve(None, 4), "reserve")

@@ -10,6 +10,8 @@ Full-size layers (OLMoE and Qwen3-30B-A3B shapes) are generated and
 quantised on the GPU, copied to the host for the oracle.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -313,6 +315,32 @@ def test_block_stage_errors(qwen64):
         st.expert_down(0, torch.zeros((3, s.m), device="cuda"), top, torch.zeros((2, s.topk), device="cuda"))
     e = torch.zeros((0, s.topk), dtype=torch.int32, device="cuda")
     assert st.combine(torch.zeros((0, s.d), device="cuda"), e).shape == (0, s.d)
+
+
+@pytest.mark.parametrize("which", ["qwen64", "qwen32", "olmoe64"])
+def test_expert_job_matches_reference(request, which):
+    """jm_expert_job (the reference's ExpertJob struct with device pointers)
+    against the reference's expert_job restated in the oracle, for a few
+    experts and routing weights."""
+    layer = request.getfixturevalue(which)
+    banner(f"expert_job {which}")
+    s = layer.shape
+    rng = np.random.default_rng(5)
+    for e, prob in ((0, 0.125), (s.E // 2, 0.5), (s.E - 1, 1.0)):
+        recs = [_host_rec(layer, 0, e, p) for p in range(3)]
+        x = rng.standard_normal(s.d).astype(np.float32)
+        ref = layer.O.expert_job(recs[0], recs[1], recs[2], s.m, s.d, layer.group, x, prob)
+        dev = [(torch.from_numpy(sc.view(np.int16).copy()).cuda(), torch.from_numpy(pk.copy()).cuda())
+               for sc, pk in recs]
+        xd = torch.from_numpy(x).cuda()
+        scratch = torch.empty(s.m + s.d, dtype=torch.float32, device="cuda")
+        j = _lib.ExpertJob(_lib.ptr(dev[0][1]), _lib.ptr(dev[0][0]), _lib.ptr(dev[1][1]), _lib.ptr(dev[1][0]),
+                           _lib.ptr(dev[2][1]), _lib.ptr(dev[2][0]), s.m, s.d, s.d, s.m, layer.group,
+                           _lib.ptr(xd), _lib.ptr(scratch), prob)
+        _lib.check(_lib.lib().jm_expert_job(ctypes.byref(j), _lib.stream_handle()), "jm_expert_job")
+        got = scratch.cpu().numpy()
+        assert _rel(got[None, :s.m], ref[None, :s.m]) <= TOL
+        assert _rel(got[None, s.m:], ref[None, s.m:]) <= TOL
 
 
 # Decode-path shapes beyond the two model shapes: rows of 16 lanes
