@@ -588,6 +588,19 @@ def probe_costs() -> dict:
         ho[str(nblk)] = {"plain_us": plain, "handoff_us": f.value, "handoff_cost_us": f.value - plain}
         log(f"probe: {nblk} blocks, launch {plain:.2f} us, with the hand-off {f.value:.2f} us")
     res["handoff_by_blocks"] = ho
+    # the stream ceilings of the B=8 block's two expert kernels: their
+    # algorithmic bytes (gate/up and down records of 51.7 routed experts)
+    # read by waves of 16 KiB, from HBM
+    P.jmp_stream.argtypes = [ctypes.c_ulonglong, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                             ctypes.POINTER(ctypes.c_float)]
+    st = {}
+    for name, nbytes in (("gateup_86MB", 86 * 1024 * 1024), ("down_43MB", 43 * 1024 * 1024)):
+        for wb in (16384, 8192, 4096):
+            chk(P.jmp_stream(nbytes, wb, 16, 64, ctypes.byref(f)))
+            st[f"{name}_wave{wb // 1024}K"] = {"us": f.value, "GBs": nbytes / (f.value * 1e-6) / 1e9}
+            log(f"probe: stream {name}, {wb // 1024} KiB per wave: {f.value:.2f} us "
+                f"({nbytes / (f.value * 1e-6) / 1e9:.0f} GB/s)")
+    res["stream"] = st
     log(f"probe: dependent launch {res['dependent_launch_us']:.2f} us, graph-replayed "
         f"{res['graph_replayed_launch_us']:.2f} us")
     return res

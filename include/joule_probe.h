@@ -31,6 +31,13 @@ int jmp_launch_chain(int n, int use_graph, int reps, float* us_per_launch);
  * receives the last-block sum (nblk * per_block with the hand-off on). */
 int jmp_handoff(int nblk, int per_block, int handoff, int reps, float* us_per_launch, float* total);
 
+/* A plain read stream: nbytes (a multiple of 4 * wave_bytes, at most
+ * 4 GiB) read by waves of 64 lanes, each wave one contiguous piece of
+ * wave_bytes (4096, 8192 or 16384) with every load in flight at once; reps
+ * launches rotate over `regions` copies (at most 16, 6 GiB in all) so that
+ * the bytes come from HBM.  *us_per_launch = elapsed / reps. */
+int jmp_stream(unsigned long long nbytes, int wave_bytes, int regions, int reps, float* us_per_launch);
+
 #ifdef __cplusplus
 }
 #endif

@@ -111,7 +111,9 @@ struct RouteArgs {
 };
 // from this many tokens the router serves 4 tokens per block from one read
 // of each group's table (k_router_quad)
+#ifndef JM_ROUTER_QUAD_MIN_B
 #define JM_ROUTER_QUAD_MIN_B 64
+#endif
 // router scores + x digits (one wave per expert group and token), then the
 // top-k of every token (unless skip_topk)
 hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st);

@@ -9,6 +9,10 @@
 //                     as the block's router -> gate/up -> down), timed with
 //                     HIP events; optionally captured once into a HIP graph
 //                     and replayed.  Result: microseconds per launch.
+//   jmp_stream        a plain read stream of nbytes, each wave reading its
+//                     own contiguous piece (the expert kernels' pattern),
+//                     rotating over regions copies so that no launch finds
+//                     its bytes in a cache; microseconds per launch.
 //   jmp_handoff       one launch of nblk blocks of 256 threads.  Each block
 //                     sums its slice of a buffer and stores its partial; with
 //                     the hand-off on, each block then issues a release fence
@@ -78,6 +82,34 @@ __global__ void __launch_bounds__(HT) k_handoff(const float* __restrict__ src, i
         // every block has taken its ticket: reset it for the next launch
         __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+// Stream: each wave reads its WB-byte piece of src (64 lanes x 16 bytes
+// per load, every load issued before any is used) and stores one word, so
+// that the loads stay live.  The plain read stream of a kernel whose waves
+// each own a contiguous piece, as the expert kernels' wave items do.
+template <int NLD>
+__global__ void __launch_bounds__(256) k_stream(const uint4* __restrict__ src, unsigned* __restrict__ out) {
+    const size_t wave = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const uint4* p = src + wave * NLD * 64 + lane;
+    uint4 v[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; i++) v[i] = p[(size_t)i * 64];
+    unsigned x = 0;
+#pragma unroll
+    for (int i = 0; i < NLD; i++) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    // every lane's loads feed the stored word (a word stored by lane 0 of
+    // its own loads only would let the compiler sink the loads into the
+    // store's branch)
+    for (int o = 32; o > 0; o >>= 1) x ^= (unsigned)__shfl_xor((int)x, o);
+    if (lane == 0) out[wave] = x;
+}
+
+// distinct words everywhere (a multiplicative hash of the index)
+__global__ void k_fill(unsigned* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = (unsigned)(i * 2654435761ull) ^ (unsigned)(i >> 29);
 }
 
 thread_local char g_err[256];
@@ -201,6 +233,58 @@ int jmp_handoff(int nblk, int per_block, int handoff, int reps, float* us_per_la
     if (part) (void)hipFree(part);
     if (out) (void)hipFree(out);
     if (ticket) (void)hipFree(ticket);
+    return rc;
+}
+
+int jmp_stream(unsigned long long nbytes, int wave_bytes, int regions, int reps, float* us_per_launch) {
+    if (wave_bytes != 4096 && wave_bytes != 8192 && wave_bytes != 16384) {
+        snprintf(g_err, sizeof g_err, "wave_bytes must be 4096, 8192 or 16384");
+        return -1;
+    }
+    const unsigned long long per_block = 4ull * (unsigned long long)wave_bytes;
+    if (nbytes == 0 || nbytes % per_block || nbytes > (1ull << 32) || regions < 1 || regions > 16 ||
+        nbytes * (unsigned long long)regions > (6ull << 30) || reps < 1 || !us_per_launch) {
+        snprintf(g_err, sizeof g_err, "bad arguments");
+        return -1;
+    }
+    const unsigned nblk = (unsigned)(nbytes / per_block);
+    char* src = nullptr;
+    unsigned* out = nullptr;
+    hipStream_t st = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0.0f;
+    auto run = [&]() -> int {
+        PCHECK(hipMalloc(&src, nbytes * regions));
+        PCHECK(hipMalloc(&out, (size_t)nblk * 4 * sizeof(unsigned)));
+        hipLaunchKernelGGL(k_fill, dim3(4096), dim3(256), 0, nullptr, (unsigned*)src, (size_t)(nbytes * regions / 4));
+        PCHECK(hipGetLastError());
+        PCHECK(hipDeviceSynchronize());
+        PCHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+        PCHECK(hipEventCreate(&e0));
+        PCHECK(hipEventCreate(&e1));
+        auto launch = [&](int r) {
+            const uint4* s4 = (const uint4*)(src + (size_t)(r % regions) * nbytes);
+            if (wave_bytes == 4096) hipLaunchKernelGGL(k_stream<4>, dim3(nblk), dim3(256), 0, st, s4, out);
+            else if (wave_bytes == 8192) hipLaunchKernelGGL(k_stream<8>, dim3(nblk), dim3(256), 0, st, s4, out);
+            else hipLaunchKernelGGL(k_stream<16>, dim3(nblk), dim3(256), 0, st, s4, out);
+        };
+        for (int r = 0; r < regions; r++) launch(r);
+        PCHECK(hipGetLastError());
+        PCHECK(hipStreamSynchronize(st));
+        PCHECK(hipEventRecord(e0, st));
+        for (int r = 0; r < reps; r++) launch(r);
+        PCHECK(hipEventRecord(e1, st));
+        PCHECK(hipEventSynchronize(e1));
+        PCHECK(hipEventElapsedTime(&ms, e0, e1));
+        *us_per_launch = ms * 1e3f / (float)reps;
+        return 0;
+    };
+    const int rc = run();
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (st) (void)hipStreamDestroy(st);
+    if (src) (void)hipFree(src);
+    if (out) (void)hipFree(out);
     return rc;
 }
 

@@ -49,7 +49,7 @@ def test_probe_library_exports_header_symbols():
         pytest.skip("libjoule_probe.so not built (run python -m joule_amd.build)")
     text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "joule_probe.h").read_text(), flags=re.S)
     declared = sorted(set(re.findall(r"\b(jmp_[a-z0-9_]+)\s*\(", text)))
-    assert declared == ["jmp_handoff", "jmp_last_error", "jmp_launch_chain"]
+    assert declared == ["jmp_handoff", "jmp_last_error", "jmp_launch_chain", "jmp_stream"]
     syms = subprocess.run(["nm", "-D", "--defined-only", str(PROBE_OUT)], capture_output=True,
                           text=True, check=True).stdout
     exported = set(re.findall(r"\bT (jmp_[a-z0-9_]+)", syms))
@@ -58,6 +58,9 @@ def test_probe_library_exports_header_symbols():
     f = ctypes.c_float()
     assert P.jmp_launch_chain(0, 0, 1, ctypes.byref(f)) == -1      # argument check, no GPU work
     assert P.jmp_handoff(0, 1, 0, 1, ctypes.byref(f), None) == -1
+    P.jmp_stream.argtypes = [ctypes.c_ulonglong, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                             ctypes.POINTER(ctypes.c_float)]
+    assert P.jmp_stream(1000, 16384, 1, 1, ctypes.byref(f)) == -1
 
 
 def test_kernel_cfg_layout():
