@@ -308,7 +308,7 @@ struct TokSrc {
 // stage c - 1's scale epilogue (products alternate by stage parity), so
 // each wave has independent MFMA and VALU work at every point.  At each
 // token phase boundary the block restages the tokens (two barriers).
-template <int G>
+template <int G, bool AHEAD = true>
 __device__ __forceinline__ void wave_product(floatx16& acc, WStream<G>& ws, uint8_t* wl, int8_t* q,
                                              const float* s, const int* cc, const TokSrc& ts, const Lay& ly) {
     constexpr int NG = 64 / G;                    // groups per stage
@@ -323,6 +323,12 @@ __device__ __forceinline__ void wave_product(floatx16& acc, WStream<G>& ws, uint
     AOps ab[2];
     IOps<G> pr[PIPE ? 2 : 1];
     float wsp[PIPE ? 2 : 1][NG];
+    // AHEAD (G = 64): the next stage's weight operands (within a
+    // super-stage) and this stage's token scales (for the epilogue of the
+    // stage before) are requested one stage ahead, so that the stage's
+    // MFMAs and epilogue wait on no LDS read of their own stage
+    int4v bn0, bn1;
+    SxOps sxn;
     const int nph = (nss + sspp - 1) / sspp;
 #pragma unroll 1
     for (int ph = 0; ph < nph; ph++) {
@@ -339,31 +345,43 @@ __device__ __forceinline__ void wave_product(floatx16& acc, WStream<G>& ws, uint
         const typename WStream<G>::ScT scs = ws.advance(wbuf, S + 2);
         const int cp = (S % sspp) * SSC;          // the super-stage's first column within the phase
         if (PIPE && pstart) ab[0] = load_aops<G>(qh, ql, cp, h);
+        if (PIPE && AHEAD) load_bops<G>(wbuf, n, h, 0, bn0, bn1);
 #pragma unroll
         for (int cs = 0; cs < 4; cs++) {
-            // keep each stage's instructions within the stage: the operands
-            // of the next stage are already requested explicitly, and
-            // hoisting more would cost registers
             __builtin_amdgcn_sched_barrier(0);
             const int c = 4 * S + cs;             // stage index over K
             const int cur = cs & 1, prv = cur ^ 1;
-            if (!PIPE) ab[cur] = load_aops<G>(qh, ql, cp + 64 * cs, h);
-            else if (!(cs == 3 && pend)) ab[prv] = load_aops<G>(qh, ql, cp + 64 * (cs + 1), h);
-            SxOps sxp;
-            if (PIPE && c > 0) sxp = load_sx(s, c - 1, h);
-            int4v b0, b1;
-            load_bops<G>(wbuf, n, h, cs, b0, b1);
             const int pc = PIPE ? cur : 0, pp = PIPE ? prv : 0;
-            // the lo accumulators start at the groups' corrections (pr[pc]'s
-            // previous products went through their epilogue already)
-#pragma unroll
-            for (int u = 0; u < NG; u++) pr[pc].il[u] = load_corr(cc, NG * c + u, h);
-            stage_mfma<G>(pr[pc], ab[cur], b0, b1);
-#pragma unroll
-            for (int u = 0; u < NG; u++) wsp[pc][u] = sc_at<G>(scs, NG * cs + u);
-            if (PIPE) {
+            if (PIPE && !AHEAD) {
+                if (!(cs == 3 && pend)) ab[prv] = load_aops<G>(qh, ql, cp + 64 * (cs + 1), h);
+                SxOps sxp;
+                if (c > 0) sxp = load_sx(s, c - 1, h);
+                int4v b0, b1;
+                load_bops<G>(wbuf, n, h, cs, b0, b1);
+                pr[pc].il[0] = load_corr(cc, c, h);
+                stage_mfma<G>(pr[pc], ab[cur], b0, b1);
+                wsp[pc][0] = sc_at<G>(scs, cs);
+                if (c > 0) group_acc(acc, pr[pp].ih[0], pr[pp].il[0], sxp, wsp[pp][0]);
+            } else if (PIPE) {
+                const int4v b0 = bn0, b1 = bn1;
+                pr[pc].il[0] = load_corr(cc, c, h);
+                const SxOps sxp = sxn;
+                // requests for the next stage
+                if (!(cs == 3 && pend)) ab[prv] = load_aops<G>(qh, ql, cp + 64 * (cs + 1), h);
+                if (cs < 3) load_bops<G>(wbuf, n, h, cs + 1, bn0, bn1);
+                sxn = load_sx(s, c, h);
+                stage_mfma<G>(pr[pc], ab[cur], b0, b1);
+                wsp[pc][0] = sc_at<G>(scs, cs);
                 if (c > 0) group_acc(acc, pr[pp].ih[0], pr[pp].il[0], sxp, wsp[pp][0]);
             } else {
+                ab[cur] = load_aops<G>(qh, ql, cp + 64 * cs, h);
+                int4v b0, b1;
+                load_bops<G>(wbuf, n, h, cs, b0, b1);
+#pragma unroll
+                for (int u = 0; u < NG; u++) pr[0].il[u] = load_corr(cc, NG * c + u, h);
+                stage_mfma<G>(pr[0], ab[cur], b0, b1);
+#pragma unroll
+                for (int u = 0; u < NG; u++) wsp[0][u] = sc_at<G>(scs, NG * cs + u);
 #pragma unroll
                 for (int u = 0; u < NG; u++)
                     group_acc(acc, pr[0].ih[u], pr[0].il[u], load_sx(s, NG * c + u, h), wsp[0][u]);
@@ -373,7 +391,7 @@ __device__ __forceinline__ void wave_product(floatx16& acc, WStream<G>& ws, uint
     }
     if (PIPE) {
         // the last stage's epilogue (stage 4 nss - 1 is odd: its products sit in buffer 1)
-        group_acc(acc, pr[PIPE ? 1 : 0].ih[0], pr[PIPE ? 1 : 0].il[0], load_sx(s, 4 * nss - 1, h),
+        group_acc(acc, pr[PIPE ? 1 : 0].ih[0], pr[PIPE ? 1 : 0].il[0], AHEAD ? sxn : load_sx(s, 4 * nss - 1, h),
                   wsp[PIPE ? 1 : 0][0]);
     }
 }
@@ -556,7 +574,8 @@ k_q4_gemm_mfma(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ 
 #pragma unroll 1
     for (int pass = 0; pass < npass; pass++) {
         floatx16 acc = {};
-        wave_product<G>(acc, ws, wl, q, s, cc, TokSrc{xqh, xql, tok, d}, ly);
+        // (operands one stage ahead would spill this kernel's registers)
+        wave_product<G, false>(acc, ws, wl, q, s, cc, TokSrc{xqh, xql, tok, d}, ly);
         const int r = row;
         if (pass + 1 < npass) row = start(pass + 1);
 #pragma unroll
