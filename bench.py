@@ -58,8 +58,8 @@ ZIPF_ALPHA = 0.28              # Zipf(1.1) bias strength: per-expert counts abou
 # FETCH_SIZE reports half of the copied bytes (factor 2.0), WRITE_SIZE all of
 # them (factor 1.0).
 BLOCK_PMC = {"batch": 8, "group": 64, "layers": 16,
-             "fetch_kib": {"k_router_grp": 570.0, "k_topk": 27.5, "k_gateup": 42100.9, "k_down_comb": 21833.5},
-             "write_kib": {"k_router_grp": 44.0, "k_topk": 0.5, "k_gateup": 338.8, "k_down_comb": 64.0},
+             "fetch_kib": {"k_router_grp": 573.0, "k_topk": 27.5, "k_gateup": 42110.5, "k_down_comb": 21816.4},
+             "write_kib": {"k_router_grp": 44.0, "k_topk": 0.5, "k_gateup": 338.9, "k_down_comb": 64.0},
              "fetch_factor": 2.0, "write_factor": 1.0,
              "source": "profiles/pmc_traffic_qwen3_b8.md"}
 
