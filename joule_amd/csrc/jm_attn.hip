@@ -332,6 +332,8 @@ __device__ __forceinline__ float head_reduce16(float (&v)[QPK]) {
     }
 }
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ float bf16_round(float f) { return __uint_as_float(f32_to_bf16_rne(f) << 16); }
 
 // Four consecutive projection values of one token (rows row .. row + 3 of
@@ -593,7 +595,8 @@ k_attn_part(AttnArgs a) {
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) qb[kk] = __builtin_bit_cast(bf16x8, qr[kk]);
 
-    // ---- scores: q . k / sqrtf_fast(hd)
+    // ---- scores: q . k / sqrtf_fast(hd), as q . k times the divisor's
+    // reciprocal (within an ulp of the division)
     floatx4 sacc[2];
 #pragma unroll
     for (int mt = 0; mt < 2; mt++) {
@@ -612,7 +615,7 @@ k_attn_part(AttnArgs a) {
             const float c = sacc[mt][i];
             const float tot = __fadd_rn(c, dpp_f<DPP_ROR8>(c));
             const int t = tw + 16 * mt + 4 * g + i;
-            const float sc = t < T ? __fdiv_rn(tot, a.sdiv) : -INFINITY;
+            const float sc = t < T ? __fmul_rn(tot, a.rsdiv) : -INFINITY;
             sv[4 * mt + i] = sc;
             mx = fmaxf(mx, sc);
         }
@@ -652,10 +655,12 @@ k_attn_part(AttnArgs a) {
         uint32_t vb[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
+            // two 16-bit reads straight into the low and high halves
             const int j0 = 2 * i, j1 = 2 * i + 1;
-            const uint32_t e0 = vw[(16 * (j0 >> 2) + 4 * g + (j0 & 3)) * VR + 16 * nt + n];
-            const uint32_t e1 = vw[(16 * (j1 >> 2) + 4 * g + (j1 & 3)) * VR + 16 * nt + n];
-            vb[i] = e0 | (e1 << 16);
+            u16x2 e;
+            e.x = vw[(16 * (j0 >> 2) + 4 * g + (j0 & 3)) * VR + 16 * nt + n];
+            e.y = vw[(16 * (j1 >> 2) + 4 * g + (j1 & 3)) * VR + 16 * nt + n];
+            vb[i] = __builtin_bit_cast(uint32_t, e);
         }
         oacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             pa, __builtin_bit_cast(bf16x8, make_uint4(vb[0], vb[1], vb[2], vb[3])),
@@ -682,24 +687,33 @@ k_attn_part(AttnArgs a) {
     }
     __syncthreads();
 
-    // ---- the waves merged with the split's max
+    // ---- the waves merged with the split's max: thread tid takes head
+    // tid / 32, dimensions 4 (tid % 32) .. + 3, so that each thread forms
+    // the 4 waves' factors of one head once
     float* po = a.part_o + (((size_t)b * a.KH + kh) * a.S + s) * QPK * HD;
-    for (int oi = tid; oi < QPK * HD; oi += 256) {
-        const int h = oi / HD;
-        const float M = fmaxf(fmaxf(mls[0][h][0], mls[1][h][0]), fmaxf(mls[2][h][0], mls[3][h][0]));
-        float O = 0.0f, L = 0.0f;
+    {
+        const int h = tid >> 5, oi = h * HD + 4 * (tid & 31);
+        if (h < QPK) {
+            const float M = fmaxf(fmaxf(mls[0][h][0], mls[1][h][0]), fmaxf(mls[2][h][0], mls[3][h][0]));
+            float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float L = 0.0f;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) {
-            const float m = mls[ww][h][0];
-            const float f = m == -INFINITY ? 0.0f : expf_fast(__fsub_rn(m, M));
-            O = __builtin_fmaf(red[ww][oi], f, O);
-            L = __builtin_fmaf(mls[ww][h][1], f, L);
-        }
-        po[oi] = O;
-        if (oi % HD == 0) {
-            float* ml = a.part_ml + ((((size_t)b * a.KH + kh) * a.S + s) * QPK + h) * 2;
-            ml[0] = M;
-            ml[1] = L;
+            for (int ww = 0; ww < 4; ww++) {
+                const float m = mls[ww][h][0];
+                const float f = m == -INFINITY ? 0.0f : expf_fast(__fsub_rn(m, M));
+                const float4 r = *(const float4*)&red[ww][oi];
+                O.x = __builtin_fmaf(r.x, f, O.x);
+                O.y = __builtin_fmaf(r.y, f, O.y);
+                O.z = __builtin_fmaf(r.z, f, O.z);
+                O.w = __builtin_fmaf(r.w, f, O.w);
+                L = __builtin_fmaf(mls[ww][h][1], f, L);
+            }
+            *(float4*)(po + oi) = O;
+            if ((tid & 31) == 0) {
+                float* ml = a.part_ml + ((((size_t)b * a.KH + kh) * a.S + s) * QPK + h) * 2;
+                ml[0] = M;
+                ml[1] = L;
+            }
         }
     }
 }

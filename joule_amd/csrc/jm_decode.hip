@@ -177,7 +177,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         at.nqkv = nqkv; at.H = H; at.KH = KH; at.B = B;
         at.qn = c->qk_norm_type == 1 ? W->qn + (size_t)l * HD : nullptr;
         at.kn = c->qk_norm_type == 1 ? W->kn + (size_t)l * HD : nullptr;
-        at.eps = c->eps; at.sdiv = sdiv;
+        at.eps = c->eps; at.rsdiv = 1.0f / sdiv;
         at.cos = W->cos; at.sin = W->sin;
         at.pos = pos_dev; at.kv = s->tab; at.L = L; at.layer = l;
         at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;

@@ -205,7 +205,7 @@ struct AttnArgs {
     const uint16_t* qn;       // [128] bf16 per-head q norm of the layer, or NULL
     const uint16_t* kn;       // [128] bf16 per-head k norm, or NULL
     float eps;
-    float sdiv;               // score divisor sqrtf_fast(128)
+    float rsdiv;              // 1 / the score divisor sqrtf_fast(128)
     const float* cos;         // [maxT][128]
     const float* sin;
     const int* pos;           // [B] position each token writes (T = pos + 1)
