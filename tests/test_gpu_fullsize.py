@@ -179,7 +179,13 @@ def test_decode_48_layers_matches_oracle(full):
     want = oracle.decode_layers_batch(x, positions, kv_h, trace=trace, n_threads=8,
                                       progress=lambda l: print(f"  oracle layer {l}", flush=True) if l % 8 == 7 else None)
 
-    # top-k per layer: equal, or the oracle's own selection is a near-tie
+    errs = {n: _rel(hid_n[n], trace[n - 1]["hidden"]) for n in depths}
+    for n in depths:
+        print(f"  error after {n:2d} layers, per token: {np.array2string(errs[n], precision=2)}", flush=True)
+
+    # top-k per layer: equal, or the oracle's own selection is a near-tie.  A
+    # token whose selection flipped at a near-tie runs through other experts
+    # from there on, so its later layers are not compared.
     flipped = np.zeros(B, bool)
     flips = []
     for l in range(L48):
@@ -187,13 +193,15 @@ def test_decode_48_layers_matches_oracle(full):
         diff = np.any(gtop[l] != otop, axis=1)
         if l == 0:
             assert not diff.any(), "layer 0 router input is bit-exact: its top-k must match"
-        if diff.any():
-            mg = _margins(trace[l]["moe_in"][diff], full.gw[l], s.topk, s.renorm)
-            flips.append((l, np.flatnonzero(diff).tolist(), mg.tolist()))
+        new = diff & ~flipped
+        if new.any():
+            mg = _margins(trace[l]["moe_in"][new], full.gw[l], s.topk, s.renorm)
+            flips.append((l, np.flatnonzero(new).tolist(), mg.tolist()))
+            print(f"  layer {l}: top-k flip of tokens {np.flatnonzero(new).tolist()} at margins {mg.tolist()}",
+                  flush=True)
             assert np.all(mg < MARGIN), f"layer {l}: top-k differs beyond a near-tie (margins {mg})"
-            flipped |= diff
+            flipped |= new
     keep = ~flipped
-    errs = {n: _rel(hid_n[n], trace[n - 1]["hidden"]) for n in depths}
     for n in depths:
         print(f"  error after {n:2d} layers: max {errs[n][keep].max():.3e}, median {np.median(errs[n][keep]):.3e}",
               flush=True)
