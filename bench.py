@@ -177,8 +177,8 @@ def zipf_block(store, gw, steps, n_layers, bz=512):
     xz_np = apply_logit_bias(gw[0], xz_np, bias)[1]
     xz = torch.from_numpy(xz_np).cuda()
     store.set_router(torch.from_numpy(gz).cuda())
-    nz = max(steps // 8, 20)
-    m2, st2, U2 = measure(store, gz, xz, nz, 5, n_layers)
+    nz = max(steps // 2, 100)
+    m2, st2, U2 = measure(store, gz, xz, nz, 10, n_layers, stage_steps=min(nz, 50))
     r = block_numbers(shape, G, bz, m2, st2, U2, nz, n_layers, rb)
     top = torch.empty((bz, shape.topk), dtype=torch.int32, device="cuda")
     store.layer_ffn_batch(0, xz, topk_idx=top)

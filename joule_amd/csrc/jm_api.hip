@@ -149,7 +149,7 @@ int check_group_shape(int d, int m, int group) {
 namespace {
 
 // Sizes of the Ws fields for B tokens, in field order.
-constexpr int WS_NF = 26;
+constexpr int WS_NF = 27;
 void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
     const int E = s->E, d = s->d, m = s->m, k = s->topk, G = s->group;
     const size_t nslot = (size_t)B * k;
@@ -170,7 +170,8 @@ void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
         nslot * 4,                    // comb
         (size_t)E * sizeof(jm::ExpertWork),   // work table
         max_tiles * 8,                // dense tiles
-        4,                            // n_tiles
+        8,                            // n_tiles (tiles, small experts)
+        (size_t)E * 4,                // small
         nslot * m * 4,                // act
         nslot * words_m * 4,          // adig
         nslot * (m / 32) * 4,         // ascale
@@ -204,7 +205,7 @@ void jm::ws_layout(const jm_store* s, int B, char* base, Ws* w) {
                            (void**)&w->xscale, (void**)&w->seg_off, (void**)&w->seg_slot,
                            (void**)&w->active, (void**)&w->n_active, (void**)&w->first_slot,
                            (void**)&w->comb, (void**)&w->work, (void**)&w->tiles,
-                           (void**)&w->n_tiles, (void**)&w->act, (void**)&w->adig,
+                           (void**)&w->n_tiles, (void**)&w->small, (void**)&w->act, (void**)&w->adig,
                            (void**)&w->ascale, (void**)&w->y, (void**)&w->aqh, (void**)&w->aql,
                            (void**)&w->xqh, (void**)&w->xql, (void**)&w->xqs, (void**)&w->aqs,
                            (void**)&w->xqc, (void**)&w->aqc};
@@ -263,7 +264,7 @@ int stage_setup(jm_store* s, int layer, const int32_t* top, int B, const char* w
     r->work = w.work; r->umax = std::min(E, nslot); r->rec = s->rec;
     r->key0 = (long long)layer * E;
     r->dense_min = 0x7FFFFFFF;                  // no MFMA tiles
-    r->tiles = w.tiles; r->n_tiles = w.n_tiles;
+    r->tiles = w.tiles; r->n_tiles = w.n_tiles; r->small = w.small;
     JM_HIP(jm::launch_dispatch_work(*r, st), "dispatch launch");
     a->blob = s->blob; a->rec = s->rec; a->key0 = r->key0; a->E = E;
     a->work = w.work; a->umax = r->umax; a->seg_slot = w.seg_slot;
@@ -272,7 +273,7 @@ int stage_setup(jm_store* s, int layer, const int32_t* top, int B, const char* w
     a->xdig = w.xdig; a->xscale = w.xscale;
     a->adig = w.adig; a->ascale = w.ascale;
     a->dense_min = 0x7FFFFFFF;
-    a->tiles = w.tiles; a->n_tiles = w.n_tiles;
+    a->tiles = w.tiles; a->n_tiles = w.n_tiles; a->small = w.small;
     return 0;
 }
 
@@ -304,7 +305,7 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     r.first_slot = w.first_slot; r.comb = w.comb;
     r.work = w.work; r.umax = umax; r.rec = s->rec;
     r.key0 = (long long)layer * E;
-    r.dense_min = s->dense_min; r.tiles = w.tiles; r.n_tiles = w.n_tiles;
+    r.dense_min = s->dense_min; r.tiles = w.tiles; r.n_tiles = w.n_tiles; r.small = w.small;
     r.skip_topk = dec && jm::gateup_topk(B, E);
     jm::ExpertArgs a;
     a.blob = s->blob; a.rec = s->rec; a.key0 = (long long)layer * E; a.E = E;
@@ -315,7 +316,7 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     a.act = w.act; a.adig = w.adig; a.ascale = w.ascale; a.y = w.y; a.out = out; a.resid = io.resid;
     a.dense_min = s->mfma_ok ? s->dense_min : 0x7FFFFFFF;
     r.dense_min = a.dense_min;
-    a.tiles = w.tiles; a.n_tiles = w.n_tiles;
+    a.tiles = w.tiles; a.n_tiles = w.n_tiles; a.small = w.small;
     const bool mfma = !dec && a.dense_min <= nslot;
     r.xqh = mfma ? w.xqh : nullptr; r.xql = w.xql; r.xqs = w.xqs; r.xqc = w.xqc;
     a.xqh = w.xqh; a.xql = w.xql; a.xqs = w.xqs; a.xqc = w.xqc;
@@ -330,22 +331,20 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     if (dec) {
         JM_HIP(jm::launch_gateup_dec(a, st), "gate/up launch");
     } else {
-        // the experts under dense_min (wave-item kernels: act digits, y rows
-        // of their slots) on the side stream, the MFMA experts (act hi/lo,
-        // their own y rows) here: disjoint slots and buffers
-        JM_HIP(hipEventRecord(s->fork_ev, st), "hipEventRecord fork");
-        JM_HIP(hipStreamWaitEvent(s->side_st, s->fork_ev, 0), "hipStreamWaitEvent fork");
-        JM_HIP(jm::launch_gateup(a, umax, s->side_st), "gate/up launch");
-        JM_HIP(jm::launch_down(a, umax, s->side_st), "down launch");
-        JM_HIP(hipEventRecord(s->join_ev, s->side_st), "hipEventRecord join");
-        JM_HIP(jm::launch_gateup_mfma(a, max_tiles, st), "gate/up MFMA launch");
+        if (mfma) {
+            // the MFMA kernels also run the experts under dense_min, as wave
+            // items on the blocks past their tiles (the grids' last round)
+            JM_HIP(jm::launch_gateup_mfma(a, max_tiles, st), "gate/up MFMA launch");
+        } else {
+            JM_HIP(jm::launch_gateup(a, umax, st), "gate/up launch");
+        }
     }
     JM_MARK(2);
     if (dec) {
         JM_HIP(jm::launch_down_comb(a, st), "down/combine launch");
     } else {
-        JM_HIP(jm::launch_down_mfma(a, max_tiles, st), "down MFMA launch");
-        JM_HIP(hipStreamWaitEvent(st, s->join_ev, 0), "hipStreamWaitEvent join");
+        if (mfma) JM_HIP(jm::launch_down_mfma(a, max_tiles, st), "down MFMA launch");
+        else JM_HIP(jm::launch_down(a, umax, st), "down launch");
         JM_HIP(jm::launch_combine(w.y, w.comb, B, k, d, io.resid, out, st), "combine launch");
     }
     JM_MARK(3);
@@ -458,13 +457,6 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
         delete s;
         return rc;
     }
-    e = hipStreamCreateWithFlags(&s->side_st, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&s->fork_ev, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&s->join_ev, hipEventDisableTiming);
-    if (e != hipSuccess) {
-        jm_store_destroy(s);
-        return hip_fail(e, "jm_store_create side stream");
-    }
     *out = s;
     return 0;
 }
@@ -478,9 +470,6 @@ int jm_store_destroy(jm_store* s) {
     if (s->ws) (void)hipFree(s->ws);
     if (s->prof)
         for (int i = 0; i <= JM_STAGES; i++) (void)hipEventDestroy(s->ev[i]);
-    if (s->side_st) (void)hipStreamDestroy(s->side_st);
-    if (s->fork_ev) (void)hipEventDestroy(s->fork_ev);
-    if (s->join_ev) (void)hipEventDestroy(s->join_ev);
     jm::decode_free_all(s);
     delete s;
     return 0;

@@ -60,7 +60,8 @@ struct ExpertArgs {
     // dispatch path, dense branch
     int dense_min;            // experts with at least this many slots take the MFMA kernels
     const int2* tiles;        // [max tiles] (work entry, token tile) of the dense experts
-    const int* n_tiles;       // [1] how many
+    const int* n_tiles;       // [2] how many tiles; how many experts under dense_min (small)
+    const int* small;         // [umax] work-table entries of the experts with 1..dense_min-1 slots
     int8_t* aqh;              // [B*k][m] act as int8 digit pairs for the MFMA down
     int8_t* aql;
     float* aqs;               // [B*k][m/G] their scales
@@ -106,7 +107,8 @@ struct RouteArgs {
     long long key0;           // layer*E
     int dense_min;            // dispatch path: slots from which an expert takes the MFMA kernels
     int2* tiles;              // dense tiles (work entry, token tile), in work-table order
-    int* n_tiles;             // [1]
+    int* n_tiles;             // [2] dense tiles; experts under dense_min
+    int* small;               // [umax] work-table entries of the experts under dense_min
     int skip_topk;            // 1: the top-k runs in the gate/up kernel
 };
 // from this many tokens the router serves 4 tokens per block from one read
@@ -146,7 +148,9 @@ hipError_t launch_down_comb(const ExpertArgs& a, hipStream_t st);
 // dispatch path: gate/up and down over the work table, then the combine
 hipError_t launch_gateup(const ExpertArgs& a, int umax, hipStream_t st);
 hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st);
-// dense branch: grids of max_tiles x (row blocks); blocks past *n_tiles exit.
+// dense branch: 1-D grids of (max_tiles + 1) x (row blocks); the blocks past
+// n_tiles[0] x (row blocks) run the wave items of the n_tiles[1] experts under
+// dense_min (the small list), so no other launch is needed for them.
 // mfma_shape_ok: d and the intermediate multiples of 256, up to 2048, and at
 // most 1024 or a multiple of 1024 (the tile's token digits stay in LDS one
 // 1024-column phase at a time); otherwise the GEMV kernels take every expert

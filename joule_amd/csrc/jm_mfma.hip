@@ -36,6 +36,7 @@
 #include <type_traits>
 
 #include "jm_device.h"
+#include "jm_items.h"
 #include "jm_kernels.h"
 
 namespace jm {
@@ -74,14 +75,14 @@ struct TileInfo {
     int e;          // expert id
 };
 
-__device__ __forceinline__ bool tile_info(const ExpertArgs& a, int t, TileInfo* ti) {
-    if (t >= *a.n_tiles) return false;
+__device__ __forceinline__ TileInfo tile_at(const ExpertArgs& a, int t) {
     const int2 tl = a.tiles[t];
     const ExpertWork wk = a.work[tl.x];
-    ti->slot0 = wk.s0 + tl.y * MT;
-    ti->nt = min(MT, wk.n - tl.y * MT);
-    ti->e = wk.e;
-    return true;
+    TileInfo ti;
+    ti.slot0 = wk.s0 + tl.y * MT;
+    ti.nt = min(MT, wk.n - tl.y * MT);
+    ti.e = wk.e;
+    return ti;
 }
 
 // LDS layout of a block with contraction length K:
@@ -399,12 +400,12 @@ __device__ __forceinline__ void wave_product(floatx16& acc, WStream<G>& ws, uint
 // ------------------------------------------------------------------ gate/up
 
 template <int G>
-__device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo& ti, unsigned char* sm) {
+__device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo& ti, int rblk, unsigned char* sm) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int d = a.d, m = a.m, ng = d / G;
     const Lay ly(d, G);
     const int mat = w & 1, rq = w >> 1;           // this wave: gate (0) or up (1), rows 32 rq .. 32 rq + 31
-    const int r0 = blockIdx.y * GU_ROWS;          // the block's first intermediate row
+    const int r0 = rblk * GU_ROWS;                // the block's first intermediate row
     int8_t* q = (int8_t*)sm;
     float* s = (float*)(sm + ly.s);
     int* cc = (int*)(sm + ly.c);
@@ -465,23 +466,48 @@ __device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo&
     }
 }
 
-template <int G>
+// The experts under dense_min (n_tiles[1] entries of the small list) as
+// wave items, run by the blocks past the tiles (first = the first such
+// block, nblk = how many): virtual block v of 8 waves takes the 8
+// consecutive items 8 (v % vpe) + w of small entry v / vpe.  The blocks are
+// dispatched after the tiles' and fill the grid's last round.  The grid
+// always has at least (row blocks) x (small experts) of them: an expert
+// under dense_min frees a whole tile of max_tiles = slots / 32 + E.
+template <int G, int LPR>
+__device__ __forceinline__ void small_gateup(const ExpertArgs& a, int first, int nblk, unsigned char* sm) {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int vpe = a.m / wi::GU_ROWS / NWAVE;
+    const int nv = a.n_tiles[1] * vpe;
+    // per group of 4 waves, the act-scale slots of wi::gateup_item
+    float (*gm)[2][4] = (float (*)[2][4])sm;
+    int (*gb)[2][4] = (int (*)[2][4])(sm + 2 * sizeof(float[2][4]));
+#pragma unroll 1
+    for (int v = first; v < nv; v += nblk) {
+        wi::gateup_item<G, JM_NDIG, LPR, 1, false>(a, a.top, a.small[v / vpe], (v % vpe) * NWAVE + w, gm[w >> 2],
+                                                   gb[w >> 2]);
+        __syncthreads();                          // the slots serve the next item
+    }
+}
+
+// 1-D grid: block f < n_tiles x (m / GU_ROWS) is tile f % n_tiles, row
+// block f / n_tiles; the rest run the small experts' items.
+template <int G, int LPR>
 __global__ void __launch_bounds__(MTHREADS, 1)
 k_gateup_mfma(ExpertArgs a) {
-    TileInfo ti;
-    if (!tile_info(a, blockIdx.x, &ti)) return;
     extern __shared__ __align__(16) unsigned char sm[];
-    gateup_tile<G>(a, ti, sm);
+    const int nt = a.n_tiles[0], ntb = nt * (a.m / GU_ROWS);
+    const int f = blockIdx.x;
+    if (f < ntb) {
+        gateup_tile<G>(a, tile_at(a, f % nt), f / nt, sm);
+        return;
+    }
+    small_gateup<G, LPR>(a, f - ntb, (int)gridDim.x - ntb, sm);
 }
 
 // --------------------------------------------------------------------- down
 
 template <int G>
-__global__ void __launch_bounds__(MTHREADS, 1)
-k_down_mfma(ExpertArgs a) {
-    TileInfo ti;
-    if (!tile_info(a, blockIdx.x, &ti)) return;
-    extern __shared__ __align__(16) unsigned char sm[];
+__device__ __forceinline__ void down_tile(const ExpertArgs& a, const TileInfo& ti, int rblk, unsigned char* sm) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int d = a.d, m = a.m, ng = m / G;
     const Lay ly(m, G);
@@ -503,7 +529,7 @@ k_down_mfma(ExpertArgs a) {
     ws.rowb = m / 2;
     ws.nss = m / SSC;
     auto start = [&](int pass) __attribute__((always_inline)) {
-        const int wrow0 = blockIdx.y * DN_BLOCK_ROWS + pass * DN_ROWS + 32 * w;
+        const int wrow0 = rblk * DN_BLOCK_ROWS + pass * DN_ROWS + 32 * w;
         ws.wbase = a.blob + po + (size_t)wrow0 * (m / 2);
         ws.srow = a.blob + so + (size_t)(wrow0 + n) * ng * 2;
         ws.load(0, 0);
@@ -528,6 +554,32 @@ k_down_mfma(ExpertArgs a) {
             if (i < ti.nt) a.y[(size_t)tok[i] * d + r] = __fmul_rn(tws[i], acc[v]);
         }
     }
+}
+
+// The small experts' down items (wi::down_item, no barriers) on the blocks
+// past the tiles, 8 consecutive items of one entry per virtual block.
+template <int G, int LPR>
+__device__ __forceinline__ void small_down(const ExpertArgs& a, int first, int nblk) {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int vpe = a.d / wi::DN_ROWS / NWAVE;
+    const int nv = a.n_tiles[1] * vpe;
+#pragma unroll 1
+    for (int v = first; v < nv; v += nblk)
+        wi::down_item<G, JM_NDIG, LPR, 1>(a, a.small[v / vpe], (v % vpe) * NWAVE + w);
+}
+
+// 1-D grid as k_gateup_mfma's, with row blocks of DN_BLOCK_ROWS hidden rows.
+template <int G, int LPR>
+__global__ void __launch_bounds__(MTHREADS, 1)
+k_down_mfma(ExpertArgs a) {
+    extern __shared__ __align__(16) unsigned char sm[];
+    const int nt = a.n_tiles[0], ntb = nt * (a.d / DN_BLOCK_ROWS);
+    const int f = blockIdx.x;
+    if (f < ntb) {
+        down_tile<G>(a, tile_at(a, f % nt), f / nt, sm);
+        return;
+    }
+    small_down<G, LPR>(a, f - ntb, (int)gridDim.x - ntb);
 }
 
 // ------------------------------------------------------ plain Q4 product
@@ -629,9 +681,11 @@ hipError_t allow_lds() {
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= MAX_DEV) return hipErrorInvalidDevice;
     if (g_lds_set[dev].load(std::memory_order_acquire)) return hipSuccess;
-    const struct { const void* f; size_t b; } k[6] = {
-        {(const void*)k_gateup_mfma<64>, gateup_lds<64>(KMAX)}, {(const void*)k_gateup_mfma<32>, gateup_lds<32>(KMAX)},
-        {(const void*)k_down_mfma<64>, Lay(KMAX, 64).total}, {(const void*)k_down_mfma<32>, Lay(KMAX, 32).total},
+    const struct { const void* f; size_t b; } k[10] = {
+        {(const void*)k_gateup_mfma<64, 32>, gateup_lds<64>(KMAX)}, {(const void*)k_gateup_mfma<64, 64>, gateup_lds<64>(KMAX)},
+        {(const void*)k_gateup_mfma<32, 32>, gateup_lds<32>(KMAX)}, {(const void*)k_gateup_mfma<32, 64>, gateup_lds<32>(KMAX)},
+        {(const void*)k_down_mfma<64, 32>, Lay(KMAX, 64).total}, {(const void*)k_down_mfma<64, 64>, Lay(KMAX, 64).total},
+        {(const void*)k_down_mfma<32, 32>, Lay(KMAX, 32).total}, {(const void*)k_down_mfma<32, 64>, Lay(KMAX, 32).total},
         {(const void*)k_q4_gemm_mfma<64>, Lay(KMAX, 64).total}, {(const void*)k_q4_gemm_mfma<32>, Lay(KMAX, 32).total}};
     for (const auto& x : k) {
         e = hipFuncSetAttribute(x.f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)x.b);
@@ -643,25 +697,47 @@ hipError_t allow_lds() {
 
 }  // namespace
 
+// Lanes per row segment of the small experts' wave items: rows of C columns
+// (C / 32 chunks of 16 bytes; C <= KMAX, so one chunk per lane).
+static int item_lanes(int C) { return C / 32 <= 32 ? 32 : 64; }
+
+// Grids of max_tiles x (row blocks) blocks, one row of blocks more: the
+// blocks past the device's tile count run the small experts' wave items.
 hipError_t launch_gateup_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st) {
     if (max_tiles == 0) return hipSuccess;
     if (!mfma_shape_ok(a.d, a.m) || (a.group != 64 && a.group != 32)) return hipErrorInvalidValue;
+    if (!a.small || (a.m / wi::GU_ROWS) % NWAVE) return hipErrorInvalidValue;
     hipError_t e = allow_lds();
     if (e != hipSuccess) return e;
-    const dim3 grid((unsigned)max_tiles, (unsigned)(a.m / GU_ROWS));
-    if (a.group == 64) hipLaunchKernelGGL(k_gateup_mfma<64>, grid, dim3(MTHREADS), gateup_lds<64>(a.d), st, a);
-    else hipLaunchKernelGGL(k_gateup_mfma<32>, grid, dim3(MTHREADS), gateup_lds<32>(a.d), st, a);
+    const int rb = a.m / GU_ROWS;
+    const dim3 grid((unsigned)((max_tiles + 1) * rb));
+    const bool l64 = item_lanes(a.d) == 64;
+    if (a.group == 64) {
+        if (l64) hipLaunchKernelGGL((k_gateup_mfma<64, 64>), grid, dim3(MTHREADS), gateup_lds<64>(a.d), st, a);
+        else hipLaunchKernelGGL((k_gateup_mfma<64, 32>), grid, dim3(MTHREADS), gateup_lds<64>(a.d), st, a);
+    } else {
+        if (l64) hipLaunchKernelGGL((k_gateup_mfma<32, 64>), grid, dim3(MTHREADS), gateup_lds<32>(a.d), st, a);
+        else hipLaunchKernelGGL((k_gateup_mfma<32, 32>), grid, dim3(MTHREADS), gateup_lds<32>(a.d), st, a);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_down_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st) {
     if (max_tiles == 0) return hipSuccess;
     if (!mfma_shape_ok(a.d, a.m) || (a.group != 64 && a.group != 32)) return hipErrorInvalidValue;
+    if (!a.small || (a.d / wi::DN_ROWS) % NWAVE) return hipErrorInvalidValue;
     hipError_t e = allow_lds();
     if (e != hipSuccess) return e;
-    const dim3 grid((unsigned)max_tiles, (unsigned)(a.d / DN_BLOCK_ROWS));
-    if (a.group == 64) hipLaunchKernelGGL(k_down_mfma<64>, grid, dim3(MTHREADS), Lay(a.m, 64).total, st, a);
-    else hipLaunchKernelGGL(k_down_mfma<32>, grid, dim3(MTHREADS), Lay(a.m, 32).total, st, a);
+    const int rb = a.d / DN_BLOCK_ROWS;
+    const dim3 grid((unsigned)((max_tiles + 1) * rb));
+    const bool l64 = item_lanes(a.m) == 64;
+    if (a.group == 64) {
+        if (l64) hipLaunchKernelGGL((k_down_mfma<64, 64>), grid, dim3(MTHREADS), Lay(a.m, 64).total, st, a);
+        else hipLaunchKernelGGL((k_down_mfma<64, 32>), grid, dim3(MTHREADS), Lay(a.m, 64).total, st, a);
+    } else {
+        if (l64) hipLaunchKernelGGL((k_down_mfma<32, 64>), grid, dim3(MTHREADS), Lay(a.m, 32).total, st, a);
+        else hipLaunchKernelGGL((k_down_mfma<32, 32>), grid, dim3(MTHREADS), Lay(a.m, 32).total, st, a);
+    }
     return hipGetLastError();
 }
 

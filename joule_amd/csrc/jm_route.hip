@@ -424,18 +424,24 @@ k_dispatch_work(RouteArgs a) {
     if ((int)threadIdx.x < a.E) rec = load_expert_rec(a.rec, a.key0, threadIdx.x);
     dispatch_block(a.top, a.B * a.topk, a.E, a.topk, lds_i, a.seg_off, a.seg_slot, a.active,
                    a.n_active, a.first_slot, a.comb, a.work, a.umax, &rec);
-    // the dense experts' token tiles, in work-table order
+    // the dense experts' token tiles, in work-table order, and the list of
+    // the experts under dense_min (their wave items run on the MFMA grids)
     __syncthreads();
     const int u = threadIdx.x;
-    int ct = 0;
+    int ct = 0, sm = 0;
     if (u < a.umax) {
         const int n = a.work[u].n;
         ct = n >= a.dense_min ? (n + JM_DENSE_TILE - 1) / JM_DENSE_TILE : 0;
+        sm = n > 0 && n < a.dense_min;
     }
     uint2 tot;
-    const uint2 ex = block_exclusive_scan2(make_uint2((unsigned)ct, 0u), (unsigned*)lds_i, &tot);
+    const uint2 ex = block_exclusive_scan2(make_uint2((unsigned)ct, (unsigned)sm), (unsigned*)lds_i, &tot);
     for (int j = 0; j < ct; j++) a.tiles[ex.x + j] = make_int2(u, j);
-    if (threadIdx.x == 0) *a.n_tiles = (int)tot.x;
+    if (sm) a.small[ex.y] = u;
+    if (threadIdx.x == 0) {
+        a.n_tiles[0] = (int)tot.x;
+        a.n_tiles[1] = (int)tot.y;
+    }
 }
 
 hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {

@@ -27,7 +27,8 @@ struct Ws {
     int* comb;                  // [B*k]
     ExpertWork* work;           // [E]
     int2* tiles;                // [B*k/32 + E] dense tiles (dispatch path)
-    int* n_tiles;               // [1]
+    int* n_tiles;               // [2] dense tiles, experts under dense_min
+    int* small;                 // [E] work-table entries of the experts under dense_min
     float* act;                 // [B*k][m]
     uint32_t* adig;             // [B*k][m/8][NDIG] act digits
     float* ascale;              // [B*k][m/32]
@@ -122,11 +123,6 @@ struct jm_store {
     // per-layer attention / MoE split of the last decode call (jm_store_profile)
     int dprof_n;
     hipEvent_t* dev_marks;      // [2 L + 2]
-    // dispatch path: the small experts' wave-item chain (gate/up, down) runs
-    // on side_st beside the MFMA chain, forked after the dispatch and joined
-    // before the combine (default priority, like every stream here)
-    hipStream_t side_st;
-    hipEvent_t fork_ev, join_ev;
 };
 
 namespace jm {

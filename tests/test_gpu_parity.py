@@ -469,6 +469,32 @@ def test_block_dispatch_path_branches(qwen64, dense_min):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("B,dense_min", [(40, 2), (40, 4), (64, 4)])
+def test_block_small_experts_on_mfma_grid(qwen64, B, dense_min):
+    """The experts under dense_min run as wave items on the MFMA kernels'
+    blocks past their tiles.  With a low threshold most experts take a tile
+    and the surplus blocks are few (at least row blocks x small experts),
+    so each runs several virtual blocks of the small experts' items."""
+    banner(f"block B={B} dense_min={dense_min}: small experts on the MFMA grids")
+    x = activations(B, QWEN3.d, seed=4000 + B)
+    qwen64.store.set_dense_min(dense_min)
+    try:
+        out, top, tw = _run_block(qwen64, 0, x)
+        tiles = qwen64.store.dense_tiles()
+    finally:
+        qwen64.store.set_dense_min(0)
+    counts = np.bincount(top.ravel(), minlength=QWEN3.E)
+    small = int(sum(1 for c in counts if 0 < c < dense_min))
+    assert tiles == int(sum((c + TILE - 1) // TILE for c in counts if c >= dense_min))
+    assert small > 0 and tiles > 0
+    rout, rtop, rtw = qwen64.oracle(0).forward(x, n_threads=8)
+    assert np.array_equal(top, rtop) and np.array_equal(tw.view(np.uint32), rtw.view(np.uint32))
+    err = _rel(out, rout)
+    print(f"  B={B} dense_min={dense_min}: {tiles} tiles, {small} small experts, max rel err {err:.3e}",
+          flush=True)
+    assert err <= TOL
+
+
 def test_block_nan_tokens(qwen64):
     """A NaN token has NaN scores: every probability is NaN, no expert beats
     -1e30, its k slots get index -1 and it contributes nothing (the
