@@ -721,7 +721,12 @@ k_attn_part(AttnArgs a) {
 // Merge of the splits of one (query head, token): out = sum_s o_s e^(m_s - M)
 // / sum_s l_s e^(m_s - M), M the max over the splits.  The splits' weights
 // are computed in parallel (128 at a time) and staged in LDS; each thread
-// then sums its dimension over them with independent loads.
+// then sums its dimension over them with independent loads.  Up to
+// CMB_SR splits (4096 positions), every load is issued first (thread t:
+// split t's max and sum, and its dimension of every split), so the merge
+// waits for one memory round trip; the sums are the same, in the same order.
+constexpr int CMB_SR = 32;
+
 __global__ void __launch_bounds__(128)
 k_attn_comb(AttnArgs a, int qpk, float* __restrict__ att) {
     __shared__ float fs[128];
@@ -731,6 +736,34 @@ k_attn_comb(AttnArgs a, int qpk, float* __restrict__ att) {
     const int ns = (a.pos[b] + 128) / 128;          // splits of T = pos + 1 positions
     const size_t base = ((size_t)b * a.KH + kh) * a.S;
     const float* ml = a.part_ml + (base * qpk + hq) * 2;      // split s at ml[2 qpk s]
+    if (ns <= CMB_SR) {
+        const float* po = a.part_o + (base * qpk + hq) * 128 + t;
+        float pv[CMB_SR];
+#pragma unroll
+        for (int s = 0; s < CMB_SR; s++) pv[s] = s < ns ? po[(size_t)128 * qpk * s] : 0.0f;
+        const float m_t = t < ns ? ml[(size_t)2 * qpk * t] : -INFINITY;
+        const float l_t = t < ns ? ml[(size_t)2 * qpk * t + 1] : 0.0f;
+        const float mx = seg_max<64>(fmaxf(-INFINITY, m_t));
+        if ((t & 63) == 0) red[t >> 6] = mx;
+        __syncthreads();
+        const float M = fmaxf(red[0], red[1]);
+        float f = 0.0f, lsum = 0.0f;
+        if (t < ns) {
+            f = expf_fast(__fsub_rn(m_t, M));
+            lsum = __builtin_fmaf(l_t, f, lsum);
+        }
+        fs[t] = f;
+        __syncthreads();
+        float O = 0.0f;
+#pragma unroll
+        for (int s = 0; s < CMB_SR; s++)
+            if (s < ns) O = __builtin_fmaf(pv[s], fs[s], O);
+        lsum = seg_sum<64>(lsum);
+        if ((t & 63) == 0) red[t >> 6] = lsum;      // every thread read M before the barrier above
+        __syncthreads();
+        att[((size_t)b * a.H + h) * 128 + t] = __fdiv_rn(O, __fadd_rn(red[0], red[1]));
+        return;
+    }
     float mx = -INFINITY;
     for (int s = t; s < ns; s += 128) mx = fmaxf(mx, ml[(size_t)2 * qpk * s]);
     mx = seg_max<64>(mx);
