@@ -618,6 +618,9 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the 48-layer decode step (B=--batch, --steps timed steps); prints its JSON")
+    ap.add_argument("--decode-layers", type=int, default=48,
+                    help="layers of the --decode-only step (1: every byte of the layer stays in the 256 MB "
+                         "Infinity Cache, which shows how much of each kernel's time is HBM bandwidth)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 48-layer 512-token prefill (--steps timed passes); prints its JSON")
     ap.add_argument("--zipf-only", action="store_true",
@@ -651,7 +654,7 @@ def main() -> int:
         print(json.dumps({"probe": probe_costs()}), flush=True)
         return 0
     if args.decode_only:
-        r = decode_step(args.batch, args.steps, args.warmup, args.group)
+        r = decode_step(args.batch, args.steps, args.warmup, args.group, n_layers=args.decode_layers)
         print(json.dumps({"decode_step": r}), flush=True)
         return 0
     if args.prefill_only:
