@@ -310,30 +310,6 @@ __device__ __forceinline__ int seg_or(int v) {
 
 // ------------------------------------------------- wave-level digit encode
 
-// Encode one group of G floats, value i held by lane i of an aligned G-lane
-// segment (G = 32 or 64), into NDIG x G/8 digit words and one scale.
-// Lane j*8 of the segment writes word j of every digit k to dig[k*(G/8)+j];
-// lane 0 writes the scale (only when `store`).  Every lane of the segment must
-// call this (the reductions cross lanes).
-template <int G, int NDIG>
-__device__ __forceinline__ void encode_group_wave(float v, bool store, uint32_t* __restrict__ dig,
-                                                  float* __restrict__ scale) {
-    const int i = threadIdx.x & (G - 1);
-    const float a = fabsf(v);
-    const int bad = seg_or<G>(!(a <= 3.4028235e38f) ? 1 : 0);
-    const float mx = seg_max<G>(a);
-    const float s = digit_scale<NDIG>(mx, bad != 0);
-    const float inv = (mx > 0.0f && !bad) ? __fdiv_rn((float)Digits<NDIG>::R, mx) : 0.0f;
-    int dg[NDIG];
-    split_digits<NDIG>((int)rintf(__fmul_rn(v, inv)), dg);
-#pragma unroll
-    for (int k = 0; k < NDIG; k++) {
-        const int word = seg_or<8>((dg[k] & 15) << (4 * (i & 7)));
-        if (store && (i & 7) == 0) dig[k * (G / 8) + (i >> 3)] = (uint32_t)word;
-    }
-    if (store && i == 0) *scale = s;
-}
-
 // --------------------------------------- int8 digit pairs (MFMA branch)
 //
 // The MFMA branch multiplies signed int8 weights (q - 8) by activations
@@ -380,6 +356,62 @@ __device__ __forceinline__ void encode_i8_group_wave(float v, bool store, int8_t
             *qsum = (int)qs;
         }
     }
+}
+
+// Both encodings of one G-value group (one value per lane of a G-lane
+// segment) from one pair of segment reductions: the NDIG base-16 digits and
+// their scale, as encode_group_wave writes them, and with i8 the int8 digit
+// pairs, scale and integer sum, as encode_i8_group_wave writes them (the
+// same values as the two calls).  Only when `store`; every lane of the
+// segment must call this.
+template <int G, int NDIG>
+__device__ __forceinline__ void encode_group_both(float v, bool store, uint32_t* __restrict__ dig,
+                                                  float* __restrict__ scale, bool i8, int8_t* __restrict__ hi,
+                                                  int8_t* __restrict__ lo, float* __restrict__ qscale,
+                                                  int* __restrict__ qsum) {
+    const int i = threadIdx.x & (G - 1);
+    const float a = fabsf(v);
+    const int bad = seg_or<G>(!(a <= 3.4028235e38f) ? 1 : 0);
+    const float mx = seg_max<G>(a);
+    {
+        const float s = digit_scale<NDIG>(mx, bad != 0);
+        const float inv = (mx > 0.0f && !bad) ? __fdiv_rn((float)Digits<NDIG>::R, mx) : 0.0f;
+        int dg[NDIG];
+        split_digits<NDIG>((int)rintf(__fmul_rn(v, inv)), dg);
+#pragma unroll
+        for (int k = 0; k < NDIG; k++) {
+            const int word = seg_or<8>((dg[k] & 15) << (4 * (i & 7)));
+            if (store && (i & 7) == 0) dig[k * (G / 8) + (i >> 3)] = (uint32_t)word;
+        }
+        if (store && i == 0) *scale = s;
+    }
+    if (i8) {
+        const float inv = (mx > 0.0f && !bad) ? __fdiv_rn((float)I8_R, mx) : 0.0f;
+        const int q = (int)rintf(__fmul_rn(v, inv));
+        const int l = ((q + 128) & 255) - 128;
+        const int h = (q - l) >> 8;
+        const float qs = seg_sum<G>((float)q);
+        if (store) {
+            const int p = (i & ~7) + i8_pos(i & 7);
+            hi[p] = (int8_t)h;
+            lo[p] = (int8_t)l;
+            if (i == 0) {
+                *qscale = bad ? __int_as_float(0x7FC00000) : __fdiv_rn(mx, (float)I8_R);
+                *qsum = (int)qs;
+            }
+        }
+    }
+}
+
+// Encode one group of G floats, value i held by lane i of an aligned G-lane
+// segment (G = 32 or 64), into NDIG x G/8 digit words and one scale.
+// Lane j*8 of the segment writes word j of every digit k to dig[k*(G/8)+j];
+// lane 0 writes the scale (only when `store`).  Every lane of the segment must
+// call this (the reductions cross lanes).
+template <int G, int NDIG>
+__device__ __forceinline__ void encode_group_wave(float v, bool store, uint32_t* __restrict__ dig,
+                                                  float* __restrict__ scale) {
+    encode_group_both<G, NDIG>(v, store, dig, scale, false, nullptr, nullptr, nullptr, nullptr);
 }
 
 // Digits of the 8 values in lanes 0..7 of the wave with the digit scale of

@@ -246,22 +246,25 @@ k_router_grp(RouteArgs a) {
     const int e = 8 * eg + el;
     if (r == 0 && e < a.E) a.logits[(size_t)b * a.E + e] = acc;
 
-    // x digits: one G-value group per G-lane segment
+    // x digits: one G-value group per G-lane segment (and, for the MFMA
+    // branch, the same group as int8 digit pairs); two groups at a time, so
+    // that their reduction chains interleave
     constexpr int ng = d / G;
     constexpr int PPW = JM_WAVE / G;
     const int sub = lane / G;
-    for (int base = eg * PPW; base < ng; base += ngrp * PPW) {
-        const int p = base + sub;
-        const bool ok = p < ng;
-        const int j = (ok ? p : 0) * G + (lane & (G - 1));
-        const float v = ok ? xT[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
-        encode_group_wave<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + (ok ? p : 0)) * (NDIG * (G / 8)),
-                                   a.xscale + (size_t)b * ng + (ok ? p : 0));
-        // the same group as int8 digit pairs for the MFMA branch
-        if (a.xqh) {
-            const size_t o = (size_t)b * d + (size_t)(ok ? p : 0) * G;
-            encode_i8_group_wave<G>(v, ok, a.xqh + o, a.xql + o, a.xqs + (size_t)b * ng + (ok ? p : 0),
-                                    a.xqc + (size_t)b * ng + (ok ? p : 0));
+    const bool i8 = a.xqh != nullptr;
+    for (int base = eg * PPW; base < ng; base += 2 * ngrp * PPW) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int p = base + u * ngrp * PPW + sub;
+            const bool ok = p < ng;
+            const int pp = ok ? p : 0;
+            const int j = pp * G + (lane & (G - 1));
+            const float v = ok ? xT[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
+            const size_t o = (size_t)b * d + (size_t)pp * G;
+            encode_group_both<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + pp) * (NDIG * (G / 8)),
+                                       a.xscale + (size_t)b * ng + pp, i8, a.xqh + (i8 ? o : 0),
+                                       a.xql + (i8 ? o : 0), a.xqs + (size_t)b * ng + pp, a.xqc + (size_t)b * ng + pp);
         }
     }
 }
@@ -393,25 +396,27 @@ k_router_quad(RouteArgs a) {
         }
     }
     // x digits (one G-value group per G-lane segment) and the MFMA digit pairs of
-    // the block's tokens: this wave's share, over the grid's nvg waves
+    // the block's tokens: this wave's share, over the grid's nvg waves.  The
+    // tokens of a group are encoded together (unconditionally, the stores
+    // guarded), so that their reduction chains interleave.
     constexpr int ng = d / G;
     constexpr int PPW = JM_WAVE / G;
     const int sub = lane / G;
-    for (int t = 0; t < nt; t++) {
-        const int b = b0 + t;
-        const float* xw = xT[t];
-        for (int base = eg * PPW; base < ng; base += nvg * PPW) {
-            const int p = base + sub;
-            const bool ok = p < ng;
-            const int j = (ok ? p : 0) * G + (lane & (G - 1));
-            const float v = ok ? xw[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
-            encode_group_wave<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + (ok ? p : 0)) * (NDIG * (G / 8)),
-                                       a.xscale + (size_t)b * ng + (ok ? p : 0));
-            if (a.xqh) {
-                const size_t o = (size_t)b * d + (size_t)(ok ? p : 0) * G;
-                encode_i8_group_wave<G>(v, ok, a.xqh + o, a.xql + o, a.xqs + (size_t)b * ng + (ok ? p : 0),
-                                    a.xqc + (size_t)b * ng + (ok ? p : 0));
-            }
+    const bool i8 = a.xqh != nullptr;
+    for (int base = eg * PPW; base < ng; base += nvg * PPW) {
+        const int p = base + sub;
+        const bool ok = p < ng;
+        const int pp = ok ? p : 0;
+        const int j = pp * G + (lane & (G - 1));
+#pragma unroll
+        for (int t = 0; t < RQ_T; t++) {
+            const bool st = ok && t < nt;
+            const size_t b = (size_t)b0 + (t < nt ? t : 0);
+            const float v = st ? xT[t][(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
+            const size_t o = b * d + (size_t)pp * G;
+            encode_group_both<G, NDIG>(v, st, a.xdig + (b * ng + pp) * (NDIG * (G / 8)), a.xscale + b * ng + pp, i8,
+                                       a.xqh + (i8 ? o : 0), a.xql + (i8 ? o : 0), a.xqs + b * ng + pp,
+                                       a.xqc + b * ng + pp);
         }
     }
 }
