@@ -164,20 +164,54 @@ k_router_grp(RouteArgs a) {
     const float4* xb = (const float4*)(a.x + (size_t)b * d);
 #pragma unroll
     for (int i = 0; i < XV; i++) xv[i] = xb[lane + 64 * i];
-    constexpr int NB = C::NC < 16 ? C::NC : 16;
+    // The decoder layer's inputs (the o_proj slices, up to RG_PS of them,
+    // and the norm weight) are requested next, before the table: all of
+    // them return in the first memory round trip instead of one round trip
+    // per slice.  The table's chunks in flight are fewer in this variant so
+    // that the slices fit in registers; the rest are requested as the chain
+    // consumes the first ones.
+    constexpr int RG_PS = LAYER ? 4 : 1;
+    float4 sv[RG_PS][XV];
+    uint2 nwv[LAYER ? XV : 1];
+    const size_t sstride = (size_t)a.B * d / 4;
+    const float4* xp = (const float4*)(a.xpart + (size_t)b * d);
+    if (LAYER && a.xpart) {
+#pragma unroll
+        for (int s = 0; s < RG_PS; s++) {
+            const int sc = s < a.nxpart ? s : a.nxpart - 1;     // clamped: every load in bounds
+#pragma unroll
+            for (int i = 0; i < XV; i++) sv[s][i] = xp[sc * sstride + lane + 64 * i];
+        }
+    }
+    if (LAYER && a.norm_w) {
+        const uint2* nw = (const uint2*)a.norm_w;
+#pragma unroll
+        for (int i = 0; i < (LAYER ? XV : 1); i++) nwv[i] = nw[lane + 64 * i];
+    }
+    constexpr int NBM = LAYER ? 6 : 16;
+    constexpr int NB = C::NC < NBM ? C::NC : NBM;
     uint4 buf[NB][C::CP];
 #pragma unroll
     for (int c = 0; c < NB; c++) C::load(buf[c], wt, eg, c, lane);
     if (LAYER && a.xpart) {
         // the decoder layer's residual add before the MoE block
         // (decode_kernel.c:1546-1547): x + the attention output, which comes
-        // as the o_proj's column slices
-        const float4* xp = (const float4*)(a.xpart + (size_t)b * d);
-        const size_t sstride = (size_t)a.B * d / 4;
+        // as the o_proj's column slices, summed in slice order
         float4 ps[XV];
 #pragma unroll
-        for (int i = 0; i < XV; i++) ps[i] = xp[lane + 64 * i];
-        for (int sl = 1; sl < a.nxpart; sl++) {
+        for (int i = 0; i < XV; i++) ps[i] = sv[0][i];
+#pragma unroll
+        for (int s = 1; s < RG_PS; s++) {
+            if (s < a.nxpart) {
+#pragma unroll
+                for (int i = 0; i < XV; i++) {
+                    const float4 u = sv[s][i];
+                    ps[i] = make_float4(__fadd_rn(ps[i].x, u.x), __fadd_rn(ps[i].y, u.y), __fadd_rn(ps[i].z, u.z),
+                                        __fadd_rn(ps[i].w, u.w));
+                }
+            }
+        }
+        for (int sl = RG_PS; sl < a.nxpart; sl++) {
 #pragma unroll
             for (int i = 0; i < XV; i++) {
                 const float4 u = xp[sl * sstride + lane + 64 * i];
@@ -207,10 +241,9 @@ k_router_grp(RouteArgs a) {
             ss = __builtin_fmaf(xv[i].w, xv[i].w, ss);
         }
         const float inv = rms_inv(seg_sum<64>(ss), d, a.eps);
-        const uint2* nw = (const uint2*)a.norm_w;
 #pragma unroll
-        for (int i = 0; i < XV; i++) {
-            const uint2 w = nw[lane + 64 * i];
+        for (int i = 0; i < (LAYER ? XV : 1); i++) {
+            const uint2 w = nwv[i];
             xv[i].x = __fmul_rn(__fmul_rn(xv[i].x, inv), bf16_bits_to_f32(w.x & 0xFFFFu));
             xv[i].y = __fmul_rn(__fmul_rn(xv[i].y, inv), bf16_bits_to_f32(w.x >> 16));
             xv[i].z = __fmul_rn(__fmul_rn(xv[i].z, inv), bf16_bits_to_f32(w.y & 0xFFFFu));
