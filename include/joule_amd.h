@@ -195,7 +195,8 @@ typedef struct jm_kv_cache {
  * decoder3.py:49-69) field for field, with device pointers.  Read here:
  * final_norm, norm1, norm2 [L][d], wq [L][H*hd][d], wk/wv [L][KH*hd][d],
  * wo [L][d][H*hd] (all bf16), bq/bk/bv (float32, when bias_qkv), qn/kn
- * [L][hd] (bf16, when qk_norm_type = 1), cos/sin [maxT][hd] (float32).
+ * (bf16: [L][hd] when qk_norm_type = 1, [L][H*hd] / [L][KH*hd] when it is 2),
+ * cos/sin [maxT][hd] (float32).
  * gate_w and the expert tables are the store's (jm_store_set_router, the
  * blob); embed and lm_head are not read by jm_decode_layers_batch; w1/w2/w3
  * and the int8 fields must be NULL and use_i8 0. */
@@ -243,7 +244,8 @@ typedef struct jm_kernel_w {
  * the final RMSNorm into hidden [B][d] float32, and the lm_head into logits.
  *   cfg        L, d, E, topk, intermediate, norm_topk_prob as the store's;
  *              n_heads, n_kv (n_heads / n_kv in 1, 2, 4, 8), hd = 128, eps,
- *              maxT, qk_norm_type (0 or 1), bias_qkv
+ *              maxT, qk_norm_type (0: none, 1: per head, 2: whole
+ *              vector, :1155-1189), bias_qkv
  *   kv         HOST array of B * L caches, entry b * L + l (as the reference)
  *   positions  HOST int32 [B]: the cache row each token writes; attention
  *              covers rows 0 .. positions[b] (the others must be filled)

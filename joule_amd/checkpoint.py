@@ -120,9 +120,6 @@ def load_decoder(model_dir: str | Path, max_tokens: int = 4096, converted_dir: s
     model_dir = Path(model_dir)
     cfg = json.loads((model_dir / "config.json").read_text())
     shape, naming = decoder_shape(cfg, max_tokens)
-    if shape.qk_norm_type == 2:
-        raise ValueError(f"{shape.name}: the whole-vector QK-norm is not supported by the GPU decoder "
-                         "(its MoE block is: HbmExpertStore.layer_ffn_batch)")
     L, moe = shape.n_layers, shape.moe
     out = Path(converted_dir) if converted_dir is not None else model_dir / "joule_q4"
     if not ((out / BIN_NAME).exists() and (out / INDEX_NAME).exists()):
@@ -145,7 +142,8 @@ def load_decoder(model_dir: str | Path, max_tokens: int = 4096, converted_dir: s
         "wo": T.stack([f"{p}.self_attn.o_proj.weight" for p in lay]),
         "embed": T.get("model.embed_tokens.weight").to(torch.bfloat16),
     }
-    if shape.qk_norm_type == 1:
+    if shape.qk_norm_type != 0:
+        # [hd] per head (qwen3), [H*hd] / [KH*hd] over the whole vector (olmoe)
         t["qn"] = T.stack([f"{p}.self_attn.q_norm.weight" for p in lay])
         t["kn"] = T.stack([f"{p}.self_attn.k_norm.weight" for p in lay])
     if shape.bias_qkv:

@@ -7,8 +7,10 @@
 //
 //   k_gemv_part   Wq/Wk/Wv . (h * norm1 weight), per 512-column slice
 //                                                             (:224-230, :1126-1145)
-//   k_attn_part   the slices summed, RMSNorm row scale, bias, per-head
-//                 QK-norm and RoPE of the block's heads (:1146-1199; the k
+//   k_qk_ss       whole-vector QK-norm only: each token's sums of squares
+//                 of q and k                                   (:1155-1167)
+//   k_attn_part   the slices summed, RMSNorm row scale, bias, per-head or
+//                 whole-vector QK-norm and RoPE of the block's heads (:1146-1199; the k
 //                 and v rows appended to the cache by the split that holds
 //                 the token's position), then scores, softmax and P.V over
 //                 one 128-position split of the cache           (:1200-1222)
@@ -368,15 +370,25 @@ __device__ __forceinline__ void fin4_load(Fin4& f, const AttnArgs& a, int b, int
     }
 }
 
+// The norm weight of q head (isq) or k head `head` of the layer: per head,
+// the one [128] vector; over the whole vector, the head's 128 entries.
+__device__ __forceinline__ const uint16_t* qk_weight(const AttnArgs& a, bool isq, int head) {
+    const uint16_t* w = isq ? a.qn : a.kn;
+    if (!w) return nullptr;
+    return a.qk_norm == 2 ? w + (size_t)head * 128 : w;
+}
+
 // The four values finished (decode_kernel.c:1126-1199): the column slices
 // summed in slice order, times the RMSNorm row scale of h (the projections
 // were taken of h * norm weight), plus the bias; then, for a q or k head,
-// the per-head RMSNorm with weight nw (:1174-1189) and RoPE rotate-half at
+// the QK-norm with weight nw (norm 1: the head's RMSNorm, :1174-1189;
+// norm 2: the whole vector's, with its sum of squares from k_qk_ss,
+// :1155-1167) and RoPE rotate-half at
 // pos (:1190-1194, :259-266) over the aligned 32-lane segment that holds
 // the head (lane j: dimensions 4 j .. 4 j + 3; dim i pairs with i + 64,
 // i.e. lane j with j ^ 16; first half a cos - b sin, second a sin + b cos).
 __device__ __forceinline__ void fin4_value(float (&v)[4], const Fin4& f, const AttnArgs& a, int b, int row,
-                                           bool norm, bool rope, int j) {
+                                           int norm, bool rope, int j) {
     constexpr int HD = 128;
     const int ns = a.nslice < 4 ? a.nslice : 4;
     float4 acc = f.sl[0];
@@ -404,12 +416,18 @@ __device__ __forceinline__ void fin4_value(float (&v)[4], const Fin4& f, const A
     v[2] = __fadd_rn(__fmul_rn(acc.z, inv), f.bias.z);
     v[3] = __fadd_rn(__fmul_rn(acc.w, inv), f.bias.w);
     if (norm) {
-        float sq = 0.0f;
+        float hinv;
+        if (norm == 1) {
+            float sq = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; e++) sq = __builtin_fmaf(v[e], v[e], sq);
-        // the reference sums the head's squares in dimension order; the
-        // tree here changes the sum by rounding only
-        const float hinv = rms_inv(seg_sum<32>(sq), HD, a.eps);
+            for (int e = 0; e < 4; e++) sq = __builtin_fmaf(v[e], v[e], sq);
+            // the reference sums the head's squares in dimension order; the
+            // tree here changes the sum by rounding only
+            hinv = rms_inv(seg_sum<32>(sq), HD, a.eps);
+        } else {
+            const bool isq = row < a.H * HD;
+            hinv = rms_inv(a.qkss[(size_t)b * 2 + (isq ? 0 : 1)], (isq ? a.H : a.KH) * HD, a.eps);
+        }
         const uint32_t nn[4] = {f.nw.x & 0xFFFFu, f.nw.x >> 16, f.nw.y & 0xFFFFu, f.nw.y >> 16};
 #pragma unroll
         for (int e = 0; e < 4; e++) v[e] = __fmul_rn(__fmul_rn(v[e], hinv), bf16_bits_to_f32(nn[e]));
@@ -439,7 +457,8 @@ __device__ __forceinline__ void kv_load(KvFin& k, const AttnArgs& a, int b, int 
     k.isk = lane < 32;
     const int j = lane & 31;
     k.row = (k.isk ? a.H + kh : a.H + a.KH + kh) * HD + 4 * j;
-    fin4_load(k.f, a, b, k.row, k.isk ? a.bk : a.bv, kh * HD + 4 * j, k.isk ? a.kn : nullptr, k.isk, pos, j);
+    fin4_load(k.f, a, b, k.row, k.isk ? a.bk : a.bv, kh * HD + 4 * j, k.isk ? qk_weight(a, false, kh) : nullptr,
+              k.isk, pos, j);
 }
 
 // Finished and appended to the token's caches kc, vc at pos (:1195-1199);
@@ -449,7 +468,7 @@ __device__ __forceinline__ void kv_store(const KvFin& k, const AttnArgs& a, int 
     constexpr int HD = 128;
     const int j = lane & 31;
     float v[4];
-    fin4_value(v, k.f, a, b, k.row, k.isk && a.kn, k.isk, j);
+    fin4_value(v, k.f, a, b, k.row, k.isk && a.kn ? a.qk_norm : 0, k.isk, j);
     uint16_t hb4[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) hb4[e] = (uint16_t)f32_to_bf16_rne(v[e]);
@@ -459,6 +478,43 @@ __device__ __forceinline__ void kv_store(const KvFin& k, const AttnArgs& a, int 
     }
     const gptr<uint16_t> dst = (k.isk ? kc : vc) + ((size_t)pos * a.KH + kh) * HD + 4 * j;
     *(uint2*)dst = make_uint2(hb4[0] | ((uint32_t)hb4[1] << 16), hb4[2] | ((uint32_t)hb4[3] << 16));
+}
+
+// The whole-vector QK-norm (decode_kernel.c:1155-1167) needs each token's
+// sum of squares over all of q (H * 128 values) and all of k (KH * 128)
+// before the attention blocks, which finish one KV head each, can scale
+// their heads.  One block per token finishes every q and k value as
+// fin4_value does (slices, row scale, bias: the same bits) and sums the
+// squares; qkss[b] = (q sum, k sum).
+__global__ void __launch_bounds__(256)
+k_qk_ss(AttnArgs a) {
+    constexpr int HD = 128;
+    __shared__ float red[2][4];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const int nq = a.H * HD / 4, nqk = (a.H + a.KH) * HD / 4;   // float4 groups of q, of q and k
+    float sq = 0.0f, sk = 0.0f;
+    for (int u = tid; u < nqk; u += 256) {
+        const bool isq = u < nq;
+        const int row = 4 * u;                    // q rows, then the k rows, as stacked in qkv
+        Fin4 f;
+        fin4_load(f, a, b, row, isq ? a.bq : a.bk, isq ? row : row - a.H * HD, nullptr, false, 0, 0);
+        float v[4];
+        fin4_value(v, f, a, b, row, 0, false, 0);
+        float t = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) t = __builtin_fmaf(v[e], v[e], t);
+        if (isq) sq = __fadd_rn(sq, t);
+        else sk = __fadd_rn(sk, t);
+    }
+    sq = seg_sum<64>(sq);
+    sk = seg_sum<64>(sk);
+    if ((tid & 63) == 0) {
+        red[0][tid >> 6] = sq;
+        red[1][tid >> 6] = sk;
+    }
+    __syncthreads();
+    if (tid < 2) a.qkss[(size_t)b * 2 + tid] = __fadd_rn(__fadd_rn(red[tid][0], red[tid][1]),
+                                                         __fadd_rn(red[tid][2], red[tid][3]));
 }
 
 // For a batch whose tokens may share a cache (a prefill chunk: the
@@ -538,7 +594,7 @@ k_attn_part(AttnArgs a) {
     const int qrow = (kh * QPK + (qh < QPK ? qh : 0)) * HD + 4 * qj;
     const bool kvw = own && w == 0;                  // wave-uniform
     Fin4 fq;
-    fin4_load(fq, a, b, qrow, a.bq, qrow, a.qn, true, pos, qj);
+    fin4_load(fq, a, b, qrow, a.bq, qrow, qk_weight(a, true, kh * QPK + (qh < QPK ? qh : 0)), true, pos, qj);
     KvFin fkv;
     if (kvw) kv_load(fkv, a, b, kh, pos, lane);
     uint4 kr[2][4], vr[8];
@@ -557,7 +613,7 @@ k_attn_part(AttnArgs a) {
     __builtin_amdgcn_sched_barrier(0);      // keep every request ahead of the arithmetic
     {
         float v[4];
-        fin4_value(v, fq, a, b, qrow, a.qn != nullptr, true, qj);
+        fin4_value(v, fq, a, b, qrow, a.qn ? a.qk_norm : 0, true, qj);
         if (QPK == 8 || qh < QPK) {                 // whole 32-lane segments
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -795,6 +851,12 @@ k_attn_comb(AttnArgs a, int qpk, float* __restrict__ att) {
 
 hipError_t launch_attn(const AttnArgs& a, int qpk, float* att, hipStream_t st) {
     if (a.B == 0) return hipSuccess;
+    if (a.qk_norm == 2) {
+        if (!a.qkss || !a.qn || !a.kn) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(k_qk_ss, dim3((unsigned)a.B), dim3(256), 0, st, a);
+        hipError_t e0 = hipGetLastError();
+        if (e0 != hipSuccess) return e0;
+    }
     if (!a.append) {
         hipLaunchKernelGGL(k_kv_append, dim3((unsigned)a.KH, (unsigned)a.B), dim3(64), 0, st, a);
         hipError_t e0 = hipGetLastError();

@@ -74,6 +74,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
         (size_t)jm::lm_blocks(V) * B * 4,         // lmv
         (size_t)jm::lm_blocks(V) * B * 4,         // lmi
         (size_t)(d / 512) * B * 4,                // rss: sums of squares of h per qkv slice
+        (size_t)B * 2 * 4,                        // qkss: sums of squares of q and k (whole-vector QK-norm)
         s->tab_cap,                               // KV pointers + positions
     };
     size_t total = 0;
@@ -85,7 +86,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     char* p = (char*)s->dws;
     void** slots[] = {(void**)&s->h, (void**)&s->h2, (void**)&s->qkv, (void**)&s->opart, (void**)&s->part_o,
                       (void**)&s->part_ml, (void**)&s->att, (void**)&s->hid, (void**)&s->xemb, (void**)&s->lmv,
-                      (void**)&s->lmi, (void**)&s->rss, (void**)&s->tab};
+                      (void**)&s->lmi, (void**)&s->rss, (void**)&s->qkss, (void**)&s->tab};
     for (size_t i = 0; i < sizeof sz / sizeof sz[0]; i++) {
         *slots[i] = p;
         p += align256(sz[i]);
@@ -109,21 +110,22 @@ int check_decode_args(const jm_store* s, const jm_kernel_cfg* c, const jm_kernel
         return fail(JM_ERR_SHAPE, "n_heads / n_kv must be 1, 2, 4 or 8 (got %d)", *qpk);
     if (!jm::gemv_shape_ok(c->d) || !jm::gemv_shape_ok(c->n_heads * HD))
         return fail(JM_ERR_SHAPE, "d=%d and n_heads*hd=%d must be multiples of 1024 up to 8192", c->d, c->n_heads * HD);
-    if (c->qk_norm_type != 0 && c->qk_norm_type != 1)
-        return fail(JM_ERR_SHAPE, "qk_norm_type %d: only 0 (none) and 1 (per head) are supported", c->qk_norm_type);
+    if (c->qk_norm_type < 0 || c->qk_norm_type > 2)
+        return fail(JM_ERR_SHAPE, "qk_norm_type %d: 0 (none), 1 (per head) or 2 (whole vector)", c->qk_norm_type);
     if (c->maxT <= 0) return fail(JM_ERR_SHAPE, "maxT must be positive");
     if (!(c->eps >= 0.0f)) return fail(JM_ERR_SHAPE, "eps must be >= 0");
     if (!W) return fail(JM_ERR_ARG, "weights are NULL");
     if (!W->final_norm || !W->norm1 || !W->norm2 || !W->wq || !W->wk || !W->wv || !W->wo || !W->cos || !W->sin)
         return fail(JM_ERR_ARG, "final_norm, norm1, norm2, wq, wk, wv, wo, cos and sin must be set");
-    if (c->qk_norm_type == 1 && (!W->qn || !W->kn)) return fail(JM_ERR_ARG, "qk_norm_type 1 needs qn and kn");
+    if (c->qk_norm_type != 0 && (!W->qn || !W->kn))
+        return fail(JM_ERR_ARG, "qk_norm_type %d needs qn and kn", c->qk_norm_type);
     if (c->bias_qkv && (!W->bq || !W->bk || !W->bv)) return fail(JM_ERR_ARG, "bias_qkv needs bq, bk and bv");
     if (W->use_i8 || W->wq_i8 || W->wk_i8 || W->wv_i8 || W->wo_i8 || W->lm_i8)
         return fail(JM_ERR_ARG, "the int8 attention weights are not supported (use_i8 = 0, *_i8 = NULL)");
     if (W->w1 || W->w2 || W->w3) return fail(JM_ERR_ARG, "dense FFN layers (w1/w2/w3) are not supported: the FFN is the store's MoE");
     const void* al[] = {W->final_norm, W->norm1, W->norm2, W->wq, W->wk, W->wv, W->wo, W->cos, W->sin,
-                        c->qk_norm_type == 1 ? (const void*)W->qn : nullptr,
-                        c->qk_norm_type == 1 ? (const void*)W->kn : nullptr,
+                        c->qk_norm_type != 0 ? (const void*)W->qn : nullptr,
+                        c->qk_norm_type != 0 ? (const void*)W->kn : nullptr,
                         c->bias_qkv ? (const void*)W->bq : nullptr, c->bias_qkv ? (const void*)W->bk : nullptr,
                         c->bias_qkv ? (const void*)W->bv : nullptr};
     for (const void* p : al)
@@ -175,8 +177,14 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
             at.bv = W->bv + (size_t)l * KH * HD;
         }
         at.nqkv = nqkv; at.H = H; at.KH = KH; at.B = B;
-        at.qn = c->qk_norm_type == 1 ? W->qn + (size_t)l * HD : nullptr;
-        at.kn = c->qk_norm_type == 1 ? W->kn + (size_t)l * HD : nullptr;
+        // per head: [L][hd] weights; whole vector (decode_kernel.c:1156-1157):
+        // [L][H*hd] and [L][KH*hd]
+        at.qk_norm = c->qk_norm_type;
+        at.qn = c->qk_norm_type == 1 ? W->qn + (size_t)l * HD
+              : c->qk_norm_type == 2 ? W->qn + (size_t)l * H * HD : nullptr;
+        at.kn = c->qk_norm_type == 1 ? W->kn + (size_t)l * HD
+              : c->qk_norm_type == 2 ? W->kn + (size_t)l * KH * HD : nullptr;
+        at.qkss = s->qkss;
         at.eps = c->eps; at.rsdiv = 1.0f / sdiv;
         at.cos = W->cos; at.sin = W->sin;
         at.pos = pos_dev; at.kv = s->tab; at.L = L; at.layer = l;

@@ -206,8 +206,11 @@ struct AttnArgs {
     const float* bk;
     const float* bv;
     int nqkv, H, KH, B;
-    const uint16_t* qn;       // [128] bf16 per-head q norm of the layer, or NULL
-    const uint16_t* kn;       // [128] bf16 per-head k norm, or NULL
+    const uint16_t* qn;       // bf16 q norm weight of the layer, or NULL: [128] per head (qk_norm 1),
+                              // [H*128] over the whole vector (qk_norm 2)
+    const uint16_t* kn;       // the k norm weight likewise: [128] or [KH*128]
+    int qk_norm;              // 0: none, 1: per head, 2: whole vector
+    float* qkss;              // qk_norm 2: [B][2] each token's sums of squares of q and of k before the norm
     float eps;
     float rsdiv;              // 1 / the score divisor sqrtf_fast(128)
     const float* cos;         // [maxT][128]

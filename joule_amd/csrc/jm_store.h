@@ -108,6 +108,7 @@ struct jm_store {
     float* lmv;                 // [lm blocks][B] per-block best logit (argmax)
     int* lmi;                   // [lm blocks][B] its row
     float* rss;                 // [B] sums of squares of h from the projection GEMM (prefill chunks)
+    float* qkss;                // [B][2] sums of squares of q and k (whole-vector QK-norm)
     unsigned long long* tab;    // [B*L][2] KV pointers, then [B] positions (device)
     unsigned long long* tab_host;   // pinned staging of tab
     size_t tab_cap;             // bytes of tab / tab_host

@@ -66,7 +66,7 @@ class DecoderShape:
     eps: float = 1e-6
     theta: float = 1e6
     maxT: int = 4096
-    qk_norm_type: int = 1        # 1: per-head RMSNorm on q and k (Qwen3)
+    qk_norm_type: int = 1        # 1: per-head RMSNorm on q and k (Qwen3); 2: over the whole q and k vectors (OLMoE)
     bias_qkv: bool = False
     V: int = 0                   # vocabulary (embedding / lm_head rows); 0: none
     name: str = ""
@@ -147,7 +147,8 @@ class DecoderWeights:
     """The dense (non-expert) weights of every layer, on the device.
 
     bf16 tensors: norm1/norm2 [L, d], final_norm [d], wq [L, H*hd, d],
-    wk/wv [L, KH*hd, d], wo [L, d, H*hd], qn/kn [L, hd]; float32 biases
+    wk/wv [L, KH*hd, d], wo [L, d, H*hd], qn/kn [L, hd] (per-head QK-norm)
+    or [L, H*hd] / [L, KH*hd] (whole-vector QK-norm); float32 biases
     bq [L, H*hd], bk/bv [L, KH*hd] when the shape has bias_qkv; optional
     embed [V, d] (bf16).  The rope tables are built from the shape.  The
     lm_head goes to the store (HipDecoder.set_lm_head).
@@ -160,6 +161,9 @@ class DecoderWeights:
                 "wk": (L, KH * hd, d), "wv": (L, KH * hd, d), "wo": (L, d, H * hd)}
         if shape.qk_norm_type == 1:
             want.update(qn=(L, hd), kn=(L, hd))
+        elif shape.qk_norm_type == 2:
+            # whole-vector weights, as decoder3.py:244-248 sizes them
+            want.update(qn=(L, H * hd), kn=(L, KH * hd))
         self.t: dict[str, torch.Tensor] = {}
         for k, shp in want.items():
             if k not in t:

@@ -175,6 +175,9 @@ def decoder_weights(shape, seed: int = 6000, device: str | torch.device = "cuda"
     if shape.qk_norm_type == 1:
         t["qn"] = norm_w(L, hd)
         t["kn"] = norm_w(L, hd)
+    elif shape.qk_norm_type == 2:
+        t["qn"] = norm_w(L, H * hd)
+        t["kn"] = norm_w(L, KH * hd)
     if shape.bias_qkv:
         t["bq"] = normal(L, H * hd)
         t["bk"] = normal(L, KH * hd)

@@ -9,8 +9,9 @@ Follows src/jouleai/native/decode_kernel.c:
   rms_norm              :224-230  x * (1 / sqrtf_fast(sum x^2 / d + eps)) * w
   matvec_f32            :234-256  out = W . x (here: float64 dot, rounded to float32)
   rope_apply            :259-266  rotate-half with the cos/sin tables
-  layer_attn_batch      :1120-1234  QKV (+ bias), per-head QK-norm
-                          (qk_norm_type 1), RoPE at positions[b], KV append,
+  layer_attn_batch      :1120-1234  QKV (+ bias), whole-vector QK-norm
+                          (qk_norm_type 2, :1155-1167) or per-head QK-norm
+                          (qk_norm_type 1, :1169-1189), RoPE at positions[b], KV append,
                           SDPA with scores / sqrtf_fast(hd) and expf_fast
                           weights normalised before P.V, o_proj
   decode_layers_batch   :1518-1556  norm1 -> attention -> residual -> norm2
@@ -96,7 +97,8 @@ class OracleDecoder:
 
     ``w`` holds float32 arrays of the bf16 weight values: norm1/norm2 [L, d],
     final_norm [d], wq [L, H*hd, d], wk/wv [L, KH*hd, d], wo [L, d, H*hd],
-    qn/kn [L, hd] (qk_norm_type 1), bq/bk/bv (bias_qkv), cos/sin [maxT, hd].
+    qn/kn [L, hd] (qk_norm_type 1) or [L, H*hd] / [L, KH*hd] (qk_norm_type
+    2), bq/bk/bv (bias_qkv), cos/sin [maxT, hd].
     ``moe[l]`` is an OracleMoE for layer l.  The caches are float32 arrays
     [B][L] of (k, v) [maxT, KH, hd] holding bf16 values; they are updated in
     place like the reference's.
@@ -118,6 +120,11 @@ class OracleDecoder:
             q = (q + w["bq"][l]).astype(F32)
             k = (k + w["bk"][l]).astype(F32)
             v = (v + w["bv"][l]).astype(F32)
+        if self.qk == 2:
+            # the whole q and k vectors of each token, before the head view
+            # (decode_kernel.c:1155-1167)
+            q = rms_norm(q, w["qn"][l], self.eps)
+            k = rms_norm(k, w["kn"][l], self.eps)
         att = np.zeros((B, H * hd), F32)
         g = H // KH
         for b in range(B):

@@ -1,6 +1,8 @@
-"""A Qwen3-MoE checkpoint (config.json + safetensors, written here at a small
-size) loaded into the GPU decoder and decoded token by token, against the
-oracle built from the same tensors and the converted store."""
+"""A Qwen3-MoE and an OLMoE checkpoint (config.json + safetensors, written
+here at a small size) loaded into the GPU decoder and decoded token by token,
+against the oracle built from the same tensors and the converted store.  The
+OLMoE one has the whole-vector QK-norm (q_norm [H*hd], k_norm [KH*hd]), no
+GQA and no top-k renormalisation."""
 
 import json
 
@@ -20,16 +22,26 @@ CFG = {"model_type": "qwen3_moe", "num_hidden_layers": 2, "hidden_size": 1024, "
        "num_key_value_heads": 2, "head_dim": 128, "num_experts": 16, "num_experts_per_tok": 4,
        "moe_intermediate_size": 256, "vocab_size": 1000, "rope_theta": 1000000.0, "rms_norm_eps": 1e-06,
        "norm_topk_prob": True, "tie_word_embeddings": False}
+OLMOE_CFG = {"model_type": "olmoe", "num_hidden_layers": 2, "hidden_size": 1024, "num_attention_heads": 8,
+             "num_key_value_heads": 8, "num_experts": 16, "num_experts_per_tok": 4, "intermediate_size": 256,
+             "vocab_size": 1000, "rope_theta": 10000.0, "rms_norm_eps": 1e-05, "norm_topk_prob": False,
+             "clip_qkv": None, "tie_word_embeddings": False}
+CFGS = {"qwen3_moe": CFG, "olmoe": OLMOE_CFG}
 
 
-def _write_checkpoint(path):
+def _dims(c):
+    H = c["num_attention_heads"]
+    return (c["num_hidden_layers"], c["hidden_size"], H, c["num_key_value_heads"],
+            c.get("head_dim") or c["hidden_size"] // H, c["num_experts"],
+            c.get("moe_intermediate_size") or c["intermediate_size"], c["vocab_size"])
+
+
+def _write_checkpoint(path, c):
     from safetensors.torch import save_file
 
     g = torch.Generator().manual_seed(31)
-    c = CFG
-    L, d, H, KH, hd, E, m, V = (c["num_hidden_layers"], c["hidden_size"], c["num_attention_heads"],
-                                c["num_key_value_heads"], c["head_dim"], c["num_experts"],
-                                c["moe_intermediate_size"], c["vocab_size"])
+    L, d, H, KH, hd, E, m, V = _dims(c)
+    whole = c["model_type"] == "olmoe"
     r = lambda *s, std=0.02: (torch.randn(s, generator=g) * std).to(torch.bfloat16)
     nw = lambda *s: (1.0 + 0.1 * torch.randn(s, generator=g)).to(torch.bfloat16)
     t = {"model.embed_tokens.weight": r(V, d, std=0.5), "lm_head.weight": r(V, d), "model.norm.weight": nw(d)}
@@ -38,7 +50,8 @@ def _write_checkpoint(path):
         t.update({f"{p}.input_layernorm.weight": nw(d), f"{p}.post_attention_layernorm.weight": nw(d),
                   f"{p}.self_attn.q_proj.weight": r(H * hd, d), f"{p}.self_attn.k_proj.weight": r(KH * hd, d),
                   f"{p}.self_attn.v_proj.weight": r(KH * hd, d), f"{p}.self_attn.o_proj.weight": r(d, H * hd),
-                  f"{p}.self_attn.q_norm.weight": nw(hd), f"{p}.self_attn.k_norm.weight": nw(hd),
+                  f"{p}.self_attn.q_norm.weight": nw(H * hd if whole else hd),
+                  f"{p}.self_attn.k_norm.weight": nw(KH * hd if whole else hd),
                   f"{p}.mlp.gate.weight": r(E, d)})
         for e in range(E):
             t[f"{p}.mlp.experts.{e}.gate_proj.weight"] = r(m, d)
@@ -46,18 +59,19 @@ def _write_checkpoint(path):
             t[f"{p}.mlp.experts.{e}.down_proj.weight"] = r(d, m)
     path.mkdir(parents=True, exist_ok=True)
     save_file(t, str(path / "model.safetensors"))
-    (path / "config.json").write_text(json.dumps(CFG))
+    (path / "config.json").write_text(json.dumps(c))
     return {k: v.float().numpy() for k, v in t.items()}
 
 
-def test_checkpoint_decode_matches_oracle(tmp_path):
-    model = tmp_path / "qwen3-moe-tiny"
-    T = _write_checkpoint(model)
-    print("[checkpoint] loading", flush=True)
+@pytest.mark.parametrize("family", list(CFGS))
+def test_checkpoint_decode_matches_oracle(tmp_path, family):
+    c = CFGS[family]
+    model = tmp_path / f"{family}-tiny"
+    T = _write_checkpoint(model, c)
+    print(f"[checkpoint] loading {family}", flush=True)
     nd = HipNativeDecoder(model, max_tokens=64, max_batch=4)
-    c = CFG
-    L, d, H, KH, hd, E, k = (c["num_hidden_layers"], c["hidden_size"], c["num_attention_heads"],
-                             c["num_key_value_heads"], c["head_dim"], c["num_experts"], c["num_experts_per_tok"])
+    L, d, H, KH, hd, E, _, _ = _dims(c)
+    k = c["num_experts_per_tok"]
     lay = [f"model.layers.{l}" for l in range(L)]
     w = {"norm1": np.stack([T[f"{p}.input_layernorm.weight"] for p in lay]),
          "norm2": np.stack([T[f"{p}.post_attention_layernorm.weight"] for p in lay]),
@@ -72,9 +86,9 @@ def test_checkpoint_decode_matches_oracle(tmp_path):
     conv = model / "joule_q4"
     blob = np.fromfile(conv / BIN_NAME, dtype=np.uint8)
     offsets = Q4Index.load(conv / INDEX_NAME).offset_table(L, E)
-    moe = [O.OracleMoE(d, c["moe_intermediate_size"], E, k, True, 64, T[f"{p}.mlp.gate.weight"], blob,
+    moe = [O.OracleMoE(d, _dims(c)[6], E, k, c["norm_topk_prob"], 64, T[f"{p}.mlp.gate.weight"], blob,
                        offsets[:, l * E:(l + 1) * E]) for l, p in enumerate(lay)]
-    oracle = D.OracleDecoder(L, d, H, KH, hd, c["rms_norm_eps"], 1, False, w, moe)
+    oracle = D.OracleDecoder(L, d, H, KH, hd, c["rms_norm_eps"], 2 if family == "olmoe" else 1, False, w, moe)
     kv = [[(np.zeros((64, KH, hd), np.float32), np.zeros((64, KH, hd), np.float32)) for _ in range(L)]
           for _ in range(4)]
     tokens, pos = [5, 999, 0, 123], [0, 0, 0, 0]

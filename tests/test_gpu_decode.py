@@ -97,6 +97,14 @@ CASES = {
     # 2 query heads per KV head, d 2048
     "gqa2_l1_b5": (DecoderShape(n_layers=1, moe=MoEShape(d=2048, m=768, E=64, topk=4, renorm=True),
                                 n_heads=16, n_kv=8, maxT=260), 64, [3, 130, 255, 64, 200]),
+    # OLMoE-1B-7B layers: 16 heads without GQA, the whole-vector QK-norm
+    # (qk_norm_type 2), 64 experts top-8 without renormalisation
+    "olmoe_l2_b4": (DecoderShape(n_layers=2, moe=MoEShape(d=2048, m=1024, E=64, topk=8, renorm=False),
+                                 n_heads=16, n_kv=16, maxT=300, qk_norm_type=2), 64, [0, 129, 255, 299]),
+    # the whole-vector QK-norm after the QKV bias, with GQA
+    "whole_bias_gqa2_l1_b3": (DecoderShape(n_layers=1, moe=MoEShape(d=1024, m=256, E=16, topk=4, renorm=True),
+                                           n_heads=8, n_kv=4, maxT=200, qk_norm_type=2, bias_qkv=True),
+                              32, [7, 150, 64]),
 }
 
 

@@ -18,9 +18,9 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
-def _model(L, maxT, B, V=3000, seed=41, moe=None, group=64):
+def _model(L, maxT, B, V=3000, seed=41, moe=None, group=64, qk=1):
     moe = moe or MoEShape(d=2048, m=768, E=128, topk=8, renorm=True)
-    shape = DecoderShape(n_layers=L, moe=moe, n_heads=16, n_kv=4, maxT=maxT, V=V)
+    shape = DecoderShape(n_layers=L, moe=moe, n_heads=16, n_kv=4, maxT=maxT, V=V, qk_norm_type=qk)
     blob, offsets = torch_store(moe, L, group)
     store = HbmExpertStore(moe, L, blob, offsets, group)
     gw = np.stack([router_weights(moe, l) for l in range(L)])
@@ -40,7 +40,7 @@ def _model(L, maxT, B, V=3000, seed=41, moe=None, group=64):
     E = moe.E
     moe_o = [O.OracleMoE(2048, moe.m, E, moe.topk, moe.renorm, group, gw[l], blob_h, offsets[:, l * E:(l + 1) * E])
              for l in range(L)]
-    oracle = D.OracleDecoder(L, 2048, 16, 4, 128, shape.eps, 1, False, w, moe_o)
+    oracle = D.OracleDecoder(L, 2048, 16, 4, 128, shape.eps, qk, False, w, moe_o)
     return dec, oracle, kv, w, lm.float().cpu().numpy()
 
 
@@ -82,15 +82,16 @@ def test_prefill_layers_matches_per_position_decode(L, T):
     dec.store.close()
 
 
-@pytest.mark.parametrize("moe,group", [(MoEShape(d=2048, m=1024, E=64, topk=8, renorm=False), 64),
-                                       (MoEShape(d=2048, m=768, E=128, topk=8, renorm=True), 32)],
+@pytest.mark.parametrize("moe,group,qk", [(MoEShape(d=2048, m=1024, E=64, topk=8, renorm=False), 64, 2),
+                                          (MoEShape(d=2048, m=768, E=128, topk=8, renorm=True), 32, 1)],
                          ids=["olmoe-g64", "qwen3-g32"])
-def test_prefill_moe_variants(moe, group):
+def test_prefill_moe_variants(moe, group, qk):
     """The prefill with the other MoE shape (64 experts, m = 1024, no
-    renormalisation) and with Q4 group 32: the dispatch path, both MFMA tile
-    shapes and the small-expert kernels at other sizes."""
+    renormalisation, OLMoE's whole-vector QK-norm) and with Q4 group 32: the
+    dispatch path, both MFMA tile shapes and the small-expert kernels at
+    other sizes."""
     T = 150
-    dec, oracle, kv, w, W_lm = _model(1, maxT=256, B=1, moe=moe, group=group)
+    dec, oracle, kv, w, W_lm = _model(1, maxT=256, B=1, moe=moe, group=group, qk=qk)
     rng = np.random.default_rng(T + group)
     prompt = rng.integers(0, 3000, size=T).tolist()
     kv_seq = [(kv.data[0, 0, 0].float().cpu().numpy(), kv.data[0, 0, 1].float().cpu().numpy())]

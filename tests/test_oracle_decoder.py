@@ -111,7 +111,7 @@ def _tiny_model(L=2, B=3, bias=False, qk=1, seed=7):
     nw = lambda *s: D.bf16_round((1.0 + 0.1 * rng.standard_normal(s)).astype(np.float32))
     w = {"wq": r(L, H * hd, 512), "wk": r(L, KH * hd, 512), "wv": r(L, KH * hd, 512),
          "wo": r(L, 512, H * hd), "norm1": nw(L, 512), "norm2": nw(L, 512), "final_norm": nw(512),
-         "qn": nw(L, hd), "kn": nw(L, hd)}
+         "qn": nw(L, hd) if qk != 2 else nw(L, H * hd), "kn": nw(L, hd) if qk != 2 else nw(L, KH * hd)}
     if bias:
         w.update(bq=r(L, H * hd), bk=r(L, KH * hd), bv=r(L, KH * hd))
     cos, sin = rope_tables(T, hd, 1e6)
@@ -147,11 +147,21 @@ def _textbook_decode(dec, shape, blob, offsets, kv, x, positions):
     for l in range(L):
         t = norm(h, w["norm1"][l])
         q, k, v = t @ w["wq"][l].T, t @ w["wk"][l].T, t @ w["wv"][l].T
+        if dec.bias:
+            q, k, v = q + w["bq"][l], k + w["bk"][l], v + w["bv"][l]
         att = np.zeros((h.shape[0], H * hd))
         for b in range(h.shape[0]):
             p = positions[b]
-            qb = rot(norm(q[b].reshape(H, hd), w["qn"][l]), w["cos"][p], w["sin"][p])
-            kb = rot(norm(k[b].reshape(KH, hd), w["kn"][l]), w["cos"][p], w["sin"][p])
+            if dec.qk == 2:                       # over the whole vector, then the heads
+                qb = norm(q[b], w["qn"][l]).reshape(H, hd)
+                kb = norm(k[b], w["kn"][l]).reshape(KH, hd)
+            elif dec.qk == 1:
+                qb = norm(q[b].reshape(H, hd), w["qn"][l])
+                kb = norm(k[b].reshape(KH, hd), w["kn"][l])
+            else:
+                qb, kb = q[b].reshape(H, hd), k[b].reshape(KH, hd)
+            qb = rot(qb, w["cos"][p], w["sin"][p])
+            kb = rot(kb, w["cos"][p], w["sin"][p])
             Kc = kv[b][l][0].astype(np.float64).copy()
             Vc = kv[b][l][1].astype(np.float64).copy()
             Kc[p], Vc[p] = D.bf16_round(kb.astype(np.float32)), D.bf16_round(v[b].reshape(KH, hd).astype(np.float32))
@@ -175,8 +185,9 @@ def _textbook_decode(dec, shape, blob, offsets, kv, x, positions):
     return norm(h, w["final_norm"])
 
 
-def test_decoder_against_textbook():
-    dec, shape, blob, offsets, kv = _tiny_model()
+@pytest.mark.parametrize("qk,bias", [(1, False), (2, True), (0, True)])
+def test_decoder_against_textbook(qk, bias):
+    dec, shape, blob, offsets, kv = _tiny_model(qk=qk, bias=bias)
     rng = np.random.default_rng(8)
     x = rng.standard_normal((3, 512)).astype(np.float32)
     positions = [0, 17, 63]
@@ -217,6 +228,70 @@ def test_gqa_head_mapping():
         assert np.all(seg > 0) and np.all(seg < kh + 1.0 + 1e-6)
         assert np.all(np.abs(seg - seg[0]) < 1e-6)
     assert o[:hd].max() < o[2 * hd:3 * hd].min()  # heads 0-1 read KV head 0, heads 2-3 KV head 1
+
+
+def _appended_k(dec, kv, x, pos):
+    """The k row layer 0 appends at pos for token x (float32 copy)."""
+    t = D.rms_norm(x, dec.w["norm1"][0], dec.eps)
+    dec.layer_attn(0, t, [pos], kv)
+    return kv[0][0][0][pos].copy()
+
+
+def test_whole_vector_qk_norm_invariants():
+    """qk_norm_type 2 (decode_kernel.c:1155-1167) pinned by what it must do,
+    observed through the appended k row and the attention output:
+    * k over all KH * hd values has mean square 1 (unit weight, eps 0,
+      position 0 where RoPE is the identity) while its heads keep their
+      relative scale (a per-head norm would make each head's mean square 1);
+    * the weight multiplies elementwise after the scaling;
+    * the norm comes before RoPE: a weight that zeroes dimensions 64..127 of
+      every head leaves a sin-rotated copy of dimensions 0..63 there;
+    * q: scaling all of wq leaves the output unchanged, scaling one head's
+      rows changes it (with a per-head norm it would not)."""
+    dec, shape, blob, offsets, kv = _tiny_model(L=1, B=1, qk=2)
+    H, KH, hd = dec.H, dec.KH, dec.hd
+    dec.eps = 0.0
+    x = np.random.default_rng(11).standard_normal((1, 512)).astype(np.float32)
+    dec.w["kn"][0][:] = 1.0
+    dec.w["wk"][0][hd:] *= 4.0                       # KV head 1 four times larger
+    k0 = _appended_k(dec, kv, x, 0).astype(np.float64)
+    assert abs((k0 ** 2).mean() - 1.0) < 4e-3        # sqrtf_fast and bf16 rounding
+    ratio = (k0[1] ** 2).mean() / (k0[0] ** 2).mean()
+    assert 8.0 < ratio < 32.0                        # not equalised per head
+    wt = D.bf16_round((1.0 + 0.5 * np.random.default_rng(12).standard_normal(KH * hd)).astype(np.float32))
+    dec.w["kn"][0][:] = wt
+    kw = _appended_k(dec, kv, x, 0).astype(np.float64)
+    rel = np.abs(kw.reshape(-1) - k0.reshape(-1) * wt) / (np.abs(k0.reshape(-1) * wt) + 1e-3)
+    assert rel.max() < 2 ** -7
+    half = np.tile(np.r_[np.ones(hd // 2), np.zeros(hd // 2)], KH).astype(np.float32)
+    dec.w["kn"][0][:] = half
+    p = 37
+    kr = _appended_k(dec, kv, x, p)
+    k_half = _appended_k(dec, kv, x, 0)              # position 0: the normed, weighted values
+    s_ = dec.w["sin"][p][:hd // 2]
+    for kh in range(KH):
+        second = kr[kh, hd // 2:]
+        assert np.abs(second).max() > 0.1
+        want = D.bf16_round((k_half[kh, :hd // 2] * s_).astype(np.float32))
+        assert np.allclose(second, want, rtol=2 ** -6, atol=1e-3)
+    # q through the attention output (two positions so the scores matter)
+    dec.w["kn"][0][:] = 1.0
+    t = D.rms_norm(x, dec.w["norm1"][0], dec.eps)
+    base = dec.layer_attn(0, t, [40], kv)
+    dec.w["wq"][0] *= 3.0
+    same = dec.layer_attn(0, t, [40], kv)
+    # unchanged up to sqrtf_fast, whose relative error (< 2e-3) differs between ss and 9 ss
+    assert np.abs(same - base).max() <= 5e-3 * np.abs(base).max()
+    dec.w["wq"][0][:hd] *= 3.0                       # query head 0 only
+    diff = dec.layer_attn(0, t, [40], kv)
+    assert np.abs(diff - base).max() > 5e-2 * np.abs(base).max()
+    dec.qk = 1                                       # per head: the same change is invisible
+    dec.w["qn"], dec.w["kn"] = np.ones((1, hd), np.float32), np.ones((1, hd), np.float32)
+    dec.w["wq"][0][:hd] /= 3.0
+    b1 = dec.layer_attn(0, t, [40], kv)
+    dec.w["wq"][0][:hd] *= 3.0
+    d1 = dec.layer_attn(0, t, [40], kv)
+    assert np.abs(d1 - b1).max() <= 5e-3 * np.abs(b1).max()
 
 
 def _lm_head_A_scan(logits, n_workers):
