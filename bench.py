@@ -321,12 +321,13 @@ def router_margins(store, n_layers, x):
             "per_layer_token": [[float(f"{v:.4g}") for v in row] for row in m]}
 
 
-def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
+def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176, kv_f32=False):
     """The full Qwen3-30B-A3B-shaped decode step: n_layers x (attention + MoE
     block) at batch B, every token at cache position `position` (attention
-    over position + 1 rows of a bf16 cache filled with N(0, 1)).  Returns
-    tokens/s, the attention / MoE split of a profiled step, and the
-    algorithmic HBM bytes of a step (routed experts counted per layer)."""
+    over position + 1 rows of a bf16 cache, or with kv_f32 a float32 one,
+    filled with N(0, 1)).  Returns tokens/s, the attention / MoE split of a
+    profiled step, and the algorithmic HBM bytes of a step (routed experts
+    counted per layer)."""
     import numpy as np
     import torch
 
@@ -339,7 +340,8 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
     log(f"decode: building {n_layers} Qwen3-30B-A3B layers (store, attention weights, KV cache)")
     store, _ = build_layers(QWEN3, n_layers, group, seed=1000)
     weights = DecoderWeights(shape, **decoder_weights(shape))
-    kv = KVCacheSet(shape, B)
+    kv_dtype = torch.float32 if kv_f32 else torch.bfloat16
+    kv = KVCacheSet(shape, B, dtype=kv_dtype)
     fill_kv(kv.data)
     dec = HipDecoder(store, weights)
     x = torch.from_numpy(activations(B, shape.d)).cuda()
@@ -380,7 +382,7 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
     T = position + 1
     moe_bytes = sum(U) * eb + n_layers * (QWEN3.E * d * store.router_bytes_per_weight() + 2 * B * d * 4)
     attn_w = n_layers * 2 * (H * hd * d + 2 * KH * hd * d + d * H * hd)
-    kv_bytes = n_layers * B * T * KH * hd * 2 * 2
+    kv_bytes = n_layers * B * T * KH * hd * 2 * kv.data.element_size()
     total = moe_bytes + attn_w + kv_bytes
     ok = bool(torch.isfinite(hid).all().item())
     # the serve path: the same step ending in the lm_head (vocabulary 151936,
@@ -416,7 +418,7 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
     dec.weights.t["embed"] = (torch.randn((shape.V, shape.d), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
     dec._w = dec.weights.kernel_w()
     prompt = torch.randint(0, shape.V, (Tp,), generator=g, device="cuda", dtype=torch.int32)
-    kvp = KVCacheSet(shape, 1)
+    kvp = KVCacheSet(shape, 1, dtype=kv_dtype)
     plog = torch.empty(shape.V, dtype=torch.float32, device="cuda")
     dec.prefill_layers(prompt, kvp, 0, plog)
     torch.cuda.synchronize()
@@ -440,7 +442,7 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
     del kvp
     res = {
         "tok_per_s": B / (ms * 1e-3), "ms_per_step": ms, "host_enqueue_ms_per_step": host_ms,
-        "layers": n_layers, "batch": B, "position": position,
+        "layers": n_layers, "batch": B, "position": position, "kv_cache": "f32" if kv_f32 else "bf16",
         "attention_ms_profiled": split["attention"], "moe_ms_profiled": split["moe"],
         "step_ms_profiled": split["total"],
         "moe_share": split["moe"] / split["total"] if split["total"] > 0 else None,
@@ -462,7 +464,7 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176):
             "GBs": (total + lm_bytes) / (ms_lm * 1e-3) / 1e9,
         },
     }
-    log(f"decode {n_layers} layers B={B}: {res['tok_per_s']:.0f} tok/s, {ms:.3f} ms/step "
+    log(f"decode {n_layers} layers B={B} ({res['kv_cache']} cache): {res['tok_per_s']:.0f} tok/s, {ms:.3f} ms/step "
         f"(host enqueue {host_ms:.3f} ms), attention {split['attention']:.3f} ms, MoE {split['moe']:.3f} ms, "
         f"{res['GBs']:.0f} GB/s over {total / 1e9:.2f} GB; with lm_head + argmax {B / (ms_lm * 1e-3):.0f} tok/s "
         f"({ms_lm:.3f} ms/step; lm_head {lm_ms * 1e3:.1f} us, {lm_bytes / (lm_ms * 1e-3) / 1e9:.0f} GB/s); "
@@ -536,7 +538,7 @@ def prefill_only(group, reps, n_layers=48, maxT=2176, Tp=512):
     dec.weights.t["embed"] = (torch.randn((shape.V, shape.d), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
     dec._w = dec.weights.kernel_w()
     prompt = torch.randint(0, shape.V, (Tp,), generator=g, device="cuda", dtype=torch.int32)
-    kvp = KVCacheSet(shape, 1)
+    kvp = KVCacheSet(shape, 1, dtype=kv_dtype)
     plog = torch.empty(shape.V, dtype=torch.float32, device="cuda")
     dec.prefill_layers(prompt, kvp, 0, plog)
     torch.cuda.synchronize()
@@ -621,6 +623,8 @@ def main() -> int:
     ap.add_argument("--decode-layers", type=int, default=48,
                     help="layers of the --decode-only step (1: every byte of the layer stays in the 256 MB "
                          "Infinity Cache, which shows how much of each kernel's time is HBM bandwidth)")
+    ap.add_argument("--kv-f32", action="store_true",
+                    help="with --decode-only: float32 caches (the reference's KVCache type) instead of bf16")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 48-layer 512-token prefill (--steps timed passes); prints its JSON")
     ap.add_argument("--zipf-only", action="store_true",
@@ -654,7 +658,8 @@ def main() -> int:
         print(json.dumps({"probe": probe_costs()}), flush=True)
         return 0
     if args.decode_only:
-        r = decode_step(args.batch, args.steps, args.warmup, args.group, n_layers=args.decode_layers)
+        r = decode_step(args.batch, args.steps, args.warmup, args.group, n_layers=args.decode_layers,
+                        kv_f32=args.kv_f32)
         print(json.dumps({"decode_step": r}), flush=True)
         return 0
     if args.prefill_only:

@@ -184,8 +184,9 @@ int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t by
 /* ---- batch decode over all layers (decode_layers_batch) ---- */
 
 /* One sequence's cache of one layer, the reference's KVCache
- * (decode_kernel.c:328-331): k and v [maxT][n_kv][hd], here bfloat16 device
- * memory (the reference's is float32). */
+ * (decode_kernel.c:328-331): k and v [maxT][n_kv][hd] in device memory,
+ * bfloat16 by default; float32, the reference's own type, after
+ * jm_store_set_kv_dtype(store, JM_DTYPE_F32). */
 typedef struct jm_kv_cache {
     void* k;
     void* v;
@@ -317,6 +318,15 @@ int jm_store_decode_graph(jm_store* s, int enable);
  * default) runs all.  The reference's setting is process-global
  * (g_max_layers); here it is per store. */
 int jm_store_set_max_layers(jm_store* s, int n);
+
+/* The element type of the caches (jm_kv_cache) that later
+ * jm_decode_layers_batch, jm_decode_layers_batch_argmax and
+ * jm_prefill_layers calls of this store read and append to:
+ * JM_DTYPE_BF16 (the default: half the bytes per attention read) or
+ * JM_DTYPE_F32, the reference's KVCache (decode_kernel.c:328-331), whose
+ * appended rows then keep float32 values and whose attention runs in
+ * float32 arithmetic throughout. */
+int jm_store_set_kv_dtype(jm_store* s, int dtype);
 
 /* With buf set (device int32, `bytes` long), each later
  * jm_decode_layers_batch also copies every layer's selected experts into

@@ -517,9 +517,25 @@ k_qk_ss(AttnArgs a) {
                                                          __fadd_rn(red[tid][2], red[tid][3]));
 }
 
+// The same for float32 caches (the reference's KVCache type): the finished
+// values are appended as they are; with kvf, also kept there (kvf[0]: k,
+// kvf[1]: v).
+__device__ __forceinline__ void kv_store_f32(const KvFin& k, const AttnArgs& a, int b, int kh, int pos, int lane,
+                                             gptr<float> kc, gptr<float> vc, float (*kvf)[128]) {
+    constexpr int HD = 128;
+    const int j = lane & 31;
+    float v[4];
+    fin4_value(v, k.f, a, b, k.row, k.isk && a.kn ? a.qk_norm : 0, k.isk, j);
+    const f32x4_t v4 = f32x4_t{v[0], v[1], v[2], v[3]};
+    if (kvf) *(f32x4_t*)&kvf[k.isk ? 0 : 1][4 * j] = v4;
+    const gptr<float> dst = (k.isk ? kc : vc) + ((size_t)pos * a.KH + kh) * HD + 4 * j;
+    *(gptr<f32x4_t>)dst = v4;
+}
+
 // For a batch whose tokens may share a cache (a prefill chunk: the
 // positions of one prompt), every token's k and v rows are appended before
 // the attention reads the caches: one wave per (KV head, token).
+template <bool F32>
 __global__ void __launch_bounds__(64)
 k_kv_append(AttnArgs a) {
     const int kh = blockIdx.x, b = blockIdx.y;
@@ -527,7 +543,45 @@ k_kv_append(AttnArgs a) {
     const unsigned long long* kvp = a.kv + ((size_t)b * a.L + a.layer) * 2;
     KvFin k;
     kv_load(k, a, b, kh, pos, threadIdx.x);
-    kv_store(k, a, b, kh, pos, threadIdx.x, (gptr<uint16_t>)kvp[0], (gptr<uint16_t>)kvp[1], nullptr);
+    if (F32) kv_store_f32(k, a, b, kh, pos, threadIdx.x, (gptr<float>)kvp[0], (gptr<float>)kvp[1], nullptr);
+    else kv_store(k, a, b, kh, pos, threadIdx.x, (gptr<uint16_t>)kvp[0], (gptr<uint16_t>)kvp[1], nullptr);
+}
+
+// The 4 waves' partial outputs of a split block merged with the split's
+// max (the flash-decoding merge within the block) into part_o / part_ml:
+// thread tid takes head tid / 32, dimensions 4 (tid % 32) .. + 3, so that
+// each thread forms the 4 waves' factors of one head once.
+template <int QPK>
+__device__ __forceinline__ void merge_waves(const AttnArgs& a, int b, int kh, int s, const float (*red)[QPK * 128],
+                                            const float (*mls)[QPK][2]) {
+    constexpr int HD = 128;
+    const int tid = threadIdx.x;
+    float* po = a.part_o + (((size_t)b * a.KH + kh) * a.S + s) * QPK * HD;
+    {
+        const int h = tid >> 5, oi = h * HD + 4 * (tid & 31);
+        if (h < QPK) {
+            const float M = fmaxf(fmaxf(mls[0][h][0], mls[1][h][0]), fmaxf(mls[2][h][0], mls[3][h][0]));
+            float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float L = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) {
+                const float m = mls[ww][h][0];
+                const float f = m == -INFINITY ? 0.0f : expf_fast(__fsub_rn(m, M));
+                const float4 r = *(const float4*)&red[ww][oi];
+                O.x = __builtin_fmaf(r.x, f, O.x);
+                O.y = __builtin_fmaf(r.y, f, O.y);
+                O.z = __builtin_fmaf(r.z, f, O.z);
+                O.w = __builtin_fmaf(r.w, f, O.w);
+                L = __builtin_fmaf(mls[ww][h][1], f, L);
+            }
+            *(float4*)(po + oi) = O;
+            if ((tid & 31) == 0) {
+                float* ml = a.part_ml + ((((size_t)b * a.KH + kh) * a.S + s) * QPK + h) * 2;
+                ml[0] = M;
+                ml[1] = L;
+            }
+        }
+    }
 }
 
 // One (position split, KV head, token): QPK query heads over positions
@@ -743,35 +797,139 @@ k_attn_part(AttnArgs a) {
     }
     __syncthreads();
 
-    // ---- the waves merged with the split's max: thread tid takes head
-    // tid / 32, dimensions 4 (tid % 32) .. + 3, so that each thread forms
-    // the 4 waves' factors of one head once
-    float* po = a.part_o + (((size_t)b * a.KH + kh) * a.S + s) * QPK * HD;
+    merge_waves<QPK>(a, b, kh, s, red, mls);
+}
+
+// The split block over float32 caches, in float32 arithmetic throughout
+// (the reference's SDPA, :1200-1222, on its own cache type): the same
+// block shape, prologue and partial outputs as k_attn_part, on the vector
+// units.  Wave w takes positions tw = 128 s + 32 w .. tw + 31.
+//   scores  lane l: position tw + l % 32 and dimensions 64 (l / 32) .. + 63
+//           of its K row (16 float4 loads), against the finished query
+//           heads in LDS; the two halves' sums added across lanes l, l ^ 32
+//   P . V   lane l: dimensions 2 l, 2 l + 1 of the 32 V rows (one float2
+//           load per row, a whole row per wave load), the softmax
+//           numerators read back from LDS
+template <int QPK>
+__global__ void __launch_bounds__(256)
+k_attn_part_f32(AttnArgs a) {
+    constexpr int HD = 128, P = 128, PW = 32;
+    __shared__ __align__(16) float qf[QPK][HD];          // the finished query heads
+    __shared__ __align__(16) float kvf[2][HD];           // the token's own k and v rows
+    __shared__ __align__(16) float pw[4][QPK][PW];       // each wave's softmax numerators
+    __shared__ __align__(16) float red[4][QPK * HD];     // each wave's outputs
+    __shared__ float mls[4][QPK][2];                     // each wave's (max, sum)
+    const int s = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int pos = a.pos[b];
+    const int T = pos + 1;
+    const int t0 = s * P;
+    if (t0 >= T) return;                 // past this token's positions (block-uniform)
+    const bool own = a.append && pos < t0 + P;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int pl = lane & 31, hf = lane >> 5;
+    const int tw = t0 + PW * w;
+    const unsigned long long* kvp = a.kv + ((size_t)b * a.L + a.layer) * 2;
+    const gptr<float> kc = (gptr<float>)kvp[0];
+    const gptr<float> vc = (gptr<float>)kvp[1];
+    // requests first, in the order of use (as k_attn_part): the prologue's
+    // inputs, the K rows, the V rows (row 0 past the end)
+    const int qh = tid >> 5, qj = tid & 31;
+    const int qhc = qh < QPK ? qh : 0;
+    const int qrow = (kh * QPK + qhc) * HD + 4 * qj;
+    const bool kvw = own && w == 0;                  // wave-uniform
+    Fin4 fq;
+    fin4_load(fq, a, b, qrow, a.bq, qrow, qk_weight(a, true, kh * QPK + qhc), true, pos, qj);
+    KvFin fkv;
+    if (kvw) kv_load(fkv, a, b, kh, pos, lane);
+    f32x4_t kr[16];
     {
-        const int h = tid >> 5, oi = h * HD + 4 * (tid & 31);
-        if (h < QPK) {
-            const float M = fmaxf(fmaxf(mls[0][h][0], mls[1][h][0]), fmaxf(mls[2][h][0], mls[3][h][0]));
-            float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            float L = 0.0f;
+        const int t = tw + pl;
+        const gptr<float> row = kc + ((size_t)(t < T ? t : 0) * a.KH + kh) * HD + 64 * hf;
 #pragma unroll
-            for (int ww = 0; ww < 4; ww++) {
-                const float m = mls[ww][h][0];
-                const float f = m == -INFINITY ? 0.0f : expf_fast(__fsub_rn(m, M));
-                const float4 r = *(const float4*)&red[ww][oi];
-                O.x = __builtin_fmaf(r.x, f, O.x);
-                O.y = __builtin_fmaf(r.y, f, O.y);
-                O.z = __builtin_fmaf(r.z, f, O.z);
-                O.w = __builtin_fmaf(r.w, f, O.w);
-                L = __builtin_fmaf(mls[ww][h][1], f, L);
-            }
-            *(float4*)(po + oi) = O;
-            if ((tid & 31) == 0) {
-                float* ml = a.part_ml + ((((size_t)b * a.KH + kh) * a.S + s) * QPK + h) * 2;
-                ml[0] = M;
-                ml[1] = L;
+        for (int i = 0; i < 16; i++) kr[i] = *(gptr<const f32x4_t>)(row + 4 * i);
+    }
+    f32x2_t vr[PW];
+#pragma unroll
+    for (int j = 0; j < PW; j++) {
+        const int t = tw + j;
+        vr[j] = *(gptr<const f32x2_t>)(vc + ((size_t)(t < T ? t : 0) * a.KH + kh) * HD + 2 * lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);      // keep every request ahead of the arithmetic
+    {
+        float v[4];
+        fin4_value(v, fq, a, b, qrow, a.qn ? a.qk_norm : 0, true, qj);
+        if (qh < QPK) *(float4*)&qf[qh][4 * qj] = make_float4(v[0], v[1], v[2], v[3]);
+        if (kvw) kv_store_f32(fkv, a, b, kh, pos, lane, kc, vc, kvf);
+    }
+    __syncthreads();
+    if (own) {
+        // the token's own row, not read from the cache (appended above)
+        if (tw + pl == pos) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) kr[i] = *(const f32x4_t*)&kvf[0][64 * hf + 4 * i];
+        }
+#pragma unroll
+        for (int j = 0; j < PW; j++)
+            if (tw + j == pos) vr[j] = *(const f32x2_t*)&kvf[1][2 * lane];
+    }
+
+    // ---- scores q . k / sqrtf_fast(hd) (as q . k times the divisor's
+    // reciprocal), softmax numerators with the wave's own max
+    const bool live = tw + pl < T;
+    float mx[QPK], lsum[QPK];
+#pragma unroll
+    for (int h = 0; h < QPK; h++) {
+        const float4* q4 = (const float4*)&qf[h][64 * hf];
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 q = q4[i];
+            acc = __builtin_fmaf(kr[i].x, q.x, acc);
+            acc = __builtin_fmaf(kr[i].y, q.y, acc);
+            acc = __builtin_fmaf(kr[i].z, q.z, acc);
+            acc = __builtin_fmaf(kr[i].w, q.w, acc);
+        }
+        const float tot = __fadd_rn(acc, __shfl_xor(acc, 32, JM_WAVE));
+        const float sc = live ? __fmul_rn(tot, a.rsdiv) : -INFINITY;
+        mx[h] = seg_max<32>(sc);
+        const float mref = mx[h] == -INFINITY ? 0.0f : mx[h];     // a wave wholly past T
+        const float p = expf_fast(__fsub_rn(sc, mref));
+        lsum[h] = seg_sum<32>(p);
+        if (hf == 0) pw[w][h][pl] = p;
+    }
+    // LDS operations of one wave complete in order; this keeps the compiler
+    // from moving the reads above the writes
+    __asm__ volatile("" : : : "memory");
+
+    // ---- P . V over the wave's positions, in position order
+    float2 o[QPK];
+#pragma unroll
+    for (int h = 0; h < QPK; h++) o[h] = make_float2(0.0f, 0.0f);
+#pragma unroll
+    for (int j4 = 0; j4 < PW / 4; j4++) {
+#pragma unroll
+        for (int h = 0; h < QPK; h++) {
+            const float4 p4 = *(const float4*)&pw[w][h][4 * j4];
+            const float pp[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                o[h].x = __builtin_fmaf(vr[4 * j4 + u].x, pp[u], o[h].x);
+                o[h].y = __builtin_fmaf(vr[4 * j4 + u].y, pp[u], o[h].y);
             }
         }
     }
+#pragma unroll
+    for (int h = 0; h < QPK; h++) *(float2*)&red[w][h * HD + 2 * lane] = o[h];
+    if (lane < QPK) {
+        float m = mx[0], l = lsum[0];
+#pragma unroll
+        for (int h = 1; h < QPK; h++)
+            if (lane == h) { m = mx[h]; l = lsum[h]; }
+        mls[w][lane][0] = m;
+        mls[w][lane][1] = l;
+    }
+    __syncthreads();
+    merge_waves<QPK>(a, b, kh, s, red, mls);
 }
 
 // Merge of the splits of one (query head, token): out = sum_s o_s e^(m_s - M)
@@ -858,18 +1016,22 @@ hipError_t launch_attn(const AttnArgs& a, int qpk, float* att, hipStream_t st) {
         if (e0 != hipSuccess) return e0;
     }
     if (!a.append) {
-        hipLaunchKernelGGL(k_kv_append, dim3((unsigned)a.KH, (unsigned)a.B), dim3(64), 0, st, a);
+        if (a.kv_f32) hipLaunchKernelGGL(k_kv_append<true>, dim3((unsigned)a.KH, (unsigned)a.B), dim3(64), 0, st, a);
+        else hipLaunchKernelGGL(k_kv_append<false>, dim3((unsigned)a.KH, (unsigned)a.B), dim3(64), 0, st, a);
         hipError_t e0 = hipGetLastError();
         if (e0 != hipSuccess) return e0;
     }
     const dim3 grid((unsigned)a.S, (unsigned)a.KH, (unsigned)a.B);
+#define JM_AP(Q) if (a.kv_f32) hipLaunchKernelGGL(k_attn_part_f32<Q>, grid, dim3(256), 0, st, a); \
+                 else hipLaunchKernelGGL(k_attn_part<Q>, grid, dim3(256), 0, st, a)
     switch (qpk) {
-        case 1: hipLaunchKernelGGL(k_attn_part<1>, grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL(k_attn_part<2>, grid, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(k_attn_part<4>, grid, dim3(256), 0, st, a); break;
-        case 8: hipLaunchKernelGGL(k_attn_part<8>, grid, dim3(256), 0, st, a); break;
+        case 1: JM_AP(1); break;
+        case 2: JM_AP(2); break;
+        case 4: JM_AP(4); break;
+        case 8: JM_AP(8); break;
         default: return hipErrorInvalidValue;
     }
+#undef JM_AP
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_comb, dim3((unsigned)a.H, (unsigned)a.B), dim3(128), 0, st, a, qpk, att);

@@ -187,7 +187,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         at.qkss = s->qkss;
         at.eps = c->eps; at.rsdiv = 1.0f / sdiv;
         at.cos = W->cos; at.sin = W->sin;
-        at.pos = pos_dev; at.kv = s->tab; at.L = L; at.layer = l;
+        at.pos = pos_dev; at.kv = s->tab; at.kv_f32 = s->kv_f32; at.L = L; at.layer = l;
         at.S = S; at.part_o = s->part_o; at.part_ml = s->part_ml;
         at.append = append ? 1 : 0;
         // the grid covers the longest token's splits; the buffers hold S_cap
@@ -362,6 +362,7 @@ int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const
         key.wt = s->wt; key.wt_bf16 = s->wt_bf16; key.lm_V = s->lm_V; key.nl = run_layers(s, c->L);
         key.dense_min = s->dense_min;
         key.append = append ? 1 : 0;
+        key.kv_f32 = s->kv_f32;
         if (!s->gexec || memcmp(&key, &s->gkey, sizeof key) != 0) {
             if (s->gexec) {
                 JM_HIP(hipStreamSynchronize(st), "hipStreamSynchronize before recapture");
@@ -524,6 +525,14 @@ int jm_embed_lookup(const jm_kernel_w* W, const jm_kernel_cfg* c, const int32_t*
 int jm_store_decode_graph(jm_store* s, int enable) {
     if (!s) return fail(JM_ERR_ARG, "store is NULL");
     s->dgraph = enable ? 1 : 0;      // a recorded step is kept for later replays
+    return 0;
+}
+
+int jm_store_set_kv_dtype(jm_store* s, int dtype) {
+    if (!s) return fail(JM_ERR_ARG, "store is NULL");
+    if (dtype != JM_DTYPE_BF16 && dtype != JM_DTYPE_F32)
+        return fail(JM_ERR_ARG, "dtype must be JM_DTYPE_BF16 or JM_DTYPE_F32 (got %d)", dtype);
+    s->kv_f32 = dtype == JM_DTYPE_F32 ? 1 : 0;
     return 0;
 }
 

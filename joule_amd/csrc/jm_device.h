@@ -105,6 +105,8 @@ template <typename T>
 using gptr = T __attribute__((address_space(1)))*;
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 // 16 bytes at a global address (16-byte aligned)
 __device__ __forceinline__ uint4 load_g16(gptr<const uint16_t> p) {

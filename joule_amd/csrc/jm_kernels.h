@@ -216,7 +216,8 @@ struct AttnArgs {
     const float* cos;         // [maxT][128]
     const float* sin;
     const int* pos;           // [B] position each token writes (T = pos + 1)
-    const unsigned long long* kv;   // [B*L][2] bf16 k, v caches [maxT][KH][128]
+    const unsigned long long* kv;   // [B*L][2] k, v caches [maxT][KH][128], bf16 or (kv_f32) float32
+    int kv_f32;               // 1: the caches hold float32 (the reference's KVCache), 0: bf16
     int L, layer;
     int append;               // 1: every token has its own cache; the attention appends its k and v
                               // rows itself.  0: k_kv_append appends every row first

@@ -64,6 +64,7 @@ struct DecKey {
     int wt_bf16;                // element type of the router copy: a reallocation may return the same address
     int lm_V;
     int nl;                     // layers the step runs (jm_store_set_max_layers)
+    int kv_f32;                 // element type of the caches (jm_store_set_kv_dtype)
     int dense_min;
     int append;                 // the attention appends the k and v rows itself (no cache shared by two tokens)
 };
@@ -109,6 +110,7 @@ struct jm_store {
     int* lmi;                   // [lm blocks][B] its row
     float* rss;                 // [B] sums of squares of h from the projection GEMM (prefill chunks)
     float* qkss;                // [B][2] sums of squares of q and k (whole-vector QK-norm)
+    int kv_f32;                 // the caches the decoder reads and writes hold float32 (else bf16)
     unsigned long long* tab;    // [B*L][2] KV pointers, then [B] positions (device)
     unsigned long long* tab_host;   // pinned staging of tab
     size_t tab_cap;             // bytes of tab / tab_host

@@ -186,16 +186,19 @@ class DecoderWeights:
 
 
 class KVCacheSet:
-    """bf16 caches for B sequences x L layers: one tensor [B, L, 2, maxT, KH, hd]
-    and the KVCache[B*L] array (entry b*L + l) that points into it."""
+    """Caches for B sequences x L layers: one tensor [B, L, 2, maxT, KH, hd]
+    and the KVCache[B*L] array (entry b*L + l) that points into it.  bfloat16
+    by default; float32 is the reference's own KVCache type
+    (decode_kernel.c:328-331)."""
 
-    def __init__(self, shape: DecoderShape, B: int, device="cuda", data: torch.Tensor | None = None):
+    def __init__(self, shape: DecoderShape, B: int, device="cuda", data: torch.Tensor | None = None,
+                 dtype: torch.dtype = torch.bfloat16):
         L, KH, hd, T = shape.n_layers, shape.n_kv, shape.hd, shape.maxT
         full = (B, L, 2, T, KH, hd)
         if data is None:
-            data = torch.zeros(full, dtype=torch.bfloat16, device=device)
-        if data.dtype != torch.bfloat16 or tuple(data.shape) != full or not data.is_contiguous():
-            raise ValueError(f"cache must be a contiguous bfloat16 tensor {full}")
+            data = torch.zeros(full, dtype=dtype, device=device)
+        if data.dtype not in (torch.bfloat16, torch.float32) or tuple(data.shape) != full or not data.is_contiguous():
+            raise ValueError(f"cache must be a contiguous bfloat16 or float32 tensor {full}")
         self.shape, self.B, self.data = shape, B, data
         self.table = (KVCache * (B * L))()
         for b in range(B):
@@ -244,6 +247,7 @@ class HipDecoder:
         if logits is not None and (logits.dtype != torch.float32 or tuple(logits.shape) != (B, self.shape.V)
                                    or not logits.is_contiguous()):
             raise ValueError(f"logits must be a contiguous float32 tensor [{B}, {self.shape.V}]")
+        self._kv_dtype(kv)
         _lib.check(_lib.lib().jm_decode_layers_batch(
             self.store._h, ctypes.byref(self._cfg), ctypes.byref(self._w), self._table(kv, B, seqs),
             pos.ctypes.data_as(ctypes.c_void_p), _lib.ptr(x), B, _lib.ptr(logits), _lib.ptr(hidden),
@@ -271,6 +275,13 @@ class HipDecoder:
         else:
             raise ValueError("lm_head dtype must be bfloat16 or float32")
         _lib.check(_lib.lib().jm_store_set_lm_head(self.store._h, _lib.ptr(lm_head), dt, V), "jm_store_set_lm_head")
+
+    def _kv_dtype(self, kv: KVCacheSet) -> None:
+        """The store reads and appends caches of kv's element type."""
+        dt = _lib.JM_DTYPE_F32 if kv.data.dtype == torch.float32 else _lib.JM_DTYPE_BF16
+        if getattr(self, "_kvdt", None) != dt:
+            _lib.check(_lib.lib().jm_store_set_kv_dtype(self.store._h, dt), "jm_store_set_kv_dtype")
+            self._kvdt = dt
 
     def _positions(self, positions, B):
         pos = np.ascontiguousarray(np.asarray(positions, dtype=np.int32).reshape(-1))
@@ -308,6 +319,7 @@ class HipDecoder:
         if not 0 <= seq < kv.B:
             raise ValueError("seq outside the cache set")
         table = (KVCache * L).from_buffer(kv.table, seq * L * ctypes.sizeof(KVCache))
+        self._kv_dtype(kv)
         _lib.check(_lib.lib().jm_prefill_layers(
             self.store._h, ctypes.byref(self._cfg), ctypes.byref(self._w), ctypes.cast(table, _vp),
             _lib.ptr(tokens), tokens.numel(), _lib.ptr(logits), _lib.stream_handle(stream)), "jm_prefill_layers")
@@ -323,6 +335,7 @@ class HipDecoder:
         pos = self._positions(positions, B)
         if out_tok is None:
             out_tok = torch.empty(B, dtype=torch.int32, device=x.device)
+        self._kv_dtype(kv)
         _lib.check(_lib.lib().jm_decode_layers_batch_argmax(
             self.store._h, ctypes.byref(self._cfg), ctypes.byref(self._w), self._table(kv, B),
             pos.ctypes.data_as(ctypes.c_void_p), _lib.ptr(x), B, _lib.ptr(out_tok), None,

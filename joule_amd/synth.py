@@ -186,12 +186,13 @@ def decoder_weights(shape, seed: int = 6000, device: str | torch.device = "cuda"
 
 
 def fill_kv(data: torch.Tensor, seed: int = 5000) -> torch.Tensor:
-    """Fill a cache tensor [B, L, 2, T, KH, hd] (bf16) with N(0, 1): one
-    generator per layer, seeded seed + layer, drawing [B, 2, T, KH, hd]."""
+    """Fill a cache tensor [B, L, 2, T, KH, hd] (bf16 or float32) with
+    N(0, 1): one generator per layer, seeded seed + layer, drawing
+    [B, 2, T, KH, hd]."""
     B, L = data.shape[0], data.shape[1]
     for l in range(L):
         gen = torch.Generator(device=data.device)
         gen.manual_seed(seed + l)
         data[:, l].copy_(torch.randn(data[:, l].shape, generator=gen, device=data.device,
-                                     dtype=torch.float32).to(torch.bfloat16))
+                                     dtype=torch.float32).to(data.dtype))
     return data

@@ -24,11 +24,12 @@ Follows src/jouleai/native/decode_kernel.c:
   embed_lookup          :1597-1600  bf16 embedding row
 
 Two deliberate differences from the reference, both matching the GPU path:
-the KV cache holds bfloat16 values (the reference's is float32,
+by default the KV cache holds bfloat16 values (the reference's is float32,
 decode_kernel.c:328-331): the appended k and v are rounded to bf16 before
-attention reads them; and dot products / sums of squares are accumulated in
-float64 and rounded once, where the reference accumulates in float32 in its
-own lane order (a difference at rounding level).
+attention reads them (kv_bf16=False keeps float32 rows, the reference's
+cache); and dot products / sums of squares are accumulated in float64 and
+rounded once, where the reference accumulates in float32 in its own lane
+order (a difference at rounding level).
 """
 
 from __future__ import annotations
@@ -100,12 +101,13 @@ class OracleDecoder:
     qn/kn [L, hd] (qk_norm_type 1) or [L, H*hd] / [L, KH*hd] (qk_norm_type
     2), bq/bk/bv (bias_qkv), cos/sin [maxT, hd].
     ``moe[l]`` is an OracleMoE for layer l.  The caches are float32 arrays
-    [B][L] of (k, v) [maxT, KH, hd] holding bf16 values; they are updated in
-    place like the reference's.
+    [B][L] of (k, v) [maxT, KH, hd], holding bf16 values unless kv_bf16 is
+    False; they are updated in place like the reference's.
     """
 
-    def __init__(self, L, d, H, KH, hd, eps, qk_norm_type, bias_qkv, w: dict, moe):
+    def __init__(self, L, d, H, KH, hd, eps, qk_norm_type, bias_qkv, w: dict, moe, kv_bf16: bool = True):
         self.L, self.d, self.H, self.KH, self.hd = L, d, H, KH, hd
+        self.kv_bf16 = bool(kv_bf16)
         self.eps, self.qk, self.bias = float(eps), int(qk_norm_type), bool(bias_qkv)
         self.w, self.moe = w, moe
         self.sdiv = sqrtf_fast(F32(hd))
@@ -139,8 +141,8 @@ class OracleDecoder:
             qb = rope(qb, c, s)
             kb = rope(kb, c, s)
             kc, vc = kv[b][l]
-            kc[pos] = bf16_round(kb)
-            vc[pos] = bf16_round(vb)
+            kc[pos] = bf16_round(kb) if self.kv_bf16 else kb
+            vc[pos] = bf16_round(vb) if self.kv_bf16 else vb
             T = pos + 1
             for h in range(H):
                 kh = h // g

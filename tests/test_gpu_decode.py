@@ -29,7 +29,7 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
-def _model(shape: DecoderShape, group: int, B: int):
+def _model(shape: DecoderShape, group: int, B: int, kv_dtype=torch.bfloat16):
     L, moe = shape.n_layers, shape.moe
     blob, offsets = torch_store(moe, L, group)
     store = HbmExpertStore(moe, L, blob, offsets, group)
@@ -37,7 +37,7 @@ def _model(shape: DecoderShape, group: int, B: int):
     store.set_router(torch.from_numpy(gw).cuda())
     t = decoder_weights(shape, norm_jitter=0.1)
     weights = DecoderWeights(shape, **t)
-    kv = KVCacheSet(shape, B)
+    kv = KVCacheSet(shape, B, dtype=kv_dtype)
     fill_kv(kv.data)
     torch.cuda.synchronize()
     # the oracle's copies
@@ -46,7 +46,7 @@ def _model(shape: DecoderShape, group: int, B: int):
     moe_o = [O.OracleMoE(moe.d, moe.m, moe.E, moe.topk, moe.renorm, group, gw[l], blob_h,
                          offsets[:, l * moe.E:(l + 1) * moe.E]) for l in range(L)]
     oracle = D.OracleDecoder(L, moe.d, shape.n_heads, shape.n_kv, shape.hd, shape.eps, shape.qk_norm_type,
-                             shape.bias_qkv, w, moe_o)
+                             shape.bias_qkv, w, moe_o, kv_bf16=kv_dtype == torch.bfloat16)
     return HipDecoder(store, weights), oracle, kv
 
 
@@ -67,20 +67,24 @@ def _check_step(dec, oracle, kv, kv_h, x, positions, label):
     assert rel.max() <= TOL, f"{label}: per-token max rel error {rel}"
     # cache rows appended at the positions
     data = kv.data
+    f32 = data.dtype == torch.float32
     n_same = n_all = 0
     for b, p in enumerate(positions):
         for l in range(L):
             for j in (0, 1):
                 g = data[b, l, j, p].float().cpu().numpy()
                 r = kv_h[b][l][j][p]
-                # one bf16 unit, plus the upstream float32 differences, which
-                # scale with the row (not with elements near zero)
-                lim = np.abs(r) * 2.0 ** -7 + 1e-4 * np.abs(r).max()
+                # one bf16 unit (bf16 caches), plus the upstream float32
+                # differences, which scale with the row (not with elements
+                # near zero)
+                lim = np.abs(r) * (0.0 if f32 else 2.0 ** -7) + 1e-4 * np.abs(r).max()
                 bad = int((np.abs(g - r) > lim).sum())
-                assert bad == 0, f"{label}: cache row b={b} l={l} {'kv'[j]}: {bad} values off by more than a bf16 unit"
+                assert bad == 0, f"{label}: cache row b={b} l={l} {'kv'[j]}: {bad} values off by more than the bound"
                 n_same += int((g == r).sum())
                 n_all += g.size
-    assert n_same >= 0.98 * n_all, f"{label}: {n_all - n_same} of {n_all} cache values differ"
+    # bf16 rows are nearly all the same bf16 value; float32 rows differ in
+    # their last bits
+    assert f32 or n_same >= 0.98 * n_all, f"{label}: {n_all - n_same} of {n_all} cache values differ"
     return rel.max()
 
 
@@ -105,14 +109,25 @@ CASES = {
     "whole_bias_gqa2_l1_b3": (DecoderShape(n_layers=1, moe=MoEShape(d=1024, m=256, E=16, topk=4, renorm=True),
                                            n_heads=8, n_kv=4, maxT=200, qk_norm_type=2, bias_qkv=True),
                               32, [7, 150, 64]),
+    # float32 caches, the reference's KVCache type: Qwen3 layers (8 query
+    # heads per KV head), and OLMoE layers (one per KV head, whole-vector norm)
+    "qwen3_l2_b8_f32kv": (qwen3_30b_a3b(n_layers=2, maxT=2176), 64, [0, 1, 127, 128, 129, 700, 2047, 2048],
+                          torch.float32),
+    "olmoe_l1_b3_f32kv": (DecoderShape(n_layers=1, moe=MoEShape(d=2048, m=1024, E=64, topk=8, renorm=False),
+                                       n_heads=16, n_kv=16, maxT=300, qk_norm_type=2), 64, [31, 128, 299],
+                          torch.float32),
+    "gqa2_bias_l1_b2_f32kv": (DecoderShape(n_layers=1, moe=MoEShape(d=1024, m=256, E=16, topk=4, renorm=True),
+                                           n_heads=8, n_kv=4, maxT=200, qk_norm_type=1, bias_qkv=True),
+                              32, [0, 199], torch.float32),
 }
 
 
 @pytest.mark.parametrize("case", list(CASES))
 def test_decode_layers_batch_matches_oracle(case):
-    shape, group, positions = CASES[case]
+    shape, group, positions = CASES[case][:3]
+    kv_dtype = CASES[case][3] if len(CASES[case]) > 3 else torch.bfloat16
     B = len(positions)
-    dec, oracle, kv = _model(shape, group, B)
+    dec, oracle, kv = _model(shape, group, B, kv_dtype)
     kv_h = _kv_host(kv, B, shape.n_layers)
     x = activations(B, shape.d)
     _check_step(dec, oracle, kv, kv_h, x, positions, case)
@@ -153,15 +168,16 @@ def test_decode_split_profile_and_errors():
     dec.store.close()
 
 
-@pytest.mark.parametrize("B", [4, 40])
-def test_decode_graph_replays_match_eager(B):
+@pytest.mark.parametrize("B,kv_dtype", [(4, torch.bfloat16), (40, torch.bfloat16), (4, torch.float32)])
+def test_decode_graph_replays_match_eager(B, kv_dtype):
     """The step replayed from a captured HIP graph gives the eager step's bits,
     replay after replay, with eager work and synchronisation in between; new
     positions within the same split count replay the same graph, a new split
-    count records a new one.  B=40 (320 slots) takes the MoE dispatch path,
-    whose small-expert chain runs on a second stream inside the graph."""
+    count records a new one.  B=40 (320 slots) takes the MoE dispatch path
+    (the small experts run on the MFMA kernels' last blocks); float32 caches
+    take the float32 attention kernels."""
     shape = qwen3_30b_a3b(n_layers=2, maxT=400)
-    dec, _, kv = _model(shape, 64, B)
+    dec, _, kv = _model(shape, 64, B, kv_dtype)
     x = torch.from_numpy(activations(B, shape.d)).cuda()
     hid = torch.empty_like(x)
     if B == 4:

@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
-def _model(L, maxT, B, V=3000, seed=41, moe=None, group=64, qk=1):
+def _model(L, maxT, B, V=3000, seed=41, moe=None, group=64, qk=1, kv_dtype=torch.bfloat16):
     moe = moe or MoEShape(d=2048, m=768, E=128, topk=8, renorm=True)
     shape = DecoderShape(n_layers=L, moe=moe, n_heads=16, n_kv=4, maxT=maxT, V=V, qk_norm_type=qk)
     blob, offsets = torch_store(moe, L, group)
@@ -32,7 +32,7 @@ def _model(L, maxT, B, V=3000, seed=41, moe=None, group=64, qk=1):
     lm = (torch.randn((V, 2048), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
     dec = HipDecoder(store, DecoderWeights(shape, **t))
     dec.set_lm_head(lm)
-    kv = KVCacheSet(shape, B)
+    kv = KVCacheSet(shape, B, dtype=kv_dtype)
     fill_kv(kv.data)                       # rows past the prompt hold noise: never read
     torch.cuda.synchronize()
     w = {k: v.float().cpu().numpy() for k, v in dec.weights.t.items()}
@@ -40,7 +40,7 @@ def _model(L, maxT, B, V=3000, seed=41, moe=None, group=64, qk=1):
     E = moe.E
     moe_o = [O.OracleMoE(2048, moe.m, E, moe.topk, moe.renorm, group, gw[l], blob_h, offsets[:, l * E:(l + 1) * E])
              for l in range(L)]
-    oracle = D.OracleDecoder(L, 2048, 16, 4, 128, shape.eps, qk, False, w, moe_o)
+    oracle = D.OracleDecoder(L, 2048, 16, 4, 128, shape.eps, qk, False, w, moe_o, kv_bf16=kv_dtype == torch.bfloat16)
     return dec, oracle, kv, w, lm.float().cpu().numpy()
 
 
@@ -58,14 +58,16 @@ def _check_rows(kv, b, kv_seq, T, L, label):
         for j in (0, 1):
             g = kv.data[b, l, j, :T].float().cpu().numpy()
             r = kv_seq[l][j][:T]
-            lim = np.abs(r) * 2.0 ** -7 + 1e-4 * np.abs(r).max(axis=-1, keepdims=True)
+            unit = 0.0 if kv.data.dtype == torch.float32 else 2.0 ** -7     # one bf16 unit for bf16 caches
+            lim = np.abs(r) * unit + 1e-4 * np.abs(r).max(axis=-1, keepdims=True)
             bad = int((np.abs(g - r) > lim).sum())
-            assert bad == 0, f"{label}: layer {l} {'kv'[j]}: {bad} cache values off by more than a bf16 unit"
+            assert bad == 0, f"{label}: layer {l} {'kv'[j]}: {bad} cache values off by more than the bound"
 
 
-@pytest.mark.parametrize("L,T", [(2, 200), (1, 600), (1, 77)])
-def test_prefill_layers_matches_per_position_decode(L, T):
-    dec, oracle, kv, w, W_lm = _model(L, maxT=640, B=1)
+@pytest.mark.parametrize("L,T,kv_dtype", [(2, 200, torch.bfloat16), (1, 600, torch.bfloat16), (1, 77, torch.bfloat16),
+                                          (1, 300, torch.float32)])
+def test_prefill_layers_matches_per_position_decode(L, T, kv_dtype):
+    dec, oracle, kv, w, W_lm = _model(L, maxT=640, B=1, kv_dtype=kv_dtype)
     rng = np.random.default_rng(T)
     prompt = rng.integers(0, 3000, size=T).tolist()
     kv_seq = [(kv.data[0, l, 0].float().cpu().numpy(), kv.data[0, l, 1].float().cpu().numpy()) for l in range(L)]
