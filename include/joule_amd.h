@@ -83,7 +83,8 @@ int jm_abi_sizes(int* kernel_cfg_bytes, int* ndig, int* nt);
  *            offset + scales_bytes)
  *   group    Q4 group size, 64 (the reference store) or 32
  * Checks that every record lies inside the blob.  The blob stays owned by
- * the caller and must outlive the store.
+ * the caller and must outlive the store.  With cfg->E == 0 it makes a dense
+ * store instead (no experts; see jm_store_set_dense_ffn).
  */
 int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint64_t blob_bytes,
                     const uint64_t* offsets, jm_store** out);
@@ -200,7 +201,9 @@ typedef struct jm_kv_cache {
  * cos/sin [maxT][hd] (float32).
  * gate_w and the expert tables are the store's (jm_store_set_router, the
  * blob); embed and lm_head are not read by jm_decode_layers_batch; w1/w2/w3
- * and the int8 fields must be NULL and use_i8 0. */
+ * are the dense FFN's (bf16 [L][m][d], [L][m][d], [L][d][m]), set for a
+ * dense store (E = 0) and NULL for an expert store; the int8 fields must be
+ * NULL and use_i8 0. */
 typedef struct jm_kernel_w {
     const uint16_t* embed;
     const void* lm_head;
@@ -327,6 +330,18 @@ int jm_store_set_max_layers(jm_store* s, int n);
  * appended rows then keep float32 values and whose attention runs in
  * float32 arithmetic throughout. */
 int jm_store_set_kv_dtype(jm_store* s, int dtype);
+
+/* A dense model's FFN (layer_ffn_batch with E == 0, decode_kernel.c:
+ * 1393-1422): act = silu(x W1^T) * (x W2^T), out = act W3^T with bf16
+ * weights shared by the batch.  jm_store_create with cfg->E == 0 (topk 0,
+ * blob and offsets NULL) makes a dense store: d a multiple of 1024 up to
+ * 8192, intermediate a multiple of 512 up to 32768.  The decoder entry
+ * points take the FFN weights from W->w1, w2, w3 ([L][m][d], [L][m][d],
+ * [L][d][m], the reference's KernelW fields); jm_layer_ffn_batch on a
+ * dense store (with topk_idx and topk_w NULL) uses the ones registered
+ * here.  The expert-store entry points (router, stages, workspace copy,
+ * the no-allocation block) refuse a dense store. */
+int jm_store_set_dense_ffn(jm_store* s, const uint16_t* w1, const uint16_t* w2, const uint16_t* w3);
 
 /* With buf set (device int32, `bytes` long), each later
  * jm_decode_layers_batch also copies every layer's selected experts into

@@ -40,6 +40,7 @@ SIGNATURES = {
     "jm_store_trace_topk": ([_vp, _vp, _u64], _i),
     "jm_store_set_max_layers": ([_vp, _i], _i),
     "jm_store_set_kv_dtype": ([_vp, _i], _i),
+    "jm_store_set_dense_ffn": ([_vp, _vp, _vp, _vp], _i),
     "jm_store_decode_graph": ([_vp, _i], _i),
     "jm_decode_layers_batch_argmax": ([_vp] * 6 + [_i, _vp, _vp, _vp], _i),
     "jm_store_set_lm_head": ([_vp, _vp, _i, _i], _i),

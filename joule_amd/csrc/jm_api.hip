@@ -217,7 +217,7 @@ void jm::ws_layout(const jm_store* s, int B, char* base, Ws* w) {
 }
 
 int jm::store_reserve(jm_store* s, int B) {
-    if (B <= s->cap_B) return 0;
+    if (B <= s->cap_B || s->E == 0) return 0;      // a dense store has no MoE workspace
     const size_t total = ws_bytes(s, B);
     void* mem = nullptr;
     JM_HIP(hipSetDevice(s->device), "hipSetDevice");
@@ -239,13 +239,52 @@ int check_store(const jm_store* s) {
     return 0;
 }
 
+// the entry points of the expert store (router, experts, MoE workspace)
+int check_moe_store(const jm_store* s, const char* what) {
+    if (!s) return fail(JM_ERR_ARG, "store is NULL");
+    if (s->E == 0) return fail(JM_ERR_ARG, "%s: a dense store (E = 0) has no router or experts", what);
+    return 0;
+}
+
+// A dense store (E = 0, decode_kernel.c:1393-1422): no expert records; the
+// FFN weights come with the decoder's KernelW or jm_store_set_dense_ffn.
+int create_dense_store(const jm_kernel_cfg* cfg, jm_store** out) {
+    const int L = cfg->L, d = cfg->d, m = cfg->intermediate;
+    if (L <= 0) return fail(JM_ERR_SHAPE, "need 0 < L (L=%d)", L);
+    if (cfg->topk != 0) return fail(JM_ERR_SHAPE, "a dense store (E = 0) has topk 0 (got %d)", cfg->topk);
+    if (cfg->expert_i8 || cfg->expert_bf16) return fail(JM_ERR_SHAPE, "expert_i8/expert_bf16 set on a dense store");
+    if (!jm::dense_shape_ok(d, m))
+        return fail(JM_ERR_SHAPE, "dense FFN: d=%d must be a multiple of 1024 up to 8192 and intermediate=%d a "
+                    "multiple of 512 up to %d", d, m, JM_DENSE_MAX_M);
+    int dev = 0;
+    JM_HIP(hipGetDevice(&dev), "hipGetDevice");
+    jm_store* s = new jm_store();
+    memset(s, 0, sizeof *s);
+    s->L = L; s->E = 0; s->d = d; s->m = m; s->topk = 0;
+    s->dense_min = JM_DENSE_MIN_DEFAULT;
+    s->max_layers = -1;
+    s->device = dev;
+    hipError_t e = hipDeviceGetAttribute(&s->n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&s->lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (e != hipSuccess) {
+        delete s;
+        return hip_fail(e, "jm_store_create device attributes");
+    }
+    if (int rc = resolve_scratch(dev)) {
+        delete s;
+        return rc;
+    }
+    *out = s;
+    return 0;
+}
+
 // Common part of the stage entry points: checks, the workspace for B
 // tokens, and the dispatch of the caller's top-k table (the counting sort,
 // the expert work table and the union order of the dispatch path) on st.
 // The stages run the dispatch path's wave-item kernels at every B.
 int stage_setup(jm_store* s, int layer, const int32_t* top, int B, const char* who, hipStream_t st,
                 jm::RouteArgs* r, jm::ExpertArgs* a) {
-    if (!s) return fail(JM_ERR_ARG, "%s: store is NULL", who);
+    if (int rc = check_moe_store(s, who)) return rc;
     if (layer < 0 || layer >= s->L) return fail(JM_ERR_ARG, "%s: layer %d outside [0, %d)", who, layer, s->L);
     if (B < 0 || (long long)B * s->topk > JM_MAX_SLOTS)
         return fail(JM_ERR_SHAPE, "%s: need 0 <= B and B * topk <= %d", who, JM_MAX_SLOTS);
@@ -373,8 +412,10 @@ int jm_abi_sizes(int* kernel_cfg_bytes, int* ndig, int* nt) {
 
 int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint64_t blob_bytes,
                     const uint64_t* offsets, jm_store** out) {
-    if (!cfg || !blob || !offsets || !out) return fail(JM_ERR_ARG, "NULL argument to jm_store_create");
+    if (!cfg || !out) return fail(JM_ERR_ARG, "NULL argument to jm_store_create");
     *out = nullptr;
+    if (cfg->E == 0) return create_dense_store(cfg, out);
+    if (!blob || !offsets) return fail(JM_ERR_ARG, "NULL argument to jm_store_create");
     const int L = cfg->L, E = cfg->E, d = cfg->d, m = cfg->intermediate, k = cfg->topk;
     if (L <= 0 || E <= 0 || E > JM_MAX_E) return fail(JM_ERR_SHAPE, "need 0 < L and 0 < E <= %d (L=%d E=%d)", JM_MAX_E, L, E);
     if (k <= 0 || k > E || k > JM_MAX_TOPK) return fail(JM_ERR_SHAPE, "need 0 < topk <= min(E, %d) (topk=%d)", JM_MAX_TOPK, k);
@@ -476,7 +517,7 @@ int jm_store_destroy(jm_store* s) {
 }
 
 int jm_store_set_router(jm_store* s, const void* gate_w, int dtype) {
-    if (int rc = check_store(s)) return rc;
+    if (int rc = check_moe_store(s, "jm_store_set_router")) return rc;
     if (!gate_w) return fail(JM_ERR_ARG, "router weights are NULL");
     if (dtype != JM_DTYPE_F32 && dtype != JM_DTYPE_BF16) return fail(JM_ERR_ARG, "router dtype must be f32 or bf16");
     if (!aligned(gate_w, 4)) return fail(JM_ERR_ARG, "router weights must be 4-byte aligned");
@@ -533,7 +574,7 @@ int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, 
 }
 
 int jm_store_router_dtype(const jm_store* s, int* dtype) {
-    if (int rc = check_store(s)) return rc;
+    if (int rc = check_moe_store(s, "jm_store_router_dtype")) return rc;
     if (!s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
     if (dtype) *dtype = s->wt_bf16 ? JM_DTYPE_BF16 : JM_DTYPE_F32;
     return 0;
@@ -542,6 +583,16 @@ int jm_store_router_dtype(const jm_store* s, int* dtype) {
 int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out,
                        int32_t* topk_idx, float* topk_w, void* stream) {
     if (int rc = check_store(s)) return rc;
+    if (s->E == 0) {
+        // the dense FFN (decode_kernel.c:1393-1422): no routing
+        if (topk_idx || topk_w) return fail(JM_ERR_ARG, "a dense store (E = 0) has no top-k: pass NULL");
+        if (layer < 0 || layer >= s->L) return fail(JM_ERR_ARG, "layer %d outside [0, %d)", layer, s->L);
+        if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
+        if (B == 0) return 0;
+        if (!x || !out) return fail(JM_ERR_ARG, "x and out must be non-NULL");
+        if (!aligned(x, 16) || !aligned(out, 16)) return fail(JM_ERR_ARG, "x and out must be 16-byte aligned");
+        return jm::dense_block(s, layer, x, B, out, (hipStream_t)stream);
+    }
     if (!s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
     if (layer < 0 || layer >= s->L) return fail(JM_ERR_ARG, "layer %d outside [0, %d)", layer, s->L);
     if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
@@ -558,7 +609,7 @@ int jm_layer_ffn_batch(jm_store* s, int layer, const float* x, int B, float* out
 
 int jm_layer_ffn_batch_noalloc(jm_store* s, int layer, const float* x, int B, float* out,
                                int32_t* topk_idx, float* topk_w, void* stream) {
-    if (int rc = check_store(s)) return rc;
+    if (int rc = check_moe_store(s, "jm_layer_ffn_batch_noalloc")) return rc;
     if (!s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
     if (layer < 0 || layer >= s->L) return fail(JM_ERR_ARG, "layer %d outside [0, %d)", layer, s->L);
     if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
@@ -610,7 +661,7 @@ int jm_store_stage_ms(jm_store* s, float* ms, int n) {
 }
 
 int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t bytes, void* stream) {
-    if (int rc = check_store(s)) return rc;
+    if (int rc = check_moe_store(s, "jm_store_copy_workspace")) return rc;
     if (!dst) return fail(JM_ERR_ARG, "destination is NULL");
     const size_t nslot = (size_t)s->last_B * s->topk;
     const void* src = nullptr;

@@ -303,7 +303,7 @@ hipError_t launch_gemm_bf16(const GemvArgs& a, hipStream_t st) {
 
 bool gemv_shape_ok(int K) { return K > 0 && K % 1024 == 0 && K <= 8192; }
 
-int gemv_slice_cols(int K) { return K >= 4096 ? 1024 : 512; }
+int gemv_slice_cols(int K) { return K >= 4096 && K % 1024 == 0 ? 1024 : 512; }
 
 hipError_t launch_gemv_part(const GemvArgs& a, hipStream_t st) {
     if (a.B == 0 || a.N == 0) return hipSuccess;

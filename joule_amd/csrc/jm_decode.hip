@@ -12,6 +12,8 @@
 //   opart    = Wo . att, per column slice                      k_gemv_part
 //   h2 = h + sum(opart); h = h2 + MoE(RMSNorm2(h2))   the sum and the norm
 //              inside the router, the add inside the down/combine kernel
+//              (a dense store, E = 0: the slices summed by k_sum_slices and
+//              the dense FFN of jm_dense.hip)
 //
 // then hidden = RMSNorm_final(h).
 #include <hip/hip_runtime.h>
@@ -60,7 +62,12 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     nqkv = std::max(nqkv, s->dec_nqkv);
     hq = std::max(hq, s->dec_hq);
     V = std::max(V, s->dec_V);
-    const int d = s->d;
+    const int d = s->d, m = s->m;
+    const bool dense = s->E == 0;
+    // the dense FFN's slices: the projections' slice count at up to 32
+    // tokens, one slice from there (the GEMM)
+    const size_t gu_rows = dense ? (size_t)std::max(jm::dense_gu_slices(d, 1) * std::min(B, JM_GEMM_MIN_B - 1), B) : 0;
+    const size_t dn_rows = dense ? (size_t)std::max(jm::dense_dn_slices(m, 1) * std::min(B, JM_GEMM_MIN_B - 1), B) : 0;
     const size_t sz[] = {
         (size_t)B * d * 4,                        // h
         (size_t)B * d * 4,                        // h2
@@ -75,6 +82,9 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
         (size_t)jm::lm_blocks(V) * B * 4,         // lmi
         (size_t)(d / 512) * B * 4,                // rss: sums of squares of h per qkv slice
         (size_t)B * 2 * 4,                        // qkss: sums of squares of q and k (whole-vector QK-norm)
+        gu_rows * 2 * m * 4,                      // dgu: dense FFN gate/up slices
+        dense ? (size_t)B * m * 4 : 0,            // dact
+        dn_rows * d * 4,                          // ddn: dense FFN down slices
         s->tab_cap,                               // KV pointers + positions
     };
     size_t total = 0;
@@ -86,7 +96,8 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     char* p = (char*)s->dws;
     void** slots[] = {(void**)&s->h, (void**)&s->h2, (void**)&s->qkv, (void**)&s->opart, (void**)&s->part_o,
                       (void**)&s->part_ml, (void**)&s->att, (void**)&s->hid, (void**)&s->xemb, (void**)&s->lmv,
-                      (void**)&s->lmi, (void**)&s->rss, (void**)&s->qkss, (void**)&s->tab};
+                      (void**)&s->lmi, (void**)&s->rss, (void**)&s->qkss, (void**)&s->dgu, (void**)&s->dact,
+                      (void**)&s->ddn, (void**)&s->tab};
     for (size_t i = 0; i < sizeof sz / sizeof sz[0]; i++) {
         *slots[i] = p;
         p += align256(sz[i]);
@@ -122,7 +133,14 @@ int check_decode_args(const jm_store* s, const jm_kernel_cfg* c, const jm_kernel
     if (c->bias_qkv && (!W->bq || !W->bk || !W->bv)) return fail(JM_ERR_ARG, "bias_qkv needs bq, bk and bv");
     if (W->use_i8 || W->wq_i8 || W->wk_i8 || W->wv_i8 || W->wo_i8 || W->lm_i8)
         return fail(JM_ERR_ARG, "the int8 attention weights are not supported (use_i8 = 0, *_i8 = NULL)");
-    if (W->w1 || W->w2 || W->w3) return fail(JM_ERR_ARG, "dense FFN layers (w1/w2/w3) are not supported: the FFN is the store's MoE");
+    if (s->E == 0) {
+        // a dense model (decode_kernel.c:1393-1422): the FFN weights come with W
+        if (!W->w1 || !W->w2 || !W->w3) return fail(JM_ERR_ARG, "a dense store (E = 0) needs W->w1, w2 and w3");
+        if (!aligned(W->w1, 16) || !aligned(W->w2, 16) || !aligned(W->w3, 16))
+            return fail(JM_ERR_ARG, "w1, w2 and w3 must be 16-byte aligned");
+    } else if (W->w1 || W->w2 || W->w3) {
+        return fail(JM_ERR_ARG, "w1/w2/w3 are the dense FFN's: a MoE store (E > 0) takes its FFN from the store");
+    }
     const void* al[] = {W->final_norm, W->norm1, W->norm2, W->wq, W->wk, W->wv, W->wo, W->cos, W->sin,
                         c->qk_norm_type != 0 ? (const void*)W->qn : nullptr,
                         c->qk_norm_type != 0 ? (const void*)W->kn : nullptr,
@@ -207,8 +225,23 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         JM_DMARK(2 * l + 2);
         // h2 = h + attention (summed from the o_proj slices in the router),
         // then h = h2 + MoE(RMSNorm(h2))
+        const int nop = go ? 1 : H * HD / jm::gemv_slice_cols(H * HD);
+        if (s->E == 0) {
+            // dense FFN (decode_kernel.c:1393-1422): h2 = h + the o_proj
+            // slices, then h = h2 + FFN(RMSNorm(h2))
+            JM_HIP(jm::launch_sum_slices(s->h, s->opart, nop, B, d, s->h2, st), "residual launch");
+            jm::DenseFfn f{};
+            const size_t md = (size_t)s->m * d;
+            f.w1 = W->w1 + l * md; f.w2 = W->w2 + l * md; f.w3 = W->w3 + l * md;
+            f.d = d; f.m = s->m; f.B = B;
+            f.x = s->h2; f.norm_w = W->norm2 + (size_t)l * d; f.eps = c->eps; f.rss = s->rss;
+            f.gu = s->dgu; f.act = s->dact; f.dn = s->ddn;
+            f.resid = s->h2; f.out = s->h;
+            JM_HIP(jm::launch_dense_ffn(f, st), "dense FFN launch");
+            continue;
+        }
         jm::FfnIo io;
-        io.xpart = s->opart; io.nxpart = go ? 1 : H * HD / jm::gemv_slice_cols(H * HD); io.xmid = s->h2;
+        io.xpart = s->opart; io.nxpart = nop; io.xmid = s->h2;
         io.norm_w = W->norm2 + (size_t)l * d; io.eps = c->eps;
         io.resid = s->h2;
         if (int rc = jm::ffn_enqueue(s, l, s->h, B, s->h, io, false, st)) return rc;
@@ -234,6 +267,22 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
 }  // namespace
 
 namespace jm {
+
+// jm_layer_ffn_batch on a dense store: out = the dense FFN of layer on x,
+// with the weights jm_store_set_dense_ffn registered, in the decode
+// workspace's buffers.
+int dense_block(jm_store* s, int layer, const float* x, int B, float* out, hipStream_t st) {
+    if (!s->dw[0]) return fail(JM_ERR_ARG, "dense FFN weights not set (jm_store_set_dense_ffn)");
+    if (int rc = decode_reserve(s, B, 0, 0, 0, 0)) return rc;
+    JM_HIP(hipSetDevice(s->device), "hipSetDevice");
+    DenseFfn f{};
+    const size_t md = (size_t)s->m * s->d;
+    f.w1 = s->dw[0] + layer * md; f.w2 = s->dw[1] + layer * md; f.w3 = s->dw[2] + layer * md;
+    f.d = s->d; f.m = s->m; f.B = B;
+    f.x = x; f.gu = s->dgu; f.act = s->dact; f.dn = s->ddn; f.out = out;
+    JM_HIP(launch_dense_ffn(f, st), "dense FFN launch");
+    return 0;
+}
 
 void decode_free_all(jm_store* s) {
     if (s->gexec) (void)hipGraphExecDestroy(s->gexec);
@@ -283,7 +332,7 @@ int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const
                 const int32_t* positions, const float* xin, int B, float* logits, int32_t* out_tok,
                 float* hidden, void* stream, bool allow_graph = true) {
     if (!s || !c) return fail(JM_ERR_ARG, "store and cfg must be non-NULL");
-    if (!s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
+    if (s->E > 0 && !s->wt) return fail(JM_ERR_ARG, "router weights not set (jm_store_set_router)");
     int qpk = 0;
     if (int rc = check_decode_args(s, c, W, &qpk)) return rc;
     if (B < 0) return fail(JM_ERR_ARG, "B must be >= 0");
@@ -525,6 +574,16 @@ int jm_embed_lookup(const jm_kernel_w* W, const jm_kernel_cfg* c, const int32_t*
 int jm_store_decode_graph(jm_store* s, int enable) {
     if (!s) return fail(JM_ERR_ARG, "store is NULL");
     s->dgraph = enable ? 1 : 0;      // a recorded step is kept for later replays
+    return 0;
+}
+
+int jm_store_set_dense_ffn(jm_store* s, const uint16_t* w1, const uint16_t* w2, const uint16_t* w3) {
+    if (!s) return fail(JM_ERR_ARG, "store is NULL");
+    if (s->E != 0) return fail(JM_ERR_ARG, "dense FFN weights are for a dense store (E = 0)");
+    if (!w1 || !w2 || !w3) return fail(JM_ERR_ARG, "w1, w2 and w3 must be non-NULL");
+    if (!aligned(w1, 16) || !aligned(w2, 16) || !aligned(w3, 16))
+        return fail(JM_ERR_ARG, "w1, w2 and w3 must be 16-byte aligned");
+    s->dw[0] = w1; s->dw[1] = w2; s->dw[2] = w3;
     return 0;
 }
 

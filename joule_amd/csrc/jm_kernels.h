@@ -183,7 +183,9 @@ struct GemvArgs {
     float* rss;               // [slices][B] receives the sums of x[b][k]^2 over each slice's columns
                               // (the GEMM: one slice of all K), or NULL: not wanted
 };
-// K a multiple of 1024 (at most 8192); slices of 512 columns, 1024 from K = 4096
+// the decoder's projections take K a multiple of 1024 up to 8192; the
+// kernel takes any multiple of its slice width: 512 columns, 1024 from
+// K = 4096 when K is a multiple of 1024
 bool gemv_shape_ok(int K);
 int gemv_slice_cols(int K);
 hipError_t launch_gemv_part(const GemvArgs& a, hipStream_t st);
@@ -245,6 +247,35 @@ hipError_t launch_lm_head(const LmArgs& a, int* out_tok, hipStream_t st);
 hipError_t launch_embed(const uint16_t* embed, int V, int d, const int* tokens, int B, float* out,
                         hipStream_t st);
 hipError_t launch_f32_bf16_bits(const float* in, long long n, uint16_t* out, hipStream_t st);
+// The dense FFN of one layer (layer_ffn_batch with E == 0): out = resid +
+// (silu(x' W1^T) * (x' W2^T)) W3^T, x' = RMSNorm(x) with norm_w (or x).
+#ifndef JM_DENSE_MAX_M
+#define JM_DENSE_MAX_M 32768
+#endif
+struct DenseFfn {
+    const uint16_t* w1;       // [m][d] bf16 gate rows of the layer
+    const uint16_t* w2;       // [m][d] up rows
+    const uint16_t* w3;       // [d][m] down rows
+    int d, m, B;
+    const float* x;           // [B][d]
+    const uint16_t* norm_w;   // [d] RMSNorm weight applied to x first, or NULL
+    float eps;
+    float* rss;               // [d/512][B] the norm's sums of squares (with norm_w)
+    float* gu;                // [dense_gu_slices][B][2m] gate and up slices
+    float* act;               // [B][m]
+    float* dn;                // [dense_dn_slices][B][d] down slices
+    const float* resid;       // [B][d] added to the result, or NULL
+    float* out;               // [B][d]
+};
+// d as the projections take it (a multiple of 1024 up to 8192), m a
+// multiple of 512 up to JM_DENSE_MAX_M
+bool dense_shape_ok(int d, int m);
+int dense_gu_slices(int d, int B);
+int dense_dn_slices(int m, int B);
+hipError_t launch_dense_ffn(const DenseFfn& f, hipStream_t st);
+// out [B][n] = resid (or 0) + the ns slices of part [ns][B][n], in order
+hipError_t launch_sum_slices(const float* resid, const float* part, int ns, int B, int n, float* out,
+                             hipStream_t st);
 hipError_t launch_rms_rows(const float* x, const uint16_t* w, int B, int d, float eps, float* out,
                            hipStream_t st);
 

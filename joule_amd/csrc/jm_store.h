@@ -110,6 +110,10 @@ struct jm_store {
     int* lmi;                   // [lm blocks][B] its row
     float* rss;                 // [B] sums of squares of h from the projection GEMM (prefill chunks)
     float* qkss;                // [B][2] sums of squares of q and k (whole-vector QK-norm)
+    float* dgu;                 // dense FFN (E = 0): gate/up slices, act, down slices
+    float* dact;
+    float* ddn;
+    const uint16_t* dw[3];      // a dense store's FFN weights for jm_layer_ffn_batch (jm_store_set_dense_ffn)
     int kv_f32;                 // the caches the decoder reads and writes hold float32 (else bf16)
     unsigned long long* tab;    // [B*L][2] KV pointers, then [B] positions (device)
     unsigned long long* tab_host;   // pinned staging of tab
@@ -162,6 +166,7 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
 
 // Release the batch-decode workspace, staging and events.
 void decode_free_all(jm_store* s);
+int dense_block(jm_store* s, int layer, const float* x, int B, float* out, hipStream_t st);
 
 }  // namespace jm
 

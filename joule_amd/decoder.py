@@ -149,9 +149,10 @@ class DecoderWeights:
     bf16 tensors: norm1/norm2 [L, d], final_norm [d], wq [L, H*hd, d],
     wk/wv [L, KH*hd, d], wo [L, d, H*hd], qn/kn [L, hd] (per-head QK-norm)
     or [L, H*hd] / [L, KH*hd] (whole-vector QK-norm); float32 biases
-    bq [L, H*hd], bk/bv [L, KH*hd] when the shape has bias_qkv; optional
-    embed [V, d] (bf16).  The rope tables are built from the shape.  The
-    lm_head goes to the store (HipDecoder.set_lm_head).
+    bq [L, H*hd], bk/bv [L, KH*hd] when the shape has bias_qkv; for a
+    dense model (shape.moe.E == 0) the FFN's w1/w2 [L, m, d] and w3
+    [L, d, m]; optional embed [V, d] (bf16).  The rope tables are built
+    from the shape.  The lm_head goes to the store (HipDecoder.set_lm_head).
     """
 
     def __init__(self, shape: DecoderShape, device="cuda", **t: torch.Tensor):
@@ -164,6 +165,10 @@ class DecoderWeights:
         elif shape.qk_norm_type == 2:
             # whole-vector weights, as decoder3.py:244-248 sizes them
             want.update(qn=(L, H * hd), kn=(L, KH * hd))
+        if shape.moe.E == 0:
+            # a dense model's FFN (decoder3.py:251-258)
+            m = shape.moe.m
+            want.update(w1=(L, m, d), w2=(L, m, d), w3=(L, d, m))
         self.t: dict[str, torch.Tensor] = {}
         for k, shp in want.items():
             if k not in t:
@@ -214,7 +219,8 @@ class KVCacheSet:
 
 
 class HipDecoder:
-    """decode_layers_batch over an HBM expert store and dense weights."""
+    """decode_layers_batch over an HBM expert store (or, for a dense model,
+    a DenseFfnStore) and the attention weights."""
 
     def __init__(self, store: HbmExpertStore, weights: DecoderWeights, graph: bool = True):
         shape = weights.shape

@@ -148,8 +148,9 @@ def decoder_weights(shape, seed: int = 6000, device: str | torch.device = "cuda"
     tensors on ``device``: projections N(0, 0.02); RMSNorm / QK-norm weights
     1.0, or 1 + N(0, norm_jitter) when norm_jitter > 0 (tests use it so
     that a weight applied to the wrong element shows); float32 biases
-    N(0, 0.02) when the shape has bias_qkv.  One torch generator seeded with
-    ``seed`` draws them in a fixed order."""
+    N(0, 0.02) when the shape has bias_qkv; a dense model's FFN weights
+    w1/w2/w3 N(0, 0.02).  One torch generator seeded with ``seed`` draws
+    them in a fixed order."""
     L, d, H, KH, hd = shape.n_layers, shape.d, shape.n_heads, shape.n_kv, shape.hd
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
@@ -178,6 +179,11 @@ def decoder_weights(shape, seed: int = 6000, device: str | torch.device = "cuda"
     elif shape.qk_norm_type == 2:
         t["qn"] = norm_w(L, H * hd)
         t["kn"] = norm_w(L, KH * hd)
+    if shape.moe.E == 0:
+        m = shape.moe.m
+        t["w1"] = normal(L, m, d).to(torch.bfloat16)
+        t["w2"] = normal(L, m, d).to(torch.bfloat16)
+        t["w3"] = normal(L, d, m).to(torch.bfloat16)
     if shape.bias_qkv:
         t["bq"] = normal(L, H * hd)
         t["bk"] = normal(L, KH * hd)

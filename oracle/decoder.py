@@ -17,6 +17,8 @@ Follows src/jouleai/native/decode_kernel.c:
   decode_layers_batch   :1518-1556  norm1 -> attention -> residual -> norm2
                           -> MoE (OracleMoE, the C restatement of
                           layer_ffn_batch) -> residual; final norm
+  dense_ffn             :1393-1422  layer_ffn_batch's E == 0 branch (dense
+                          models): silu(x w1^T) * (x w2^T), then w3
   lm_head_B             :964-1000  logits = lm_head . x (float64 dot, rounded)
   lm_head_A             :1008-1062  argmax: per-worker strict-> scans from
                           (-1e30, row 0) over contiguous row ranges, merged
@@ -100,7 +102,8 @@ class OracleDecoder:
     final_norm [d], wq [L, H*hd, d], wk/wv [L, KH*hd, d], wo [L, d, H*hd],
     qn/kn [L, hd] (qk_norm_type 1) or [L, H*hd] / [L, KH*hd] (qk_norm_type
     2), bq/bk/bv (bias_qkv), cos/sin [maxT, hd].
-    ``moe[l]`` is an OracleMoE for layer l.  The caches are float32 arrays
+    ``moe[l]`` is an OracleMoE for layer l; with ``moe`` None the model is
+    dense and ``w`` holds w1/w2 [L, m, d] and w3 [L, d, m].  The caches are float32 arrays
     [B][L] of (k, v) [maxT, KH, hd], holding bf16 values unless kv_bf16 is
     False; they are updated in place like the reference's.
     """
@@ -162,13 +165,28 @@ class OracleDecoder:
             t = rms_norm(h, w["norm1"][l], self.eps)
             h = (h + self.layer_attn(l, t, positions, kv)).astype(F32)
             t = rms_norm(h, w["norm2"][l], self.eps)
-            out, top, _ = self.moe[l].forward(t, n_threads=n_threads)
+            if self.moe is None:                  # a dense model (E == 0)
+                out, top = dense_ffn(t, w["w1"][l], w["w2"][l], w["w3"][l]), None
+            else:
+                out, top, _ = self.moe[l].forward(t, n_threads=n_threads)
             h = (h + out).astype(F32)
             if trace is not None:
                 trace.append({"moe_in": t, "top": top, "hidden": rms_norm(h, w["final_norm"], self.eps)})
             if progress:
                 progress(l)
         return rms_norm(h, w["final_norm"], self.eps)
+
+
+def dense_ffn(x: np.ndarray, w1: np.ndarray, w2: np.ndarray, w3: np.ndarray) -> np.ndarray:
+    """layer_ffn_batch with E == 0 (decode_kernel.c:1393-1422) on rows x
+    [B, d]: g = x . w1^T and u = x . w2^T (float32 holding bf16 values;
+    float64 dots rounded once), act = (g / (1 + expf_fast(-g))) * u in
+    float32 as the reference writes it, out = act . w3^T."""
+    g = matvec(w1, x)
+    u = matvec(w2, x)
+    e = O.expf_fast_array(-g).reshape(g.shape).astype(F32)
+    act = ((g / (F32(1.0) + e)).astype(F32) * u).astype(F32)
+    return matvec(w3, act)
 
 
 def lm_head(W: np.ndarray, x: np.ndarray) -> np.ndarray:

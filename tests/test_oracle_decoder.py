@@ -101,7 +101,7 @@ def test_attention_against_softmax():
     assert np.abs(got - want).max() / np.abs(want).max() < 2e-5
 
 
-def _tiny_model(L=2, B=3, bias=False, qk=1, seed=7):
+def _tiny_model(L=2, B=3, bias=False, qk=1, seed=7, dense=False):
     """A small decoder: d 512, 4 query heads over 2 KV heads of 128, MoE with
     8 experts of 128, top-2 renormalised; weights as float32 numpy."""
     shape = MoEShape(d=512, m=128, E=8, topk=2, renorm=True, name="tiny")
@@ -119,6 +119,9 @@ def _tiny_model(L=2, B=3, bias=False, qk=1, seed=7):
     blob, offsets = numpy_store(shape, L, 32)
     moe = [O.OracleMoE(shape.d, shape.m, shape.E, shape.topk, shape.renorm, 32, router_weights(shape, l),
                        blob, offsets[:, l * shape.E:(l + 1) * shape.E]) for l in range(L)]
+    if dense:                                   # a dense FFN of 1024 instead of the MoE block
+        w.update(w1=r(L, 1024, 512), w2=r(L, 1024, 512), w3=r(L, 512, 1024))
+        moe = None
     kv = [[(D.bf16_round(rng.standard_normal((T, KH, hd)).astype(np.float32)),
             D.bf16_round(rng.standard_normal((T, KH, hd)).astype(np.float32))) for _ in range(L)]
           for _ in range(B)]
@@ -171,6 +174,10 @@ def _textbook_decode(dec, shape, blob, offsets, kv, x, positions):
                 att[b, hh * hd:(hh + 1) * hd] = (e / e.sum()) @ Vc[:p + 1, hh // g]
         h = h + att @ w["wo"][l].T
         t = norm(h, w["norm2"][l])
+        if dec.moe is None:                          # dense FFN: silu with the true exponential
+            g_, u_ = t @ w["w1"][l].T, t @ w["w2"][l].T
+            h = h + (g_ / (1.0 + np.exp(-g_)) * u_) @ w["w3"][l].T
+            continue
         gate_w = router_weights(shape, l)
 
         def experts(e, l=l):
@@ -185,9 +192,9 @@ def _textbook_decode(dec, shape, blob, offsets, kv, x, positions):
     return norm(h, w["final_norm"])
 
 
-@pytest.mark.parametrize("qk,bias", [(1, False), (2, True), (0, True)])
-def test_decoder_against_textbook(qk, bias):
-    dec, shape, blob, offsets, kv = _tiny_model(qk=qk, bias=bias)
+@pytest.mark.parametrize("qk,bias,dense", [(1, False, False), (2, True, False), (0, True, False), (1, False, True)])
+def test_decoder_against_textbook(qk, bias, dense):
+    dec, shape, blob, offsets, kv = _tiny_model(qk=qk, bias=bias, dense=dense)
     rng = np.random.default_rng(8)
     x = rng.standard_normal((3, 512)).astype(np.float32)
     positions = [0, 17, 63]
@@ -228,6 +235,25 @@ def test_gqa_head_mapping():
         assert np.all(seg > 0) and np.all(seg < kh + 1.0 + 1e-6)
         assert np.all(np.abs(seg - seg[0]) < 1e-6)
     assert o[:hd].max() < o[2 * hd:3 * hd].min()  # heads 0-1 read KV head 0, heads 2-3 KV head 1
+
+
+def test_dense_ffn_against_float64():
+    """layer_ffn_batch's E == 0 branch (decode_kernel.c:1393-1422) against
+    silu(g) * u with the true exponential in float64 (the reference's
+    expf_fast is within 1e-5 of it); zero up rows or zero gate rows give
+    exactly zero (silu(0) = 0)."""
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal((4, 512)).astype(np.float32)
+    w1, w2 = (D.bf16_round((rng.standard_normal((1536, 512)) * 0.05).astype(np.float32)) for _ in range(2))
+    w3 = D.bf16_round((rng.standard_normal((512, 1536)) * 0.05).astype(np.float32))
+    got = D.dense_ffn(x, w1, w2, w3).astype(np.float64)
+    x64 = x.astype(np.float64)
+    g, u = x64 @ w1.T.astype(np.float64), x64 @ w2.T.astype(np.float64)
+    want = (g / (1.0 + np.exp(-g)) * u) @ w3.T.astype(np.float64)
+    rel = np.abs(got - want).max(axis=1) / np.abs(want).max(axis=1)
+    assert rel.max() < 1e-4, rel
+    assert not np.any(D.dense_ffn(x, w1, np.zeros_like(w2), w3))
+    assert not np.any(D.dense_ffn(x, np.zeros_like(w1), w2, w3))
 
 
 def _appended_k(dec, kv, x, pos):
