@@ -518,6 +518,54 @@ def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 32, 33, 36, 512), reps=200):
     return {"m": m, "d": d, "group": group, "sizes": out}
 
 
+def dense_step(B, steps, warmup, n_layers=36, position=2048, maxT=2176):
+    """A dense model's decode step (layer_ffn_batch's E == 0 branch in every
+    layer): Qwen3-8B-shaped layers (hidden 4096, GQA 32 / 8 heads of 128,
+    per-head QK-norm, FFN intermediate 12288, bf16 weights N(0, 0.02)),
+    every token at cache position `position` of a bf16 cache.  Returns
+    tokens/s and the step's algorithmic bytes (weights once, KV rows)."""
+    import torch
+
+    from joule_amd.decoder import DecoderShape, DecoderWeights, HipDecoder, KVCacheSet
+    from joule_amd.dense import DenseFfnStore, dense_ffn_shape
+    from joule_amd.synth import activations, decoder_weights, fill_kv
+
+    d, m, H, KH, hd = 4096, 12288, 32, 8, 128
+    shape = DecoderShape(n_layers=n_layers, moe=dense_ffn_shape(d, m), n_heads=H, n_kv=KH, maxT=maxT,
+                         qk_norm_type=1, name="qwen3-8b-shaped")
+    log(f"dense decode: building {n_layers} Qwen3-8B-shaped layers")
+    store = DenseFfnStore(d, m, n_layers)
+    dec = HipDecoder(store, DecoderWeights(shape, **decoder_weights(shape)))
+    kv = KVCacheSet(shape, B)
+    fill_kv(kv.data)
+    x = torch.from_numpy(activations(B, d)).cuda()
+    hid = torch.empty_like(x)
+    pos = [position] * B
+    for _ in range(warmup):
+        dec.decode_layers_batch(x, pos, kv, hid)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        dec.decode_layers_batch(x, pos, kv, hid)
+    e1.record(st)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    w_bytes = n_layers * 2 * (H * hd * d + 2 * KH * hd * d + d * H * hd + 3 * m * d)
+    kv_bytes = n_layers * B * (position + 1) * KH * hd * 2 * 2
+    total = w_bytes + kv_bytes
+    ok = bool(torch.isfinite(hid).all().item())
+    res = {"tok_per_s": B / (ms * 1e-3), "ms_per_step": ms, "layers": n_layers, "batch": B, "position": position,
+           "bytes_alg": total, "GBs": total / (ms * 1e-3) / 1e9,
+           "hbm_frac": total / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "hidden_finite": ok}
+    log(f"dense decode {n_layers} layers B={B}: {res['tok_per_s']:.0f} tok/s, {ms:.3f} ms/step, "
+        f"{res['GBs']:.0f} GB/s over {total / 1e9:.2f} GB")
+    del dec, kv, store
+    torch.cuda.empty_cache()
+    return res
+
+
 def prefill_only(group, reps, n_layers=48, maxT=2176, Tp=512):
     """Only the 512-token prefill of decode_step's model (for kernel
     profiles): one warm-up pass, then `reps` timed passes of
@@ -625,6 +673,8 @@ def main() -> int:
                          "Infinity Cache, which shows how much of each kernel's time is HBM bandwidth)")
     ap.add_argument("--kv-f32", action="store_true",
                     help="with --decode-only: float32 caches (the reference's KVCache type) instead of bf16")
+    ap.add_argument("--dense-only", action="store_true",
+                    help="only a dense model's decode step (Qwen3-8B-shaped, 36 layers) at B=1 and --batch")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 48-layer 512-token prefill (--steps timed passes); prints its JSON")
     ap.add_argument("--zipf-only", action="store_true",
@@ -665,6 +715,10 @@ def main() -> int:
     if args.prefill_only:
         r = prefill_only(args.group, args.steps)
         print(json.dumps({"prefill_512": r}), flush=True)
+        return 0
+    if args.dense_only:
+        r = {f"B{b}": dense_step(b, args.steps, args.warmup) for b in (1, args.batch)}
+        print(json.dumps({"dense_decode": r}), flush=True)
         return 0
     if args.plugin_only:
         print(json.dumps({"plugin_q4_gemm": plugin_q4_gemm(args.group)}), flush=True)

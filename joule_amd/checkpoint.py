@@ -1,4 +1,4 @@
-"""A HuggingFace-layout MoE checkpoint to a GPU decoder.
+"""A HuggingFace-layout checkpoint (MoE or dense) to a GPU decoder.
 
 Mirrors the reference's native decoder construction
 (src/jouleai/native/decoder3.py:86-135 ``NativeDecoder.__init__``,
@@ -11,7 +11,9 @@ registry (src/jouleai/arch/registry.py:56-94 ``get_spec``):
 * ``load_decoder(model_dir)`` converts the experts to the Q4 store once
   (``convert_experts_q4``, same file format), puts it in HBM, and loads the
   router, norms, attention projections, embedding and lm_head by the
-  checkpoint's own tensor names into device tensors;
+  checkpoint's own tensor names into device tensors; a dense model
+  (qwen2, qwen3, llama, mistral) gets a DenseFfnStore and its
+  gate/up/down projections as the FFN weights (decoder3.py:251-280);
 * ``HipNativeDecoder`` keeps per-sequence KV caches across calls and offers
   ``decode_batch`` / ``decode_batch_argmax`` as NativeDecoder does
   (decoder3.py:580-629).
@@ -27,6 +29,7 @@ import numpy as np
 import torch
 
 from .decoder import DecoderShape, DecoderWeights, HipDecoder, KVCacheSet
+from .dense import DenseFfnStore, dense_ffn_shape
 from .moe import HbmExpertStore, MoEShape
 from .q4_store import BIN_NAME, INDEX_NAME, convert_experts_q4
 
@@ -35,14 +38,19 @@ from .q4_store import BIN_NAME, INDEX_NAME, convert_experts_q4
 # vector, the others not at all; mixtral/deepseek name experts block_sparse_moe)
 _MOE_TYPES = {"qwen3_moe": (1, "qwen"), "olmoe": (2, "qwen"), "mixtral": (0, "block_sparse_moe"),
               "deepseek": (0, "block_sparse_moe")}
+# the dense families the reference's native decoder runs through
+# layer_ffn_batch's E == 0 branch (registry.py:50, decoder3.py:251-280);
+# gemma's (1 + w) norms and phi / gpt_oss are not taken here
+_DENSE_TYPES = {"qwen2": 0, "qwen3": 1, "llama": 0, "mistral": 0}
 
 
 def decoder_shape(cfg: dict, max_tokens: int = 4096) -> tuple[DecoderShape, str]:
     """(shape, expert naming) of a config.json dict (registry.py:56-94)."""
     mt = cfg.get("model_type", "?")
-    if mt not in _MOE_TYPES:
-        raise ValueError(f"model_type '{mt}': the GPU decoder runs MoE checkpoints ({', '.join(_MOE_TYPES)})")
-    qk, naming = _MOE_TYPES[mt]
+    if mt not in _MOE_TYPES and mt not in _DENSE_TYPES:
+        raise ValueError(f"model_type '{mt}': the GPU decoder runs {', '.join(list(_MOE_TYPES) + list(_DENSE_TYPES))}")
+    dense = mt in _DENSE_TYPES
+    qk, naming = (_DENSE_TYPES[mt], "qwen") if dense else _MOE_TYPES[mt]
     if cfg.get("q_lora_rank") or cfg.get("kv_lora_rank"):
         raise ValueError("MLA attention (latent KV) is not supported")
     if cfg.get("clip_qkv") is not None:
@@ -63,14 +71,17 @@ def decoder_shape(cfg: dict, max_tokens: int = 4096) -> tuple[DecoderShape, str]
             raise ValueError(f"rope_scaling type '{rtype}' is not supported (llama3 only)")
     heads = cfg["num_attention_heads"]
     hd = cfg.get("head_dim") or cfg["hidden_size"] // heads
-    moe = MoEShape(d=cfg["hidden_size"], m=cfg.get("moe_intermediate_size") or cfg.get("intermediate_size", 0),
-                   E=cfg.get("num_experts", 0), topk=cfg.get("num_experts_per_tok", 0),
-                   renorm=bool(cfg.get("norm_topk_prob", False)), name=mt)
+    if dense:
+        moe = dense_ffn_shape(cfg["hidden_size"], cfg["intermediate_size"])
+    else:
+        moe = MoEShape(d=cfg["hidden_size"], m=cfg.get("moe_intermediate_size") or cfg.get("intermediate_size", 0),
+                       E=cfg.get("num_experts", 0), topk=cfg.get("num_experts_per_tok", 0),
+                       renorm=bool(cfg.get("norm_topk_prob", False)), name=mt)
     shape = DecoderShape(n_layers=cfg["num_hidden_layers"], moe=moe, n_heads=heads,
                          n_kv=cfg.get("num_key_value_heads", heads), hd=hd,
                          eps=cfg.get("rms_norm_eps", cfg.get("layer_norm_eps", 1e-5)),
                          theta=cfg.get("rope_theta", 1e4), maxT=max_tokens, qk_norm_type=qk,
-                         bias_qkv=bool(cfg.get("attention_bias", False)), V=cfg["vocab_size"], name=mt,
+                         bias_qkv=bool(cfg.get("attention_bias", mt == "qwen2")), V=cfg["vocab_size"], name=mt,
                          rope_scaling=rope_scaling)
     return shape, naming
 
@@ -121,17 +132,19 @@ def load_decoder(model_dir: str | Path, max_tokens: int = 4096, converted_dir: s
     cfg = json.loads((model_dir / "config.json").read_text())
     shape, naming = decoder_shape(cfg, max_tokens)
     L, moe = shape.n_layers, shape.moe
-    out = Path(converted_dir) if converted_dir is not None else model_dir / "joule_q4"
-    if not ((out / BIN_NAME).exists() and (out / INDEX_NAME).exists()):
-        convert_experts_q4(model_dir, out, L, moe.E, naming=naming, group=group)
-    store = HbmExpertStore.from_dir(out, moe, n_layers=L, device=device)
-
     T = _Tensors(model_dir)
+    lay = [f"model.layers.{l}" for l in range(L)]
+    if moe.E == 0:
+        store = DenseFfnStore(moe.d, moe.m, L, device=device)
+    else:
+        out = Path(converted_dir) if converted_dir is not None else model_dir / "joule_q4"
+        if not ((out / BIN_NAME).exists() and (out / INDEX_NAME).exists()):
+            convert_experts_q4(model_dir, out, L, moe.E, naming=naming, group=group)
+        store = HbmExpertStore.from_dir(out, moe, n_layers=L, device=device)
+        store.set_router(T.stack([f"{p}.{_router_name(naming)}.weight" for p in lay]).to(device).contiguous())
     # a qwen2-style bias flag without bias tensors runs unbiased (decoder3.py:107-114)
     if shape.bias_qkv and "model.layers.0.self_attn.q_proj.bias" not in T:
         shape = dataclasses.replace(shape, bias_qkv=False)
-    lay = [f"model.layers.{l}" for l in range(L)]
-    store.set_router(T.stack([f"{p}.{_router_name(naming)}.weight" for p in lay]).to(device).contiguous())
     t = {
         "norm1": T.stack([f"{p}.input_layernorm.weight" for p in lay]),
         "norm2": T.stack([f"{p}.post_attention_layernorm.weight" for p in lay]),
@@ -149,7 +162,13 @@ def load_decoder(model_dir: str | Path, max_tokens: int = 4096, converted_dir: s
     if shape.bias_qkv:
         for k, n in (("bq", "q_proj"), ("bk", "k_proj"), ("bv", "v_proj")):
             t[k] = T.stack([f"{p}.self_attn.{n}.bias" for p in lay], torch.float32)
+    if moe.E == 0:
+        # dense FFN: gate_proj / up_proj / down_proj (decoder3.py:276-280)
+        for k, n in (("w1", "gate_proj"), ("w2", "up_proj"), ("w3", "down_proj")):
+            t[k] = T.stack([f"{p}.mlp.{n}.weight" for p in lay])
     dec = HipDecoder(store, DecoderWeights(shape, device=device, **t))
+    if moe.E == 0:
+        store.set_weights(*(dec.weights.t[k] for k in ("w1", "w2", "w3")))
     tied = bool(cfg.get("tie_word_embeddings", False))
     lm = t["embed"] if tied else T.get("lm_head.weight").to(torch.bfloat16)
     dec.set_lm_head(lm.to(device).contiguous())

@@ -36,8 +36,16 @@ def test_registry_defaults_and_families():
     mix = dict(olmoe, model_type="mixtral", num_key_value_heads=8)
     s, naming = decoder_shape(mix)
     assert naming == "block_sparse_moe" and s.qk_norm_type == 0 and s.n_kv == 8
+    # dense families: no experts, the FFN of intermediate_size; qwen2's
+    # attention bias by default, qwen3's per-head QK-norm
+    s, _ = decoder_shape(dict(olmoe, model_type="qwen3"))
+    assert (s.moe.E, s.moe.topk, s.moe.m, s.qk_norm_type, s.bias_qkv) == (0, 0, 1024, 1, False)
+    s, _ = decoder_shape(dict(olmoe, model_type="qwen2"))
+    assert (s.moe.E, s.qk_norm_type, s.bias_qkv) == (0, 0, True)
+    s, _ = decoder_shape(dict(olmoe, model_type="llama", attention_bias=False))
+    assert (s.moe.E, s.qk_norm_type, s.bias_qkv) == (0, 0, False)
     with pytest.raises(ValueError):
-        decoder_shape(dict(olmoe, model_type="qwen3"))          # dense: not the MoE path
+        decoder_shape(dict(olmoe, model_type="gemma"))          # (1 + w) norms: not taken
     with pytest.raises(ValueError):
         decoder_shape(dict(olmoe, model_type="deepseek", kv_lora_rank=512))   # MLA attention
 
