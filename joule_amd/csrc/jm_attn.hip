@@ -64,15 +64,16 @@ k_gemv_part(GemvArgs a) {
     const uint16_t* wp = wr + k0 + 8 * g;
     // requests first: the tokens' slice (needed first; thread tid serves
     // token tb0 + tid % 8 throughout), then the weight rows
-    constexpr int XI = NK * 32 / (WV * 64);        // staging items per thread
-    static_assert(NK * 32 % (WV * 64) == 0 && (WV * 64) % 8 == 0, "whole staging items, token fixed");
+    constexpr int NI = NK * 32;                    // staging items (8 columns of one token)
+    constexpr int XI = (NI + WV * 64 - 1) / (WV * 64);     // per thread, the last one partial
+    static_assert((WV * 64) % 8 == 0, "token fixed per thread");
     const int tx = tid & 7;
     const bool tin = tb0 + tx < a.B;
     float4 xv[XI][2];
     uint4 nwv[XI];
 #pragma unroll
     for (int it = 0; it < XI; it++) {
-        const int i = tid + it * WV * 64;
+        const int i = (tid + it * WV * 64) % NI;   // items past NI repeat one (same token), not stored
         const int c = k0 + 32 * (i >> 5) + 8 * ((i >> 3) & 3);
         const float4* xp = (const float4*)(a.x + (size_t)(tin ? tb0 + tx : tb0) * a.K + c);
         xv[it][0] = xp[0];
@@ -92,6 +93,7 @@ k_gemv_part(GemvArgs a) {
 #pragma unroll
     for (int it = 0; it < XI; it++) {
         const int i = tid + it * WV * 64;
+        if (NI % (WV * 64) != 0 && i >= NI) break;         // the partial last item of the thread
         const int ks = i >> 5, gg = (i >> 3) & 3;
         float v[8] = {xv[it][0].x, xv[it][0].y, xv[it][0].z, xv[it][0].w,
                       xv[it][1].x, xv[it][1].y, xv[it][1].z, xv[it][1].w};
@@ -305,14 +307,49 @@ bool gemv_shape_ok(int K) { return K > 0 && K % 1024 == 0 && K <= 8192; }
 
 int gemv_slice_cols(int K) { return K >= 4096 && K % 1024 == 0 ? 1024 : 512; }
 
+// Waves per block (16 rows each) of a projection: the one of 5, 4 and 2
+// whose grid fills its last round of the CUs best (one block per CU and
+// round), the larger on ties.  A grid of 1.25 rounds (320 blocks on 256
+// CUs) leaves the CUs with two blocks to set the time.
+static int gemv_waves(int N, int slices, int zgroups) {
+    static int ncu = 0;
+    if (ncu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+            ncu = 256;
+    }
+    int best = 4;
+    double best_eff = -1.0;
+    for (int wv : {5, 4, 2}) {
+        const long long nb = (long long)((N + 16 * wv - 1) / (16 * wv)) * slices * zgroups;
+        const long long rounds = (nb + ncu - 1) / ncu;
+        const double eff = (double)nb / (double)(rounds * ncu);
+        if (eff > best_eff + 1e-9) {
+            best_eff = eff;
+            best = wv;
+        }
+    }
+    return best;
+}
+
 hipError_t launch_gemv_part(const GemvArgs& a, hipStream_t st) {
     if (a.B == 0 || a.N == 0) return hipSuccess;
     if (a.rows[0] % 16 || a.rows[1] % 16 || a.rows[2] % 16) return hipErrorInvalidValue;
-    constexpr int WV = 4;
     const int sw = gemv_slice_cols(a.K);
-    const dim3 grid((unsigned)((a.N + 16 * WV - 1) / (16 * WV)), (unsigned)(a.K / sw), (unsigned)((a.B + 7) / 8));
-    if (sw == 1024) hipLaunchKernelGGL((k_gemv_part<1024, WV>), grid, dim3(WV * 64), 0, st, a);
-    else hipLaunchKernelGGL((k_gemv_part<512, WV>), grid, dim3(WV * 64), 0, st, a);
+    const int zg = (a.B + 7) / 8;
+    const int wv = gemv_waves(a.N, a.K / sw, zg);
+    const dim3 grid((unsigned)((a.N + 16 * wv - 1) / (16 * wv)), (unsigned)(a.K / sw), (unsigned)zg);
+#define JM_GV(SWV, WVV) hipLaunchKernelGGL((k_gemv_part<SWV, WVV>), grid, dim3(WVV * 64), 0, st, a)
+    if (sw == 1024) {
+        if (wv == 5) JM_GV(1024, 5);
+        else if (wv == 2) JM_GV(1024, 2);
+        else JM_GV(1024, 4);
+    } else {
+        if (wv == 5) JM_GV(512, 5);
+        else if (wv == 2) JM_GV(512, 2);
+        else JM_GV(512, 4);
+    }
+#undef JM_GV
     return hipGetLastError();
 }
 
