@@ -586,7 +586,7 @@ def prefill_only(group, reps, n_layers=48, maxT=2176, Tp=512):
     dec.weights.t["embed"] = (torch.randn((shape.V, shape.d), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
     dec._w = dec.weights.kernel_w()
     prompt = torch.randint(0, shape.V, (Tp,), generator=g, device="cuda", dtype=torch.int32)
-    kvp = KVCacheSet(shape, 1, dtype=kv_dtype)
+    kvp = KVCacheSet(shape, 1)
     plog = torch.empty(shape.V, dtype=torch.float32, device="cuda")
     dec.prefill_layers(prompt, kvp, 0, plog)
     torch.cuda.synchronize()

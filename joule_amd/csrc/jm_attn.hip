@@ -190,7 +190,10 @@ k_gemm_bf16(GemvArgs a) {
     const bool want_ss = a.rss && blockIdx.x == 0;
     float ss = 0.0f;
     const int row0 = blockIdx.x * GM_R, tb0 = blockIdx.y * GM_T;
-    const int K = a.K, nstage = K / GM_KS;
+    // block z takes the z-th of gridDim.z equal column ranges and writes
+    // slice z of part (and of rss)
+    const int K = a.K, nstage = K / GM_KS / (int)gridDim.z, kz = blockIdx.z;
+    const int kcol0 = kz * nstage * GM_KS;
     // the 128-row tile lies in one matrix (row counts are multiples of 128)
     const uint16_t* wm;
     int wr0;
@@ -202,8 +205,8 @@ k_gemm_bf16(GemvArgs a) {
     const int xt = tid >> 3, xp = tid & 7;
     const int wrw = tid >> 3, wp = tid & 7;
     const bool xlive = tb0 + xt < a.B;
-    const float* xrow = a.x + (size_t)(xlive ? tb0 + xt : 0) * K + 8 * xp;
-    const uint16_t* wp0 = wm + (size_t)(wr0 + wrw) * K + 8 * wp;
+    const float* xrow = a.x + (size_t)(xlive ? tb0 + xt : 0) * K + kcol0 + 8 * xp;
+    const uint16_t* wp0 = wm + (size_t)(wr0 + wrw) * K + kcol0 + 8 * wp;
     const uint16_t* wp1 = wp0 + (size_t)64 * K;
 
     // every load is unconditional (past the last stage: the last stage again)
@@ -213,7 +216,7 @@ k_gemm_bf16(GemvArgs a) {
         const float4* xs = (const float4*)(xrow + s * GM_KS);
         r.x0 = xs[0];
         r.x1 = xs[1];
-        if (a.norm_w) r.nw = *(const uint4*)(a.norm_w + s * GM_KS + 8 * xp);
+        if (a.norm_w) r.nw = *(const uint4*)(a.norm_w + kcol0 + s * GM_KS + 8 * xp);
         r.w[0] = *(const uint4*)(wp0 + s * GM_KS);
         r.w[1] = *(const uint4*)(wp1 + s * GM_KS);
     };
@@ -277,7 +280,7 @@ k_gemm_bf16(GemvArgs a) {
 #pragma unroll
     for (int v = 0; v < 16; v++) {
         const int t = tb0 + th * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-        if (t < a.B) a.part[(size_t)t * a.N + n] = acc[v];
+        if (t < a.B) a.part[((size_t)kz * a.B + t) * a.N + n] = acc[v];
     }
     if (want_ss) {
         ss_l[xt][xp] = ss;
@@ -286,7 +289,7 @@ k_gemm_bf16(GemvArgs a) {
             float t = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; i++) t = __fadd_rn(t, ss_l[tid][i]);
-            a.rss[tb0 + tid] = t;
+            a.rss[(size_t)kz * a.B + tb0 + tid] = t;
         }
     }
 }
@@ -295,10 +298,44 @@ bool gemm_shape_ok(const GemvArgs& a) {
     return a.K % (2 * GM_KS) == 0 && a.rows[0] % GM_R == 0 && a.rows[1] % GM_R == 0 && a.rows[2] % GM_R == 0;
 }
 
+static int device_cus() {
+    static int ncu = 0;
+    if (ncu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+            ncu = 256;
+    }
+    return ncu;
+}
+
+// Column ranges (K slices) of the GEMM, 1, 2 or 4: one block per CU runs at
+// a time, so a grid of (N / 128) x (B / 64) tiles that leaves CUs idle in
+// its last round is split along K into more, shorter blocks.  Time is
+// modelled as rounds x (1 / slices + 0.15), the constant a block's fixed
+// part (prologue, output stores); ties keep fewer slices (fewer partial
+// outputs to write and sum).
+int gemm_slices(const GemvArgs& a) {
+    const int ncu = device_cus();
+    const long long tiles = (long long)(a.N / GM_R) * ((a.B + GM_T - 1) / GM_T);
+    const int nstage = a.K / GM_KS;
+    int best = 1;
+    double best_t = 1e30;
+    for (int kz : {1, 2, 4}) {
+        if (nstage % (2 * kz) != 0) continue;
+        const long long rounds = (tiles * kz + ncu - 1) / ncu;
+        const double t = (double)rounds * (1.0 / kz + 0.15);
+        if (t < best_t - 1e-9) {
+            best_t = t;
+            best = kz;
+        }
+    }
+    return best;
+}
+
 hipError_t launch_gemm_bf16(const GemvArgs& a, hipStream_t st) {
     if (a.B == 0 || a.N == 0) return hipSuccess;
     if (!gemm_shape_ok(a)) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(a.N / GM_R), (unsigned)((a.B + GM_T - 1) / GM_T));
+    const dim3 grid((unsigned)(a.N / GM_R), (unsigned)((a.B + GM_T - 1) / GM_T), (unsigned)gemm_slices(a));
     hipLaunchKernelGGL(k_gemm_bf16, grid, dim3(512), 0, st, a);
     return hipGetLastError();
 }
@@ -312,12 +349,7 @@ int gemv_slice_cols(int K) { return K >= 4096 && K % 1024 == 0 ? 1024 : 512; }
 // round), the larger on ties.  A grid of 1.25 rounds (320 blocks on 256
 // CUs) leaves the CUs with two blocks to set the time.
 static int gemv_waves(int N, int slices, int zgroups) {
-    static int ncu = 0;
-    if (ncu == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
-            ncu = 256;
-    }
+    const int ncu = device_cus();
     int best = 4;
     double best_eff = -1.0;
     for (int wv : {5, 4, 2}) {

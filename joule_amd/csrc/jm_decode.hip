@@ -64,15 +64,19 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     V = std::max(V, s->dec_V);
     const int d = s->d, m = s->m;
     const bool dense = s->E == 0;
-    // the dense FFN's slices: the projections' slice count at up to 32
-    // tokens, one slice from there (the GEMM)
-    const size_t gu_rows = dense ? (size_t)std::max(jm::dense_gu_slices(d, 1) * std::min(B, JM_GEMM_MIN_B - 1), B) : 0;
-    const size_t dn_rows = dense ? (size_t)std::max(jm::dense_dn_slices(m, 1) * std::min(B, JM_GEMM_MIN_B - 1), B) : 0;
+    // slices of a projection's output: the GEMV's K / 512 at most up to 32
+    // tokens, the GEMM's K slices (at most 4) from there
+    const int gmax = B >= JM_GEMM_MIN_B ? 4 : 0;
+    const size_t qkv_sl = (size_t)std::max(d / 512, gmax), op_sl = (size_t)std::max(hq / 512, gmax);
+    const size_t gu_rows = dense ? (size_t)std::max(jm::dense_gu_slices(d, 1) * std::min(B, JM_GEMM_MIN_B - 1),
+                                                    gmax * B) : 0;
+    const size_t dn_rows = dense ? (size_t)std::max(jm::dense_dn_slices(m, 1) * std::min(B, JM_GEMM_MIN_B - 1),
+                                                    gmax * B) : 0;
     const size_t sz[] = {
         (size_t)B * d * 4,                        // h
         (size_t)B * d * 4,                        // h2
-        (size_t)(d / 512) * B * nqkv * 4,         // qkv slices (at most d / 512 of them)
-        (size_t)(hq / 512) * B * d * 4,           // o_proj slices
+        qkv_sl * B * nqkv * 4,                    // qkv slices
+        op_sl * B * d * 4,                        // o_proj slices
         (size_t)B * S * hq * 4,                   // part_o: H heads x hd per split
         (size_t)B * S * (hq / HD) * 2 * 4,        // part_ml
         (size_t)B * hq * 4,                       // att
@@ -80,7 +84,7 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
         (size_t)B * d * 4,                        // xemb: embedded prompt tokens (prefill)
         (size_t)jm::lm_blocks(V) * B * 4,         // lmv
         (size_t)jm::lm_blocks(V) * B * 4,         // lmi
-        (size_t)(d / 512) * B * 4,                // rss: sums of squares of h per qkv slice
+        qkv_sl * B * 4,                           // rss: sums of squares of h per qkv slice
         (size_t)B * 2 * 4,                        // qkss: sums of squares of q and k (whole-vector QK-norm)
         gu_rows * 2 * m * 4,                      // dgu: dense FFN gate/up slices
         dense ? (size_t)B * m * 4 : 0,            // dact
@@ -187,7 +191,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         else JM_HIP(jm::launch_gemv_part(g, st), "qkv launch");
 
         jm::AttnArgs at{};
-        at.qkv = s->qkv; at.nslice = gq ? 1 : d / jm::gemv_slice_cols(d); at.d = d;
+        at.qkv = s->qkv; at.nslice = gq ? jm::gemm_slices(g) : d / jm::gemv_slice_cols(d); at.d = d;
         at.rss = g.rss;
         if (c->bias_qkv) {
             at.bq = W->bq + (size_t)l * H * HD;
@@ -225,7 +229,7 @@ int enqueue_step(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, cons
         JM_DMARK(2 * l + 2);
         // h2 = h + attention (summed from the o_proj slices in the router),
         // then h = h2 + MoE(RMSNorm(h2))
-        const int nop = go ? 1 : H * HD / jm::gemv_slice_cols(H * HD);
+        const int nop = go ? jm::gemm_slices(o) : H * HD / jm::gemv_slice_cols(H * HD);
         if (s->E == 0) {
             // dense FFN (decode_kernel.c:1393-1422): h2 = h + the o_proj
             // slices, then h = h2 + FFN(RMSNorm(h2))

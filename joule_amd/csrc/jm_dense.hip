@@ -76,9 +76,11 @@ k_swiglu_slices(const float* __restrict__ gu, int ns, const float* __restrict__ 
 
 bool dense_shape_ok(int d, int m) { return gemv_shape_ok(d) && m >= 512 && m % 512 == 0 && m <= JM_DENSE_MAX_M; }
 
-int dense_gu_slices(int d, int B) { return B >= JM_GEMM_MIN_B ? 1 : d / gemv_slice_cols(d); }
+// the most slices the gate/up and down outputs hold at B tokens (the
+// GEMM's K slices from JM_GEMM_MIN_B tokens, at most 4)
+int dense_gu_slices(int d, int B) { return B >= JM_GEMM_MIN_B ? 4 : d / gemv_slice_cols(d); }
 
-int dense_dn_slices(int m, int B) { return B >= JM_GEMM_MIN_B ? 1 : m / gemv_slice_cols(m); }
+int dense_dn_slices(int m, int B) { return B >= JM_GEMM_MIN_B ? 4 : m / gemv_slice_cols(m); }
 
 hipError_t launch_dense_ffn(const DenseFfn& f, hipStream_t st) {
     if (f.B == 0) return hipSuccess;
@@ -94,7 +96,7 @@ hipError_t launch_dense_ffn(const DenseFfn& f, hipStream_t st) {
     const bool gq = f.B >= JM_GEMM_MIN_B && gemm_shape_ok(g);
     hipError_t e = gq ? launch_gemm_bf16(g, st) : launch_gemv_part(g, st);
     if (e != hipSuccess) return e;
-    const int ng = gq ? 1 : f.d / gemv_slice_cols(f.d);
+    const int ng = gq ? gemm_slices(g) : f.d / gemv_slice_cols(f.d);
     const dim3 ga((unsigned)((f.m / 4 + 255) / 256), (unsigned)f.B);
     hipLaunchKernelGGL(k_swiglu_slices, ga, dim3(256), 0, st, f.gu, ng, g.rss, ng, f.d, f.eps, f.B, f.m, f.act);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -107,7 +109,7 @@ hipError_t launch_dense_ffn(const DenseFfn& f, hipStream_t st) {
     const bool go = f.B >= JM_GEMM_MIN_B && gemm_shape_ok(o);
     e = go ? launch_gemm_bf16(o, st) : launch_gemv_part(o, st);
     if (e != hipSuccess) return e;
-    const int nd = go ? 1 : f.m / gemv_slice_cols(f.m);
+    const int nd = go ? gemm_slices(o) : f.m / gemv_slice_cols(f.m);
     const dim3 gs((unsigned)((f.d / 4 + 255) / 256), (unsigned)f.B);
     hipLaunchKernelGGL(k_sum_slices, gs, dim3(256), 0, st, f.resid, f.dn, nd, f.B, f.d, f.out);
     return hipGetLastError();

@@ -192,6 +192,8 @@ hipError_t launch_gemv_part(const GemvArgs& a, hipStream_t st);
 // many tokens (a prefill chunk): the whole sum into part[0] (one slice);
 // every row count a multiple of 128, K a multiple of 128
 bool gemm_shape_ok(const GemvArgs& a);
+// the K slices the GEMM writes for a (1, 2 or 4; the consumer sums them)
+int gemm_slices(const GemvArgs& a);
 hipError_t launch_gemm_bf16(const GemvArgs& a, hipStream_t st);
 // from this many tokens the projections take the GEMM
 #define JM_GEMM_MIN_B 33
