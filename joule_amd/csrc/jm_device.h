@@ -765,6 +765,15 @@ __host__ __device__ constexpr int dispatch_lds_ints(int nslot, int E) {
 // the record offsets of expert tid (tid < E).  A slot's rank among the
 // earlier slots of its chunk with the same expert comes from ballots over
 // the bits of the expert id (lanes with equal ids agree on every bit).
+// STABLE false (the block's own dispatch): the slots of a segment in no
+// particular order.  A slot's place in its segment comes from an LDS atomic
+// add on its expert's count and each expert's first slot from an atomic
+// min, so the chunk counts, ballots and chunk scans drop out.  Nothing the
+// block computes depends on that order: a slot's products, act, y and its
+// place in the union order (from the first slots) are the same wherever
+// it sits in its segment; the work table and tile lists come from the
+// counts alone.
+template <bool STABLE = true>
 __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E, int k, int* lds,
                                                int* __restrict__ seg_off, int* __restrict__ seg_slot,
                                                int* __restrict__ active, int* __restrict__ n_active,
@@ -772,20 +781,29 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
                                                ExpertWork* __restrict__ work = nullptr,
                                                int umax = 0, const ExpertRec* rec = nullptr) {
     constexpr unsigned short NONE = 0xFFFF;
-    const int nchunk = (nslot + DISP_CHUNK - 1) / DISP_CHUNK;
-    int* cnt = lds;                              // [E][nchunk]
+    const int nchunk = STABLE ? (nslot + DISP_CHUNK - 1) / DISP_CHUNK : 1;
+    int* cnt = lds;                              // [E][nchunk] (STABLE) or [E]
     int* off = cnt + nchunk * E;                 // [E + 1]
     int* fs = off + E + 1;                       // [E]
     unsigned* wsum = (unsigned*)(fs + E);        // [32]
     unsigned short* te = (unsigned short*)(wsum + 32);   // [nslot] expert id, NONE: no expert
-    unsigned short* rk = te + 2 * ((nslot + 1) / 2);     // [nslot] in-chunk rank, then union key
+    unsigned short* rk = te + 2 * ((nslot + 1) / 2);     // [nslot] rank (in chunk or segment), then union key
     const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, w = tid >> 6, nw = nth >> 6;
     for (int i = tid; i < nchunk * E; i += nth) cnt[i] = 0;
+    if (!STABLE)
+        for (int i = tid; i < E; i += nth) fs[i] = 0x7FFFFFFF;
+    if (!STABLE) __syncthreads();
     for (int s = tid; s < nslot; s += nth) {
         const int e = top[s];
-        te[s] = (e >= 0 && e < E) ? (unsigned short)e : NONE;
+        const bool ok = e >= 0 && e < E;
+        te[s] = ok ? (unsigned short)e : NONE;
+        if (!STABLE) {
+            rk[s] = ok ? (unsigned short)atomicAdd(&cnt[ok ? e : 0], 1) : NONE;
+            if (ok) atomicMin(&fs[e], s);
+        }
     }
     __syncthreads();
+    if (STABLE) {
     int nbits = 1;
     while ((1 << nbits) < E) nbits++;
     for (int c = w; c < nchunk; c += nw) {
@@ -817,9 +835,10 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
         if (lane == 0) off[e] = (int)carry;
     }
     __syncthreads();
+    }
     // one block scan of (count, multi << 16 | single) gives segment starts
     // and the work-table positions of both groups
-    const int total_e = tid < E ? off[tid] : 0;
+    const int total_e = tid < E ? (STABLE ? off[tid] : cnt[tid]) : 0;
     uint2 tot;
     const uint2 excl = block_exclusive_scan2(
         make_uint2((unsigned)total_e, ((unsigned)(total_e > 1) << 16) | (unsigned)(total_e == 1)), wsum, &tot);
@@ -865,10 +884,11 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
         const unsigned short r = rk[s];
         if (r == NONE) continue;
         const int e = te[s];
-        const int pos = off[e] + cnt[e * nchunk + s / DISP_CHUNK] + r;
+        const int pos = off[e] + (STABLE ? cnt[e * nchunk + s / DISP_CHUNK] : 0) + r;
         seg_slot[pos] = s;
-        if (pos == off[e]) { first_slot[e] = s; fs[e] = s; }
+        if (STABLE && pos == off[e]) { first_slot[e] = s; fs[e] = s; }
     }
+    if (!STABLE && tid < E && total_e > 0) first_slot[tid] = fs[tid];
     __syncthreads();
     // union order per token: its slots ranked by the first slot of their
     // expert (distinct experts -> distinct keys); slots without an expert go

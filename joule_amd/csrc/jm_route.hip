@@ -460,7 +460,7 @@ k_dispatch_work(RouteArgs a) {
     extern __shared__ int lds_i[];
     ExpertRec rec;
     if ((int)threadIdx.x < a.E) rec = load_expert_rec(a.rec, a.key0, threadIdx.x);
-    dispatch_block(a.top, a.B * a.topk, a.E, a.topk, lds_i, a.seg_off, a.seg_slot, a.active,
+    dispatch_block<false>(a.top, a.B * a.topk, a.E, a.topk, lds_i, a.seg_off, a.seg_slot, a.active,
                    a.n_active, a.first_slot, a.comb, a.work, a.umax, &rec);
     // the dense experts' token tiles, in work-table order, and the list of
     // the experts under dense_min (their wave items run on the MFMA grids)
