@@ -259,6 +259,28 @@ k_router_grp(RouteArgs a) {
         xT[((j + 3) & 7) * TP + ((j + 3) >> 3)] = xv[i].w;
     }
     __syncthreads();
+    // x digits: one G-value group per G-lane segment (and, for the MFMA
+    // branch, the same group as int8 digit pairs); two groups at a time, so
+    // that their reduction chains interleave.  Before the chains: they need
+    // only the staged token, so they run while the table's chunks arrive.
+    constexpr int ng = d / G;
+    constexpr int PPW = JM_WAVE / G;
+    const int sub = lane / G;
+    const bool i8 = a.xqh != nullptr;
+    for (int base = eg * PPW; base < ng; base += 2 * ngrp * PPW) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int p = base + u * ngrp * PPW + sub;
+            const bool ok = p < ng;
+            const int pp = ok ? p : 0;
+            const int j = pp * G + (lane & (G - 1));
+            const float v = ok ? xT[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
+            const size_t o = (size_t)b * d + (size_t)pp * G;
+            encode_group_both<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + pp) * (NDIG * (G / 8)),
+                                       a.xscale + (size_t)b * ng + pp, i8, a.xqh + (i8 ? o : 0),
+                                       a.xql + (i8 ? o : 0), a.xqs + (size_t)b * ng + pp, a.xqc + (size_t)b * ng + pp);
+        }
+    }
     const float* xr = xT + (size_t)r * TP;
     float acc = 0.0f;
     // Pinned order: chunk c's token reads and fused multiply-adds, then the
@@ -278,28 +300,6 @@ k_router_grp(RouteArgs a) {
     acc = __fadd_rn(acc, __shfl_xor(acc, 1, JM_WAVE));
     const int e = 8 * eg + el;
     if (r == 0 && e < a.E) a.logits[(size_t)b * a.E + e] = acc;
-
-    // x digits: one G-value group per G-lane segment (and, for the MFMA
-    // branch, the same group as int8 digit pairs); two groups at a time, so
-    // that their reduction chains interleave
-    constexpr int ng = d / G;
-    constexpr int PPW = JM_WAVE / G;
-    const int sub = lane / G;
-    const bool i8 = a.xqh != nullptr;
-    for (int base = eg * PPW; base < ng; base += 2 * ngrp * PPW) {
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int p = base + u * ngrp * PPW + sub;
-            const bool ok = p < ng;
-            const int pp = ok ? p : 0;
-            const int j = pp * G + (lane & (G - 1));
-            const float v = ok ? xT[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
-            const size_t o = (size_t)b * d + (size_t)pp * G;
-            encode_group_both<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + pp) * (NDIG * (G / 8)),
-                                       a.xscale + (size_t)b * ng + pp, i8, a.xqh + (i8 ? o : 0),
-                                       a.xql + (i8 ? o : 0), a.xqs + (size_t)b * ng + pp, a.xqc + (size_t)b * ng + pp);
-        }
-    }
 }
 
 // The same for batches of many tokens: block (4 expert groups, 4 tokens),
@@ -330,19 +330,23 @@ k_router_quad(RouteArgs a) {
 
     constexpr int XV = d / 4 / 64;
     constexpr int NB = C::NC < 16 ? C::NC : 16;
+    // wave w stages token b0 + w: its loads first, so that staging waits
+    // for them only, then the table's
+    const int bw = b0 + w;
+    float4 xv[XV];
+    {
+        const float4* xb = (const float4*)(a.x + (size_t)(bw < a.B ? bw : b0) * d);
+#pragma unroll
+        for (int i = 0; i < XV; i++) xv[i] = xb[lane + 64 * i];
+    }
     uint4 buf[NB][C::CP];
     if (chains) {
 #pragma unroll
         for (int c = 0; c < NB; c++) C::load(buf[c], wt, eg, c, lane);
     }
-    // wave w stages token b0 + w
     {
-        const int b = b0 + w;
-        float4 xv[XV];
+        const int b = bw;
         if (b < a.B) {
-            const float4* xb = (const float4*)(a.x + (size_t)b * d);
-#pragma unroll
-            for (int i = 0; i < XV; i++) xv[i] = xb[lane + 64 * i];
             if (LAYER && a.xpart) {
                 const float4* xp = (const float4*)(a.xpart + (size_t)b * d);
                 const size_t sstride = (size_t)a.B * d / 4;
@@ -403,6 +407,32 @@ k_router_quad(RouteArgs a) {
     }
     __syncthreads();
     const int nt = min(RQ_T, a.B - b0);           // tokens of this block (>= 1)
+    // x digits (one G-value group per G-lane segment) and the MFMA digit
+    // pairs of the block's tokens, this wave's share over the grid's nvg
+    // waves, before the chains: they need only the staged tokens, so they
+    // run while the table's chunks are still arriving.  The tokens of a
+    // group are encoded together (unconditionally, the stores guarded), so
+    // that their reduction chains interleave.
+    constexpr int ng = d / G;
+    constexpr int PPW = JM_WAVE / G;
+    const int sub = lane / G;
+    const bool i8 = a.xqh != nullptr;
+    for (int base = eg * PPW; base < ng; base += nvg * PPW) {
+        const int p = base + sub;
+        const bool ok = p < ng;
+        const int pp = ok ? p : 0;
+        const int j = pp * G + (lane & (G - 1));
+#pragma unroll
+        for (int t = 0; t < RQ_T; t++) {
+            const bool st = ok && t < nt;
+            const size_t b = (size_t)b0 + (t < nt ? t : 0);
+            const float v = st ? xT[t][(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
+            const size_t o = b * d + (size_t)pp * G;
+            encode_group_both<G, NDIG>(v, st, a.xdig + (b * ng + pp) * (NDIG * (G / 8)), a.xscale + b * ng + pp, i8,
+                                       a.xqh + (i8 ? o : 0), a.xql + (i8 ? o : 0), a.xqs + b * ng + pp,
+                                       a.xqc + b * ng + pp);
+        }
+    }
     if (chains) {
         float acc[RQ_T];
 #pragma unroll
@@ -426,30 +456,6 @@ k_router_quad(RouteArgs a) {
             v = __fadd_rn(v, __shfl_xor(v, 2, JM_WAVE));
             v = __fadd_rn(v, __shfl_xor(v, 1, JM_WAVE));
             if (r == 0 && e < a.E && t < nt) a.logits[(size_t)(b0 + t) * a.E + e] = v;
-        }
-    }
-    // x digits (one G-value group per G-lane segment) and the MFMA digit pairs of
-    // the block's tokens: this wave's share, over the grid's nvg waves.  The
-    // tokens of a group are encoded together (unconditionally, the stores
-    // guarded), so that their reduction chains interleave.
-    constexpr int ng = d / G;
-    constexpr int PPW = JM_WAVE / G;
-    const int sub = lane / G;
-    const bool i8 = a.xqh != nullptr;
-    for (int base = eg * PPW; base < ng; base += nvg * PPW) {
-        const int p = base + sub;
-        const bool ok = p < ng;
-        const int pp = ok ? p : 0;
-        const int j = pp * G + (lane & (G - 1));
-#pragma unroll
-        for (int t = 0; t < RQ_T; t++) {
-            const bool st = ok && t < nt;
-            const size_t b = (size_t)b0 + (t < nt ? t : 0);
-            const float v = st ? xT[t][(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
-            const size_t o = b * d + (size_t)pp * G;
-            encode_group_both<G, NDIG>(v, st, a.xdig + (b * ng + pp) * (NDIG * (G / 8)), a.xscale + b * ng + pp, i8,
-                                       a.xqh + (i8 ? o : 0), a.xql + (i8 ? o : 0), a.xqs + b * ng + pp,
-                                       a.xqc + b * ng + pp);
         }
     }
 }
