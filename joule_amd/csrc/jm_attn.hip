@@ -616,12 +616,13 @@ k_kv_append(AttnArgs a) {
     else kv_store(k, a, b, kh, pos, threadIdx.x, (gptr<uint16_t>)kvp[0], (gptr<uint16_t>)kvp[1], nullptr);
 }
 
-// The 4 waves' partial outputs of a split block merged with the split's
-// max (the flash-decoding merge within the block) into part_o / part_ml:
+// The 4 waves' partial outputs of a split block (wave w's at red + w *
+// wstride, [QPK][128]) merged with the split's max (the flash-decoding
+// merge within the block) into part_o / part_ml:
 // thread tid takes head tid / 32, dimensions 4 (tid % 32) .. + 3, so that
 // each thread forms the 4 waves' factors of one head once.
 template <int QPK>
-__device__ __forceinline__ void merge_waves(const AttnArgs& a, int b, int kh, int s, const float (*red)[QPK * 128],
+__device__ __forceinline__ void merge_waves(const AttnArgs& a, int b, int kh, int s, const float* red, int wstride,
                                             const float (*mls)[QPK][2]) {
     constexpr int HD = 128;
     const int tid = threadIdx.x;
@@ -636,7 +637,7 @@ __device__ __forceinline__ void merge_waves(const AttnArgs& a, int b, int kh, in
             for (int ww = 0; ww < 4; ww++) {
                 const float m = mls[ww][h][0];
                 const float f = m == -INFINITY ? 0.0f : expf_fast(__fsub_rn(m, M));
-                const float4 r = *(const float4*)&red[ww][oi];
+                const float4 r = *(const float4*)&red[(size_t)ww * wstride + oi];
                 O.x = __builtin_fmaf(r.x, f, O.x);
                 O.y = __builtin_fmaf(r.y, f, O.y);
                 O.z = __builtin_fmaf(r.z, f, O.z);
@@ -682,15 +683,22 @@ template <int QPK>
 __global__ void __launch_bounds__(256)
 k_attn_part(AttnArgs a) {
     constexpr int HD = 128, P = 128, PW = 32, VR = 132;
-    __shared__ __align__(16) uint16_t vt[4][PW * VR];   // each wave's V rows
-    __shared__ __align__(16) float red[4][QPK * HD];    // each wave's outputs
+    // Each wave's V rows, then (its own region, once its last P.V read is
+    // issued: a wave's LDS operations complete in order) its outputs for the
+    // merge.  Until every wave has read them (the barrier after the query
+    // columns), the start holds the finished query heads (bf16 hi, lo) and
+    // the token's own k and v row (the split that holds it).  34 KB per
+    // block: the 544 blocks of an 8-token step at 2049 positions are
+    // resident at once (with a separate 16 KB output buffer, two blocks fit
+    // a CU and the last 32 ran as a second round).
+    __shared__ __align__(16) uint16_t vt[4][PW * VR];
     __shared__ float mls[4][QPK][2];                    // each wave's (max, sum)
-    // until every wave has read them (the barrier after the query columns),
-    // red holds the finished query heads (bf16 hi, lo) and the token's own
-    // k and v row (the split that holds it): 3 blocks of 256 threads fit a CU
-    static_assert(QPK * 2 * HD * 2 + 2 * HD * 2 <= sizeof(float) * 4 * QPK * HD, "prologue fits red");
-    uint16_t (*qs)[2][HD] = (uint16_t (*)[2][HD])&red[0][0];
-    uint16_t (*kvn)[HD] = (uint16_t (*)[HD])((char*)&red[0][0] + QPK * 2 * HD * 2);
+    constexpr int RSTRIDE = PW * VR / 2;                // floats between the waves' output regions
+    static_assert(QPK * HD <= RSTRIDE, "a wave's outputs fit its V region");
+    static_assert(QPK * 2 * HD * 2 + 2 * HD * 2 <= sizeof(vt), "prologue fits the V rows' space");
+    float* const red0 = (float*)&vt[0][0];
+    uint16_t (*qs)[2][HD] = (uint16_t (*)[2][HD])&vt[0][0];
+    uint16_t (*kvn)[HD] = (uint16_t (*)[HD])((char*)&vt[0][0] + QPK * 2 * HD * 2);
     const int s = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int pos = a.pos[b];
     const int T = pos + 1;
@@ -728,15 +736,18 @@ k_attn_part(AttnArgs a) {
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) kr[mt][kk] = load_g16(row + 32 * kk);
     }
-#pragma unroll
-    for (int jv = 0; jv < 8; jv++) {
-        const int t = tw + 4 * jv + g;
-        vr[jv] = load_g16(vc + ((size_t)(t < T ? t : 0) * a.KH + kh) * HD + 8 * n);
-    }
-    __builtin_amdgcn_sched_barrier(0);      // keep every request ahead of the arithmetic
+    __builtin_amdgcn_sched_barrier(0);      // keep the K requests ahead of the arithmetic
     {
         float v[4];
         fin4_value(v, fq, a, b, qrow, a.qn ? a.qk_norm : 0, true, qj);
+        // the V rows once the query's inputs are consumed: the registers
+        // they take are the prologue's, so that the kernel stays at 3
+        // blocks per CU (the rows arrive while the scores are formed)
+#pragma unroll
+        for (int jv = 0; jv < 8; jv++) {
+            const int t = tw + 4 * jv + g;
+            vr[jv] = load_g16(vc + ((size_t)(t < T ? t : 0) * a.KH + kh) * HD + 8 * n);
+        }
         if (QPK == 8 || qh < QPK) {                 // whole 32-lane segments
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -769,7 +780,7 @@ k_attn_part(AttnArgs a) {
         for (int j = 0; j < 8; j++)
             if (tw + 4 * j + g == pos) vr[j] = *(const uint4*)&kvn[1][8 * n];
     }
-    __syncthreads();                        // red is free from here
+    __syncthreads();                        // vt is free from here
     bf16x8 qb[4];
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) qb[kk] = __builtin_bit_cast(bf16x8, qr[kk]);
@@ -858,7 +869,7 @@ k_attn_part(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int hh = 4 * (g & 1) + i;
-            if (hh < QPK) red[w][hh * HD + 16 * (nt + 4 * (g >> 1)) + n] = o[4 * nt + i];
+            if (hh < QPK) red0[(size_t)w * RSTRIDE + hh * HD + 16 * (nt + 4 * (g >> 1)) + n] = o[4 * nt + i];
         }
     if (g == 0 && n < QPK) {
         mls[w][n][0] = mx;
@@ -866,7 +877,7 @@ k_attn_part(AttnArgs a) {
     }
     __syncthreads();
 
-    merge_waves<QPK>(a, b, kh, s, red, mls);
+    merge_waves<QPK>(a, b, kh, s, red0, RSTRIDE, mls);
 }
 
 // The split block over float32 caches, in float32 arithmetic throughout
@@ -998,7 +1009,7 @@ k_attn_part_f32(AttnArgs a) {
         mls[w][lane][1] = l;
     }
     __syncthreads();
-    merge_waves<QPK>(a, b, kh, s, red, mls);
+    merge_waves<QPK>(a, b, kh, s, &red[0][0], QPK * HD, mls);
 }
 
 // Merge of the splits of one (query head, token): out = sum_s o_s e^(m_s - M)
