@@ -462,17 +462,17 @@ __device__ __forceinline__ float wave_max_f(float v) {
 // round without candidates yields index -1 and weight -1e30, the reference's
 // values when nothing beats its -1e30 start.
 // p_lds holds 64*EPL floats.  Lane i < k writes top[i] and tw[i].
+// topk_vals takes the scores in registers (v[j] = score of expert lane +
+// 64 j; entries past E are ignored); topk_wave loads them from s.
 template <int EPL>
-__device__ __forceinline__ void topk_wave(const float* __restrict__ s, int E, int k, int renorm,
-                                          float* p_lds, int* __restrict__ top, float* __restrict__ tw) {
+__device__ __forceinline__ void topk_vals(const float (&v)[EPL], int E, int k, int renorm, float* p_lds,
+                                          int* __restrict__ top, float* __restrict__ tw) {
     const int lane = threadIdx.x & 63;
-    float v[EPL];
     float mx = -1e30f;
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? s[e] : __int_as_float(0x7FC00000);
-        if (v[j] > mx) mx = v[j];
+        if (e < E && v[j] > mx) mx = v[j];
     }
     mx = wave_max_f(mx);                       // lane values are >= -1e30, never NaN
     float ex[EPL];
@@ -537,6 +537,19 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ s, int E, in
         top[lane] = my_e;
         tw[lane] = my_w;
     }
+}
+
+template <int EPL>
+__device__ __forceinline__ void topk_wave(const float* __restrict__ s, int E, int k, int renorm,
+                                          float* p_lds, int* __restrict__ top, float* __restrict__ tw) {
+    const int lane = threadIdx.x & 63;
+    float v[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? s[e] : 0.0f;
+    }
+    topk_vals<EPL>(v, E, k, renorm, p_lds, top, tw);
 }
 
 // ------------------------------------------------------------- dispatch

@@ -26,6 +26,7 @@
 // chains' order.
 #include <algorithm>
 
+#include "jm_chain.h"
 #include "jm_device.h"
 #include "jm_kernels.h"
 
@@ -86,53 +87,6 @@ hipError_t launch_bf16_exact(const float* in, long long n, unsigned* flag, hipSt
     return hipGetLastError();
 }
 
-
-// Chain loads in chunks of CP pieces (16 chain values of a bf16 table, 8
-// of a float32 one); a ring of chunks is kept in flight, the loads of chunk
-// c + ring issued as soon as chunk c's registers are consumed.
-template <int DV, bool WBF16>
-struct Chain {
-    static constexpr int T = DV * 64;                 // chain length (d / 8)
-    static constexpr int P = WBF16 ? 8 : 4;           // chain values per 16-byte piece
-    static constexpr int NP = T / P;                  // pieces per chain
-    static constexpr int CP = 2;                      // pieces per chunk
-    static constexpr int NC = NP / CP;                // chunks
-
-    static __device__ __forceinline__ void load(uint4 (&buf)[CP], const uint4* __restrict__ wt, int eg,
-                                                int c, int lane) {
-        const uint4* p = wt + ((size_t)eg * NP + (size_t)c * CP) * 64 + lane;
-#pragma unroll
-        for (int i = 0; i < CP; i++) buf[i] = p[(size_t)i * 64];
-    }
-
-    // acc += chunk c of the chain (values in order), x from the staged row
-    static __device__ __forceinline__ float fma_chunk(const uint4 (&buf)[CP], const float* xr, int c,
-                                                      float acc) {
-        const float4* xq = (const float4*)xr + (size_t)c * CP * P / 4;
-#pragma unroll
-        for (int i = 0; i < CP; i++) {
-            if (WBF16) {
-                const float4 x0 = xq[2 * i], x1 = xq[2 * i + 1];
-                const unsigned w[4] = {buf[i].x, buf[i].y, buf[i].z, buf[i].w};
-                acc = __builtin_fmaf(__uint_as_float(w[0] << 16), x0.x, acc);
-                acc = __builtin_fmaf(__uint_as_float(w[0] & 0xFFFF0000u), x0.y, acc);
-                acc = __builtin_fmaf(__uint_as_float(w[1] << 16), x0.z, acc);
-                acc = __builtin_fmaf(__uint_as_float(w[1] & 0xFFFF0000u), x0.w, acc);
-                acc = __builtin_fmaf(__uint_as_float(w[2] << 16), x1.x, acc);
-                acc = __builtin_fmaf(__uint_as_float(w[2] & 0xFFFF0000u), x1.y, acc);
-                acc = __builtin_fmaf(__uint_as_float(w[3] << 16), x1.z, acc);
-                acc = __builtin_fmaf(__uint_as_float(w[3] & 0xFFFF0000u), x1.w, acc);
-            } else {
-                const float4 xv = xq[i];
-                acc = __builtin_fmaf(__uint_as_float(buf[i].x), xv.x, acc);
-                acc = __builtin_fmaf(__uint_as_float(buf[i].y), xv.y, acc);
-                acc = __builtin_fmaf(__uint_as_float(buf[i].z), xv.z, acc);
-                acc = __builtin_fmaf(__uint_as_float(buf[i].w), xv.w, acc);
-            }
-        }
-        return acc;
-    }
-};
 
 // Router scores of one expert group (8 experts) for one token: block
 // (eg, b) is one wave; lane 8 * el + r runs chain r of expert 8 * eg + el
@@ -250,14 +204,7 @@ k_router_grp(RouteArgs a) {
             xv[i].w = __fmul_rn(__fmul_rn(xv[i].w, inv), bf16_bits_to_f32(w.y >> 16));
         }
     }
-#pragma unroll
-    for (int i = 0; i < XV; i++) {
-        const int j = 4 * (lane + 64 * i);
-        xT[((j + 0) & 7) * TP + ((j + 0) >> 3)] = xv[i].x;
-        xT[((j + 1) & 7) * TP + ((j + 1) >> 3)] = xv[i].y;
-        xT[((j + 2) & 7) * TP + ((j + 2) >> 3)] = xv[i].z;
-        xT[((j + 3) & 7) * TP + ((j + 3) >> 3)] = xv[i].w;
-    }
+    stage_chain_order<XV, TP>(xv, xT);
     __syncthreads();
     // x digits: one G-value group per G-lane segment (and, for the MFMA
     // branch, the same group as int8 digit pairs); two groups at a time, so
@@ -281,23 +228,7 @@ k_router_grp(RouteArgs a) {
                                        a.xql + (i8 ? o : 0), a.xqs + (size_t)b * ng + pp, a.xqc + (size_t)b * ng + pp);
         }
     }
-    const float* xr = xT + (size_t)r * TP;
-    float acc = 0.0f;
-    // Pinned order: chunk c's token reads and fused multiply-adds, then the
-    // loads of chunk c + NB into the registers chunk c used.  The empty asm
-    // takes the running sum and fences memory operations, so the compiler
-    // neither sinks the arithmetic to the end of the chain nor hoists later
-    // chunks' reads.
-#pragma unroll
-    for (int c = 0; c < C::NC; c++) {
-        acc = C::fma_chunk(buf[c % NB], xr, c, acc);
-        __asm__ volatile("" : "+v"(acc) : : "memory");
-        if (c + NB < C::NC) C::load(buf[c % NB], wt, eg, c + NB, lane);
-    }
-    // horizontal sum in the AVX2 order: (r, r^4), then ^2, then ^1
-    acc = __fadd_rn(acc, __shfl_xor(acc, 4, JM_WAVE));
-    acc = __fadd_rn(acc, __shfl_xor(acc, 2, JM_WAVE));
-    acc = __fadd_rn(acc, __shfl_xor(acc, 1, JM_WAVE));
+    const float acc = router_chains<DV, WBF16, NB>(buf, wt, eg, xT);
     const int e = 8 * eg + el;
     if (r == 0 && e < a.E) a.logits[(size_t)b * a.E + e] = acc;
 }

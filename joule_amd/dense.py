@@ -58,10 +58,15 @@ class DenseFfnStore:
         """out [B, d] = the dense FFN of layer l on x [B, d] (float32, CUDA)."""
         if self.w is None:
             raise RuntimeError("FFN weights not set (set_weights)")
-        if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or x.dim() != 2:
-            raise ValueError("x must be a contiguous float32 CUDA tensor [B, d]")
+        d = self.shape.d
+        if (x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or x.dim() != 2
+                or x.shape[1] != d):
+            raise ValueError(f"x must be a contiguous float32 CUDA tensor [B, {d}]")
         if out is None:
             out = torch.empty_like(x)
+        elif (out.dtype != torch.float32 or not out.is_cuda or not out.is_contiguous()
+              or tuple(out.shape) != tuple(x.shape) or out.device != x.device):
+            raise ValueError(f"out must be a contiguous float32 CUDA tensor [B, {d}] on x's device")
         _lib.check(_lib.lib().jm_layer_ffn_batch(self._h, int(l), _lib.ptr(x), x.shape[0], _lib.ptr(out), None, None,
                                                  _lib.stream_handle(stream)), "jm_layer_ffn_batch")
         return out

@@ -145,8 +145,22 @@ class HbmExpertStore:
         with more than 256 slots); 0 restores the default."""
         _lib.check(_lib.lib().jm_store_set_dense_min(self._h, int(min_tokens)), "jm_store_set_dense_min")
 
+    def set_small_path(self, mode: int) -> None:
+        """Batches of up to 64 slots: 2 front kernel with the router inside
+        where it applies, 1 front kernel after the router kernel, 0 (default)
+        the three-launch decode path."""
+        _lib.check(_lib.lib().jm_store_set_small_path(self._h, int(mode)), "jm_store_set_small_path")
+
+    def sync_words(self, stream=None) -> tuple[int, int]:
+        """(call counter, polls that ran out) of the small-batch front kernel."""
+        t = torch.zeros(2, dtype=torch.int32, device=self.blob.device)
+        _lib.check(_lib.lib().jm_store_copy_workspace(self._h, _lib.WS_SYNC, _lib.ptr(t), 8,
+                                                      _lib.stream_handle(stream)), "jm_store_copy_workspace")
+        v = t.cpu().tolist()
+        return int(v[0]) & 0xFFFFFFFF, int(v[1]) & 0xFFFFFFFF
+
     def dense_tiles(self, stream=None) -> int:
-        """64-token tiles the MFMA branch computed in the last call."""
+        """32-token tiles the MFMA branch computed in the last call."""
         t = torch.zeros(1, dtype=torch.int32, device=self.blob.device)
         _lib.check(_lib.lib().jm_store_copy_workspace(self._h, _lib.WS_N_DENSE_TILES, _lib.ptr(t), 4,
                                                       _lib.stream_handle(stream)), "jm_store_copy_workspace")
@@ -192,14 +206,20 @@ class HbmExpertStore:
         """out[B, d] = MoE block of layer l on x[B, d] (float32, CUDA)."""
         if self.router is None:
             raise RuntimeError("router weights not set (set_router)")
-        if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or x.dim() != 2:
-            raise ValueError("x must be a contiguous float32 CUDA tensor [B, d]")
-        B = x.shape[0]
+        B = x.shape[0] if x.dim() == 2 else -1
+        self._stage_in(x, "x", (B, self.shape.d), torch.float32)
         if out is None:
             out = torch.empty_like(x)
+        else:
+            self._stage_in(out, "out", (B, self.shape.d), torch.float32)
         for t, dt in ((topk_idx, torch.int32), (topk_w, torch.float32)):
-            if t is not None and (t.dtype != dt or t.numel() != B * self.shape.topk or not t.is_contiguous()):
-                raise ValueError("topk outputs must be contiguous [B, topk] int32 / float32")
+            if t is not None and (t.dtype != dt or t.numel() != B * self.shape.topk or not t.is_contiguous()
+                                  or not t.is_cuda):
+                raise ValueError("topk outputs must be contiguous [B, topk] int32 / float32 CUDA tensors")
+            if t is not None and t.device != x.device:
+                raise ValueError("topk outputs must be on x's device")
+        if out.device != x.device:
+            raise ValueError("out must be on x's device")
         _lib.check(_lib.lib().jm_layer_ffn_batch(self._h, int(l), _lib.ptr(x), B, _lib.ptr(out),
                                                  _lib.ptr(topk_idx), _lib.ptr(topk_w),
                                                  _lib.stream_handle(stream)), "jm_layer_ffn_batch")
