@@ -126,7 +126,11 @@ int jm_store_set_dense_min(jm_store* s, int min_tokens);
  * router inside the front kernel when the call has no decoder-layer extras
  * and ceil(E/8) * B fits the device's compute units; mode 1 keeps the router
  * kernel before it; mode 0 (the default) runs such batches on the
- * three-launch decode path like larger ones.  The results agree within the
+ * three-launch decode path like larger ones.  mode 3 (B <= 8, records'
+ * scales 16-byte aligned) keeps the three launches with the gate/up on the
+ * matrix cores: the router kernel also writes the tokens' int8 digit pairs,
+ * the gate/up kernel selects the experts in every block and multiplies each
+ * item's 32 gate and up rows against all B tokens on int8 MFMA.  The results agree within the
  * block's tolerance on every path; router indices and weights are the same
  * bits.  No counterpart in the reference (a switch between this build's
  * kernels). */

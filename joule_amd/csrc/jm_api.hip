@@ -367,8 +367,20 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
 #define JM_MARK(i) if (s->prof && stage_marks) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
     // small batches: the front kernel (top-k + gate/up, with the router inside
     // when the call has no decoder-layer extras) and the LDS down kernel
-    const bool small = dec && s->small_path > 0 &&
+    const bool small = dec && (s->small_path == 1 || s->small_path == 2) &&
                        jm::front_ok(B, E, d, s->m, k, G, s->n_cu, s->lds_max);
+    // small batches on the matrix cores: the router kernel also writes the
+    // tokens' int8 digit pairs, the MFMA gate/up kernel selects the experts
+    const bool mx = dec && s->small_path == 3 && s->sc16 && jm::gu_mx_ok(B, E, d, s->m, k, G);
+    jm::GuMxArgs g;
+    if (mx) {
+        r.skip_topk = 1;
+        r.xqh = w.xqh;
+        g.logits = w.logits; g.xqh = w.xqh; g.xql = w.xql; g.xqs = w.xqs; g.xqc = w.xqc;
+        g.B = B; g.E = E; g.d = d; g.m = s->m; g.topk = k; g.renorm = s->renorm; g.group = G;
+        g.blob = s->blob; g.rec = s->rec; g.key0 = (long long)layer * E;
+        g.top = w.top; g.tw = w.tw; g.act = w.act; g.adig = w.adig; g.ascale = w.ascale;
+    }
     if (small) {
         const bool rin = s->small_path == 2 && !io.xpart && !io.norm_w && jm::front_router_ok(B, E, s->n_cu);
         jm::FrontArgs f;
@@ -404,7 +416,9 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     JM_HIP(jm::launch_route_tok(r, st), "route launch");
     if (!dec) JM_HIP(jm::launch_dispatch_work(r, st), "dispatch launch");
     JM_MARK(1);
-    if (dec) {
+    if (mx) {
+        JM_HIP(jm::launch_gu_mx(g, s->n_cu, st), "gate/up MFMA launch");
+    } else if (dec) {
         JM_HIP(jm::launch_gateup_dec(a, st), "gate/up launch");
     } else {
         if (mfma) {
@@ -488,6 +502,7 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
     s->group = group;
     s->dense_min = JM_DENSE_MIN_DEFAULT;
     s->small_path = 0;
+    s->sc16 = sc16;
     s->mfma_ok = jm::mfma_shape_ok(d, m) && sc16;
     s->max_layers = -1;
     s->blob = (const uint8_t*)blob;
@@ -602,7 +617,7 @@ int jm_store_set_dense_min(jm_store* s, int min_tokens) {
 
 int jm_store_set_small_path(jm_store* s, int mode) {
     if (int rc = check_moe_store(s, "jm_store_set_small_path")) return rc;
-    if (mode < 0 || mode > 2) return fail(JM_ERR_ARG, "small-batch path mode must be 0, 1 or 2 (got %d)", mode);
+    if (mode < 0 || mode > 3) return fail(JM_ERR_ARG, "small-batch path mode must be 0..3 (got %d)", mode);
     s->small_path = mode;
     return 0;
 }

@@ -39,6 +39,7 @@
 //               (:1502-1507).
 #include <atomic>
 
+#include "jm_bufld.h"
 #include "jm_chain.h"
 #include "jm_items.h"
 
@@ -53,7 +54,6 @@ constexpr int FR_WAVES = FR_THREADS / 64;
 constexpr int FR_MAX_E = 256;
 constexpr int FR_OUT = JM_FRONT_SLOTS;    // staged outputs per wave: its items have distinct experts
 constexpr int FR_SPIN = 1 << 16;          // polls of one token's scores before giving up (~0.1 s)
-constexpr unsigned RSRC_W3 = 0x00020000u; // buffer descriptor word 3 (gfx9: 32-bit data format)
 
 __host__ __device__ constexpr size_t align_up(size_t n, size_t a) { return (n + a - 1) / a * a; }
 
@@ -66,25 +66,6 @@ struct FrontOut {
     uint32_t dig[4];          // one word per digit plane
 };
 static_assert(sizeof(FrontOut) == 64, "64-byte staged outputs");
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(unsigned long long addr, int bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)addr, (short)0, bytes, (int)RSRC_W3);
-}
-
-__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, unsigned off) {
-    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-__device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, unsigned off) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-}
-
-__device__ __forceinline__ unsigned long long uniform64(unsigned long long v) {
-    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
-    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
-    return ((unsigned long long)hi << 32) | lo;
-}
 
 // Digits of 8 consecutive values of one token (one word per digit plane,
 // nibble i = value i), the G-value group's scale from the G/8 lanes that

@@ -199,6 +199,35 @@ bool front_ok(int B, int E, int d, int m, int topk, int group, int n_cu, int lds
 bool front_router_ok(int B, int E, int n_cu);
 hipError_t launch_front(const FrontArgs& a, int n_cu, int lds_max, hipStream_t st);
 hipError_t launch_down_lds(const DownArgs& a, int n_cu, int lds_max, hipStream_t st);
+
+// ---- small-batch gate/up on the matrix cores (jm_gumx.hip): B <= 8 tokens
+// Top-k of every token in every block, then items (routed expert, 32
+// intermediate rows) per block, the block's 8 waves splitting the hidden
+// columns, on v_mfma_i32_32x32x32_i8 against the tokens' int8 digit pairs
+// (the router kernel's xqh/xql/xqs/xqc).  Writes the top-k table (block 0),
+// act and its digits in the decode path's format (32 values per scale), for
+// k_down_comb.
+struct GuMxArgs {
+    const float* logits;      // [B][E] router scores
+    const int8_t* xqh;        // [B][d] token digit pairs in int8 operand order
+    const int8_t* xql;
+    const float* xqs;         // [B][d/G] their scales
+    const int* xqc;           // [B][d/G] sums of their integers 256 h + l per group
+    int B, E, d, m, topk, renorm, group;
+    const uint8_t* blob;
+    RecLoc rec;
+    long long key0;
+    int* top;                 // [B*k] the top-k table (written by block 0)
+    float* tw;                // [B*k]
+    float* act;               // [B*k][m]
+    uint32_t* adig;           // [B*k][m/32][NDIG][4] act digits (ExpertArgs::adig)
+    float* ascale;            // [B*k][m/32]
+};
+// B <= 8, B * topk <= 64, d 1024 or 2048, intermediate a multiple of 32,
+// at most 256 experts, group 32 or 64; the records' scales 16-byte aligned
+// (checked by the caller)
+bool gu_mx_ok(int B, int E, int d, int m, int topk, int group);
+hipError_t launch_gu_mx(const GuMxArgs& a, int n_cu, hipStream_t st);
 // dispatch path: gate/up and down over the work table, then the combine
 hipError_t launch_gateup(const ExpertArgs& a, int umax, hipStream_t st);
 hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st);

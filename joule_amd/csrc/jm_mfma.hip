@@ -17,9 +17,8 @@
 //            Q4 group (jm_device.h: encode_i8_group_wave): the router kernel
 //            writes them for x, the gate/up epilogue for act.
 // v_mfma_i32_32x32x32_i8 tiles, tokens on the A side (i), weight rows on the
-// B side (n).  Lane layout (checked on the device): A[i][k] at lane i % 32,
-// k = 16 (l / 32) + j; B[k][n] at lane n % 32, k = 16 (l / 32) + j; D
-// register v of lane l = (i = 8 (v / 4) + 4 (l / 32) + v % 4, n = l % 32).
+// B side (n), in the lane layout of jm_mx.h; the lo plane's accumulator
+// starts at -8 times the tokens' group sums (wdigits takes q, not q - 8).
 // So a lane holds one weight row and 16 tokens: the row's group scale is one
 // value per lane, the tokens' scales 16.
 //
@@ -38,13 +37,9 @@
 #include "jm_device.h"
 #include "jm_items.h"
 #include "jm_kernels.h"
+#include "jm_mx.h"
 
 namespace jm {
-
-typedef int int4v __attribute__((ext_vector_type(4)));
-typedef int int8v __attribute__((ext_vector_type(8)));
-typedef int int16v __attribute__((ext_vector_type(16)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int MT = JM_DENSE_TILE;   // tokens per tile (32)
 static_assert(MT == 32, "the tile's tokens are the 32 A rows of one MFMA");
@@ -59,15 +54,6 @@ constexpr int KPH_MAX = 1024;       // columns of a token phase (the tokens' LDS
 constexpr int SSC = 256;            // columns of a weight super-stage: 128 bytes (one cache line) per row
 constexpr int WRS = 144;            // LDS bytes per row of a wave's weight buffer (128 + bank spread)
 constexpr int WBUF = 32 * WRS;      // one super-stage of a wave's 32 rows
-
-// Two dwords of 8 packed nibbles each (value i in bits 4i..4i+3) as four
-// dwords of unsigned int8 q in i8_pos order: of each dword, values 0 2 4 6,
-// then 1 3 5 7.  The products take q, not q - 8: the lo plane's accumulator
-// starts at -8 times the tokens' group sums, which carries the -8.
-__device__ __forceinline__ int4v wdigits(uint32_t w0, uint32_t w1) {
-    return int4v{(int)(w0 & 0x0F0F0F0Fu), (int)((w0 >> 4) & 0x0F0F0F0Fu), (int)(w1 & 0x0F0F0F0Fu),
-                 (int)((w1 >> 4) & 0x0F0F0F0Fu)};
-}
 
 struct TileInfo {
     int slot0;      // first position of the tile in seg_slot

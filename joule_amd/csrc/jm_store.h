@@ -95,7 +95,9 @@ struct jm_store {
     hipEvent_t ev[JM_STAGES + 1];
     int dense_min;              // segment size from which an expert takes the MFMA branch
     int small_path;             // jm_store_set_small_path: 0 off, 1 front kernel after the router
-                                // kernel, 2 router inside the front kernel where it applies
+                                // kernel, 2 router inside the front kernel where it applies, 3 the
+                                // MFMA gate/up kernel (B <= 8)
+    bool sc16;                  // every record's scales start 16-byte aligned
     bool mfma_ok;               // the shape and the records' alignment allow the MFMA branch
     // ---- batch decode (jm_decode_layers_batch) ----
     int max_layers;             // jm_store_set_max_layers: < 0 runs every layer

@@ -148,7 +148,8 @@ class HbmExpertStore:
     def set_small_path(self, mode: int) -> None:
         """Batches of up to 64 slots: 2 front kernel with the router inside
         where it applies, 1 front kernel after the router kernel, 0 (default)
-        the three-launch decode path."""
+        the three-launch decode path, 3 the same with the gate/up on the
+        matrix cores (B <= 8)."""
         _lib.check(_lib.lib().jm_store_set_small_path(self._h, int(mode)), "jm_store_set_small_path")
 
     def sync_words(self, stream=None) -> tuple[int, int]:

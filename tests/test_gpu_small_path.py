@@ -4,7 +4,8 @@ The path is two launches: the front kernel (top-k in every block, then the
 gate/up rows of the routed experts, double-buffered per wave; with the router
 inside the launch in mode 2) and the down + combine kernel that requests
 every routed expert's rows at once.  Mode 1 runs the router kernel first,
-mode 0 the three-launch decode path.
+mode 0 the three-launch decode path, mode 3 the same three launches with the
+gate/up on the matrix cores (int8 MFMA against the tokens' digit pairs).
 
 Bars (written here):
 * router indices and routing weights bit-exact against the oracle;
@@ -69,7 +70,7 @@ CASES = [("qwen64", 1), ("qwen64", 2), ("qwen64", 5), ("qwen64", 8), ("qwen32", 
          ("olmoe64", 1), ("olmoe64", 8)]
 
 
-@pytest.mark.parametrize("mode", [2, 1, 0])
+@pytest.mark.parametrize("mode", [3, 2, 1, 0])
 @pytest.mark.parametrize("which,B", CASES)
 def test_small_path_parity(request, which, B, mode):
     layer = request.getfixturevalue(which)
@@ -156,7 +157,7 @@ def test_small_path_graph_replay(qwen64):
     del g
 
 
-@pytest.mark.parametrize("mode", [2, 1])
+@pytest.mark.parametrize("mode", [3, 2, 1])
 def test_small_path_nan_tokens(qwen64, mode):
     banner(f"small path NaN tokens mode {mode}")
     x = activations(8, QWEN3.d)
