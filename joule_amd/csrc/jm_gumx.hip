@@ -50,14 +50,6 @@ constexpr int GX_SLOTS = 64;
 constexpr int GX_MAX_E = 256;
 constexpr int GX_NE = 64;              // staged act outputs (slot, item) per block; a full list is written out early
 
-// A block barrier that orders LDS only: the LDS writes before it are
-// complete, the global loads in flight stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // NB bytes (4, 8 or 16) of a row's scales
 template <int NB>
 __device__ __forceinline__ uint4 bload_sc(__amdgpu_buffer_rsrc_t r, unsigned off) {
