@@ -683,10 +683,6 @@ def main() -> int:
                     help="only the plugin product HipBackend.q4_gemm at T = 1, 32, 33, 36, 512; prints its JSON")
     ap.add_argument("--probe", action="store_true",
                     help="only the launch and hand-off cost probes (libjoule_probe.so); prints their JSON")
-    ap.add_argument("--ab-small-path", action="store_true",
-                    help="only A/B of the small-batch path modes (0 three launches, 1 front kernel after the "
-                         "router kernel, 2 router inside the front kernel, 3 three launches with the gate/up on "
-                         "the matrix cores) at B = 1, 2, 4, 8; prints their JSON")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after timing, run 8 torch copies of this many MiB (a known-size kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -732,20 +728,6 @@ def main() -> int:
     store, gw = build_layers(shape, NL, G, seed=1000)
     if args.zipf_only:
         print(json.dumps({"qwen3_zipf512": zipf_block(store, gw, args.steps, NL)[0]}), flush=True)
-        return 0
-    if args.ab_small_path:
-        res = {}
-        for b in (1, 2, 4, 8):
-            xb = torch.from_numpy(activations(b, shape.d)).cuda()
-            for rep in range(2):
-                for mode in (0, 1, 2, 3):
-                    store.set_small_path(mode)
-                    m2, st2, _ = measure(store, gw, xb, args.steps, args.warmup, NL)
-                    res.setdefault(f"B{b}_mode{mode}", []).append(
-                        {"us": round(m2 * 1e3, 2), "stages_us": {k: round(v * 1e3, 2) for k, v in st2.items()}})
-                    log(f"B={b} mode {mode}: {m2 * 1e3:.2f} us/step, stages {st2}")
-        store.set_small_path(0)
-        print(json.dumps({"ab_small_path": res}), flush=True)
         return 0
     x_np = activations(B, shape.d)
     x = torch.from_numpy(x_np).cuda()

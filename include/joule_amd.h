@@ -118,24 +118,6 @@ int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, 
  * reference, whose batch is at most 16 tokens (decode_kernel.c:1522). */
 int jm_store_set_dense_min(jm_store* s, int min_tokens);
 
-/* Batches with B * topk <= 64 slots (and the shapes the kernels take: d
- * 1024 or 2048, intermediate a multiple of 32 up to 1024, E <= 256) run as
- * two launches: a persistent front kernel (top-k, then the gate/up rows of
- * the routed experts, double-buffered per wave) and a down + combine kernel
- * that requests every routed expert's rows at once.  mode 2 also runs the
- * router inside the front kernel when the call has no decoder-layer extras
- * and ceil(E/8) * B fits the device's compute units; mode 1 keeps the router
- * kernel before it; mode 0 (the default) runs such batches on the
- * three-launch decode path like larger ones.  mode 3 (B <= 8, records'
- * scales 16-byte aligned) keeps the three launches with the gate/up on the
- * matrix cores: the router kernel also writes the tokens' int8 digit pairs,
- * the gate/up kernel selects the experts in every block and multiplies each
- * item's 32 gate and up rows against all B tokens on int8 MFMA.  The results agree within the
- * block's tolerance on every path; router indices and weights are the same
- * bits.  No counterpart in the reference (a switch between this build's
- * kernels). */
-int jm_store_set_small_path(jm_store* s, int mode);
-
 /*
  * The MoE block of one layer: layer_ffn_batch(cfg, W, l, x, B, out)
  * (decode_kernel.c:1387-1508), for any B >= 0 (the reference clamps B to 16
@@ -188,10 +170,7 @@ int jm_store_stage_ms(jm_store* s, float* ms, int n);
  *   JM_WS_FIRST_SLOT int32 [E] first slot of each active expert
  *   JM_WS_ACT        float [B*topk][intermediate] SiLU(gate)*up per slot
  *   JM_WS_Y          float [B*topk][d] weighted expert output per slot
- *   JM_WS_N_DENSE_TILES int32 [1] 32-token tiles the MFMA branch computed
- *   JM_WS_SYNC       uint32 [2] the small-batch front kernel's call counter
- *                    and how many of its waits for the router scores ran out
- *                    of polls (0 unless something is wrong); any path */
+ *   JM_WS_N_DENSE_TILES int32 [1] 32-token tiles the MFMA branch computed */
 #define JM_WS_LOGITS 0
 #define JM_WS_SEG_OFF 1
 #define JM_WS_SEG_SLOT 2
@@ -201,7 +180,6 @@ int jm_store_stage_ms(jm_store* s, float* ms, int n);
 #define JM_WS_ACT 6
 #define JM_WS_Y 7
 #define JM_WS_N_DENSE_TILES 8
-#define JM_WS_SYNC 9
 int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t bytes, void* stream);
 
 /* ---- batch decode over all layers (decode_layers_batch) ---- */

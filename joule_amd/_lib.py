@@ -29,7 +29,6 @@ SIGNATURES = {
     "jm_store_reserve": ([_vp, _i], _i),
     "jm_store_info": ([_vp] + [_vp] * 6, _i),
     "jm_store_set_dense_min": ([_vp, _i], _i),
-    "jm_store_set_small_path": ([_vp, _i], _i),
     "jm_store_router_dtype": ([_vp, _vp], _i),
     "jm_layer_ffn_batch": ([_vp, _i, _vp, _i, _vp, _vp, _vp, _vp], _i),
     "jm_layer_ffn_batch_noalloc": ([_vp, _i, _vp, _i, _vp, _vp, _vp, _vp], _i),
@@ -80,7 +79,7 @@ STAGES = ("route", "gateup", "down")
 
 # jm_store_copy_workspace fields
 (WS_LOGITS, WS_SEG_OFF, WS_SEG_SLOT, WS_ACTIVE, WS_N_ACTIVE, WS_FIRST_SLOT, WS_ACT, WS_Y,
- WS_N_DENSE_TILES, WS_SYNC) = range(10)
+ WS_N_DENSE_TILES) = range(9)
 
 
 class JouleError(RuntimeError):

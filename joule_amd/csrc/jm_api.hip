@@ -149,7 +149,7 @@ int check_group_shape(int d, int m, int group) {
 namespace {
 
 // Sizes of the Ws fields for B tokens, in field order.
-constexpr int WS_NF = 29;
+constexpr int WS_NF = 27;
 void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
     const int E = s->E, d = s->d, m = s->m, k = s->topk, G = s->group;
     const size_t nslot = (size_t)B * k;
@@ -157,8 +157,6 @@ void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
     const size_t words_m = (size_t)(m / 8) * JM_NDIG;
     const size_t max_tiles = nslot / JM_DENSE_TILE + E;
     const size_t v[WS_NF] = {
-        256,                          // sync (first: the same place for every B)
-        (size_t)B * E * 8,            // ll
         (size_t)B * E * 4,            // logits
         nslot * 4,                    // top
         nslot * 4,                    // tw
@@ -176,7 +174,7 @@ void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
         (size_t)E * 4,                // small
         nslot * m * 4,                // act
         nslot * words_m * 4,          // adig
-        nslot * (m / 8) * 4,          // ascale
+        nslot * (m / 32) * 4,         // ascale
         nslot * d * 4,                // y
         nslot * m,                    // aqh
         nslot * m,                    // aql
@@ -203,7 +201,7 @@ size_t jm::ws_bytes(const jm_store* s, int B) {
 void jm::ws_layout(const jm_store* s, int B, char* base, Ws* w) {
     size_t sz[WS_NF];
     ws_sizes(s, B, sz);
-    void** slots[WS_NF] = {(void**)&w->sync, (void**)&w->ll, (void**)&w->logits, (void**)&w->top, (void**)&w->tw, (void**)&w->xdig,
+    void** slots[WS_NF] = {(void**)&w->logits, (void**)&w->top, (void**)&w->tw, (void**)&w->xdig,
                            (void**)&w->xscale, (void**)&w->seg_off, (void**)&w->seg_slot,
                            (void**)&w->active, (void**)&w->n_active, (void**)&w->first_slot,
                            (void**)&w->comb, (void**)&w->work, (void**)&w->tiles,
@@ -365,60 +363,11 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     a.logits = w.logits; a.renorm = s->renorm; a.top_w = w.top; a.tw_w = w.tw;
     const int max_tiles = nslot / JM_DENSE_TILE + E;
 #define JM_MARK(i) if (s->prof && stage_marks) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
-    // small batches: the front kernel (top-k + gate/up, with the router inside
-    // when the call has no decoder-layer extras) and the LDS down kernel
-    const bool small = dec && (s->small_path == 1 || s->small_path == 2) &&
-                       jm::front_ok(B, E, d, s->m, k, G, s->n_cu, s->lds_max);
-    // small batches on the matrix cores: the router kernel also writes the
-    // tokens' int8 digit pairs, the MFMA gate/up kernel selects the experts
-    const bool mx = dec && s->small_path == 3 && s->sc16 && jm::gu_mx_ok(B, E, d, s->m, k, G);
-    jm::GuMxArgs g;
-    if (mx) {
-        r.skip_topk = 1;
-        r.xqh = w.xqh;
-        g.logits = w.logits; g.xqh = w.xqh; g.xql = w.xql; g.xqs = w.xqs; g.xqc = w.xqc;
-        g.B = B; g.E = E; g.d = d; g.m = s->m; g.topk = k; g.renorm = s->renorm; g.group = G;
-        g.blob = s->blob; g.rec = s->rec; g.key0 = (long long)layer * E;
-        g.top = w.top; g.tw = w.tw; g.act = w.act; g.adig = w.adig; g.ascale = w.ascale;
-    }
-    if (small) {
-        const bool rin = s->small_path == 2 && !io.xpart && !io.norm_w && jm::front_router_ok(B, E, s->n_cu);
-        jm::FrontArgs f;
-        f.wt = rin ? r.wt : nullptr; f.wt_bf16 = r.wt_bf16; f.x = x;
-        f.logits_in = w.logits; f.xdig = w.xdig; f.xscale = w.xscale;
-        f.logits = w.logits; f.ll = w.ll; f.sync = w.sync;
-        f.B = B; f.E = E; f.d = d; f.m = s->m; f.topk = k; f.renorm = s->renorm; f.group = G;
-        f.blob = s->blob; f.rec = s->rec; f.key0 = (long long)layer * E;
-        f.top = w.top; f.tw = w.tw; f.act = w.act; f.adig = w.adig; f.ascale = (uint16_t*)w.ascale;
-        jm::DownArgs dn;
-        dn.blob = s->blob; dn.rec = s->rec; dn.key0 = f.key0;
-        dn.top = w.top; dn.tw = w.tw;
-        dn.B = B; dn.E = E; dn.d = d; dn.m = s->m; dn.topk = k; dn.group = G;
-        dn.adig = w.adig; dn.ascale = (const uint16_t*)w.ascale;
-        dn.out = out; dn.resid = io.resid; dn.sync = w.sync;
-        JM_MARK(0);
-        if (!rin) {
-            r.skip_topk = 1;                    // the front kernel selects the experts
-            JM_HIP(jm::launch_route_tok(r, st), "route launch");
-        }
-        JM_MARK(1);
-        JM_HIP(jm::launch_front(f, s->n_cu, s->lds_max, st), "front launch");
-        JM_MARK(2);
-        JM_HIP(jm::launch_down_lds(dn, s->n_cu, s->lds_max, st), "down launch");
-        JM_MARK(3);
-        if (!wsp) {
-            s->dec_last = 1;
-            s->last_B = B;
-        }
-        return 0;
-    }
     JM_MARK(0);
     JM_HIP(jm::launch_route_tok(r, st), "route launch");
     if (!dec) JM_HIP(jm::launch_dispatch_work(r, st), "dispatch launch");
     JM_MARK(1);
-    if (mx) {
-        JM_HIP(jm::launch_gu_mx(g, s->n_cu, st), "gate/up MFMA launch");
-    } else if (dec) {
+    if (dec) {
         JM_HIP(jm::launch_gateup_dec(a, st), "gate/up launch");
     } else {
         if (mfma) {
@@ -501,8 +450,6 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
     s->renorm = cfg->norm_topk_prob ? 1 : 0;
     s->group = group;
     s->dense_min = JM_DENSE_MIN_DEFAULT;
-    s->small_path = 0;
-    s->sc16 = sc16;
     s->mfma_ok = jm::mfma_shape_ok(d, m) && sc16;
     s->max_layers = -1;
     s->blob = (const uint8_t*)blob;
@@ -612,13 +559,6 @@ int jm_store_set_dense_min(jm_store* s, int min_tokens) {
     if (int rc = check_store(s)) return rc;
     if (min_tokens < 0) return fail(JM_ERR_ARG, "min_tokens must be >= 0 (0 = default)");
     s->dense_min = min_tokens == 0 ? JM_DENSE_MIN_DEFAULT : min_tokens;
-    return 0;
-}
-
-int jm_store_set_small_path(jm_store* s, int mode) {
-    if (int rc = check_moe_store(s, "jm_store_set_small_path")) return rc;
-    if (mode < 0 || mode > 3) return fail(JM_ERR_ARG, "small-batch path mode must be 0..3 (got %d)", mode);
-    s->small_path = mode;
     return 0;
 }
 
@@ -736,11 +676,10 @@ int jm_store_copy_workspace(const jm_store* s, int field, void* dst, uint64_t by
         case JM_WS_ACT: src = s->w.act; cap = nslot * s->m * 4; break;
         case JM_WS_Y: src = s->w.y; cap = nslot * s->d * 4; break;
         case JM_WS_N_DENSE_TILES: src = s->w.n_tiles; cap = 4; break;
-        case JM_WS_SYNC: src = s->w.sync; cap = 8; break;
         default: return fail(JM_ERR_ARG, "unknown workspace field %d", field);
     }
     if (!src || s->last_B == 0) return fail(JM_ERR_ARG, "no call has run on this store yet");
-    if (s->dec_last && field != JM_WS_LOGITS && field != JM_WS_ACT && field != JM_WS_SYNC)
+    if (s->dec_last && field != JM_WS_LOGITS && field != JM_WS_ACT)
         return fail(JM_ERR_ARG, "field %d is written only by the dispatch path (B * topk > %d)", field, JM_DEC_SLOTS);
     if (bytes > cap) return fail(JM_ERR_ARG, "%llu bytes requested, field holds %zu", (unsigned long long)bytes, cap);
     JM_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "workspace copy");

@@ -434,15 +434,6 @@ __device__ __forceinline__ void encode_digits_shared(float v, float mx, bool nf,
     }
 }
 
-// A block barrier that orders LDS only: the LDS writes before it are
-// complete, the global loads in flight stay in flight (__syncthreads waits
-// for every outstanding memory access).
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // ---------------------------------------------------------- router top-k
 
 // Float max over the whole wave; every lane gets the result (non-NaN

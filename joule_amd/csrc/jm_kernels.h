@@ -145,89 +145,6 @@ hipError_t launch_dispatch(const int* top, int nslot, int E, int k, int* seg_off
 bool gateup_topk(int B, int E);
 hipError_t launch_gateup_dec(const ExpertArgs& a, hipStream_t st);
 hipError_t launch_down_comb(const ExpertArgs& a, hipStream_t st);
-
-// ---- small-batch decode path (jm_front.hip): B * topk <= JM_FRONT_SLOTS
-
-#define JM_FRONT_SLOTS 64
-// Front kernel: [router waves ->] top-k -> gate/up, one persistent block of
-// 8 waves per CU.  With the router inside (wt != NULL), wave 0 of block g <
-// ceil(E/8) * B computes one expert group's scores for one token and
-// publishes them as tagged 64-bit words; otherwise the scores and the token
-// digits come from the router kernel (logits_in, xdig, xscale).
-struct FrontArgs {
-    const void* wt;           // interleaved router copy of the layer (router inside), or NULL
-    int wt_bf16;
-    const float* x;           // [B][d] (router inside)
-    const float* logits_in;   // [B][E] router scores (router outside)
-    const uint32_t* xdig;     // [B][d/G][NDIG][G/8] token digits (router outside)
-    const float* xscale;      // [B][d/G]
-    float* logits;            // [B][E] the scores the router waves computed (router inside)
-    unsigned long long* ll;   // [B][E] tagged scores: bits | tag << 32 (router inside)
-    unsigned* sync;           // [0] call counter (this call's tag is sync[0] + 1), [1] spin time-outs
-    int B, E, d, m, topk, renorm, group;
-    const uint8_t* blob;
-    RecLoc rec;
-    long long key0;
-    int* top;                 // [B*k] the top-k table (written by block 0)
-    float* tw;                // [B*k]
-    float* act;               // [B*k][m]
-    uint32_t* adig;           // [B*k][4][m/32][4] act digits: 8-value groups 4 col + j at [j][col], one word per digit plane
-    uint16_t* ascale;         // [B*k][m/32][4] bf16 scale of each 8-value group
-};
-// Down + combine of the small-batch path: block c owns hidden rows 8c..8c+7
-// of every token; every routed expert's rows are requested at once and the
-// act digits of every slot are copied into LDS beside them.
-struct DownArgs {
-    const uint8_t* blob;
-    RecLoc rec;
-    long long key0;
-    const int* top;           // [B*k] (written by the front kernel)
-    const float* tw;
-    int B, E, d, m, topk, group;
-    const uint32_t* adig;     // the front kernel's act digits and scales
-    const uint16_t* ascale;
-    float* out;               // [B][d]
-    const float* resid;       // [B][d] added to the block output (NULL: none); may alias out
-    unsigned* sync;           // sync[0] advanced by one (the front kernel's next tag)
-};
-// The shapes the small-batch path takes (otherwise the three-launch decode
-// path runs): B * topk <= JM_FRONT_SLOTS, d 1024 or 2048, intermediate a
-// multiple of 32 up to 1024 whose act digits of every slot fit the LDS, at
-// most 256 experts, group 32 or 64.
-bool front_ok(int B, int E, int d, int m, int topk, int group, int n_cu, int lds_max);
-// the router inside the front kernel: one router wave per block
-bool front_router_ok(int B, int E, int n_cu);
-hipError_t launch_front(const FrontArgs& a, int n_cu, int lds_max, hipStream_t st);
-hipError_t launch_down_lds(const DownArgs& a, int n_cu, int lds_max, hipStream_t st);
-
-// ---- small-batch gate/up on the matrix cores (jm_gumx.hip): B <= 8 tokens
-// Top-k of every token in every block, then items (routed expert, 32
-// intermediate rows) per block, the block's 8 waves splitting the hidden
-// columns, on v_mfma_i32_32x32x32_i8 against the tokens' int8 digit pairs
-// (the router kernel's xqh/xql/xqs/xqc).  Writes the top-k table (block 0),
-// act and its digits in the decode path's format (32 values per scale), for
-// k_down_comb.
-struct GuMxArgs {
-    const float* logits;      // [B][E] router scores
-    const int8_t* xqh;        // [B][d] token digit pairs in int8 operand order
-    const int8_t* xql;
-    const float* xqs;         // [B][d/G] their scales
-    const int* xqc;           // [B][d/G] sums of their integers 256 h + l per group
-    int B, E, d, m, topk, renorm, group;
-    const uint8_t* blob;
-    RecLoc rec;
-    long long key0;
-    int* top;                 // [B*k] the top-k table (written by block 0)
-    float* tw;                // [B*k]
-    float* act;               // [B*k][m]
-    uint32_t* adig;           // [B*k][m/32][NDIG][4] act digits (ExpertArgs::adig)
-    float* ascale;            // [B*k][m/32]
-};
-// B <= 8, B * topk <= 64, d 1024 or 2048, intermediate a multiple of 32,
-// at most 256 experts, group 32 or 64; the records' scales 16-byte aligned
-// (checked by the caller)
-bool gu_mx_ok(int B, int E, int d, int m, int topk, int group);
-hipError_t launch_gu_mx(const GuMxArgs& a, int n_cu, hipStream_t st);
 // dispatch path: gate/up and down over the work table, then the combine
 hipError_t launch_gateup(const ExpertArgs& a, int umax, hipStream_t st);
 hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st);

@@ -14,9 +14,6 @@ namespace jm {
 // The MoE block's workspace for B tokens: one device region, each field
 // 256-byte aligned, in this order (ws_layout).
 struct Ws {
-    unsigned* sync;             // 256 bytes at the start of the region: [0] the front kernel's call
-                                // counter, [1] its spin time-outs (the same place for every B)
-    unsigned long long* ll;     // [B][E] tagged router scores of the front kernel
     float* logits;              // [B][E]
     int* top;                   // [B*k]
     float* tw;                  // [B*k]
@@ -34,8 +31,7 @@ struct Ws {
     int* small;                 // [E] work-table entries of the experts under dense_min
     float* act;                 // [B*k][m]
     uint32_t* adig;             // [B*k][m/8][NDIG] act digits
-    float* ascale;              // [B*k][m/8] bytes x 4: [m/32] float (32-value groups) or [m/8] bf16
-                                // (the small-batch path's 8-value groups)
+    float* ascale;              // [B*k][m/32]
     float* y;                   // [B*k][d]
     int8_t* aqh;                // [B*k][m] act as int8 digit pairs for the MFMA down
     int8_t* aql;
@@ -94,10 +90,6 @@ struct jm_store {
     int prof;
     hipEvent_t ev[JM_STAGES + 1];
     int dense_min;              // segment size from which an expert takes the MFMA branch
-    int small_path;             // jm_store_set_small_path: 0 off, 1 front kernel after the router
-                                // kernel, 2 router inside the front kernel where it applies, 3 the
-                                // MFMA gate/up kernel (B <= 8)
-    bool sc16;                  // every record's scales start 16-byte aligned
     bool mfma_ok;               // the shape and the records' alignment allow the MFMA branch
     // ---- batch decode (jm_decode_layers_batch) ----
     int max_layers;             // jm_store_set_max_layers: < 0 runs every layer

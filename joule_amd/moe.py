@@ -145,21 +145,6 @@ class HbmExpertStore:
         with more than 256 slots); 0 restores the default."""
         _lib.check(_lib.lib().jm_store_set_dense_min(self._h, int(min_tokens)), "jm_store_set_dense_min")
 
-    def set_small_path(self, mode: int) -> None:
-        """Batches of up to 64 slots: 2 front kernel with the router inside
-        where it applies, 1 front kernel after the router kernel, 0 (default)
-        the three-launch decode path, 3 the same with the gate/up on the
-        matrix cores (B <= 8)."""
-        _lib.check(_lib.lib().jm_store_set_small_path(self._h, int(mode)), "jm_store_set_small_path")
-
-    def sync_words(self, stream=None) -> tuple[int, int]:
-        """(call counter, polls that ran out) of the small-batch front kernel."""
-        t = torch.zeros(2, dtype=torch.int32, device=self.blob.device)
-        _lib.check(_lib.lib().jm_store_copy_workspace(self._h, _lib.WS_SYNC, _lib.ptr(t), 8,
-                                                      _lib.stream_handle(stream)), "jm_store_copy_workspace")
-        v = t.cpu().tolist()
-        return int(v[0]) & 0xFFFFFFFF, int(v[1]) & 0xFFFFFFFF
-
     def dense_tiles(self, stream=None) -> int:
         """32-token tiles the MFMA branch computed in the last call."""
         t = torch.zeros(1, dtype=torch.int32, device=self.blob.device)
