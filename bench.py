@@ -16,7 +16,10 @@ Reported (one JSON line):
                dominant_kernel, the same ratio for the gate/up expert kernel
                (the largest): its routed gate+up records / its average
                duration, measured with HIP events on the stream the kernels
-               run on.  traffic: HBM bytes per call from rocprofv3 counters
+               run on.  traffic: HBM bytes per call from two rocprofv3
+               counter runs of this workload that the script starts before it
+               touches the GPU (traffic_counters: per-kernel KiB, calibration
+               and the ratio to the algorithmic bytes)
   stages       average milliseconds of each kernel
   router_margins  per token and layer, (p8 - p9) / p8 of the router softmax
                (how far each selection is from a tie)
@@ -26,6 +29,16 @@ Reported (one JSON line):
                full 48-layer Qwen3-30B-A3B decode step at B=8 (attention over
                2049 cached positions + the MoE block per layer), with the MoE
                share of the step isolated
+  per_call_us  median, p10 and p90 of the per-call times (events between
+               consecutive calls), for the headline and each sweep config
+  parity       for the headline and every MoE config of the sweep, the timed
+               workload against the oracle (oracle/): block outputs of every
+               rotated layer (the Zipf block: layer 0), normwise per token
+               max|gpu - oracle| / max|oracle| (the 1e-3 bar) and the
+               elementwise p99 of |gpu - oracle| / |oracle| over outputs with
+               |oracle| >= 1e-3 of the token's largest; router indices and
+               weights compared bit for bit on every layer.  A config over the
+               bar or with a routing mismatch makes the run exit non-zero.
   cpu_baseline the C restatement of the reference block (oracle/) on this
                host's cores as the reference runs it (inline at B=1, 8 pool
                workers + the caller above; batches in chunks of 16 tokens),
@@ -50,22 +63,137 @@ PEAK_HBM_GBS = 8000.0
 PEAK_MFMA_I8_TOPS = 5000.0     # dense int8 MFMA (the dense branch's operands)
 ZIPF_ALPHA = 0.28              # Zipf(1.1) bias strength: per-expert counts about 5..200 over 512 tokens
 
-# HBM traffic of the block's kernels on the default workload (B=8, group 64,
-# 16 rotating layers), measured by two rocprofv3 --pmc runs of this script
-# (FETCH_SIZE, then WRITE_SIZE; --steps 48 --warmup 16 --calib-copy-mib 256),
-# KiB per dispatch averaged over every dispatch of each kernel.  Each counter
-# is scaled by what it reads for the 256 MiB copy in the same run:
-# FETCH_SIZE reports half of the copied bytes (factor 2.0), WRITE_SIZE all of
-# them (factor 1.0).
-BLOCK_PMC = {"batch": 8, "group": 64, "layers": 16,
-             "fetch_kib": {"k_router_grp": 573.0, "k_topk": 27.5, "k_gateup": 42110.5, "k_down_comb": 21816.4},
-             "write_kib": {"k_router_grp": 44.0, "k_topk": 0.5, "k_gateup": 338.9, "k_down_comb": 64.0},
-             "fetch_factor": 2.0, "write_factor": 1.0,
-             "source": "profiles/pmc_traffic_qwen3_b8.md"}
+# HBM traffic of the block's kernels: two rocprofv3 --pmc runs of this
+# script on the default workload (FETCH_SIZE, then WRITE_SIZE; KiB per
+# dispatch, averaged over every dispatch of each kernel), started before this
+# process touches the GPU (measure_traffic).  Each counter is scaled by what
+# it reads for a 256 MiB copy in the same run (FETCH_SIZE counts half of the
+# copied bytes, WRITE_SIZE all of them on MI355X).
+TRAFFIC_KERNELS = ("k_router_grp", "k_topk", "k_gateup", "k_down_comb")
+TRAFFIC_ARGS = ["--no-sweep", "--cpu-seconds", "0", "--steps", "48", "--warmup", "16", "--calib-copy-mib", "256",
+                "--no-traffic", "--no-parity"]
+PARITY_TOL = 1e-3
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def measure_traffic(batch: int, group: int, layers: int) -> dict:
+    """HBM bytes per launch of the block's kernels, from two rocprofv3 --pmc
+    runs of this script (one counter each) on the same workload with
+    --calib-copy-mib 256.  Runs before this process initialises the GPU;
+    returns the per-kernel KiB, the calibration factors and the scaled bytes,
+    or the reason it could not."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    from collections import defaultdict
+
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return {"error": "rocprofv3 not found"}
+    tmp = tempfile.gettempdir()
+    tail = [sys.executable, str(ROOT / "bench.py"), *TRAFFIC_ARGS, "--batch", str(batch), "--group", str(group),
+            "--layers", str(layers)]
+    kib, factor = {}, {}
+    calib_kib = 256 * 1024.0
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="jm_pmc_", dir=tmp)
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "run", "--", *tail]
+        log(f"traffic: {counter} run ({' '.join(cmd[:4])} ... -- bench.py {' '.join(TRAFFIC_ARGS[:6])} ...)")
+        try:
+            r = subprocess.run(cmd, cwd=tmp, env={**os.environ, "TMPDIR": tmp}, stdout=subprocess.DEVNULL,
+                               stderr=subprocess.PIPE, timeout=240)
+            rc = r.returncode
+        except subprocess.TimeoutExpired:
+            shutil.rmtree(d, ignore_errors=True)
+            return {"error": f"{counter} run timed out"}
+        files = sorted(Path(d).rglob("*counter_collection.csv"))
+        if not files:
+            shutil.rmtree(d, ignore_errors=True)
+            return {"error": f"{counter} run wrote no counter file (exit {rc})"}
+        vals = defaultdict(list)
+        with open(files[0]) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                vals[row["Kernel_Name"]].append(float(row["Counter_Value"]))
+        shutil.rmtree(d, ignore_errors=True)
+        per = {}
+        for k in TRAFFIC_KERNELS:
+            v = [x for name, xs in vals.items() if k + "<" in name or name.endswith(k) for x in xs]
+            per[k] = sum(v) / len(v) if v else None
+        cp = [x for name, xs in vals.items() if "copyBuffer" in name for x in xs if x > 0.25 * calib_kib]
+        if not cp or any(per[k] is None for k in TRAFFIC_KERNELS):
+            return {"error": f"{counter}: kernels or the calibration copy missing from the counter file"}
+        kib[counter] = per
+        factor[counter] = calib_kib / (sum(cp) / len(cp))
+        log(f"traffic: {counter} KiB per dispatch {per}, calibration factor {factor[counter]:.3f} (exit {rc})")
+    scaled = {k: 1024.0 * (kib["FETCH_SIZE"][k] * factor["FETCH_SIZE"] + kib["WRITE_SIZE"][k] * factor["WRITE_SIZE"])
+              for k in TRAFFIC_KERNELS}
+    return {"fetch_kib": kib["FETCH_SIZE"], "write_kib": kib["WRITE_SIZE"],
+            "fetch_factor": factor["FETCH_SIZE"], "write_factor": factor["WRITE_SIZE"],
+            "bytes": scaled, "block_bytes": sum(scaled.values()),
+            "command": f"rocprofv3 --pmc <FETCH_SIZE|WRITE_SIZE> --output-format csv -d <dir> -o run -- "
+                       f"python3 bench.py {' '.join(TRAFFIC_ARGS)} --batch {batch} --group {group} --layers {layers}"}
+
+
+def percentiles_us(times_ms) -> dict:
+    import numpy as np
+
+    t = np.asarray(times_ms, dtype=np.float64) * 1e3
+    return {"median": float(np.median(t)), "p10": float(np.percentile(t, 10)), "p90": float(np.percentile(t, 90)),
+            "calls": int(t.size)}
+
+
+def normwise(out, ref) -> float:
+    """max over tokens of max_i |out - ref| / max_i |ref| (the 1e-3 bar)."""
+    import numpy as np
+
+    den = np.abs(ref).max(axis=1)
+    num = np.abs(out.astype(np.float64) - ref.astype(np.float64)).max(axis=1)
+    return float(np.max(num / np.where(den > 0, den, 1.0)))
+
+
+def elementwise_p99(out, ref) -> float:
+    """p99 of |out - ref| / |ref| over the outputs with |ref| >= 1e-3 of the
+    token's largest."""
+    import numpy as np
+
+    big = np.abs(ref) >= 1e-3 * np.abs(ref).max(axis=1, keepdims=True)
+    rel = np.abs(out.astype(np.float64) - ref)[big] / np.abs(ref)[big]
+    return float(np.percentile(rel, 99)) if rel.size else 0.0
+
+
+def block_parity(store, moes, x_np, layers) -> dict:
+    """The timed workload against the oracle: block outputs, router indices
+    and weights of each layer in `layers` for the tokens x_np."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    B, k = x_np.shape[0], store.shape.topk
+    x = torch.from_numpy(x_np).cuda()
+    out = torch.empty_like(x)
+    top = torch.empty((B, k), dtype=torch.int32, device="cuda")
+    tw = torch.empty((B, k), dtype=torch.float32, device="cuda")
+    threads = min(9, max(1, O.cpu_count()))
+    nerr, p99, top_ok, tw_ok = 0.0, 0.0, 0, 0
+    for l in layers:
+        store.layer_ffn_batch(l, x, out, topk_idx=top, topk_w=tw)
+        o, t, w = out.cpu().numpy(), top.cpu().numpy(), tw.cpu().numpy()
+        ro, rt, rw = moes[l].forward(x_np, n_threads=threads)
+        top_ok += int(np.array_equal(t, rt))
+        tw_ok += int(np.array_equal(w.view(np.uint32), rw.view(np.uint32)))
+        nerr = max(nerr, normwise(o, ro))
+        p99 = max(p99, elementwise_p99(o, ro))
+    n = len(layers)
+    return {"layers_checked": n, "normwise_max": nerr, "elementwise_p99_max": p99,
+            "topk_bitexact_layers": top_ok, "weights_bitexact_layers": tw_ok,
+            "ok": bool(nerr <= PARITY_TOL and top_ok == n and tw_ok == n)}
 
 
 def build_layers(shape, n_layers, group, seed):
@@ -100,7 +228,8 @@ def routed_experts(store, n_layers, x):
 
 
 def measure(store, gw, x, steps, warmup, n_layers, stage_steps=None):
-    """(ms_per_step, per-stage ms averages, routed experts per layer)."""
+    """(ms_per_step, per-stage ms averages, routed experts per layer,
+    per-call time percentiles)."""
     import torch
 
     from joule_amd._lib import STAGES
@@ -118,6 +247,14 @@ def measure(store, gw, x, steps, warmup, n_layers, stage_steps=None):
     e1.record(st)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    # the per-call distribution: the same calls with an event between each two
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    evs[0].record(st)
+    for i in range(steps):
+        store.layer_ffn_batch(i % n_layers, x, out)
+        evs[i + 1].record(st)
+    torch.cuda.synchronize()
+    dist = percentiles_us([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)])
     # per-kernel durations: same calls with an event before/after each kernel
     store.profile(True)
     acc = {k: 0.0 for k in STAGES}
@@ -129,7 +266,7 @@ def measure(store, gw, x, steps, warmup, n_layers, stage_steps=None):
     store.profile(False)
     stages = {k: v / ns for k, v in acc.items()}
     U = routed_experts(store, n_layers, x)
-    return ms, stages, U
+    return ms, stages, U, dist
 
 
 def block_numbers(shape, group, B, ms, stages, U, steps, n_layers, router_bytes=4):
@@ -159,11 +296,12 @@ def block_numbers(shape, group, B, ms, stages, U, steps, n_layers, router_bytes=
     }
 
 
-def zipf_block(store, gw, steps, n_layers, bz=512):
+def zipf_block(store, gw, steps, n_layers, bz=512, check=True):
     """The prefill-style Qwen3 block: bz tokens with Zipf(1.1)-biased routing
     (per-expert counts about 5..200 at bz = 512); the experts with at least
-    dense_min (8) slots take the MFMA branch.  Returns (results, biased
-    router table, biased x)."""
+    dense_min (8) slots take the MFMA branch.  With check, layer 0's block
+    is compared with the oracle.  Returns (results, biased router table,
+    biased x)."""
     import numpy as np
     import torch
 
@@ -178,7 +316,7 @@ def zipf_block(store, gw, steps, n_layers, bz=512):
     xz = torch.from_numpy(xz_np).cuda()
     store.set_router(torch.from_numpy(gz).cuda())
     nz = max(steps // 2, 100)
-    m2, st2, U2 = measure(store, gz, xz, nz, 10, n_layers, stage_steps=min(nz, 50))
+    m2, st2, U2, dist = measure(store, gz, xz, nz, 10, n_layers, stage_steps=min(nz, 50))
     r = block_numbers(shape, G, bz, m2, st2, U2, nz, n_layers, rb)
     top = torch.empty((bz, shape.topk), dtype=torch.int32, device="cuda")
     store.layer_ffn_batch(0, xz, topk_idx=top)
@@ -191,8 +329,11 @@ def zipf_block(store, gw, steps, n_layers, bz=512):
         "mfma_frac_of_int8_peak": flops / (m2 * 1e-3) / 1e12 / PEAK_MFMA_I8_TOPS,
         "zipf_alpha": ZIPF_ALPHA, "count_max": int(counts.max()), "count_min": int(counts.min()),
         "dense_experts": int((counts >= 8).sum()), "dense_tiles": tiles,
-        "stages_ms": st2,
+        "stages_ms": st2, "per_call_us": dist,
     }
+    if check:
+        res["parity"] = block_parity(store, oracle_moes(store, gz, 1), xz_np, [0])
+        log(f"parity qwen3 zipf B={bz}: {res['parity']}")
     log(f"sweep qwen3 zipf B={bz}: {r['tok_per_s']:.0f} tok/s, {m2 * 1e3:.1f} us/step, "
         f"{flops / (m2 * 1e-3) / 1e12:.1f} TFLOP/s, counts {counts.min()}..{counts.max()}, "
         f"dense tiles {tiles}, stages {st2}")
@@ -361,6 +502,13 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176, 
     host_ms = (time.perf_counter() - t0) * 1e3 / steps      # enqueue time per step
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    evs[0].record(st)
+    for i in range(steps):
+        dec.decode_layers_batch(x, pos, kv, hid)
+        evs[i + 1].record(st)
+    torch.cuda.synchronize()
+    dist = percentiles_us([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)])
     # attention / MoE split (events at every layer's boundaries)
     store.profile(True)
     split = {"attention": 0.0, "moe": 0.0, "total": 0.0}
@@ -441,7 +589,7 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176, 
     b1_ms = e0.elapsed_time(e1) / steps
     del kvp
     res = {
-        "tok_per_s": B / (ms * 1e-3), "ms_per_step": ms, "host_enqueue_ms_per_step": host_ms,
+        "tok_per_s": B / (ms * 1e-3), "ms_per_step": ms, "per_step_us": dist, "host_enqueue_ms_per_step": host_ms,
         "layers": n_layers, "batch": B, "position": position, "kv_cache": "f32" if kv_f32 else "bf16",
         "attention_ms_profiled": split["attention"], "moe_ms_profiled": split["moe"],
         "step_ms_profiled": split["total"],
@@ -683,6 +831,10 @@ def main() -> int:
                     help="only the plugin product HipBackend.q4_gemm at T = 1, 32, 33, 36, 512; prints its JSON")
     ap.add_argument("--probe", action="store_true",
                     help="only the launch and hand-off cost probes (libjoule_probe.so); prints their JSON")
+    ap.add_argument("--no-parity", action="store_true",
+                    help="skip the comparison of the timed workload with the oracle")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc runs that measure roofline.traffic")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after timing, run 8 torch copies of this many MiB (a known-size kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -693,6 +845,13 @@ def main() -> int:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
               f"(--gpus {args.gpus}, WORLD_SIZE {world}); run with --gpus 1.", file=sys.stderr)
         return 2
+
+    # the counter runs first, while this process has not touched the GPU
+    only = (args.probe or args.decode_only or args.prefill_only or args.dense_only or args.plugin_only
+            or args.zipf_only)
+    traffic = None
+    if not only and not args.no_traffic:
+        traffic = measure_traffic(args.batch, args.group, args.layers)
 
     import numpy as np
     import torch
@@ -727,16 +886,20 @@ def main() -> int:
     log(f"building {NL} Qwen3-shaped layers (G={G}) on the GPU")
     store, gw = build_layers(shape, NL, G, seed=1000)
     if args.zipf_only:
-        print(json.dumps({"qwen3_zipf512": zipf_block(store, gw, args.steps, NL)[0]}), flush=True)
+        print(json.dumps({"qwen3_zipf512": zipf_block(store, gw, args.steps, NL, check=not args.no_parity)[0]}),
+              flush=True)
         return 0
     x_np = activations(B, shape.d)
     x = torch.from_numpy(x_np).cuda()
     log(f"timing B={B}: {args.warmup} warm-up + {args.steps} steps")
-    ms, stages, U = measure(store, gw, x, args.steps, args.warmup, NL)
+    ms, stages, U, dist = measure(store, gw, x, args.steps, args.warmup, NL)
     rb = store.router_bytes_per_weight()
     main_res = block_numbers(shape, G, B, ms, stages, U, args.steps, NL, rb)
     log(f"B={B}: {main_res['tok_per_s']:.0f} tok/s, {ms * 1e3:.1f} us/step, block "
-        f"{main_res['block_GBs']:.0f} GB/s, gate/up {main_res['gateup_GBs']:.0f} GB/s, stages {stages}")
+        f"{main_res['block_GBs']:.0f} GB/s, gate/up {main_res['gateup_GBs']:.0f} GB/s, stages {stages}, "
+        f"per call {dist}")
+    check = not args.no_parity
+    parity = {}
 
     if args.calib_copy_mib > 0:
         n = args.calib_copy_mib * (1 << 20) // 4
@@ -758,22 +921,32 @@ def main() -> int:
     gpu_top0 = torch.empty((B, shape.topk), dtype=torch.int32, device="cuda")
     store.layer_ffn_batch(0, x, topk_idx=gpu_top0)
     gpu_top0 = gpu_top0.cpu().numpy()
-    moes = oracle_moes(store, gw, NL) if cpu_on else None
+    moes = oracle_moes(store, gw, NL) if (cpu_on or check) else None
+    if check:
+        parity[f"qwen3_B{B}"] = block_parity(store, moes, x_np, list(range(NL)))
+        log(f"parity qwen3 B={B}: {parity[f'qwen3_B{B}']}")
     xs = {}
     if not args.no_sweep:
         for b in (1, 32):
             xs[b] = activations(b, shape.d)
             xb = torch.from_numpy(xs[b]).cuda()
-            m2, st2, U2 = measure(store, gw, xb, max(args.steps // 2, 50), 10, NL)
+            m2, st2, U2, d2 = measure(store, gw, xb, max(args.steps // 2, 50), 10, NL)
             r = block_numbers(shape, G, b, m2, st2, U2, max(args.steps // 2, 50), NL, rb)
             sweep[f"qwen3_B{b}"] = {k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac",
                                                       "gateup_GBs", "experts_routed_avg")}
-            log(f"sweep qwen3 B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s")
+            sweep[f"qwen3_B{b}"]["per_call_us"] = d2
+            log(f"sweep qwen3 B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s, per call {d2}")
+            if check:
+                sweep[f"qwen3_B{b}"]["parity"] = parity[f"qwen3_B{b}"] = block_parity(store, moes, xs[b],
+                                                                                     list(range(NL)))
+                log(f"parity qwen3 B={b}: {parity[f'qwen3_B{b}']}")
             if cpu_on:
                 cpu_sweep[f"qwen3_B{b}"] = cpu_case(moes, xs[b], cpu_share, f"qwen3 B={b}")[0]
 
     if not args.no_sweep:
-        sweep["qwen3_zipf512"], gz, xz_np = zipf_block(store, gw, args.steps, NL)
+        sweep["qwen3_zipf512"], gz, xz_np = zipf_block(store, gw, args.steps, NL, check=check)
+        if check:
+            parity["qwen3_zipf512"] = sweep["qwen3_zipf512"]["parity"]
         if cpu_on:
             zmoes = oracle_moes(store, gz, 1)
             cpu_sweep["qwen3_zipf512"] = cpu_case(zmoes, xz_np, cpu_share, "qwen3 zipf B=512", min_calls=1)[0]
@@ -791,16 +964,21 @@ def main() -> int:
         del store
         torch.cuda.empty_cache()
         ostore, ogw = build_layers(OLMOE, NL, G, seed=1000)
-        omoes = oracle_moes(ostore, ogw, NL) if cpu_on else None
+        omoes = oracle_moes(ostore, ogw, NL) if (cpu_on or check) else None
         for b in (1, 8):
             xo_np = activations(b, OLMOE.d)
             xb = torch.from_numpy(xo_np).cuda()
-            m2, st2, U2 = measure(ostore, ogw, xb, max(args.steps // 2, 50), 10, NL)
+            m2, st2, U2, d2 = measure(ostore, ogw, xb, max(args.steps // 2, 50), 10, NL)
             r = block_numbers(OLMOE, G, b, m2, st2, U2, max(args.steps // 2, 50), NL,
                               ostore.router_bytes_per_weight())
             sweep[f"olmoe_B{b}"] = {k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac",
                                                       "gateup_GBs", "experts_routed_avg")}
-            log(f"sweep olmoe B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s")
+            sweep[f"olmoe_B{b}"]["per_call_us"] = d2
+            log(f"sweep olmoe B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s, per call {d2}")
+            if check:
+                sweep[f"olmoe_B{b}"]["parity"] = parity[f"olmoe_B{b}"] = block_parity(ostore, omoes, xo_np,
+                                                                                     list(range(NL)))
+                log(f"parity olmoe B={b}: {parity[f'olmoe_B{b}']}")
             if cpu_on:
                 cpu_sweep[f"olmoe_B{b}"] = cpu_case(omoes, xo_np, cpu_share, f"olmoe B={b}")[0]
         del omoes
@@ -820,11 +998,16 @@ def main() -> int:
 
     gu_ms = stages["gateup"]
     gate_traffic = block_traffic = None
-    if (B, G, NL) == (BLOCK_PMC["batch"], BLOCK_PMC["group"], BLOCK_PMC["layers"]):
-        kib = {k: BLOCK_PMC["fetch_kib"][k] * BLOCK_PMC["fetch_factor"]
-               + BLOCK_PMC["write_kib"][k] * BLOCK_PMC["write_factor"] for k in BLOCK_PMC["fetch_kib"]}
-        gate_traffic = 1024.0 * kib["k_gateup"]
-        block_traffic = 1024.0 * sum(kib.values())
+    if traffic and "block_bytes" in traffic:
+        gate_traffic = traffic["bytes"]["k_gateup"]
+        block_traffic = traffic["block_bytes"]
+        traffic["ratio_to_algorithmic"] = {
+            "k_gateup": gate_traffic / main_res["gateup_bytes"],
+            "k_down_comb": traffic["bytes"]["k_down_comb"] / main_res["down_bytes"],
+            "block": block_traffic / main_res["bytes_alg"]}
+        log(f"traffic: block {block_traffic / 1e6:.2f} MB per call against {main_res['bytes_alg'] / 1e6:.2f} MB "
+            f"algorithmic, ratios {traffic['ratio_to_algorithmic']}")
+    parity_ok = all(v["ok"] for v in parity.values()) if parity else None
     res = {
         "metric": "MoE decode tok/s + achieved HBM GB/s, Qwen3-30B-A3B-shape Q4, B=1 and B=8",
         "value": main_res["tok_per_s"],
@@ -849,7 +1032,8 @@ def main() -> int:
                      "achieved": main_res["block_GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": main_res["block_frac"], "traffic": block_traffic,
                      "bytes_per_launch": main_res["bytes_alg"], "avg_launch_ms": ms,
-                     "traffic_source": BLOCK_PMC["source"] if block_traffic else None,
+                     "traffic_source": ("rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this workload before the "
+                                        "timing (traffic_counters)") if block_traffic else None,
                      "dominant_kernel": {"kernel": "k_gateup", "achieved": main_res["gateup_GBs"],
                                          "frac": main_res["gateup_GBs"] / PEAK_HBM_GBS,
                                          "traffic": gate_traffic, "bytes_per_launch": main_res["gateup_bytes"],
@@ -857,11 +1041,18 @@ def main() -> int:
         "block": {k: main_res[k] for k in ("bytes_alg", "block_GBs", "block_frac", "experts_routed_avg",
                                            "down_GBs")},
         "stages_ms": stages,
+        "per_call_us": dist,
+        "parity": {"ok": parity_ok, "bar_normwise": PARITY_TOL, "configs": parity} if parity else None,
+        "traffic_counters": traffic,
         "router_margins": margins,
         "sweep": sweep,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
+    if parity_ok is False:
+        bad = [k for k, v in parity.items() if not v["ok"]]
+        log(f"PARITY FAILURE against the oracle in {bad}: the numbers above are not valid")
+        return 1
     return 0
 
 
