@@ -624,30 +624,34 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176, 
     return res
 
 
-def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 32, 33, 36, 512), reps=200):
+def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 2, 4, 8, 12, 16, 20, 24, 28, 32, 33, 36, 48, 64, 512),
+                   reps=200):
     """The plugin product HipBackend.q4_gemm (jm_q4_gemm_f32, the reference's
     q4_gemm_f32) on one Qwen3 expert matrix shape (m=768 rows of d=2048),
-    at each token count: microseconds per call on the stream (inputs and the
-    packed matrix resident on the GPU; the workspace is cached after the
-    first call) and algorithmic bytes per call.  From 33 tokens the call
-    takes the matrix cores (int8 digit pairs); below, the v_dot8 digit
-    kernel."""
+    at each token count T: microseconds per call on the stream (inputs and
+    the packed matrix resident on the GPU; the workspace cached after the
+    first call) with the library's own choice of kernel, and with each of the
+    two kernels forced (the v_dot8 digit kernel, the int8 matrix cores), from
+    which the crossover is read.  At T = 1 the host-side time of a call
+    (enqueue and wait) is reported beside the GPU's."""
     import numpy as np
     import torch
 
+    from joule_amd import _lib
     from joule_amd import q4_store as q4
     from joule_amd.backend import HipBackend
 
+    L = _lib.lib()
     rng = np.random.default_rng(7)
     sb, pb = q4.quantize(rng.normal(0, 0.02, (m, d)).astype(np.float32), group)
     sc = torch.from_numpy(np.frombuffer(sb, np.uint16).copy().view(np.int16)).cuda()
     pk = torch.from_numpy(np.frombuffer(pb, np.uint8).copy()).cuda()
     be = HipBackend()
     st = torch.cuda.current_stream()
-    out = {}
-    for T in sizes:
-        X = torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).cuda()
-        y = torch.empty((T, m), dtype=torch.float32, device="cuda")
+    default_min = L.jm_get_q4_gemm_min_tokens()
+
+    def time_calls(y, X, min_t):
+        _lib.check(L.jm_set_q4_gemm_min_tokens(min_t), "jm_set_q4_gemm_min_tokens")
         for _ in range(5):
             be.q4_gemm(y, X, pk, sc, m, d, group)
         torch.cuda.synchronize()
@@ -657,13 +661,42 @@ def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 32, 33, 36, 512), reps=200):
             be.q4_gemm(y, X, pk, sc, m, d, group)
         e1.record(st)
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / reps
-        nbytes = m * d // 2 + m * (d // group) * 2 + T * d * 4 + T * m * 4
-        out[f"T{T}"] = {"us_per_call": us, "bytes": nbytes, "GBs": nbytes / (us * 1e-6) / 1e9,
-                        "path": "mfma_i8" if T >= 33 else "dot8_digits",
-                        "tflops_equiv": 2.0 * T * m * d / (us * 1e-6) / 1e12}
-        log(f"plugin q4_gemm m={m} d={d} T={T}: {us:.1f} us ({out[f'T{T}']['path']})")
-    return {"m": m, "d": d, "group": group, "sizes": out}
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    out = {}
+    try:
+        for T in sizes:
+            X = torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).cuda()
+            y = torch.empty((T, m), dtype=torch.float32, device="cuda")
+            dot8_us = time_calls(y, X, 1 << 30)
+            mfma_us = time_calls(y, X, 1)
+            us = time_calls(y, X, 0)
+            nbytes = m * d // 2 + m * (d // group) * 2 + T * d * 4 + T * m * 4
+            path = "mfma_i8" if T >= default_min else "dot8_digits"
+            out[f"T{T}"] = {"us_per_call": us, "bytes": nbytes, "GBs": nbytes / (us * 1e-6) / 1e9, "path": path,
+                            "dot8_us": dot8_us, "mfma_us": mfma_us,
+                            "tflops_equiv": 2.0 * T * m * d / (us * 1e-6) / 1e12}
+            log(f"plugin q4_gemm m={m} d={d} T={T}: {us:.1f} us ({path}); dot8 {dot8_us:.1f}, mfma {mfma_us:.1f}")
+            if T == 1:
+                # host-side: each call enqueued and waited for
+                hs = []
+                for _ in range(50):
+                    t0 = time.perf_counter()
+                    be.q4_gemm(y, X, pk, sc, m, d, group)
+                    torch.cuda.synchronize()
+                    hs.append((time.perf_counter() - t0) * 1e6)
+                out["T1"]["host_us_per_call_synced"] = float(np.median(hs))
+    finally:
+        L.jm_set_q4_gemm_min_tokens(0)
+    # the smallest T from which the matrix cores are no slower at every larger measured T
+    ts = [int(k[1:]) for k in out]
+    cross = None
+    for t in ts:
+        if all(out[f"T{u}"]["mfma_us"] <= out[f"T{u}"]["dot8_us"] for u in ts if u >= t):
+            cross = t
+            break
+    return {"m": m, "d": d, "group": group, "default_min_tokens": default_min, "measured_crossover_T": cross,
+            "sizes": out}
 
 
 def dense_step(B, steps, warmup, n_layers=36, position=2048, maxT=2176):

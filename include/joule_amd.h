@@ -420,9 +420,20 @@ int jm_q4_gemv_f32(float* out, const float* x, const uint8_t* packed, const uint
                    int m, int d, int group, void* stream);
 
 /* out[T][m] = X[T][d] . dequant(W[m][d])^T; argument order of q4_gemm_f32
- * (expert_ffn.c:201) plus the stream. */
+ * (expert_ffn.c:201) plus the stream.  From jm_get_q4_gemm_min_tokens()
+ * tokens the product runs on the int8 matrix cores (when m, d and group
+ * allow it and scales is 16-byte aligned), below on the v_dot8 digit
+ * kernel.  Workspace: one buffer per (device, stream), kept and grown; a
+ * call under stream capture takes a stream-ordered allocation instead. */
 int jm_q4_gemm_f32(float* out, const float* X, int T, const uint8_t* packed, const uint16_t* scales,
                    int m, int d, int group, void* stream);
+
+/* The token count from which jm_q4_gemm_f32 takes the matrix cores, for the
+ * whole process (0 restores the default, the measured crossover of the two
+ * kernels).  No counterpart in the reference (a switch between this build's
+ * kernels). */
+int jm_set_q4_gemm_min_tokens(int tokens);
+int jm_get_q4_gemm_min_tokens(void);
 
 #ifdef __cplusplus
 }

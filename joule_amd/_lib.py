@@ -56,6 +56,8 @@ SIGNATURES = {
     "jm_expert_job": ([_vp, _vp], _i),
     "jm_q4_gemv_f32": ([_vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
     "jm_q4_gemm_f32": ([_vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
+    "jm_set_q4_gemm_min_tokens": ([_i], _i),
+    "jm_get_q4_gemm_min_tokens": ([], _i),
 }
 
 

@@ -11,10 +11,12 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <vector>
 
+#include "jm_plugin_ws.h"
 #include "jm_store.h"
 
 namespace jm {
@@ -38,11 +40,9 @@ int hip_fail(hipError_t e, const char* what) {
 namespace {
 
 // Workspace of the plugin products (jm_q4_gemm_f32 / jm_q4_gemv_f32): one
-// buffer per (device, stream), grown on demand and kept until the process
-// ends.  Calls on one stream run in order, so they share it; a growth waits
-// for the stream before freeing the smaller buffer.  Under stream capture a
-// call whose buffer is too small takes a stream-ordered allocation instead
-// (freed after the call), since a capture cannot synchronise.
+// buffer per (device, stream), the policy of jm_plugin_ws.h (reuse, grow
+// with the old buffer retired, or a stream-ordered allocation under
+// capture, freed after the call).
 struct PluginWs {
     void* p = nullptr;
     bool async = false;
@@ -57,40 +57,44 @@ struct PluginBuf {
 
 std::mutex g_pws_mu;
 std::vector<PluginBuf> g_pws;
+std::vector<void*> g_pws_retired;           // replaced buffers, kept until the process ends
 
 int plugin_ws(hipStream_t st, size_t bytes, PluginWs* out) {
     int dev = 0;
     JM_HIP(hipGetDevice(&dev), "hipGetDevice");
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    JM_HIP(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
     std::lock_guard<std::mutex> lk(g_pws_mu);
     PluginBuf* b = nullptr;
     for (auto& x : g_pws)
         if (x.dev == dev && x.st == st) b = &x;
-    if (b && b->bytes >= bytes) {
-        out->p = b->p;
-        return 0;
+    switch (jm::plugin_ws_action(b ? b->bytes : 0, bytes, cs != hipStreamCaptureStatusNone)) {
+        case jm::WsAction::StreamOrdered:
+            JM_HIP(hipMallocAsync(&out->p, bytes, st), "hipMallocAsync plugin workspace");
+            out->async = true;
+            return 0;
+        case jm::WsAction::Reuse:
+            out->p = b->p;
+            return 0;
+        case jm::WsAction::Grow:
+            break;
     }
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    JM_HIP(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
-    if (cs != hipStreamCaptureStatusNone) {
-        JM_HIP(hipMallocAsync(&out->p, bytes, st), "hipMallocAsync plugin workspace");
-        out->async = true;
-        return 0;
-    }
+    const size_t grow = jm::plugin_ws_grow(b ? b->bytes : 0, bytes);
+    void* p = nullptr;
+    JM_HIP(hipMalloc(&p, grow), "hipMalloc plugin workspace");
     if (b) {
-        JM_HIP(hipStreamSynchronize(st), "hipStreamSynchronize before plugin workspace growth");
-        JM_HIP(hipFree(b->p), "hipFree plugin workspace");
-        b->p = nullptr;
-        b->bytes = 0;
+        if (b->p) g_pws_retired.push_back(b->p);
+        b->p = p;
+        b->bytes = grow;
     } else {
-        g_pws.push_back(PluginBuf{dev, st, nullptr, 0});
-        b = &g_pws.back();
+        g_pws.push_back(PluginBuf{dev, st, p, grow});
     }
-    const size_t grow = std::max(bytes, (size_t)1 << 20);
-    JM_HIP(hipMalloc(&b->p, grow), "hipMalloc plugin workspace");
-    b->bytes = grow;
-    out->p = b->p;
+    out->p = p;
     return 0;
 }
+
+// token count from which jm_q4_gemm_f32 takes the matrix cores
+std::atomic<int> g_q4_gemm_min_t{JM_Q4_GEMM_MIN_T};
 
 }  // namespace
 
@@ -735,8 +739,10 @@ int jm_q4_gemm_f32(float* out, const float* X, int T, const uint8_t* packed, con
     if (!aligned(packed, 16) || !aligned(X, 16)) return fail(JM_ERR_ARG, "packed and X must be 16-byte aligned");
     if (T == 0 || m == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    // from JM_GEMM_MIN_B tokens on the matrix cores (int8 digit pairs of X)
-    const bool mfma = T >= JM_GEMM_MIN_B && jm::q4_gemm_mfma_ok(m, d, group) && aligned(scales, 16);
+    // from jm_set_q4_gemm_min_tokens tokens on the matrix cores (int8 digit
+    // pairs of X)
+    const bool mfma = T >= g_q4_gemm_min_t.load(std::memory_order_relaxed) && jm::q4_gemm_mfma_ok(m, d, group) &&
+                      aligned(scales, 16);
     const size_t ng = (size_t)d / group;
     const size_t dig_bytes = align256((size_t)T * ng * JM_NDIG * (group / 8) * 4);
     const size_t sc_bytes = align256((size_t)T * ng * 4);
@@ -757,6 +763,14 @@ int jm_q4_gemm_f32(float* out, const float* X, int T, const uint8_t* packed, con
     if (f != hipSuccess) return hip_fail(f, "hipFreeAsync");
     return 0;
 }
+
+int jm_set_q4_gemm_min_tokens(int tokens) {
+    if (tokens < 0) return fail(JM_ERR_ARG, "tokens must be >= 0 (0 = default)");
+    g_q4_gemm_min_t.store(tokens == 0 ? JM_Q4_GEMM_MIN_T : tokens, std::memory_order_relaxed);
+    return 0;
+}
+
+int jm_get_q4_gemm_min_tokens(void) { return g_q4_gemm_min_t.load(std::memory_order_relaxed); }
 
 // ------------------------------------------------- block stages one by one
 

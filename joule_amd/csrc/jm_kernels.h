@@ -162,6 +162,11 @@ hipError_t launch_down_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st);
 // row's scales a multiple of 16 (G = 32) or 8 bytes (G = 64); ws holds
 // q4_gemm_mfma_ws bytes
 bool q4_gemm_mfma_ok(int m, int d, int group);
+// default token count from which jm_q4_gemm_f32 takes the matrix cores
+// (jm_set_q4_gemm_min_tokens changes it): the measured crossover
+#ifndef JM_Q4_GEMM_MIN_T
+#define JM_Q4_GEMM_MIN_T 22
+#endif
 size_t q4_gemm_mfma_ws(int T, int d, int group);
 hipError_t launch_q4_gemm_mfma(const uint8_t* packed, const uint16_t* scales, const float* X, int T, int m, int d,
                                int group, void* ws, float* out, hipStream_t st);

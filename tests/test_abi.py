@@ -140,3 +140,21 @@ def test_ctypes_argument_counts_match_the_header():
         params = params.strip()
         n = 0 if params in ("", "void") else params.count(",") + 1
         assert n == len(_lib.SIGNATURES[name][0]), (name, n, len(_lib.SIGNATURES[name][0]))
+
+
+def test_q4_gemm_min_tokens_setting():
+    """The plugin product's kernel threshold: process-wide, 0 restores the
+    default (the measured crossover, 22 tokens), negative is an error.  No
+    GPU work."""
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libjoule_amd.so not built")
+    L = _lib.lib()
+    assert L.jm_get_q4_gemm_min_tokens() == 22
+    try:
+        assert L.jm_set_q4_gemm_min_tokens(-1) == -1
+        assert L.jm_get_q4_gemm_min_tokens() == 22
+        assert L.jm_set_q4_gemm_min_tokens(5) == 0
+        assert L.jm_get_q4_gemm_min_tokens() == 5
+    finally:
+        assert L.jm_set_q4_gemm_min_tokens(0) == 0
+    assert L.jm_get_q4_gemm_min_tokens() == 22

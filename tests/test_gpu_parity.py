@@ -579,10 +579,11 @@ def test_block_empty_and_errors(qwen64):
 # ----------------------------------------------------------------- backend
 
 @pytest.mark.parametrize("group", [64, 32])
-@pytest.mark.parametrize("m,d,T", [(768, 2048, 1), (2048, 768, 3), (1024, 2048, 7),
-                                   # from 33 tokens the matrix cores (m a multiple of 256): whole and
-                                   # partial 32-token tiles, one and two 256-row passes per block
-                                   (768, 2048, 33), (2048, 768, 70), (8192, 512, 512),
+@pytest.mark.parametrize("m,d,T", [(768, 2048, 1), (2048, 768, 3), (1024, 2048, 7), (768, 2048, 21),
+                                   # from 22 tokens (the default crossover) the matrix cores (m a
+                                   # multiple of 256): whole and partial 32-token tiles, one and two
+                                   # 256-row passes per block
+                                   (768, 2048, 22), (768, 2048, 33), (2048, 768, 70), (8192, 512, 512),
                                    # shapes the matrix-core kernel does not take: the digit kernel
                                    (1000, 2048, 40), (768, 1536, 36)])
 def test_hip_backend_q4_gemm(gpu, oracle_lib, group, m, d, T):
@@ -601,3 +602,33 @@ def test_hip_backend_q4_gemm(gpu, oracle_lib, group, m, d, T):
     assert _rel(out.cpu().numpy(), ref) <= TOL
     v = be.q4_gemv(torch.from_numpy(X[0]).cuda(), pk, sc, m, d, group).cpu().numpy()
     assert _rel(v[None], ref[:1]) <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_q4_gemm_min_tokens_switch(gpu, oracle_lib, T):
+    """Both kernels of the plugin product forced at the same T (the switch
+    the bench's crossover sweep uses) agree with the oracle; 0 restores the
+    default threshold."""
+    banner(f"q4_gemm kernel switch T={T}")
+    L = _lib.lib()
+    m, d, group = 768, 2048, 64
+    rng = np.random.default_rng(90 + T)
+    sb, pb = Q.quantize(rng.normal(0, 0.02, (m, d)).astype(np.float32), group)
+    sc = np.frombuffer(sb, np.uint16).copy()
+    pk = np.frombuffer(pb, np.uint8).copy()
+    X = rng.standard_normal((T, d)).astype(np.float32)
+    ref = oracle_lib.q4_gemm_ffn(X, pk, sc, m, d, group)
+    be = HipBackend()
+    default = L.jm_get_q4_gemm_min_tokens()
+    try:
+        for min_t in (1, 1 << 30):
+            assert L.jm_set_q4_gemm_min_tokens(min_t) == 0
+            assert L.jm_get_q4_gemm_min_tokens() == min_t
+            out = torch.empty((T, m), dtype=torch.float32, device="cuda")
+            be.q4_gemm(out, torch.from_numpy(X).cuda(), pk, sc, m, d, group)
+            torch.cuda.synchronize()
+            assert _rel(out.cpu().numpy(), ref) <= TOL, min_t
+    finally:
+        assert L.jm_set_q4_gemm_min_tokens(0) == 0
+    assert L.jm_get_q4_gemm_min_tokens() == default
+    assert L.jm_set_q4_gemm_min_tokens(-1) == -1
