@@ -62,7 +62,12 @@ def decoder_shape(cfg: dict, max_tokens: int = 4096) -> tuple[DecoderShape, str]
                                      else None)
     rope_scaling: tuple = ()
     if rs:
-        rtype = rs.get("rope_type", rs.get("type", "default"))
+        if "type" in rs and "rope_type" not in rs:
+            # the older key: the reference's decoder reads rope_type only
+            # (decoder3.py:405-410) and would decode with unscaled tables;
+            # refuse rather than decode it differently from either reading
+            raise ValueError("rope_scaling uses the legacy key 'type'; rename it to 'rope_type'")
+        rtype = rs.get("rope_type", "default")
         if rtype == "llama3":
             rope_scaling = tuple(sorted((k, v) for k, v in rs.items() if isinstance(v, (int, float, str))))
         elif rtype != "default":

@@ -68,10 +68,11 @@ int decode_reserve(jm_store* s, int B, int S, int nqkv, int hq, int V) {
     // tokens, the GEMM's K slices (at most 4) from there
     const int gmax = B >= JM_GEMM_MIN_B ? 4 : 0;
     const size_t qkv_sl = (size_t)std::max(d / 512, gmax), op_sl = (size_t)std::max(hq / 512, gmax);
-    const size_t gu_rows = dense ? (size_t)std::max(jm::dense_gu_slices(d, 1) * std::min(B, JM_GEMM_MIN_B - 1),
-                                                    gmax * B) : 0;
-    const size_t dn_rows = dense ? (size_t)std::max(jm::dense_dn_slices(m, 1) * std::min(B, JM_GEMM_MIN_B - 1),
-                                                    gmax * B) : 0;
+    // (the dense FFN's products: the most slices over every batch up to B)
+    const size_t gu_rows = dense ? (size_t)std::max(jm::dense_gu_slices(d, m, 1) * std::min(B, JM_GEMM_MIN_B - 1),
+                                                    jm::dense_gu_slices(d, m, B) * B) : 0;
+    const size_t dn_rows = dense ? (size_t)std::max(jm::dense_dn_slices(d, m, 1) * std::min(B, JM_GEMM_MIN_B - 1),
+                                                    jm::dense_dn_slices(d, m, B) * B) : 0;
     const size_t sz[] = {
         (size_t)B * d * 4,                        // h
         (size_t)B * d * 4,                        // h2

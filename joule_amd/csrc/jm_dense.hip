@@ -76,37 +76,53 @@ k_swiglu_slices(const float* __restrict__ gu, int ns, const float* __restrict__ 
 
 bool dense_shape_ok(int d, int m) { return gemv_shape_ok(d) && m >= 512 && m % 512 == 0 && m <= JM_DENSE_MAX_M; }
 
-// the most slices the gate/up and down outputs hold at B tokens (the
-// GEMM's K slices from JM_GEMM_MIN_B tokens, at most 4)
-int dense_gu_slices(int d, int B) { return B >= JM_GEMM_MIN_B ? 4 : d / gemv_slice_cols(d); }
+// The two products' shapes, and whether launch_dense_ffn takes the GEMM
+// (from JM_GEMM_MIN_B tokens, when its shape allows) or the GEMV for them:
+// the workspace sizing and the launcher make the same decision here.
+static GemvArgs gu_shape(int d, int m, int B) {
+    GemvArgs g{};
+    g.rows[0] = m; g.rows[1] = m; g.rows[2] = 0;
+    g.K = d; g.N = 2 * m; g.B = B;
+    return g;
+}
 
-int dense_dn_slices(int m, int B) { return B >= JM_GEMM_MIN_B ? 4 : m / gemv_slice_cols(m); }
+static GemvArgs dn_shape(int d, int m, int B) {
+    GemvArgs o{};
+    o.rows[0] = d;
+    o.K = m; o.N = d; o.B = B;
+    return o;
+}
+
+static bool gu_gemm(int d, int m, int B) { return B >= JM_GEMM_MIN_B && gemm_shape_ok(gu_shape(d, m, B)); }
+static bool dn_gemm(int d, int m, int B) { return B >= JM_GEMM_MIN_B && gemm_shape_ok(dn_shape(d, m, B)); }
+
+// the most slices the gate/up and down outputs hold at B tokens (the
+// GEMM's K slices, at most 4, or the GEMV's K / slice columns)
+int dense_gu_slices(int d, int m, int B) { return gu_gemm(d, m, B) ? 4 : d / gemv_slice_cols(d); }
+
+int dense_dn_slices(int d, int m, int B) { return dn_gemm(d, m, B) ? 4 : m / gemv_slice_cols(m); }
 
 hipError_t launch_dense_ffn(const DenseFfn& f, hipStream_t st) {
     if (f.B == 0) return hipSuccess;
     if (!dense_shape_ok(f.d, f.m)) return hipErrorInvalidValue;
-    GemvArgs g{};
+    GemvArgs g = gu_shape(f.d, f.m, f.B);
     g.x = f.x;
     g.norm_w = f.norm_w;
     g.w[0] = f.w1; g.w[1] = f.w2; g.w[2] = nullptr;
-    g.rows[0] = f.m; g.rows[1] = f.m; g.rows[2] = 0;
-    g.K = f.d; g.N = 2 * f.m; g.B = f.B;
     g.part = f.gu;
     g.rss = f.norm_w ? f.rss : nullptr;
-    const bool gq = f.B >= JM_GEMM_MIN_B && gemm_shape_ok(g);
+    const bool gq = gu_gemm(f.d, f.m, f.B);
     hipError_t e = gq ? launch_gemm_bf16(g, st) : launch_gemv_part(g, st);
     if (e != hipSuccess) return e;
     const int ng = gq ? gemm_slices(g) : f.d / gemv_slice_cols(f.d);
     const dim3 ga((unsigned)((f.m / 4 + 255) / 256), (unsigned)f.B);
     hipLaunchKernelGGL(k_swiglu_slices, ga, dim3(256), 0, st, f.gu, ng, g.rss, ng, f.d, f.eps, f.B, f.m, f.act);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    GemvArgs o{};
+    GemvArgs o = dn_shape(f.d, f.m, f.B);
     o.x = f.act;
     o.w[0] = f.w3;
-    o.rows[0] = f.d;
-    o.K = f.m; o.N = f.d; o.B = f.B;
     o.part = f.dn;
-    const bool go = f.B >= JM_GEMM_MIN_B && gemm_shape_ok(o);
+    const bool go = dn_gemm(f.d, f.m, f.B);
     e = go ? launch_gemm_bf16(o, st) : launch_gemv_part(o, st);
     if (e != hipSuccess) return e;
     const int nd = go ? gemm_slices(o) : f.m / gemv_slice_cols(f.m);

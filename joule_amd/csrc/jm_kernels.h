@@ -277,8 +277,8 @@ struct DenseFfn {
 // d as the projections take it (a multiple of 1024 up to 8192), m a
 // multiple of 512 up to JM_DENSE_MAX_M
 bool dense_shape_ok(int d, int m);
-int dense_gu_slices(int d, int B);
-int dense_dn_slices(int m, int B);
+int dense_gu_slices(int d, int m, int B);
+int dense_dn_slices(int d, int m, int B);
 hipError_t launch_dense_ffn(const DenseFfn& f, hipStream_t st);
 // out [B][n] = resid (or 0) + the ns slices of part [ns][B][n], in order
 hipError_t launch_sum_slices(const float* resid, const float* part, int ns, int B, int n, float* out,

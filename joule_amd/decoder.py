@@ -100,9 +100,11 @@ def llama3_inv_freq(hd: int, theta: float, scaling: dict) -> np.ndarray:
     """Inverse frequencies of rope_type "llama3" (generic_streamer.py:21-39):
     the float32 base frequencies 1 / theta^(2i/hd), unchanged above the
     high-frequency wavelength bound, divided by `factor` below the
-    low-frequency one, and blended linearly in between; float32 out."""
-    inv = (np.float32(1.0) / (np.float32(theta) ** (np.arange(0, hd, 2, dtype=np.float32) / np.float32(hd))))
-    inv = inv.astype(np.float32)
+    low-frequency one, and blended linearly in between; float32 out.  The
+    base frequencies come from torch's float32 pow on the CPU, as the
+    reference computes them: numpy's float32 pow differs from it in the last
+    bit for some exponents."""
+    inv = (1.0 / (theta ** (torch.arange(0, hd, 2).float() / hd))).numpy().astype(np.float32)
     orig_max = float(scaling.get("original_max_position_tokens", 8192))
     factor = float(scaling.get("factor", 1.0))
     low_f = float(scaling.get("low_freq_factor", 1.0))

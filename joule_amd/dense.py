@@ -17,7 +17,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .moe import MoEShape
+from .moe import MoEShape, check_tensor
 
 
 def dense_ffn_shape(d: int, m: int) -> MoEShape:
@@ -59,14 +59,12 @@ class DenseFfnStore:
         if self.w is None:
             raise RuntimeError("FFN weights not set (set_weights)")
         d = self.shape.d
-        if (x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or x.dim() != 2
-                or x.shape[1] != d):
-            raise ValueError(f"x must be a contiguous float32 CUDA tensor [B, {d}]")
+        B = x.shape[0] if isinstance(x, torch.Tensor) and x.dim() == 2 else -1
+        check_tensor(x, "x", (B, d), torch.float32, self.blob.device)
         if out is None:
             out = torch.empty_like(x)
-        elif (out.dtype != torch.float32 or not out.is_cuda or not out.is_contiguous()
-              or tuple(out.shape) != tuple(x.shape) or out.device != x.device):
-            raise ValueError(f"out must be a contiguous float32 CUDA tensor [B, {d}] on x's device")
+        else:
+            check_tensor(out, "out", (B, d), torch.float32, self.blob.device)
         _lib.check(_lib.lib().jm_layer_ffn_batch(self._h, int(l), _lib.ptr(x), x.shape[0], _lib.ptr(out), None, None,
                                                  _lib.stream_handle(stream)), "jm_layer_ffn_batch")
         return out

@@ -54,6 +54,18 @@ OLMOE = MoEShape(d=2048, m=1024, E=64, topk=8, renorm=False, name="olmoe-1b-7b")
 QWEN3 = MoEShape(d=2048, m=768, E=128, topk=8, renorm=True, name="qwen3-30b-a3b")
 
 
+def check_tensor(t, name: str, shape: tuple, dtype, device) -> None:
+    """Raise ValueError unless t is a contiguous tensor of exactly this shape
+    and dtype on `device` (the kernels take raw pointers and sizes, so a
+    wrong shape would make them read or write past the tensor)."""
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if t.dtype != dtype or t.device != torch.device(device) or not t.is_contiguous() or tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must be a contiguous {dtype} tensor {list(shape)} on {device} "
+                         f"(got {t.dtype} {list(t.shape)} on {t.device}"
+                         f"{'' if t.is_contiguous() else ', not contiguous'})")
+
+
 def offsets_for_layout(shape: MoEShape, n_layers: int, group: int) -> tuple[np.ndarray, int]:
     """(offset table [3, L*E, 2], total bytes) of a store written in the
     reference order (layer, expert, part) with records [scales][packed]."""
@@ -192,20 +204,16 @@ class HbmExpertStore:
         """out[B, d] = MoE block of layer l on x[B, d] (float32, CUDA)."""
         if self.router is None:
             raise RuntimeError("router weights not set (set_router)")
-        B = x.shape[0] if x.dim() == 2 else -1
+        B = x.shape[0] if isinstance(x, torch.Tensor) and x.dim() == 2 else -1
         self._stage_in(x, "x", (B, self.shape.d), torch.float32)
         if out is None:
             out = torch.empty_like(x)
         else:
             self._stage_in(out, "out", (B, self.shape.d), torch.float32)
-        for t, dt in ((topk_idx, torch.int32), (topk_w, torch.float32)):
-            if t is not None and (t.dtype != dt or t.numel() != B * self.shape.topk or not t.is_contiguous()
-                                  or not t.is_cuda):
-                raise ValueError("topk outputs must be contiguous [B, topk] int32 / float32 CUDA tensors")
-            if t is not None and t.device != x.device:
-                raise ValueError("topk outputs must be on x's device")
-        if out.device != x.device:
-            raise ValueError("out must be on x's device")
+        if topk_idx is not None:
+            self._stage_in(topk_idx, "topk_idx", (B, self.shape.topk), torch.int32)
+        if topk_w is not None:
+            self._stage_in(topk_w, "topk_w", (B, self.shape.topk), torch.float32)
         _lib.check(_lib.lib().jm_layer_ffn_batch(self._h, int(l), _lib.ptr(x), B, _lib.ptr(out),
                                                  _lib.ptr(topk_idx), _lib.ptr(topk_w),
                                                  _lib.stream_handle(stream)), "jm_layer_ffn_batch")
@@ -214,8 +222,7 @@ class HbmExpertStore:
     # ------------------------------------------------ the block's stages
 
     def _stage_in(self, t: torch.Tensor, name: str, shape: tuple, dtype) -> None:
-        if (t.dtype != dtype or not t.is_cuda or not t.is_contiguous() or tuple(t.shape) != shape):
-            raise ValueError(f"{name} must be a contiguous {dtype} CUDA tensor {list(shape)}")
+        check_tensor(t, name, shape, dtype, self.blob.device)
 
     def expert_gateup(self, l: int, x: torch.Tensor, top: torch.Tensor, stream=None) -> torch.Tensor:
         """act[B * topk, m]: SwiGLU of each slot's expert's gate and up rows

@@ -61,6 +61,10 @@ def test_clip_qkv_and_unknown_rope_scaling_are_refused():
     assert s.rope_scaling == ()
     s, _ = decoder_shape(dict(QWEN3_30B, rope_parameters={"rope_type": "llama3", "factor": 8.0}))
     assert dict(s.rope_scaling)["rope_type"] == "llama3"
+    # the legacy key: the reference's decoder reads rope_type only and would
+    # decode unscaled, so it is refused rather than read either way
+    with pytest.raises(ValueError, match="legacy key 'type'"):
+        decoder_shape(dict(QWEN3_30B, rope_scaling={"type": "llama3", "factor": 8.0}))
 
 
 def test_llama3_rope_tables():
@@ -76,7 +80,12 @@ def test_llama3_rope_tables():
     hd, theta = 128, 500000.0
     sc = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
           "original_max_position_tokens": 8192}
-    base = (np.float32(1.0) / (np.float32(theta) ** (np.arange(0, hd, 2, dtype=np.float32) / np.float32(hd))))
+    import torch
+
+    # the base frequencies as the reference computes them: torch's float32
+    # pow (generic_streamer.py:23; numpy's float32 pow differs in the last bit
+    # for some exponents)
+    base = (1.0 / (theta ** (torch.arange(0, hd, 2).float() / hd))).numpy()
     inv = llama3_inv_freq(hd, theta, sc)
     wl = 2 * np.pi / base.astype(np.float64)
     hi, lo = wl < 8192 / 4.0, wl > 8192 / 1.0
@@ -88,6 +97,9 @@ def test_llama3_rope_tables():
     np.testing.assert_allclose(inv[mid], (1 - smooth) * base[mid] / 8.0 + smooth * base[mid], rtol=1e-6)
     # blended frequencies lie between the two ends
     assert np.all(inv[mid] <= base[mid]) and np.all(inv[mid] >= base[mid] / 8.0)
+    # the divided frequencies are the float64 quotient rounded to float32
+    assert np.array_equal(inv[lo].view(np.uint32),
+                          (base[lo].astype(np.float64) / 8.0).astype(np.float32).view(np.uint32))
     cos, sin = rope_tables(16, hd, theta, tuple(sorted(sc.items())))
     ang = (np.arange(16, dtype=np.float64)[:, None] * inv.astype(np.float64)[None, :])
     emb = np.concatenate([ang, ang], axis=1).astype(np.float32)
