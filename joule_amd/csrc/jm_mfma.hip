@@ -439,10 +439,9 @@ __device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo&
         if (i >= ti.nt) continue;                 // wave-uniform
         const int slot = slots[i];
         const int rr = 64 * piece + lane;         // row within the block
-        // SiLU(g) * u with a hardware reciprocal: act is quantized to 15-bit
-        // digits next, far coarser than the reciprocal's rounding
+        // SiLU(g) * u, dividing as the reference does (decode_kernel.c:1375)
         const float g = gu[(size_t)i * RP + rr], u = gu[((size_t)MT + i) * RP + rr];
-        const float av = __fmul_rn(__fmul_rn(g, __builtin_amdgcn_rcpf(__fadd_rn(1.0f, expf_fast(-g)))), u);
+        const float av = swiglu(g, u);
         const int row = r0 + rr;
         a.act[(size_t)slot * m + row] = av;
         const int g0 = row / G;                   // this lane's group (a G-lane segment)
