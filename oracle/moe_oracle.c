@@ -32,8 +32,15 @@
  * The AVX2 reference keeps 8 partial sums (one per SIMD lane r, summing the
  * elements j == r mod 8) and reduces them as ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)).
  * The lane8_* helpers below hold those 8 partials in a plain array.
+ *
+ * The block driver runs either that scalar form or an AVX2 form of the same
+ * operations (jmo_set_simd): the 8 partial sums in one __m256 with
+ * _mm256_fmadd_ps per step and the same reduction tree, so both forms give
+ * the same bits (tests/test_oracle_simd.py); the AVX2 form is the timed CPU
+ * baseline, the scalar one stays the readable statement.
  */
 #define _GNU_SOURCE
+#include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
 #include <sched.h>
@@ -201,6 +208,137 @@ JMO_API void jmo_q4_row_dot_B(const uint8_t* row, const uint16_t* sc,
             acc[b] = fmaf(ga, s, acc[b]);
         }
     }
+}
+
+/* ------------------------------------------------------------------ */
+/* AVX2 forms of the router dot and the batched Q4 row dot              */
+/* ------------------------------------------------------------------ */
+
+/* ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) of the 8 lanes, as lane8_reduce. */
+static inline float lane8_reduce_v(__m256 v) {
+    __m128 h = _mm_add_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));   /* l_i + l_(i+4) */
+    h = _mm_add_ps(h, _mm_movehl_ps(h, h));                                           /* (0+4)+(2+6), (1+5)+(3+7) */
+    h = _mm_add_ss(h, _mm_shuffle_ps(h, h, 1));
+    return _mm_cvtss_f32(h);
+}
+
+JMO_API float jmo_router_dot_avx2(const float* w, const float* x, int d) {
+    __m256 l = _mm256_setzero_ps();
+    int j = 0;
+    for (; j + 8 <= d; j += 8) l = _mm256_fmadd_ps(_mm256_loadu_ps(w + j), _mm256_loadu_ps(x + j), l);
+    float acc = lane8_reduce_v(l);
+    for (; j < d; j++) acc = fmaf(w[j], x[j], acc);
+    return acc;
+}
+
+/* Values (q - 8) of 8 consecutive elements as floats, from the dword that
+ * packs them (element k in bits 4k..4k+3): the dword broadcast, shifted per
+ * lane and masked, then 2^23 + q read as a float less 2^23 + 8 (exact). */
+static inline __m256 q4_vec8(const uint8_t* p) {
+    const __m256i sh = _mm256_setr_epi32(0, 4, 8, 12, 16, 20, 24, 28);
+    int w;
+    memcpy(&w, p, sizeof w);
+    const __m256i q = _mm256_and_si256(_mm256_srlv_epi32(_mm256_set1_epi32(w), sh),
+                                       _mm256_set1_epi32(0x0F));
+    return _mm256_sub_ps(_mm256_castsi256_ps(_mm256_or_si256(q, _mm256_set1_epi32(0x4B000000))),
+                         _mm256_set1_ps(8388616.0f));
+}
+
+/* jmo_q4_row_dot_B with each group's 8 lane chains in one register: the same
+ * fmaf per lane and step as q4_group_lane8, the same tree, the same
+ * acc[b] = fmaf(h, s, acc[b]) in group order.  Independent chains are
+ * interleaved (four groups of one token, or two tokens of one group) so that
+ * the FMA latency overlaps; no lane's order changes. */
+JMO_API void jmo_q4_row_dot_B_avx2(const uint8_t* row, const uint16_t* sc,
+                                   const float* x, int B, float* acc,
+                                   int cols, int group, int stride) {
+    if (group != 32 && group != 64) {
+        jmo_q4_row_dot_B(row, sc, x, B, acc, cols, group, stride);
+        return;
+    }
+    const int ng = cols / group, nv = group / 8, gb = group / 2;
+    int g = 0;
+    if (B == 1) {
+        float a = 0.0f;
+        for (; g + 4 <= ng; g += 4) {
+            __m256 l0 = _mm256_setzero_ps(), l1 = l0, l2 = l0, l3 = l0;
+            const uint8_t* r = row + (size_t)g * gb;
+            const float* xg = x + (size_t)g * group;
+            for (int t = 0; t < nv; t++) {
+                l0 = _mm256_fmadd_ps(q4_vec8(r + 4 * t), _mm256_loadu_ps(xg + 8 * t), l0);
+                l1 = _mm256_fmadd_ps(q4_vec8(r + gb + 4 * t), _mm256_loadu_ps(xg + group + 8 * t), l1);
+                l2 = _mm256_fmadd_ps(q4_vec8(r + 2 * gb + 4 * t), _mm256_loadu_ps(xg + 2 * group + 8 * t), l2);
+                l3 = _mm256_fmadd_ps(q4_vec8(r + 3 * gb + 4 * t), _mm256_loadu_ps(xg + 3 * group + 8 * t), l3);
+            }
+            a = fmaf(lane8_reduce_v(l0), jmo_fp16_to_f32(sc[g]), a);
+            a = fmaf(lane8_reduce_v(l1), jmo_fp16_to_f32(sc[g + 1]), a);
+            a = fmaf(lane8_reduce_v(l2), jmo_fp16_to_f32(sc[g + 2]), a);
+            a = fmaf(lane8_reduce_v(l3), jmo_fp16_to_f32(sc[g + 3]), a);
+        }
+        for (; g < ng; g++) {
+            __m256 l = _mm256_setzero_ps();
+            for (int t = 0; t < nv; t++)
+                l = _mm256_fmadd_ps(q4_vec8(row + (size_t)g * gb + 4 * t), _mm256_loadu_ps(x + (size_t)g * group + 8 * t), l);
+            a = fmaf(lane8_reduce_v(l), jmo_fp16_to_f32(sc[g]), a);
+        }
+        acc[0] = a;
+    } else {
+        for (int b = 0; b < B; b++) acc[b] = 0.0f;
+        __m256 v[8];
+        for (; g < ng; g++) {
+            const float s = jmo_fp16_to_f32(sc[g]);
+            for (int t = 0; t < nv; t++) v[t] = q4_vec8(row + (size_t)g * gb + 4 * t);
+            int b = 0;
+            for (; b + 2 <= B; b += 2) {
+                const float* x0 = x + (size_t)b * stride + (size_t)g * group;
+                const float* x1 = x0 + stride;
+                __m256 l0 = _mm256_setzero_ps(), l1 = l0;
+                for (int t = 0; t < nv; t++) {
+                    l0 = _mm256_fmadd_ps(v[t], _mm256_loadu_ps(x0 + 8 * t), l0);
+                    l1 = _mm256_fmadd_ps(v[t], _mm256_loadu_ps(x1 + 8 * t), l1);
+                }
+                acc[b] = fmaf(lane8_reduce_v(l0), s, acc[b]);
+                acc[b + 1] = fmaf(lane8_reduce_v(l1), s, acc[b + 1]);
+            }
+            for (; b < B; b++) {
+                const float* x0 = x + (size_t)b * stride + (size_t)g * group;
+                __m256 l0 = _mm256_setzero_ps();
+                for (int t = 0; t < nv; t++) l0 = _mm256_fmadd_ps(v[t], _mm256_loadu_ps(x0 + 8 * t), l0);
+                acc[b] = fmaf(lane8_reduce_v(l0), s, acc[b]);
+            }
+        }
+    }
+    const int tail0 = ng * group;
+    if (tail0 < cols) {
+        const float s = jmo_fp16_to_f32(sc[ng]);
+        for (int b = 0; b < B; b++) {
+            const float* xb = x + (size_t)b * stride;
+            float ga = 0.0f;
+            for (int c = tail0; c < cols; c += 2) {
+                const uint8_t byte = row[c / 2];
+                const float lo = (float)((int)(byte & 0x0Fu) - 8);
+                const float hi = (float)((int)(byte >> 4) - 8);
+                ga = ga + fmaf(lo, xb[c], hi * xb[c + 1]);
+            }
+            acc[b] = fmaf(ga, s, acc[b]);
+        }
+    }
+}
+
+/* which form the block driver runs: 0 scalar, 1 AVX2 */
+static _Atomic int g_simd = 0;
+
+JMO_API void jmo_set_simd(int on) { atomic_store(&g_simd, on ? 1 : 0); }
+JMO_API int jmo_get_simd(void) { return atomic_load(&g_simd); }
+
+static inline float router_dot_sel(const float* w, const float* x, int d) {
+    return atomic_load_explicit(&g_simd, memory_order_relaxed) ? jmo_router_dot_avx2(w, x, d) : jmo_router_dot(w, x, d);
+}
+
+static inline void row_dot_sel(const uint8_t* row, const uint16_t* sc, const float* x, int B, float* acc,
+                               int cols, int group, int stride) {
+    if (atomic_load_explicit(&g_simd, memory_order_relaxed)) jmo_q4_row_dot_B_avx2(row, sc, x, B, acc, cols, group, stride);
+    else jmo_q4_row_dot_B(row, sc, x, B, acc, cols, group, stride);
 }
 
 /* ------------------------------------------------------------------ */
@@ -465,7 +603,7 @@ static void router_worker(void* ctx, long id, long lo, long hi) {
     for (long e = lo; e < hi; e++)
         for (int b = 0; b < j->B; b++)
             j->scores[(size_t)b * p->E + e] =
-                jmo_router_dot(p->gate_w + (size_t)e * p->d, j->x + (size_t)b * p->d, p->d);
+                router_dot_sel(p->gate_w + (size_t)e * p->d, j->x + (size_t)b * p->d, p->d);
 }
 
 static void expert_worker(void* ctx, long id, long lo, long hi) {
@@ -491,13 +629,13 @@ static void expert_worker(void* ctx, long id, long lo, long hi) {
         for (int s = s0; s < s1; s++) tok[nt++] = j->uidx[s] / p->topk;
         for (int i = 0; i < m; i++) {
             if (j->all_tokens) {
-                jmo_q4_row_dot_B(pkg + (size_t)i * (d / 2), scg + (size_t)i * (d / G), j->x, B, gacc, d, G, d);
-                jmo_q4_row_dot_B(pku + (size_t)i * (d / 2), scu + (size_t)i * (d / G), j->x, B, uacc, d, G, d);
+                row_dot_sel(pkg + (size_t)i * (d / 2), scg + (size_t)i * (d / G), j->x, B, gacc, d, G, d);
+                row_dot_sel(pku + (size_t)i * (d / 2), scu + (size_t)i * (d / G), j->x, B, uacc, d, G, d);
             } else {
                 for (int t = 0; t < nt; t++) {
                     const int b = tok[t];
-                    jmo_q4_row_dot_B(pkg + (size_t)i * (d / 2), scg + (size_t)i * (d / G), j->x + (size_t)b * d, 1, gacc + b, d, G, d);
-                    jmo_q4_row_dot_B(pku + (size_t)i * (d / 2), scu + (size_t)i * (d / G), j->x + (size_t)b * d, 1, uacc + b, d, G, d);
+                    row_dot_sel(pkg + (size_t)i * (d / 2), scg + (size_t)i * (d / G), j->x + (size_t)b * d, 1, gacc + b, d, G, d);
+                    row_dot_sel(pku + (size_t)i * (d / 2), scu + (size_t)i * (d / G), j->x + (size_t)b * d, 1, uacc + b, d, G, d);
                 }
             }
             for (int t = 0; t < nt; t++) {
@@ -508,11 +646,11 @@ static void expert_worker(void* ctx, long id, long lo, long hi) {
         }
         for (int i = 0; i < d; i++) {
             if (j->all_tokens) {
-                jmo_q4_row_dot_B(pkd + (size_t)i * (m / 2), scd + (size_t)i * (m / G), acte, B, dacc, m, G, m);
+                row_dot_sel(pkd + (size_t)i * (m / 2), scd + (size_t)i * (m / G), acte, B, dacc, m, G, m);
             } else {
                 for (int t = 0; t < nt; t++) {
                     const int b = tok[t];
-                    jmo_q4_row_dot_B(pkd + (size_t)i * (m / 2), scd + (size_t)i * (m / G), acte + (size_t)b * m, 1, dacc + b, m, G, m);
+                    row_dot_sel(pkd + (size_t)i * (m / 2), scd + (size_t)i * (m / G), acte + (size_t)b * m, 1, dacc + b, m, G, m);
                 }
             }
             for (int s = s0; s < s1; s++) {

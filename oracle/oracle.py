@@ -92,6 +92,14 @@ def lib() -> ctypes.CDLL:
         L.jmo_pool_init.restype = ctypes.c_int
         L.jmo_pool_init.argtypes = [ctypes.c_int]
         L.jmo_pool_shutdown.restype = None
+        L.jmo_router_dot_avx2.restype = ctypes.c_float
+        L.jmo_router_dot_avx2.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+        L.jmo_q4_row_dot_B_avx2.restype = None
+        L.jmo_q4_row_dot_B_avx2.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int, ctypes.c_void_p] + [ctypes.c_int] * 3
+        L.jmo_set_simd.restype = None
+        L.jmo_set_simd.argtypes = [ctypes.c_int]
+        L.jmo_get_simd.restype = ctypes.c_int
+        L.jmo_get_simd.argtypes = []
         _lib = L
     return _lib
 
@@ -131,6 +139,23 @@ def router_dot(w: np.ndarray, x: np.ndarray) -> float:
     w = np.ascontiguousarray(w, np.float32)
     x = np.ascontiguousarray(x, np.float32)
     return lib().jmo_router_dot(_ptr(w), _ptr(x), w.size)
+
+
+def router_dot_avx2(w: np.ndarray, x: np.ndarray) -> float:
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    return lib().jmo_router_dot_avx2(_ptr(w), _ptr(x), w.size)
+
+
+def set_simd(on: bool) -> None:
+    """Which form of the router and Q4 row dots the block (OracleMoE.forward)
+    runs, process-wide: the AVX2 form (the same bits, the timed CPU
+    baseline) or the scalar statement (the default)."""
+    lib().jmo_set_simd(int(bool(on)))
+
+
+def get_simd() -> bool:
+    return bool(lib().jmo_get_simd())
 
 
 def router_logits(w: np.ndarray, x: np.ndarray) -> np.ndarray:
@@ -183,6 +208,14 @@ def q4_row_dot_B(row, sc, X, cols, group=64) -> np.ndarray:
     B = X.shape[0]
     acc = np.empty(B, np.float32)
     lib().jmo_q4_row_dot_B(_ptr(row), _ptr(sc), _ptr(X), B, _ptr(acc), cols, group, X.shape[1])
+    return acc
+
+
+def q4_row_dot_B_avx2(row, sc, X, cols, group=64) -> np.ndarray:
+    X = np.ascontiguousarray(X, np.float32)
+    B = X.shape[0]
+    acc = np.empty(B, np.float32)
+    lib().jmo_q4_row_dot_B_avx2(_ptr(row), _ptr(sc), _ptr(X), B, _ptr(acc), cols, group, X.shape[1])
     return acc
 
 

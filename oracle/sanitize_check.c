@@ -49,6 +49,7 @@ void jmo_expert_job(const uint8_t* pk_g, const uint16_t* sc_g, const uint8_t* pk
                     float* scratch, float prob);
 void jmo_q4_dequant(float* out, const uint8_t* packed, const uint16_t* scales, int64_t numel, int group);
 void jmo_softmax_topk(float* probs, int E, int topk, int renorm, int32_t* top, float* tw);
+void jmo_set_simd(int on);
 int jmo_pool_init(int n_workers);
 void jmo_pool_shutdown(void);
 int jmo_layer_ffn_batch(const jmo_moe* p, const float* x, int B, float* out, int32_t* top, float* tw,
@@ -150,6 +151,16 @@ int main(void) {
                 CHECK(memcmp(out, ref, sizeof(float) * B * d) == 0, "out B=%d threads=%d all=%d", B, th[ti], all);
             }
         }
+        /* the AVX2 form of the same block: the same bits */
+        jmo_set_simd(1);
+        for (int ti = 0; ti < 4; ti++) {
+            for (int all = 0; all < 2; all++) {
+                CHECK(jmo_layer_ffn_batch(&p, x, B, out, topb, twb, th[ti], all) == 0, "block");
+                CHECK(memcmp(topb, topr, sizeof(int32_t) * B * k) == 0, "avx2 top B=%d threads=%d", B, th[ti]);
+                CHECK(memcmp(out, ref, sizeof(float) * B * d) == 0, "avx2 out B=%d threads=%d all=%d", B, th[ti], all);
+            }
+        }
+        jmo_set_simd(0);
         if (bi == 1) jmo_pool_shutdown();
     }
     jmo_pool_shutdown();
