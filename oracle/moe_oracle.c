@@ -244,6 +244,86 @@ static inline __m256 q4_vec8(const uint8_t* p) {
                          _mm256_set1_ps(8388616.0f));
 }
 
+/* Four groups' lane reductions at once, each the tree of lane8_reduce_v:
+ * h_i = l_i + l_(i+4) for both groups of a 256-bit pair, then
+ * (h_0 + h_2) and (h_1 + h_3) side by side for all four, then their sum.
+ * Returns [r0, r1, r2, r3]. */
+static inline __m128 lane8_reduce4_v(__m256 l0, __m256 l1, __m256 l2, __m256 l3) {
+    const __m256 h01 = _mm256_add_ps(_mm256_permute2f128_ps(l0, l1, 0x20), _mm256_permute2f128_ps(l0, l1, 0x31));
+    const __m256 h23 = _mm256_add_ps(_mm256_permute2f128_ps(l2, l3, 0x20), _mm256_permute2f128_ps(l2, l3, 0x31));
+    /* per 128-bit half: [h0+h2, h1+h3] of group 0 (low) / 1 (high), then of 2 / 3 */
+    const __m256 t = _mm256_add_ps(_mm256_shuffle_ps(h01, h23, _MM_SHUFFLE(1, 0, 1, 0)),
+                                   _mm256_shuffle_ps(h01, h23, _MM_SHUFFLE(3, 2, 3, 2)));
+    const __m256 u = _mm256_hadd_ps(t, t);           /* low: r0, r2; high: r1, r3 */
+    return _mm_unpacklo_ps(_mm256_castps256_ps128(u), _mm256_extractf128_ps(u, 1));
+}
+
+/* Up to 64 packed bytes (128 elements) as signed bytes q - 8 in element order. */
+static inline void q4_bytes(const uint8_t* p, int nbytes, int8_t* out) {
+    const __m128i m = _mm_set1_epi8(0x0F), k8 = _mm_set1_epi8(8);
+    int i = 0;
+    for (; i + 16 <= nbytes; i += 16) {
+        const __m128i b = _mm_loadu_si128((const __m128i*)(p + i));
+        const __m128i lo = _mm_and_si128(b, m), hi = _mm_and_si128(_mm_srli_epi16(b, 4), m);
+        _mm_storeu_si128((__m128i*)(out + 2 * i), _mm_sub_epi8(_mm_unpacklo_epi8(lo, hi), k8));
+        _mm_storeu_si128((__m128i*)(out + 2 * i + 16), _mm_sub_epi8(_mm_unpackhi_epi8(lo, hi), k8));
+    }
+    for (; i < nbytes; i++) {
+        out[2 * i] = (int8_t)((int)(p[i] & 0x0Fu) - 8);
+        out[2 * i + 1] = (int8_t)((int)(p[i] >> 4) - 8);
+    }
+}
+
+/* 8 values from signed bytes as floats (exact). */
+static inline __m256 q4_vec8_b(const int8_t* q) {
+    return _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(_mm_loadl_epi64((const __m128i*)q)));
+}
+
+/* One token's dot with one row (group 32 or 64): the row decoded to bytes
+ * in chunks of four groups, each group's 8 lane chains in one register
+ * (the fmaf of q4_group_lane8 per lane and step), four groups' chains
+ * interleaved, reduced by the lane8 tree, and a = fmaf(r, s, a) in group
+ * order. */
+static inline __attribute__((always_inline)) float q4_row_dot1_body(const uint8_t* row, const uint16_t* sc,
+                                                                   const float* x, int ng, int group) {
+    const int nv = group / 8, gb = group / 2;
+    int8_t q[256];
+    float a = 0.0f;
+    int g = 0;
+    for (; g + 4 <= ng; g += 4) {
+        q4_bytes(row + (size_t)g * gb, 4 * gb, q);
+        /* keep q in memory: 8-byte sign-extending loads from it cost one
+         * instruction each, extracting them from registers three */
+        __asm__ volatile("" : : "r"(q) : "memory");
+        const float* xg = x + (size_t)g * group;
+        __m256 l0 = _mm256_setzero_ps(), l1 = l0, l2 = l0, l3 = l0;
+        for (int t = 0; t < nv; t++) {
+            l0 = _mm256_fmadd_ps(q4_vec8_b(q + 8 * t), _mm256_loadu_ps(xg + 8 * t), l0);
+            l1 = _mm256_fmadd_ps(q4_vec8_b(q + group + 8 * t), _mm256_loadu_ps(xg + group + 8 * t), l1);
+            l2 = _mm256_fmadd_ps(q4_vec8_b(q + 2 * group + 8 * t), _mm256_loadu_ps(xg + 2 * group + 8 * t), l2);
+            l3 = _mm256_fmadd_ps(q4_vec8_b(q + 3 * group + 8 * t), _mm256_loadu_ps(xg + 3 * group + 8 * t), l3);
+        }
+        const __m128 r = lane8_reduce4_v(l0, l1, l2, l3);
+        a = fmaf(_mm_cvtss_f32(r), jmo_fp16_to_f32(sc[g]), a);
+        a = fmaf(_mm_cvtss_f32(_mm_shuffle_ps(r, r, 1)), jmo_fp16_to_f32(sc[g + 1]), a);
+        a = fmaf(_mm_cvtss_f32(_mm_shuffle_ps(r, r, 2)), jmo_fp16_to_f32(sc[g + 2]), a);
+        a = fmaf(_mm_cvtss_f32(_mm_shuffle_ps(r, r, 3)), jmo_fp16_to_f32(sc[g + 3]), a);
+    }
+    for (; g < ng; g++) {
+        q4_bytes(row + (size_t)g * gb, gb, q);
+        __m256 l = _mm256_setzero_ps();
+        for (int t = 0; t < nv; t++)
+            l = _mm256_fmadd_ps(q4_vec8_b(q + 8 * t), _mm256_loadu_ps(x + (size_t)g * group + 8 * t), l);
+        a = fmaf(lane8_reduce_v(l), jmo_fp16_to_f32(sc[g]), a);
+    }
+    return a;
+}
+
+/* the body with the group size a constant (32 or 64 values) */
+static float q4_row_dot1_avx2(const uint8_t* row, const uint16_t* sc, const float* x, int ng, int group) {
+    return group == 64 ? q4_row_dot1_body(row, sc, x, ng, 64) : q4_row_dot1_body(row, sc, x, ng, 32);
+}
+
 /* jmo_q4_row_dot_B with each group's 8 lane chains in one register: the same
  * fmaf per lane and step as q4_group_lane8, the same tree, the same
  * acc[b] = fmaf(h, s, acc[b]) in group order.  Independent chains are
@@ -257,35 +337,13 @@ JMO_API void jmo_q4_row_dot_B_avx2(const uint8_t* row, const uint16_t* sc,
         return;
     }
     const int ng = cols / group, nv = group / 8, gb = group / 2;
-    int g = 0;
+    int g = ng;
     if (B == 1) {
-        float a = 0.0f;
-        for (; g + 4 <= ng; g += 4) {
-            __m256 l0 = _mm256_setzero_ps(), l1 = l0, l2 = l0, l3 = l0;
-            const uint8_t* r = row + (size_t)g * gb;
-            const float* xg = x + (size_t)g * group;
-            for (int t = 0; t < nv; t++) {
-                l0 = _mm256_fmadd_ps(q4_vec8(r + 4 * t), _mm256_loadu_ps(xg + 8 * t), l0);
-                l1 = _mm256_fmadd_ps(q4_vec8(r + gb + 4 * t), _mm256_loadu_ps(xg + group + 8 * t), l1);
-                l2 = _mm256_fmadd_ps(q4_vec8(r + 2 * gb + 4 * t), _mm256_loadu_ps(xg + 2 * group + 8 * t), l2);
-                l3 = _mm256_fmadd_ps(q4_vec8(r + 3 * gb + 4 * t), _mm256_loadu_ps(xg + 3 * group + 8 * t), l3);
-            }
-            a = fmaf(lane8_reduce_v(l0), jmo_fp16_to_f32(sc[g]), a);
-            a = fmaf(lane8_reduce_v(l1), jmo_fp16_to_f32(sc[g + 1]), a);
-            a = fmaf(lane8_reduce_v(l2), jmo_fp16_to_f32(sc[g + 2]), a);
-            a = fmaf(lane8_reduce_v(l3), jmo_fp16_to_f32(sc[g + 3]), a);
-        }
-        for (; g < ng; g++) {
-            __m256 l = _mm256_setzero_ps();
-            for (int t = 0; t < nv; t++)
-                l = _mm256_fmadd_ps(q4_vec8(row + (size_t)g * gb + 4 * t), _mm256_loadu_ps(x + (size_t)g * group + 8 * t), l);
-            a = fmaf(lane8_reduce_v(l), jmo_fp16_to_f32(sc[g]), a);
-        }
-        acc[0] = a;
+        acc[0] = q4_row_dot1_avx2(row, sc, x, ng, group);
     } else {
         for (int b = 0; b < B; b++) acc[b] = 0.0f;
         __m256 v[8];
-        for (; g < ng; g++) {
+        for (g = 0; g < ng; g++) {
             const float s = jmo_fp16_to_f32(sc[g]);
             for (int t = 0; t < nv; t++) v[t] = q4_vec8(row + (size_t)g * gb + 4 * t);
             int b = 0;
@@ -337,8 +395,12 @@ static inline float router_dot_sel(const float* w, const float* x, int d) {
 
 static inline void row_dot_sel(const uint8_t* row, const uint16_t* sc, const float* x, int B, float* acc,
                                int cols, int group, int stride) {
-    if (atomic_load_explicit(&g_simd, memory_order_relaxed)) jmo_q4_row_dot_B_avx2(row, sc, x, B, acc, cols, group, stride);
-    else jmo_q4_row_dot_B(row, sc, x, B, acc, cols, group, stride);
+    if (!atomic_load_explicit(&g_simd, memory_order_relaxed))
+        jmo_q4_row_dot_B(row, sc, x, B, acc, cols, group, stride);
+    else if (B == 1 && (group == 32 || group == 64) && cols % group == 0)
+        acc[0] = q4_row_dot1_avx2(row, sc, x, cols / group, group);
+    else
+        jmo_q4_row_dot_B_avx2(row, sc, x, B, acc, cols, group, stride);
 }
 
 /* ------------------------------------------------------------------ */
