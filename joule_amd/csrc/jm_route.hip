@@ -88,6 +88,36 @@ hipError_t launch_bf16_exact(const float* in, long long n, unsigned* flag, hipSt
 }
 
 
+// x digits of token b staged in xT (chain order), wave eg's share of the
+// token's groups over ngrp waves: one G-value group per G-lane segment (and,
+// for the MFMA branch, the same group as int8 digit pairs), two groups at a
+// time so that their reduction chains interleave.  Run before the router
+// chains: it needs only the staged token, so it runs while the table's
+// chunks arrive.
+template <int G, int NDIG, int d>
+__device__ __forceinline__ void encode_token_share(const RouteArgs& a, int b, int eg, int ngrp, const float* xT) {
+    constexpr int TP = d / 8 + 4;
+    constexpr int ng = d / G;
+    constexpr int PPW = JM_WAVE / G;
+    const int lane = threadIdx.x & 63;
+    const int sub = lane / G;
+    const bool i8 = a.xqh != nullptr;
+    for (int base = eg * PPW; base < ng; base += 2 * ngrp * PPW) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int p = base + u * ngrp * PPW + sub;
+            const bool ok = p < ng;
+            const int pp = ok ? p : 0;
+            const int j = pp * G + (lane & (G - 1));
+            const float v = ok ? xT[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
+            const size_t o = (size_t)b * d + (size_t)pp * G;
+            encode_group_both<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + pp) * (NDIG * (G / 8)),
+                                       a.xscale + (size_t)b * ng + pp, i8, a.xqh + (i8 ? o : 0),
+                                       a.xql + (i8 ? o : 0), a.xqs + (size_t)b * ng + pp, a.xqc + (size_t)b * ng + pp);
+        }
+    }
+}
+
 // Router scores of one expert group (8 experts) for one token: block
 // (eg, b) is one wave; lane 8 * el + r runs chain r of expert 8 * eg + el
 // with up to 16 chunks of its chain in flight.  The block also encodes its
@@ -206,28 +236,7 @@ k_router_grp(RouteArgs a) {
     }
     stage_chain_order<XV, TP>(xv, xT);
     __syncthreads();
-    // x digits: one G-value group per G-lane segment (and, for the MFMA
-    // branch, the same group as int8 digit pairs); two groups at a time, so
-    // that their reduction chains interleave.  Before the chains: they need
-    // only the staged token, so they run while the table's chunks arrive.
-    constexpr int ng = d / G;
-    constexpr int PPW = JM_WAVE / G;
-    const int sub = lane / G;
-    const bool i8 = a.xqh != nullptr;
-    for (int base = eg * PPW; base < ng; base += 2 * ngrp * PPW) {
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int p = base + u * ngrp * PPW + sub;
-            const bool ok = p < ng;
-            const int pp = ok ? p : 0;
-            const int j = pp * G + (lane & (G - 1));
-            const float v = ok ? xT[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
-            const size_t o = (size_t)b * d + (size_t)pp * G;
-            encode_group_both<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + pp) * (NDIG * (G / 8)),
-                                       a.xscale + (size_t)b * ng + pp, i8, a.xqh + (i8 ? o : 0),
-                                       a.xql + (i8 ? o : 0), a.xqs + (size_t)b * ng + pp, a.xqc + (size_t)b * ng + pp);
-        }
-    }
+    encode_token_share<G, NDIG, d>(a, b, eg, ngrp, xT);
     const float acc = router_chains<DV, WBF16, NB>(buf, wt, eg, xT);
     const int e = 8 * eg + el;
     if (r == 0 && e < a.E) a.logits[(size_t)b * a.E + e] = acc;
