@@ -119,6 +119,15 @@ CASES = {
     "gqa2_bias_l1_b2_f32kv": (DecoderShape(n_layers=1, moe=MoEShape(d=1024, m=256, E=16, topk=4, renorm=True),
                                            n_heads=8, n_kv=4, maxT=200, qk_norm_type=1, bias_qkv=True),
                               32, [0, 199], torch.float32),
+    # one token: the o_proj merges the attention splits itself (17 splits
+    # at position 2048, one at position 0, a split boundary at 127 -> 128)
+    "qwen3_l2_b1": (qwen3_30b_a3b(n_layers=2, maxT=2176), 64, [2048]),
+    "qwen3_l1_b1_p0": (qwen3_30b_a3b(n_layers=1, maxT=300), 64, [0]),
+    "gqa4_l1_b1_p127": (DecoderShape(n_layers=1, moe=MoEShape(d=1024, m=512, E=32, topk=8, renorm=True),
+                                     n_heads=8, n_kv=2, maxT=520), 32, [127]),
+    "olmoe_l1_b1_f32kv": (DecoderShape(n_layers=1, moe=MoEShape(d=2048, m=1024, E=64, topk=8, renorm=False),
+                                       n_heads=16, n_kv=16, maxT=300, qk_norm_type=2), 64, [255],
+                          torch.float32),
 }
 
 
@@ -168,7 +177,36 @@ def test_decode_split_profile_and_errors():
     dec.store.close()
 
 
-@pytest.mark.parametrize("B,kv_dtype", [(4, torch.bfloat16), (40, torch.bfloat16), (4, torch.float32)])
+@pytest.mark.parametrize("shape_name,position", [("qwen3", 2048), ("qwen3", 128), ("gqa4", 300)])
+def test_decode_one_token_matches_batch(shape_name, position):
+    """A one-token step (its o_proj merges the attention splits) gives the
+    bits of token 0 of a two-token step (the split-merge kernel) when both
+    tokens carry the same input, position and cache contents."""
+    if shape_name == "qwen3":
+        shape, group = qwen3_30b_a3b(n_layers=2, maxT=2176), 64
+    else:
+        shape, group = DecoderShape(n_layers=1, moe=MoEShape(d=1024, m=512, E=32, topk=8, renorm=True),
+                                    n_heads=8, n_kv=2, maxT=520), 32
+    print(f"[decode] one token vs two at position {position}, {shape_name}", flush=True)
+    dec, _, kv2 = _model(shape, group, 2)
+    kv2.data[1].copy_(kv2.data[0])
+    kv1 = KVCacheSet(shape, 1, dtype=kv2.data.dtype)
+    kv1.data.copy_(kv2.data[0:1])
+    x = activations(1, shape.d)
+    x2 = np.concatenate([x, x])
+    for graph in (False, True):
+        dec.set_graph(graph)
+        one = dec.decode_layers_batch(torch.from_numpy(x).cuda(), [position], kv1).clone()
+        two = dec.decode_layers_batch(torch.from_numpy(x2).cuda(), [position, position], kv2).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(two[0], two[1])
+        assert torch.equal(one[0], two[0]), f"graph={graph}: one-token step differs from the batch's token 0"
+        assert torch.equal(kv1.data[0], kv2.data[0])
+    dec.store.close()
+
+
+@pytest.mark.parametrize("B,kv_dtype", [(4, torch.bfloat16), (40, torch.bfloat16), (4, torch.float32),
+                                        (1, torch.bfloat16)])
 def test_decode_graph_replays_match_eager(B, kv_dtype):
     """The step replayed from a captured HIP graph gives the eager step's bits,
     replay after replay, with eager work and synchronisation in between; new
