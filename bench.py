@@ -28,7 +28,9 @@ Reported (one JSON line):
                routing, whose large segments take the MFMA branch, and the
                full 48-layer Qwen3-30B-A3B decode step at B=8 (attention over
                2049 cached positions + the MoE block per layer), with the MoE
-               share of the step isolated
+               share of the step isolated; act_digits_5: the Qwen3 block at
+               the headline B and at B=1 with 5 activation digit planes
+               (the precise setting) instead of 4
   per_call_us  median, p10 and p90 of the per-call times (events between
                consecutive calls), for the headline and each sweep config
   parity       for the headline and every MoE config of the sweep, the timed
@@ -989,6 +991,28 @@ def main() -> int:
                 log(f"parity qwen3 B={b}: {parity[f'qwen3_B{b}']}")
             if cpu_on:
                 cpu_sweep[f"qwen3_B{b}"] = cpu_case(moes, xs[b], cpu_share, f"qwen3 B={b}")[0]
+
+    if not args.no_sweep:
+        # the same blocks with 5 activation digit planes (jm_store_set_act_digits):
+        # time and error of the precise setting beside the default's
+        prec = {}
+        store.set_act_digits(5)
+        try:
+            for b in (B, 1):
+                xp_np = x_np if b == B else xs.get(1, activations(1, shape.d))
+                xp = torch.from_numpy(xp_np).cuda()
+                m5, st5, U5, d5 = measure(store, gw, xp, max(args.steps // 2, 50), 10, NL)
+                r5 = block_numbers(shape, G, b, m5, st5, U5, max(args.steps // 2, 50), NL, rb)
+                e = {k: r5[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac")}
+                e["per_call_us"] = d5
+                if check:
+                    e["parity"] = parity[f"qwen3_B{b}_digits5"] = block_parity(store, moes, xp_np, list(range(NL)))
+                prec[f"qwen3_B{b}"] = e
+                log(f"5 digits qwen3 B={b}: {r5['tok_per_s']:.0f} tok/s, {m5 * 1e3:.1f} us/step, "
+                    f"parity {e.get('parity')}")
+        finally:
+            store.set_act_digits(0)
+        sweep["act_digits_5"] = prec
 
     if not args.no_sweep:
         sweep["qwen3_zipf512"], gz, xz_np = zipf_block(store, gw, args.steps, NL, check=check)

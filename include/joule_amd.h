@@ -118,6 +118,18 @@ int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, 
  * reference, whose batch is at most 16 tokens (decode_kernel.c:1522). */
 int jm_store_set_dense_min(jm_store* s, int min_tokens);
 
+/* Base-16 digit planes per activation value on the GEMV (wave-item)
+ * kernels: each Q4 group of x, and each 32-value chunk of the SwiGLU act, is
+ * carried as block integers of ndig signed digits under one scale (the
+ * group's largest magnitude / R, R = 30583 for 4 digits, 489335 for 5).  4
+ * (the default; 0 restores it) keeps about 15 bits per group, 5 about 19 bits
+ * at more dot products per row.  Router indices and weights do not depend on
+ * it.  The MFMA branch's int8 digit pairs are not affected.  No counterpart in
+ * the reference, whose activations are float32. */
+int jm_store_set_act_digits(jm_store* s, int ndig);
+/* The store's digit planes (4 or 5), -1 for a NULL store. */
+int jm_store_act_digits(const jm_store* s);
+
 /*
  * The MoE block of one layer: layer_ffn_batch(cfg, W, l, x, B, out)
  * (decode_kernel.c:1387-1508), for any B >= 0 (the reference clamps B to 16

@@ -29,6 +29,8 @@ SIGNATURES = {
     "jm_store_reserve": ([_vp, _i], _i),
     "jm_store_info": ([_vp] + [_vp] * 6, _i),
     "jm_store_set_dense_min": ([_vp, _i], _i),
+    "jm_store_set_act_digits": ([_vp, _i], _i),
+    "jm_store_act_digits": ([_vp], _i),
     "jm_store_router_dtype": ([_vp, _vp], _i),
     "jm_layer_ffn_batch": ([_vp, _i, _vp, _i, _vp, _vp, _vp, _vp], _i),
     "jm_layer_ffn_batch_noalloc": ([_vp, _i, _vp, _i, _vp, _vp, _vp, _vp], _i),

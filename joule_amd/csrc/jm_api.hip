@@ -157,8 +157,9 @@ constexpr int WS_NF = 27;
 void ws_sizes(const jm_store* s, int B, size_t (&sz)[WS_NF]) {
     const int E = s->E, d = s->d, m = s->m, k = s->topk, G = s->group;
     const size_t nslot = (size_t)B * k;
-    const size_t words_d = (size_t)(d / G) * JM_NDIG * (G / 8);
-    const size_t words_m = (size_t)(m / 8) * JM_NDIG;
+    // digit planes: room for the most (jm_store_set_act_digits)
+    const size_t words_d = (size_t)(d / G) * JM_NDIG_MAX * (G / 8);
+    const size_t words_m = (size_t)(m / 8) * JM_NDIG_MAX;
     const size_t max_tiles = nslot / JM_DENSE_TILE + E;
     const size_t v[WS_NF] = {
         (size_t)B * E * 4,            // logits
@@ -266,6 +267,7 @@ int create_dense_store(const jm_kernel_cfg* cfg, jm_store** out) {
     memset(s, 0, sizeof *s);
     s->L = L; s->E = 0; s->d = d; s->m = m; s->topk = 0;
     s->dense_min = JM_DENSE_MIN_DEFAULT;
+    s->ndig = JM_NDIG;
     s->max_layers = -1;
     s->device = dev;
     hipError_t e = hipDeviceGetAttribute(&s->n_cu, hipDeviceAttributeMultiprocessorCount, dev);
@@ -307,6 +309,7 @@ int stage_setup(jm_store* s, int layer, const int32_t* top, int B, const char* w
     r->work = w.work; r->umax = std::min(E, nslot); r->rec = s->rec;
     r->key0 = (long long)layer * E;
     r->dense_min = 0x7FFFFFFF;                  // no MFMA tiles
+    r->ndig = s->ndig;
     r->tiles = w.tiles; r->n_tiles = w.n_tiles; r->small = w.small;
     JM_HIP(jm::launch_dispatch_work(*r, st), "dispatch launch");
     a->blob = s->blob; a->rec = s->rec; a->key0 = r->key0; a->E = E;
@@ -317,6 +320,7 @@ int stage_setup(jm_store* s, int layer, const int32_t* top, int B, const char* w
     a->adig = w.adig; a->ascale = w.ascale;
     a->dense_min = 0x7FFFFFFF;
     a->tiles = w.tiles; a->n_tiles = w.n_tiles; a->small = w.small;
+    a->ndig = s->ndig;
     return 0;
 }
 
@@ -350,6 +354,7 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     r.key0 = (long long)layer * E;
     r.dense_min = s->dense_min; r.tiles = w.tiles; r.n_tiles = w.n_tiles; r.small = w.small;
     r.skip_topk = dec && jm::gateup_topk(B, E);
+    r.ndig = s->ndig;
     jm::ExpertArgs a;
     a.blob = s->blob; a.rec = s->rec; a.key0 = (long long)layer * E; a.E = E;
     a.work = w.work; a.umax = umax; a.seg_slot = w.seg_slot;
@@ -365,6 +370,7 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     a.xqh = w.xqh; a.xql = w.xql; a.xqs = w.xqs; a.xqc = w.xqc;
     a.aqh = w.aqh; a.aql = w.aql; a.aqs = w.aqs; a.aqc = w.aqc;
     a.logits = w.logits; a.renorm = s->renorm; a.top_w = w.top; a.tw_w = w.tw;
+    a.ndig = s->ndig;
     const int max_tiles = nslot / JM_DENSE_TILE + E;
 #define JM_MARK(i) if (s->prof && stage_marks) JM_HIP(hipEventRecord(s->ev[i], st), "hipEventRecord")
     JM_MARK(0);
@@ -454,6 +460,7 @@ int jm_store_create(const jm_kernel_cfg* cfg, int group, const void* blob, uint6
     s->renorm = cfg->norm_topk_prob ? 1 : 0;
     s->group = group;
     s->dense_min = JM_DENSE_MIN_DEFAULT;
+    s->ndig = JM_NDIG;
     s->mfma_ok = jm::mfma_shape_ok(d, m) && sc16;
     s->max_layers = -1;
     s->blob = (const uint8_t*)blob;
@@ -565,6 +572,15 @@ int jm_store_set_dense_min(jm_store* s, int min_tokens) {
     s->dense_min = min_tokens == 0 ? JM_DENSE_MIN_DEFAULT : min_tokens;
     return 0;
 }
+
+int jm_store_set_act_digits(jm_store* s, int ndig) {
+    if (int rc = check_store(s)) return rc;
+    if (ndig != 0 && ndig != 4 && ndig != 5) return fail(JM_ERR_ARG, "ndig must be 4, 5 or 0 (the default, %d)", JM_NDIG);
+    s->ndig = ndig == 0 ? JM_NDIG : ndig;
+    return 0;
+}
+
+int jm_store_act_digits(const jm_store* s) { return s ? s->ndig : -1; }
 
 int jm_store_info(const jm_store* s, int* L, int* E, int* d, int* m, int* topk, int* group) {
     if (int rc = check_store(s)) return rc;
@@ -785,7 +801,7 @@ int jm_expert_gateup(jm_store* s, int layer, const float* x, const int32_t* top,
     const jm::Ws& w = s->w;
     // the tokens' digits as the router writes them, then gate/up + SwiGLU
     // of every slot into act (fp32) and the act digits
-    JM_HIP(jm::launch_prep_digits(x, s->d, B, s->d, s->group, w.xdig, w.xscale, st), "digits launch");
+    JM_HIP(jm::launch_prep_digits(x, s->d, B, s->d, s->group, w.xdig, w.xscale, st, s->ndig), "digits launch");
     a.act = act;
     JM_HIP(jm::launch_gateup(a, a.umax, st), "gate/up launch");
     return 0;
@@ -803,7 +819,7 @@ int jm_expert_down(jm_store* s, int layer, const float* act, const int32_t* top,
     const jm::Ws& w = s->w;
     // act's digits in 32-value groups, as the gate/up epilogue writes them,
     // then y[slot] = tw[slot] * (down rows . act[slot])
-    JM_HIP(jm::launch_prep_digits(act, s->m, B * s->topk, s->m, 32, w.adig, w.ascale, st), "digits launch");
+    JM_HIP(jm::launch_prep_digits(act, s->m, B * s->topk, s->m, 32, w.adig, w.ascale, st, s->ndig), "digits launch");
     a.tw = tw;
     a.y = y;
     JM_HIP(jm::launch_down(a, a.umax, st), "down launch");

@@ -415,6 +415,7 @@ int decode_impl(jm_store* s, const jm_kernel_cfg* c, const jm_kernel_w* W, const
         key.trace = s->trace; key.trace_bytes = s->trace_bytes; key.ws = s->ws; key.dws = s->dws;
         key.wt = s->wt; key.wt_bf16 = s->wt_bf16; key.lm_V = s->lm_V; key.nl = run_layers(s, c->L);
         key.dense_min = s->dense_min;
+        key.ndig = s->ndig;
         key.append = append ? 1 : 0;
         key.kv_f32 = s->kv_f32;
         if (!s->gexec || memcmp(&key, &s->gkey, sizeof key) != 0) {

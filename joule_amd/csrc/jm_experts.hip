@@ -303,7 +303,9 @@ static hipError_t gateup_launch(const ExpertArgs& a, long long items, hipStream_
     const dim3 grid((unsigned)((waves + 3) / 4));
     int lpr, qc;
     row_lanes(a.d, &lpr, &qc);
-#define JM_GU(GG, L, Q) hipLaunchKernelGGL((k_gateup<GG, JM_NDIG, L, Q, BALLOT, EPL>), grid, dim3(256), 0, st, a)
+    if (a.ndig != 4 && a.ndig != 5) return hipErrorInvalidValue;
+#define JM_GU(GG, L, Q) do { if (a.ndig == 5) hipLaunchKernelGGL((k_gateup<GG, 5, L, Q, BALLOT, EPL>), grid, dim3(256), 0, st, a); \
+                             else hipLaunchKernelGGL((k_gateup<GG, 4, L, Q, BALLOT, EPL>), grid, dim3(256), 0, st, a); } while (0)
 #define JM_GUG(GG) if (qc == 2) JM_GU(GG, 64, 2); else if (lpr == 64) JM_GU(GG, 64, 1); \
                    else if (lpr == 32) JM_GU(GG, 32, 1); else JM_GU(GG, 16, 1);
     if (qc > 2) return hipErrorInvalidValue;
@@ -332,7 +334,9 @@ hipError_t launch_down_comb(const ExpertArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)(a.d / DC_ROWS));
     int lpr, qc;
     row_lanes(a.m, &lpr, &qc);
-#define JM_DC(GG, L, Q) hipLaunchKernelGGL((k_down_comb<GG, JM_NDIG, L, Q>), grid, dim3(DcShape<L>::THREADS), 0, st, a)
+    if (a.ndig != 4 && a.ndig != 5) return hipErrorInvalidValue;
+#define JM_DC(GG, L, Q) do { if (a.ndig == 5) hipLaunchKernelGGL((k_down_comb<GG, 5, L, Q>), grid, dim3(DcShape<L>::THREADS), 0, st, a); \
+                             else hipLaunchKernelGGL((k_down_comb<GG, 4, L, Q>), grid, dim3(DcShape<L>::THREADS), 0, st, a); } while (0)
 #define JM_DCG(GG) if (qc == 2) JM_DC(GG, 64, 2); else if (lpr == 64) JM_DC(GG, 64, 1); \
                    else if (lpr == 32) JM_DC(GG, 32, 1); else JM_DC(GG, 16, 1);
     if (qc > 2) return hipErrorInvalidValue;
@@ -348,7 +352,9 @@ hipError_t launch_down(const ExpertArgs& a, int umax, hipStream_t st) {
     const dim3 grid((unsigned)((waves + 3) / 4));
     int lpr, qc;
     row_lanes(a.m, &lpr, &qc);
-#define JM_DN(GG, L, Q) hipLaunchKernelGGL((k_down<GG, JM_NDIG, L, Q>), grid, dim3(256), 0, st, a)
+    if (a.ndig != 4 && a.ndig != 5) return hipErrorInvalidValue;
+#define JM_DN(GG, L, Q) do { if (a.ndig == 5) hipLaunchKernelGGL((k_down<GG, 5, L, Q>), grid, dim3(256), 0, st, a); \
+                             else hipLaunchKernelGGL((k_down<GG, 4, L, Q>), grid, dim3(256), 0, st, a); } while (0)
 #define JM_DNG(GG) if (qc == 2) JM_DN(GG, 64, 2); else if (lpr == 64) JM_DN(GG, 64, 1); \
                    else if (lpr == 32) JM_DN(GG, 32, 1); else JM_DN(GG, 16, 1);
     if (qc > 2) return hipErrorInvalidValue;

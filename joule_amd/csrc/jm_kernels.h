@@ -7,6 +7,10 @@
 #include "jm_device.h"
 
 // Signed base-16 digits per activation value in the Q4 dot (see jm_device.h).
+// base-16 digit planes per activation value on the GEMV kernels: 4 by
+// default (15-bit block integers), 5 on request (jm_store_set_act_digits:
+// 19-bit); the workspace holds JM_NDIG_MAX
+#define JM_NDIG_MAX 5
 #ifndef JM_NDIG
 #define JM_NDIG 4
 #endif
@@ -72,6 +76,7 @@ struct ExpertArgs {
     int renorm;
     int* top_w;               // [B*k] (the same memory as top)
     float* tw_w;              // [B*k] (the same memory as tw)
+    int ndig;                 // digit planes of xdig and adig (4 or 5)
 };
 
 // Routing front: router scores, top-k, x digits and (dispatch path) the
@@ -110,6 +115,7 @@ struct RouteArgs {
     int* n_tiles;             // [2] dense tiles; experts under dense_min
     int* small;               // [umax] work-table entries of the experts under dense_min
     int skip_topk;            // 1: the top-k runs in the gate/up kernel
+    int ndig;                 // digit planes the router writes to xdig (4 or 5)
 };
 // from this many tokens the router serves 4 tokens per block from one read
 // of each group's table (k_router_quad)
@@ -130,7 +136,7 @@ hipError_t launch_bf16_exact(const float* in, long long n, unsigned* flag, hipSt
 hipError_t launch_router(const void* gate_w, int bf16, const float* x, float* logits,
                          int B, int E, int d, hipStream_t st);
 hipError_t launch_prep_digits(const float* src, int stride, int rows, int cols, int group,
-                              uint32_t* dig, float* scale, hipStream_t st);
+                              uint32_t* dig, float* scale, hipStream_t st, int ndig = JM_NDIG);
 hipError_t launch_topk(const float* logits, int B, int E, int k, int renorm, int* top, float* tw,
                        hipStream_t st);
 // E <= JM_MAX_E, nslot <= JM_MAX_SLOTS

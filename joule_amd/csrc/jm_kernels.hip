@@ -135,14 +135,15 @@ hipError_t launch_router(const void* gate_w, int bf16, const float* x, float* lo
 }
 
 hipError_t launch_prep_digits(const float* src, int stride, int rows, int cols, int group,
-                              uint32_t* dig, float* scale, hipStream_t st) {
+                              uint32_t* dig, float* scale, hipStream_t st, int ndig) {
     const int ng = cols / group;
     const long long lanes = (long long)rows * ng * group;
     if (lanes == 0) return hipSuccess;
-    if (group == 64)
-        hipLaunchKernelGGL((k_prep_digits<64, JM_NDIG>), grid1(lanes, 256), dim3(256), 0, st, src, stride, rows, ng, dig, scale);
-    else
-        hipLaunchKernelGGL((k_prep_digits<32, JM_NDIG>), grid1(lanes, 256), dim3(256), 0, st, src, stride, rows, ng, dig, scale);
+    if (ndig != 4 && ndig != 5) return hipErrorInvalidValue;
+#define JM_PD(GG, N) hipLaunchKernelGGL((k_prep_digits<GG, N>), grid1(lanes, 256), dim3(256), 0, st, src, stride, rows, ng, dig, scale)
+    if (group == 64) { if (ndig == 5) JM_PD(64, 5); else JM_PD(64, 4); }
+    else { if (ndig == 5) JM_PD(32, 5); else JM_PD(32, 4); }
+#undef JM_PD
     return hipGetLastError();
 }
 

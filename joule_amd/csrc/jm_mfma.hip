@@ -458,7 +458,7 @@ __device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo&
 // dispatched after the tiles' and fill the grid's last round.  The grid
 // always has at least (row blocks) x (small experts) of them: an expert
 // under dense_min frees a whole tile of max_tiles = slots / 32 + E.
-template <int G, int LPR>
+template <int G, int LPR, int NDIG>
 __device__ __forceinline__ void small_gateup(const ExpertArgs& a, int first, int nblk, unsigned char* sm) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int vpe = a.m / wi::GU_ROWS / NWAVE;
@@ -468,7 +468,7 @@ __device__ __forceinline__ void small_gateup(const ExpertArgs& a, int first, int
     int (*gb)[2][4] = (int (*)[2][4])(sm + 2 * sizeof(float[2][4]));
 #pragma unroll 1
     for (int v = first; v < nv; v += nblk) {
-        wi::gateup_item<G, JM_NDIG, LPR, 1, false>(a, a.top, a.small[v / vpe], (v % vpe) * NWAVE + w, gm[w >> 2],
+        wi::gateup_item<G, NDIG, LPR, 1, false>(a, a.top, a.small[v / vpe], (v % vpe) * NWAVE + w, gm[w >> 2],
                                                    gb[w >> 2]);
         __syncthreads();                          // the slots serve the next item
     }
@@ -476,7 +476,7 @@ __device__ __forceinline__ void small_gateup(const ExpertArgs& a, int first, int
 
 // 1-D grid: block f < n_tiles x (m / GU_ROWS) is tile f % n_tiles, row
 // block f / n_tiles; the rest run the small experts' items.
-template <int G, int LPR>
+template <int G, int LPR, int NDIG>
 __global__ void __launch_bounds__(MTHREADS, 1)
 k_gateup_mfma(ExpertArgs a) {
     extern __shared__ __align__(16) unsigned char sm[];
@@ -486,7 +486,7 @@ k_gateup_mfma(ExpertArgs a) {
         gateup_tile<G>(a, tile_at(a, f % nt), f / nt, sm);
         return;
     }
-    small_gateup<G, LPR>(a, f - ntb, (int)gridDim.x - ntb, sm);
+    small_gateup<G, LPR, NDIG>(a, f - ntb, (int)gridDim.x - ntb, sm);
 }
 
 // --------------------------------------------------------------------- down
@@ -543,18 +543,18 @@ __device__ __forceinline__ void down_tile(const ExpertArgs& a, const TileInfo& t
 
 // The small experts' down items (wi::down_item, no barriers) on the blocks
 // past the tiles, 8 consecutive items of one entry per virtual block.
-template <int G, int LPR>
+template <int G, int LPR, int NDIG>
 __device__ __forceinline__ void small_down(const ExpertArgs& a, int first, int nblk) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int vpe = a.d / wi::DN_ROWS / NWAVE;
     const int nv = a.n_tiles[1] * vpe;
 #pragma unroll 1
     for (int v = first; v < nv; v += nblk)
-        wi::down_item<G, JM_NDIG, LPR, 1>(a, a.small[v / vpe], (v % vpe) * NWAVE + w);
+        wi::down_item<G, NDIG, LPR, 1>(a, a.small[v / vpe], (v % vpe) * NWAVE + w);
 }
 
 // 1-D grid as k_gateup_mfma's, with row blocks of DN_BLOCK_ROWS hidden rows.
-template <int G, int LPR>
+template <int G, int LPR, int NDIG>
 __global__ void __launch_bounds__(MTHREADS, 1)
 k_down_mfma(ExpertArgs a) {
     extern __shared__ __align__(16) unsigned char sm[];
@@ -564,7 +564,7 @@ k_down_mfma(ExpertArgs a) {
         down_tile<G>(a, tile_at(a, f % nt), f / nt, sm);
         return;
     }
-    small_down<G, LPR>(a, f - ntb, (int)gridDim.x - ntb);
+    small_down<G, LPR, NDIG>(a, f - ntb, (int)gridDim.x - ntb);
 }
 
 // ------------------------------------------------------ plain Q4 product
@@ -666,12 +666,15 @@ hipError_t allow_lds() {
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= MAX_DEV) return hipErrorInvalidDevice;
     if (g_lds_set[dev].load(std::memory_order_acquire)) return hipSuccess;
-    const struct { const void* f; size_t b; } k[10] = {
-        {(const void*)k_gateup_mfma<64, 32>, gateup_lds<64>(KMAX)}, {(const void*)k_gateup_mfma<64, 64>, gateup_lds<64>(KMAX)},
-        {(const void*)k_gateup_mfma<32, 32>, gateup_lds<32>(KMAX)}, {(const void*)k_gateup_mfma<32, 64>, gateup_lds<32>(KMAX)},
-        {(const void*)k_down_mfma<64, 32>, Lay(KMAX, 64).total}, {(const void*)k_down_mfma<64, 64>, Lay(KMAX, 64).total},
-        {(const void*)k_down_mfma<32, 32>, Lay(KMAX, 32).total}, {(const void*)k_down_mfma<32, 64>, Lay(KMAX, 32).total},
+#define JM_MF(N) \
+        {(const void*)k_gateup_mfma<64, 32, N>, gateup_lds<64>(KMAX)}, {(const void*)k_gateup_mfma<64, 64, N>, gateup_lds<64>(KMAX)}, \
+        {(const void*)k_gateup_mfma<32, 32, N>, gateup_lds<32>(KMAX)}, {(const void*)k_gateup_mfma<32, 64, N>, gateup_lds<32>(KMAX)}, \
+        {(const void*)k_down_mfma<64, 32, N>, Lay(KMAX, 64).total}, {(const void*)k_down_mfma<64, 64, N>, Lay(KMAX, 64).total}, \
+        {(const void*)k_down_mfma<32, 32, N>, Lay(KMAX, 32).total}, {(const void*)k_down_mfma<32, 64, N>, Lay(KMAX, 32).total}
+    const struct { const void* f; size_t b; } k[18] = {
+        JM_MF(4), JM_MF(5),
         {(const void*)k_q4_gemm_mfma<64>, Lay(KMAX, 64).total}, {(const void*)k_q4_gemm_mfma<32>, Lay(KMAX, 32).total}};
+#undef JM_MF
     for (const auto& x : k) {
         e = hipFuncSetAttribute(x.f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)x.b);
         if (e != hipSuccess) return e;
@@ -697,13 +700,17 @@ hipError_t launch_gateup_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st
     const int rb = a.m / GU_ROWS;
     const dim3 grid((unsigned)((max_tiles + 1) * rb));
     const bool l64 = item_lanes(a.d) == 64;
+    if (a.ndig != 4 && a.ndig != 5) return hipErrorInvalidValue;
+#define JM_GM(GG, L) do { if (a.ndig == 5) hipLaunchKernelGGL((k_gateup_mfma<GG, L, 5>), grid, dim3(MTHREADS), gateup_lds<GG>(a.d), st, a); \
+                          else hipLaunchKernelGGL((k_gateup_mfma<GG, L, 4>), grid, dim3(MTHREADS), gateup_lds<GG>(a.d), st, a); } while (0)
     if (a.group == 64) {
-        if (l64) hipLaunchKernelGGL((k_gateup_mfma<64, 64>), grid, dim3(MTHREADS), gateup_lds<64>(a.d), st, a);
-        else hipLaunchKernelGGL((k_gateup_mfma<64, 32>), grid, dim3(MTHREADS), gateup_lds<64>(a.d), st, a);
+        if (l64) JM_GM(64, 64);
+        else JM_GM(64, 32);
     } else {
-        if (l64) hipLaunchKernelGGL((k_gateup_mfma<32, 64>), grid, dim3(MTHREADS), gateup_lds<32>(a.d), st, a);
-        else hipLaunchKernelGGL((k_gateup_mfma<32, 32>), grid, dim3(MTHREADS), gateup_lds<32>(a.d), st, a);
+        if (l64) JM_GM(32, 64);
+        else JM_GM(32, 32);
     }
+#undef JM_GM
     return hipGetLastError();
 }
 
@@ -716,13 +723,17 @@ hipError_t launch_down_mfma(const ExpertArgs& a, int max_tiles, hipStream_t st) 
     const int rb = a.d / DN_BLOCK_ROWS;
     const dim3 grid((unsigned)((max_tiles + 1) * rb));
     const bool l64 = item_lanes(a.m) == 64;
+    if (a.ndig != 4 && a.ndig != 5) return hipErrorInvalidValue;
+#define JM_DM(GG, L) do { if (a.ndig == 5) hipLaunchKernelGGL((k_down_mfma<GG, L, 5>), grid, dim3(MTHREADS), Lay(a.m, GG).total, st, a); \
+                          else hipLaunchKernelGGL((k_down_mfma<GG, L, 4>), grid, dim3(MTHREADS), Lay(a.m, GG).total, st, a); } while (0)
     if (a.group == 64) {
-        if (l64) hipLaunchKernelGGL((k_down_mfma<64, 64>), grid, dim3(MTHREADS), Lay(a.m, 64).total, st, a);
-        else hipLaunchKernelGGL((k_down_mfma<64, 32>), grid, dim3(MTHREADS), Lay(a.m, 64).total, st, a);
+        if (l64) JM_DM(64, 64);
+        else JM_DM(64, 32);
     } else {
-        if (l64) hipLaunchKernelGGL((k_down_mfma<32, 64>), grid, dim3(MTHREADS), Lay(a.m, 32).total, st, a);
-        else hipLaunchKernelGGL((k_down_mfma<32, 32>), grid, dim3(MTHREADS), Lay(a.m, 32).total, st, a);
+        if (l64) JM_DM(32, 64);
+        else JM_DM(32, 32);
     }
+#undef JM_DM
     return hipGetLastError();
 }
 

@@ -434,9 +434,11 @@ hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {
     const bool quad = a.B >= JM_ROUTER_QUAD_MIN_B;
     const dim3 grid((unsigned)ngrp, (unsigned)a.B);
     const dim3 gridq((unsigned)((ngrp + 3) / 4), (unsigned)((a.B + RQ_T - 1) / RQ_T));
-#define JM_RT1(GG, DVV, BF, LY)                                                                          \
-    if (quad) hipLaunchKernelGGL((k_router_quad<GG, JM_NDIG, DVV, BF, LY>), gridq, dim3(256), 0, st, a); \
-    else hipLaunchKernelGGL((k_router_grp<GG, JM_NDIG, DVV, BF, LY>), grid, dim3(64), 0, st, a)
+    if (a.ndig != 4 && a.ndig != 5) return hipErrorInvalidValue;
+#define JM_RTN(GG, N, DVV, BF, LY)                                                                  \
+    if (quad) hipLaunchKernelGGL((k_router_quad<GG, N, DVV, BF, LY>), gridq, dim3(256), 0, st, a); \
+    else hipLaunchKernelGGL((k_router_grp<GG, N, DVV, BF, LY>), grid, dim3(64), 0, st, a)
+#define JM_RT1(GG, DVV, BF, LY) if (a.ndig == 5) { JM_RTN(GG, 5, DVV, BF, LY); } else { JM_RTN(GG, 4, DVV, BF, LY); }
 #define JM_RT(GG, DVV, BF) if (a.xpart || a.norm_w) { JM_RT1(GG, DVV, BF, true); } else { JM_RT1(GG, DVV, BF, false); }
 #define JM_RTB(GG, DVV) if (a.wt_bf16) { JM_RT(GG, DVV, true); } else { JM_RT(GG, DVV, false); }
 #define JM_RTD(GG) switch (a.d / 512) { case 1: JM_RTB(GG, 1); break; case 2: JM_RTB(GG, 2); break; \
@@ -447,6 +449,7 @@ hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {
 #undef JM_RTB
 #undef JM_RT
 #undef JM_RT1
+#undef JM_RTN
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.skip_topk) return e;
     return launch_topk(a.logits, a.B, a.E, a.topk, a.renorm, a.top, a.tw, st);

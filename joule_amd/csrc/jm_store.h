@@ -66,6 +66,7 @@ struct DecKey {
     int nl;                     // layers the step runs (jm_store_set_max_layers)
     int kv_f32;                 // element type of the caches (jm_store_set_kv_dtype)
     int dense_min;
+    int ndig;
     int append;                 // the attention appends the k and v rows itself (no cache shared by two tokens)
 };
 
@@ -90,6 +91,7 @@ struct jm_store {
     int prof;
     hipEvent_t ev[JM_STAGES + 1];
     int dense_min;              // segment size from which an expert takes the MFMA branch
+    int ndig;                   // activation digit planes of the GEMV kernels (jm_store_set_act_digits)
     bool mfma_ok;               // the shape and the records' alignment allow the MFMA branch
     // ---- batch decode (jm_decode_layers_batch) ----
     int max_layers;             // jm_store_set_max_layers: < 0 runs every layer

@@ -157,6 +157,17 @@ class HbmExpertStore:
         with more than 256 slots); 0 restores the default."""
         _lib.check(_lib.lib().jm_store_set_dense_min(self._h, int(min_tokens)), "jm_store_set_dense_min")
 
+    def set_act_digits(self, ndig: int) -> None:
+        """Base-16 digit planes per activation value on the GEMV kernels: 4
+        (the default; 0 restores it, about 15 bits per Q4 group) or 5 (about
+        19 bits, more dot products per weight row).  Routing does not depend
+        on it; the MFMA branch's int8 digit pairs are not affected."""
+        _lib.check(_lib.lib().jm_store_set_act_digits(self._h, int(ndig)), "jm_store_set_act_digits")
+
+    @property
+    def act_digits(self) -> int:
+        return int(_lib.lib().jm_store_act_digits(self._h))
+
     def dense_tiles(self, stream=None) -> int:
         """32-token tiles the MFMA branch computed in the last call."""
         t = torch.zeros(1, dtype=torch.int32, device=self.blob.device)

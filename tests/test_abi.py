@@ -142,6 +142,16 @@ def test_ctypes_argument_counts_match_the_header():
         assert n == len(_lib.SIGNATURES[name][0]), (name, n, len(_lib.SIGNATURES[name][0]))
 
 
+def test_act_digits_setting_null_store():
+    """The digit-plane setting refuses a NULL store and reports -1 for it.
+    No GPU work."""
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libjoule_amd.so not built")
+    L = _lib.lib()
+    assert L.jm_store_set_act_digits(None, 5) < 0
+    assert L.jm_store_act_digits(None) == -1
+
+
 def test_q4_gemm_min_tokens_setting():
     """The plugin product's kernel threshold: process-wide, 0 restores the
     default (the measured crossover, 22 tokens), negative is an error.  No

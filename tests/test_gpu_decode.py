@@ -385,3 +385,35 @@ def test_decode_graph_follows_router_dtype_and_max_layers():
     rel = np.abs(full - trace[1]["hidden"]).max(axis=1) / np.abs(trace[1]["hidden"]).max(axis=1)
     assert rel.max() <= TOL, rel
     dec.store.close()
+
+
+def test_decode_five_digits_and_graph_key():
+    """The decode step with 5 activation digit planes: within the tolerance
+    of the oracle, graph replay equal to the eager step, and a change of the
+    setting records a new graph (the 4-digit replay equals the 4-digit eager
+    step, not the 5-digit one)."""
+    shape = qwen3_30b_a3b(n_layers=2, maxT=2176)
+    B = 4
+    dec, oracle, kv = _model(shape, 64, B)
+    kv_h = _kv_host(kv, B, shape.n_layers)
+    x = activations(B, shape.d)
+    positions = [5, 300, 1000, 2048]
+    st = dec.store
+    try:
+        st.set_act_digits(5)
+        err5 = _check_step(dec, oracle, kv, kv_h, x, positions, "five digits")
+        xd = torch.from_numpy(x).cuda()
+        want = {}
+        for nd in (5, 4):
+            st.set_act_digits(nd)
+            dec.set_graph(False)
+            want[nd] = dec.decode_layers_batch(xd, positions, kv, torch.empty_like(xd)).clone()
+            dec.set_graph(True)
+            got = dec.decode_layers_batch(xd, positions, kv, torch.empty_like(xd)).clone()
+            torch.cuda.synchronize()
+            assert torch.equal(got, want[nd]), f"{nd} digits: graph replay differs from the eager step"
+        assert not torch.equal(want[4], want[5])
+        print(f"  five-digit step error {err5:.3e}", flush=True)
+    finally:
+        st.set_act_digits(0)
+        dec.store.close()
