@@ -23,7 +23,9 @@ Reported (one JSON line):
   stages       average milliseconds of each kernel
   router_margins  per token and layer, (p8 - p9) / p8 of the router softmax
                (how far each selection is from a tie)
-  sweep        the same measurement at B=1 and B=32 (Qwen3), OLMoE B=1/8, the
+  sweep        the same measurement at B=1 and B=32 (Qwen3), OLMoE B=1/8 (Q4
+               blocks of 32 values and a float32 router table, as those
+               configurations are stated), the
                prefill-style Qwen3 block: 512 tokens with Zipf(1.1)-biased
                routing, whose large segments take the MFMA branch, and the
                full 48-layer Qwen3-30B-A3B decode step at B=8 (attention over
@@ -200,7 +202,7 @@ def block_parity(store, moes, x_np, layers) -> dict:
             "ok": bool(nerr <= PARITY_TOL and top_ok == n and tw_ok == n)}
 
 
-def build_layers(shape, n_layers, group, seed):
+def build_layers(shape, n_layers, group, seed, router_bf16=True):
     import numpy as np
     import torch
 
@@ -209,7 +211,7 @@ def build_layers(shape, n_layers, group, seed):
 
     blob, offsets = torch_store(shape, n_layers, group, seed)
     store = HbmExpertStore(shape, n_layers, blob, offsets, group)
-    gw = np.stack([router_weights(shape, l) for l in range(n_layers)])
+    gw = np.stack([router_weights(shape, l, bf16=router_bf16) for l in range(n_layers)])
     store.set_router(torch.from_numpy(gw).cuda())
     torch.cuda.synchronize()
     return store, gw
@@ -1034,16 +1036,20 @@ def main() -> int:
     if not args.no_sweep:
         del store
         torch.cuda.empty_cache()
-        ostore, ogw = build_layers(OLMOE, NL, G, seed=1000)
+        # the OLMoE-shaped configurations as stated: Q4 blocks of 32 values,
+        # the router table left float32
+        GO = 32
+        ostore, ogw = build_layers(OLMOE, NL, GO, seed=1000, router_bf16=False)
         omoes = oracle_moes(ostore, ogw, NL) if (cpu_on or check) else None
         for b in (1, 8):
             xo_np = activations(b, OLMOE.d)
             xb = torch.from_numpy(xo_np).cuda()
             m2, st2, U2, d2 = measure(ostore, ogw, xb, max(args.steps // 2, 50), 10, NL)
-            r = block_numbers(OLMOE, G, b, m2, st2, U2, max(args.steps // 2, 50), NL,
+            r = block_numbers(OLMOE, GO, b, m2, st2, U2, max(args.steps // 2, 50), NL,
                               ostore.router_bytes_per_weight())
             sweep[f"olmoe_B{b}"] = {k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac",
                                                       "gateup_GBs", "experts_routed_avg")}
+            sweep[f"olmoe_B{b}"].update({"group": GO, "router": "float32"})
             sweep[f"olmoe_B{b}"]["per_call_us"] = d2
             log(f"sweep olmoe B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s, per call {d2}")
             if check:

@@ -36,9 +36,12 @@ def bf16_round(a: np.ndarray) -> np.ndarray:
     return out.astype(np.float32)
 
 
-def router_weights(shape: MoEShape, layer: int, seed: int = 2000) -> np.ndarray:
+def router_weights(shape: MoEShape, layer: int, seed: int = 2000, bf16: bool = True) -> np.ndarray:
+    """N(0, 0.02) router table [E, d] of one layer, rounded to bf16 values
+    (a bf16 checkpoint's gate) or, with bf16=False, left float32."""
     rng = np.random.default_rng(seed + layer)
-    return bf16_round(rng.normal(0.0, 0.02, (shape.E, shape.d)).astype(np.float32))
+    w = rng.normal(0.0, 0.02, (shape.E, shape.d)).astype(np.float32)
+    return bf16_round(w) if bf16 else w
 
 
 def activations(B: int, d: int, seed: int = 3000) -> np.ndarray:
