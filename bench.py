@@ -23,9 +23,10 @@ Reported (one JSON line):
   stages       average milliseconds of each kernel
   router_margins  per token and layer, (p8 - p9) / p8 of the router softmax
                (how far each selection is from a tie)
-  sweep        the same measurement at B=1 and B=32 (Qwen3), OLMoE B=1/8 (Q4
-               blocks of 32 values and a float32 router table, as those
-               configurations are stated), the
+  sweep        the same measurement at B=1 and B=32 (Qwen3), the headline
+               batch at Q4 groups of 32 (qwen3_B8_G32), OLMoE B=1/8 (a
+               float32 router table, as those configurations state; Q4
+               groups of 64 and, as _G32, of 32), the
                prefill-style Qwen3 block: 512 tokens with Zipf(1.1)-biased
                routing, whose large segments take the MFMA branch, and the
                full 48-layer Qwen3-30B-A3B decode step at B=8 (attention over
@@ -1036,33 +1037,52 @@ def main() -> int:
     if not args.no_sweep:
         del store
         torch.cuda.empty_cache()
-        # the OLMoE-shaped configurations as stated: Q4 blocks of 32 values,
-        # the router table left float32
-        GO = 32
-        ostore, ogw = build_layers(OLMOE, NL, GO, seed=1000, router_bf16=False)
-        omoes = oracle_moes(ostore, ogw, NL) if (cpu_on or check) else None
-        for b in (1, 8):
-            xo_np = activations(b, OLMOE.d)
-            xb = torch.from_numpy(xo_np).cuda()
-            m2, st2, U2, d2 = measure(ostore, ogw, xb, max(args.steps // 2, 50), 10, NL)
-            r = block_numbers(OLMOE, GO, b, m2, st2, U2, max(args.steps // 2, 50), NL,
-                              ostore.router_bytes_per_weight())
-            sweep[f"olmoe_B{b}"] = {k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac",
-                                                      "gateup_GBs", "experts_routed_avg")}
-            sweep[f"olmoe_B{b}"].update({"group": GO, "router": "float32"})
-            sweep[f"olmoe_B{b}"]["per_call_us"] = d2
-            log(f"sweep olmoe B={b}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s, per call {d2}")
-            if check:
-                sweep[f"olmoe_B{b}"]["parity"] = parity[f"olmoe_B{b}"] = block_parity(ostore, omoes, xo_np,
-                                                                                     list(range(NL)))
-                log(f"parity olmoe B={b}: {parity[f'olmoe_B{b}']}")
-            if cpu_on:
-                cpu_sweep[f"olmoe_B{b}"] = cpu_case(omoes, xo_np, cpu_share, f"olmoe B={b}")[0]
-        del omoes
+        # the OLMoE-shaped configurations: the router table left float32 as
+        # they state; Q4 groups of 64 (the reference store's and decode
+        # kernel's group) and of 32 (the configurations' wording)
+        for GO in (64, 32):
+            ostore, ogw = build_layers(OLMOE, NL, GO, seed=1000, router_bf16=False)
+            omoes = oracle_moes(ostore, ogw, NL) if (cpu_on or check) else None
+            sfx = "" if GO == 64 else f"_G{GO}"
+            for b in (1, 8):
+                key = f"olmoe_B{b}{sfx}"
+                xo_np = activations(b, OLMOE.d)
+                xb = torch.from_numpy(xo_np).cuda()
+                m2, st2, U2, d2 = measure(ostore, ogw, xb, max(args.steps // 2, 50), 10, NL)
+                r = block_numbers(OLMOE, GO, b, m2, st2, U2, max(args.steps // 2, 50), NL,
+                                  ostore.router_bytes_per_weight())
+                sweep[key] = {k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac",
+                                                "gateup_GBs", "experts_routed_avg")}
+                sweep[key].update({"group": GO, "router": "float32"})
+                sweep[key]["per_call_us"] = d2
+                log(f"sweep {key}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s, per call {d2}")
+                if check:
+                    sweep[key]["parity"] = parity[key] = block_parity(ostore, omoes, xo_np, list(range(NL)))
+                    log(f"parity {key}: {parity[key]}")
+                if cpu_on:
+                    cpu_sweep[key] = cpu_case(omoes, xo_np, cpu_share, key)[0]
+            del omoes, ostore
+            torch.cuda.empty_cache()
+        # the metric's Qwen3 block at Q4 groups of 32 (the configurations'
+        # wording; the headline is at the reference store's 64)
+        qstore, qgw = build_layers(QWEN3, NL, 32, seed=1000)
+        qmoes = oracle_moes(qstore, qgw, NL) if (cpu_on or check) else None
+        m2, st2, U2, d2 = measure(qstore, qgw, x, max(args.steps // 2, 50), 10, NL)
+        r = block_numbers(QWEN3, 32, B, m2, st2, U2, max(args.steps // 2, 50), NL, qstore.router_bytes_per_weight())
+        key = f"qwen3_B{B}_G32"
+        sweep[key] = {k: r[k] for k in ("tok_per_s", "ms_per_step", "block_GBs", "block_frac", "gateup_GBs",
+                                        "experts_routed_avg")}
+        sweep[key].update({"group": 32, "per_call_us": d2})
+        log(f"sweep {key}: {r['tok_per_s']:.0f} tok/s, block {r['block_GBs']:.0f} GB/s, per call {d2}")
+        if check:
+            sweep[key]["parity"] = parity[key] = block_parity(qstore, qmoes, x_np, list(range(NL)))
+            log(f"parity {key}: {parity[key]}")
+        if cpu_on:
+            cpu_sweep[key] = cpu_case(qmoes, x_np, cpu_share, key)[0]
+        del qmoes, qstore
+        torch.cuda.empty_cache()
 
     if not args.no_sweep:
-        del ostore
-        torch.cuda.empty_cache()
         sweep["qwen3_decode48_B8"] = decode_step(8, max(args.steps // 20, 10), 3, G)
         sweep["plugin_q4_gemm"] = plugin_q4_gemm(G)
 
