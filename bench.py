@@ -643,16 +643,24 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176, 
     return res
 
 
-def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 2, 4, 8, 12, 16, 20, 24, 28, 32, 33, 36, 48, 64, 512),
-                   reps=200):
+def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 2, 4, 6, 7, 8, 12, 16, 20, 24, 28, 32, 33, 36, 48, 64, 512),
+                   reps=100, rounds=5):
     """The plugin product HipBackend.q4_gemm (jm_q4_gemm_f32, the reference's
     q4_gemm_f32) on one Qwen3 expert matrix shape (m=768 rows of d=2048),
-    at each token count T: microseconds per call on the stream (inputs and
-    the packed matrix resident on the GPU; the workspace cached after the
-    first call) with the library's own choice of kernel, and with each of the
-    two kernels forced (the v_dot8 digit kernel, the int8 matrix cores), from
-    which the crossover is read.  At T = 1 the host-side time of a call
-    (enqueue and wait) is reported beside the GPU's."""
+    at each token count T (inputs and the packed matrix resident on the GPU;
+    the workspace cached after the first call), with the library's own
+    choice of kernel and with each of the two kernels forced (the v_dot8
+    digit kernel, the int8 matrix cores), from which the crossover is read.
+
+    `us_per_call` is the GPU's time per call: a bounded spin kernel
+    (torch.cuda._sleep) holds the stream while the host enqueues the `reps`
+    calls, so that they run back to back whatever the host's pace; an event
+    query after the enqueue confirms that the GPU had not reached the calls
+    yet (`queued_ahead`).  Median of `rounds` such runs.  `host_paced_us`
+    is the same calls enqueued with the stream idle (each call's host work
+    and launches on the critical path: the rate a caller issuing one call
+    after another sees), and at T = 1 the host-side time of one call
+    enqueued and waited for is reported too."""
     import numpy as np
     import torch
 
@@ -669,33 +677,63 @@ def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 2, 4, 8, 12, 16, 20, 24, 28, 
     st = torch.cuda.current_stream()
     default_min = L.jm_get_q4_gemm_min_tokens()
 
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    # the spin kernel's microseconds per requested cycle
+    torch.cuda._sleep(1000)
+    torch.cuda.synchronize()
+    e0.record(st)
+    torch.cuda._sleep(1_000_000)
+    e1.record(st)
+    torch.cuda.synchronize()
+    us_per_cycle = e0.elapsed_time(e1) * 1e3 / 1_000_000
+
+    def run(y, X, hold_cycles):
+        if hold_cycles:
+            torch.cuda._sleep(hold_cycles)
+        e0.record(st)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            be.q4_gemm(y, X, pk, sc, m, d, group)
+        host_us = (time.perf_counter() - t0) * 1e6
+        e1.record(st)
+        ahead = not e0.query()          # the GPU still in the spin when the last call was enqueued
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps, host_us, ahead
+
     def time_calls(y, X, min_t):
+        """(GPU us per call, its spread over the rounds, host-paced us per
+        call, every run queued ahead)"""
         _lib.check(L.jm_set_q4_gemm_min_tokens(min_t), "jm_set_q4_gemm_min_tokens")
         for _ in range(5):
             be.q4_gemm(y, X, pk, sc, m, d, group)
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        for _ in range(reps):
-            be.q4_gemm(y, X, pk, sc, m, d, group)
-        e1.record(st)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / reps
+        paced, host_us, _ = run(y, X, 0)
+        # hold the stream for twice the host's enqueue time of the calls
+        hold = max(1000, int(2.0 * host_us / us_per_cycle))
+        gpu, ahead = [], True
+        for _ in range(rounds):
+            us, _, a = run(y, X, hold)
+            gpu.append(us)
+            ahead = ahead and a
+        return float(np.median(gpu)), float(max(gpu) - min(gpu)), paced, ahead
 
     out = {}
     try:
         for T in sizes:
             X = torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).cuda()
             y = torch.empty((T, m), dtype=torch.float32, device="cuda")
-            dot8_us = time_calls(y, X, 1 << 30)
-            mfma_us = time_calls(y, X, 1)
-            us = time_calls(y, X, 0)
+            dot8_us, _, _, a1 = time_calls(y, X, 1 << 30)
+            mfma_us, _, _, a2 = time_calls(y, X, 1)
+            us, spread, paced, a3 = time_calls(y, X, 0)
             nbytes = m * d // 2 + m * (d // group) * 2 + T * d * 4 + T * m * 4
             path = "mfma_i8" if T >= default_min else "dot8_digits"
-            out[f"T{T}"] = {"us_per_call": us, "bytes": nbytes, "GBs": nbytes / (us * 1e-6) / 1e9, "path": path,
-                            "dot8_us": dot8_us, "mfma_us": mfma_us,
+            out[f"T{T}"] = {"us_per_call": us, "spread_us": spread, "host_paced_us": paced, "bytes": nbytes,
+                            "GBs": nbytes / (us * 1e-6) / 1e9, "path": path,
+                            "dot8_us": dot8_us, "mfma_us": mfma_us, "queued_ahead": a1 and a2 and a3,
                             "tflops_equiv": 2.0 * T * m * d / (us * 1e-6) / 1e12}
-            log(f"plugin q4_gemm m={m} d={d} T={T}: {us:.1f} us ({path}); dot8 {dot8_us:.1f}, mfma {mfma_us:.1f}")
+            log(f"plugin q4_gemm m={m} d={d} T={T}: {us:.2f} us ({path}; host-paced {paced:.2f}); "
+                f"dot8 {dot8_us:.2f}, mfma {mfma_us:.2f}")
             if T == 1:
                 # host-side: each call enqueued and waited for
                 hs = []
@@ -714,8 +752,13 @@ def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 2, 4, 8, 12, 16, 20, 24, 28, 
         if all(out[f"T{u}"]["mfma_us"] <= out[f"T{u}"]["dot8_us"] for u in ts if u >= t):
             cross = t
             break
+    gpu_us = [out[f"T{t}"]["us_per_call"] for t in ts]
     return {"m": m, "d": d, "group": group, "default_min_tokens": default_min, "measured_crossover_T": cross,
-            "sizes": out}
+            "us_per_call_monotone_in_T": all(b >= a for a, b in zip(gpu_us, gpu_us[1:])),
+            # the most by which a size's time exceeds that of a larger size (sizes within one
+            # 32-token tile do the same work on the matrix cores and differ by noise)
+            "max_inversion_us": max(0.0, max(gpu_us[i] - min(gpu_us[i + 1:]) for i in range(len(ts) - 1))),
+            "queued_ahead": all(v["queued_ahead"] for v in out.values()), "sizes": out}
 
 
 def dense_step(B, steps, warmup, n_layers=36, position=2048, maxT=2176):
@@ -880,7 +923,7 @@ def main() -> int:
     ap.add_argument("--zipf-only", action="store_true",
                     help="only the 512-token Zipf-routed block (MFMA branch) on the 16-layer store; prints its JSON")
     ap.add_argument("--plugin-only", action="store_true",
-                    help="only the plugin product HipBackend.q4_gemm at T = 1, 32, 33, 36, 512; prints its JSON")
+                    help="only the plugin product HipBackend.q4_gemm at T = 1 to 512 (both kernels); prints its JSON")
     ap.add_argument("--probe", action="store_true",
                     help="only the launch and hand-off cost probes (libjoule_probe.so); prints their JSON")
     ap.add_argument("--no-parity", action="store_true",

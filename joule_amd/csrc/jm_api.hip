@@ -762,7 +762,7 @@ int jm_q4_gemm_f32(float* out, const float* X, int T, const uint8_t* packed, con
     const size_t ng = (size_t)d / group;
     const size_t dig_bytes = align256((size_t)T * ng * JM_NDIG * (group / 8) * 4);
     const size_t sc_bytes = align256((size_t)T * ng * 4);
-    const size_t need = mfma ? jm::q4_gemm_mfma_ws(T, d, group) : dig_bytes + sc_bytes;
+    const size_t need = mfma ? jm::q4_gemm_mfma_ws(T, m, d, group) : dig_bytes + sc_bytes;
     PluginWs ws;
     if (int rc = plugin_ws(st, need, &ws)) return rc;
     hipError_t e;

@@ -171,9 +171,12 @@ bool q4_gemm_mfma_ok(int m, int d, int group);
 // default token count from which jm_q4_gemm_f32 takes the matrix cores
 // (jm_set_q4_gemm_min_tokens changes it): the measured crossover
 #ifndef JM_Q4_GEMM_MIN_T
-#define JM_Q4_GEMM_MIN_T 22
+#define JM_Q4_GEMM_MIN_T 7
 #endif
-size_t q4_gemm_mfma_ws(int T, int d, int group);
+// K splits the product takes at this shape (1: none); their partial sums
+// are part of the workspace
+int q4_gemm_splits(int T, int m, int d);
+size_t q4_gemm_mfma_ws(int T, int m, int d, int group);
 hipError_t launch_q4_gemm_mfma(const uint8_t* packed, const uint16_t* scales, const float* X, int T, int m, int d,
                                int group, void* ws, float* out, hipStream_t st);
 // out[b] = (resid[b] +) sum of the token's slots of y in the order comb gives

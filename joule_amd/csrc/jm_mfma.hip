@@ -126,13 +126,13 @@ __device__ __forceinline__ void stage_phase(const int8_t* __restrict__ hi, const
     }
 }
 
-// The tile's token scales and group-sum corrections over all of K
-// (padding tokens, i >= nt: 0).
+// The tile's token scales and group-sum corrections of ng groups (padding
+// tokens, i >= nt: 0); token row r's groups start at r * stride.
 __device__ __forceinline__ void stage_scales(const float* __restrict__ sc, const int* __restrict__ qc, const int* src,
-                                             int nt, int ng, float* s, int* c) {
+                                             int nt, int ng, int stride, float* s, int* c) {
     for (int u = threadIdx.x; u < ng * MT; u += MTHREADS) {
         const int g = u / MT, i = u % MT;
-        const size_t o = (size_t)src[i] * ng + g;
+        const size_t o = (size_t)src[i] * stride + g;
         s[u] = i < nt ? sc[o] : 0.0f;
         c[u] = i < nt ? -8 * qc[o] : 0;
     }
@@ -416,7 +416,7 @@ __device__ __forceinline__ void gateup_tile(const ExpertArgs& a, const TileInfo&
     ws.load(1, 1);
     __syncthreads();
     stage_phase(a.xqh, a.xql, tok, d, 0, ly.kph, q);
-    stage_scales(a.xqs, a.xqc, tok, ti.nt, ng, s, cc);
+    stage_scales(a.xqs, a.xqc, tok, ti.nt, ng, ng, s, cc);
     __syncthreads();
     floatx16 acc = {};
     wave_product<G>(acc, ws, wl, q, s, cc, TokSrc{a.xqh, a.xql, tok, d}, ly);
@@ -524,7 +524,7 @@ __device__ __forceinline__ void down_tile(const ExpertArgs& a, const TileInfo& t
     int row = start(0);
     __syncthreads();
     stage_phase(a.aqh, a.aql, tok, m, 0, ly.kph, q);
-    stage_scales(a.aqs, a.aqc, tok, ti.nt, ng, s, cc);
+    stage_scales(a.aqs, a.aqc, tok, ti.nt, ng, ng, s, cc);
     __syncthreads();
     // the staged act digits serve DN_BLOCK_ROWS / DN_ROWS passes over the rows
 #pragma unroll 1
@@ -571,20 +571,24 @@ k_down_mfma(ExpertArgs a) {
 
 // out[t][row] = X[t] . dequant(W[row]) for one Q4 matrix (the plugin
 // product q4_gemm_f32, expert_ffn.c:200-215, at prefill-sized T): block
-// (32-token tile, npass x 256 rows), 8 waves x 32 rows per pass over the
-// tile's staged digits, as the down kernel without routing.  The digits of X
-// come from k_prep_i8.
+// (32-token tile, npass x 256 rows, K split z), 8 waves x 32 rows per pass
+// over the tile's staged digits, as the down kernel without routing.  The
+// digits of X come from k_prep_i8.  With gridDim.z > 1 split z covers the
+// columns [z kl, z kl + kl) (whole Q4 groups and super-stages) and writes
+// its partial sums to out + z T m, which k_sum_splits adds in split order.
 template <int G>
 __global__ void __launch_bounds__(MTHREADS, 1)
 k_q4_gemm_mfma(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scales,
                const int8_t* __restrict__ xqh, const int8_t* __restrict__ xql, const float* __restrict__ xqs,
-               const int* __restrict__ xqc, int T, int m, int d, int npass, float* __restrict__ out) {
+               const int* __restrict__ xqc, int T, int m, int d, int kl, int npass, float* __restrict__ out) {
     extern __shared__ __align__(16) unsigned char sm[];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int ng = d / G;
-    const Lay ly(d, G);
+    const int ng = d / G;                         // groups per row (the scales' row stride)
+    const int k0 = (int)blockIdx.z * kl;          // the split's first column
+    const Lay ly(kl, G);
     const int t0 = blockIdx.x * MT;
     const int nt = min(MT, T - t0);
+    float* const o = out + (size_t)blockIdx.z * T * m;
     int8_t* q = (int8_t*)sm;
     float* s = (float*)(sm + ly.s);
     int* cc = (int*)(sm + ly.c);
@@ -594,33 +598,55 @@ k_q4_gemm_mfma(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ 
     const int n = lane & 31, h = lane >> 5;
     WStream<G> ws;
     ws.rowb = d / 2;
-    ws.nss = d / SSC;
+    ws.nss = kl / SSC;
     auto start = [&](int pass) __attribute__((always_inline)) {
         const int wrow0 = (blockIdx.y * npass + pass) * DN_ROWS + 32 * w;
-        ws.wbase = packed + (size_t)wrow0 * (d / 2);
-        ws.srow = (const uint8_t*)scales + (size_t)(wrow0 + n) * ng * 2;
+        ws.wbase = packed + (size_t)wrow0 * (d / 2) + k0 / 2;
+        ws.srow = (const uint8_t*)scales + ((size_t)(wrow0 + n) * ng + k0 / G) * 2;
         ws.load(0, 0);
         ws.load(1, 1);
         return wrow0 + n;
     };
     int row = start(0);
     __syncthreads();
-    stage_phase(xqh, xql, tok, d, 0, ly.kph, q);
-    stage_scales(xqs, xqc, tok, nt, ng, s, cc);
+    stage_phase(xqh + k0, xql + k0, tok, d, 0, ly.kph, q);
+    stage_scales(xqs + k0 / G, xqc + k0 / G, tok, nt, kl / G, ng, s, cc);
     __syncthreads();
 #pragma unroll 1
     for (int pass = 0; pass < npass; pass++) {
         floatx16 acc = {};
         // (operands one stage ahead would spill this kernel's registers)
-        wave_product<G, false>(acc, ws, wl, q, s, cc, TokSrc{xqh, xql, tok, d}, ly);
+        wave_product<G, false>(acc, ws, wl, q, s, cc, TokSrc{xqh + k0, xql + k0, tok, d}, ly);
         const int r = row;
         if (pass + 1 < npass) row = start(pass + 1);
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int i = 8 * (v / 4) + 4 * h + (v % 4);
-            if (i < nt) out[(size_t)(t0 + i) * m + r] = acc[v];
+            if (i < nt) o[(size_t)(t0 + i) * m + r] = acc[v];
         }
     }
+}
+
+// out[i] = the sum of the ns partial products part[z][i], z = 0, 1, ... in
+// order (n4 float4 elements each).
+__global__ void __launch_bounds__(256)
+k_sum_splits(const float4* __restrict__ part, long long n4, int ns, float4* __restrict__ out) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    float4 v[8];
+#pragma unroll
+    for (int z = 0; z < 8; z++)
+        if (z < ns) v[z] = part[(size_t)z * n4 + i];
+    float4 r = v[0];
+#pragma unroll
+    for (int z = 1; z < 8; z++)
+        if (z < ns) {
+            r.x = __fadd_rn(r.x, v[z].x);
+            r.y = __fadd_rn(r.y, v[z].y);
+            r.z = __fadd_rn(r.z, v[z].z);
+            r.w = __fadd_rn(r.w, v[z].w);
+        }
+    out[i] = r;
 }
 
 // Int8 digit pairs and scales of T rows of d floats, one G-lane segment per
@@ -746,8 +772,23 @@ bool q4_gemm_mfma_ok(int m, int d, int group) {
            ((d / group) * 2) % (group == 64 ? 8 : 16) == 0;
 }
 
-size_t q4_gemm_mfma_ws(int T, int d, int group) {
-    return pad256((size_t)T * d) * 2 + pad256((size_t)T * (d / group) * 4) * 2;
+// K splits of the plain product: when the grid of token tiles x row blocks
+// would leave most of the 256 CUs idle, ns blocks share each one's
+// contraction (ns a divisor of the super-stages over d, at most 8): the
+// smallest ns that fills one round of 256 blocks, else the largest.
+int q4_gemm_splits(int T, int m, int d) {
+    const long long blocks = (long long)((T + MT - 1) / MT) * (m / DN_ROWS);
+    const int nss = d / SSC;
+    int ns = 1;
+    for (int c = 2; c <= 8 && blocks * ns < 256; c++)
+        if (nss % c == 0 && mfma_k_ok(d / c)) ns = c;
+    return ns;
+}
+
+size_t q4_gemm_mfma_ws(int T, int m, int d, int group) {
+    const int ns = q4_gemm_splits(T, m, d);
+    return pad256((size_t)T * d) * 2 + pad256((size_t)T * (d / group) * 4) * 2 +
+           (ns > 1 ? pad256((size_t)ns * T * m * 4) : 0);
 }
 
 hipError_t launch_q4_gemm_mfma(const uint8_t* packed, const uint16_t* scales, const float* X, int T, int m, int d,
@@ -760,20 +801,29 @@ hipError_t launch_q4_gemm_mfma(const uint8_t* packed, const uint16_t* scales, co
     int8_t* lo = hi + pad256((size_t)T * d);
     float* sc = (float*)(lo + pad256((size_t)T * d));
     int* qc = (int*)((char*)sc + pad256((size_t)T * (d / group) * 4));
+    float* part = (float*)((char*)qc + pad256((size_t)T * (d / group) * 4));
     const long long lanes = (long long)T * d;
     const unsigned pblocks = (unsigned)((lanes + 255) / 256);
+    const int ns = q4_gemm_splits(T, m, d);
+    const int kl = d / ns;
+    float* dst = ns > 1 ? part : out;
     // two passes per block when the rows allow and the grid still fills the chip
     const int tiles = (T + MT - 1) / MT;
     const int npass = (m % (2 * DN_ROWS) == 0 && (long long)tiles * (m / (2 * DN_ROWS)) >= 256) ? 2 : 1;
-    const dim3 grid((unsigned)tiles, (unsigned)(m / (DN_ROWS * npass)));
+    const dim3 grid((unsigned)tiles, (unsigned)(m / (DN_ROWS * npass)), (unsigned)ns);
     if (group == 64) {
         hipLaunchKernelGGL(k_prep_i8<64>, dim3(pblocks), dim3(256), 0, st, X, T, d, hi, lo, sc, qc);
-        hipLaunchKernelGGL(k_q4_gemm_mfma<64>, grid, dim3(MTHREADS), Lay(d, 64).total, st, packed, scales, hi, lo, sc,
-                           qc, T, m, d, npass, out);
+        hipLaunchKernelGGL(k_q4_gemm_mfma<64>, grid, dim3(MTHREADS), Lay(kl, 64).total, st, packed, scales, hi, lo, sc,
+                           qc, T, m, d, kl, npass, dst);
     } else {
         hipLaunchKernelGGL(k_prep_i8<32>, dim3(pblocks), dim3(256), 0, st, X, T, d, hi, lo, sc, qc);
-        hipLaunchKernelGGL(k_q4_gemm_mfma<32>, grid, dim3(MTHREADS), Lay(d, 32).total, st, packed, scales, hi, lo, sc,
-                           qc, T, m, d, npass, out);
+        hipLaunchKernelGGL(k_q4_gemm_mfma<32>, grid, dim3(MTHREADS), Lay(kl, 32).total, st, packed, scales, hi, lo, sc,
+                           qc, T, m, d, kl, npass, dst);
+    }
+    if (ns > 1) {
+        const long long n4 = (long long)T * m / 4;
+        hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float4*)part, n4,
+                           ns, (float4*)out);
     }
     return hipGetLastError();
 }

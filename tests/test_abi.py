@@ -154,17 +154,17 @@ def test_act_digits_setting_null_store():
 
 def test_q4_gemm_min_tokens_setting():
     """The plugin product's kernel threshold: process-wide, 0 restores the
-    default (the measured crossover, 22 tokens), negative is an error.  No
+    default (the measured crossover, 7 tokens), negative is an error.  No
     GPU work."""
     if not _lib.LIB_PATH.exists():
         pytest.skip("libjoule_amd.so not built")
     L = _lib.lib()
-    assert L.jm_get_q4_gemm_min_tokens() == 22
+    assert L.jm_get_q4_gemm_min_tokens() == 7
     try:
         assert L.jm_set_q4_gemm_min_tokens(-1) == -1
-        assert L.jm_get_q4_gemm_min_tokens() == 22
+        assert L.jm_get_q4_gemm_min_tokens() == 7
         assert L.jm_set_q4_gemm_min_tokens(5) == 0
         assert L.jm_get_q4_gemm_min_tokens() == 5
     finally:
         assert L.jm_set_q4_gemm_min_tokens(0) == 0
-    assert L.jm_get_q4_gemm_min_tokens() == 22
+    assert L.jm_get_q4_gemm_min_tokens() == 7

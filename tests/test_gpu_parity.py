@@ -579,11 +579,16 @@ def test_block_empty_and_errors(qwen64):
 # ----------------------------------------------------------------- backend
 
 @pytest.mark.parametrize("group", [64, 32])
-@pytest.mark.parametrize("m,d,T", [(768, 2048, 1), (2048, 768, 3), (1024, 2048, 7), (768, 2048, 21),
-                                   # from 22 tokens (the default crossover) the matrix cores (m a
+@pytest.mark.parametrize("m,d,T", [(768, 2048, 1), (2048, 768, 3), (1024, 2048, 6),
+                                   # from 7 tokens (the default crossover) the matrix cores (m a
                                    # multiple of 256): whole and partial 32-token tiles, one and two
                                    # 256-row passes per block
+                                   (1024, 2048, 7), (768, 2048, 21),
                                    (768, 2048, 22), (768, 2048, 33), (2048, 768, 70), (8192, 512, 512),
+                                   # the contraction split over 8, 2 and 4 blocks per tile and row block
+                                   # (fewer than 256 blocks otherwise; 2048 x 768 above: 3), the partial
+                                   # sums added afterwards
+                                   (256, 2048, 30), (8192, 512, 128), (8192, 1024, 64),
                                    # shapes the matrix-core kernel does not take: the digit kernel
                                    (1000, 2048, 40), (768, 1536, 36)])
 def test_hip_backend_q4_gemm(gpu, oracle_lib, group, m, d, T):
