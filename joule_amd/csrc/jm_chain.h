@@ -34,6 +34,32 @@ struct Chain {
         for (int i = 0; i < CP; i++) buf[i] = p[(size_t)i * 64];
     }
 
+    // The same for NT tokens at once (staged rows xr[t]): every token's x
+    // values of the chunk are read first, then each weight value is applied
+    // to the NT chains in turn, so that NT independent chains are in flight
+    // (each chain's values still in order).
+    template <int NT>
+    static __device__ __forceinline__ void fma_chunk_n(const uint4 (&buf)[CP], const float* const (&xr)[NT], int c,
+                                                       float (&acc)[NT]) {
+        constexpr int NV = CP * P;                    // values per chunk
+        float4 xq[NT][NV / 4];
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int i = 0; i < NV / 4; i++) xq[t][i] = ((const float4*)xr[t] + (size_t)c * NV / 4)[i];
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+            const unsigned wd = ((const unsigned*)&buf[v / P])[WBF16 ? (v % P) / 2 : v % P];
+            const float wv = WBF16 ? __uint_as_float((v & 1) ? (wd & 0xFFFF0000u) : (wd << 16)) : __uint_as_float(wd);
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const float4 q = xq[t][v / 4];
+                const float xv = (v & 3) == 0 ? q.x : (v & 3) == 1 ? q.y : (v & 3) == 2 ? q.z : q.w;
+                acc[t] = __builtin_fmaf(wv, xv, acc[t]);
+            }
+        }
+    }
+
     // acc += chunk c of the chain (values in order), x from the staged row
     static __device__ __forceinline__ float fma_chunk(const uint4 (&buf)[CP], const float* xr, int c,
                                                       float acc) {

@@ -279,10 +279,15 @@ k_router_quad(RouteArgs a) {
 #pragma unroll
         for (int i = 0; i < XV; i++) xv[i] = xb[lane + 64 * i];
     }
+    __builtin_amdgcn_sched_barrier(0);      // the token's loads ahead of the table's
+    // The table's first chunks, unconditionally (group 0 stands in for a
+    // wave past the last group): behind a branch, the staging below would
+    // wait for every table load as well as the token's.
     uint4 buf[NB][C::CP];
-    if (chains) {
+    {
+        const int egl = chains ? eg : 0;
 #pragma unroll
-        for (int c = 0; c < NB; c++) C::load(buf[c], wt, eg, c, lane);
+        for (int c = 0; c < NB; c++) C::load(buf[c], wt, egl, c, lane);
     }
     {
         const int b = bw;
@@ -378,14 +383,15 @@ k_router_quad(RouteArgs a) {
 #pragma unroll
         for (int t = 0; t < RQ_T; t++) acc[t] = 0.0f;
         // each token's chain in k_router_grp's order: chunk c's fused
-        // multiply-adds, pinned before the loads of chunk c + NB
+        // multiply-adds for the 4 tokens interleaved (4 independent chains
+        // in flight), pinned before the loads of chunk c + NB
 #pragma unroll
         for (int c = 0; c < C::NC; c++) {
-#pragma unroll
-            for (int t = 0; t < RQ_T; t++) {
-                acc[t] = C::fma_chunk(buf[c % NB], xT[t] + (size_t)r * TP, c, acc[t]);
-                __asm__ volatile("" : "+v"(acc[t]) : : "memory");
-            }
+            const float* const xr[RQ_T] = {xT[0] + (size_t)r * TP, xT[1] + (size_t)r * TP, xT[2] + (size_t)r * TP,
+                                            xT[3] + (size_t)r * TP};
+            C::template fma_chunk_n<RQ_T>(buf[c % NB], xr, c, acc);
+            static_assert(RQ_T == 4, "one pin per chunk for the 4 tokens");
+            __asm__ volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]) : : "memory");
             if (c + NB < C::NC) C::load(buf[c % NB], wt, eg, c + NB, lane);
         }
         const int e = 8 * eg + el;

@@ -153,20 +153,24 @@ def test_router_bitexact(gpu, oracle_lib, shape, B):
     assert np.array_equal(lg2.view(np.uint32), lg.view(np.uint32)) and np.array_equal(top2, top)
 
 
-def test_router_lane_grouping_kat(gpu, oracle_lib):
+@pytest.mark.parametrize("B", [2, 64])
+def test_router_lane_grouping_kat(gpu, oracle_lib, B):
     """The lane-grouping known answer of tests/test_oracle_math.py through
     the GPU router (float32 and bf16 tables, d = 512 and 2048): a row whose
     products are 2^24, 1, 1, 1, -2^24 at j = 0, 8, 16, 9, 4 scores exactly 1
-    against x = ones only in the reference's chain order and sum tree."""
+    against x = ones only in the reference's chain order and sum tree.
+    B = 64 takes the 4-token router, whose 4 chains per lane are interleaved;
+    with E = 16 (2 expert groups) half of its waves have no chains."""
     from test_oracle_math import router_kat_row
-    banner("router lane-grouping KAT")
+    banner(f"router lane-grouping KAT B={B}")
     for d in (512, 2048):
         gw = router_weights(MoEShape(d=d, m=64, E=16, topk=4, renorm=True), 0)
         gw[3] = router_kat_row(d)
-        x = np.ones((2, d), np.float32)
+        x = np.ones((B, d), np.float32)
+        x[1::2] = activations(B // 2, d)           # other tokens between the known answers
         for bf16 in (False, True):
             lg, _, _ = _gpu_router(gw, x, 4, True, bf16=bf16)
-            assert np.all(lg[:, 3] == 1.0), (d, bf16, lg[:, 3])
+            assert np.all(lg[0::2, 3] == 1.0), (d, bf16, lg[0::2, 3])
             rl, _, _ = oracle_lib.route(gw, x, 4, True)
             assert np.array_equal(lg.view(np.uint32), rl.view(np.uint32))
 
