@@ -578,11 +578,21 @@ __device__ __forceinline__ unsigned wave_inclusive_scan(unsigned x) {
 // Exclusive prefix sums of two 32-bit fields over the block (blockDim.x <=
 // 1024); every thread must call it.  wsum is LDS scratch of 32 unsigned;
 // tot receives both totals.
+// A block barrier that orders LDS only: the LDS accesses before it are
+// complete, while global stores and loads in flight stay in flight
+// (__syncthreads also waits for every outstanding global access).  For
+// blocks whose threads exchange data through LDS only.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ uint2 block_exclusive_scan2(uint2 v, unsigned* wsum, uint2* tot) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const unsigned a = wave_inclusive_scan(v.x), b = wave_inclusive_scan(v.y);
     if (lane == 63) { wsum[w] = a; wsum[16 + w] = b; }
-    __syncthreads();
+    lds_barrier();
     unsigned offa = 0, offb = 0, alla = 0, allb = 0;
     for (int j = 0; j < nw; j++) {
         const unsigned ta = wsum[j], tb = wsum[16 + j];
@@ -592,7 +602,7 @@ __device__ __forceinline__ uint2 block_exclusive_scan2(uint2 v, unsigned* wsum, 
         allb += tb;
     }
     *tot = make_uint2(alla, allb);
-    __syncthreads();
+    lds_barrier();
     return make_uint2(offa + a - v.x, offb + b - v.y);
 }
 
@@ -785,14 +795,18 @@ __host__ __device__ constexpr int dispatch_lds_ints(int nslot, int E) {
 // block computes depends on that order: a slot's products, act, y and its
 // place in the union order (from the first slots) are the same wherever
 // it sits in its segment; the work table and tile lists come from the
-// counts alone.
+// counts alone.  The block's threads exchange data through LDS only (its
+// global outputs are not read back), so its barriers wait for LDS alone and
+// the outputs' stores stay in flight.  With wn (STABLE false only: it may
+// alias the counts, which are dead once the segment starts are scanned),
+// wn[u] = the slot count of work entry u, for u < umax.
 template <bool STABLE = true>
 __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E, int k, int* lds,
                                                int* __restrict__ seg_off, int* __restrict__ seg_slot,
                                                int* __restrict__ active, int* __restrict__ n_active,
                                                int* __restrict__ first_slot, int* __restrict__ comb,
                                                ExpertWork* __restrict__ work = nullptr,
-                                               int umax = 0, const ExpertRec* rec = nullptr) {
+                                               int umax = 0, const ExpertRec* rec = nullptr, int* wn = nullptr) {
     constexpr unsigned short NONE = 0xFFFF;
     const int nchunk = STABLE ? (nslot + DISP_CHUNK - 1) / DISP_CHUNK : 1;
     int* cnt = lds;                              // [E][nchunk] (STABLE) or [E]
@@ -805,17 +819,30 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
     for (int i = tid; i < nchunk * E; i += nth) cnt[i] = 0;
     if (!STABLE)
         for (int i = tid; i < E; i += nth) fs[i] = 0x7FFFFFFF;
-    if (!STABLE) __syncthreads();
-    for (int s = tid; s < nslot; s += nth) {
-        const int e = top[s];
-        const bool ok = e >= 0 && e < E;
-        te[s] = ok ? (unsigned short)e : NONE;
-        if (!STABLE) {
-            rk[s] = ok ? (unsigned short)atomicAdd(&cnt[ok ? e : 0], 1) : NONE;
-            if (ok) atomicMin(&fs[e], s);
+    if (!STABLE) lds_barrier();
+    // the thread's entries of the top-k table, DISP_PF at a time with every
+    // load issued before the first is used (indices past the end read the
+    // last entry and are not used)
+    constexpr int DISP_PF = 4;
+    for (int s0 = tid; s0 < nslot; s0 += DISP_PF * nth) {
+        int ev[DISP_PF];
+#pragma unroll
+        for (int j = 0; j < DISP_PF; j++) ev[j] = top[min(s0 + j * nth, nslot - 1)];
+#pragma unroll
+        for (int j = 0; j < DISP_PF; j++) {
+            const int s = s0 + j * nth;
+            const int e = ev[j];
+            const bool ok = e >= 0 && e < E;
+            if (s < nslot) {
+                te[s] = ok ? (unsigned short)e : NONE;
+                if (!STABLE) {
+                    rk[s] = ok ? (unsigned short)atomicAdd(&cnt[ok ? e : 0], 1) : NONE;
+                    if (ok) atomicMin(&fs[e], s);
+                }
+            }
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (STABLE) {
     int nbits = 1;
     while ((1 << nbits) < E) nbits++;
@@ -833,7 +860,7 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
         if (s < nslot) rk[s] = ok ? (unsigned short)r : NONE;
         if (ok && r == 0) cnt[e * nchunk + c] = __popcll(same);
     }
-    __syncthreads();
+    lds_barrier();
     // per expert: exclusive prefix over its chunks (one wave per expert, a
     // wave scan per 64 chunks); the expert's total goes to off[e]
     for (int e = w; e < E; e += nw) {
@@ -847,7 +874,7 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
         }
         if (lane == 0) off[e] = (int)carry;
     }
-    __syncthreads();
+    lds_barrier();
     }
     // one block scan of (count, multi << 16 | single) gives segment starts
     // and the work-table positions of both groups
@@ -880,7 +907,10 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
 #pragma unroll
             for (int p = 0; p < 3; p++) { wk.sc[p] = rec->sc[p]; wk.pk[p] = rec->pk[p]; }
             const int u = total_e > 1 ? im : n_multi + is;
-            if (u < umax) work[u] = wk;
+            if (u < umax) {
+                work[u] = wk;
+                if (wn) wn[u] = total_e;
+            }
         }
     }
     if (work) {
@@ -890,9 +920,10 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
 #pragma unroll
             for (int p = 0; p < 3; p++) { wk.sc[p] = 0; wk.pk[p] = 0; }
             work[u] = wk;
+            if (wn) wn[u] = 0;
         }
     }
-    __syncthreads();
+    lds_barrier();
     for (int s = tid; s < nslot; s += nth) {
         const unsigned short r = rk[s];
         if (r == NONE) continue;
@@ -902,7 +933,7 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
         if (STABLE && pos == off[e]) { first_slot[e] = s; fs[e] = s; }
     }
     if (!STABLE && tid < E && total_e > 0) first_slot[tid] = fs[tid];
-    __syncthreads();
+    lds_barrier();
     // union order per token: its slots ranked by the first slot of their
     // expert (distinct experts -> distinct keys); slots without an expert go
     // last and are stored as -1.  Each slot's key replaces its rank.
@@ -910,9 +941,12 @@ __device__ __forceinline__ void dispatch_block(const int* top, int nslot, int E,
         const unsigned short e = te[bi];
         rk[bi] = e != NONE ? (unsigned short)fs[e] : NONE;
     }
-    __syncthreads();
+    lds_barrier();
+    // bi / k as a multiply-high for k >= 2: exact for bi * k < 2^32
+    // (nslot < 65536, k <= 32); the constant wraps to 0 for k = 1
+    const unsigned kmagic = 0xFFFFFFFFu / (unsigned)k + 1u;
     for (int bi = tid; bi < nslot; bi += nth) {
-        const int b = bi / k, i = bi % k;
+        const int b = k == 1 ? bi : (int)__umulhi((unsigned)bi, kmagic), i = bi - b * k;
         const unsigned short key = rk[bi];
         int r = 0;
 #pragma unroll 8

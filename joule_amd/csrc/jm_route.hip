@@ -412,20 +412,24 @@ k_dispatch_work(RouteArgs a) {
     extern __shared__ int lds_i[];
     ExpertRec rec;
     if ((int)threadIdx.x < a.E) rec = load_expert_rec(a.rec, a.key0, threadIdx.x);
+    // the work entries' slot counts come back in LDS (over the expert
+    // counts, dead by then); the scan below uses the dispatch's scan scratch
+    int* const wn = lds_i;
+    unsigned* const wsum = (unsigned*)(lds_i + 3 * a.E + 1);
     dispatch_block<false>(a.top, a.B * a.topk, a.E, a.topk, lds_i, a.seg_off, a.seg_slot, a.active,
-                   a.n_active, a.first_slot, a.comb, a.work, a.umax, &rec);
+                   a.n_active, a.first_slot, a.comb, a.work, a.umax, &rec, wn);
     // the dense experts' token tiles, in work-table order, and the list of
     // the experts under dense_min (their wave items run on the MFMA grids)
-    __syncthreads();
+    lds_barrier();
     const int u = threadIdx.x;
     int ct = 0, sm = 0;
     if (u < a.umax) {
-        const int n = a.work[u].n;
+        const int n = wn[u];
         ct = n >= a.dense_min ? (n + JM_DENSE_TILE - 1) / JM_DENSE_TILE : 0;
         sm = n > 0 && n < a.dense_min;
     }
     uint2 tot;
-    const uint2 ex = block_exclusive_scan2(make_uint2((unsigned)ct, (unsigned)sm), (unsigned*)lds_i, &tot);
+    const uint2 ex = block_exclusive_scan2(make_uint2((unsigned)ct, (unsigned)sm), wsum, &tot);
     for (int j = 0; j < ct; j++) a.tiles[ex.x + j] = make_int2(u, j);
     if (sm) a.small[ex.y] = u;
     if (threadIdx.x == 0) {
