@@ -578,10 +578,10 @@ __device__ __forceinline__ unsigned wave_inclusive_scan(unsigned x) {
 // Exclusive prefix sums of two 32-bit fields over the block (blockDim.x <=
 // 1024); every thread must call it.  wsum is LDS scratch of 32 unsigned;
 // tot receives both totals.
-// A block barrier that orders LDS only: the LDS accesses before it are
-// complete, while global stores and loads in flight stay in flight
-// (__syncthreads also waits for every outstanding global access).  For
-// blocks whose threads exchange data through LDS only.
+// A block barrier whose fences cover LDS only (the LDS accesses before it
+// are complete and visible to the block after it), for blocks whose threads
+// exchange data through LDS alone: it states that the block's global
+// accesses need no ordering among its threads.
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
@@ -796,8 +796,8 @@ __host__ __device__ constexpr int dispatch_lds_ints(int nslot, int E) {
 // place in the union order (from the first slots) are the same wherever
 // it sits in its segment; the work table and tile lists come from the
 // counts alone.  The block's threads exchange data through LDS only (its
-// global outputs are not read back), so its barriers wait for LDS alone and
-// the outputs' stores stay in flight.  With wn (STABLE false only: it may
+// global outputs are not read back), so its barriers order LDS alone.
+// With wn (STABLE false only: it may
 // alias the counts, which are dead once the segment starts are scanned),
 // wn[u] = the slot count of work entry u, for u < umax.
 template <bool STABLE = true>
