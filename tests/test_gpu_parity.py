@@ -195,13 +195,16 @@ def test_router_ties_lowest_index(gpu, oracle_lib):
 
 # ---------------------------------------------------------------- dispatch
 
-@pytest.mark.parametrize("B,E,k", [(1, 128, 8), (8, 128, 8), (8, 64, 8), (512, 128, 8), (3, 16, 4)])
+@pytest.mark.parametrize("B,E,k", [(1, 128, 8), (8, 128, 8), (8, 64, 8), (512, 128, 8), (3, 16, 4),
+                                   # top-k widths that are not powers of two, and 1 (the token of a
+                                   # slot is its index over k by a multiply-high)
+                                   (300, 16, 1), (100, 40, 3), (64, 24, 5)])
 def test_dispatch_stable_sort(gpu, B, E, k):
     banner(f"dispatch B={B} E={E}")
     rng = np.random.default_rng(B * 31 + E)
     top = np.stack([rng.permutation(E)[:k] for _ in range(B)]).astype(np.int32)
     if B >= 8:
-        top[1, 2] = -1                         # a slot without an expert (NaN scores)
+        top[1, min(2, k - 1)] = -1             # a slot without an expert (NaN scores)
     t = torch.from_numpy(top.ravel()).cuda()
     outs = [torch.full((n,), -7, dtype=torch.int32, device="cuda") for n in (E + 1, B * k, E, 1, E, B * k)]
     _lib.check(_lib.lib().jm_dispatch(_lib.ptr(t), B * k, E, k, *[_lib.ptr(o) for o in outs],
@@ -364,6 +367,28 @@ def test_block_decode_launch_shapes(gpu, oracle_lib, shape, B):
         x = activations(B, shape.d)
         out, top, tw = _run_block(layer, 0, x)
         rout, rtop, rtw = layer.oracle(0).forward(x)
+        assert np.array_equal(top, rtop)
+        assert np.array_equal(tw.view(np.uint32), rtw.view(np.uint32))
+        err = _rel(out, rout)
+        print(f"  max rel err {shape.name} B={B}: {err:.3e}", flush=True)
+        assert err <= TOL
+    finally:
+        layer.store.close()
+
+
+# The dispatch path (more than 256 slots) at top-k widths 3 and 1: the
+# block dispatch's token index over k, the work table and the MFMA grids
+# (about 12 slots per expert).
+@pytest.mark.parametrize("shape,B", [(MoEShape(1024, 1024, 24, 3, True, "d1024-E24-k3"), 100),
+                                     (MoEShape(1024, 1024, 16, 1, False, "d1024-E16-k1"), 260)],
+                         ids=lambda v: v.name if isinstance(v, MoEShape) else str(v))
+def test_block_dispatch_path_topk_widths(gpu, oracle_lib, shape, B):
+    banner(f"block {shape.name} B={B}")
+    layer = Layer(shape, 64, 1, oracle_lib)
+    try:
+        x = activations(B, shape.d)
+        out, top, tw = _run_block(layer, 0, x)
+        rout, rtop, rtw = layer.oracle(0).forward(x, n_threads=8)
         assert np.array_equal(top, rtop)
         assert np.array_equal(tw.view(np.uint32), rtw.view(np.uint32))
         err = _rel(out, rout)
