@@ -699,7 +699,7 @@ k_attn_part(AttnArgs a) {
     float* const red0 = (float*)&vt[0][0];
     uint16_t (*qs)[2][HD] = (uint16_t (*)[2][HD])&vt[0][0];
     uint16_t (*kvn)[HD] = (uint16_t (*)[HD])((char*)&vt[0][0] + QPK * 2 * HD * 2);
-    const int s = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int kh = blockIdx.x, b = blockIdx.y, s = (int)gridDim.z - 1 - (int)blockIdx.z;
     const int pos = a.pos[b];
     const int T = pos + 1;
     const int t0 = s * P;
@@ -899,7 +899,7 @@ k_attn_part_f32(AttnArgs a) {
     __shared__ __align__(16) float pw[4][QPK][PW];       // each wave's softmax numerators
     __shared__ __align__(16) float red[4][QPK * HD];     // each wave's outputs
     __shared__ float mls[4][QPK][2];                     // each wave's (max, sum)
-    const int s = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int kh = blockIdx.x, b = blockIdx.y, s = (int)gridDim.z - 1 - (int)blockIdx.z;
     const int pos = a.pos[b];
     const int T = pos + 1;
     const int t0 = s * P;
@@ -1101,7 +1101,13 @@ hipError_t launch_attn(const AttnArgs& a, int qpk, float* att, hipStream_t st) {
         hipError_t e0 = hipGetLastError();
         if (e0 != hipSuccess) return e0;
     }
-    const dim3 grid((unsigned)a.S, (unsigned)a.KH, (unsigned)a.B);
+    // Split s of (KV head kh, token b) is block (kh, b, S - 1 - s): the
+    // splits are dispatched from the last one, which holds the fewest
+    // positions (or none, for a token whose prefix is short).  A block that
+    // lands on a CU after others has its first requests served behind
+    // theirs; dispatched this way, the blocks that land late are mostly full
+    // splits behind light ones rather than full splits behind full ones.
+    const dim3 grid((unsigned)a.KH, (unsigned)a.B, (unsigned)a.S);
 #define JM_AP(Q) if (a.kv_f32) hipLaunchKernelGGL(k_attn_part_f32<Q>, grid, dim3(256), 0, st, a); \
                  else hipLaunchKernelGGL(k_attn_part<Q>, grid, dim3(256), 0, st, a)
     switch (qpk) {
