@@ -434,7 +434,9 @@ int jm_q4_gemv_f32(float* out, const float* x, const uint8_t* packed, const uint
 /* out[T][m] = X[T][d] . dequant(W[m][d])^T; argument order of q4_gemm_f32
  * (expert_ffn.c:201) plus the stream.  From jm_get_q4_gemm_min_tokens()
  * tokens the product runs on the int8 matrix cores (when m, d and group
- * allow it and scales is 16-byte aligned), below on the v_dot8 digit
+ * allow it and scales is 16-byte aligned; when its 32-token tiles x 256-row
+ * blocks are fewer than 256, the contraction is split over up to 8 blocks
+ * and the partial sums are added in split order), below on the v_dot8 digit
  * kernel.  Workspace: one buffer per (device, stream), kept and grown; a
  * call under stream capture takes a stream-ordered allocation instead. */
 int jm_q4_gemm_f32(float* out, const float* X, int T, const uint8_t* packed, const uint16_t* scales,
