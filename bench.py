@@ -643,6 +643,13 @@ def decode_step(B, steps, warmup, group, n_layers=48, position=2048, maxT=2176, 
     return res
 
 
+def monotone_stats(times):
+    """(non-decreasing, the largest amount by which a time exceeds a later one)
+    for times in the order of increasing size."""
+    inv = max((times[i] - min(times[i + 1:]) for i in range(len(times) - 1)), default=0.0)
+    return all(b >= a for a, b in zip(times, times[1:])), max(0.0, inv)
+
+
 def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 2, 4, 6, 7, 8, 12, 16, 20, 24, 28, 32, 33, 36, 48, 64, 512),
                    reps=100, rounds=5):
     """The plugin product HipBackend.q4_gemm (jm_q4_gemm_f32, the reference's
@@ -752,12 +759,12 @@ def plugin_q4_gemm(group, m=768, d=2048, sizes=(1, 2, 4, 6, 7, 8, 12, 16, 20, 24
         if all(out[f"T{u}"]["mfma_us"] <= out[f"T{u}"]["dot8_us"] for u in ts if u >= t):
             cross = t
             break
-    gpu_us = [out[f"T{t}"]["us_per_call"] for t in ts]
+    monotone, inversion = monotone_stats([out[f"T{t}"]["us_per_call"] for t in ts])
     return {"m": m, "d": d, "group": group, "default_min_tokens": default_min, "measured_crossover_T": cross,
-            "us_per_call_monotone_in_T": all(b >= a for a, b in zip(gpu_us, gpu_us[1:])),
+            "us_per_call_monotone_in_T": monotone,
             # the most by which a size's time exceeds that of a larger size (sizes within one
             # 32-token tile do the same work on the matrix cores and differ by noise)
-            "max_inversion_us": max(0.0, max(gpu_us[i] - min(gpu_us[i + 1:]) for i in range(len(ts) - 1))),
+            "max_inversion_us": inversion,
             "queued_ahead": all(v["queued_ahead"] for v in out.values()), "sizes": out}
 
 

@@ -72,6 +72,14 @@ def test_block_bytes_count_each_routed_expert_once():
     assert r["block_frac"] == pytest.approx(r["bytes_alg"] / 42e-6 / 8e12, rel=1e-9)
 
 
+def test_monotone_stats_reports_the_largest_inversion():
+    assert bench.monotone_stats([1.0, 2.0, 2.0, 5.0]) == (True, 0.0)
+    ok, inv = bench.monotone_stats([5.0, 6.0, 5.5, 7.0, 5.8])
+    assert not ok and inv == pytest.approx(1.2)       # 7.0 against the later 5.8 (6.0 / 5.5: 0.5)
+    assert bench.monotone_stats([3.0]) == (True, 0.0)
+    assert bench.monotone_stats([]) == (True, 0.0)
+
+
 def test_more_than_one_gpu_is_refused_before_the_gpu_is_touched():
     p = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                        timeout=120, cwd=str(ROOT))
