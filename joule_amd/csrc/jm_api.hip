@@ -355,6 +355,15 @@ int ffn_enqueue(jm_store* s, int layer, const float* x, int B, float* out, const
     r.dense_min = s->dense_min; r.tiles = w.tiles; r.n_tiles = w.n_tiles; r.small = w.small;
     r.skip_topk = dec && jm::gateup_topk(B, E);
     r.ndig = s->ndig;
+    // From the quad router's batch sizes on the dispatch path, the tokens'
+    // digits are encoded by the dispatch launch, on the CUs its dispatch
+    // block leaves idle, instead of by the router.  The decoder layer's
+    // normalised tokens reach it through y, which the down stage writes
+    // only later.
+    r.enc_late = !dec && B >= JM_ROUTER_QUAD_MIN_B;
+    const bool layer_in = io.xpart || io.norm_w;
+    r.xn = r.enc_late && layer_in ? w.y : nullptr;
+    r.xenc = layer_in ? w.y : x;
     jm::ExpertArgs a;
     a.blob = s->blob; a.rec = s->rec; a.key0 = (long long)layer * E; a.E = E;
     a.work = w.work; a.umax = umax; a.seg_slot = w.seg_slot;

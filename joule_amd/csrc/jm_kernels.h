@@ -116,6 +116,9 @@ struct RouteArgs {
     int* small;               // [umax] work-table entries of the experts under dense_min
     int skip_topk;            // 1: the top-k runs in the gate/up kernel
     int ndig;                 // digit planes the router writes to xdig (4 or 5)
+    int enc_late;             // 1: the dispatch launch encodes the tokens, not the router (k_router_quad only)
+    float* xn;                // [B][d] the router's staged tokens, for that encode (NULL: not written)
+    const float* xenc;        // [B][d] the tokens that encode reads (x, or xn)
 };
 // from this many tokens the router serves 4 tokens per block from one read
 // of each group's table (k_router_quad)
@@ -125,7 +128,8 @@ struct RouteArgs {
 // router scores + x digits (one wave per expert group and token), then the
 // top-k of every token (unless skip_topk)
 hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st);
-// dispatch + work table from a.top (dispatch path)
+// dispatch + work table from a.top (dispatch path); with enc_late, also the
+// tokens' digits from a.xenc, on the launch's blocks past the first
 hipError_t launch_dispatch_work(const RouteArgs& a, hipStream_t st);
 // experts per layer in the router copy: E rounded up to whole groups of 8
 __host__ __device__ constexpr int router_experts_padded(int E) { return (E + 7) / 8 * 8; }

@@ -336,6 +336,11 @@ k_router_quad(RouteArgs a) {
                     xv[i].w = __fmul_rn(__fmul_rn(xv[i].w, inv), bf16_bits_to_f32(wv.y >> 16));
                 }
             }
+            if (LAYER && blockIdx.x == 0 && a.xn) {
+                float4* xo = (float4*)(a.xn + (size_t)b * d);
+#pragma unroll
+                for (int i = 0; i < XV; i++) xo[lane + 64 * i] = xv[i];
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < XV; i++) xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -357,12 +362,14 @@ k_router_quad(RouteArgs a) {
     // waves, before the chains: they need only the staged tokens, so they
     // run while the table's chunks are still arriving.  The tokens of a
     // group are encoded together (unconditionally, the stores guarded), so
-    // that their reduction chains interleave.
+    // that their reduction chains interleave.  With enc_late the dispatch
+    // launch encodes them instead, on the CUs its one dispatch block leaves
+    // idle.
     constexpr int ng = d / G;
     constexpr int PPW = JM_WAVE / G;
     const int sub = lane / G;
     const bool i8 = a.xqh != nullptr;
-    for (int base = eg * PPW; base < ng; base += nvg * PPW) {
+    for (int base = a.enc_late ? ng : eg * PPW; base < ng; base += nvg * PPW) {
         const int p = base + sub;
         const bool ok = p < ng;
         const int pp = ok ? p : 0;
@@ -406,10 +413,52 @@ k_router_quad(RouteArgs a) {
     }
 }
 
-// Dispatch and work table of all slots from the top-k table (dispatch path).
+// The dispatch launch's token encode (enc_late): the x digits and, for the
+// MFMA branch, the digit pairs of every token, from a.xenc (the tokens as the
+// router scored them).  Item (token quad, group position) per wave, one
+// G-value group per G-lane segment, the 4 tokens' loads issued together and
+// their encodes interleaved; the same values as the router's encode.
+template <int G, int NDIG>
+__device__ __forceinline__ void encode_late(const RouteArgs& a, int gw, int nw) {
+    constexpr int PPW = JM_WAVE / G;
+    const int lane = threadIdx.x & 63, sub = lane / G;
+    const int d = a.d, ng = d / G, ngw = ng / PPW;
+    const int nq = (a.B + RQ_T - 1) / RQ_T;
+    const bool i8 = a.xqh != nullptr;
+    for (int it = gw; it < nq * ngw; it += nw) {
+        const int q = it / ngw;
+        const int p = (it - q * ngw) * PPW + sub;
+        const int b0 = q * RQ_T;
+        const int nt = min(RQ_T, a.B - b0);
+        float v[RQ_T];
+#pragma unroll
+        for (int t = 0; t < RQ_T; t++) {
+            const size_t b = (size_t)b0 + (t < nt ? t : 0);
+            v[t] = a.xenc[b * d + (size_t)p * G + (lane & (G - 1))];
+        }
+#pragma unroll
+        for (int t = 0; t < RQ_T; t++) {
+            const bool st = t < nt;
+            const size_t b = (size_t)b0 + (st ? t : 0);
+            const size_t o = b * d + (size_t)p * G;
+            encode_group_both<G, NDIG>(st ? v[t] : 0.0f, st, a.xdig + (b * ng + p) * (NDIG * (G / 8)),
+                                       a.xscale + b * ng + p, i8, a.xqh + (i8 ? o : 0), a.xql + (i8 ? o : 0),
+                                       a.xqs + b * ng + p, a.xqc + b * ng + p);
+        }
+    }
+}
+
+// Dispatch and work table of all slots from the top-k table (dispatch
+// path), on block 0; with enc_late, the blocks past it encode the tokens.
+template <int G, int NDIG>
 __global__ void __launch_bounds__(1024)
 k_dispatch_work(RouteArgs a) {
     extern __shared__ int lds_i[];
+    if (blockIdx.x > 0) {
+        encode_late<G, NDIG>(a, (blockIdx.x - 1) * (blockDim.x / JM_WAVE) + (threadIdx.x >> 6),
+                             (gridDim.x - 1) * (blockDim.x / JM_WAVE));
+        return;
+    }
     ExpertRec rec;
     if ((int)threadIdx.x < a.E) rec = load_expert_rec(a.rec, a.key0, threadIdx.x);
     // the work entries' slot counts come back in LDS (over the expert
@@ -465,8 +514,27 @@ hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {
     return launch_topk(a.logits, a.B, a.E, a.topk, a.renorm, a.top, a.tw, st);
 }
 
+// Blocks of 16 encode waves past the dispatch block: one (token quad, group
+// position) item per wave up to 512 blocks, more per wave past that.
+constexpr int ENC_LATE_MAX_BLOCKS = 512;
+
 hipError_t launch_dispatch_work(const RouteArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL(k_dispatch_work, dim3(1), dim3(1024), (size_t)dispatch_lds_ints(a.B * a.topk, a.E) * 4, st, a);
+    int nenc = 0;
+    if (a.enc_late) {
+        if (a.group != 32 && a.group != 64) return hipErrorInvalidValue;
+        if (a.ndig != 4 && a.ndig != 5) return hipErrorInvalidValue;
+        const long long items = (long long)((a.B + RQ_T - 1) / RQ_T) * (a.d / 64);
+        nenc = (int)std::min<long long>(ENC_LATE_MAX_BLOCKS, (items + 15) / 16);
+    }
+    const dim3 grid((unsigned)(1 + nenc));
+    const size_t lds = (size_t)dispatch_lds_ints(a.B * a.topk, a.E) * 4;
+    if (a.group == 64) {
+        if (a.ndig == 5) hipLaunchKernelGGL((k_dispatch_work<64, 5>), grid, dim3(1024), lds, st, a);
+        else hipLaunchKernelGGL((k_dispatch_work<64, 4>), grid, dim3(1024), lds, st, a);
+    } else {
+        if (a.ndig == 5) hipLaunchKernelGGL((k_dispatch_work<32, 5>), grid, dim3(1024), lds, st, a);
+        else hipLaunchKernelGGL((k_dispatch_work<32, 4>), grid, dim3(1024), lds, st, a);
+    }
     return hipGetLastError();
 }
 
