@@ -405,6 +405,68 @@ __device__ __forceinline__ void encode_group_both(float v, bool store, uint32_t*
     }
 }
 
+// encode_group_both for NT groups at once, one value of each per lane: the
+// groups' reductions, divisions and digits first, with no branch among them,
+// then every store.  The NT dependency chains overlap instead of running one
+// after another between the stores' branches.  The same values as NT calls
+// of encode_group_both (every step is the same per group).
+template <int G, int NDIG, int NT>
+__device__ __forceinline__ void encode_groups_n(const float* v, const bool* store, uint32_t* const* dig,
+                                                float* const* scale, bool i8, int8_t* const* hi, int8_t* const* lo,
+                                                float* const* qscale, int* const* qsum) {
+    const int i = threadIdx.x & (G - 1);
+    int bad[NT];
+    float mx[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const float a = fabsf(v[t]);
+        bad[t] = seg_or<G>(!(a <= 3.4028235e38f) ? 1 : 0);
+        mx[t] = seg_max<G>(a);
+    }
+    float sc[NT];
+    uint32_t word[NT][NDIG];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        sc[t] = digit_scale<NDIG>(mx[t], bad[t] != 0);
+        const float inv = (mx[t] > 0.0f && !bad[t]) ? __fdiv_rn((float)Digits<NDIG>::R, mx[t]) : 0.0f;
+        int dg[NDIG];
+        split_digits<NDIG>((int)rintf(__fmul_rn(v[t], inv)), dg);
+#pragma unroll
+        for (int k = 0; k < NDIG; k++) word[t][k] = (uint32_t)seg_or<8>((dg[k] & 15) << (4 * (i & 7)));
+    }
+    int hv[NT], lv[NT], qi[NT];
+    float qsc[NT];
+    if (i8) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const float inv = (mx[t] > 0.0f && !bad[t]) ? __fdiv_rn((float)I8_R, mx[t]) : 0.0f;
+            const int q = (int)rintf(__fmul_rn(v[t], inv));
+            lv[t] = ((q + 128) & 255) - 128;
+            hv[t] = (q - lv[t]) >> 8;
+            qi[t] = (int)seg_sum<G>((float)q);
+            qsc[t] = bad[t] ? __int_as_float(0x7FC00000) : __fdiv_rn(mx[t], (float)I8_R);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        if (!store[t]) continue;
+        if ((i & 7) == 0) {
+#pragma unroll
+            for (int k = 0; k < NDIG; k++) dig[t][k * (G / 8) + (i >> 3)] = word[t][k];
+        }
+        if (i == 0) *scale[t] = sc[t];
+        if (i8) {
+            const int p = (i & ~7) + i8_pos(i & 7);
+            hi[t][p] = (int8_t)hv[t];
+            lo[t][p] = (int8_t)lv[t];
+            if (i == 0) {
+                *qscale[t] = qsc[t];
+                *qsum[t] = qi[t];
+            }
+        }
+    }
+}
+
 // Encode one group of G floats, value i held by lane i of an aligned G-lane
 // segment (G = 32 or 64), into NDIG x G/8 digit words and one scale.
 // Lane j*8 of the segment writes word j of every digit k to dig[k*(G/8)+j];

@@ -88,6 +88,28 @@ hipError_t launch_bf16_exact(const float* in, long long n, unsigned* flag, hipSt
 }
 
 
+// Where the encodes of NT groups go: entry t receives group p of token b
+// (its x digits and their scale; for the MFMA branch also its digit pairs,
+// their scale and integer sum).
+template <int G, int NDIG, int NT>
+struct EncDst {
+    uint32_t* dig[NT];
+    float* sc[NT];
+    int8_t* hi[NT];
+    int8_t* lo[NT];
+    float* qs[NT];
+    int* qc[NT];
+    __device__ __forceinline__ void set(int t, const RouteArgs& a, size_t b, int p, bool i8) {
+        const size_t ng = (size_t)(a.d / G), g = b * ng + p, o = b * a.d + (size_t)p * G;
+        dig[t] = a.xdig + g * (NDIG * (G / 8));
+        sc[t] = a.xscale + g;
+        hi[t] = a.xqh + (i8 ? o : 0);
+        lo[t] = a.xql + (i8 ? o : 0);
+        qs[t] = a.xqs + g;
+        qc[t] = a.xqc + g;
+    }
+};
+
 // x digits of token b staged in xT (chain order), wave eg's share of the
 // token's groups over ngrp waves: one G-value group per G-lane segment (and,
 // for the MFMA branch, the same group as int8 digit pairs), two groups at a
@@ -103,18 +125,19 @@ __device__ __forceinline__ void encode_token_share(const RouteArgs& a, int b, in
     const int sub = lane / G;
     const bool i8 = a.xqh != nullptr;
     for (int base = eg * PPW; base < ng; base += 2 * ngrp * PPW) {
+        float v[2];
+        bool ok[2];
+        EncDst<G, NDIG, 2> dst;
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int p = base + u * ngrp * PPW + sub;
-            const bool ok = p < ng;
-            const int pp = ok ? p : 0;
+            ok[u] = p < ng;
+            const int pp = ok[u] ? p : 0;
             const int j = pp * G + (lane & (G - 1));
-            const float v = ok ? xT[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
-            const size_t o = (size_t)b * d + (size_t)pp * G;
-            encode_group_both<G, NDIG>(v, ok, a.xdig + ((size_t)b * ng + pp) * (NDIG * (G / 8)),
-                                       a.xscale + (size_t)b * ng + pp, i8, a.xqh + (i8 ? o : 0),
-                                       a.xql + (i8 ? o : 0), a.xqs + (size_t)b * ng + pp, a.xqc + (size_t)b * ng + pp);
+            v[u] = ok[u] ? xT[(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
+            dst.set(u, a, (size_t)b, pp, i8);
         }
+        encode_groups_n<G, NDIG, 2>(v, ok, dst.dig, dst.sc, i8, dst.hi, dst.lo, dst.qs, dst.qc);
     }
 }
 
@@ -374,16 +397,16 @@ k_router_quad(RouteArgs a) {
         const bool ok = p < ng;
         const int pp = ok ? p : 0;
         const int j = pp * G + (lane & (G - 1));
+        float v[RQ_T];
+        bool st[RQ_T];
+        EncDst<G, NDIG, RQ_T> dst;
 #pragma unroll
         for (int t = 0; t < RQ_T; t++) {
-            const bool st = ok && t < nt;
-            const size_t b = (size_t)b0 + (t < nt ? t : 0);
-            const float v = st ? xT[t][(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
-            const size_t o = b * d + (size_t)pp * G;
-            encode_group_both<G, NDIG>(v, st, a.xdig + (b * ng + pp) * (NDIG * (G / 8)), a.xscale + b * ng + pp, i8,
-                                       a.xqh + (i8 ? o : 0), a.xql + (i8 ? o : 0), a.xqs + b * ng + pp,
-                                       a.xqc + b * ng + pp);
+            st[t] = ok && t < nt;
+            v[t] = st[t] ? xT[t][(size_t)(j & 7) * TP + (j >> 3)] : 0.0f;
+            dst.set(t, a, (size_t)b0 + (t < nt ? t : 0), pp, i8);
         }
+        encode_groups_n<G, NDIG, RQ_T>(v, st, dst.dig, dst.sc, i8, dst.hi, dst.lo, dst.qs, dst.qc);
     }
     if (chains) {
         float acc[RQ_T];
@@ -416,8 +439,9 @@ k_router_quad(RouteArgs a) {
 // The dispatch launch's token encode (enc_late): the x digits and, for the
 // MFMA branch, the digit pairs of every token, from a.xenc (the tokens as the
 // router scored them).  Item (token quad, group position) per wave, one
-// G-value group per G-lane segment, the 4 tokens' loads issued together and
-// their encodes interleaved; the same values as the router's encode.
+// G-value group per G-lane segment, the 4 tokens' loads issued together;
+// the same values as the router's encode.  (The 4 encodes through
+// encode_groups_n made the 512-token block about 0.5 us slower.)
 template <int G, int NDIG>
 __device__ __forceinline__ void encode_late(const RouteArgs& a, int gw, int nw) {
     constexpr int PPW = JM_WAVE / G;
@@ -436,14 +460,13 @@ __device__ __forceinline__ void encode_late(const RouteArgs& a, int gw, int nw) 
             const size_t b = (size_t)b0 + (t < nt ? t : 0);
             v[t] = a.xenc[b * d + (size_t)p * G + (lane & (G - 1))];
         }
+        EncDst<G, NDIG, RQ_T> dst;
 #pragma unroll
         for (int t = 0; t < RQ_T; t++) {
             const bool st = t < nt;
-            const size_t b = (size_t)b0 + (st ? t : 0);
-            const size_t o = b * d + (size_t)p * G;
-            encode_group_both<G, NDIG>(st ? v[t] : 0.0f, st, a.xdig + (b * ng + p) * (NDIG * (G / 8)),
-                                       a.xscale + b * ng + p, i8, a.xqh + (i8 ? o : 0), a.xql + (i8 ? o : 0),
-                                       a.xqs + b * ng + p, a.xqc + b * ng + p);
+            dst.set(t, a, (size_t)b0 + (st ? t : 0), p, i8);
+            encode_group_both<G, NDIG>(st ? v[t] : 0.0f, st, dst.dig[t], dst.sc[t], i8, dst.hi[t], dst.lo[t],
+                                       dst.qs[t], dst.qc[t]);
         }
     }
 }
