@@ -438,31 +438,35 @@ k_router_quad(RouteArgs a) {
 
 // The dispatch launch's token encode (enc_late): the x digits and, for the
 // MFMA branch, the digit pairs of every token, from a.xenc (the tokens as the
-// router scored them).  Item (token quad, group position) per wave, one
-// G-value group per G-lane segment, the 4 tokens' loads issued together;
-// the same values as the router's encode.  (The 4 encodes through
+// router scored them).  Item (ENC_T tokens, group position) per wave, one
+// G-value group per G-lane segment, the tokens' loads issued together; the
+// same values as the router's encode.  Two tokens per item measured best:
+// at 512 tokens the block took 1.2 us less than with 4 (0.9 us at 64); with
+// 1 token per item it took as long at 512 and 0.4 us more at 64 tokens.
+// (The 4 encodes of a 4-token item through
 // encode_groups_n made the 512-token block about 0.5 us slower.)
+constexpr int ENC_T = 2;
 template <int G, int NDIG>
 __device__ __forceinline__ void encode_late(const RouteArgs& a, int gw, int nw) {
     constexpr int PPW = JM_WAVE / G;
     const int lane = threadIdx.x & 63, sub = lane / G;
     const int d = a.d, ng = d / G, ngw = ng / PPW;
-    const int nq = (a.B + RQ_T - 1) / RQ_T;
+    const int nq = (a.B + ENC_T - 1) / ENC_T;
     const bool i8 = a.xqh != nullptr;
     for (int it = gw; it < nq * ngw; it += nw) {
         const int q = it / ngw;
         const int p = (it - q * ngw) * PPW + sub;
-        const int b0 = q * RQ_T;
-        const int nt = min(RQ_T, a.B - b0);
-        float v[RQ_T];
+        const int b0 = q * ENC_T;
+        const int nt = min(ENC_T, a.B - b0);
+        float v[ENC_T];
 #pragma unroll
-        for (int t = 0; t < RQ_T; t++) {
+        for (int t = 0; t < ENC_T; t++) {
             const size_t b = (size_t)b0 + (t < nt ? t : 0);
             v[t] = a.xenc[b * d + (size_t)p * G + (lane & (G - 1))];
         }
-        EncDst<G, NDIG, RQ_T> dst;
+        EncDst<G, NDIG, ENC_T> dst;
 #pragma unroll
-        for (int t = 0; t < RQ_T; t++) {
+        for (int t = 0; t < ENC_T; t++) {
             const bool st = t < nt;
             dst.set(t, a, (size_t)b0 + (st ? t : 0), p, i8);
             encode_group_both<G, NDIG>(st ? v[t] : 0.0f, st, dst.dig[t], dst.sc[t], i8, dst.hi[t], dst.lo[t],
@@ -537,16 +541,16 @@ hipError_t launch_route_tok(const RouteArgs& a, hipStream_t st) {
     return launch_topk(a.logits, a.B, a.E, a.topk, a.renorm, a.top, a.tw, st);
 }
 
-// Blocks of 16 encode waves past the dispatch block: one (token quad, group
-// position) item per wave up to 512 blocks, more per wave past that.
-constexpr int ENC_LATE_MAX_BLOCKS = 512;
+// Blocks of 16 encode waves past the dispatch block: one item per wave up
+// to 1024 blocks, more per wave past that.
+constexpr int ENC_LATE_MAX_BLOCKS = 1024;
 
 hipError_t launch_dispatch_work(const RouteArgs& a, hipStream_t st) {
     int nenc = 0;
     if (a.enc_late) {
         if (a.group != 32 && a.group != 64) return hipErrorInvalidValue;
         if (a.ndig != 4 && a.ndig != 5) return hipErrorInvalidValue;
-        const long long items = (long long)((a.B + RQ_T - 1) / RQ_T) * (a.d / 64);
+        const long long items = (long long)((a.B + ENC_T - 1) / ENC_T) * (a.d / 64);
         nenc = (int)std::min<long long>(ENC_LATE_MAX_BLOCKS, (items + 15) / 16);
     }
     const dim3 grid((unsigned)(1 + nenc));
