@@ -4,12 +4,15 @@
 //                    in the reference's 8-chain order (decode_kernel.c:
 //                    234-256, 693-718) and a share of the token's x digits
 //                    for the expert dots
+//   k_router_quad    the same from 64 tokens, 4 tokens per block from one
+//                    read of the table
 //   k_topk           (jm_kernels.hip) one wave per token: softmax + top-k +
 //                    renormalisation (:1425-1448)
-//   k_dispatch_work  dispatch path only (more than 256 slots): the counting
-//                    sort of all slots (:1449-1485), the expert work table
-//                    and the token tiles of the experts that take the MFMA
-//                    branch
+//   k_dispatch_work  dispatch path only (more than 256 slots): block 0 the
+//                    counting sort of all slots (:1449-1485), the expert
+//                    work table and the token tiles of the experts that take
+//                    the MFMA branch; from 64 tokens the other blocks encode
+//                    the tokens' digits (the router then skips its encode)
 //
 // No block waits for or reads data written by another block of the same
 // launch: on MI355X each XCD has its own L2, and a device-scope handoff
