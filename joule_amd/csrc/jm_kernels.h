@@ -121,9 +121,13 @@ struct RouteArgs {
     const float* xenc;        // [B][d] the tokens that encode reads (x, or xn)
 };
 // from this many tokens the router serves 4 tokens per block from one read
-// of each group's table (k_router_quad)
+// of each group's table (k_router_quad), and on the dispatch path the
+// dispatch launch encodes the tokens.  Measured crossover of the Qwen3
+// block: below it one wave per (group, token) with its own encode is
+// 1.1 us faster at 64 tokens and about even at 128; from 192 tokens the
+// 4-token form is 3 us faster (10 us at 512).
 #ifndef JM_ROUTER_QUAD_MIN_B
-#define JM_ROUTER_QUAD_MIN_B 64
+#define JM_ROUTER_QUAD_MIN_B 144
 #endif
 // router scores + x digits (one wave per expert group and token), then the
 // top-k of every token (unless skip_topk)

@@ -4,14 +4,14 @@
 //                    in the reference's 8-chain order (decode_kernel.c:
 //                    234-256, 693-718) and a share of the token's x digits
 //                    for the expert dots
-//   k_router_quad    the same from 64 tokens, 4 tokens per block from one
+//   k_router_quad    the same from 144 tokens, 4 tokens per block from one
 //                    read of the table
 //   k_topk           (jm_kernels.hip) one wave per token: softmax + top-k +
 //                    renormalisation (:1425-1448)
 //   k_dispatch_work  dispatch path only (more than 256 slots): block 0 the
 //                    counting sort of all slots (:1449-1485), the expert
 //                    work table and the token tiles of the experts that take
-//                    the MFMA branch; from 64 tokens the other blocks encode
+//                    the MFMA branch; from 144 tokens the other blocks encode
 //                    the tokens' digits (the router then skips its encode)
 //
 // No block waits for or reads data written by another block of the same
@@ -445,7 +445,8 @@ k_router_quad(RouteArgs a) {
 // G-value group per G-lane segment, the tokens' loads issued together; the
 // same values as the router's encode.  Two tokens per item measured best:
 // at 512 tokens the block took 1.2 us less than with 4 (0.9 us at 64); with
-// 1 token per item it took as long at 512 and 0.4 us more at 64 tokens.
+// 1 token per item it took as long at 512 and 0.4 us more at 64 tokens (when
+// the encode moved here from 64 tokens on).
 // (The 4 encodes of a 4-token item through
 // encode_groups_n made the 512-token block about 0.5 us slower.)
 constexpr int ENC_T = 2;

@@ -153,13 +153,13 @@ def test_router_bitexact(gpu, oracle_lib, shape, B):
     assert np.array_equal(lg2.view(np.uint32), lg.view(np.uint32)) and np.array_equal(top2, top)
 
 
-@pytest.mark.parametrize("B", [2, 64])
+@pytest.mark.parametrize("B", [2, 160])
 def test_router_lane_grouping_kat(gpu, oracle_lib, B):
     """The lane-grouping known answer of tests/test_oracle_math.py through
     the GPU router (float32 and bf16 tables, d = 512 and 2048): a row whose
     products are 2^24, 1, 1, 1, -2^24 at j = 0, 8, 16, 9, 4 scores exactly 1
     against x = ones only in the reference's chain order and sum tree.
-    B = 64 takes the 4-token router, whose 4 chains per lane are interleaved;
+    B = 160 takes the 4-token router, whose 4 chains per lane are interleaved;
     with E = 16 (2 expert groups) half of its waves have no chains."""
     from test_oracle_math import router_kat_row
     banner(f"router lane-grouping KAT B={B}")
